@@ -1,0 +1,92 @@
+/*
+ * tlx.h -- C ABI of libtlx_hip.so, the gfx950 (MI355X) quantized-weight matmul library.
+ *
+ * Every entry point:
+ *   - takes device pointers and plain sizes (no HIP or torch types; `stream` is a
+ *     hipStream_t passed as void*, NULL = the default stream);
+ *   - keeps the reference kernel's positional argument order, then appends the sizes the
+ *     reference bakes into kernel names / #defines (M, N, K) and a layout flag;
+ *   - is asynchronous on `stream`, never allocates, never aborts;
+ *   - returns TLX_OK, a negative TLX_E_* code for a rejected argument (nothing launched),
+ *     or a positive hipError_t from the launch.
+ *
+ * Activations and outputs named *_f16 hold IEEE binary16 bit patterns (uint16_t).
+ */
+#ifndef TLX_H
+#define TLX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TLX_OK 0
+#define TLX_E_ARG (-1)     /* size / M / layout out of range */
+#define TLX_E_ALIGN (-2)   /* a pointer or row stride is not aligned as the layout needs */
+#define TLX_E_NODEV (-3)   /* no usable gfx950 device */
+
+/* Weight layouts (row-major over output rows). */
+#define TLX_LAYOUT_RAW 0     /* GGUF blocks as stored in the file */
+#define TLX_LAYOUT_PACKED 1  /* IQ3_XXS: pack_w1c regions [qs 64NB][sw 32NB][d 2NB];
+                                Q6_K: pack_w1c 212-B blocks [pad2][d2][sc16][lo128][qh64] */
+
+#define TLX_MAX_M 16         /* decode GEMVs accept 1..16 activation rows */
+
+int tlx_version(void);
+const char* tlx_strerror(int code);
+
+/* ------------------------------------------------------------------ dequantization
+ * Oracle-parity kernels: decode `rows` x `kdim` weights.  out_f16 = 0 writes float32 (the
+ * exact GGUF value), 1 writes fp16 bits (the value the reference's GEMVs consume).
+ * No reference counterpart (the reference dequantizes on the CPU in numpy:
+ * engine/pack_w4.py:39-68, engine/mm/MM_P2_ports.py:21-45,
+ * engine/mm/MM_P0_d2_repack.py:78-93).
+ */
+int tlx_iq3xxs_dequant(const void* w, const float* gridf, void* out, int64_t rows, int64_t kdim,
+                       int layout, int out_f16, void* stream);
+int tlx_q6k_dequant(const void* w, void* out, int64_t rows, int64_t kdim, int layout, int out_f16,
+                    void* stream);
+int tlx_iq4xs_dequant(const void* w, const float* iq4nl, float* out, int64_t rows, int64_t kdim,
+                      void* stream);
+
+/* ------------------------------------------------------------------ decode / spec-verify GEMVs */
+
+/* Fused IQ3_XXS FFN gate+up GEMV + SwiGLU:
+ *   gact[m][n] = silu16(half(Wg[n]·x[m])) * half(Wu[n]·x[m])
+ * Replaces ffn8 / ffn8v{3..11} (engine/ffn8.cu:134-185, engine/ffn8v11.cu:88-133):
+ * ffn8(wg, wu, gridf, hhx, gact).  wg, wu: N rows x 98*(K/256) B (layout PACKED);
+ * gridf: float[1024]; hhx_f16: [M][K]; gact_f16: [M][N]. */
+int tlx_ffn8(const void* wg, const void* wu, const float* gridf, const uint16_t* hhx_f16,
+             uint16_t* gact_f16, int M, int N, int K, int layout, void* stream);
+
+/* IQ3_XXS down GEMV + residual:  y[m][n] = hh[m][n] + float(half(Wd[n]·gact[m]))
+ * Replaces down8 / down8nw32_{3..11} (engine/down8.cu:134-144,
+ * engine/down8nw32_11.cu:88-125): down8(wd, gridf, gact, hh, y). */
+int tlx_down8(const void* wd, const float* gridf, const uint16_t* gact_f16, const float* hh,
+              float* y, int M, int N, int K, int layout, void* stream);
+
+/* Plain IQ3_XXS GEMV with fp16 output: out[m][n] = half(W[n]·x[m]).  The per-segment body
+ * of the fused attention / GDN projections (IQ3ROWP, engine/aq3k8.cu:99-131). */
+int tlx_iq3_gemv(const void* w, const float* gridf, const uint16_t* x_f16, uint16_t* out_f16,
+                 int M, int N, int K, int layout, void* stream);
+
+/* Fused attention q/k/v projections, all three IQ3_XXS (the BASELINE dense config):
+ * warp ranges [0,Nq) q, [Nq,Nq+Nk) k, [.., +Nv) v in one launch.
+ * Replaces aq3k8 / aq3k8v{4..11} (engine/aq3k8.cu:134-145, engine/aq3k8v11.cu:88-180):
+ * aq3k8(wq, wk, wv4, gridf, xh, qrow, krow, vrow). */
+int tlx_aq3k8(const void* wq, const void* wk, const void* wv, const float* gridf,
+              const uint16_t* xh_f16, uint16_t* qrow_f16, uint16_t* krow_f16, uint16_t* vrow_f16,
+              int M, int Nq, int Nk, int Nv, int K, int layout, void* stream);
+
+/* Q6_K GEMV, fp32 activations and outputs: y[n] = sum_k ((d*sc)*(q-32))[n][k] * x[k].
+ * The contract of h6k2048 (engine/mm/MM_P34_h6k2048.cu:8-52): h6k2048(w, x, y, rows),
+ * generalised to any K (multiple of 256) and to the raw 210-B / padded 212-B layouts. */
+int tlx_q6k_gemv(const void* w, const float* x, float* y, int rows, int K, int layout,
+                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TLX_H */

@@ -1,0 +1,60 @@
+"""The C ABI: the built library loads, exports every entry point include/tlx.h declares,
+the ctypes table matches the header, and argument validation rejects bad calls before any
+device work (these calls return before touching the GPU, so they run on the CPU host)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from thunderllamax_amd import _lib
+
+HDR = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "tlx.h")
+
+
+def _declared():
+    src = open(HDR).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(tlx_\w+)\s*\(", src)))
+
+
+def test_header_and_binding_agree():
+    assert _declared() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared():
+        assert hasattr(L, name), name
+
+
+def test_version_and_strerror():
+    L = _lib.lib()
+    assert L.tlx_version() >= 1
+    assert b"argument" in L.tlx_strerror(_lib.TLX_E_ARG)
+    assert b"align" in L.tlx_strerror(_lib.TLX_E_ALIGN)
+
+
+@pytest.mark.parametrize("M,N,K,layout,code", [
+    (0, 64, 5120, 1, _lib.TLX_E_ARG),        # M below range
+    (17, 64, 5120, 1, _lib.TLX_E_ARG),       # M above TLX_MAX_M
+    (1, 64, 5000, 1, _lib.TLX_E_ARG),        # K not a multiple of 256
+    (1, 64, 5120, 0, _lib.TLX_E_ARG),        # raw layout not accepted by the GEMV
+    (1, 64, 256 * 21, 1, _lib.TLX_E_ALIGN),  # odd block count -> rows not dword aligned
+])
+def test_ffn8_argument_validation(M, N, K, layout, code):
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.addressof(buf)
+    p = (p + 15) & ~15
+    rc = L.tlx_ffn8(p, p, p, p, p, M, N, K, layout, None)
+    assert rc == code
+
+
+def test_q6k_gemv_argument_validation():
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(64)
+    p = (ctypes.addressof(buf) + 15) & ~15
+    assert L.tlx_q6k_gemv(p, p, p, 0, 5120, 0, None) == _lib.TLX_E_ARG
+    assert L.tlx_q6k_gemv(p, p, p, 16, 5120, 7, None) == _lib.TLX_E_ARG
+    assert L.tlx_q6k_gemv(p + 1, p, p, 16, 5120, 0, None) == _lib.TLX_E_ALIGN

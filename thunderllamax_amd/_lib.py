@@ -1,0 +1,74 @@
+"""ctypes binding of libtlx_hip.so (the C ABI declared in include/tlx.h).
+
+The library is loaded from this package directory only; there is no fallback: if it is
+missing the import of any op raises, so a GPU run can never silently use another path.
+torch is imported first so the process has exactly one HIP runtime (torch's), which the
+library then binds to.
+"""
+import ctypes
+import os
+
+import torch  # noqa: F401  (loads the HIP runtime the library binds to)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtlx_hip.so")
+
+TLX_OK = 0
+TLX_E_ARG = -1
+TLX_E_ALIGN = -2
+TLX_E_NODEV = -3
+LAYOUT_RAW = 0
+LAYOUT_PACKED = 1
+MAX_M = 16
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+
+# name -> argument types (return type is int for all but tlx_strerror)
+SIGNATURES = {
+    "tlx_version": [],
+    "tlx_strerror": [_i],
+    "tlx_iq3xxs_dequant": [_p, _p, _p, _i64, _i64, _i, _i, _p],
+    "tlx_q6k_dequant": [_p, _p, _i64, _i64, _i, _i, _p],
+    "tlx_iq4xs_dequant": [_p, _p, _p, _i64, _i64, _p],
+    "tlx_ffn8": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "tlx_down8": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "tlx_iq3_gemv": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "tlx_aq3k8": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
+    "tlx_q6k_gemv": [_p, _p, _p, _i, _i, _i, _p],
+}
+
+
+class TlxError(RuntimeError):
+    """A libtlx entry point returned a non-zero status."""
+
+    def __init__(self, name, code, msg):
+        super().__init__(f"{name}: {msg} (status {code})")
+        self.code = code
+
+
+_LIB = None
+
+
+def lib():
+    """The loaded library (loaded on first use; raises if it was never built)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with `python -m thunderllamax_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = ctypes.c_char_p if name == "tlx_strerror" else ctypes.c_int
+        _LIB = L
+    return _LIB
+
+
+def call(name, *args):
+    """Call entry point `name`; raise TlxError on a non-zero status."""
+    L = lib()
+    rc = getattr(L, name)(*args)
+    if rc != TLX_OK:
+        raise TlxError(name, rc, L.tlx_strerror(rc).decode())
+    return rc

@@ -1,0 +1,62 @@
+// Shared device/host helpers for the gfx950 quantized-matmul library.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../../include/tlx.h"
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+
+#define TLX_WAVE 64
+
+// ---------------------------------------------------------------- host-side checks
+#define TLX_RET_IF(cond, code) \
+  do {                         \
+    if (cond) return (code);   \
+  } while (0)
+
+static inline int tlx_launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TLX_OK : (int)e;
+}
+
+static inline bool tlx_aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+// ---------------------------------------------------------------- device helpers
+__device__ __forceinline__ float tlx_h2f(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+
+__device__ __forceinline__ uint16_t tlx_f2h_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Loads through a byte pointer whose alignment is only known to be 2 (raw GGUF blocks).
+template <typename T>
+__device__ __forceinline__ T tlx_ldu(const uint8_t* p) {
+  T v;
+  __builtin_memcpy(&v, p, sizeof(T));
+  return v;
+}
+
+// fp16 SiLU chain of the reference FFN epilogue (/root/reference/engine/ffn8.cu:22-24):
+// h * rcp(1 + exp2(h * fp16(-log2 e))) with every step rounded to fp16.  The constant
+// -1.4423828125 is fp16(-log2(e)).  exp2 and rcp are the ROCm device-library fp16 routines.
+__device__ __forceinline__ __half tlx_hsilu(__half h) {
+  const __half t = __hmul(h, __float2half(-1.4423828125f));
+  const __half den = __hadd(__float2half(1.0f), hexp2(t));
+  return __hmul(h, hrcp(den));
+}
+
+// SwiGLU epilogue: gact = silu16(half(g)) * half(u), all in fp16.
+__device__ __forceinline__ uint16_t tlx_swiglu_bits(float g, float u) {
+  const __half hg = __float2half(g);
+  const __half hu = __float2half(u);
+  return __builtin_bit_cast(uint16_t, __hmul(tlx_hsilu(hg), hu));
+}

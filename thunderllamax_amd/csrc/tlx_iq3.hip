@@ -1,0 +1,350 @@
+// IQ3_XXS kernels for gfx950: bit-exact dequantization and the MFMA decode GEMV family
+// (FFN gate+up + SwiGLU, down + residual, fused attention q/k/v, plain GEMV).
+//
+// GEMV design (one kernel for every M in 1..16):
+//   * a workgroup owns a tile of 16 weight rows; its waves split the K blocks between them
+//     (block b goes to wave b % WAVES) and reduce through LDS in a fixed order, so the
+//     result does not depend on scheduling;
+//   * lane l of a wave owns weight row (l & 15) and the 64 consecutive k of each 256-block
+//     starting at 64*(l >> 4): one 16-B load of its 8 grid-index words, one 8-B load of its
+//     two scale/sign words, one 2-B load of the block's d;
+//   * each of the 8 lane-chunks (8 weights) becomes the B operand of one
+//     v_mfma_f32_16x16x32_f16; the A operand is the matching 8 activations of row (l & 15)
+//     (zero for rows >= M).  MFMA sums over k, and k is paired the same way in A and B, so
+//     the lane -> k assignment inside an instruction is free;
+//   * the decoded operand is exact: |grid| * (2s+1)/4 with the sign folded in (at most 10
+//     significant bits, so exact in fp16); the per-block d is applied once per block to the
+//     fp32 MFMA partial.  Products are therefore the exact products of the GGUF weight and
+//     the fp16 activation, accumulated in fp32;
+//   * grid magnitude and sign come from one LDS lookup per 4 weights in a 4096-entry table
+//     (sign nibble << 8 | grid index) of four fp16 values, built per workgroup from the
+//     caller's gridf buffer.
+#include "tlx_common.h"
+
+namespace {
+
+constexpr int kIq3BlockBytes = 98;
+constexpr int kTblEntries = 4096;
+constexpr int kTile = 16;
+
+enum Epi { EPI_F16 = 0, EPI_SWIGLU = 1, EPI_RESID = 2 };
+
+// entry (nib << 8 | g): grid[g][j] with the sign of bit j of nib, j = 0..3, as fp16.
+__device__ __forceinline__ void iq3_build_table(u2_t* tbl, const float* __restrict__ gridf) {
+  for (int e = threadIdx.x; e < 256 * 4; e += blockDim.x) {
+    const int g = e & 255, q = e >> 8;  // thread builds nibbles 4q..4q+3 of grid word g
+    const float4 v = reinterpret_cast<const float4*>(gridf)[g];
+    const h2_t lo = {(_Float16)v.x, (_Float16)v.y};
+    const h2_t hi = {(_Float16)v.z, (_Float16)v.w};
+    const uint32_t l = __builtin_bit_cast(uint32_t, lo), h = __builtin_bit_cast(uint32_t, hi);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t nib = 4 * q + i;
+      const uint32_t ml = ((nib & 1u) << 15) | ((nib & 2u) << 30);
+      const uint32_t mh = ((nib & 4u) << 13) | ((nib & 8u) << 28);
+      tbl[(nib << 8) | g] = u2_t{l ^ ml, h ^ mh};
+    }
+  }
+}
+
+// 8 signed grid magnitudes of one lane-chunk: q word = two grid indices, sidx = the 7-bit
+// sign field; the 8th sign is the parity of sidx.
+__device__ __forceinline__ h8_t iq3_chunk(const u2_t* tbl, uint32_t qw, uint32_t sidx) {
+  const uint32_t par = __builtin_popcount(sidx) & 1u;
+  const uint32_t i0 = ((sidx & 0xFu) << 8) | (qw & 0xFFu);
+  const uint32_t i1 = (((sidx >> 4) | (par << 3)) << 8) | ((qw >> 8) & 0xFFu);
+  const u2_t a = tbl[i0];
+  const u2_t b = tbl[i1];
+  return __builtin_bit_cast(h8_t, u4_t{a.x, a.y, b.x, b.y});
+}
+
+__device__ __forceinline__ h8_t splat8(_Float16 v) { return h8_t{v, v, v, v, v, v, v, v}; }
+
+struct Iq3Seg {
+  const uint8_t* w0;   // weights (packed rows)
+  const uint8_t* w1;   // second matrix of a pair (SwiGLU up), else null
+  void* out;           // fp16 [M][n] or fp32 [M][n]
+  const float* res;    // residual [M][n] (EPI_RESID)
+  int n;               // rows in this segment
+  int tile0;           // first workgroup of this segment
+};
+
+struct Iq3Launch {
+  Iq3Seg seg[3];
+  int nseg;
+  const float* gridf;
+  const _Float16* x;   // [M][K]
+  int M, K;
+};
+
+template <int NMAT>
+struct Iq3Regs {
+  u4_t qs[NMAT];
+  u2_t sw[NMAT];
+  uint32_t d[NMAT];
+};
+
+template <int NMAT>
+__device__ __forceinline__ void iq3_load(Iq3Regs<NMAT>& r, const uint8_t* const* rp, int nb, int b,
+                                         int kq) {
+#pragma unroll
+  for (int i = 0; i < NMAT; ++i) {
+    r.qs[i] = *reinterpret_cast<const u4_t*>(rp[i] + 64 * b + 16 * kq);
+    r.sw[i] = *reinterpret_cast<const u2_t*>(rp[i] + 64 * nb + 32 * b + 8 * kq);
+    r.d[i] = *reinterpret_cast<const uint16_t*>(rp[i] + 96 * nb + 2 * b);
+  }
+}
+
+template <int NMAT, int EPI, int WAVES>
+__global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Launch a) {
+  __shared__ u2_t tbl[kTblEntries];
+  iq3_build_table(tbl, a.gridf);
+  __syncthreads();
+
+  int s = 0;
+  while (s + 1 < a.nseg && (int)blockIdx.x >= a.seg[s + 1].tile0) ++s;
+  const Iq3Seg& sg = a.seg[s];
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, kq = lane >> 4;
+  const int K = a.K, M = a.M, nb = K >> 8;
+  const size_t rowb = (size_t)kIq3BlockBytes * nb;
+  const int row0 = ((int)blockIdx.x - sg.tile0) * kTile;
+  const int row = min(row0 + col, sg.n - 1);  // tail tile: clamp the loads, mask the stores
+
+  const uint8_t* rp[NMAT];
+  rp[0] = sg.w0 + (size_t)row * rowb;
+  if constexpr (NMAT == 2) rp[1] = sg.w1 + (size_t)row * rowb;
+
+  const bool xact = col < M;
+  const _Float16* xr = a.x + (size_t)(xact ? col : 0) * K + 64 * kq;
+
+  f4_t acc[NMAT];
+#pragma unroll
+  for (int i = 0; i < NMAT; ++i) acc[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  int b = wave;
+  Iq3Regs<NMAT> cur;
+  if (b < nb) iq3_load<NMAT>(cur, rp, nb, b, kq);
+  for (; b < nb; b += WAVES) {
+    Iq3Regs<NMAT> nxt;
+    const bool more = b + WAVES < nb;
+    if (more) iq3_load<NMAT>(nxt, rp, nb, b + WAVES, kq);
+
+    h8_t X[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      X[t] = xact ? *reinterpret_cast<const h8_t*>(xr + 256 * b + 8 * t) : splat8((_Float16)0.f);
+
+#pragma unroll
+    for (int i = 0; i < NMAT; ++i) {
+      const _Float16 ks0 = (_Float16)((float)(2u * (cur.sw[i].x >> 28) + 1u) * 0.25f);
+      const _Float16 ks1 = (_Float16)((float)(2u * (cur.sw[i].y >> 28) + 1u) * 0.25f);
+      f4_t D = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const uint32_t qd = cur.qs[i][t >> 1];
+        const uint32_t qw = (t & 1) ? (qd >> 16) : (qd & 0xFFFFu);
+        const uint32_t sw = (t < 4) ? cur.sw[i].x : cur.sw[i].y;
+        const uint32_t sidx = (sw >> (7 * (t & 3))) & 0x7Fu;
+        const h8_t B = iq3_chunk(tbl, qw, sidx) * splat8(t < 4 ? ks0 : ks1);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(X[t], B, D, 0, 0, 0);
+      }
+      const float d = tlx_h2f((uint16_t)cur.d[i]);
+      acc[i] += d * D;
+    }
+    if (more) cur = nxt;
+  }
+
+  // fixed-order split-K reduction through LDS (the table is dead after this barrier)
+  __syncthreads();
+  if constexpr (WAVES > 1) {
+    float* red = reinterpret_cast<float*>(tbl);
+    if (wave > 0) {
+#pragma unroll
+      for (int i = 0; i < NMAT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(((wave - 1) * NMAT + i) * 4 + r) * TLX_WAVE + lane] = acc[i][r];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    for (int w = 1; w < WAVES; ++w)
+#pragma unroll
+      for (int i = 0; i < NMAT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][r] += red[(((w - 1) * NMAT + i) * 4 + r) * TLX_WAVE + lane];
+  }
+
+  // lane (col, kq) holds D[m = 4*kq + r][col]
+  const int n = row0 + col;
+  if (n >= sg.n) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * kq + r;
+    if (m >= M) break;
+    const size_t o = (size_t)m * sg.n + n;
+    if constexpr (EPI == EPI_SWIGLU) {
+      reinterpret_cast<uint16_t*>(sg.out)[o] = tlx_swiglu_bits(acc[0][r], acc[1][r]);
+    } else if constexpr (EPI == EPI_RESID) {
+      reinterpret_cast<float*>(sg.out)[o] = sg.res[o] + (float)(_Float16)acc[0][r];
+    } else {
+      reinterpret_cast<uint16_t*>(sg.out)[o] = tlx_f2h_bits(acc[0][r]);
+    }
+  }
+}
+
+template <int NMAT, int EPI>
+int iq3_launch(const Iq3Launch& a, int tiles, hipStream_t st) {
+  const int nb = a.K >> 8;
+  int waves = 4;
+  while (tiles * waves < 4096 && waves < 16 && nb >= 4 * waves) waves *= 2;
+  switch (waves) {
+    case 4: iq3_gemv_kernel<NMAT, EPI, 4><<<tiles, 4 * TLX_WAVE, 0, st>>>(a); break;
+    case 8: iq3_gemv_kernel<NMAT, EPI, 8><<<tiles, 8 * TLX_WAVE, 0, st>>>(a); break;
+    default: iq3_gemv_kernel<NMAT, EPI, 16><<<tiles, 16 * TLX_WAVE, 0, st>>>(a); break;
+  }
+  return tlx_launch_status();
+}
+
+int iq3_check(const void* w, int M, int N, int K, int layout) {
+  if (M < 1 || M > TLX_MAX_M || N < 1 || K < 256 || (K & 255)) return TLX_E_ARG;
+  if (layout != TLX_LAYOUT_PACKED) return TLX_E_ARG;
+  // 16-B operand loads need dword-aligned rows: row bytes 98*NB with NB even
+  if (((K >> 8) & 1) || !tlx_aligned(w, 4)) return TLX_E_ALIGN;
+  return TLX_OK;
+}
+
+inline int tiles_of(int n) { return (n + kTile - 1) / kTile; }
+
+// ------------------------------------------------------------------ dequantization
+// One thread per lane-chunk (8 weights).  Exact fp32 arithmetic in the reference order
+// d*((sw>>28)+0.5)*0.5, then *grid, then *sign; fp16 output rounds that exact value once.
+__global__ __launch_bounds__(256) void iq3_dequant_kernel(const uint8_t* __restrict__ w,
+                                                          const float* __restrict__ gridf,
+                                                          void* __restrict__ out, int64_t rows,
+                                                          int nb, int layout, int out_f16) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // chunk index
+  const int64_t nchunk = rows * nb * 32;
+  if (c >= nchunk) return;
+  const int lc = (int)(c & 31);
+  const int64_t rb = c >> 5;  // row * nb + b
+  const int b = (int)(rb % nb);
+  const int64_t row = rb / nb;
+  uint32_t q, sw;
+  uint16_t dbits;
+  if (layout == TLX_LAYOUT_RAW) {
+    const uint8_t* blk = w + rb * kIq3BlockBytes;
+    dbits = tlx_ldu<uint16_t>(blk);
+    q = tlx_ldu<uint16_t>(blk + 2 + 2 * lc);
+    sw = tlx_ldu<uint32_t>(blk + 66 + 4 * (lc >> 2));
+  } else {
+    const uint8_t* rp = w + row * (int64_t)(kIq3BlockBytes * nb);
+    q = tlx_ldu<uint16_t>(rp + 64 * b + 2 * lc);
+    sw = tlx_ldu<uint32_t>(rp + 64 * nb + 32 * b + 4 * (lc >> 2));
+    dbits = tlx_ldu<uint16_t>(rp + 96 * nb + 2 * b);
+  }
+  const float d = tlx_h2f(dbits);
+  const float db = d * ((float)(sw >> 28) + 0.5f) * 0.5f;
+  const uint32_t sidx = (sw >> (7 * (lc & 3))) & 0x7Fu;
+  const uint32_t sbyte = sidx | ((__builtin_popcount(sidx) & 1u) << 7);
+  const float4 g0 = reinterpret_cast<const float4*>(gridf)[q & 0xFFu];
+  const float4 g1 = reinterpret_cast<const float4*>(gridf)[q >> 8];
+  const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+  const int64_t k0 = rb * 256 + 8 * lc;
+  if (out_f16) {
+    uint16_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = tlx_f2h_bits(db * g[j] * (((sbyte >> j) & 1u) ? -1.f : 1.f));
+    uint4 pk;
+    __builtin_memcpy(&pk, v, 16);
+    reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + k0)[0] = pk;
+  } else {
+    float* o = reinterpret_cast<float*>(out) + k0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = db * g[j] * (((sbyte >> j) & 1u) ? -1.f : 1.f);
+  }
+}
+
+}  // namespace
+
+extern "C" int tlx_iq3xxs_dequant(const void* w, const float* gridf, void* out, int64_t rows,
+                                  int64_t kdim, int layout, int out_f16, void* stream) {
+  TLX_RET_IF(rows < 1 || kdim < 256 || (kdim & 255), TLX_E_ARG);
+  TLX_RET_IF(layout != TLX_LAYOUT_RAW && layout != TLX_LAYOUT_PACKED, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(out, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
+  const int nb = (int)(kdim >> 8);
+  const int64_t nchunk = rows * nb * 32;
+  const int64_t grid = (nchunk + 255) / 256;
+  TLX_RET_IF(grid > 0x7fffffff, TLX_E_ARG);
+  iq3_dequant_kernel<<<(unsigned)grid, 256, 0, (hipStream_t)stream>>>(
+      (const uint8_t*)w, gridf, out, rows, nb, layout, out_f16);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_ffn8(const void* wg, const void* wu, const float* gridf, const uint16_t* hhx_f16,
+                        uint16_t* gact_f16, int M, int N, int K, int layout, void* stream) {
+  int rc = iq3_check(wg, M, N, K, layout);
+  if (rc == TLX_OK) rc = iq3_check(wu, M, N, K, layout);
+  TLX_RET_IF(rc != TLX_OK, rc);
+  TLX_RET_IF(!tlx_aligned(hhx_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
+  Iq3Launch a{};
+  a.seg[0] = Iq3Seg{(const uint8_t*)wg, (const uint8_t*)wu, gact_f16, nullptr, N, 0};
+  a.nseg = 1;
+  a.gridf = gridf;
+  a.x = (const _Float16*)hhx_f16;
+  a.M = M;
+  a.K = K;
+  return iq3_launch<2, EPI_SWIGLU>(a, tiles_of(N), (hipStream_t)stream);
+}
+
+extern "C" int tlx_down8(const void* wd, const float* gridf, const uint16_t* gact_f16,
+                         const float* hh, float* y, int M, int N, int K, int layout, void* stream) {
+  const int rc = iq3_check(wd, M, N, K, layout);
+  TLX_RET_IF(rc != TLX_OK, rc);
+  TLX_RET_IF(!tlx_aligned(gact_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
+  Iq3Launch a{};
+  a.seg[0] = Iq3Seg{(const uint8_t*)wd, nullptr, y, hh, N, 0};
+  a.nseg = 1;
+  a.gridf = gridf;
+  a.x = (const _Float16*)gact_f16;
+  a.M = M;
+  a.K = K;
+  return iq3_launch<1, EPI_RESID>(a, tiles_of(N), (hipStream_t)stream);
+}
+
+extern "C" int tlx_iq3_gemv(const void* w, const float* gridf, const uint16_t* x_f16,
+                            uint16_t* out_f16, int M, int N, int K, int layout, void* stream) {
+  const int rc = iq3_check(w, M, N, K, layout);
+  TLX_RET_IF(rc != TLX_OK, rc);
+  TLX_RET_IF(!tlx_aligned(x_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
+  Iq3Launch a{};
+  a.seg[0] = Iq3Seg{(const uint8_t*)w, nullptr, out_f16, nullptr, N, 0};
+  a.nseg = 1;
+  a.gridf = gridf;
+  a.x = (const _Float16*)x_f16;
+  a.M = M;
+  a.K = K;
+  return iq3_launch<1, EPI_F16>(a, tiles_of(N), (hipStream_t)stream);
+}
+
+extern "C" int tlx_aq3k8(const void* wq, const void* wk, const void* wv, const float* gridf,
+                         const uint16_t* xh_f16, uint16_t* qrow_f16, uint16_t* krow_f16,
+                         uint16_t* vrow_f16, int M, int Nq, int Nk, int Nv, int K, int layout,
+                         void* stream) {
+  int rc = iq3_check(wq, M, Nq, K, layout);
+  if (rc == TLX_OK) rc = iq3_check(wk, M, Nk, K, layout);
+  if (rc == TLX_OK) rc = iq3_check(wv, M, Nv, K, layout);
+  TLX_RET_IF(rc != TLX_OK, rc);
+  TLX_RET_IF(!tlx_aligned(xh_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
+  Iq3Launch a{};
+  const int tq = tiles_of(Nq), tk = tiles_of(Nk), tv = tiles_of(Nv);
+  a.seg[0] = Iq3Seg{(const uint8_t*)wq, nullptr, qrow_f16, nullptr, Nq, 0};
+  a.seg[1] = Iq3Seg{(const uint8_t*)wk, nullptr, krow_f16, nullptr, Nk, tq};
+  a.seg[2] = Iq3Seg{(const uint8_t*)wv, nullptr, vrow_f16, nullptr, Nv, tq + tk};
+  a.nseg = 3;
+  a.gridf = gridf;
+  a.x = (const _Float16*)xh_f16;
+  a.M = M;
+  a.K = K;
+  return iq3_launch<1, EPI_F16>(a, tq + tk + tv, (hipStream_t)stream);
+}

@@ -1,0 +1,131 @@
+// Q6_K kernels for gfx950: bit-exact dequantization (raw 210-B and padded 212-B blocks) and
+// the fp32-activation GEMV (the h6k2048 contract, engine/mm/MM_P34_h6k2048.cu:8-52).
+//
+// GEMV design (fp32 x, fp32 y -- a VALU kernel; fp32 activations do not fit the fp16 MFMA
+// operand without rounding them):
+//   * a workgroup of 4 waves owns 4 consecutive rows; every wave covers all 4 rows (one per
+//     16-lane quarter) and the waves split the K blocks (block b -> wave b % 4);
+//   * within a quarter, lane i owns half h = i >> 3 and the l-quad p = i & 7 of a block,
+//     i.e. the 16 weights k = 128h + 32g + 4p + j (g, j = 0..3): one dword each of
+//     ql[64h+4p], ql[64h+32+4p], qh[32h+4p] decodes all 16 with byte-parallel masks;
+//   * per (lane, g) the four products x*(q-32) are summed, then scaled once by d*sc[g]
+//     (the 4 weights share one 16-element scale group);
+//   * a 16-lane butterfly then a fixed-order LDS sum over the 4 waves finish the row.
+#include "tlx_common.h"
+
+namespace {
+
+constexpr int kQ6Raw = 210;
+constexpr int kQ6Pad = 212;
+
+struct Q6Off {  // byte offsets of the fields inside one block
+  int ql, qh, sc, d;
+};
+
+__device__ __forceinline__ Q6Off q6_offsets(int layout) {
+  return layout == TLX_LAYOUT_RAW ? Q6Off{0, 128, 192, 208} : Q6Off{20, 148, 4, 2};
+}
+
+// ------------------------------------------------------------------ dequantization
+// One thread per (row, block, l in 0..31, h in 0..1): 4 outputs k = 128h + 32g + l.
+__global__ __launch_bounds__(256) void q6k_dequant_kernel(const uint8_t* __restrict__ w,
+                                                          void* __restrict__ out, int64_t nblk,
+                                                          int layout, int out_f16) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= nblk * 64) return;
+  const int64_t blkid = t >> 6;
+  const int l = (int)(t & 31), h = (int)((t >> 5) & 1);
+  const int bs = layout == TLX_LAYOUT_RAW ? kQ6Raw : kQ6Pad;
+  const Q6Off o = q6_offsets(layout);
+  const uint8_t* blk = w + blkid * bs;
+  const float d = tlx_h2f(tlx_ldu<uint16_t>(blk + o.d));
+  const int qa = blk[o.ql + 64 * h + l], qb = blk[o.ql + 64 * h + l + 32];
+  const int hb = blk[o.qh + 32 * h + l];
+  const int q[4] = {(qa & 0xF) | ((hb & 3) << 4), (qb & 0xF) | (((hb >> 2) & 3) << 4),
+                    (qa >> 4) | (((hb >> 4) & 3) << 4), (qb >> 4) | (((hb >> 6) & 3) << 4)};
+  const int64_t k0 = blkid * 256 + 128 * h + l;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float sc = (float)(int8_t)blk[o.sc + 8 * h + (l >> 4) + 2 * g];
+    const float v = (d * sc) * (float)(q[g] - 32);
+    if (out_f16)
+      reinterpret_cast<uint16_t*>(out)[k0 + 32 * g] = tlx_f2h_bits(v);
+    else
+      reinterpret_cast<float*>(out)[k0 + 32 * g] = v;
+  }
+}
+
+// ------------------------------------------------------------------ fp32 GEMV
+__global__ __launch_bounds__(256) void q6k_gemv_f32_kernel(const uint8_t* __restrict__ w,
+                                                           const float* __restrict__ x,
+                                                           float* __restrict__ y, int rows,
+                                                           int K, int layout) {
+  __shared__ float red[3][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int quarter = lane >> 4, i = lane & 15;
+  const int h = i >> 3, p = i & 7;
+  const int nb = K >> 8;
+  const int bs = layout == TLX_LAYOUT_RAW ? kQ6Raw : kQ6Pad;
+  const Q6Off o = q6_offsets(layout);
+  const int row = min((int)blockIdx.x * 4 + quarter, rows - 1);
+  const uint8_t* rp = w + (size_t)row * bs * nb;
+
+  float acc = 0.f;
+  for (int b = wave; b < nb; b += 4) {
+    const uint8_t* blk = rp + (size_t)b * bs;
+    const uint32_t qla = tlx_ldu<uint32_t>(blk + o.ql + 64 * h + 4 * p);
+    const uint32_t qlb = tlx_ldu<uint32_t>(blk + o.ql + 64 * h + 32 + 4 * p);
+    const uint32_t qh = tlx_ldu<uint32_t>(blk + o.qh + 32 * h + 4 * p);
+    const uint64_t sc8 = tlx_ldu<uint64_t>(blk + o.sc + 8 * h);
+    const float d = tlx_h2f(tlx_ldu<uint16_t>(blk + o.d));
+    const float* xb = x + 256 * b + 128 * h + 4 * p;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 xv = *reinterpret_cast<const float4*>(xb + 32 * g);
+      const uint32_t lo = (((g & 1) ? qlb : qla) >> ((g >> 1) * 4)) & 0x0F0F0F0Fu;
+      const uint32_t q = lo | (((qh >> (2 * g)) & 0x03030303u) << 4);
+      float s = xv.x * (float)((int)(q & 0xFF) - 32);
+      s += xv.y * (float)((int)((q >> 8) & 0xFF) - 32);
+      s += xv.z * (float)((int)((q >> 16) & 0xFF) - 32);
+      s += xv.w * (float)((int)(q >> 24) - 32);
+      const float sc = (float)(int8_t)(uint8_t)(sc8 >> (8 * ((p >> 2) + 2 * g)));
+      acc += (d * sc) * s;
+    }
+  }
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 16);
+  if (wave > 0 && i == 0) red[wave - 1][quarter] = acc;
+  __syncthreads();
+  if (wave == 0 && i == 0) {
+    acc += red[0][quarter];
+    acc += red[1][quarter];
+    acc += red[2][quarter];
+    const int r = (int)blockIdx.x * 4 + quarter;
+    if (r < rows) y[r] = acc;
+  }
+}
+
+}  // namespace
+
+extern "C" int tlx_q6k_dequant(const void* w, void* out, int64_t rows, int64_t kdim, int layout,
+                               int out_f16, void* stream) {
+  TLX_RET_IF(rows < 1 || kdim < 256 || (kdim & 255), TLX_E_ARG);
+  TLX_RET_IF(layout != TLX_LAYOUT_RAW && layout != TLX_LAYOUT_PACKED, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(w, 2) || !tlx_aligned(out, 4), TLX_E_ALIGN);
+  const int64_t nblk = rows * (kdim >> 8);
+  const int64_t grid = (nblk * 64 + 255) / 256;
+  TLX_RET_IF(grid > 0x7fffffff, TLX_E_ARG);
+  q6k_dequant_kernel<<<(unsigned)grid, 256, 0, (hipStream_t)stream>>>((const uint8_t*)w, out, nblk,
+                                                                        layout, out_f16);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_q6k_gemv(const void* w, const float* x, float* y, int rows, int K, int layout,
+                            void* stream) {
+  TLX_RET_IF(rows < 1 || K < 256 || (K & 255), TLX_E_ARG);
+  TLX_RET_IF(layout != TLX_LAYOUT_RAW && layout != TLX_LAYOUT_PACKED, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(w, 4) || !tlx_aligned(x, 16), TLX_E_ALIGN);
+  q6k_gemv_f32_kernel<<<(rows + 3) / 4, 256, 0, (hipStream_t)stream>>>((const uint8_t*)w, x, y,
+                                                                        rows, K, layout);
+  return tlx_launch_status();
+}

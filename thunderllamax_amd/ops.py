@@ -1,0 +1,100 @@
+"""Python mirror of the reference's kernel call sites, running on libtlx_hip.
+
+Each function keeps the reference kernel's name and positional argument order
+(``ffn8(wg, wu, gridf, hhx, gact)`` etc., /root/reference/engine/ffn8.cu:134-136) and takes
+torch tensors on the GPU.  Sizes the reference bakes into kernel names (M, N, K) are read
+from the tensor shapes.  Like the reference, the output buffers are caller-owned; nothing is
+allocated here.  Errors raise ``TlxError`` (the reference asserts in Python).
+"""
+import torch
+
+from ._lib import LAYOUT_PACKED, LAYOUT_RAW, call
+
+_F16 = torch.float16
+
+
+def _stream(stream):
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    return getattr(stream, "cuda_stream", stream)
+
+
+def _dev(*ts):
+    for t in ts:
+        if not (t.is_cuda and t.is_contiguous()):
+            raise ValueError("all buffers must be contiguous tensors on the GPU")
+
+
+def _mk(x):
+    """[K] or [M, K] activations -> M."""
+    return 1 if x.dim() == 1 else x.shape[0]
+
+
+# ------------------------------------------------------------------ dequantization
+def iq3xxs_dequant(w, gridf, out, kdim, layout=LAYOUT_PACKED, stream=None):
+    _dev(w, gridf, out)
+    rows = w.numel() // (98 * (kdim // 256))
+    call("tlx_iq3xxs_dequant", w.data_ptr(), gridf.data_ptr(), out.data_ptr(), rows, kdim, layout,
+         int(out.dtype == _F16), _stream(stream))
+    return out
+
+
+def q6k_dequant(w, out, kdim, layout=LAYOUT_RAW, stream=None):
+    _dev(w, out)
+    bs = 210 if layout == LAYOUT_RAW else 212
+    rows = w.numel() // (bs * (kdim // 256))
+    call("tlx_q6k_dequant", w.data_ptr(), out.data_ptr(), rows, kdim, layout, int(out.dtype == _F16),
+         _stream(stream))
+    return out
+
+
+def iq4xs_dequant(w, iq4nl, out, kdim, stream=None):
+    _dev(w, iq4nl, out)
+    rows = w.numel() // (136 * (kdim // 256))
+    call("tlx_iq4xs_dequant", w.data_ptr(), iq4nl.data_ptr(), out.data_ptr(), rows, kdim, _stream(stream))
+    return out
+
+
+# ------------------------------------------------------------------ decode GEMVs
+def ffn8(wg, wu, gridf, hhx, gact, layout=LAYOUT_PACKED, stream=None):
+    """gact[m] = silu16(half(Wg·hhx[m])) * half(Wu·hhx[m])   (ffn8 / ffn8v{M})."""
+    _dev(wg, wu, gridf, hhx, gact)
+    M, K, N = _mk(hhx), hhx.shape[-1], gact.shape[-1]
+    call("tlx_ffn8", wg.data_ptr(), wu.data_ptr(), gridf.data_ptr(), hhx.data_ptr(), gact.data_ptr(),
+         M, N, K, layout, _stream(stream))
+    return gact
+
+
+def down8(wd, gridf, gact, hh, y, layout=LAYOUT_PACKED, stream=None):
+    """y[m] = hh[m] + float(half(Wd·gact[m]))   (down8 / down8nw32_{M})."""
+    _dev(wd, gridf, gact, hh, y)
+    M, K, N = _mk(gact), gact.shape[-1], y.shape[-1]
+    call("tlx_down8", wd.data_ptr(), gridf.data_ptr(), gact.data_ptr(), hh.data_ptr(), y.data_ptr(),
+         M, N, K, layout, _stream(stream))
+    return y
+
+
+def iq3_gemv(w, gridf, x, out, layout=LAYOUT_PACKED, stream=None):
+    """out[m] = half(W·x[m])   (the IQ3ROWP segment body)."""
+    _dev(w, gridf, x, out)
+    M, K, N = _mk(x), x.shape[-1], out.shape[-1]
+    call("tlx_iq3_gemv", w.data_ptr(), gridf.data_ptr(), x.data_ptr(), out.data_ptr(), M, N, K, layout,
+         _stream(stream))
+    return out
+
+
+def aq3k8(wq, wk, wv, gridf, xh, qrow, krow, vrow, layout=LAYOUT_PACKED, stream=None):
+    """Fused q/k/v IQ3_XXS projections in one launch   (aq3k8 / aq3k8v{M})."""
+    _dev(wq, wk, wv, gridf, xh, qrow, krow, vrow)
+    M, K = _mk(xh), xh.shape[-1]
+    call("tlx_aq3k8", wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), gridf.data_ptr(), xh.data_ptr(),
+         qrow.data_ptr(), krow.data_ptr(), vrow.data_ptr(), M, qrow.shape[-1], krow.shape[-1],
+         vrow.shape[-1], K, layout, _stream(stream))
+
+
+def h6k_gemv(w, x, y, layout=LAYOUT_RAW, stream=None):
+    """y = W·x, Q6_K weights, fp32 x and y   (h6k2048 contract)."""
+    _dev(w, x, y)
+    call("tlx_q6k_gemv", w.data_ptr(), x.data_ptr(), y.data_ptr(), y.numel(), x.numel(), layout,
+         _stream(stream))
+    return y
