@@ -10,8 +10,9 @@
 //     two scale/sign words, one 2-B load of the block's d;
 //   * each of the 8 lane-chunks (8 weights) becomes the B operand of one
 //     v_mfma_f32_16x16x32_f16; the A operand is the matching 8 activations of row (l & 15)
-//     (zero for rows >= M).  MFMA sums over k, and k is paired the same way in A and B, so
-//     the lane -> k assignment inside an instruction is free;
+//     (rows >= M load a valid row; their outputs are never stored).  MFMA sums over k, and k
+//     is paired the same way in A and B, so the lane -> k assignment inside an instruction
+//     is free;
 //   * the decoded operand is exact: |grid| * (2s+1)/4 with the sign folded in (at most 10
 //     significant bits, so exact in fp16); the per-block d is applied once per block to the
 //     fp32 MFMA partial.  Products are therefore the exact products of the GGUF weight and
@@ -84,14 +85,16 @@ struct Iq3Regs {
   uint32_t d[NMAT];
 };
 
+// Loads one block of the lane's row: 16 B of grid indices, 8 B of scale/sign words, the d.
+// Offsets are 32-bit (a matrix is < 4 GiB) from the matrix base.
 template <int NMAT>
-__device__ __forceinline__ void iq3_load(Iq3Regs<NMAT>& r, const uint8_t* const* rp, int nb, int b,
-                                         int kq) {
+__device__ __forceinline__ void iq3_load(Iq3Regs<NMAT>& r, const uint8_t* const* base, uint32_t qoff,
+                                         uint32_t soff, uint32_t doff, int b) {
 #pragma unroll
   for (int i = 0; i < NMAT; ++i) {
-    r.qs[i] = *reinterpret_cast<const u4_t*>(rp[i] + 64 * b + 16 * kq);
-    r.sw[i] = *reinterpret_cast<const u2_t*>(rp[i] + 64 * nb + 32 * b + 8 * kq);
-    r.d[i] = *reinterpret_cast<const uint16_t*>(rp[i] + 96 * nb + 2 * b);
+    r.qs[i] = *reinterpret_cast<const u4_t*>(base[i] + qoff + 64u * b);
+    r.sw[i] = *reinterpret_cast<const u2_t*>(base[i] + soff + 32u * b);
+    r.d[i] = *reinterpret_cast<const uint16_t*>(base[i] + doff + 2u * b);
   }
 }
 
@@ -108,16 +111,19 @@ __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Lau
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kq = lane >> 4;
   const int K = a.K, M = a.M, nb = K >> 8;
-  const size_t rowb = (size_t)kIq3BlockBytes * nb;
+  const uint32_t rowb = (uint32_t)kIq3BlockBytes * nb;
   const int row0 = ((int)blockIdx.x - sg.tile0) * kTile;
-  const int row = min(row0 + col, sg.n - 1);  // tail tile: clamp the loads, mask the stores
+  // tail tile: clamp the loads, mask the stores
+  const uint32_t roff = (uint32_t)min(row0 + col, sg.n - 1) * rowb;
+  const uint32_t qoff = roff + 16u * kq, soff = roff + 64u * nb + 8u * kq, doff = roff + 96u * nb;
 
-  const uint8_t* rp[NMAT];
-  rp[0] = sg.w0 + (size_t)row * rowb;
-  if constexpr (NMAT == 2) rp[1] = sg.w1 + (size_t)row * rowb;
+  const uint8_t* base[NMAT];
+  base[0] = sg.w0;
+  if constexpr (NMAT == 2) base[1] = sg.w1;
 
-  const bool xact = col < M;
-  const _Float16* xr = a.x + (size_t)(xact ? col : 0) * K + 64 * kq;
+  // Activation rows >= M only reach output rows that are never stored, so those lanes load a
+  // valid row instead of being masked: no branches, and the wait counters stay exact.
+  const _Float16* xr = a.x + (size_t)min(col, M - 1) * K + 64 * kq;
 
   f4_t acc[NMAT];
 #pragma unroll
@@ -125,16 +131,16 @@ __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Lau
 
   int b = wave;
   Iq3Regs<NMAT> cur;
-  if (b < nb) iq3_load<NMAT>(cur, rp, nb, b, kq);
+  if (b < nb) iq3_load<NMAT>(cur, base, qoff, soff, doff, b);
   for (; b < nb; b += WAVES) {
-    Iq3Regs<NMAT> nxt;
-    const bool more = b + WAVES < nb;
-    if (more) iq3_load<NMAT>(nxt, rp, nb, b + WAVES, kq);
-
+    // this block's activations first, then the next block's weights: waiting for the
+    // activations leaves the weight prefetch in flight
     h8_t X[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
-      X[t] = xact ? *reinterpret_cast<const h8_t*>(xr + 256 * b + 8 * t) : splat8((_Float16)0.f);
+    for (int t = 0; t < 8; ++t) X[t] = *reinterpret_cast<const h8_t*>(xr + 256 * b + 8 * t);
+    Iq3Regs<NMAT> nxt;
+    const bool more = b + WAVES < nb;
+    if (more) iq3_load<NMAT>(nxt, base, qoff, soff, doff, b + WAVES);
 
 #pragma unroll
     for (int i = 0; i < NMAT; ++i) {
