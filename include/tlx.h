@@ -85,6 +85,29 @@ int tlx_aq3k8(const void* wq, const void* wk, const void* wv, const float* gridf
 int tlx_q6k_gemv(const void* w, const float* x, float* y, int rows, int K, int layout,
                  void* stream);
 
+/* ---- prefill dequant-GEMM (M rows of a prompt chunk, MFMA fp16 x fp16 -> fp32) ----
+ * x16 is M x K fp16 row-major; W is N packed IQ3_XXS rows.  M % 256 == 0, K % 512 == 0,
+ * 16-byte aligned buffers.  Each output element is one fp32 MFMA sum over k of
+ * x[m][k] * half(W[n][k]); its k order differs from the reference's mma.sync order, so
+ * results agree to rounding (relative error <= 1e-3), not bitwise. */
+
+/* FFN gate+up fused with SwiGLU: out16[m][n] = hsilu(half(g)) * half(u), N % 128 == 0.
+ * Replaces pf_gemm3 with FFN=1 (engine/pf_gemm3.cu:313-323, epilogue :415-420):
+ * kernel(w1, w2, gridf, x16, out16). */
+int tlx_pfg3_ffn(const void* wg, const void* wu, const float* gridf, const uint16_t* x16,
+                 uint16_t* out16, int M, int N, int K, int layout, void* stream);
+
+/* Residual GEMM (down / o projection): out32[m][n] = res[m][n] + acc, N % 256 == 0.
+ * Replaces pf_gemm3 with RES=1 (engine/pf_gemm3.cu:313-323, epilogue :410-414):
+ * kernel(w1, gridf, x16, res16, out32). */
+int tlx_pfg3_iq3d(const void* w, const float* gridf, const uint16_t* x16, const float* res,
+                  float* out32, int M, int N, int K, int layout, void* stream);
+
+/* Plain GEMM with fp16 output: out16[m][n] = half(acc), N % 256 == 0.
+ * Replaces pf_gemm3 with FFN=0, RES=0 (engine/pf_gemm3.cu:313-323, epilogue :421-423). */
+int tlx_pfg3_iq3o(const void* w, const float* gridf, const uint16_t* x16, uint16_t* out16,
+                  int M, int N, int K, int layout, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,6 +82,24 @@ def iq3_gemv_fp16_products(W16, x16):
     return out
 
 
+def pf_ffn_ref(Wg, Wu, x16):
+    """pf_gemm3 FFN=1 epilogue ``hmul(hsilu_h(half(g)), half(u))``
+    (/root/reference/engine/pf_gemm3.cu:87-89, :415-420): the ffn8 epilogue on M rows."""
+    return ffn8_ref(Wg, Wu, x16)
+
+
+def pf_res_ref(W, x16, res):
+    """pf_gemm3 RES=1 epilogue ``out32 = res16 + acc`` -- fp32, no half rounding of acc
+    (/root/reference/engine/pf_gemm3.cu:410-414) -> (acc float64, out float32)."""
+    acc = matvec64(W, x16)
+    return acc, (np.asarray(res, dtype=np.float64) + acc).astype(np.float32)
+
+
+def pf_o_ref(W, x16):
+    """pf_gemm3 plain epilogue ``out16 = half(acc)`` (/root/reference/engine/pf_gemm3.cu:421-423)."""
+    return gemv16_ref(W, x16)
+
+
 def rel_err(y, ref):
     """Norm-wise relative error ||y - ref|| / ||ref|| (float64)."""
     y = np.asarray(y, dtype=np.float64)

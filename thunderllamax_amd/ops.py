@@ -98,3 +98,32 @@ def h6k_gemv(w, x, y, layout=LAYOUT_RAW, stream=None):
     call("tlx_q6k_gemv", w.data_ptr(), x.data_ptr(), y.data_ptr(), y.numel(), x.numel(), layout,
          _stream(stream))
     return y
+
+
+# ------------------------------------------------------------------ prefill dequant-GEMMs
+def pfg3_ffn(wg, wu, gridf, x16, out16, layout=LAYOUT_PACKED, stream=None):
+    """out16[m] = silu16(half(Wg·x16[m])) * half(Wu·x16[m]) over a prompt chunk
+    (pf_gemm3 FFN=1: kernel(w1, w2, gridf, x16, out16))."""
+    _dev(wg, wu, gridf, x16, out16)
+    M, K, N = x16.shape[0], x16.shape[1], out16.shape[1]
+    call("tlx_pfg3_ffn", wg.data_ptr(), wu.data_ptr(), gridf.data_ptr(), x16.data_ptr(), out16.data_ptr(),
+         M, N, K, layout, _stream(stream))
+    return out16
+
+
+def pfg3_iq3d(w, gridf, x16, res16, out32, layout=LAYOUT_PACKED, stream=None):
+    """out32[m] = res16[m] + W·x16[m]   (pf_gemm3 RES=1: kernel(w1, gridf, x16, res16, out32))."""
+    _dev(w, gridf, x16, res16, out32)
+    M, K, N = x16.shape[0], x16.shape[1], out32.shape[1]
+    call("tlx_pfg3_iq3d", w.data_ptr(), gridf.data_ptr(), x16.data_ptr(), res16.data_ptr(), out32.data_ptr(),
+         M, N, K, layout, _stream(stream))
+    return out32
+
+
+def pfg3_iq3o(w, gridf, x16, out16, layout=LAYOUT_PACKED, stream=None):
+    """out16[m] = half(W·x16[m])   (pf_gemm3 plain: kernel(w1, gridf, x16, out16))."""
+    _dev(w, gridf, x16, out16)
+    M, K, N = x16.shape[0], x16.shape[1], out16.shape[1]
+    call("tlx_pfg3_iq3o", w.data_ptr(), gridf.data_ptr(), x16.data_ptr(), out16.data_ptr(), M, N, K, layout,
+         _stream(stream))
+    return out16
