@@ -5,20 +5,24 @@
 //            F16  out16[m][n] = half(acc)
 //
 // Design:
-//   * workgroup tile 256 (m) x 256 (n): for FFN the 256 n are 128 gate + 128 up rows of one
-//     n-range, so a lane holds g and u of the same output element;
-//   * 4 waves (one per SIMD, so each owns 512 registers), wave (wm, wn) computes m [128wm, +128)
+//   * workgroup tile 256 (m) x 256 (n) x 32 (k) per step; for FFN the 256 n are 128 gate + 128
+//     up rows of one n-range, so a lane holds g and u of the same output element;
+//   * 4 waves (one per SIMD, so each owns 512 registers); wave (wm, wn) computes m [128wm, +128)
 //     x 128 n (FFN: 64 gate + 64 up columns of one n-range) with v_mfma_f32_16x16x32_f16,
-//     64 MFMAs per K-step; K-step = 32 = one IQ3 sub-block;
-//   * activations stream into a 3-deep LDS ring with direct global->LDS 16-B loads issued two
-//     steps ahead; each wave waits only for the step it needs (vmcnt), so later loads stay in
-//     flight; the next 256-k block of weights is prefetched into registers;
-//   * weights are dequantized to the reference's fp16 values, fp16((+-g*(2s+1)/4) * d) =
-//     fp16(db*g) (the first product is exact in fp16, the second rounds once), into a
-//     double-buffered LDS tile [256 n][32 k]; the sign-folded grid table is the one the GEMV
-//     uses;
-//   * workgroup w runs on XCD w % 8; the m-tile is taken from w % 8 so every XCD reuses one
-//     activation slice from its own L2.
+//     64 MFMAs per step into 256 accumulator registers;
+//   * A and B tiles sit in LDS in fragment order: the 16-B piece p (8 k) of tile row R is at
+//     ((R / 16) * 64 + p * 16 + R % 16) * 16 bytes, so the MFMA operand of lane l for a 16-row
+//     group is 16 bytes at l * 16 -- every operand read is one lane-linear, bank-conflict-free
+//     1 KB; a direct global->LDS load of 16 rows x 64 B lands in the same order;
+//   * activations stream into a 3-deep ring two steps ahead; weights are staged raw (half-blocks
+//     of 4 sub-blocks, 3-deep ring, one direct load per wave per step) and dequantized one
+//     sub-block ahead into a double-buffered B tile, to the reference's fp16 values
+//     fp16((+-g*(2s+1)/4) * d) = fp16(db*g) (the first product is exact in fp16, the second
+//     rounds once) via the sign-folded grid table the GEMV uses;
+//   * one barrier per step; the step's operand loads come first, then the producers of later
+//     steps, which the compiler interleaves with the step's MFMAs;
+//   * workgroup w runs on XCD w % 8; when M is a multiple of 2048 each XCD sweeps the n-tiles
+//     of one m-tile at a time, so its L2 keeps that activation slice.
 #include "tlx_common.h"
 
 namespace {
@@ -26,17 +30,21 @@ namespace {
 constexpr int kBM = 256, kBN = 256, kBK = 32;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * TLX_WAVE;
+constexpr int kTile = kBM * kBK;          // halfs per A or B tile
 
 enum PfEpi { PF_FFN = 0, PF_RES = 1, PF_F16 = 2 };
 
 struct __attribute__((aligned(16))) PfLds {
   uint32_t tbl[4096 * 2];                 // sign-folded grid table, 4 fp16 per entry
-  _Float16 a[3][kBM * kBK];               // activation ring, [m][32 k]
-  _Float16 b[2][kBN * kBK];               // dequantized weights, [n][32 k]
-  uint8_t wq[kBN * 64];                   // raw weight block being staged: grid indices
-  uint8_t ws[kBN * 32];                   //   scale/sign words
-  uint32_t wd[kBN];                       //   the aligned d pair holding d (blocks 2i, 2i+1)
+  _Float16 a[3][kTile];                   // activation ring, fragment order
+  _Float16 b[2][kTile];                   // dequantized weights, fragment order
+  uint8_t wq[3][kBN * 32];                // raw half-blocks (4 sub-blocks): grid indices
+  uint8_t ws[3][kBN * 16];                //   scale/sign words
+  uint32_t wd[3][kBN];                    //   the aligned d pair holding d (blocks 2i, 2i+1)
 };
+
+// fragment-order offset (halfs) of piece p of tile row R
+__device__ __forceinline__ int pf_frag(int R, int p) { return ((R >> 4) * 64 + p * 16 + (R & 15)) * 8; }
 
 __device__ __forceinline__ void pf_build_table(uint32_t* tbl, const float* __restrict__ gridf) {
   for (int e = threadIdx.x; e < 256 * 4; e += blockDim.x) {
@@ -54,122 +62,190 @@ __device__ __forceinline__ void pf_build_table(uint32_t* tbl, const float* __res
   }
 }
 
-// One weight row's 256-k block: 64 B of grid indices, the 8 scale/sign words, d.
-struct PfW {
-  uint32_t q[16];
-  u4_t s[2];
-  uint32_t d;
-};
-
-// Stage block b of the tile's 256 weight rows into LDS with direct loads: 1024 16-B index
-// pieces, 512 16-B scale pieces and 256 dwords holding d = 28 wave-loads, 7 per wave.  The d
-// words are the dword-aligned pairs (block b & ~1, b | 1) -- rows are dword-aligned since NB
-// is even -- because a sub-dword direct load still spaces lanes 4 bytes apart in LDS.
-__device__ __forceinline__ void pf_dma_w(PfLds& L, const uint8_t* __restrict__ w1, const uint8_t* __restrict__ w2,
-                                         bool ffn, int nt, size_t rowb, int nb, int b, int wave, int lane) {
-#pragma unroll
-  for (int j = 0; j < 7; ++j) {
-    const int ins = 7 * wave + j;              // 0..27; 0..15 qs, 16..23 sw, 24..27 d
-    int row, off, size;
-    __attribute__((address_space(3))) void* dst;
-    if (ins < 16) {
-      row = 16 * ins + (lane >> 2); off = 64 * b + 16 * (lane & 3); size = 16;
-      dst = (__attribute__((address_space(3))) void*)(L.wq + 1024 * ins);
-    } else if (ins < 24) {
-      row = 32 * (ins - 16) + (lane >> 1); off = 64 * nb + 32 * b + 16 * (lane & 1); size = 16;
-      dst = (__attribute__((address_space(3))) void*)(L.ws + 1024 * (ins - 16));
-    } else {
-      row = 64 * (ins - 24) + lane; off = 96 * nb + 4 * (b >> 1); size = 4;
-      dst = (__attribute__((address_space(3))) void*)(L.wd + 64 * (ins - 24));
-    }
-    const uint8_t* src;
-    if (ffn) src = (row < 128 ? w1 : w2) + (size_t)(nt * 128 + (row & 127)) * rowb + off;
-    else src = w1 + (size_t)(nt * kBN + row) * rowb + off;
-    if (size == 16) __builtin_amdgcn_global_load_lds((const void*)src, dst, 16, 0, 0);
-    else __builtin_amdgcn_global_load_lds((const void*)src, dst, 4, 0, 0);
+// One of the 16 wave-loads that stage half-block hb (block hb/2, sub-blocks 4(hb&1)..+3) of the
+// tile's 256 weight rows into buffer `buf` with direct global->LDS loads.  Role 0/1: load
+// 4*role + idx of the 16-B grid-index pieces (32 rows x 2 each); role 2: load idx of the 16-B
+// scale/sign pieces (64 rows each); role 3: load idx of the d dwords (64 rows each).  The d
+// words are the dword-aligned pairs (block & ~1, block | 1) -- rows are dword-aligned since NB
+// is even -- because a sub-dword direct load still spaces lanes 4 bytes apart in LDS.  `role`
+// and `idx` are wave-uniform.
+__device__ __forceinline__ void pf_dma_w(PfLds& L, int buf, const uint8_t* __restrict__ w1,
+                                         const uint8_t* __restrict__ w2, bool ffn, int nt, uint32_t rowb,
+                                         int nb, int hb, int role, int idx, int lane) {
+  const int blk = hb >> 1, half = hb & 1;
+  int row;
+  uint32_t off;
+  uint8_t* dst;
+  if (role < 2) {
+    const int q = 4 * role + idx;
+    row = 32 * q + (lane >> 1);
+    off = 64 * blk + 32 * half + 16 * (lane & 1);
+    dst = L.wq[buf] + 1024 * q;
+  } else if (role == 2) {
+    row = 64 * idx + lane;
+    off = 64 * nb + 32 * blk + 16 * half;
+    dst = L.ws[buf] + 1024 * idx;
+  } else {
+    row = 64 * idx + lane;
+    off = 96 * nb + 4 * (blk >> 1);
+    dst = reinterpret_cast<uint8_t*>(L.wd[buf] + 64 * idx);
   }
+  const uint8_t* src;
+  if (ffn) src = (row < 128 ? w1 : w2) + (size_t)(nt * 128 + (row & 127)) * rowb + off;
+  else src = w1 + (size_t)(nt * kBN + row) * rowb + off;
+  auto* d3 = (__attribute__((address_space(3))) void*)dst;
+  if (role == 3) __builtin_amdgcn_global_load_lds((const void*)src, d3, 4, 0, 0);
+  else __builtin_amdgcn_global_load_lds((const void*)src, d3, 16, 0, 0);
 }
 
-__device__ __forceinline__ void pf_read_w(PfW& w, const PfLds& L, int r, int b) {
-  const u4_t* q = reinterpret_cast<const u4_t*>(L.wq + 64 * r);
+// All 16 loads of half-block hb, 4 per wave (prologue).
+__device__ __forceinline__ void pf_dma_w_all(PfLds& L, int buf, const uint8_t* __restrict__ w1,
+                                             const uint8_t* __restrict__ w2, bool ffn, int nt, uint32_t rowb,
+                                             int nb, int hb, int wave, int lane) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const u4_t v = q[i];
-    w.q[4 * i] = v.x; w.q[4 * i + 1] = v.y; w.q[4 * i + 2] = v.z; w.q[4 * i + 3] = v.w;
-  }
-  w.s[0] = *reinterpret_cast<const u4_t*>(L.ws + 32 * r);
-  w.s[1] = *reinterpret_cast<const u4_t*>(L.ws + 32 * r + 16);
-  w.d = L.wd[r] >> (16 * (b & 1));
+  for (int role = 0; role < 4; ++role) pf_dma_w(L, buf, w1, w2, ffn, nt, rowb, nb, hb, role, wave, lane);
 }
 
-// Dequantize sub-block S (32 weights) of the thread's row into dst (32 fp16).
-template <int S>
-__device__ __forceinline__ void pf_dequant(const PfW& w, const uint32_t* tbl, _Float16* dst) {
-  const uint32_t sw = w.s[S >> 2][S & 3];
+// Dequantize sub-block u (32 weights) of tile row r into the B tile.
+__device__ __forceinline__ void pf_dequant(const PfLds& L, _Float16* bt, int r, int u) {
+  const int buf = (u >> 2) % 3, k = u & 3;
+  const u2_t qd = *reinterpret_cast<const u2_t*>(L.wq[buf] + 32 * r + 8 * k);
+  const uint32_t sw = *reinterpret_cast<const uint32_t*>(L.ws[buf] + 16 * r + 4 * k);
+  const uint32_t dd = L.wd[buf][r] >> (16 * ((u >> 3) & 1));
   const _Float16 ks = (_Float16)((float)(2u * (sw >> 28) + 1u) * 0.25f);
-  const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)w.d);
+  const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)dd);
   const h8_t kv = {ks, ks, ks, ks, ks, ks, ks, ks};
   const h8_t dv = {d, d, d, d, d, d, d, d};
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const uint32_t qd = w.q[2 * S + (c >> 1)];
-    const uint32_t qw = (c & 1) ? (qd >> 16) : (qd & 0xFFFFu);
+    const uint32_t qw = (c & 1) ? (qd[c >> 1] >> 16) : (qd[c >> 1] & 0xFFFFu);
     const uint32_t sidx = (sw >> (7 * c)) & 0x7Fu;
     const uint32_t par = __builtin_popcount(sidx) & 1u;
     const uint32_t i0 = ((sidx & 0xFu) << 8) | (qw & 0xFFu);
     const uint32_t i1 = (((sidx >> 4) | (par << 3)) << 8) | ((qw >> 8) & 0xFFu);
-    const u2_t e0 = *reinterpret_cast<const u2_t*>(tbl + 2 * i0);
-    const u2_t e1 = *reinterpret_cast<const u2_t*>(tbl + 2 * i1);
+    const u2_t e0 = *reinterpret_cast<const u2_t*>(L.tbl + 2 * i0);
+    const u2_t e1 = *reinterpret_cast<const u2_t*>(L.tbl + 2 * i1);
     h8_t v = __builtin_bit_cast(h8_t, u4_t{e0.x, e0.y, e1.x, e1.y});
     v = (v * kv) * dv;
-    *reinterpret_cast<h8_t*>(dst + 8 * c) = v;
+    *reinterpret_cast<h8_t*>(bt + pf_frag(r, c)) = v;
   }
 }
 
+// Activations of k-step `step` (32 k) for the tile's 256 rows: 16 wave-loads, 4 per wave.  Load
+// g moves rows 16g..16g+15 x 64 B; lane l takes row 16g + l % 16, piece l / 16, which is
+// exactly fragment order.
 __device__ __forceinline__ void pf_dma_a(_Float16* abuf, const _Float16* __restrict__ x, int m0, int K,
                                          int step, int wave, int lane) {
-  // 256 rows x 64 B = 16 x 1 KB; wave w moves rows [64w, 64w+64)
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int blk = 4 * wave + j;
-    const int row = 16 * blk + (lane >> 2);
-    const _Float16* src = x + (size_t)(m0 + row) * K + kBK * step + 8 * (lane & 3);
+    const int g = 4 * wave + j;
+    const _Float16* src = x + (size_t)(m0 + 16 * g + (lane & 15)) * K + kBK * step + 8 * (lane >> 4);
     __builtin_amdgcn_global_load_lds((const void*)src,
-                                     (__attribute__((address_space(3))) void*)(abuf + 512 * blk), 16, 0, 0);
+                                     (__attribute__((address_space(3))) void*)(abuf + 512 * g), 16, 0, 0);
   }
+}
+
+struct PfFrag {
+  h8_t a[8], b[8];
+};
+
+__device__ __forceinline__ void pf_load_frag(PfFrag& f, const _Float16* A, const _Float16* B, const int* bg,
+                                             int wm, int lane) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f.b[j] = *reinterpret_cast<const h8_t*>(B + 512 * bg[j] + 8 * lane);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f.a[i] = *reinterpret_cast<const h8_t*>(A + 512 * (8 * wm + i) + 8 * lane);
+}
+
+template <int I0, int I1>
+__device__ __forceinline__ void pf_mfma(f4_t (&acc)[8][8], const PfFrag& f) {
+#pragma unroll
+  for (int i = I0; i < I1; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+}
+
+struct PfArgs {
+  const uint8_t* w1;
+  const uint8_t* w2;
+  const _Float16* x;
+  int K, steps, nb, nhb, m0, nt;
+  uint32_t rowb;
+};
+
+// One k-step t: operand loads of step t (written before the last barrier), then the producers
+// -- activations of step t+2, one weight load, the dequant of sub-block t+1 -- which the
+// scheduler interleaves with the 64 MFMAs of step t, then the barrier.
+template <bool kFfn>
+__device__ __forceinline__ void pf_step(PfLds& L, f4_t (&acc)[8][8], const PfArgs& g, const int* bg, int t,
+                                        int ra, int wave, int wm, int lane) {
+  // ring slots: step t in a[ra = t % 3]; t+2 goes to the slot read at step t-1, whose reads all
+  // completed before the previous barrier
+  const int ra2 = ra == 0 ? 2 : ra - 1;
+  PfFrag f;
+  pf_load_frag(f, L.a[ra], L.b[t & 1], bg, wm, lane);
+  pf_dma_a(L.a[ra2], g.x, g.m0, g.K, min(t + 2, g.steps - 1), wave, lane);
+  // weights: half-block t/4 + 2 is staged over the 4 steps of quad t/4 into ring slot
+  // (t/4 + 2) % 3 (role t % 4: grid indices twice, then scale words, then d words); this
+  // quad's dequants read half-blocks t/4 and t/4 + 1 only.  Past the tail the source is
+  // clamped (the slot written is then never read).
+  {
+    const int hb = (t >> 2) + 2;
+    pf_dma_w(L, hb % 3, g.w1, g.w2, kFfn, g.nt, g.rowb, g.nb, min(hb, g.nhb - 1), t & 3, wave, lane);
+  }
+  // sub-block t+1 into the other B buffer (clamped on the last step: not read again)
+  pf_dequant(L, L.b[(t + 1) & 1], threadIdx.x, min(t + 1, g.steps - 1));
+  pf_mfma<0, 8>(acc, f);
+  // step t+1's activations (issued one step earlier) and everything staged before this step
+  // must have landed; this step's 5 loads stay in flight.  Then a barrier without a memory
+  // fence (a fence would also wait for those).  The scheduling fences keep every MFMA of the
+  // step on its side of the barrier (MFMAs touch no memory, so the asm alone would not).
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt vmcnt(5)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
     const uint8_t* __restrict__ w1, const uint8_t* __restrict__ w2, const float* __restrict__ gridf,
     const _Float16* __restrict__ x, void* __restrict__ out, const float* __restrict__ res, int M, int N,
-    int K, int mtiles) {
+    int K, int mtiles, int ntiles) {
   __shared__ PfLds L;
-  // wave index as a scalar: the per-wave DMA selection below then branches on SGPRs
+  constexpr bool kFfn = EPI == PF_FFN;
+  // wave index as a scalar: the per-wave DMA selection branches on SGPRs
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int col = lane & 15, kq = lane >> 4;
   const int wm = wave >> 1, wn = wave & 1;
-  const int mt = (int)blockIdx.x % mtiles, nt = (int)blockIdx.x / mtiles;
-  const int m0 = mt * kBM;
-  const int nb = K >> 8, steps = K / kBK;
-  const size_t rowb = (size_t)98 * nb;
+  int mt, nt;
+  if ((mtiles & 7) == 0) {   // XCD x = w % 8 sweeps the n-tiles of m-tiles x, x+8, ... in turn
+    const int l = (int)blockIdx.x >> 3;
+    mt = ((int)blockIdx.x & 7) + 8 * (l / ntiles);
+    nt = l % ntiles;
+  } else {
+    mt = (int)blockIdx.x % mtiles;
+    nt = (int)blockIdx.x / mtiles;
+  }
+  PfArgs g;
+  g.w1 = w1; g.w2 = w2; g.x = x; g.K = K;
+  g.nb = K >> 8; g.steps = K / kBK; g.nhb = 2 * g.nb;
+  g.m0 = mt * kBM; g.nt = nt; g.rowb = 98u * g.nb;
 
-  // dequant role of this thread: B-tile row r
-  const int r = threadIdx.x;
-  constexpr bool kFfn = EPI == PF_FFN;
-
-  // prologue: activation steps 0 and 1 in flight, weight block 0 staged, then block 1
-  pf_dma_a(L.a[0], x, m0, K, 0, wave, lane);
-  pf_dma_a(L.a[1], x, m0, K, min(1, steps - 1), wave, lane);
-  pf_dma_w(L, w1, w2, kFfn, nt, rowb, nb, 0, wave, lane);
+  // prologue: activation steps 0, 1 and weight half-blocks 0, 1 in flight; table; sub-block 0
+  pf_dma_a(L.a[0], x, g.m0, K, 0, wave, lane);
+  pf_dma_a(L.a[1], x, g.m0, K, 1, wave, lane);
+  pf_dma_w_all(L, 0, w1, w2, kFfn, nt, g.rowb, g.nb, 0, wave, lane);
+  pf_dma_w_all(L, 1, w1, w2, kFfn, nt, g.rowb, g.nb, 1, wave, lane);
   pf_build_table(L.tbl, gridf);
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
   __syncthreads();
-  PfW wc;
-  pf_read_w(wc, L, r, 0);
-  pf_dequant<0>(wc, L.tbl, L.b[0] + r * kBK);
-  __syncthreads();                      // staging area read by everyone
-  pf_dma_w(L, w1, w2, kFfn, nt, rowb, nb, min(1, nb - 1), wave, lane);
+  pf_dequant(L, L.b[0], threadIdx.x, 0);
+  __syncthreads();
+
+  // the wave's eight 16-column n-tiles (row groups of the B tile); for FFN tiles 0..3 are gate
+  // columns [64wn, +64) and tiles 4..7 the up columns of the same range
+  int bg[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) bg[j] = kFfn ? (j < 4 ? 4 * wn + j : 8 + 4 * wn + (j - 4)) : 8 * wn + j;
 
   f4_t acc[8][8];
 #pragma unroll
@@ -177,53 +253,10 @@ __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  // the wave's eight 16-column n-tiles inside the 256-row B tile; for FFN tiles 0..3 are gate
-  // columns [64wn, +64) and tiles 4..7 the up columns of the same range
-  int ncol[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) ncol[j] = kFfn ? (j < 4 ? 64 * wn + 16 * j : 128 + 64 * wn + 16 * (j - 4)) : 128 * wn + 16 * j;
-
-  for (int b = 0; b < nb; ++b) {
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int t = 8 * b + s;
-      const _Float16* A = L.a[t % 3];
-      const _Float16* B = L.b[s & 1];
-      // produce: activations two steps ahead (clamped at the end: the extra tiles land in ring
-      // slots that are never read); weights of the next step; at s == 0 the weight block
-      // b+1 starts staging (the staging area was last read before the previous barrier)
-      pf_dma_a(L.a[(t + 2) % 3], x, m0, K, min(t + 2, steps - 1), wave, lane);
-      if (s == 0 && b > 0) pf_dma_w(L, w1, w2, kFfn, nt, rowb, nb, min(b + 1, nb - 1), wave, lane);
-      switch (s) {
-        case 0: pf_dequant<1>(wc, L.tbl, L.b[1] + r * kBK); break;
-        case 1: pf_dequant<2>(wc, L.tbl, L.b[0] + r * kBK); break;
-        case 2: pf_dequant<3>(wc, L.tbl, L.b[1] + r * kBK); break;
-        case 3: pf_dequant<4>(wc, L.tbl, L.b[0] + r * kBK); break;
-        case 4: pf_dequant<5>(wc, L.tbl, L.b[1] + r * kBK); break;
-        case 5: pf_dequant<6>(wc, L.tbl, L.b[0] + r * kBK); break;
-        case 6: pf_dequant<7>(wc, L.tbl, L.b[1] + r * kBK); break;
-        default:
-          if (b + 1 < nb) {   // block b+1 has been staged since step 2 of this block
-            pf_read_w(wc, L, r, b + 1);
-            pf_dequant<0>(wc, L.tbl, L.b[0] + r * kBK);
-          }
-      }
-      // consume step t
-      h8_t bf[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) bf[j] = *reinterpret_cast<const h8_t*>(B + (ncol[j] + col) * kBK + 8 * kq);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const h8_t af = *reinterpret_cast<const h8_t*>(A + (128 * wm + 16 * i + col) * kBK + 8 * kq);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
-      }
-      // step t+1's activations (issued one step earlier) must have landed; the loads issued in
-      // this step (4 activation DMAs, plus 7 weight DMAs at s == 0 of blocks b > 0) stay in
-      // flight.  Then a barrier without a memory fence (a fence would also wait for those).
-      if (s == 0 && b > 0) asm volatile("s_waitcnt vmcnt(11)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(4)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    }
+  int ra = 0;
+  for (int t = 0; t < g.steps; ++t) {
+    pf_step<kFfn>(L, acc, g, bg, t, ra, wave, wm, lane);
+    ra = ra == 2 ? 0 : ra + 1;
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);   // drain the clamped tail loads before the block exits
 
@@ -232,17 +265,17 @@ __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
   for (int i = 0; i < 8; ++i) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int m = m0 + 128 * wm + 16 * i + 4 * kq + e;
+      const int m = g.m0 + 128 * wm + 16 * i + 4 * kq + e;
       if constexpr (EPI == PF_FFN) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int n = nt * (kBN / 2) + ncol[j] + col;
+          const int n = nt * (kBN / 2) + 16 * bg[j] + col;
           reinterpret_cast<uint16_t*>(out)[(size_t)m * N + n] = tlx_swiglu_bits(acc[i][j][e], acc[i][j + 4][e]);
         }
       } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const int n = nt * kBN + ncol[j] + col;
+          const int n = nt * kBN + 16 * bg[j] + col;
           const size_t o = (size_t)m * N + n;
           if constexpr (EPI == PF_RES)
             reinterpret_cast<float*>(out)[o] = res[o] + acc[i][j][e];
@@ -271,7 +304,7 @@ extern "C" int tlx_pfg3_ffn(const void* wg, const void* wu, const float* gridf, 
   TLX_RET_IF(!tlx_aligned(gridf, 16), TLX_E_ALIGN);
   const int mtiles = M / kBM, ntiles = N / (kBN / 2);
   pf_gemm_kernel<PF_FFN><<<mtiles * ntiles, kThreads, 0, (hipStream_t)stream>>>(
-      (const uint8_t*)wg, (const uint8_t*)wu, gridf, (const _Float16*)x16, out16, nullptr, M, N, K, mtiles);
+      (const uint8_t*)wg, (const uint8_t*)wu, gridf, (const _Float16*)x16, out16, nullptr, M, N, K, mtiles, ntiles);
   return tlx_launch_status();
 }
 
@@ -282,7 +315,7 @@ extern "C" int tlx_pfg3_iq3d(const void* w, const float* gridf, const uint16_t* 
   TLX_RET_IF(!tlx_aligned(gridf, 16), TLX_E_ALIGN);
   const int mtiles = M / kBM, ntiles = N / kBN;
   pf_gemm_kernel<PF_RES><<<mtiles * ntiles, kThreads, 0, (hipStream_t)stream>>>(
-      (const uint8_t*)w, nullptr, gridf, (const _Float16*)x16, out32, res, M, N, K, mtiles);
+      (const uint8_t*)w, nullptr, gridf, (const _Float16*)x16, out32, res, M, N, K, mtiles, ntiles);
   return tlx_launch_status();
 }
 
@@ -293,6 +326,6 @@ extern "C" int tlx_pfg3_iq3o(const void* w, const float* gridf, const uint16_t* 
   TLX_RET_IF(!tlx_aligned(gridf, 16), TLX_E_ALIGN);
   const int mtiles = M / kBM, ntiles = N / kBN;
   pf_gemm_kernel<PF_F16><<<mtiles * ntiles, kThreads, 0, (hipStream_t)stream>>>(
-      (const uint8_t*)w, nullptr, gridf, (const _Float16*)x16, out16, nullptr, M, N, K, mtiles);
+      (const uint8_t*)w, nullptr, gridf, (const _Float16*)x16, out16, nullptr, M, N, K, mtiles, ntiles);
   return tlx_launch_status();
 }
