@@ -14,6 +14,10 @@ stream the kernels are launched on.
 
 ``cpu_baseline`` times the numpy restatement of the reference's CPU path (dequantize, then
 an fp32 matmul) on a bounded sample of rows of the same workload, on this host's cores.
+
+``gemm`` is the metric's second half: the prefill dequant-GEMM of config 4 at M=2048 --
+gate+up with SwiGLU (K=5120, N=2x17408) and down with the residual epilogue (K=17408,
+N=5120) -- in TFLOP/s (2*M*N*K per GEMM) and as a fraction of the dense fp16 MFMA peak.
 """
 import argparse
 import json
@@ -24,6 +28,7 @@ import time
 import numpy as np
 
 PEAK_HBM_GBS = 8000.0
+PEAK_F16_TFLOPS = 2500.0
 ROT_BYTES = 300 * 2**20
 
 
@@ -34,6 +39,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--ms", default="1,4,8,11", help="activation widths to time")
+    ap.add_argument("--gemm-m", type=int, default=2048, help="prefill rows for the GEMM leg (0: skip)")
     return ap.parse_args()
 
 
@@ -53,6 +59,52 @@ def time_ffn(ops, wsets, gridf, x, gact, steps, warmup, torch):
     t1.record(stream)
     torch.cuda.synchronize()
     return t0.elapsed_time(t1) / steps
+
+
+def time_call(fn, steps, warmup, torch):
+    """Average ms of fn(stream) over `steps` calls after `warmup`, HIP events on its stream."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn(stream)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        fn(stream)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup):
+    """Config 4: IQ3_XXS FFN prefill GEMMs at M rows, synthetic seeded weights."""
+    rng = synth.config_rng(4)
+    H, F = 5120, 17408
+    pg = torch.from_numpy(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, F, H), H)).to(dev)
+    pu = torch.from_numpy(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, F, H), H)).to(dev)
+    pd = torch.from_numpy(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, H, F), F)).to(dev)
+    gridf = formats.gridf_tensor(dev)
+    x = torch.from_numpy(synth.activations_f16(rng, M, H)).to(dev)
+    act = torch.empty(M, F, dtype=torch.float16, device=dev)
+    res = torch.randn(M, H, device=dev)
+    y = torch.empty(M, H, dtype=torch.float32, device=dev)
+    t_ffn = time_call(lambda s: ops.pfg3_ffn(pg, pu, gridf, x, act, stream=s), steps, warmup, torch)
+    t_down = time_call(lambda s: ops.pfg3_iq3d(pd, gridf, act, res, y, stream=s), steps, warmup, torch)
+    f_ffn, f_down = 2.0 * M * H * 2 * F, 2.0 * M * F * H
+    tf_ffn = f_ffn / (t_ffn * 1e-3) / 1e12
+    tf_down = f_down / (t_down * 1e-3) / 1e12
+    tf_layer = (f_ffn + f_down) / ((t_ffn + t_down) * 1e-3) / 1e12
+    return {
+        "workload": f"IQ3_XXS prefill FFN, M={M}: gate+up+SwiGLU K={H} N=2x{F}; down+residual K={F} N={H}",
+        "M": M,
+        "ffn_ms": round(t_ffn, 4), "ffn_tflops": round(tf_ffn, 1),
+        "down_ms": round(t_down, 4), "down_tflops": round(tf_down, 1),
+        "tflops": round(tf_layer, 1),
+        "roofline": {"bound": "mfma", "achieved": round(tf_ffn, 1), "peak": PEAK_F16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tf_ffn / PEAK_F16_TFLOPS, 4), "traffic": None,
+                     "kernel": "pf_gemm_kernel<FFN> (gate+up)"},
+    }
 
 
 def cpu_baseline(N, K, M, seconds=10.0):
@@ -147,6 +199,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": value, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(value / PEAK_HBM_GBS, 4), "traffic": None},
     }
+    if args.gemm_m > 0:
+        out["gemm"] = gemm_leg(ops, formats, synth, torch, dev, args.gemm_m, max(3, args.steps // 5),
+                               max(1, args.warmup // 5))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(N, K, int(head))
     print(json.dumps(out), flush=True)

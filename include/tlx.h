@@ -30,6 +30,8 @@ extern "C" {
 #define TLX_LAYOUT_RAW 0     /* GGUF blocks as stored in the file */
 #define TLX_LAYOUT_PACKED 1  /* IQ3_XXS: pack_w1c regions [qs 64NB][sw 32NB][d 2NB];
                                 Q6_K: pack_w1c 212-B blocks [pad2][d2][sc16][lo128][qh64] */
+#define TLX_LAYOUT_PACK7 2   /* IQ3_XXS packed7 (engine/pack_w7.py:7-21): [N/8 groups][K/128
+                                chunks][32 units r*4+c][16 B: q u16 x4, sw u32, d u16, pad] */
 
 #define TLX_MAX_M 16         /* decode GEMVs accept 1..16 activation rows */
 
@@ -86,7 +88,8 @@ int tlx_q6k_gemv(const void* w, const float* x, float* y, int rows, int K, int l
                  void* stream);
 
 /* ---- prefill dequant-GEMM (M rows of a prompt chunk, MFMA fp16 x fp16 -> fp32) ----
- * x16 is M x K fp16 row-major; W is N packed IQ3_XXS rows.  M % 256 == 0, K % 512 == 0,
+ * x16 is M x K fp16 row-major; W is N IQ3_XXS rows in the packed7 layout (TLX_LAYOUT_PACK7,
+ * the layout the reference's pf_gemm3 REPACK=1 kernels read).  M % 256 == 0, K % 128 == 0,
  * 16-byte aligned buffers.  Each output element is one fp32 MFMA sum over k of
  * x[m][k] * half(W[n][k]); its k order differs from the reference's mma.sync order, so
  * results agree to rounding (relative error <= 1e-3), not bitwise. */

@@ -12,15 +12,16 @@ import torch
 
 from oracle import gemv, quants
 from thunderllamax_amd import formats, ops, synth
-from thunderllamax_amd._lib import LAYOUT_RAW, TlxError
+from thunderllamax_amd._lib import LAYOUT_PACKED, TlxError
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
 
 
 def _iq3(rng, rows, kdim, dev):
+    """Packed rows (what the oracle dequantizes) and their packed7 units on the GPU."""
     packed = formats.iq3_pack_rows(synth.iq3xxs_raw(rng, rows, kdim), kdim)
-    return packed, torch.from_numpy(packed).to(dev)
+    return packed, torch.from_numpy(formats.iq3_pack7(packed, kdim)).to(dev)
 
 
 def _rows_err(y, ref):
@@ -43,7 +44,7 @@ def test_pfg3_ffn_parity(gpu, M, N, K):
     assert err <= TOL
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 256, 512), (512, 512, 2048), (256, 256, 6144)])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 512), (512, 512, 2048), (256, 256, 6144), (256, 256, 768)])
 def test_pfg3_iq3o_parity(gpu, M, N, K):
     print(f"[case] pfg3_iq3o M={M} N={N} K={K}", flush=True)
     rng = synth.config_rng(4)
@@ -141,10 +142,9 @@ def test_pfg3_bad_arguments_raise(gpu):
     out = torch.empty(256, 256, dtype=torch.float16, device=gpu)
     with pytest.raises(TlxError):   # M not a multiple of 256
         ops.pfg3_iq3o(w, g, x[:128], out[:128])
-    with pytest.raises(TlxError):   # raw layout is not accepted
-        ops.pfg3_iq3o(w, g, x, out, layout=LAYOUT_RAW)
-    _, w3 = _iq3(rng, 256, 768, gpu)
-    with pytest.raises(TlxError):   # K / 256 odd: rows not dword-aligned
-        ops.pfg3_iq3o(w3, g, torch.zeros(256, 768, dtype=torch.float16, device=gpu), out)
+    with pytest.raises(TlxError):   # only the packed7 layout is accepted
+        ops.pfg3_iq3o(w, g, x, out, layout=LAYOUT_PACKED)
+    with pytest.raises(TlxError):   # K not a multiple of 128
+        ops.pfg3_iq3o(w, g, torch.zeros(256, 320, dtype=torch.float16, device=gpu), out)
     with pytest.raises(TlxError):   # N not a multiple of the 256-row tile
         ops.pfg3_iq3o(w, g, x, torch.empty(256, 128, dtype=torch.float16, device=gpu))

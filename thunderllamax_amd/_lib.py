@@ -18,6 +18,7 @@ TLX_E_ALIGN = -2
 TLX_E_NODEV = -3
 LAYOUT_RAW = 0
 LAYOUT_PACKED = 1
+LAYOUT_PACK7 = 2
 MAX_M = 16
 
 _p = ctypes.c_void_p

@@ -1,5 +1,8 @@
-// IQ3_XXS prefill dequant-GEMM for gfx950 (the pf_gemm3 family, engine/pf_gemm3.cu:313-430):
-//   C[m][n] = sum_k X[m][k] * W[n][k],  X fp16 [M][K] row-major, W packed IQ3_XXS rows.
+// IQ3_XXS prefill dequant-GEMM for gfx950 (the pf_gemm3 family with REPACK=1,
+// engine/pf_gemm3.cu:313-430): C[m][n] = sum_k X[m][k] * W[n][k], X fp16 [M][K] row-major,
+// W in the packed7 unit layout (engine/pack_w7.py:7-21): per 8-row group and 128-k chunk, 32
+// 16-byte units, unit r*4+c = everything row r needs for sub-block c of the chunk (8 bytes of
+// grid indices, the scale/sign word, d, 2 pad bytes).
 // Epilogues: FFN  out16[m][n] = silu16(half(g)) * half(u)   (W = gate rows, W2 = up rows)
 //            RES  out32[m][n] = res[m][n] + acc             (no half rounding, as the reference)
 //            F16  out16[m][n] = half(acc)
@@ -10,15 +13,19 @@
 //   * 4 waves (one per SIMD, so each owns 512 registers); wave (wm, wn) computes m [128wm, +128)
 //     x 128 n (FFN: 64 gate + 64 up columns of one n-range) with v_mfma_f32_16x16x32_f16,
 //     64 MFMAs per step into 256 accumulator registers;
-//   * A and B tiles sit in LDS in fragment order: the 16-B piece p (8 k) of tile row R is at
-//     ((R / 16) * 64 + p * 16 + R % 16) * 16 bytes, so the MFMA operand of lane l for a 16-row
-//     group is 16 bytes at l * 16 -- every operand read is one lane-linear, bank-conflict-free
-//     1 KB; a direct global->LDS load of 16 rows x 64 B lands in the same order;
-//   * activations stream into a 3-deep ring two steps ahead; weights are staged raw (half-blocks
-//     of 4 sub-blocks, 3-deep ring, one direct load per wave per step) and dequantized one
-//     sub-block ahead into a double-buffered B tile, to the reference's fp16 values
-//     fp16((+-g*(2s+1)/4) * d) = fp16(db*g) (the first product is exact in fp16, the second
-//     rounds once) via the sign-folded grid table the GEMV uses;
+//   * every global->LDS load is a direct (LDS-DMA) 16-byte load in which each group of 4 lanes
+//     reads 64 contiguous bytes: that is what keeps the vector-memory path at full rate (a load
+//     whose 4-lane groups span 4 rows runs at a quarter of it);
+//   * activations: a 3-deep ring, two steps ahead; a 16-row group is stored row-major (64 B a
+//     row), the 16-B piece p of row r at piece p ^ ((r >> 1) & 3), which makes the MFMA operand
+//     reads (lane l: row l % 16, piece l / 16) bank-conflict-free;
+//   * weights: the tile's 128-k chunk of packed7 units (32 groups x 512 contiguous bytes) is
+//     staged in one burst into a 2-deep ring, four steps before its first use; each sub-block
+//     is dequantized one step ahead into a double-buffered B tile in fragment order (16-B piece
+//     p of row R at ((R / 16) * 64 + p * 16 + R % 16) * 16 bytes, so operand reads are
+//     lane-linear), to the reference's fp16 values fp16((+-g*(2s+1)/4) * d) = fp16(db*g) (the
+//     first product is exact in fp16, the second rounds once) via the sign-folded grid table
+//     the GEMV uses;
 //   * one barrier per step; the step's operand loads come first, then the producers of later
 //     steps, which the compiler interleaves with the step's MFMAs;
 //   * workgroup w runs on XCD w % 8; when M is a multiple of 2048 each XCD sweeps the n-tiles
@@ -36,14 +43,12 @@ enum PfEpi { PF_FFN = 0, PF_RES = 1, PF_F16 = 2 };
 
 struct __attribute__((aligned(16))) PfLds {
   uint32_t tbl[4096 * 2];                 // sign-folded grid table, 4 fp16 per entry
-  _Float16 a[3][kTile];                   // activation ring, fragment order
+  _Float16 a[3][kTile];                   // activation ring: 16-row groups, row-major, swizzled
   _Float16 b[2][kTile];                   // dequantized weights, fragment order
-  uint8_t wq[3][kBN * 32];                // raw half-blocks (4 sub-blocks): grid indices
-  uint8_t ws[3][kBN * 16];                //   scale/sign words
-  uint32_t wd[3][kBN];                    //   the aligned d pair holding d (blocks 2i, 2i+1)
+  u4_t w[2][kBN * 4];                     // packed7 units of one 128-k chunk: [group][r*4+c]
 };
 
-// fragment-order offset (halfs) of piece p of tile row R
+// B tile: fragment-order offset (halfs) of piece p of tile row R
 __device__ __forceinline__ int pf_frag(int R, int p) { return ((R >> 4) * 64 + p * 16 + (R & 15)) * 8; }
 
 __device__ __forceinline__ void pf_build_table(uint32_t* tbl, const float* __restrict__ gridf) {
@@ -62,63 +67,38 @@ __device__ __forceinline__ void pf_build_table(uint32_t* tbl, const float* __res
   }
 }
 
-// One of the 16 wave-loads that stage half-block hb (block hb/2, sub-blocks 4(hb&1)..+3) of the
-// tile's 256 weight rows into buffer `buf` with direct global->LDS loads.  Role 0/1: load
-// 4*role + idx of the 16-B grid-index pieces (32 rows x 2 each); role 2: load idx of the 16-B
-// scale/sign pieces (64 rows each); role 3: load idx of the d dwords (64 rows each).  The d
-// words are the dword-aligned pairs (block & ~1, block | 1) -- rows are dword-aligned since NB
-// is even -- because a sub-dword direct load still spaces lanes 4 bytes apart in LDS.  `role`
-// and `idx` are wave-uniform.
-__device__ __forceinline__ void pf_dma_w(PfLds& L, int buf, const uint8_t* __restrict__ w1,
-                                         const uint8_t* __restrict__ w2, bool ffn, int nt, uint32_t rowb,
-                                         int nb, int hb, int role, int idx, int lane) {
-  const int blk = hb >> 1, half = hb & 1;
-  int row;
-  uint32_t off;
-  uint8_t* dst;
-  if (role < 2) {
-    const int q = 4 * role + idx;
-    row = 32 * q + (lane >> 1);
-    off = 64 * blk + 32 * half + 16 * (lane & 1);
-    dst = L.wq[buf] + 1024 * q;
-  } else if (role == 2) {
-    row = 64 * idx + lane;
-    off = 64 * nb + 32 * blk + 16 * half;
-    dst = L.ws[buf] + 1024 * idx;
-  } else {
-    row = 64 * idx + lane;
-    off = 96 * nb + 4 * (blk >> 1);
-    dst = reinterpret_cast<uint8_t*>(L.wd[buf] + 64 * idx);
-  }
-  const uint8_t* src;
-  if (ffn) src = (row < 128 ? w1 : w2) + (size_t)(nt * 128 + (row & 127)) * rowb + off;
-  else src = w1 + (size_t)(nt * kBN + row) * rowb + off;
-  auto* d3 = (__attribute__((address_space(3))) void*)dst;
-  if (role == 3) __builtin_amdgcn_global_load_lds((const void*)src, d3, 4, 0, 0);
-  else __builtin_amdgcn_global_load_lds((const void*)src, d3, 16, 0, 0);
-}
-
-// All 16 loads of half-block hb, 4 per wave (prologue).
-__device__ __forceinline__ void pf_dma_w_all(PfLds& L, int buf, const uint8_t* __restrict__ w1,
-                                             const uint8_t* __restrict__ w2, bool ffn, int nt, uint32_t rowb,
-                                             int nb, int hb, int wave, int lane) {
+// Stage chunk h (128 k) of the tile's 256 weight rows into ring slot `slot`: 32 groups x 512 B,
+// 16 wave-loads, wave w doing loads 4w..4w+3; load j moves tile groups 2j, 2j+1 (lane l: group
+// 2j + l / 32, unit l % 32).  FFN tiles take gate groups 16nt.. for tile groups 0-15 and the up
+// groups for 16-31.
+__device__ __forceinline__ void pf_dma_w(PfLds& L, int slot, const u4_t* __restrict__ w1, const u4_t* __restrict__ w2,
+                                         bool ffn, int nt, int nch, int h, int wave, int lane) {
 #pragma unroll
-  for (int role = 0; role < 4; ++role) pf_dma_w(L, buf, w1, w2, ffn, nt, rowb, nb, hb, role, wave, lane);
+  for (int jj = 0; jj < 4; ++jj) {
+    const int j = 4 * wave + jj;
+    const int G = 2 * j + (lane >> 5);
+    const u4_t* base;
+    int grp;
+    if (ffn) { base = G < 16 ? w1 : w2; grp = 16 * nt + (G & 15); }
+    else { base = w1; grp = 32 * nt + G; }
+    const u4_t* src = base + ((size_t)grp * nch + h) * 32 + (lane & 31);
+    __builtin_amdgcn_global_load_lds((const void*)src,
+                                     (__attribute__((address_space(3))) void*)(L.w[slot] + 64 * j), 16, 0, 0);
+  }
 }
 
 // Dequantize sub-block u (32 weights) of tile row r into the B tile.
 __device__ __forceinline__ void pf_dequant(const PfLds& L, _Float16* bt, int r, int u) {
-  const int buf = (u >> 2) % 3, k = u & 3;
-  const u2_t qd = *reinterpret_cast<const u2_t*>(L.wq[buf] + 32 * r + 8 * k);
-  const uint32_t sw = *reinterpret_cast<const uint32_t*>(L.ws[buf] + 16 * r + 4 * k);
-  const uint32_t dd = L.wd[buf][r] >> (16 * ((u >> 3) & 1));
+  const u4_t unit = L.w[(u >> 2) & 1][4 * r + (u & 3)];
+  const uint32_t sw = unit.z;
   const _Float16 ks = (_Float16)((float)(2u * (sw >> 28) + 1u) * 0.25f);
-  const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)dd);
+  const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)unit.w);
   const h8_t kv = {ks, ks, ks, ks, ks, ks, ks, ks};
   const h8_t dv = {d, d, d, d, d, d, d, d};
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const uint32_t qw = (c & 1) ? (qd[c >> 1] >> 16) : (qd[c >> 1] & 0xFFFFu);
+    const uint32_t qd = (c >> 1) ? unit.y : unit.x;
+    const uint32_t qw = (c & 1) ? (qd >> 16) : (qd & 0xFFFFu);
     const uint32_t sidx = (sw >> (7 * c)) & 0x7Fu;
     const uint32_t par = __builtin_popcount(sidx) & 1u;
     const uint32_t i0 = ((sidx & 0xFu) << 8) | (qw & 0xFFu);
@@ -131,15 +111,15 @@ __device__ __forceinline__ void pf_dequant(const PfLds& L, _Float16* bt, int r, 
   }
 }
 
-// Activations of k-step `step` (32 k) for the tile's 256 rows: 16 wave-loads, 4 per wave.  Load
-// g moves rows 16g..16g+15 x 64 B; lane l takes row 16g + l % 16, piece l / 16, which is
-// exactly fragment order.
+// Activations of k-step `step` (32 k) for the tile's 256 rows: 16 wave-loads, 4 per wave.  Load g
+// moves rows 16g..16g+15 x 64 B: lane l fills LDS piece l % 4 of row 16g + l / 4 with logical
+// piece (l % 4) ^ ((l / 8) % 4), the swizzle of row l / 4.
 __device__ __forceinline__ void pf_dma_a(_Float16* abuf, const _Float16* __restrict__ x, int m0, int K,
                                          int step, int wave, int lane) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int g = 4 * wave + j;
-    const _Float16* src = x + (size_t)(m0 + 16 * g + (lane & 15)) * K + kBK * step + 8 * (lane >> 4);
+    const _Float16* src = x + (size_t)(m0 + 16 * g + (lane >> 2)) * K + kBK * step + 8 * ((lane & 3) ^ ((lane >> 3) & 3));
     __builtin_amdgcn_global_load_lds((const void*)src,
                                      (__attribute__((address_space(3))) void*)(abuf + 512 * g), 16, 0, 0);
   }
@@ -149,12 +129,14 @@ struct PfFrag {
   h8_t a[8], b[8];
 };
 
+// Operand loads of one step: A rows (group 8wm + i, row l % 16, piece l / 16 stored at
+// (l / 16) ^ ((l % 16 >> 1) & 3)) and B rows (fragment order: lane-linear).
 __device__ __forceinline__ void pf_load_frag(PfFrag& f, const _Float16* A, const _Float16* B, const int* bg,
-                                             int wm, int lane) {
+                                             int aoff, int wm, int lane) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) f.b[j] = *reinterpret_cast<const h8_t*>(B + 512 * bg[j] + 8 * lane);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) f.a[i] = *reinterpret_cast<const h8_t*>(A + 512 * (8 * wm + i) + 8 * lane);
+  for (int i = 0; i < 8; ++i) f.a[i] = *reinterpret_cast<const h8_t*>(A + 512 * (8 * wm + i) + aoff);
 }
 
 template <int I0, int I1>
@@ -166,48 +148,48 @@ __device__ __forceinline__ void pf_mfma(f4_t (&acc)[8][8], const PfFrag& f) {
 }
 
 struct PfArgs {
-  const uint8_t* w1;
-  const uint8_t* w2;
+  const u4_t* w1;
+  const u4_t* w2;
   const _Float16* x;
-  int K, steps, nb, nhb, m0, nt;
-  uint32_t rowb;
+  int K, steps, nch, m0, nt;
 };
 
 // One k-step t: operand loads of step t (written before the last barrier), then the producers
-// -- activations of step t+2, one weight load, the dequant of sub-block t+1 -- which the
-// scheduler interleaves with the 64 MFMAs of step t, then the barrier.
+// -- activations of step t+2, on every 4th step the burst staging the next chunk, the dequant
+// of sub-block t+1 -- which the scheduler interleaves with the 64 MFMAs of step t, then the
+// barrier.
 template <bool kFfn>
-__device__ __forceinline__ void pf_step(PfLds& L, f4_t (&acc)[8][8], const PfArgs& g, const int* bg, int t,
-                                        int ra, int wave, int wm, int lane) {
-  // ring slots: step t in a[ra = t % 3]; t+2 goes to the slot read at step t-1, whose reads all
-  // completed before the previous barrier
-  const int ra2 = ra == 0 ? 2 : ra - 1;
+__device__ __forceinline__ void pf_step(PfLds& L, f4_t (&acc)[8][8], const PfArgs& g, const int* bg, int aoff,
+                                        int t, int ra, int wave, int wm, int lane) {
   PfFrag f;
-  pf_load_frag(f, L.a[ra], L.b[t & 1], bg, wm, lane);
+  pf_load_frag(f, L.a[ra], L.b[t & 1], bg, aoff, wm, lane);
+  // activations of step t+2 into the ring slot read at step t-1 (its reads completed before the
+  // previous barrier; past the tail the source step is clamped and the slot is not read again)
+  const int ra2 = ra == 0 ? 2 : ra - 1;
   pf_dma_a(L.a[ra2], g.x, g.m0, g.K, min(t + 2, g.steps - 1), wave, lane);
-  // weights: half-block t/4 + 2 is staged over the 4 steps of quad t/4 into ring slot
-  // (t/4 + 2) % 3 (role t % 4: grid indices twice, then scale words, then d words); this
-  // quad's dequants read half-blocks t/4 and t/4 + 1 only.  Past the tail the source is
-  // clamped (the slot written is then never read).
-  {
-    const int hb = (t >> 2) + 2;
-    pf_dma_w(L, hb % 3, g.w1, g.w2, kFfn, g.nt, g.rowb, g.nb, min(hb, g.nhb - 1), t & 3, wave, lane);
+  // weights: at t = 4h-1 chunk h+1 goes into ring slot (h+1) & 1, whose chunk h-1 was last read
+  // at step 4h-2; it is first read at step t+4.  Past the tail the source is clamped.
+  const bool wstep = (t & 3) == 3;
+  if (wstep) {
+    const int h = ((t + 1) >> 2) + 1;
+    pf_dma_w(L, h & 1, g.w1, g.w2, kFfn, g.nt, g.nch, min(h, g.nch - 1), wave, lane);
   }
   // sub-block t+1 into the other B buffer (clamped on the last step: not read again)
   pf_dequant(L, L.b[(t + 1) & 1], threadIdx.x, min(t + 1, g.steps - 1));
   pf_mfma<0, 8>(acc, f);
-  // step t+1's activations (issued one step earlier) and everything staged before this step
-  // must have landed; this step's 5 loads stay in flight.  Then a barrier without a memory
-  // fence (a fence would also wait for those).  The scheduling fences keep every MFMA of the
-  // step on its side of the barrier (MFMAs touch no memory, so the asm alone would not).
+  // step t+1's activations (issued one step earlier) and every earlier chunk burst must have
+  // landed; this step's loads (4, or 8 on a burst step) stay in flight.  Then a barrier without
+  // a memory fence (a fence would also wait for those).  The scheduling fences keep every MFMA
+  // of the step on its side of the barrier (MFMAs touch no memory, so the asm alone would not).
   __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_waitcnt vmcnt(5)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (wstep) asm volatile("s_waitcnt vmcnt(8)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(4)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 }
 
 template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
-    const uint8_t* __restrict__ w1, const uint8_t* __restrict__ w2, const float* __restrict__ gridf,
+    const u4_t* __restrict__ w1, const u4_t* __restrict__ w2, const float* __restrict__ gridf,
     const _Float16* __restrict__ x, void* __restrict__ out, const float* __restrict__ res, int M, int N,
     int K, int mtiles, int ntiles) {
   __shared__ PfLds L;
@@ -227,14 +209,14 @@ __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
   }
   PfArgs g;
   g.w1 = w1; g.w2 = w2; g.x = x; g.K = K;
-  g.nb = K >> 8; g.steps = K / kBK; g.nhb = 2 * g.nb;
-  g.m0 = mt * kBM; g.nt = nt; g.rowb = 98u * g.nb;
+  g.steps = K / kBK; g.nch = K / 128;
+  g.m0 = mt * kBM; g.nt = nt;
 
-  // prologue: activation steps 0, 1 and weight half-blocks 0, 1 in flight; table; sub-block 0
+  // prologue: activation steps 0, 1 and weight chunks 0, 1 in flight; table; sub-block 0
   pf_dma_a(L.a[0], x, g.m0, K, 0, wave, lane);
-  pf_dma_a(L.a[1], x, g.m0, K, 1, wave, lane);
-  pf_dma_w_all(L, 0, w1, w2, kFfn, nt, g.rowb, g.nb, 0, wave, lane);
-  pf_dma_w_all(L, 1, w1, w2, kFfn, nt, g.rowb, g.nb, 1, wave, lane);
+  pf_dma_a(L.a[1], x, g.m0, K, min(1, g.steps - 1), wave, lane);
+  pf_dma_w(L, 0, w1, w2, kFfn, nt, g.nch, 0, wave, lane);
+  pf_dma_w(L, 1, w1, w2, kFfn, nt, g.nch, min(1, g.nch - 1), wave, lane);
   pf_build_table(L.tbl, gridf);
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
   __syncthreads();
@@ -246,6 +228,7 @@ __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
   int bg[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) bg[j] = kFfn ? (j < 4 ? 4 * wn + j : 8 + 4 * wn + (j - 4)) : 8 * wn + j;
+  const int aoff = 8 * (4 * col + (kq ^ ((col >> 1) & 3)));
 
   f4_t acc[8][8];
 #pragma unroll
@@ -255,7 +238,7 @@ __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
 
   int ra = 0;
   for (int t = 0; t < g.steps; ++t) {
-    pf_step<kFfn>(L, acc, g, bg, t, ra, wave, wm, lane);
+    pf_step<kFfn>(L, acc, g, bg, aoff, t, ra, wave, wm, lane);
     ra = ra == 2 ? 0 : ra + 1;
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);   // drain the clamped tail loads before the block exits
@@ -288,9 +271,9 @@ __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
 }
 
 int pf_check(const void* w, const void* x, int M, int N, int K, int layout, int ntile) {
-  if (M < kBM || (M % kBM) || N < ntile || (N % ntile) || K < 256 || (K & 255)) return TLX_E_ARG;
-  if (layout != TLX_LAYOUT_PACKED) return TLX_E_ARG;
-  if (((K >> 8) & 1) || !tlx_aligned(w, 16) || !tlx_aligned(x, 16)) return TLX_E_ALIGN;
+  if (M < kBM || (M % kBM) || N < ntile || (N % ntile) || K < 128 || (K % 128)) return TLX_E_ARG;
+  if (layout != TLX_LAYOUT_PACK7) return TLX_E_ARG;
+  if (!tlx_aligned(w, 16) || !tlx_aligned(x, 16)) return TLX_E_ALIGN;
   return TLX_OK;
 }
 
@@ -304,7 +287,7 @@ extern "C" int tlx_pfg3_ffn(const void* wg, const void* wu, const float* gridf, 
   TLX_RET_IF(!tlx_aligned(gridf, 16), TLX_E_ALIGN);
   const int mtiles = M / kBM, ntiles = N / (kBN / 2);
   pf_gemm_kernel<PF_FFN><<<mtiles * ntiles, kThreads, 0, (hipStream_t)stream>>>(
-      (const uint8_t*)wg, (const uint8_t*)wu, gridf, (const _Float16*)x16, out16, nullptr, M, N, K, mtiles, ntiles);
+      (const u4_t*)wg, (const u4_t*)wu, gridf, (const _Float16*)x16, out16, nullptr, M, N, K, mtiles, ntiles);
   return tlx_launch_status();
 }
 
@@ -315,7 +298,7 @@ extern "C" int tlx_pfg3_iq3d(const void* w, const float* gridf, const uint16_t* 
   TLX_RET_IF(!tlx_aligned(gridf, 16), TLX_E_ALIGN);
   const int mtiles = M / kBM, ntiles = N / kBN;
   pf_gemm_kernel<PF_RES><<<mtiles * ntiles, kThreads, 0, (hipStream_t)stream>>>(
-      (const uint8_t*)w, nullptr, gridf, (const _Float16*)x16, out32, res, M, N, K, mtiles, ntiles);
+      (const u4_t*)w, nullptr, gridf, (const _Float16*)x16, out32, res, M, N, K, mtiles, ntiles);
   return tlx_launch_status();
 }
 
@@ -326,6 +309,6 @@ extern "C" int tlx_pfg3_iq3o(const void* w, const float* gridf, const uint16_t* 
   TLX_RET_IF(!tlx_aligned(gridf, 16), TLX_E_ALIGN);
   const int mtiles = M / kBM, ntiles = N / kBN;
   pf_gemm_kernel<PF_F16><<<mtiles * ntiles, kThreads, 0, (hipStream_t)stream>>>(
-      (const uint8_t*)w, nullptr, gridf, (const _Float16*)x16, out16, nullptr, M, N, K, mtiles, ntiles);
+      (const u4_t*)w, nullptr, gridf, (const _Float16*)x16, out16, nullptr, M, N, K, mtiles, ntiles);
   return tlx_launch_status();
 }

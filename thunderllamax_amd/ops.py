@@ -8,7 +8,7 @@ allocated here.  Errors raise ``TlxError`` (the reference asserts in Python).
 """
 import torch
 
-from ._lib import LAYOUT_PACKED, LAYOUT_RAW, call
+from ._lib import LAYOUT_PACK7, LAYOUT_PACKED, LAYOUT_RAW, call
 
 _F16 = torch.float16
 
@@ -101,7 +101,9 @@ def h6k_gemv(w, x, y, layout=LAYOUT_RAW, stream=None):
 
 
 # ------------------------------------------------------------------ prefill dequant-GEMMs
-def pfg3_ffn(wg, wu, gridf, x16, out16, layout=LAYOUT_PACKED, stream=None):
+# Weights are IQ3_XXS in the packed7 unit layout (``formats.iq3_pack7``), as the reference's
+# prefill GEMMs read them.
+def pfg3_ffn(wg, wu, gridf, x16, out16, layout=LAYOUT_PACK7, stream=None):
     """out16[m] = silu16(half(Wg·x16[m])) * half(Wu·x16[m]) over a prompt chunk
     (pf_gemm3 FFN=1: kernel(w1, w2, gridf, x16, out16))."""
     _dev(wg, wu, gridf, x16, out16)
@@ -111,7 +113,7 @@ def pfg3_ffn(wg, wu, gridf, x16, out16, layout=LAYOUT_PACKED, stream=None):
     return out16
 
 
-def pfg3_iq3d(w, gridf, x16, res16, out32, layout=LAYOUT_PACKED, stream=None):
+def pfg3_iq3d(w, gridf, x16, res16, out32, layout=LAYOUT_PACK7, stream=None):
     """out32[m] = res16[m] + W·x16[m]   (pf_gemm3 RES=1: kernel(w1, gridf, x16, res16, out32))."""
     _dev(w, gridf, x16, res16, out32)
     M, K, N = x16.shape[0], x16.shape[1], out32.shape[1]
@@ -120,7 +122,7 @@ def pfg3_iq3d(w, gridf, x16, res16, out32, layout=LAYOUT_PACKED, stream=None):
     return out32
 
 
-def pfg3_iq3o(w, gridf, x16, out16, layout=LAYOUT_PACKED, stream=None):
+def pfg3_iq3o(w, gridf, x16, out16, layout=LAYOUT_PACK7, stream=None):
     """out16[m] = half(W·x16[m])   (pf_gemm3 plain: kernel(w1, gridf, x16, out16))."""
     _dev(w, gridf, x16, out16)
     M, K, N = x16.shape[0], x16.shape[1], out16.shape[1]
