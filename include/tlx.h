@@ -111,6 +111,54 @@ int tlx_pfg3_iq3d(const void* w, const float* gridf, const uint16_t* x16, const 
 int tlx_pfg3_iq3o(const void* w, const float* gridf, const uint16_t* x16, uint16_t* out16,
                   int M, int N, int K, int layout, void* stream);
 
+/* ---- MoE grouped-expert path (256 routed experts + 1 shared, hidden 2048, expert FF 512,
+ * top-8; IQ4_XS weights).  Pairs are position-major, rank ascending: pair = 8*pos + rank.
+ * Expert e's gate/up slab at ptbl[e] (512 gate rows, then 512 up rows 557,056 B later; 1088 B
+ * a row), its down slab at ptbl_dn[e] (2048 rows x 272 B).  ptbl / ptbl_dn are device arrays
+ * of 256 device addresses. */
+
+/* Top-8 + renormalized softmax from router logits f32[P][256] (the router epilogue of
+ * engine/mm/MM_P1_rt8e256.cu:41-60: strict >, ties to the lower id).  eids u16[P][8],
+ * gates f32[P][8].  No reference counterpart on its own: BASELINE config 5 feeds logits. */
+int tlx_moe_topk(const float* logits, uint16_t* eids, float* gates, int P, void* stream);
+
+/* Router: logits = wrt[256][2048] . h[P][2048], top-8 + softmax, sg = sigmoid(wsh . h).
+ * Replaces rt8e256 (engine/mm/MM_P1_rt8e256.cu:14-21): rt8e256(wrt, wsh, h, eids, gates, sg). */
+int tlx_moe_route(const float* wrt, const float* wsh, const float* h, uint16_t* eids, float* gates,
+                  float* sg, int P, void* stream);
+
+/* Deterministic stable sort of the np = 8P pairs by expert: eoff i32[257] (exclusive bin
+ * offsets), plist u16[np] (pair ids, pair order inside a bin), items u32[tlx_moe_max_items(np)]
+ * (expert << 16 | first pair in bin, one per 64 pairs), nitp u32[1] (item count).  np <= 16384.
+ * Replaces mmsort8 (engine/mm/MM_B_mmsort8.cu:22-31): mmsort8(eids, eoff, plist, items, nitp, np);
+ * eoff / plist are the reference's, the item granularity is this library's own. */
+int tlx_moe_sort(const uint16_t* eids, int* eoff, uint16_t* plist, uint32_t* items, uint32_t* nitp,
+                 int np, void* stream);
+int tlx_moe_max_items(int np);
+
+/* Grouped gate+up + SwiGLU: ys[pair][512] = silu(Wg_e . x[pos]) * (Wu_e . x[pos]), f32.
+ * Replaces gx8e256up4 / gxu_gm (engine/mm/MM_P2_gx8e256up4.cu:8-14, engine/mm/MM_E_gxu_gm.cu:86-93):
+ * (ptbl, eoff, plist, xs f32[P][2048], iq4nl f32[16], ys). */
+int tlx_moe_up4(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const uint32_t* items,
+                const uint32_t* nitp, const float* xs, const float* iq4nl, float* ys, int np, void* stream);
+
+/* Grouped down: parts[pair][2048] = fp16(Wd_e . act[pair]).
+ * Replaces gx8e256dn / gxd_gm (engine/mm/MM_P2_gx8e256dn.cu:9-15, engine/mm/MM_E_gxd_gm.cu:91-174). */
+int tlx_moe_dn4(const uint64_t* ptbl_dn, const int* eoff, const uint16_t* plist, const uint32_t* items,
+                const uint32_t* nitp, const float* act, const float* iq4nl, uint16_t* parts, int np,
+                void* stream);
+
+/* Shared expert over all P positions: act[P][512] (caller scratch) then out[P][2048] f32.
+ * ptbl_sh = {gate/up slab, down slab}.  Replaces shgu32 / shdn32 (engine/mm/MM_P2_ports.py:195-201
+ * restates them) with the IQ4_XS weights of BASELINE config 5. */
+int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const float* iq4nl, float* act, float* out,
+                   int P, void* stream);
+
+/* y = hres + (sum_r gates[r] * parts[pos][r] + sg * shared), f32[P][2048].
+ * Replaces cmbz2048 (engine/mm/MM_P34_cmbz2048.cu:6-13): cmbz2048(parts, gates, sg, shared, hres, y). */
+int tlx_moe_combine(const uint16_t* parts, const float* gates, const float* sg, const float* shared,
+                    const float* hres, float* y, int P, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

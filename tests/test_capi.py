@@ -22,6 +22,14 @@ def test_header_and_binding_agree():
     assert _declared() == sorted(_lib.SIGNATURES)
 
 
+def test_header_and_binding_argument_counts_agree():
+    src = re.sub(r"/\*.*?\*/", "", open(HDR).read(), flags=re.S)
+    for name, params in re.findall(r"\b(tlx_\w+)\s*\(([^)]*)\)\s*;", src):
+        params = params.strip()
+        n = 0 if params in ("", "void") else params.count(",") + 1
+        assert n == len(_lib.SIGNATURES[name]), name
+
+
 def test_library_exports_every_declared_symbol():
     L = ctypes.CDLL(_lib.LIB_PATH)
     for name in _declared():

@@ -1,0 +1,206 @@
+"""GPU MoE path (config 5: 256 IQ4_XS experts + 1 shared, hidden 2048, FF 512, top-8) against
+the oracle.
+
+Router ids and the sort are bit-exact; gates / sg within float32 exp rounding; the expert
+GEMMs (fp16 operands, fp32 accumulation) within norm-wise rel-err 1e-3 per output row of the
+exact float64 products of the dequantized weights.  The layer tests scale the N(0,1) hidden
+states by 0.05: with config 5's weight statistics an unscaled input drives the down
+projection past the fp16 range of its output (the reference stores it as fp16 too).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemv, moe
+from thunderllamax_amd import formats, ops, synth
+from thunderllamax_amd._lib import TlxError
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def experts(gpu):
+    rng = synth.config_rng(5)
+    gu, dn = synth.moe_expert_slabs(rng, moe.E + 1)
+    dgu = [torch.from_numpy(s).to(gpu) for s in gu]
+    ddn = [torch.from_numpy(s).to(gpu) for s in dn]
+    return {
+        "gu": gu, "dn": dn, "dgu": dgu, "ddn": ddn,
+        "ptbl": formats.pointer_table(dgu[:moe.E], gpu),
+        "ptbl_dn": formats.pointer_table(ddn[:moe.E], gpu),
+        "ptbl_sh": formats.pointer_table([dgu[moe.E], ddn[moe.E]], gpu),
+        "iq4nl": formats.iq4nl_tensor(gpu),
+    }
+
+
+def _rows_err(y, ref):
+    return max(gemv.rel_err(y[i], ref[i]) for i in range(ref.shape[0]))
+
+
+def _run_layer(gpu, ex, x, logits, sg, hres):
+    P = x.shape[0]
+    np_ = 8 * P
+    dx = torch.from_numpy(x).to(gpu)
+    eids = torch.empty(P, 8, dtype=torch.int16, device=gpu)
+    gates = torch.empty(P, 8, dtype=torch.float32, device=gpu)
+    ops.moe_topk(torch.from_numpy(logits).to(gpu), eids, gates)
+    eoff = torch.empty(257, dtype=torch.int32, device=gpu)
+    plist = torch.empty(np_, dtype=torch.int16, device=gpu)
+    items = torch.empty(ops.moe_max_items(np_), dtype=torch.int32, device=gpu)
+    nitp = torch.empty(1, dtype=torch.int32, device=gpu)
+    ops.moe_sort(eids, eoff, plist, items, nitp)
+    act = torch.empty(np_, moe.FF, dtype=torch.float32, device=gpu)
+    ops.moe_up4(ex["ptbl"], eoff, plist, items, nitp, dx, ex["iq4nl"], act)
+    parts = torch.empty(np_, moe.HID, dtype=torch.float16, device=gpu)
+    ops.moe_dn4(ex["ptbl_dn"], eoff, plist, items, nitp, act, ex["iq4nl"], parts)
+    sact = torch.empty(P, moe.FF, dtype=torch.float32, device=gpu)
+    shared = torch.empty(P, moe.HID, dtype=torch.float32, device=gpu)
+    ops.moe_shared(ex["ptbl_sh"], dx, ex["iq4nl"], sact, shared)
+    y = torch.empty(P, moe.HID, dtype=torch.float32, device=gpu)
+    ops.moe_combine(parts, gates, torch.from_numpy(sg).to(gpu), shared, torch.from_numpy(hres).to(gpu), y)
+    torch.cuda.synchronize()
+    return {k: v.cpu().numpy() for k, v in dict(eids=eids, gates=gates, eoff=eoff, plist=plist, items=items,
+                                                   nitp=nitp, act=act, parts=parts, shared=shared, y=y).items()}
+
+
+def _inputs(rng, P):
+    x = synth.bf16_round(0.05 * rng.standard_normal((P, moe.HID)).astype(np.float32))
+    logits = rng.standard_normal((P, moe.E)).astype(np.float32)
+    sg = (1.0 / (1.0 + np.exp(-rng.standard_normal(P)))).astype(np.float32)
+    hres = rng.standard_normal((P, moe.HID)).astype(np.float32)
+    return x, logits, sg, hres
+
+
+def test_moe_topk_ties_and_gates(gpu):
+    print("[case] moe topk P=300 with planted ties", flush=True)
+    rng = np.random.default_rng(11)
+    P = 300
+    lg = rng.standard_normal((P, moe.E)).astype(np.float32)
+    for p in range(0, P, 2):
+        top = np.argsort(-lg[p])[:10]
+        lg[p, top[6]] = lg[p, top[3]]
+        lg[p, rng.integers(0, moe.E)] = lg[p, top[0]]
+    eids = torch.empty(P, 8, dtype=torch.int16, device=gpu)
+    gates = torch.empty(P, 8, dtype=torch.float32, device=gpu)
+    ops.moe_topk(torch.from_numpy(lg).to(gpu), eids, gates)
+    torch.cuda.synchronize()
+    ref_e, ref_g = moe.topk_ref(lg)
+    assert np.array_equal(eids.cpu().numpy().view(np.uint16), ref_e)
+    np.testing.assert_allclose(gates.cpu().numpy(), ref_g, rtol=2e-6, atol=1e-7)
+
+
+def test_moe_route(gpu):
+    print("[case] moe route P=16", flush=True)
+    rng = np.random.default_rng(12)
+    P = 16
+    wrt = (rng.standard_normal((moe.E, moe.HID)) * 0.02).astype(np.float32)
+    wsh = (rng.standard_normal(moe.HID) * 0.02).astype(np.float32)
+    h = rng.standard_normal((P, moe.HID)).astype(np.float32)
+    eids = torch.empty(P, 8, dtype=torch.int16, device=gpu)
+    gates = torch.empty(P, 8, dtype=torch.float32, device=gpu)
+    sg = torch.empty(P, dtype=torch.float32, device=gpu)
+    ops.moe_route(torch.from_numpy(wrt).to(gpu), torch.from_numpy(wsh).to(gpu), torch.from_numpy(h).to(gpu),
+                  eids, gates, sg)
+    torch.cuda.synchronize()
+    lg64, ref_e, ref_g, ref_sg = moe.route_ref(wrt, wsh, h)
+    got = eids.cpu().numpy().view(np.uint16)
+    checked = 0
+    for p in range(P):
+        srt = np.sort(lg64[p])[::-1]
+        if np.min(np.abs(np.diff(srt[:9]))) < 1e-4:   # fp32 summation order could flip a near-tie
+            continue
+        assert np.array_equal(got[p], ref_e[p]), p
+        np.testing.assert_allclose(gates.cpu().numpy()[p], ref_g[p], rtol=1e-4)
+        checked += 1
+    assert checked >= P // 2
+    np.testing.assert_allclose(sg.cpu().numpy(), ref_sg, rtol=1e-5)
+
+
+@pytest.mark.parametrize("P", [11, 2048])
+def test_moe_sort(gpu, P):
+    print(f"[case] moe sort P={P}", flush=True)
+    rng = np.random.default_rng(13 + P)
+    ref_e, _ = moe.topk_ref(rng.standard_normal((P, moe.E)).astype(np.float32))
+    np_ = 8 * P
+    eids = torch.from_numpy(ref_e.view(np.int16)).to(gpu)
+    eoff = torch.empty(257, dtype=torch.int32, device=gpu)
+    plist = torch.empty(np_, dtype=torch.int16, device=gpu)
+    items = torch.empty(ops.moe_max_items(np_), dtype=torch.int32, device=gpu)
+    nitp = torch.empty(1, dtype=torch.int32, device=gpu)
+    ops.moe_sort(eids, eoff, plist, items, nitp)
+    torch.cuda.synchronize()
+    ref_off, ref_pl = moe.sort_ref(ref_e)
+    assert np.array_equal(eoff.cpu().numpy(), ref_off)
+    assert np.array_equal(plist.cpu().numpy().view(np.uint16), ref_pl)
+    cnt = np.diff(ref_off)
+    want = [(e << 16) | k for e in range(moe.E) for k in range(0, int(cnt[e]), 64)]
+    n = int(nitp.cpu().numpy()[0])
+    assert n == len(want)
+    assert np.array_equal(items.cpu().numpy().view(np.uint32)[:n], np.array(want, dtype=np.uint32))
+
+
+def _check_layer(ex, x, logits, sg, hres, out, pairs, positions):
+    """Compares the sampled pairs' act/parts and the sampled positions' y with the oracle."""
+    eids, gates = moe.topk_ref(logits)
+    assert np.array_equal(out["eids"].view(np.uint16), eids)
+    by_e = {}
+    for pair in pairs:
+        by_e.setdefault(int(eids[pair // 8, pair % 8]), []).append(pair)
+    for e, prs in by_e.items():
+        xa = x[[p // 8 for p in prs]]
+        act = moe.up_ref(ex["gu"][e], xa)
+        assert _rows_err(out["act"][prs], act) <= TOL, e
+        part = moe.down_ref(ex["dn"][e], act)
+        assert _rows_err(out["parts"][prs].astype(np.float64), part) <= TOL, e
+    sh = moe.down_ref(ex["dn"][moe.E], moe.up_ref(ex["gu"][moe.E], x[positions]))
+    assert _rows_err(out["shared"][positions], sh) <= TOL
+    # y from the GPU's own parts/shared (the combine alone): float32 rounding of ~10 operations,
+    # bounded relative to the magnitude of the summands (the sum itself can cancel)
+    pp = out["parts"][[8 * p + r for p in positions for r in range(8)]].reshape(len(positions), 8, moe.HID)
+    g, s_, h = out["gates"][positions], sg[positions], hres[positions]
+    yref = moe.combine_ref(pp, g, s_, out["shared"][positions], h)
+    scale = np.abs(h) + np.einsum("pr,prk->pk", np.abs(g), np.abs(pp.astype(np.float64))) \
+        + np.abs(s_)[:, None] * np.abs(out["shared"][positions])
+    assert np.all(np.abs(out["y"][positions] - yref) <= 4e-6 * scale + 1e-30)
+
+
+def test_moe_layer_decode_m11(gpu, experts):
+    print("[case] moe layer P=11", flush=True)
+    rng = np.random.default_rng(21)
+    P = 11
+    x, logits, sg, hres = _inputs(rng, P)
+    out = _run_layer(gpu, experts, x, logits, sg, hres)
+    _check_layer(experts, x, logits, sg, hres, out, list(range(8 * P)), list(range(P)))
+
+
+def test_moe_layer_prefill_m2048_sampled(gpu, experts):
+    print("[case] moe layer P=2048", flush=True)
+    rng = np.random.default_rng(22)
+    P = 2048
+    x, logits, sg, hres = _inputs(rng, P)
+    out = _run_layer(gpu, experts, x, logits, sg, hres)
+    srng = np.random.default_rng(5)
+    pairs = sorted(srng.choice(8 * P, 96, replace=False).tolist())
+    positions = sorted(srng.choice(P, 24, replace=False).tolist())
+    _check_layer(experts, x, logits, sg, hres, out, pairs, positions)
+    assert np.isfinite(out["y"]).all()
+
+
+def test_moe_layer_deterministic(gpu, experts):
+    print("[case] moe determinism P=256", flush=True)
+    rng = np.random.default_rng(23)
+    x, logits, sg, hres = _inputs(rng, 256)
+    a = _run_layer(gpu, experts, x, logits, sg, hres)
+    b = _run_layer(gpu, experts, x, logits, sg, hres)
+    for k in ("plist", "act", "parts", "shared", "y"):
+        assert np.array_equal(a[k], b[k]), k
+
+
+def test_moe_bad_arguments(gpu, experts):
+    print("[case] moe argument checks", flush=True)
+    z = torch.zeros(16, dtype=torch.int32, device=gpu)
+    with pytest.raises(TlxError):
+        ops.moe_sort(torch.zeros(16385 * 8, dtype=torch.int16, device=gpu)[:16385], z, z, z, z)
+    with pytest.raises(TlxError):
+        ops.moe_topk(torch.zeros(0, 256, dtype=torch.float32, device=gpu), z, z)

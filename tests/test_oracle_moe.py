@@ -1,0 +1,82 @@
+"""Pins the MoE oracle (router top-8, sort, expert FFN, combine) against library routines and
+closed forms, independently of how the oracle restates them."""
+import numpy as np
+import pytest
+from scipy.special import expit, softmax
+
+from oracle import moe
+
+
+def _logits_with_ties(rng, P):
+    lg = rng.standard_normal((P, moe.E)).astype(np.float32)
+    for p in range(0, P, 3):           # plant exact ties among the leaders
+        top = np.argsort(-lg[p])[:10]
+        lg[p, top[5]] = lg[p, top[2]]
+        lg[p, rng.integers(0, moe.E)] = lg[p, top[0]]
+    return lg
+
+
+def test_topk_matches_stable_argsort_and_softmax():
+    rng = np.random.default_rng(0)
+    lg = _logits_with_ties(rng, 40)
+    eids, gates = moe.topk_ref(lg)
+    want = np.argsort(-lg, axis=1, kind="stable")[:, :moe.TOPK]   # ties: lower id first
+    assert np.array_equal(eids.astype(np.int64), want)
+    for p in range(lg.shape[0]):
+        np.testing.assert_allclose(gates[p], softmax(lg[p, want[p]].astype(np.float64)), rtol=1e-6)
+
+
+def test_route_shared_gate_is_sigmoid_of_dot():
+    rng = np.random.default_rng(1)
+    wrt = rng.standard_normal((moe.E, moe.HID)).astype(np.float32) * 0.02
+    wsh = rng.standard_normal(moe.HID).astype(np.float32) * 0.02
+    h = rng.standard_normal((3, moe.HID)).astype(np.float32)
+    lg64, eids, _, sg = moe.route_ref(wrt, wsh, h)
+    np.testing.assert_allclose(lg64, np.einsum("ek,pk->pe", wrt.astype(np.float64), h.astype(np.float64)), rtol=1e-12)
+    np.testing.assert_allclose(sg, expit(h.astype(np.float64) @ wsh.astype(np.float64)), rtol=1e-6)
+    assert eids.shape == (3, moe.TOPK)
+
+
+@pytest.mark.parametrize("n", [1, 88, 1000])
+def test_sort_matches_python_sorted(n):
+    rng = np.random.default_rng(n)
+    e = rng.integers(0, moe.E, size=n).astype(np.uint16)
+    eoff, plist = moe.sort_ref(e)
+    assert np.array_equal(plist.astype(np.int64), np.array(sorted(range(n), key=lambda i: (int(e[i]), i))))
+    assert np.array_equal(eoff, np.searchsorted(np.sort(e.astype(np.int64)), np.arange(moe.E + 1)))
+
+
+def _const_iq4_rows(rows, kdim, qbyte):
+    """IQ4_XS rows whose every weight is kv[qbyte & 15] (low) / kv[qbyte >> 4] (high):
+    d = 1.0, ls = 33 for every group (dl = 1)."""
+    blk = np.zeros(136, dtype=np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[2:4] = np.frombuffer(np.uint16(0xAAAA).tobytes(), np.uint8)   # high 2 bits of ls = 2
+    blk[4:8] = 0x11                                                    # low 4 bits of ls = 1
+    blk[8:136] = qbyte
+    return np.tile(blk, (rows, kdim // 256))
+
+
+def test_expert_ffn_closed_form():
+    # kv[8] = 1: every gate/up weight is 1, so g = u = sum(x); every down weight kv[9] = 13
+    gu = np.concatenate([_const_iq4_rows(moe.FF, moe.HID, 0x88).ravel(), _const_iq4_rows(moe.FF, moe.HID, 0x88).ravel()])
+    dn = _const_iq4_rows(moe.HID, moe.FF, 0x99).ravel()
+    x = np.random.default_rng(2).standard_normal((4, moe.HID))
+    s = x.sum(axis=1)
+    act = moe.up_ref(gu, x)
+    np.testing.assert_allclose(act, np.repeat((s / (1 + np.exp(-s)) * s)[:, None], moe.FF, axis=1), rtol=1e-12)
+    part = moe.down_ref(dn, act)
+    np.testing.assert_allclose(part, np.repeat(13.0 * act.sum(axis=1)[:, None], moe.HID, axis=1), rtol=1e-12)
+
+
+def test_combine_one_hot_gates():
+    rng = np.random.default_rng(3)
+    P = 5
+    parts = rng.standard_normal((P, moe.TOPK, moe.HID))
+    gates = np.zeros((P, moe.TOPK))
+    gates[np.arange(P), np.arange(P) % moe.TOPK] = 1.0
+    sg = rng.random(P)
+    shared = rng.standard_normal((P, moe.HID))
+    hres = rng.standard_normal((P, moe.HID))
+    y = moe.combine_ref(parts, gates, sg, shared, hres)
+    np.testing.assert_allclose(y, hres + parts[np.arange(P), np.arange(P) % moe.TOPK] + sg[:, None] * shared)

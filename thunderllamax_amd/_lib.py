@@ -40,6 +40,14 @@ SIGNATURES = {
     "tlx_pfg3_ffn": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_pfg3_iq3d": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_pfg3_iq3o": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "tlx_moe_topk": [_p, _p, _p, _i, _p],
+    "tlx_moe_route": [_p, _p, _p, _p, _p, _p, _i, _p],
+    "tlx_moe_sort": [_p, _p, _p, _p, _p, _i, _p],
+    "tlx_moe_max_items": [_i],
+    "tlx_moe_up4": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _p],
+    "tlx_moe_dn4": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _p],
+    "tlx_moe_shared": [_p, _p, _p, _p, _p, _i, _p],
+    "tlx_moe_combine": [_p, _p, _p, _p, _p, _p, _i, _p],
 }
 
 

@@ -1,0 +1,417 @@
+// MoE grouped-expert path for gfx950 (the reference's mm/ family): router top-8 + softmax,
+// deterministic expert sort, grouped IQ4_XS gate+up (SwiGLU) and down GEMMs on MFMA, and the
+// combine with the shared expert and the residual.
+//
+// Layouts (as the reference): routed expert e's gate/up slab at ptbl[e] -- 512 gate rows then
+// 512 up rows (GATE_B4 = 557,056 bytes apart), 1088 B per row (8 IQ4_XS blocks of 136 B,
+// k = 2048); its down slab at ptbl_dn[e] -- 2048 rows x 272 B (k = 512).  Pairs are
+// position-major, rank ascending: pair = 8 * pos + rank.
+//
+// Grouped GEMM design: a workgroup owns (expert, chunk of up to 64 of its pairs, stripe of 128
+// weight rows -- 64 gate + 64 up for the FFN, 128 rows for down); per 32-k step the 256
+// threads stage the 64 activation rows (gathered through the sorted pair list, converted to
+// fp16) and dequantize the 128 x 32 weights into LDS, then 4 waves run 16 pairs x 128 rows of
+// v_mfma_f32_16x16x32_f16 each.  IQ4_XS decode: a 256-entry LDS table maps a quant byte to
+// (kv[lo], kv[hi]) as fp16, so one lookup yields the two weights that byte holds (elements j
+// and j+16 of the group); the MFMA k order is chosen to pair them (A is staged in the same
+// order), and the group scale d*(ls-32) multiplies in fp16.
+#include "tlx_common.h"
+
+namespace {
+
+constexpr int kE = 256, kTopK = 8, kHid = 2048, kFf = 512;
+constexpr int kGateBytes = kFf * 1088;     // GATE_B4
+
+// ------------------------------------------------------------------ router
+// 8 masked-argmax passes over one position's 256 logits held 4 per lane (lane l: experts
+// l, l+64, l+128, l+192), wave-wide: larger value wins, equal values go to the lower id.
+__device__ __forceinline__ void topk8_wave(float v[4], int lane, uint16_t* eids, float* gates) {
+  float m = -3.402823466e38f, ex[kTopK], s8 = 0.f;
+  int ids[kTopK];
+#pragma unroll
+  for (int r = 0; r < kTopK; ++r) {
+    float bv = v[0];
+    int bi = lane;
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+      if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if (r == 0) m = bv;
+    ids[r] = bi;
+    ex[r] = expf(bv - m);
+    s8 += ex[r];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (bi == lane + 64 * j) v[j] = -3.402823466e38f;
+  }
+  if (lane < kTopK) {
+    int id = ids[0];
+    float e = ex[0];
+#pragma unroll
+    for (int r = 1; r < kTopK; ++r)
+      if (lane == r) { id = ids[r]; e = ex[r]; }
+    eids[lane] = (uint16_t)id;
+    gates[lane] = e / s8;
+  }
+}
+
+// one wave per position, 4 positions per 256-thread workgroup
+__global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__ logits, uint16_t* __restrict__ eids,
+                                                       float* __restrict__ gates, int P) {
+  const int p = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (p >= P) return;
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = logits[(size_t)p * kE + lane + 64 * j];
+  topk8_wave(v, lane, eids + (size_t)p * kTopK, gates + (size_t)p * kTopK);
+}
+
+// rt8e256: logits = wrt . h, shared gate sg = sigmoid(wsh . h), then the top-8.  One 256-thread
+// workgroup per position; logit e is thread e's fixed-order sum (4-way split of k, then the
+// partials in order), the shared gate a fixed-order tree.
+__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ wrt, const float* __restrict__ wsh,
+                                                        const float* __restrict__ h, uint16_t* __restrict__ eids,
+                                                        float* __restrict__ gates, float* __restrict__ sg) {
+  __shared__ float lg[kE];
+  __shared__ float shp[256];
+  const int p = blockIdx.x, t = threadIdx.x;
+  const float4* hr = reinterpret_cast<const float4*>(h + (size_t)p * kHid);
+  {
+    const float4* wr = reinterpret_cast<const float4*>(wrt + (size_t)t * kHid);
+    float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int i = 0; i < kHid / 16; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 w = wr[q * (kHid / 16) + i], x = hr[q * (kHid / 16) + i];
+        part[q] += w.x * x.x + w.y * x.y + w.z * x.z + w.w * x.w;
+      }
+    }
+    lg[t] = ((part[0] + part[1]) + part[2]) + part[3];
+    const float2* ws2 = reinterpret_cast<const float2*>(wsh);
+    const float2* hr2 = reinterpret_cast<const float2*>(h + (size_t)p * kHid);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float2 a = ws2[t + 256 * i], b = hr2[t + 256 * i];
+      s += a.x * b.x + a.y * b.y;
+    }
+    shp[t] = s;
+  }
+  __syncthreads();
+  for (int w = 128; w >= 1; w >>= 1) {
+    if (t < w) shp[t] += shp[t + w];
+    __syncthreads();
+  }
+  if (t < 64) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = lg[t + 64 * j];
+    topk8_wave(v, t, eids + (size_t)p * kTopK, gates + (size_t)p * kTopK);
+    if (t == 0) sg[p] = 1.f / (1.f + expf(-shp[0]));
+  }
+}
+
+// ------------------------------------------------------------------ sort
+// Stable counting sort of the pairs by expert, no atomics: chunk histograms (chunk c = pairs
+// [256c, 256c+256), counted by thread c), per-expert prefix over chunks, then each pair's rank
+// inside its chunk.  Items: per expert, ceil(count / 64) chunks of its pairs, expert ascending,
+// item = expert << 16 | first pair offset in the bin.
+constexpr int kSortChunk = 256;
+constexpr int kMaxPairs = 16384;
+constexpr int kTok = 64;
+
+__global__ __launch_bounds__(1024) void moe_sort_kernel(const uint16_t* __restrict__ eids, int* __restrict__ eoff,
+                                                        uint16_t* __restrict__ plist, uint32_t* __restrict__ items,
+                                                        uint32_t* __restrict__ nitp, int np) {
+  __shared__ uint16_t se[kMaxPairs];
+  __shared__ uint16_t hist[kMaxPairs / kSortChunk][kE];   // chunk c, expert e: count, then base
+  __shared__ int eo[kE + 1];
+  const int t = threadIdx.x;
+  const int nch = (np + kSortChunk - 1) / kSortChunk;
+  for (int i = t; i < np; i += 1024) se[i] = eids[i] & 0xFFu;   // ids are < 256 by contract; never index past the tables
+  for (int i = t; i < nch * kE; i += 1024) hist[i / kE][i % kE] = 0;
+  __syncthreads();
+  if (t < nch) {
+    const int i1 = min(np, (t + 1) * kSortChunk);
+    for (int i = t * kSortChunk; i < i1; ++i) hist[t][se[i]]++;
+  }
+  __syncthreads();
+  if (t < kE) {   // expert t: exclusive prefix over chunks
+    int s = 0;
+    for (int c = 0; c < nch; ++c) {
+      const int v = hist[c][t];
+      hist[c][t] = (uint16_t)s;
+      s += v;
+    }
+    eo[t] = s;   // the count, for now
+  }
+  __syncthreads();
+  if (t == 0) {
+    int s = 0, b = 0;
+    for (int e = 0; e < kE; ++e) {
+      const int c = eo[e];
+      eoff[e] = s;
+      for (int k = 0; k < c; k += kTok) items[b++] = ((uint32_t)e << 16) | (uint32_t)k;
+      eo[e] = s;
+      s += c;
+    }
+    eoff[kE] = s;
+    eo[kE] = s;
+    *nitp = (uint32_t)b;
+  }
+  __syncthreads();
+  for (int i = t; i < np; i += 1024) {
+    const int e = se[i], c = i / kSortChunk;
+    int r = 0;
+    for (int j = c * kSortChunk; j < i; ++j) r += (se[j] == e);
+    plist[eo[e] + hist[c][e] + r] = (uint16_t)i;
+  }
+}
+
+// ------------------------------------------------------------------ grouped IQ4_XS GEMM
+enum MoeKind { MOE_UP = 0, MOE_DN = 1, MOE_DN_DENSE = 2, MOE_UP_DENSE = 3 };
+
+template <int KIND> struct MoeShape;
+template <> struct MoeShape<MOE_UP> { static constexpr int K = kHid, ROWS = kFf, STRIPES = kFf / 64; };
+template <> struct MoeShape<MOE_UP_DENSE> { static constexpr int K = kHid, ROWS = kFf, STRIPES = kFf / 64; };
+template <> struct MoeShape<MOE_DN> { static constexpr int K = kFf, ROWS = kHid, STRIPES = kHid / 128; };
+template <> struct MoeShape<MOE_DN_DENSE> { static constexpr int K = kFf, ROWS = kHid, STRIPES = kHid / 128; };
+
+struct __attribute__((aligned(16))) MoeLds {
+  _Float16 a[2][kTok * 32];      // activations, fragment order (16-B piece p of row R at ((R/16)*64 + p*16 + R%16))
+  _Float16 b[2][128 * 32];       // dequantized weights, same order
+  uint32_t lut[256];             // quant byte -> (kv[lo], kv[hi]) fp16
+  int xrow[kTok];                // activation row of token slot t
+  int orow[kTok];                // output row of token slot t
+};
+
+__device__ __forceinline__ int moe_frag(int R, int p) { return ((R >> 4) * 64 + p * 16 + (R & 15)) * 8; }
+
+template <int KIND>
+__global__ __launch_bounds__(256) void moe_gemm_kernel(const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff,
+                                                       const uint16_t* __restrict__ plist,
+                                                       const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp,
+                                                       const float* __restrict__ xs, const float* __restrict__ iq4nl,
+                                                       void* __restrict__ out, int P) {
+  using S = MoeShape<KIND>;
+  constexpr bool kDense = KIND == MOE_DN_DENSE || KIND == MOE_UP_DENSE;
+  constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
+  constexpr int kRowBytes = (S::K / 256) * 136;
+  __shared__ MoeLds L;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int col = lane & 15, kq = lane >> 4;
+
+  // work item: expert, first pair of the chunk, number of pairs; stripe from blockIdx.y
+  int e, m0, ntok;
+  const uint8_t* base;
+  if constexpr (kDense) {
+    e = 0;
+    m0 = (int)blockIdx.x * kTok;
+    ntok = min(kTok, P - m0);
+    base = reinterpret_cast<const uint8_t*>(ptbl[0]);
+  } else {
+    if (blockIdx.x >= *nitp) return;
+    const uint32_t it = items[blockIdx.x];
+    e = (int)(it >> 16);
+    m0 = (int)(it & 0xFFFFu);
+    const int eb0 = eoff[e];
+    ntok = min(kTok, eoff[e + 1] - eb0 - m0);
+    m0 += eb0;
+    base = reinterpret_cast<const uint8_t*>(ptbl[e]);
+  }
+  const int s = blockIdx.y;
+
+  if (t < kTok) {
+    const int slot = min(t, ntok - 1);   // padded slots repeat the last pair; never stored
+    if constexpr (kDense) {
+      L.xrow[t] = m0 + slot;
+      L.orow[t] = m0 + slot;
+    } else {
+      const int pair = plist[m0 + slot];
+      L.xrow[t] = kUp ? (pair >> 3) : pair;
+      L.orow[t] = pair;
+    }
+  }
+  {
+    const int v = t;   // 256 table entries, one per thread
+    const _Float16 lo = (_Float16)iq4nl[v & 15], hi = (_Float16)iq4nl[v >> 4];
+    L.lut[v] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+  }
+  __syncthreads();
+
+  // staging roles: activations -- token slot t/4, k-pieces {4j..4j+3} and {16+4j..} (j = t%4);
+  // weights -- tile row t/2, quant bytes 8h..8h+7 of the group (h = t%2)
+  const int at = t >> 2, aj = t & 3;
+  const float* xr = xs + (size_t)L.xrow[at] * S::K;
+  const int br = t >> 1, bh = t & 1;
+  const uint8_t* wrow;
+  if constexpr (kUp) wrow = base + (br >= 64 ? kGateBytes : 0) + (size_t)(64 * s + (br & 63)) * kRowBytes;
+  else wrow = base + (size_t)(128 * s + br) * kRowBytes;
+
+  auto stage = [&](int g, int buf) {
+    // activations: x[4j..4j+3] and x[16+4j..19+4j] of group g, interleaved (the pairing of
+    // the weight bytes' low and high nibbles)
+    const float4 x0 = *reinterpret_cast<const float4*>(xr + 32 * g + 4 * aj);
+    const float4 x1 = *reinterpret_cast<const float4*>(xr + 32 * g + 16 + 4 * aj);
+    const h8_t av = {(_Float16)x0.x, (_Float16)x1.x, (_Float16)x0.y, (_Float16)x1.y,
+                     (_Float16)x0.z, (_Float16)x1.z, (_Float16)x0.w, (_Float16)x1.w};
+    *reinterpret_cast<h8_t*>(L.a[buf] + moe_frag(at, aj)) = av;
+    // weights: block g/8, group ib = g%8
+    const uint8_t* blk = wrow + 136 * (g >> 3);
+    const int ib = g & 7;
+    const u2_t hdr = *reinterpret_cast<const u2_t*>(blk);           // d | sh << 16, sl
+    const u2_t q = *reinterpret_cast<const u2_t*>(blk + 8 + 16 * ib + 8 * bh);
+    const uint32_t sh = hdr.x >> 16;
+    const uint32_t ls = ((hdr.y >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xFu) | (((sh >> (2 * ib)) & 3u) << 4);
+    const float dl = tlx_h2f((uint16_t)hdr.x) * (float)((int)ls - 32);
+    const _Float16 dh = (_Float16)dl;
+    const h8_t dv = {dh, dh, dh, dh, dh, dh, dh, dh};
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const uint32_t qw = c ? q.y : q.x;
+      const u4_t w4 = {L.lut[qw & 0xFF], L.lut[(qw >> 8) & 0xFF], L.lut[(qw >> 16) & 0xFF], L.lut[qw >> 24]};
+      const h8_t wv = __builtin_bit_cast(h8_t, w4) * dv;
+      *reinterpret_cast<h8_t*>(L.b[buf] + moe_frag(br, 2 * bh + c)) = wv;
+    }
+  };
+
+  f4_t acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  constexpr int kSteps = S::K / 32;
+  stage(0, 0);
+  __syncthreads();
+  for (int g = 0; g < kSteps; ++g) {
+    const int buf = g & 1;
+    if (g + 1 < kSteps) stage(g + 1, buf ^ 1);
+    const h8_t af = *reinterpret_cast<const h8_t*>(L.a[buf] + 512 * wave + 8 * lane);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const h8_t bf = *reinterpret_cast<const h8_t*>(L.b[buf] + 512 * j + 8 * lane);
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[j], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+
+  // lane (col, kq) holds tokens 16*wave + 4kq + r, rows 16j + col of the stripe tile
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int slot = 16 * wave + 4 * kq + r;
+    if (slot >= ntok) break;
+    const int orow = L.orow[slot];
+    if constexpr (kUp) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float gv = acc[j][r], uv = acc[j + 4][r];
+        reinterpret_cast<float*>(out)[(size_t)orow * kFf + 64 * s + 16 * j + col] = gv / (1.f + expf(-gv)) * uv;
+      }
+    } else if constexpr (KIND == MOE_DN) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        reinterpret_cast<uint16_t*>(out)[(size_t)orow * kHid + 128 * s + 16 * j + col] = tlx_f2h_bits(acc[j][r]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        reinterpret_cast<float*>(out)[(size_t)orow * kHid + 128 * s + 16 * j + col] = acc[j][r];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ combine
+// y = hres + (sum_r g_r * part_r (r ascending) + sg * shared), fp32; 8 elements per thread.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ parts, const float* __restrict__ gates,
+                                                          const float* __restrict__ sg, const float* __restrict__ shared,
+                                                          const float* __restrict__ hres, float* __restrict__ y) {
+  const int p = blockIdx.x, i0 = 8 * threadIdx.x;
+  float g[kTopK];
+#pragma unroll
+  for (int r = 0; r < kTopK; ++r) g[r] = gates[p * kTopK + r];
+  const float sgp = sg[p];
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < kTopK; ++r) {
+    const h8_t v = *reinterpret_cast<const h8_t*>(parts + ((size_t)p * kTopK + r) * kHid + i0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] = __builtin_fmaf(g[r], (float)v[k], acc[k]);
+  }
+  const float* sh = shared + (size_t)p * kHid + i0;
+  const float* hr = hres + (size_t)p * kHid + i0;
+  float* yo = y + (size_t)p * kHid + i0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) yo[k] = hr[k] + __builtin_fmaf(sgp, sh[k], acc[k]);
+}
+
+int moe_max_items(int np) { return (np + kTok - 1) / kTok + kE; }
+
+}  // namespace
+
+extern "C" int tlx_moe_topk(const float* logits, uint16_t* eids, float* gates, int P, void* stream) {
+  TLX_RET_IF(P < 1, TLX_E_ARG);
+  moe_topk_kernel<<<(P + 3) / 4, 256, 0, (hipStream_t)stream>>>(logits, eids, gates, P);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_moe_route(const float* wrt, const float* wsh, const float* h, uint16_t* eids, float* gates,
+                             float* sg, int P, void* stream) {
+  TLX_RET_IF(P < 1, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(wrt, 16) || !tlx_aligned(h, 16) || !tlx_aligned(wsh, 8), TLX_E_ALIGN);
+  moe_route_kernel<<<P, 256, 0, (hipStream_t)stream>>>(wrt, wsh, h, eids, gates, sg);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_moe_sort(const uint16_t* eids, int* eoff, uint16_t* plist, uint32_t* items, uint32_t* nitp,
+                            int np, void* stream) {
+  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+  moe_sort_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(eids, eoff, plist, items, nitp, np);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_moe_max_items(int np) { return moe_max_items(np); }
+
+extern "C" int tlx_moe_up4(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const uint32_t* items,
+                           const uint32_t* nitp, const float* xs, const float* iq4nl, float* ys, int np, void* stream) {
+  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(xs, 16), TLX_E_ALIGN);
+  const dim3 grid(moe_max_items(np), MoeShape<MOE_UP>::STRIPES);
+  moe_gemm_kernel<MOE_UP><<<grid, 256, 0, (hipStream_t)stream>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, 0);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_moe_dn4(const uint64_t* ptbl_dn, const int* eoff, const uint16_t* plist, const uint32_t* items,
+                           const uint32_t* nitp, const float* act, const float* iq4nl, uint16_t* parts, int np,
+                           void* stream) {
+  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(act, 16) || !tlx_aligned(parts, 16), TLX_E_ALIGN);
+  const dim3 grid(moe_max_items(np), MoeShape<MOE_DN>::STRIPES);
+  moe_gemm_kernel<MOE_DN><<<grid, 256, 0, (hipStream_t)stream>>>(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const float* iq4nl, float* act, float* out,
+                              int P, void* stream) {
+  TLX_RET_IF(P < 1, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(xs, 16) || !tlx_aligned(act, 16), TLX_E_ALIGN);
+  const int chunks = (P + kTok - 1) / kTok;
+  moe_gemm_kernel<MOE_UP_DENSE><<<dim3(chunks, MoeShape<MOE_UP>::STRIPES), 256, 0, (hipStream_t)stream>>>(
+      ptbl_sh, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, act, P);
+  int rc = tlx_launch_status();
+  TLX_RET_IF(rc != TLX_OK, rc);
+  moe_gemm_kernel<MOE_DN_DENSE><<<dim3(chunks, MoeShape<MOE_DN>::STRIPES), 256, 0, (hipStream_t)stream>>>(
+      ptbl_sh + 1, nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_moe_combine(const uint16_t* parts, const float* gates, const float* sg, const float* shared,
+                               const float* hres, float* y, int P, void* stream) {
+  TLX_RET_IF(P < 1, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(parts, 16), TLX_E_ALIGN);
+  moe_combine_kernel<<<P, 256, 0, (hipStream_t)stream>>>(parts, gates, sg, shared, hres, y);
+  return tlx_launch_status();
+}

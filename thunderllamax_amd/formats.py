@@ -69,3 +69,9 @@ def iq4nl_tensor(device="cuda"):
     """The IQ4_NL level buffer (float32[16])."""
     import torch
     return torch.from_numpy(iq4nl_f32()).to(device)
+
+
+def pointer_table(tensors, device="cuda"):
+    """Device int64 array of the tensors' device addresses (the MoE per-expert slab table)."""
+    import torch
+    return torch.tensor([t.data_ptr() for t in tensors], dtype=torch.int64, device=device)

@@ -129,3 +129,59 @@ def pfg3_iq3o(w, gridf, x16, out16, layout=LAYOUT_PACK7, stream=None):
     call("tlx_pfg3_iq3o", w.data_ptr(), gridf.data_ptr(), x16.data_ptr(), out16.data_ptr(), M, N, K, layout,
          _stream(stream))
     return out16
+
+
+# ------------------------------------------------------------------ MoE grouped experts
+# 256 routed experts + 1 shared, hidden 2048, expert intermediate 512, top-8, IQ4_XS weights.
+# ptbl / ptbl_dn: int64 device tensors of 256 slab addresses (formats.pointer_table).
+def moe_topk(logits, eids, gates, stream=None):
+    """Top-8 + renormalized softmax from router logits [P][256] (the rt8e256 epilogue)."""
+    _dev(logits, eids, gates)
+    call("tlx_moe_topk", logits.data_ptr(), eids.data_ptr(), gates.data_ptr(), logits.shape[0], _stream(stream))
+
+
+def moe_route(wrt, wsh, h, eids, gates, sg, stream=None):
+    """rt8e256(wrt, wsh, h, eids, gates, sg)."""
+    _dev(wrt, wsh, h, eids, gates, sg)
+    call("tlx_moe_route", wrt.data_ptr(), wsh.data_ptr(), h.data_ptr(), eids.data_ptr(), gates.data_ptr(),
+         sg.data_ptr(), h.shape[0], _stream(stream))
+
+
+def moe_max_items(npair):
+    from ._lib import lib
+    return lib().tlx_moe_max_items(npair)
+
+
+def moe_sort(eids, eoff, plist, items, nitp, stream=None):
+    """mmsort8(eids, eoff, plist, items, nitp, np) with np = eids.numel()."""
+    _dev(eids, eoff, plist, items, nitp)
+    call("tlx_moe_sort", eids.data_ptr(), eoff.data_ptr(), plist.data_ptr(), items.data_ptr(), nitp.data_ptr(),
+         eids.numel(), _stream(stream))
+
+
+def moe_up4(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, stream=None):
+    """ys[pair][512] = silu(Wg_e . x[pos]) * (Wu_e . x[pos])   (gx8e256up4 / gxu_gm)."""
+    _dev(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys)
+    call("tlx_moe_up4", ptbl.data_ptr(), eoff.data_ptr(), plist.data_ptr(), items.data_ptr(), nitp.data_ptr(),
+         xs.data_ptr(), iq4nl.data_ptr(), ys.data_ptr(), ys.shape[0], _stream(stream))
+
+
+def moe_dn4(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, stream=None):
+    """parts[pair][2048] = fp16(Wd_e . act[pair])   (gx8e256dn / gxd_gm)."""
+    _dev(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts)
+    call("tlx_moe_dn4", ptbl_dn.data_ptr(), eoff.data_ptr(), plist.data_ptr(), items.data_ptr(), nitp.data_ptr(),
+         act.data_ptr(), iq4nl.data_ptr(), parts.data_ptr(), act.shape[0], _stream(stream))
+
+
+def moe_shared(ptbl_sh, xs, iq4nl, act, out, stream=None):
+    """Shared expert over all positions: act [P][512] (scratch), out [P][2048] f32."""
+    _dev(ptbl_sh, xs, iq4nl, act, out)
+    call("tlx_moe_shared", ptbl_sh.data_ptr(), xs.data_ptr(), iq4nl.data_ptr(), act.data_ptr(), out.data_ptr(),
+         xs.shape[0], _stream(stream))
+
+
+def moe_combine(parts, gates, sg, shared, hres, y, stream=None):
+    """cmbz2048(parts, gates, sg, shared, hres, y)."""
+    _dev(parts, gates, sg, shared, hres, y)
+    call("tlx_moe_combine", parts.data_ptr(), gates.data_ptr(), sg.data_ptr(), shared.data_ptr(), hres.data_ptr(),
+         y.data_ptr(), y.shape[0], _stream(stream))

@@ -75,3 +75,12 @@ def activations_f16(rng, m, k):
     """bf16 N(0,1) activations quantized to fp16 the way the reference feeds its kernels
     (round-to-nearest-even ``__float2half``)."""
     return bf16_round(rng.standard_normal((m, k)).astype(np.float32)).astype(np.float16)
+
+
+def moe_expert_slabs(rng, n_experts):
+    """Config 5 expert weights: per expert a gate/up slab u8[2*512*1088] (512 gate rows, then
+    512 up rows, k = 2048) and a down slab u8[2048*272] (k = 512), GGUF IQ4_XS rows."""
+    gu = [np.concatenate([iq4xs_raw(rng, 512, 2048).ravel(), iq4xs_raw(rng, 512, 2048).ravel()])
+          for _ in range(n_experts)]
+    dn = [iq4xs_raw(rng, 2048, 512).ravel() for _ in range(n_experts)]
+    return gu, dn
