@@ -17,6 +17,8 @@
 // order), and the group scale d*(ls-32) multiplies in fp16.
 #include "tlx_common.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int kE = 256, kTopK = 8, kHid = 2048, kFf = 512;
@@ -118,80 +120,110 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
 }
 
 // ------------------------------------------------------------------ sort
-// Stable counting sort of the pairs by expert, no atomics: chunk histograms (chunk c = pairs
-// [256c, 256c+256), counted by thread c), per-expert prefix over chunks, then each pair's rank
-// inside its chunk.  Items: per expert, ceil(count / 64) chunks of its pairs, expert ascending,
-// item = expert << 16 | first pair offset in the bin.
-constexpr int kSortChunk = 256;
+// Stable counting sort of the pairs by expert, no atomics.  The pairs are taken in rounds of
+// 1024 (16 waves x 64 lanes, pair order = wave-major, lane-minor).  In a wave, 8 ballots over the
+// bits of the expert id give every lane the mask of lanes holding the same expert; its rank among
+// them is the popcount below it, and the lowest such lane writes the group's count.  Pass 1
+// accumulates the per-expert totals (-> eoff and the work items), pass 2 repeats the rounds and
+// scatters each pair to eoff[e] + (pairs of e in earlier rounds) + (in earlier waves of this
+// round) + (its rank in the wave).  Items: per expert, ceil(count / 64) chunks of its pairs,
+// expert ascending, item = expert << 16 | first pair offset in the bin.
 constexpr int kMaxPairs = 16384;
 constexpr int kTok = 64;
+constexpr int kSortWaves = 16;
+
+// lanes of this wave holding the same 8-bit key as this lane
+__device__ __forceinline__ uint64_t same_key_mask(uint32_t key) {
+  uint64_t m = ~0ull;
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const uint64_t bal = __ballot((key >> b) & 1u);
+    m &= ((key >> b) & 1u) ? bal : ~bal;
+  }
+  return m;
+}
 
 __global__ __launch_bounds__(1024) void moe_sort_kernel(const uint16_t* __restrict__ eids, int* __restrict__ eoff,
                                                         uint16_t* __restrict__ plist, uint32_t* __restrict__ items,
                                                         uint32_t* __restrict__ nitp, int np) {
-  __shared__ uint16_t se[kMaxPairs];
-  __shared__ uint16_t hist[kMaxPairs / kSortChunk][kE];   // chunk c, expert e: count, then base
-  __shared__ int eo[kE + 1];
-  const int t = threadIdx.x;
-  const int nch = (np + kSortChunk - 1) / kSortChunk;
-  for (int i = t; i < np; i += 1024) se[i] = eids[i] & 0xFFu;   // ids are < 256 by contract; never index past the tables
-  for (int i = t; i < nch * kE; i += 1024) hist[i / kE][i % kE] = 0;
-  __syncthreads();
-  if (t < nch) {
-    const int i1 = min(np, (t + 1) * kSortChunk);
-    for (int i = t * kSortChunk; i < i1; ++i) hist[t][se[i]]++;
-  }
-  __syncthreads();
-  if (t < kE) {   // expert t: exclusive prefix over chunks
-    int s = 0;
-    for (int c = 0; c < nch; ++c) {
-      const int v = hist[c][t];
-      hist[c][t] = (uint16_t)s;
-      s += v;
+  __shared__ uint16_t wcnt[kSortWaves][kE];   // this round: pairs of expert e in wave w
+  __shared__ int run[kE];                     // pairs of expert e before this round (pass 2: + eoff)
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int rounds = (np + 1023) / 1024;
+  if (t < kE) run[t] = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    for (int r = 0; r < rounds; ++r) {
+      for (int e = lane; e < kE; e += 64) wcnt[wave][e] = 0;
+      const int i = 1024 * r + t;
+      const bool valid = i < np;
+      const uint32_t key = valid ? (eids[i] & 0xFFu) : 0u;   // ids are < 256 by contract
+      uint64_t same = same_key_mask(key) & __ballot(valid);
+      if (!valid) same = 0;
+      const int rank = __builtin_popcountll(same & below);
+      __syncthreads();                                         // wcnt cleared
+      if (valid && rank == 0) wcnt[wave][key] = (uint16_t)__builtin_popcountll(same);
+      __syncthreads();
+      if (pass == 1 && valid) {
+        int pre = run[key];
+        for (int w = 0; w < wave; ++w) pre += wcnt[w][key];
+        plist[pre + rank] = (uint16_t)i;
+      }
+      __syncthreads();
+      if (t < kE) {
+        int s = 0;
+#pragma unroll
+        for (int w = 0; w < kSortWaves; ++w) s += wcnt[w][t];
+        run[t] += s;
+      }
+      __syncthreads();
     }
-    eo[t] = s;   // the count, for now
-  }
-  __syncthreads();
-  if (t == 0) {
-    int s = 0, b = 0;
-    for (int e = 0; e < kE; ++e) {
-      const int c = eo[e];
-      eoff[e] = s;
-      for (int k = 0; k < c; k += kTok) items[b++] = ((uint32_t)e << 16) | (uint32_t)k;
-      eo[e] = s;
-      s += c;
+    if (pass == 0) {
+      if (t == 0) {   // totals -> bin offsets and work items; run[] becomes the bin starts
+        int sum = 0, b = 0;
+        for (int e = 0; e < kE; ++e) {
+          const int c = run[e];
+          eoff[e] = sum;
+          for (int k = 0; k < c; k += kTok) items[b++] = ((uint32_t)e << 16) | (uint32_t)k;
+          run[e] = sum;
+          sum += c;
+        }
+        eoff[kE] = sum;
+        *nitp = (uint32_t)b;
+      }
+      __syncthreads();
     }
-    eoff[kE] = s;
-    eo[kE] = s;
-    *nitp = (uint32_t)b;
-  }
-  __syncthreads();
-  for (int i = t; i < np; i += 1024) {
-    const int e = se[i], c = i / kSortChunk;
-    int r = 0;
-    for (int j = c * kSortChunk; j < i; ++j) r += (se[j] == e);
-    plist[eo[e] + hist[c][e] + r] = (uint16_t)i;
   }
 }
 
 // ------------------------------------------------------------------ grouped IQ4_XS GEMM
 enum MoeKind { MOE_UP = 0, MOE_DN = 1, MOE_DN_DENSE = 2, MOE_UP_DENSE = 3 };
 
+// K: reduction length; TROWS: weight rows per workgroup tile (FFN: half gate, half up);
+// STRIPES: tiles per expert matrix
 template <int KIND> struct MoeShape;
-template <> struct MoeShape<MOE_UP> { static constexpr int K = kHid, ROWS = kFf, STRIPES = kFf / 64; };
-template <> struct MoeShape<MOE_UP_DENSE> { static constexpr int K = kHid, ROWS = kFf, STRIPES = kFf / 64; };
-template <> struct MoeShape<MOE_DN> { static constexpr int K = kFf, ROWS = kHid, STRIPES = kHid / 128; };
-template <> struct MoeShape<MOE_DN_DENSE> { static constexpr int K = kFf, ROWS = kHid, STRIPES = kHid / 128; };
+template <> struct MoeShape<MOE_UP> { static constexpr int K = kHid, TROWS = 256, STRIPES = kFf / 128; };
+template <> struct MoeShape<MOE_UP_DENSE> { static constexpr int K = kHid, TROWS = 256, STRIPES = kFf / 128; };
+template <> struct MoeShape<MOE_DN> { static constexpr int K = kFf, TROWS = 128, STRIPES = kHid / 128; };
+template <> struct MoeShape<MOE_DN_DENSE> { static constexpr int K = kFf, TROWS = 128, STRIPES = kHid / 128; };
 
 struct __attribute__((aligned(16))) MoeLds {
   _Float16 a[2][kTok * 32];      // activations, fragment order (16-B piece p of row R at ((R/16)*64 + p*16 + R%16))
-  _Float16 b[2][128 * 32];       // dequantized weights, same order
+  _Float16 b[2][256 * 32];       // dequantized weights, same order
   uint32_t lut[256];             // quant byte -> (kv[lo], kv[hi]) fp16
   int xrow[kTok];                // activation row of token slot t
   int orow[kTok];                // output row of token slot t
 };
 
 __device__ __forceinline__ int moe_frag(int R, int p) { return ((R >> 4) * 64 + p * 16 + (R & 15)) * 8; }
+
+// raw global data of one 32-k step for one thread (registers, prefetched two steps ahead)
+template <int TROWS>
+struct MoeRaw {
+  float4 x0, x1;                         // activations k 4j..4j+3 and 16+4j..19+4j
+  u2_t hdr;                              // block header: d | sh << 16, sl
+  std::conditional_t<TROWS == 256, u4_t, u2_t> q;   // quant bytes (16 or 8)
+};
 
 template <int KIND>
 __global__ __launch_bounds__(256) void moe_gemm_kernel(const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff,
@@ -203,18 +235,22 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const uint64_t* __restric
   constexpr bool kDense = KIND == MOE_DN_DENSE || KIND == MOE_UP_DENSE;
   constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
   constexpr int kRowBytes = (S::K / 256) * 136;
+  constexpr int kRG = S::TROWS / 64;     // 16-row groups per wave
   __shared__ MoeLds L;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const int col = lane & 15, kq = lane >> 4;
 
   // work item: expert, first pair of the chunk, number of pairs; stripe from blockIdx.y
+  // the slab address is loaded from a table: give it the global address space explicitly, or the
+  // compiler falls back to flat loads, whose completion every LDS wait would then also wait for
+  using gbyte = const __attribute__((address_space(1))) uint8_t;
   int e, m0, ntok;
-  const uint8_t* base;
+  gbyte* base;
   if constexpr (kDense) {
     e = 0;
     m0 = (int)blockIdx.x * kTok;
     ntok = min(kTok, P - m0);
-    base = reinterpret_cast<const uint8_t*>(ptbl[0]);
+    base = (gbyte*)(ptbl[0]);
   } else {
     if (blockIdx.x >= *nitp) return;
     const uint32_t it = items[blockIdx.x];
@@ -223,7 +259,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const uint64_t* __restric
     const int eb0 = eoff[e];
     ntok = min(kTok, eoff[e + 1] - eb0 - m0);
     m0 += eb0;
-    base = reinterpret_cast<const uint8_t*>(ptbl[e]);
+    base = (gbyte*)(ptbl[e]);
   }
   const int s = blockIdx.y;
 
@@ -246,80 +282,99 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const uint64_t* __restric
   __syncthreads();
 
   // staging roles: activations -- token slot t/4, k-pieces {4j..4j+3} and {16+4j..} (j = t%4);
-  // weights -- tile row t/2, quant bytes 8h..8h+7 of the group (h = t%2)
+  // weights -- FFN: tile row t (gate rows 128s.. for t < 128, then the up rows), all 16 quant
+  // bytes of the group; down: tile row t/2, quant bytes 8h..8h+7 (h = t%2)
   const int at = t >> 2, aj = t & 3;
   const float* xr = xs + (size_t)L.xrow[at] * S::K;
-  const int br = t >> 1, bh = t & 1;
-  const uint8_t* wrow;
-  if constexpr (kUp) wrow = base + (br >= 64 ? kGateBytes : 0) + (size_t)(64 * s + (br & 63)) * kRowBytes;
+  const int br = kUp ? t : (t >> 1), bh = kUp ? 0 : (t & 1);
+  gbyte* wrow;
+  if constexpr (kUp) wrow = base + (br >= 128 ? kGateBytes : 0) + (size_t)(128 * s + (br & 127)) * kRowBytes;
   else wrow = base + (size_t)(128 * s + br) * kRowBytes;
 
-  auto stage = [&](int g, int buf) {
-    // activations: x[4j..4j+3] and x[16+4j..19+4j] of group g, interleaved (the pairing of
-    // the weight bytes' low and high nibbles)
-    const float4 x0 = *reinterpret_cast<const float4*>(xr + 32 * g + 4 * aj);
-    const float4 x1 = *reinterpret_cast<const float4*>(xr + 32 * g + 16 + 4 * aj);
-    const h8_t av = {(_Float16)x0.x, (_Float16)x1.x, (_Float16)x0.y, (_Float16)x1.y,
-                     (_Float16)x0.z, (_Float16)x1.z, (_Float16)x0.w, (_Float16)x1.w};
+  auto load = [&](int g, MoeRaw<S::TROWS>& r) {
+    r.x0 = *reinterpret_cast<const float4*>(xr + 32 * g + 4 * aj);
+    r.x1 = *reinterpret_cast<const float4*>(xr + 32 * g + 16 + 4 * aj);
+    gbyte* blk = wrow + 136 * (g >> 3);
+    r.hdr = *(const __attribute__((address_space(1))) u2_t*)(blk);
+    if constexpr (kUp) r.q = *(const __attribute__((address_space(1))) u4_t*)(blk + 8 + 16 * (g & 7));
+    else r.q = *(const __attribute__((address_space(1))) u2_t*)(blk + 8 + 16 * (g & 7) + 8 * bh);
+  };
+  auto store = [&](int g, const MoeRaw<S::TROWS>& r, int buf) {
+    // activations, interleaved to pair with the weight bytes' low and high nibbles
+    const h8_t av = {(_Float16)r.x0.x, (_Float16)r.x1.x, (_Float16)r.x0.y, (_Float16)r.x1.y,
+                     (_Float16)r.x0.z, (_Float16)r.x1.z, (_Float16)r.x0.w, (_Float16)r.x1.w};
     *reinterpret_cast<h8_t*>(L.a[buf] + moe_frag(at, aj)) = av;
-    // weights: block g/8, group ib = g%8
-    const uint8_t* blk = wrow + 136 * (g >> 3);
     const int ib = g & 7;
-    const u2_t hdr = *reinterpret_cast<const u2_t*>(blk);           // d | sh << 16, sl
-    const u2_t q = *reinterpret_cast<const u2_t*>(blk + 8 + 16 * ib + 8 * bh);
-    const uint32_t sh = hdr.x >> 16;
-    const uint32_t ls = ((hdr.y >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xFu) | (((sh >> (2 * ib)) & 3u) << 4);
-    const float dl = tlx_h2f((uint16_t)hdr.x) * (float)((int)ls - 32);
-    const _Float16 dh = (_Float16)dl;
+    const uint32_t sh = r.hdr.x >> 16;
+    const uint32_t ls = ((r.hdr.y >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xFu) | (((sh >> (2 * ib)) & 3u) << 4);
+    const _Float16 dh = (_Float16)(tlx_h2f((uint16_t)r.hdr.x) * (float)((int)ls - 32));
     const h8_t dv = {dh, dh, dh, dh, dh, dh, dh, dh};
+    constexpr int kChunks = kUp ? 4 : 2;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const uint32_t qw = c ? q.y : q.x;
+    for (int c = 0; c < kChunks; ++c) {
+      const uint32_t qw = r.q[c];
       const u4_t w4 = {L.lut[qw & 0xFF], L.lut[(qw >> 8) & 0xFF], L.lut[(qw >> 16) & 0xFF], L.lut[qw >> 24]};
-      const h8_t wv = __builtin_bit_cast(h8_t, w4) * dv;
-      *reinterpret_cast<h8_t*>(L.b[buf] + moe_frag(br, 2 * bh + c)) = wv;
+      *reinterpret_cast<h8_t*>(L.b[buf] + moe_frag(br, (kUp ? 0 : 2 * bh) + c)) = __builtin_bit_cast(h8_t, w4) * dv;
     }
   };
 
-  f4_t acc[8];
+  // the wave's weight row groups: FFN gate groups 2w, 2w+1 and up groups 8+2w, 8+2w+1; down 2w, 2w+1
+  int bgrp[kRG];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < kRG; ++j) bgrp[j] = kUp ? ((j < 2) ? 2 * wave + j : 8 + 2 * wave + (j - 2)) : 2 * wave + j;
+
+  f4_t acc[4][kRG];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < kRG; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
   constexpr int kSteps = S::K / 32;
-  stage(0, 0);
+  MoeRaw<S::TROWS> r0, r1;
+  load(0, r0);
+  load(1, r1);
+  store(0, r0, 0);
   __syncthreads();
   for (int g = 0; g < kSteps; ++g) {
     const int buf = g & 1;
-    if (g + 1 < kSteps) stage(g + 1, buf ^ 1);
-    const h8_t af = *reinterpret_cast<const h8_t*>(L.a[buf] + 512 * wave + 8 * lane);
+    if (g + 2 < kSteps) load(g + 2, r0);          // two steps ahead
+    if (g + 1 < kSteps) store(g + 1, r1, buf ^ 1);  // the step after this one (loaded last step)
+    h8_t af[4], bf[kRG];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const h8_t bf = *reinterpret_cast<const h8_t*>(L.b[buf] + 512 * j + 8 * lane);
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[j], 0, 0, 0);
-    }
+    for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const h8_t*>(L.a[buf] + 512 * i + 8 * lane);
+#pragma unroll
+    for (int j = 0; j < kRG; ++j) bf[j] = *reinterpret_cast<const h8_t*>(L.b[buf] + 512 * bgrp[j] + 8 * lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < kRG; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     __syncthreads();
+    r1 = r0;
   }
 
-  // lane (col, kq) holds tokens 16*wave + 4kq + r, rows 16j + col of the stripe tile
+  // lane (col, kq) holds, for token tile i, tokens 16i + 4kq + r and row 16*bgrp[j] + col
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int slot = 16 * wave + 4 * kq + r;
-    if (slot >= ntok) break;
-    const int orow = L.orow[slot];
-    if constexpr (kUp) {
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float gv = acc[j][r], uv = acc[j + 4][r];
-        reinterpret_cast<float*>(out)[(size_t)orow * kFf + 64 * s + 16 * j + col] = gv / (1.f + expf(-gv)) * uv;
+    for (int r = 0; r < 4; ++r) {
+      const int slot = 16 * i + 4 * kq + r;
+      if (slot >= ntok) continue;
+      const int orow = L.orow[slot];
+      if constexpr (kUp) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float gv = acc[i][j][r], uv = acc[i][j + 2][r];
+          reinterpret_cast<float*>(out)[(size_t)orow * kFf + 128 * s + 16 * bgrp[j] + col] = gv / (1.f + expf(-gv)) * uv;
+        }
+      } else if constexpr (KIND == MOE_DN) {
+#pragma unroll
+        for (int j = 0; j < kRG; ++j)
+          reinterpret_cast<uint16_t*>(out)[(size_t)orow * kHid + 128 * s + 16 * bgrp[j] + col] = tlx_f2h_bits(acc[i][j][r]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < kRG; ++j)
+          reinterpret_cast<float*>(out)[(size_t)orow * kHid + 128 * s + 16 * bgrp[j] + col] = acc[i][j][r];
       }
-    } else if constexpr (KIND == MOE_DN) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        reinterpret_cast<uint16_t*>(out)[(size_t)orow * kHid + 128 * s + 16 * j + col] = tlx_f2h_bits(acc[j][r]);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        reinterpret_cast<float*>(out)[(size_t)orow * kHid + 128 * s + 16 * j + col] = acc[j][r];
     }
   }
 }
