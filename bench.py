@@ -18,6 +18,11 @@ an fp32 matmul) on a bounded sample of rows of the same workload, on this host's
 ``gemm`` is the metric's second half: the prefill dequant-GEMM of config 4 at M=2048 --
 gate+up with SwiGLU (K=5120, N=2x17408) and down with the residual epilogue (K=17408,
 N=5120) -- in TFLOP/s (2*M*N*K per GEMM) and as a fraction of the dense fp16 MFMA peak.
+
+``moe`` is config 5: the whole MoE layer (top-8 from N(0,1) logits, sort, grouped IQ4_XS
+gate+up and down, shared expert, combine) at M=11 and M=2048, seeded expert weights; at
+M=11 each step reads a different copy of the 257 expert slabs (3 copies, 1.3 GB), so the
+weights come from HBM.
 """
 import argparse
 import json
@@ -40,6 +45,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--ms", default="1,4,8,11", help="activation widths to time")
     ap.add_argument("--gemm-m", type=int, default=2048, help="prefill rows for the GEMM leg (0: skip)")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MoE leg")
     return ap.parse_args()
 
 
@@ -81,9 +87,9 @@ def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup):
     """Config 4: IQ3_XXS FFN prefill GEMMs at M rows, synthetic seeded weights."""
     rng = synth.config_rng(4)
     H, F = 5120, 17408
-    pg = torch.from_numpy(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, F, H), H)).to(dev)
-    pu = torch.from_numpy(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, F, H), H)).to(dev)
-    pd = torch.from_numpy(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, H, F), F)).to(dev)
+    def pack7(rows, k):   # the prefill GEMMs read the packed7 unit layout
+        return torch.from_numpy(formats.iq3_pack7(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, rows, k), k), k)).to(dev)
+    pg, pu, pd = pack7(F, H), pack7(F, H), pack7(H, F)
     gridf = formats.gridf_tensor(dev)
     x = torch.from_numpy(synth.activations_f16(rng, M, H)).to(dev)
     act = torch.empty(M, F, dtype=torch.float16, device=dev)
@@ -105,6 +111,58 @@ def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup):
                      "unit": "TFLOP/s", "frac": round(tf_ffn / PEAK_F16_TFLOPS, 4), "traffic": None,
                      "kernel": "pf_gemm_kernel<FFN> (gate+up)"},
     }
+
+
+def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
+    """Config 5: the MoE layer at M=11 (HBM-bound) and M=2048 (MFMA-bound)."""
+    rng = synth.config_rng(5)
+    E, H, F = 256, 2048, 512
+    copies = []
+    for _ in range(3):
+        gu, dn = synth.moe_expert_slabs(rng, E + 1)
+        dgu = [torch.from_numpy(a).to(dev) for a in gu]
+        ddn = [torch.from_numpy(a).to(dev) for a in dn]
+        copies.append(dict(keep=(dgu, ddn), ptbl=formats.pointer_table(dgu[:E], dev),
+                           ptbl_dn=formats.pointer_table(ddn[:E], dev),
+                           ptbl_sh=formats.pointer_table([dgu[E], ddn[E]], dev)))
+    iq4nl = formats.iq4nl_tensor(dev)
+    out = {"workload": "MoE layer, 256 IQ4_XS experts + 1 shared, hidden 2048, FF 512, top-8"}
+    for P in (11, 2048):
+        np_ = 8 * P
+        x = torch.from_numpy(synth.bf16_round(0.05 * rng.standard_normal((P, H)).astype(np.float32))).to(dev)
+        logits = torch.from_numpy(rng.standard_normal((P, E)).astype(np.float32)).to(dev)
+        sg = torch.rand(P, device=dev)
+        hres = torch.randn(P, H, device=dev)
+        eids = torch.empty(P, 8, dtype=torch.int16, device=dev)
+        gates = torch.empty(P, 8, device=dev)
+        eoff = torch.empty(E + 1, dtype=torch.int32, device=dev)
+        plist = torch.empty(np_, dtype=torch.int16, device=dev)
+        items = torch.empty(ops.moe_max_items(np_), dtype=torch.int32, device=dev)
+        nitp = torch.empty(1, dtype=torch.int32, device=dev)
+        act = torch.empty(np_, F, device=dev)
+        parts = torch.empty(np_, H, dtype=torch.float16, device=dev)
+        sact = torch.empty(P, F, device=dev)
+        shared = torch.empty(P, H, device=dev)
+        y = torch.empty(P, H, device=dev)
+        state = {"i": 0}
+
+        def layer(st):
+            c = copies[state["i"] % len(copies)]
+            state["i"] += 1
+            ops.moe_topk(logits, eids, gates, stream=st)
+            ops.moe_sort(eids, eoff, plist, items, nitp, stream=st)
+            ops.moe_up4(c["ptbl"], eoff, plist, items, nitp, x, iq4nl, act, stream=st)
+            ops.moe_dn4(c["ptbl_dn"], eoff, plist, items, nitp, act, iq4nl, parts, stream=st)
+            ops.moe_shared(c["ptbl_sh"], x, iq4nl, sact, shared, stream=st)
+            ops.moe_combine(parts, gates, sg, shared, hres, y, stream=st)
+
+        t = time_call(layer, steps, warmup, torch)
+        hit = int((torch.diff(eoff) > 0).sum().item())
+        flops = 2.0 * 3 * F * H * (8 * P + P)
+        wbytes = (hit + 1) * 1671168
+        out[f"M{P}"] = {"ms": round(t, 4), "tflops": round(flops / (t * 1e-3) / 1e12, 2),
+                        "experts_hit": hit, "weight_gbs": round(wbytes / (t * 1e-3) / 1e9, 1)}
+    return out
 
 
 def cpu_baseline(N, K, M, seconds=10.0):
@@ -202,6 +260,8 @@ def main():
     if args.gemm_m > 0:
         out["gemm"] = gemm_leg(ops, formats, synth, torch, dev, args.gemm_m, max(3, args.steps // 5),
                                max(1, args.warmup // 5))
+    if not args.no_moe:
+        out["moe"] = moe_leg(ops, formats, synth, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(N, K, int(head))
     print(json.dumps(out), flush=True)

@@ -199,8 +199,18 @@ def test_moe_layer_deterministic(gpu, experts):
 
 def test_moe_bad_arguments(gpu, experts):
     print("[case] moe argument checks", flush=True)
+    n = 16385   # one pair more than the sort supports: the library rejects it
+    with pytest.raises(TlxError):
+        ops.moe_sort(torch.zeros(n, dtype=torch.int16, device=gpu), torch.zeros(257, dtype=torch.int32, device=gpu),
+                     torch.zeros(n, dtype=torch.int16, device=gpu),
+                     torch.zeros(ops.moe_max_items(n), dtype=torch.int32, device=gpu),
+                     torch.zeros(1, dtype=torch.int32, device=gpu))
     z = torch.zeros(16, dtype=torch.int32, device=gpu)
     with pytest.raises(TlxError):
-        ops.moe_sort(torch.zeros(16385 * 8, dtype=torch.int16, device=gpu)[:16385], z, z, z, z)
-    with pytest.raises(TlxError):
         ops.moe_topk(torch.zeros(0, 256, dtype=torch.float32, device=gpu), z, z)
+    with pytest.raises(ValueError):   # a pointer table shorter than 256 entries never reaches the library
+        ops.moe_up4(experts["ptbl"][:8], torch.zeros(257, dtype=torch.int32, device=gpu),
+                    torch.zeros(8, dtype=torch.int16, device=gpu),
+                    torch.zeros(ops.moe_max_items(8), dtype=torch.int32, device=gpu),
+                    torch.zeros(1, dtype=torch.int32, device=gpu), torch.zeros(1, 2048, device=gpu),
+                    experts["iq4nl"], torch.zeros(8, 512, device=gpu))

@@ -30,27 +30,48 @@ def _mk(x):
     return 1 if x.dim() == 1 else x.shape[0]
 
 
+def _need(t, nbytes, what):
+    """Raise unless buffer `t` holds at least `nbytes` bytes: the library sees only pointers,
+    so a buffer too small for the shape and layout it is described with must be caught here."""
+    have = t.numel() * t.element_size()
+    if have < nbytes:
+        raise ValueError(f"{what}: {have} bytes, the call needs {nbytes}")
+
+
+def _iq3_rows(n, k):
+    return n * 98 * (k // 256)
+
+
+def _pack7(n, k):
+    return n * (k // 2)
+
+
 # ------------------------------------------------------------------ dequantization
 def iq3xxs_dequant(w, gridf, out, kdim, layout=LAYOUT_PACKED, stream=None):
+    rows = w.numel() * w.element_size() // (98 * (kdim // 256))
+    _need(out, rows * kdim * out.element_size(), "out")
+    _need(gridf, 4096, "gridf")
     _dev(w, gridf, out)
-    rows = w.numel() // (98 * (kdim // 256))
     call("tlx_iq3xxs_dequant", w.data_ptr(), gridf.data_ptr(), out.data_ptr(), rows, kdim, layout,
          int(out.dtype == _F16), _stream(stream))
     return out
 
 
 def q6k_dequant(w, out, kdim, layout=LAYOUT_RAW, stream=None):
-    _dev(w, out)
     bs = 210 if layout == LAYOUT_RAW else 212
-    rows = w.numel() // (bs * (kdim // 256))
+    rows = w.numel() * w.element_size() // (bs * (kdim // 256))
+    _need(out, rows * kdim * out.element_size(), "out")
+    _dev(w, out)
     call("tlx_q6k_dequant", w.data_ptr(), out.data_ptr(), rows, kdim, layout, int(out.dtype == _F16),
          _stream(stream))
     return out
 
 
 def iq4xs_dequant(w, iq4nl, out, kdim, stream=None):
+    rows = w.numel() * w.element_size() // (136 * (kdim // 256))
+    _need(out, rows * kdim * 4, "out")
+    _need(iq4nl, 64, "iq4nl")
     _dev(w, iq4nl, out)
-    rows = w.numel() // (136 * (kdim // 256))
     call("tlx_iq4xs_dequant", w.data_ptr(), iq4nl.data_ptr(), out.data_ptr(), rows, kdim, _stream(stream))
     return out
 
@@ -58,8 +79,12 @@ def iq4xs_dequant(w, iq4nl, out, kdim, stream=None):
 # ------------------------------------------------------------------ decode GEMVs
 def ffn8(wg, wu, gridf, hhx, gact, layout=LAYOUT_PACKED, stream=None):
     """gact[m] = silu16(half(Wg·hhx[m])) * half(Wu·hhx[m])   (ffn8 / ffn8v{M})."""
-    _dev(wg, wu, gridf, hhx, gact)
     M, K, N = _mk(hhx), hhx.shape[-1], gact.shape[-1]
+    _need(wg, _iq3_rows(N, K), "wg")
+    _need(wu, _iq3_rows(N, K), "wu")
+    _need(gridf, 4096, "gridf")
+    _need(gact, M * N * 2, "gact")
+    _dev(wg, wu, gridf, hhx, gact)
     call("tlx_ffn8", wg.data_ptr(), wu.data_ptr(), gridf.data_ptr(), hhx.data_ptr(), gact.data_ptr(),
          M, N, K, layout, _stream(stream))
     return gact
@@ -67,8 +92,12 @@ def ffn8(wg, wu, gridf, hhx, gact, layout=LAYOUT_PACKED, stream=None):
 
 def down8(wd, gridf, gact, hh, y, layout=LAYOUT_PACKED, stream=None):
     """y[m] = hh[m] + float(half(Wd·gact[m]))   (down8 / down8nw32_{M})."""
-    _dev(wd, gridf, gact, hh, y)
     M, K, N = _mk(gact), gact.shape[-1], y.shape[-1]
+    _need(wd, _iq3_rows(N, K), "wd")
+    _need(gridf, 4096, "gridf")
+    _need(hh, M * N * 4, "hh")
+    _need(y, M * N * 4, "y")
+    _dev(wd, gridf, gact, hh, y)
     call("tlx_down8", wd.data_ptr(), gridf.data_ptr(), gact.data_ptr(), hh.data_ptr(), y.data_ptr(),
          M, N, K, layout, _stream(stream))
     return y
@@ -76,8 +105,11 @@ def down8(wd, gridf, gact, hh, y, layout=LAYOUT_PACKED, stream=None):
 
 def iq3_gemv(w, gridf, x, out, layout=LAYOUT_PACKED, stream=None):
     """out[m] = half(W·x[m])   (the IQ3ROWP segment body)."""
-    _dev(w, gridf, x, out)
     M, K, N = _mk(x), x.shape[-1], out.shape[-1]
+    _need(w, _iq3_rows(N, K), "w")
+    _need(gridf, 4096, "gridf")
+    _need(out, M * N * 2, "out")
+    _dev(w, gridf, x, out)
     call("tlx_iq3_gemv", w.data_ptr(), gridf.data_ptr(), x.data_ptr(), out.data_ptr(), M, N, K, layout,
          _stream(stream))
     return out
@@ -85,8 +117,12 @@ def iq3_gemv(w, gridf, x, out, layout=LAYOUT_PACKED, stream=None):
 
 def aq3k8(wq, wk, wv, gridf, xh, qrow, krow, vrow, layout=LAYOUT_PACKED, stream=None):
     """Fused q/k/v IQ3_XXS projections in one launch   (aq3k8 / aq3k8v{M})."""
-    _dev(wq, wk, wv, gridf, xh, qrow, krow, vrow)
     M, K = _mk(xh), xh.shape[-1]
+    for t, o, nm in ((wq, qrow, "wq"), (wk, krow, "wk"), (wv, vrow, "wv")):
+        _need(t, _iq3_rows(o.shape[-1], K), nm)
+        _need(o, M * o.shape[-1] * 2, nm + " output")
+    _need(gridf, 4096, "gridf")
+    _dev(wq, wk, wv, gridf, xh, qrow, krow, vrow)
     call("tlx_aq3k8", wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), gridf.data_ptr(), xh.data_ptr(),
          qrow.data_ptr(), krow.data_ptr(), vrow.data_ptr(), M, qrow.shape[-1], krow.shape[-1],
          vrow.shape[-1], K, layout, _stream(stream))
@@ -94,6 +130,7 @@ def aq3k8(wq, wk, wv, gridf, xh, qrow, krow, vrow, layout=LAYOUT_PACKED, stream=
 
 def h6k_gemv(w, x, y, layout=LAYOUT_RAW, stream=None):
     """y = W·x, Q6_K weights, fp32 x and y   (h6k2048 contract)."""
+    _need(w, y.numel() * (210 if layout == LAYOUT_RAW else 212) * (x.numel() // 256), "w")
     _dev(w, x, y)
     call("tlx_q6k_gemv", w.data_ptr(), x.data_ptr(), y.data_ptr(), y.numel(), x.numel(), layout,
          _stream(stream))
@@ -106,8 +143,12 @@ def h6k_gemv(w, x, y, layout=LAYOUT_RAW, stream=None):
 def pfg3_ffn(wg, wu, gridf, x16, out16, layout=LAYOUT_PACK7, stream=None):
     """out16[m] = silu16(half(Wg·x16[m])) * half(Wu·x16[m]) over a prompt chunk
     (pf_gemm3 FFN=1: kernel(w1, w2, gridf, x16, out16))."""
-    _dev(wg, wu, gridf, x16, out16)
     M, K, N = x16.shape[0], x16.shape[1], out16.shape[1]
+    _need(wg, _pack7(N, K), "wg (packed7)")
+    _need(wu, _pack7(N, K), "wu (packed7)")
+    _need(gridf, 4096, "gridf")
+    _need(out16, M * N * 2, "out16")
+    _dev(wg, wu, gridf, x16, out16)
     call("tlx_pfg3_ffn", wg.data_ptr(), wu.data_ptr(), gridf.data_ptr(), x16.data_ptr(), out16.data_ptr(),
          M, N, K, layout, _stream(stream))
     return out16
@@ -115,8 +156,12 @@ def pfg3_ffn(wg, wu, gridf, x16, out16, layout=LAYOUT_PACK7, stream=None):
 
 def pfg3_iq3d(w, gridf, x16, res16, out32, layout=LAYOUT_PACK7, stream=None):
     """out32[m] = res16[m] + W·x16[m]   (pf_gemm3 RES=1: kernel(w1, gridf, x16, res16, out32))."""
-    _dev(w, gridf, x16, res16, out32)
     M, K, N = x16.shape[0], x16.shape[1], out32.shape[1]
+    _need(w, _pack7(N, K), "w (packed7)")
+    _need(gridf, 4096, "gridf")
+    _need(res16, M * N * 4, "res16")
+    _need(out32, M * N * 4, "out32")
+    _dev(w, gridf, x16, res16, out32)
     call("tlx_pfg3_iq3d", w.data_ptr(), gridf.data_ptr(), x16.data_ptr(), res16.data_ptr(), out32.data_ptr(),
          M, N, K, layout, _stream(stream))
     return out32
@@ -124,8 +169,11 @@ def pfg3_iq3d(w, gridf, x16, res16, out32, layout=LAYOUT_PACK7, stream=None):
 
 def pfg3_iq3o(w, gridf, x16, out16, layout=LAYOUT_PACK7, stream=None):
     """out16[m] = half(W·x16[m])   (pf_gemm3 plain: kernel(w1, gridf, x16, out16))."""
-    _dev(w, gridf, x16, out16)
     M, K, N = x16.shape[0], x16.shape[1], out16.shape[1]
+    _need(w, _pack7(N, K), "w (packed7)")
+    _need(gridf, 4096, "gridf")
+    _need(out16, M * N * 2, "out16")
+    _dev(w, gridf, x16, out16)
     call("tlx_pfg3_iq3o", w.data_ptr(), gridf.data_ptr(), x16.data_ptr(), out16.data_ptr(), M, N, K, layout,
          _stream(stream))
     return out16
@@ -136,12 +184,23 @@ def pfg3_iq3o(w, gridf, x16, out16, layout=LAYOUT_PACK7, stream=None):
 # ptbl / ptbl_dn: int64 device tensors of 256 slab addresses (formats.pointer_table).
 def moe_topk(logits, eids, gates, stream=None):
     """Top-8 + renormalized softmax from router logits [P][256] (the rt8e256 epilogue)."""
+    P = logits.shape[0]
+    _need(logits, P * 256 * 4, "logits")
+    _need(eids, P * 8 * 2, "eids")
+    _need(gates, P * 8 * 4, "gates")
     _dev(logits, eids, gates)
     call("tlx_moe_topk", logits.data_ptr(), eids.data_ptr(), gates.data_ptr(), logits.shape[0], _stream(stream))
 
 
 def moe_route(wrt, wsh, h, eids, gates, sg, stream=None):
     """rt8e256(wrt, wsh, h, eids, gates, sg)."""
+    P = h.shape[0]
+    _need(wrt, 256 * 2048 * 4, "wrt")
+    _need(wsh, 2048 * 4, "wsh")
+    _need(h, P * 2048 * 4, "h")
+    _need(eids, P * 8 * 2, "eids")
+    _need(gates, P * 8 * 4, "gates")
+    _need(sg, P * 4, "sg")
     _dev(wrt, wsh, h, eids, gates, sg)
     call("tlx_moe_route", wrt.data_ptr(), wsh.data_ptr(), h.data_ptr(), eids.data_ptr(), gates.data_ptr(),
          sg.data_ptr(), h.shape[0], _stream(stream))
@@ -154,6 +213,11 @@ def moe_max_items(npair):
 
 def moe_sort(eids, eoff, plist, items, nitp, stream=None):
     """mmsort8(eids, eoff, plist, items, nitp, np) with np = eids.numel()."""
+    n = eids.numel()
+    _need(eoff, 257 * 4, "eoff")
+    _need(plist, n * 2, "plist")
+    _need(items, moe_max_items(n) * 4, "items")
+    _need(nitp, 4, "nitp")
     _dev(eids, eoff, plist, items, nitp)
     call("tlx_moe_sort", eids.data_ptr(), eoff.data_ptr(), plist.data_ptr(), items.data_ptr(), nitp.data_ptr(),
          eids.numel(), _stream(stream))
@@ -161,6 +225,14 @@ def moe_sort(eids, eoff, plist, items, nitp, stream=None):
 
 def moe_up4(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, stream=None):
     """ys[pair][512] = silu(Wg_e . x[pos]) * (Wu_e . x[pos])   (gx8e256up4 / gxu_gm)."""
+    n = ys.shape[0]
+    _need(ptbl, 256 * 8, "ptbl")
+    _need(eoff, 257 * 4, "eoff")
+    _need(plist, n * 2, "plist")
+    _need(items, moe_max_items(n) * 4, "items")
+    _need(xs, (n // 8) * 2048 * 4, "xs")
+    _need(ys, n * 512 * 4, "ys")
+    _need(iq4nl, 64, "iq4nl")
     _dev(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys)
     call("tlx_moe_up4", ptbl.data_ptr(), eoff.data_ptr(), plist.data_ptr(), items.data_ptr(), nitp.data_ptr(),
          xs.data_ptr(), iq4nl.data_ptr(), ys.data_ptr(), ys.shape[0], _stream(stream))
@@ -168,6 +240,14 @@ def moe_up4(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, stream=None):
 
 def moe_dn4(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, stream=None):
     """parts[pair][2048] = fp16(Wd_e . act[pair])   (gx8e256dn / gxd_gm)."""
+    n = act.shape[0]
+    _need(ptbl_dn, 256 * 8, "ptbl_dn")
+    _need(eoff, 257 * 4, "eoff")
+    _need(plist, n * 2, "plist")
+    _need(items, moe_max_items(n) * 4, "items")
+    _need(act, n * 512 * 4, "act")
+    _need(parts, n * 2048 * 2, "parts")
+    _need(iq4nl, 64, "iq4nl")
     _dev(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts)
     call("tlx_moe_dn4", ptbl_dn.data_ptr(), eoff.data_ptr(), plist.data_ptr(), items.data_ptr(), nitp.data_ptr(),
          act.data_ptr(), iq4nl.data_ptr(), parts.data_ptr(), act.shape[0], _stream(stream))
@@ -175,6 +255,12 @@ def moe_dn4(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, stream=None):
 
 def moe_shared(ptbl_sh, xs, iq4nl, act, out, stream=None):
     """Shared expert over all positions: act [P][512] (scratch), out [P][2048] f32."""
+    P = xs.shape[0]
+    _need(ptbl_sh, 2 * 8, "ptbl_sh")
+    _need(xs, P * 2048 * 4, "xs")
+    _need(act, P * 512 * 4, "act")
+    _need(out, P * 2048 * 4, "out")
+    _need(iq4nl, 64, "iq4nl")
     _dev(ptbl_sh, xs, iq4nl, act, out)
     call("tlx_moe_shared", ptbl_sh.data_ptr(), xs.data_ptr(), iq4nl.data_ptr(), act.data_ptr(), out.data_ptr(),
          xs.shape[0], _stream(stream))
@@ -182,6 +268,12 @@ def moe_shared(ptbl_sh, xs, iq4nl, act, out, stream=None):
 
 def moe_combine(parts, gates, sg, shared, hres, y, stream=None):
     """cmbz2048(parts, gates, sg, shared, hres, y)."""
+    P = y.shape[0]
+    _need(parts, P * 8 * 2048 * 2, "parts")
+    _need(gates, P * 8 * 4, "gates")
+    _need(sg, P * 4, "sg")
+    for t, nm in ((shared, "shared"), (hres, "hres"), (y, "y")):
+        _need(t, P * 2048 * 4, nm)
     _dev(parts, gates, sg, shared, hres, y)
     call("tlx_moe_combine", parts.data_ptr(), gates.data_ptr(), sg.data_ptr(), shared.data_ptr(), hres.data_ptr(),
          y.data_ptr(), y.shape[0], _stream(stream))
