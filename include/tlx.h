@@ -87,6 +87,24 @@ int tlx_aq3k8(const void* wq, const void* wk, const void* wv, const float* gridf
 int tlx_q6k_gemv(const void* w, const float* x, float* y, int rows, int K, int layout,
                  void* stream);
 
+/* Q6_K GEMV with fp16 activations and fp16 outputs: out[m][n] = half(sum_k W[n][k]*x[m][k]),
+ * W = (d*sc)*(q-32) per GGUF Q6_K block; layout TLX_LAYOUT_RAW (210-B blocks) or
+ * TLX_LAYOUT_PACKED (the padded 212-B blocks [pad2][d2][sc16][ql128][qh64] of
+ * engine/pack_w1c.py:33-45).  The q-branch body of aq6k8 (engine/aq6k8.cu:141-173) and
+ * a_qkv_q6 (engine/a_qkv_q6.cu:95-124), and the Q6_K lm_head.  M in 1..16; M rows whose
+ * activations do not fit the LDS budget run as consecutive row groups. */
+int tlx_q6k_gemv16(const void* w, const uint16_t* x_f16, uint16_t* out_f16, int M, int N, int K,
+                   int layout, void* stream);
+
+/* Fused attention q/k/v projections with a Q6_K q (the reference's Q6_K attention layers):
+ * q through tlx_q6k_gemv16 (layout as there; the padded 212-B blocks for aq6k8), k and v
+ * IQ3_XXS packed rows (BASELINE's dense config; the reference's v is Q4_K).
+ * Replaces aq6k8 / aq6k8v{4..11} (engine/aq6k8.cu:134-173): aq6k8(wq, wk, wv4, gridf, xh,
+ * qrow, krow, vrow).  Two launches on `stream`; arguments are validated before either. */
+int tlx_aq6k8(const void* wq, const void* wk, const void* wv, const float* gridf,
+              const uint16_t* xh_f16, uint16_t* qrow_f16, uint16_t* krow_f16, uint16_t* vrow_f16,
+              int M, int Nq, int Nk, int Nv, int K, int layout, void* stream);
+
 /* ---- prefill dequant-GEMM (M rows of a prompt chunk, MFMA fp16 x fp16 -> fp32) ----
  * x16 is M x K fp16 row-major; W is N IQ3_XXS rows in the packed7 layout (TLX_LAYOUT_PACK7,
  * the layout the reference's pf_gemm3 REPACK=1 kernels read).  M % 256 == 0, K % 128 == 0,

@@ -37,6 +37,8 @@ SIGNATURES = {
     "tlx_iq3_gemv": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_aq3k8": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
     "tlx_q6k_gemv": [_p, _p, _p, _i, _i, _i, _p],
+    "tlx_q6k_gemv16": [_p, _p, _p, _i, _i, _i, _i, _p],
+    "tlx_aq6k8": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
     "tlx_pfg3_ffn": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_pfg3_iq3d": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_pfg3_iq3o": [_p, _p, _p, _p, _i, _i, _i, _i, _p],

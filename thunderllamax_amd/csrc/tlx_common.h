@@ -60,3 +60,25 @@ __device__ __forceinline__ uint16_t tlx_swiglu_bits(float g, float u) {
   const __half hu = __float2half(u);
   return __builtin_bit_cast(uint16_t, __hmul(tlx_hsilu(hg), hu));
 }
+
+// ---------------------------------------------------------------- device properties
+// Compute-unit count of the current device (cached per device id; a benign race on first use
+// writes the same value twice).
+static inline int tlx_cu_count() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// k/v segments of the fused attention projections on IQ3_XXS packed rows (tlx_iq3.hip);
+// launch == false validates the arguments only.
+int tlx_iq3_kv(const void* wk, const void* wv, const float* gridf, const uint16_t* xh_f16,
+               uint16_t* krow_f16, uint16_t* vrow_f16, int M, int Nk, int Nv, int K, bool launch,
+               void* stream);

@@ -354,3 +354,25 @@ extern "C" int tlx_aq3k8(const void* wq, const void* wk, const void* wv, const f
   a.K = K;
   return iq3_launch<1, EPI_F16>(a, tq + tk + tv, (hipStream_t)stream);
 }
+
+// k and v segments of the fused attention projections (IQ3_XXS packed rows), used by the Q6_K
+// q-branch entry point.  With launch == false only the arguments are validated.
+int tlx_iq3_kv(const void* wk, const void* wv, const float* gridf, const uint16_t* xh_f16,
+               uint16_t* krow_f16, uint16_t* vrow_f16, int M, int Nk, int Nv, int K, bool launch,
+               void* stream) {
+  int rc = iq3_check(wk, M, Nk, K, TLX_LAYOUT_PACKED);
+  if (rc == TLX_OK) rc = iq3_check(wv, M, Nv, K, TLX_LAYOUT_PACKED);
+  TLX_RET_IF(rc != TLX_OK, rc);
+  TLX_RET_IF(!tlx_aligned(xh_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
+  if (!launch) return TLX_OK;
+  Iq3Launch a{};
+  const int tk = tiles_of(Nk), tv = tiles_of(Nv);
+  a.seg[0] = Iq3Seg{(const uint8_t*)wk, nullptr, krow_f16, nullptr, Nk, 0};
+  a.seg[1] = Iq3Seg{(const uint8_t*)wv, nullptr, vrow_f16, nullptr, Nv, tk};
+  a.nseg = 2;
+  a.gridf = gridf;
+  a.x = (const _Float16*)xh_f16;
+  a.M = M;
+  a.K = K;
+  return iq3_launch<1, EPI_F16>(a, tk + tv, (hipStream_t)stream);
+}

@@ -137,6 +137,39 @@ def h6k_gemv(w, x, y, layout=LAYOUT_RAW, stream=None):
     return y
 
 
+def _q6_rows(n, k, layout):
+    return n * (210 if layout == LAYOUT_RAW else 212) * (k // 256)
+
+
+def q6k_gemv16(w, x, out, layout=LAYOUT_PACKED, stream=None):
+    """out[m][n] = half(W[n]·x[m]), Q6_K weights (raw 210-B or padded 212-B blocks), fp16
+    activations and outputs (the q-branch body of aq6k8 / a_qkv_q6 and the Q6_K head)."""
+    M, K = x.shape
+    N = out.shape[-1]
+    _need(w, _q6_rows(N, K, layout), "w")
+    _need(out, M * N * 2, "out")
+    _dev(w, x, out)
+    call("tlx_q6k_gemv16", w.data_ptr(), x.data_ptr(), out.data_ptr(), M, N, K, layout,
+         _stream(stream))
+    return out
+
+
+def aq6k8(wq, wk, wv, gridf, xh, qrow, krow, vrow, layout=LAYOUT_PACKED, stream=None):
+    """Fused attention projections with a Q6_K q (padded 212-B blocks for ``LAYOUT_PACKED``,
+    raw 210-B for ``LAYOUT_RAW``) and IQ3_XXS packed-row k and v."""
+    M, K = xh.shape
+    _need(wq, _q6_rows(qrow.shape[-1], K, layout), "wq")
+    _need(qrow, M * qrow.shape[-1] * 2, "wq output")
+    for t, o, nm in ((wk, krow, "wk"), (wv, vrow, "wv")):
+        _need(t, _iq3_rows(o.shape[-1], K), nm)
+        _need(o, M * o.shape[-1] * 2, nm + " output")
+    _need(gridf, 4096, "gridf")
+    _dev(wq, wk, wv, gridf, xh, qrow, krow, vrow)
+    call("tlx_aq6k8", wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), gridf.data_ptr(), xh.data_ptr(),
+         qrow.data_ptr(), krow.data_ptr(), vrow.data_ptr(), M, qrow.shape[-1], krow.shape[-1],
+         vrow.shape[-1], K, layout, _stream(stream))
+
+
 # ------------------------------------------------------------------ prefill dequant-GEMMs
 # Weights are IQ3_XXS in the packed7 unit layout (``formats.iq3_pack7``), as the reference's
 # prefill GEMMs read them.
