@@ -212,11 +212,14 @@ int iq3_launch(const Iq3Launch& a, int tiles, hipStream_t st) {
   return tlx_launch_status();
 }
 
+
 int iq3_check(const void* w, int M, int N, int K, int layout) {
   if (M < 1 || M > TLX_MAX_M || N < 1 || K < 256 || (K & 255)) return TLX_E_ARG;
   if (layout != TLX_LAYOUT_PACKED) return TLX_E_ARG;
   // 16-B operand loads need dword-aligned rows: row bytes 98*NB with NB even
   if (((K >> 8) & 1) || !tlx_aligned(w, 4)) return TLX_E_ALIGN;
+  // kernels address a matrix with 32-bit byte offsets
+  if ((size_t)N * kIq3BlockBytes * (K >> 8) > 0xFFFFFFFFull) return TLX_E_ARG;
   return TLX_OK;
 }
 

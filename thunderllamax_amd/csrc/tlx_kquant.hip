@@ -28,6 +28,7 @@ constexpr int kStgRow = 240;            // staging bytes per weight row (16 x od
 constexpr int kStgItem = 16 * kStgRow;  // one item: 16 rows x one 256-weight block
 constexpr int kSlot = 64 * 16;          // one wave's 16x16 fp32 partial tile
 constexpr int kLdsMax = 160 * 1024;
+constexpr int kPrefetch = 2;          // items in flight per wave (even: fragments ping-pong)
 
 struct Q6Geo {
   int bs, qoff, scoff, doff;  // block bytes; offsets of ql (qh follows), scales, d
@@ -55,13 +56,14 @@ struct Q6Frag {  // one lane's share in fragment order: 32 ql bytes, 32 qh bytes
   uint32_t d;
 };
 
+// `off` is the block's 32-bit byte offset from the matrix base (scalar base + vector offset)
 template <int LAYOUT>
-__device__ __forceinline__ void q6_load(Q6Ld& L, const uint8_t* blk, int c) {
+__device__ __forceinline__ void q6_load(Q6Ld& L, const uint8_t* w, uint32_t off, int c) {
   constexpr Q6Geo G = q6_geo(LAYOUT);
 #pragma unroll
-  for (int j = 0; j < 3; ++j) L.q[j] = tlx_ldu<u4_t>(blk + G.qoff + 64 * j + 16 * c);
-  L.sc = tlx_ldu<uint32_t>(blk + G.scoff + 4 * c);
-  L.d = tlx_ldu<uint16_t>(blk + G.doff);
+  for (int j = 0; j < 3; ++j) L.q[j] = tlx_ldu<u4_t>(w + (off + G.qoff + 64 * j + 16 * c));
+  L.sc = tlx_ldu<uint32_t>(w + (off + G.scoff + 4 * c));
+  L.d = tlx_ldu<uint16_t>(w + (off + G.doff));
 }
 
 // staging row r: [ql 128][qh 64][sc 16][d 2][pad]
@@ -145,22 +147,34 @@ __global__ __launch_bounds__(kWaves * TLX_WAVE) void q6_gemv16_kernel(const KqAr
   const int r = lane >> 2, c = lane & 3;       // load role: row r, 16-B piece c of each 64 B
   const int col = lane & 15, kq = lane >> 4;   // MFMA role
   const int h = kq >> 1, e = kq & 1;
-  const size_t rowb = (size_t)G.bs * nb;
-  auto blk_of = [&](int i) -> const uint8_t* {
+  const uint32_t rowb = (uint32_t)G.bs * nb;
+  auto blk_of = [&](int i) -> uint32_t {
     const int t = t0 + i / nb, b = i - (i / nb) * nb;
     const int n = min(16 * t + r, N - 1);  // tail tile: clamp the loads, mask the stores
-    return a.w + (size_t)n * rowb + (size_t)b * G.bs;
+    return (uint32_t)n * rowb + (uint32_t)b * G.bs;
   };
 
-  Q6Ld g0, g1;
-  if (lo < hi) q6_load<LAYOUT>(g0, blk_of(lo), c);
-  if (lo + 1 < hi) q6_load<LAYOUT>(g1, blk_of(lo + 1), c);
+  // Every load, staging write and fragment read below is unconditional (item indices are
+  // clamped to the wave's last item), so the loop body is straight-line and the compiler's
+  // wait counts stay exact.
+  const int last = hi - 1;
+  Q6Ld g[kPrefetch];  // ring: item i sits in g[(i - lo) % kPrefetch] until it is staged
+  if (lo < hi) {
+#pragma unroll
+    for (int p = 0; p < kPrefetch; ++p) q6_load<LAYOUT>(g[p], a.w, blk_of(min(lo + p, last)), c);
+  }
 
-  const int kv = K >> 3;
-  for (int v = threadIdx.x; v < M * kv; v += kWaves * TLX_WAVE) {
-    const int m = v / kv, k8 = v - m * kv;
-    *reinterpret_cast<u4_t*>(xs + m * XS + 8 * k8) =
-        *reinterpret_cast<const u4_t*>(a.x + (size_t)m * K + 8 * k8);
+  // activations: 1-KB LDS-DMA pieces (row m, halves [512j, 512j + 512)), in flight together
+  // with the weight prefetch; when K % 512 == 256 a row's last piece is half a wave wide
+  {
+    const int pr = (K + 511) >> 9;
+    for (int p = wave; p < M * pr; p += kWaves) {
+      const int m = p / pr, j = p - m * pr;
+      if (512 * j + 8 * lane < K)
+        __builtin_amdgcn_global_load_lds(
+            (const void*)(a.x + (size_t)m * K + 512 * j + 8 * lane),
+            (__attribute__((address_space(3))) void*)(xs + m * XS + 512 * j), 16, 0, 0);
+    }
   }
   __syncthreads();
 
@@ -178,37 +192,39 @@ __global__ __launch_bounds__(kWaves * TLX_WAVE) void q6_gemv16_kernel(const KqAr
   };
 
   f4_t acc = {0.f, 0.f, 0.f, 0.f}, accFirst = acc, accLast = acc;
-  Q6Frag F;
+  Q6Frag F[2];  // item i's fragments in F[(i - lo) & 1]
   if (lo < hi) {
-    q6_stage(stg, g0, r, c);
-    q6_frag(F, stg, col, h, e);
+    q6_stage(stg, g[0], r, c);
+    q6_frag(F[0], stg, col, h, e);
+    q6_load<LAYOUT>(g[0], a.w, blk_of(min(lo + kPrefetch, last)), c);
   }
   int seg = lo;
-  for (int i = lo; i < hi; ++i) {
-    Q6Ld g2;
-    if (i + 2 < hi) q6_load<LAYOUT>(g2, blk_of(i + 2), c);
-    const int tl = i / nb, b = i - tl * nb;
-    h8_t A[8];
+  for (int i0 = lo; i0 < hi; i0 += kPrefetch) {
 #pragma unroll
-    for (int o = 0; o < 8; ++o)
-      A[o] = *reinterpret_cast<const h8_t*>(xa + 256 * b + 64 * (o >> 2) + 8 * (o & 3));
-    // the single staging buffer is rewritten only after this item's fragment reads were
-    // issued: LDS executes a wave's instructions in order
-    Q6Frag Fn;
-    if (i + 1 < hi) {
-      q6_stage(stg, g1, r, c);
-      q6_frag(Fn, stg, col, h, e);
-    }
-    const f4_t D = q6_block(F, A, e);
-    acc += (tlx_h2f((uint16_t)F.d) * 1024.0f) * D;
-    F = Fn;
-    g1 = g2;
-    if (b == nb - 1 || i == hi - 1) {  // end of a tile segment
-      if (seg - tl * nb == 0 && b == nb - 1) store(acc, t0 + tl);
-      else if (tl == lo / nb) accFirst = acc;
-      else accLast = acc;
-      acc = f4_t{0.f, 0.f, 0.f, 0.f};
-      seg = i + 1;
+    for (int p = 0; p < kPrefetch; ++p) {
+      const int i = i0 + p;  // i >= hi: padding steps of the last round, computed and discarded
+      const int ic = min(i, last);
+      const int tl = ic / nb, b = ic - tl * nb;
+      h8_t A[8];
+#pragma unroll
+      for (int o = 0; o < 8; ++o)
+        A[o] = *reinterpret_cast<const h8_t*>(xa + 256 * b + 64 * (o >> 2) + 8 * (o & 3));
+      // item i+1 goes through the single staging tile after item i's fragment reads were
+      // issued (LDS executes a wave's instructions in order); its ring slot is then refilled
+      q6_stage(stg, g[(p + 1) % kPrefetch], r, c);
+      q6_frag(F[(p + 1) & 1], stg, col, h, e);
+      const f4_t D = q6_block(F[p & 1], A, e);
+      q6_load<LAYOUT>(g[(p + 1) % kPrefetch], a.w, blk_of(min(i + 1 + kPrefetch, last)), c);
+      if (i < hi) {
+        acc += (tlx_h2f((uint16_t)F[p & 1].d) * 1024.0f) * D;
+        if (b == nb - 1 || i == hi - 1) {  // end of a tile segment
+          if (seg - tl * nb == 0 && b == nb - 1) store(acc, t0 + tl);
+          else if (tl == lo / nb) accFirst = acc;
+          else accLast = acc;
+          acc = f4_t{0.f, 0.f, 0.f, 0.f};
+          seg = i + 1;
+        }
+      }
     }
   }
 
@@ -263,8 +279,7 @@ int q6_gemv16_launch(const uint8_t* w, const _Float16* x, uint16_t* out, int M, 
   for (int m0 = 0; m0 < M; m0 += mc) {
     KqArgs a{w, x + (size_t)m0 * K, out + (size_t)m0 * N, std::min(mc, M - m0), N, K, 0};
     const size_t lds = q6_lds_bytes(a.M, K);
-    const int per_cu = lds * 2 <= (size_t)kLdsMax ? 2 : 1;
-    int grid = std::min(T, tlx_cu_count() * per_cu);
+    int grid = std::min(T, tlx_cu_count());  // one resident workgroup per CU (VGPR-bound)
     a.tw = (T + grid - 1) / grid;
     grid = (T + a.tw - 1) / a.tw;
     q6_gemv16_kernel<LAYOUT><<<grid, kWaves * TLX_WAVE, lds, st>>>(a);
@@ -277,7 +292,8 @@ int q6_gemv16_launch(const uint8_t* w, const _Float16* x, uint16_t* out, int M, 
 int q6_check(const void* w, const void* x, const void* out, int M, int N, int K, int layout) {
   if (M < 1 || M > TLX_MAX_M || N < 1 || K < 256 || (K & 255)) return TLX_E_ARG;
   if (layout != TLX_LAYOUT_RAW && layout != TLX_LAYOUT_PACKED) return TLX_E_ARG;
-  if ((size_t)N * q6_geo(layout).bs * (K >> 8) > 0xFFFFFFFFull * 4) return TLX_E_ARG;
+  // 32-bit byte offsets inside the matrix
+  if ((size_t)N * q6_geo(layout).bs * (K >> 8) > 0xFFFFFFFFull) return TLX_E_ARG;
   if (!tlx_aligned(w, 2) || !tlx_aligned(x, 16) || !tlx_aligned(out, 2)) return TLX_E_ALIGN;
   return TLX_OK;
 }
