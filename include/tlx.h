@@ -49,6 +49,11 @@ int tlx_iq3xxs_dequant(const void* w, const float* gridf, void* out, int64_t row
                        int layout, int out_f16, void* stream);
 int tlx_q6k_dequant(const void* w, void* out, int64_t rows, int64_t kdim, int layout, int out_f16,
                     void* stream);
+/* Q4_K / Q5_K dequantization, bit-exact with ggml's dequantize_row_q4_K / q5_K (the order the
+ * reference's row bodies use: engine/aq3k8.cu:44-53, engine/head8.cu:70-89):
+ * y = (d*sc)*q - dmin*m in fp32.  out: float32 or (out_f16 != 0) fp16 [rows][kdim]. */
+int tlx_q4k_dequant(const void* w, void* out, int64_t rows, int64_t kdim, int out_f16, void* stream);
+int tlx_q5k_dequant(const void* w, void* out, int64_t rows, int64_t kdim, int out_f16, void* stream);
 int tlx_iq4xs_dequant(const void* w, const float* iq4nl, float* out, int64_t rows, int64_t kdim,
                       void* stream);
 
@@ -95,6 +100,21 @@ int tlx_q6k_gemv(const void* w, const float* x, float* y, int rows, int K, int l
  * activations do not fit the LDS budget run as consecutive row groups. */
 int tlx_q6k_gemv16(const void* w, const uint16_t* x_f16, uint16_t* out_f16, int M, int N, int K,
                    int layout, void* stream);
+
+/* Q4_K / Q5_K GEMV with fp16 activations and fp16 outputs: out[m][n] = half(sum_k W[n][k]*x[m][k])
+ * with W = (d*sc)*q - dmin*m per GGUF block (144 B / 176 B raw, 16-B aligned rows).  The Q4_K
+ * body is the v-row body of the fused attention projections (KVBODY8, engine/aq3k8.cu:27-61);
+ * the Q5_K body is the dense lm_head's Q5ROW (engine/head8.cu:65-96).  M in 1..16. */
+int tlx_q4k_gemv16(const void* w, const uint16_t* x_f16, uint16_t* out_f16, int M, int N, int K,
+                   void* stream);
+int tlx_q5k_gemv16(const void* w, const uint16_t* x_f16, uint16_t* out_f16, int M, int N, int K,
+                   void* stream);
+
+/* Dense lm_head, Q5_K: logits[m][v] = half(W[v]·xh[m]).
+ * Replaces head8 / head8v{M} (engine/head8.cu:134-141, engine/head8v11.cu:88-121):
+ * head8(wq5, xh, logits); the vocabulary size and K are explicit. */
+int tlx_head8(const void* wq5, const uint16_t* xh_f16, uint16_t* logits_f16, int M, int vocab,
+              int K, void* stream);
 
 /* Fused attention q/k/v projections with a Q6_K q (the reference's Q6_K attention layers):
  * q through tlx_q6k_gemv16 (layout as there; the padded 212-B blocks for aq6k8), k and v

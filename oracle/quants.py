@@ -13,6 +13,8 @@ IQ3XXS_BYTES = 98                # d f16 | qs[64] | sw u32[8]
 Q6K_BYTES = 210                  # ql[128] | qh[64] | sc i8[16] | d f16
 Q6K_PAD_BYTES = 212              # pad[2] | d f16 | sc[16] | ql[128] | qh[64]
 IQ4XS_BYTES = 136                # d f16 | scales_h u16 | scales_l[4] | qs[128]
+Q4K_BYTES = 144                  # d f16 | dmin f16 | scales[12] | qs[128]
+Q5K_BYTES = 176                  # d f16 | dmin f16 | scales[12] | qh[32] | qs[128]
 
 
 def _grid_f32():
@@ -279,3 +281,107 @@ def dequant_iq4xs_lanes(raw, kdim):
                     dl = np.float32(d * np.float32(ls - 32))
                     out[r, b * 256 + ibb * 32 + lane] = np.float32(dl * kv[nib])
     return out
+
+
+# --------------------------------------------------------------------------- Q4_K / Q5_K
+# The reference has no numpy statement of these two formats; its CUDA row bodies define them
+# (Q5ROW, /root/reference/engine/head8.cu:65-96; KVBODY8's Q4_K v rows,
+# /root/reference/engine/aq3k8.cu:27-61; the index law in /root/reference/docs/DEXT_LAWS.md:
+# 190-192).  Both follow ggml's ``dequantize_row_q4_K`` / ``dequantize_row_q5_K`` (the GGUF
+# format definition, reached by the reference through tinygrad's ggml bindings):
+# ``y = (d*sc)*q - (dmin*m)`` in fp32, no fused multiply-add.  Each format is restated twice:
+# in ggml's loop form and in the reference kernels' per-lane form.
+
+def k4_scale_min(sc12):
+    """6-bit (scale, min) pairs of the 8 sub-blocks from the 12 packed bytes
+    (ggml ``get_scale_min_k4``): j < 4 -> (q[j] & 63, q[j+4] & 63); j >= 4 ->
+    ((q[j+4] & 0xF) | (q[j-4] >> 6) << 4, (q[j+4] >> 4) | (q[j] >> 6) << 4)."""
+    q = np.asarray(sc12, dtype=np.int64)
+    sc = np.empty(q.shape[:-1] + (8,), dtype=np.int64)
+    mn = np.empty_like(sc)
+    for j in range(8):
+        if j < 4:
+            sc[..., j] = q[..., j] & 63
+            mn[..., j] = q[..., j + 4] & 63
+        else:
+            sc[..., j] = (q[..., j + 4] & 0xF) | ((q[..., j - 4] >> 6) << 4)
+            mn[..., j] = (q[..., j + 4] >> 4) | ((q[..., j] >> 6) << 4)
+    return sc, mn
+
+
+def _kq_dequant_loop(raw, kdim, five):
+    nbytes = Q5K_BYTES if five else Q4K_BYTES
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    n = raw.shape[0]
+    nb = kdim >> 8
+    assert raw.shape[1] == nbytes * nb, raw.shape
+    blk = raw.reshape(n, nb, nbytes)
+    d = _f16(blk[:, :, 0:2])
+    dmin = _f16(blk[:, :, 2:4])
+    sc, mn = k4_scale_min(blk[:, :, 4:16])
+    qh = blk[:, :, 16:48].astype(np.int64) if five else None
+    qs = blk[:, :, 48:176].astype(np.int64) if five else blk[:, :, 16:144].astype(np.int64)
+    y = np.empty((n, nb, QK), dtype=np.float32)
+    for j in range(4):  # 64 elements per step: low nibbles (sub-block 2j), then high (2j+1)
+        for half in range(2):
+            s_ = 2 * j + half
+            d1 = d * sc[:, :, s_].astype(np.float32)
+            m1 = dmin * mn[:, :, s_].astype(np.float32)
+            q = (qs[:, :, 32 * j:32 * j + 32] >> (4 * half)) & 0xF
+            if five:
+                q = q + (((qh >> s_) & 1) << 4)
+            y[:, :, 64 * j + 32 * half:64 * j + 32 * half + 32] = (
+                d1[:, :, None] * q.astype(np.float32) - m1[:, :, None])
+    return y.reshape(n, kdim)
+
+
+def dequant_q4k(raw, kdim):
+    """GGUF Q4_K rows u8[N, 144*NB] -> float32[N, kdim] (ggml loop form)."""
+    return _kq_dequant_loop(raw, kdim, False)
+
+
+def dequant_q5k(raw, kdim):
+    """GGUF Q5_K rows u8[N, 176*NB] -> float32[N, kdim] (ggml loop form)."""
+    return _kq_dequant_loop(raw, kdim, True)
+
+
+def _kq_dequant_lanes(raw, kdim, five):
+    nbytes = Q5K_BYTES if five else Q4K_BYTES
+    qoff = 48 if five else 16
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    n = raw.shape[0]
+    nb = kdim >> 8
+    out = np.empty((n, kdim), dtype=np.float32)
+    for r in range(n):
+        for b in range(nb):
+            blk = raw[r, b * nbytes:(b + 1) * nbytes].astype(np.int64)
+            d = np.float32(raw[r, b * nbytes:b * nbytes + 2].view(np.float16)[0])
+            dm = np.float32(raw[r, b * nbytes + 2:b * nbytes + 4].view(np.float16)[0])
+            for lane in range(32):
+                s_ = lane >> 2
+                if s_ < 4:
+                    sc, mn = blk[4 + s_] & 63, blk[8 + s_] & 63
+                else:
+                    sc = (blk[8 + s_] & 0xF) | ((blk[s_] >> 6) << 4)
+                    mn = (blk[8 + s_] >> 4) | ((blk[s_ + 4] >> 6) << 4)
+                nsh = ((lane >> 2) & 1) * 4
+                for j in range(8):
+                    qv = (int(blk[qoff + ((lane >> 3) << 5) + ((lane & 3) << 3) + j]) >> nsh) & 0xF
+                    if five:
+                        qv += ((int(blk[16 + ((lane & 3) << 3) + j]) >> s_) & 1) << 4
+                    t = np.float32(d * np.float32(sc))
+                    out[r, 256 * b + 8 * lane + j] = np.float32(t * np.float32(qv)) - np.float32(dm * np.float32(mn))
+    return out
+
+
+def dequant_q4k_lanes(raw, kdim):
+    """Q4_K rows -> float32 via the per-lane form of KVBODY8 (/root/reference/engine/aq3k8.cu:
+    36-55): lane l owns k = 8l + j; qs byte 16 + 32(l>>3) + 8(l&3) + j, nibble 4((l>>2)&1);
+    sub-block l>>2 for the 6-bit scale and min."""
+    return _kq_dequant_lanes(raw, kdim, False)
+
+
+def dequant_q5k_lanes(raw, kdim):
+    """Q5_K rows -> float32 via the per-lane form of Q5ROW (/root/reference/engine/head8.cu:
+    68-90): as Q4_K with qs at byte 48, plus bit (l>>2) of qh byte 16 + 8(l&3) + j as q's bit 4."""
+    return _kq_dequant_lanes(raw, kdim, True)

@@ -158,3 +158,67 @@ def test_iq4_zero_scale_group():
 def test_iq4_two_restatements_agree(rows, kdim):
     raw = synth.iq4xs_raw(np.random.default_rng(9 + rows), rows, kdim)
     assert np.array_equal(quants.dequant_iq4xs(raw, kdim), quants.dequant_iq4xs_lanes(raw, kdim))
+
+
+# --------------------------------------------------------------------------- Q4_K / Q5_K
+def _k4_pack_scales(sc, mn):
+    """12-byte encoding of eight 6-bit (scale, min) pairs, written from the bit layout: bytes
+    0-3 hold scales 0-3 in bits 0-5 and bits 4-5 of scales 4-7 in bits 6-7; bytes 4-7 the same
+    for the mins; bytes 8-11 hold the low nibbles of scale 4+j (bits 0-3) and min 4+j (4-7)."""
+    q = np.zeros(12, dtype=np.uint8)
+    for j in range(4):
+        q[j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+        q[j + 4] = mn[j] | ((mn[j + 4] >> 4) << 6)
+        q[j + 8] = (sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4)
+    return q
+
+
+def _k4_block(five, d, dmin, sc, mn, qs_byte, qh_byte=0):
+    blk = np.zeros(176 if five else 144, dtype=np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    blk[2:4] = np.frombuffer(np.float16(dmin).tobytes(), np.uint8)
+    blk[4:16] = _k4_pack_scales(sc, mn)
+    if five:
+        blk[16:48] = qh_byte
+        blk[48:176] = qs_byte
+    else:
+        blk[16:144] = qs_byte
+    return blk[None, :]
+
+
+def test_k4_scale_min_round_trip():
+    rng = np.random.default_rng(4)
+    for _ in range(50):
+        sc = rng.integers(0, 64, 8)
+        mn = rng.integers(0, 64, 8)
+        got_sc, got_mn = quants.k4_scale_min(_k4_pack_scales(sc, mn))
+        assert np.array_equal(got_sc, sc) and np.array_equal(got_mn, mn)
+
+
+@pytest.mark.parametrize("five", [False, True])
+def test_k4_known_answers(five):
+    sc = np.arange(8) * 7 + 1          # distinct 6-bit scales 1..50
+    mn = 63 - np.arange(8) * 5         # distinct mins 63..28
+    deq = quants.dequant_q5k if five else quants.dequant_q4k
+    # all quants zero: every weight is -dmin*m of its sub-block
+    y = deq(_k4_block(five, 0.5, 0.25, sc, mn, 0x00), 256)[0]
+    np.testing.assert_array_equal(y, np.repeat(-0.25 * mn.astype(np.float32), 32))
+    # all quants at their maximum: (d*sc)*qmax - dmin*m
+    qmax = 31 if five else 15
+    y = deq(_k4_block(five, 0.5, 0.25, sc, mn, 0xFF, 0xFF), 256)[0]
+    np.testing.assert_array_equal(y, np.repeat((0.5 * sc * qmax - 0.25 * mn).astype(np.float32), 32))
+    # low nibble 3, high nibble 9 (and for Q5_K only the bits of sub-blocks 1 and 6 set):
+    # element k reads nibble (k >> 5) & 1 of byte 32(k >> 6) + (k & 31), qh bit k >> 5
+    y = deq(_k4_block(five, 1.0, 0.0, np.ones(8, int), np.zeros(8, int), 0x93, 0b01000010), 256)[0]
+    k = np.arange(256)
+    want = np.where((k >> 5) & 1, 9, 3) + (16 * np.isin(k >> 5, [1, 6]) if five else 0)
+    np.testing.assert_array_equal(y, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("five", [False, True])
+@pytest.mark.parametrize("rows,kdim", [(3, 512), (1, 2048)])
+def test_k4_two_restatements_agree(five, rows, kdim):
+    raw = synth.k4_raw(np.random.default_rng(rows + kdim + five), rows, kdim, five)
+    a = (quants.dequant_q5k if five else quants.dequant_q4k)(raw, kdim)
+    b = (quants.dequant_q5k_lanes if five else quants.dequant_q4k_lanes)(raw, kdim)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

@@ -38,6 +38,11 @@ SIGNATURES = {
     "tlx_aq3k8": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
     "tlx_q6k_gemv": [_p, _p, _p, _i, _i, _i, _p],
     "tlx_q6k_gemv16": [_p, _p, _p, _i, _i, _i, _i, _p],
+    "tlx_q4k_gemv16": [_p, _p, _p, _i, _i, _i, _p],
+    "tlx_q5k_gemv16": [_p, _p, _p, _i, _i, _i, _p],
+    "tlx_head8": [_p, _p, _p, _i, _i, _i, _p],
+    "tlx_q4k_dequant": [_p, _p, _i64, _i64, _i, _p],
+    "tlx_q5k_dequant": [_p, _p, _i64, _i64, _i, _p],
     "tlx_aq6k8": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
     "tlx_pfg3_ffn": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_pfg3_iq3d": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],

@@ -154,6 +154,47 @@ def q6k_gemv16(w, x, out, layout=LAYOUT_PACKED, stream=None):
     return out
 
 
+def _k4_gemv(name, nbytes, w, x, out, stream):
+    M, K = x.shape
+    N = out.shape[-1]
+    _need(w, N * nbytes * (K // 256), "w")
+    _need(out, M * N * 2, "out")
+    _dev(w, x, out)
+    call(name, w.data_ptr(), x.data_ptr(), out.data_ptr(), M, N, K, _stream(stream))
+    return out
+
+
+def q4k_gemv16(w, x, out, stream=None):
+    """out[m][n] = half(W[n]·x[m]), GGUF Q4_K rows (144-B blocks), fp16 x and out."""
+    return _k4_gemv("tlx_q4k_gemv16", 144, w, x, out, stream)
+
+
+def q5k_gemv16(w, x, out, stream=None):
+    """out[m][n] = half(W[n]·x[m]), GGUF Q5_K rows (176-B blocks), fp16 x and out."""
+    return _k4_gemv("tlx_q5k_gemv16", 176, w, x, out, stream)
+
+
+def head8(wq5, xh, logits, stream=None):
+    """Dense Q5_K lm_head: logits[m][v] = half(W[v]·xh[m])   (head8 contract)."""
+    return _k4_gemv("tlx_head8", 176, wq5, xh, logits, stream)
+
+
+def _k4_dequant(name, nbytes, w, out, kdim, stream):
+    rows = w.numel() // (nbytes * (kdim // 256))
+    _need(out, rows * kdim * out.element_size(), "out")
+    _dev(w, out)
+    call(name, w.data_ptr(), out.data_ptr(), rows, kdim, int(out.dtype == _F16), _stream(stream))
+    return out
+
+
+def q4k_dequant(w, out, kdim, stream=None):
+    return _k4_dequant("tlx_q4k_dequant", 144, w, out, kdim, stream)
+
+
+def q5k_dequant(w, out, kdim, stream=None):
+    return _k4_dequant("tlx_q5k_dequant", 176, w, out, kdim, stream)
+
+
 def aq6k8(wq, wk, wv, gridf, xh, qrow, krow, vrow, layout=LAYOUT_PACKED, stream=None):
     """Fused attention projections with a Q6_K q (padded 212-B blocks for ``LAYOUT_PACKED``,
     raw 210-B for ``LAYOUT_RAW``) and IQ3_XXS packed-row k and v."""

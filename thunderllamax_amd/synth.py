@@ -40,6 +40,19 @@ def q6k_raw(rng, rows, kdim):
     return blk.reshape(rows, nb * 210)
 
 
+def k4_raw(rng, rows, kdim, five):
+    """GGUF Q4_K (five=False, 144*NB B) or Q5_K (176*NB B) rows: d and dmin as above, then
+    uniform scale, qh and qs bytes."""
+    nb = kdim // 256
+    nbytes = 176 if five else 144
+    d = _d16(rng, (rows, nb, 2))
+    rest = rng.integers(0, 256, size=(rows, nb, nbytes - 4), dtype=np.uint8)
+    blk = np.empty((rows, nb, nbytes), dtype=np.uint8)
+    blk[:, :, 0:4] = d.view(np.uint8).reshape(rows, nb, 4)
+    blk[:, :, 4:] = rest
+    return blk.reshape(rows, nb * nbytes)
+
+
 def iq3xxs_raw(rng, rows, kdim):
     """GGUF IQ3_XXS rows u8[rows, 98*NB]: d, then grid-index bytes, then scale/sign words."""
     nb = kdim // 256
