@@ -78,13 +78,32 @@ int tlx_down8(const void* wd, const float* gridf, const uint16_t* gact_f16, cons
 int tlx_iq3_gemv(const void* w, const float* gridf, const uint16_t* x_f16, uint16_t* out_f16,
                  int M, int N, int K, int layout, void* stream);
 
-/* Fused attention q/k/v projections, all three IQ3_XXS (the BASELINE dense config):
- * warp ranges [0,Nq) q, [Nq,Nq+Nk) k, [.., +Nv) v in one launch.
- * Replaces aq3k8 / aq3k8v{4..11} (engine/aq3k8.cu:134-145, engine/aq3k8v11.cu:88-180):
- * aq3k8(wq, wk, wv4, gridf, xh, qrow, krow, vrow). */
+/* Fused attention q/k/v projections (one entry per reference kernel; one launch per quant
+ * format on `stream`; all arguments are validated before any launch):
+ *   tlx_aq3k8: q, k (and v) IQ3_XXS in `layout` (PACKED rows or RAW blocks); v is IQ3_XXS
+ *     (the benchmark's dense configuration) unless `layout` has TLX_V_Q4K, then GGUF Q4_K (the reference's
+ *     wv4).  Replaces aq3k8 / aq3k8v{4..11} (engine/aq3k8.cu:134-145, engine/aq3k8v11.cu:88-180):
+ *     aq3k8(wq, wk, wv4, gridf, xh, qrow, krow, vrow).
+ *   tlx_aq6k8: q Q6_K (layout PACKED = padded 212-B blocks, RAW = 210-B), k (and v) IQ3_XXS
+ *     packed rows, v Q4_K with TLX_V_Q4K.  Replaces aq6k8 (engine/aq6k8.cu:134-173).
+ *   tlx_a_qkv_iq3: q, k IQ3_XXS GGUF blocks, v Q4_K.  Replaces a_qkv_iq3
+ *     (engine/a_qkv_iq3.cu:88-127).
+ *   tlx_a_qkv_q6: q Q6_K 210-B blocks, k IQ3_XXS GGUF blocks, v Q4_K.  Replaces a_qkv_q6
+ *     (engine/a_qkv_q6.cu:88-125).
+ * xh_f16: [M][K]; qrow/krow/vrow: fp16 [M][Nq|Nk|Nv]. */
+#define TLX_V_Q4K 0x100  /* or-ed into `layout`: v rows are GGUF Q4_K */
 int tlx_aq3k8(const void* wq, const void* wk, const void* wv, const float* gridf,
               const uint16_t* xh_f16, uint16_t* qrow_f16, uint16_t* krow_f16, uint16_t* vrow_f16,
               int M, int Nq, int Nk, int Nv, int K, int layout, void* stream);
+int tlx_aq6k8(const void* wq, const void* wk, const void* wv, const float* gridf,
+              const uint16_t* xh_f16, uint16_t* qrow_f16, uint16_t* krow_f16, uint16_t* vrow_f16,
+              int M, int Nq, int Nk, int Nv, int K, int layout, void* stream);
+int tlx_a_qkv_iq3(const void* wq, const void* wk, const void* wv4, const float* gridf,
+                  const uint16_t* xh_f16, uint16_t* qrow_f16, uint16_t* krow_f16,
+                  uint16_t* vrow_f16, int M, int Nq, int Nk, int Nv, int K, void* stream);
+int tlx_a_qkv_q6(const void* wq, const void* wk, const void* wv4, const float* gridf,
+                 const uint16_t* xh_f16, uint16_t* qrow_f16, uint16_t* krow_f16,
+                 uint16_t* vrow_f16, int M, int Nq, int Nk, int Nv, int K, void* stream);
 
 /* Q6_K GEMV, fp32 activations and outputs: y[n] = sum_k ((d*sc)*(q-32))[n][k] * x[k].
  * The contract of h6k2048 (engine/mm/MM_P34_h6k2048.cu:8-52): h6k2048(w, x, y, rows),
@@ -116,14 +135,6 @@ int tlx_q5k_gemv16(const void* w, const uint16_t* x_f16, uint16_t* out_f16, int 
 int tlx_head8(const void* wq5, const uint16_t* xh_f16, uint16_t* logits_f16, int M, int vocab,
               int K, void* stream);
 
-/* Fused attention q/k/v projections with a Q6_K q (the reference's Q6_K attention layers):
- * q through tlx_q6k_gemv16 (layout as there; the padded 212-B blocks for aq6k8), k and v
- * IQ3_XXS packed rows (BASELINE's dense config; the reference's v is Q4_K).
- * Replaces aq6k8 / aq6k8v{4..11} (engine/aq6k8.cu:134-173): aq6k8(wq, wk, wv4, gridf, xh,
- * qrow, krow, vrow).  Two launches on `stream`; arguments are validated before either. */
-int tlx_aq6k8(const void* wq, const void* wk, const void* wv, const float* gridf,
-              const uint16_t* xh_f16, uint16_t* qrow_f16, uint16_t* krow_f16, uint16_t* vrow_f16,
-              int M, int Nq, int Nk, int Nv, int K, int layout, void* stream);
 
 /* ---- prefill dequant-GEMM (M rows of a prompt chunk, MFMA fp16 x fp16 -> fp32) ----
  * x16 is M x K fp16 row-major; W is N IQ3_XXS rows in the packed7 layout (TLX_LAYOUT_PACK7,
@@ -157,7 +168,7 @@ int tlx_pfg3_iq3o(const void* w, const float* gridf, const uint16_t* x16, uint16
 
 /* Top-8 + renormalized softmax from router logits f32[P][256] (the router epilogue of
  * engine/mm/MM_P1_rt8e256.cu:41-60: strict >, ties to the lower id).  eids u16[P][8],
- * gates f32[P][8].  No reference counterpart on its own: BASELINE config 5 feeds logits. */
+ * gates f32[P][8].  No reference counterpart on its own: the benchmark's MoE configuration feeds logits. */
 int tlx_moe_topk(const float* logits, uint16_t* eids, float* gates, int P, void* stream);
 
 /* Router: logits = wrt[256][2048] . h[P][2048], top-8 + softmax, sg = sigmoid(wsh . h).
@@ -188,7 +199,7 @@ int tlx_moe_dn4(const uint64_t* ptbl_dn, const int* eoff, const uint16_t* plist,
 
 /* Shared expert over all P positions: act[P][512] (caller scratch) then out[P][2048] f32.
  * ptbl_sh = {gate/up slab, down slab}.  Replaces shgu32 / shdn32 (engine/mm/MM_P2_ports.py:195-201
- * restates them) with the IQ4_XS weights of BASELINE config 5. */
+ * restates them) with the IQ4_XS weights of the benchmark's MoE configuration. */
 int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const float* iq4nl, float* act, float* out,
                    int P, void* stream);
 

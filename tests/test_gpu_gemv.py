@@ -209,3 +209,84 @@ def test_bad_arguments_raise(gpu):
     out = torch.zeros(17, 16, dtype=torch.float16, device=gpu)
     with pytest.raises(TlxError):
         ops.ffn8(w, w, g, x, out)
+
+
+# ---------------------------------------------------------------- GGUF-block (raw) IQ3_XXS rows
+@pytest.mark.parametrize("M,K", [(1, 5120), (11, 5120), (4, 768)])
+def test_iq3_gemv_raw_blocks(gpu, M, K):
+    """The GEMV on GGUF-ordered blocks (2-B aligned fields; an odd block count is allowed)."""
+    print(f"[case] iq3_gemv raw M={M} K={K}", flush=True)
+    rng = np.random.default_rng(400 + M + K)
+    N = 300
+    raw = synth.iq3xxs_raw(rng, N, K)
+    x = synth.activations_f16(rng, M, K)
+    out = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    ops.iq3_gemv(torch.from_numpy(raw).to(gpu), formats.gridf_tensor(gpu), torch.from_numpy(x).to(gpu),
+                 out, LAYOUT_RAW)
+    torch.cuda.synchronize()
+    _, ref = gemv.gemv16_ref(quants.dequant_iq3xxs_blocks(raw.reshape(-1, 98)).reshape(N, K), x)
+    assert _rows_err(out.cpu().numpy(), ref) <= TOL
+
+
+def test_ffn8_and_down8_raw_blocks(gpu):
+    print("[case] ffn8/down8 raw", flush=True)
+    rng = np.random.default_rng(501)
+    N, K, M = 256, 5120, 5
+    rg, ru = synth.iq3xxs_raw(rng, N, K), synth.iq3xxs_raw(rng, N, K)
+    x = synth.activations_f16(rng, M, K)
+    g = formats.gridf_tensor(gpu)
+    gact = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    ops.ffn8(torch.from_numpy(rg).to(gpu), torch.from_numpy(ru).to(gpu), g, torch.from_numpy(x).to(gpu),
+             gact, LAYOUT_RAW)
+    deq = lambda r, k: quants.dequant_iq3xxs_blocks(r.reshape(-1, 98)).reshape(len(r), k)
+    _, _, ref = gemv.ffn8_ref(deq(rg, K), deq(ru, K), x)
+    assert _rows_err(gact.cpu().numpy(), ref) <= TOL
+    Kd = 1024
+    rd = synth.iq3xxs_raw(rng, N, Kd)
+    xd = synth.activations_f16(rng, M, Kd)
+    hh = rng.standard_normal((M, N)).astype(np.float32)
+    y = torch.empty(M, N, dtype=torch.float32, device=gpu)
+    ops.down8(torch.from_numpy(rd).to(gpu), g, torch.from_numpy(xd).to(gpu), torch.from_numpy(hh).to(gpu),
+              y, LAYOUT_RAW)
+    torch.cuda.synchronize()
+    _, refd = gemv.down8_ref(deq(rd, Kd), xd, hh)
+    assert _rows_err(y.cpu().numpy() - hh, refd - hh) <= TOL
+
+
+# ---------------------------------------------------------------- fused attention variants
+def _attn_case(gpu, name, M, seed):
+    from thunderllamax_amd._lib import V_Q4K
+    rng = np.random.default_rng(seed)
+    K, Nq, Nk, Nv = 5120, 384, 64, 48
+    deq3 = lambda r: quants.dequant_iq3xxs_blocks(r.reshape(-1, 98)).reshape(len(r), K)
+    rq3, rk3, rv3 = synth.iq3xxs_raw(rng, Nq, K), synth.iq3xxs_raw(rng, Nk, K), synth.iq3xxs_raw(rng, Nv, K)
+    rq6 = synth.q6k_raw(rng, Nq, K)
+    rv4 = synth.k4_raw(rng, Nv, K, False)
+    x = synth.activations_f16(rng, M, K)
+    pk = lambda r: formats.iq3_pack_rows(r, K)
+    if name == "aq3k8_v4":
+        w = (pk(rq3), pk(rk3), rv4); fn = lambda *a: ops.aq3k8(*a, layout=LAYOUT_PACKED | V_Q4K)
+        W = (deq3(rq3), deq3(rk3), quants.dequant_q4k(rv4, K))
+    elif name == "aq6k8_raw_v4":
+        w = (rq6, pk(rk3), rv4); fn = lambda *a: ops.aq6k8(*a, layout=LAYOUT_RAW | V_Q4K)
+        W = (quants.dequant_q6k(rq6, K), deq3(rk3), quants.dequant_q4k(rv4, K))
+    elif name == "a_qkv_iq3":
+        w = (rq3, rk3, rv4); fn = ops.a_qkv_iq3
+        W = (deq3(rq3), deq3(rk3), quants.dequant_q4k(rv4, K))
+    else:
+        w = (rq6, rk3, rv4); fn = ops.a_qkv_q6
+        W = (quants.dequant_q6k(rq6, K), deq3(rk3), quants.dequant_q4k(rv4, K))
+    outs = [torch.empty(M, n, dtype=torch.float16, device=gpu) for n in (Nq, Nk, Nv)]
+    fn(*[torch.from_numpy(np.ascontiguousarray(t)).to(gpu) for t in w], formats.gridf_tensor(gpu),
+       torch.from_numpy(x).to(gpu), *outs)
+    torch.cuda.synchronize()
+    return [_rows_err(o.cpu().numpy(), gemv.gemv16_ref(Wm, x)[1]) for o, Wm in zip(outs, W)]
+
+
+@pytest.mark.parametrize("name", ["aq3k8_v4", "aq6k8_raw_v4", "a_qkv_iq3", "a_qkv_q6"])
+@pytest.mark.parametrize("M", [1, 11])
+def test_attention_variants(gpu, name, M):
+    print(f"[case] attention {name} M={M}", flush=True)
+    errs = _attn_case(gpu, name, M, 600 + M)
+    print(f"[{name} M={M}] q/k/v rel-err {errs}")
+    assert max(errs) <= TOL

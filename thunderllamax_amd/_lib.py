@@ -19,6 +19,7 @@ TLX_E_NODEV = -3
 LAYOUT_RAW = 0
 LAYOUT_PACKED = 1
 LAYOUT_PACK7 = 2
+V_Q4K = 0x100   # or-ed into the fused attention layout: v rows are GGUF Q4_K
 MAX_M = 16
 
 _p = ctypes.c_void_p
@@ -38,6 +39,8 @@ SIGNATURES = {
     "tlx_aq3k8": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
     "tlx_q6k_gemv": [_p, _p, _p, _i, _i, _i, _p],
     "tlx_q6k_gemv16": [_p, _p, _p, _i, _i, _i, _i, _p],
+    "tlx_a_qkv_iq3": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
+    "tlx_a_qkv_q6": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "tlx_q4k_gemv16": [_p, _p, _p, _i, _i, _i, _p],
     "tlx_q5k_gemv16": [_p, _p, _p, _i, _i, _i, _p],
     "tlx_head8": [_p, _p, _p, _i, _i, _i, _p],

@@ -77,8 +77,13 @@ static inline int tlx_cu_count() {
   return cache[dev];
 }
 
-// k/v segments of the fused attention projections on IQ3_XXS packed rows (tlx_iq3.hip);
-// launch == false validates the arguments only.
-int tlx_iq3_kv(const void* wk, const void* wv, const float* gridf, const uint16_t* xh_f16,
-               uint16_t* krow_f16, uint16_t* vrow_f16, int M, int Nk, int Nv, int K, bool launch,
-               void* stream);
+// Internal entry points shared by the fused attention projections (tlx_attn.hip).  With
+// launch == false they validate the arguments only.
+//   IQ3_XXS: up to three matrices (packed rows or GGUF blocks) sharing the activations, one
+//   launch (tlx_iq3.hip);
+int tlx_iq3_segments(const void* const* w, uint16_t* const* out, const int* n, int nseg,
+                     const float* gridf, const uint16_t* xh_f16, int M, int K, int layout,
+                     bool launch, void* stream);
+//   k-quants: fmt 0 = Q6_K raw, 1 = Q6_K padded, 2 = Q4_K, 3 = Q5_K (tlx_kquant.hip).
+int tlx_kq_gemv(int fmt, const void* w, const uint16_t* x_f16, uint16_t* out_f16, int M, int N,
+                int K, bool launch, void* stream);

@@ -76,6 +76,7 @@ struct Iq3Launch {
   const float* gridf;
   const _Float16* x;   // [M][K]
   int M, K;
+  int raw;             // GGUF blocks [d][qs 64][sw 32] (1) or packed rows [qs][sw][d] (0)
 };
 
 template <int NMAT>
@@ -87,14 +88,17 @@ struct Iq3Regs {
 
 // Loads one block of the lane's row: 16 B of grid indices, 8 B of scale/sign words, the d.
 // Offsets are 32-bit (a matrix is < 4 GiB) from the matrix base.
+// The per-block strides are those of the layout: 64/32/2 B (packed rows) or 98 B (GGUF blocks,
+// whose fields are only 2-B aligned: the loads are unaligned there).
 template <int NMAT>
 __device__ __forceinline__ void iq3_load(Iq3Regs<NMAT>& r, const uint8_t* const* base, uint32_t qoff,
-                                         uint32_t soff, uint32_t doff, int b) {
+                                         uint32_t soff, uint32_t doff, uint32_t qst, uint32_t sst,
+                                         uint32_t dst, int b) {
 #pragma unroll
   for (int i = 0; i < NMAT; ++i) {
-    r.qs[i] = *reinterpret_cast<const u4_t*>(base[i] + qoff + 64u * b);
-    r.sw[i] = *reinterpret_cast<const u2_t*>(base[i] + soff + 32u * b);
-    r.d[i] = *reinterpret_cast<const uint16_t*>(base[i] + doff + 2u * b);
+    r.qs[i] = tlx_ldu<u4_t>(base[i] + (qoff + qst * b));
+    r.sw[i] = tlx_ldu<u2_t>(base[i] + (soff + sst * b));
+    r.d[i] = tlx_ldu<uint16_t>(base[i] + (doff + dst * b));
   }
 }
 
@@ -115,7 +119,10 @@ __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Lau
   const int row0 = ((int)blockIdx.x - sg.tile0) * kTile;
   // tail tile: clamp the loads, mask the stores
   const uint32_t roff = (uint32_t)min(row0 + col, sg.n - 1) * rowb;
-  const uint32_t qoff = roff + 16u * kq, soff = roff + 64u * nb + 8u * kq, doff = roff + 96u * nb;
+  const uint32_t qoff = roff + (a.raw ? 2u : 0u) + 16u * kq;
+  const uint32_t soff = roff + (a.raw ? 66u : 64u * nb) + 8u * kq;
+  const uint32_t doff = roff + (a.raw ? 0u : 96u * nb);
+  const uint32_t qst = a.raw ? 98u : 64u, sst = a.raw ? 98u : 32u, dst = a.raw ? 98u : 2u;
 
   const uint8_t* base[NMAT];
   base[0] = sg.w0;
@@ -131,7 +138,7 @@ __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Lau
 
   int b = wave;
   Iq3Regs<NMAT> cur;
-  if (b < nb) iq3_load<NMAT>(cur, base, qoff, soff, doff, b);
+  if (b < nb) iq3_load<NMAT>(cur, base, qoff, soff, doff, qst, sst, dst, b);
   for (; b < nb; b += WAVES) {
     // this block's activations first, then the next block's weights: waiting for the
     // activations leaves the weight prefetch in flight
@@ -140,7 +147,7 @@ __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Lau
     for (int t = 0; t < 8; ++t) X[t] = *reinterpret_cast<const h8_t*>(xr + 256 * b + 8 * t);
     Iq3Regs<NMAT> nxt;
     const bool more = b + WAVES < nb;
-    if (more) iq3_load<NMAT>(nxt, base, qoff, soff, doff, b + WAVES);
+    if (more) iq3_load<NMAT>(nxt, base, qoff, soff, doff, qst, sst, dst, b + WAVES);
 
 #pragma unroll
     for (int i = 0; i < NMAT; ++i) {
@@ -215,9 +222,11 @@ int iq3_launch(const Iq3Launch& a, int tiles, hipStream_t st) {
 
 int iq3_check(const void* w, int M, int N, int K, int layout) {
   if (M < 1 || M > TLX_MAX_M || N < 1 || K < 256 || (K & 255)) return TLX_E_ARG;
-  if (layout != TLX_LAYOUT_PACKED) return TLX_E_ARG;
-  // 16-B operand loads need dword-aligned rows: row bytes 98*NB with NB even
-  if (((K >> 8) & 1) || !tlx_aligned(w, 4)) return TLX_E_ALIGN;
+  if (layout != TLX_LAYOUT_PACKED && layout != TLX_LAYOUT_RAW) return TLX_E_ARG;
+  // packed rows: the operand loads are dword-aligned when the row bytes 98*NB are (NB even);
+  // GGUF blocks are 2-B aligned throughout
+  if (layout == TLX_LAYOUT_PACKED && (((K >> 8) & 1) || !tlx_aligned(w, 4))) return TLX_E_ALIGN;
+  if (!tlx_aligned(w, 2)) return TLX_E_ALIGN;
   // kernels address a matrix with 32-bit byte offsets
   if ((size_t)N * kIq3BlockBytes * (K >> 8) > 0xFFFFFFFFull) return TLX_E_ARG;
   return TLX_OK;
@@ -298,6 +307,7 @@ extern "C" int tlx_ffn8(const void* wg, const void* wu, const float* gridf, cons
   TLX_RET_IF(!tlx_aligned(hhx_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
   Iq3Launch a{};
   a.seg[0] = Iq3Seg{(const uint8_t*)wg, (const uint8_t*)wu, gact_f16, nullptr, N, 0};
+  a.raw = layout == TLX_LAYOUT_RAW;
   a.nseg = 1;
   a.gridf = gridf;
   a.x = (const _Float16*)hhx_f16;
@@ -313,6 +323,7 @@ extern "C" int tlx_down8(const void* wd, const float* gridf, const uint16_t* gac
   TLX_RET_IF(!tlx_aligned(gact_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
   Iq3Launch a{};
   a.seg[0] = Iq3Seg{(const uint8_t*)wd, nullptr, y, hh, N, 0};
+  a.raw = layout == TLX_LAYOUT_RAW;
   a.nseg = 1;
   a.gridf = gridf;
   a.x = (const _Float16*)gact_f16;
@@ -328,6 +339,7 @@ extern "C" int tlx_iq3_gemv(const void* w, const float* gridf, const uint16_t* x
   TLX_RET_IF(!tlx_aligned(x_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
   Iq3Launch a{};
   a.seg[0] = Iq3Seg{(const uint8_t*)w, nullptr, out_f16, nullptr, N, 0};
+  a.raw = layout == TLX_LAYOUT_RAW;
   a.nseg = 1;
   a.gridf = gridf;
   a.x = (const _Float16*)x_f16;
@@ -336,46 +348,29 @@ extern "C" int tlx_iq3_gemv(const void* w, const float* gridf, const uint16_t* x
   return iq3_launch<1, EPI_F16>(a, tiles_of(N), (hipStream_t)stream);
 }
 
-extern "C" int tlx_aq3k8(const void* wq, const void* wk, const void* wv, const float* gridf,
-                         const uint16_t* xh_f16, uint16_t* qrow_f16, uint16_t* krow_f16,
-                         uint16_t* vrow_f16, int M, int Nq, int Nk, int Nv, int K, int layout,
-                         void* stream) {
-  int rc = iq3_check(wq, M, Nq, K, layout);
-  if (rc == TLX_OK) rc = iq3_check(wk, M, Nk, K, layout);
-  if (rc == TLX_OK) rc = iq3_check(wv, M, Nv, K, layout);
-  TLX_RET_IF(rc != TLX_OK, rc);
-  TLX_RET_IF(!tlx_aligned(xh_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
-  Iq3Launch a{};
-  const int tq = tiles_of(Nq), tk = tiles_of(Nk), tv = tiles_of(Nv);
-  a.seg[0] = Iq3Seg{(const uint8_t*)wq, nullptr, qrow_f16, nullptr, Nq, 0};
-  a.seg[1] = Iq3Seg{(const uint8_t*)wk, nullptr, krow_f16, nullptr, Nk, tq};
-  a.seg[2] = Iq3Seg{(const uint8_t*)wv, nullptr, vrow_f16, nullptr, Nv, tq + tk};
-  a.nseg = 3;
-  a.gridf = gridf;
-  a.x = (const _Float16*)xh_f16;
-  a.M = M;
-  a.K = K;
-  return iq3_launch<1, EPI_F16>(a, tq + tk + tv, (hipStream_t)stream);
-}
-
-// k and v segments of the fused attention projections (IQ3_XXS packed rows), used by the Q6_K
-// q-branch entry point.  With launch == false only the arguments are validated.
-int tlx_iq3_kv(const void* wk, const void* wv, const float* gridf, const uint16_t* xh_f16,
-               uint16_t* krow_f16, uint16_t* vrow_f16, int M, int Nk, int Nv, int K, bool launch,
-               void* stream) {
-  int rc = iq3_check(wk, M, Nk, K, TLX_LAYOUT_PACKED);
-  if (rc == TLX_OK) rc = iq3_check(wv, M, Nv, K, TLX_LAYOUT_PACKED);
-  TLX_RET_IF(rc != TLX_OK, rc);
+// IQ3_XXS segments of the fused attention projections (tlx_attn.hip): up to three matrices
+// sharing the activations, one launch.  With launch == false only the arguments are checked.
+int tlx_iq3_segments(const void* const* w, uint16_t* const* out, const int* n, int nseg,
+                     const float* gridf, const uint16_t* xh_f16, int M, int K, int layout,
+                     bool launch, void* stream) {
+  TLX_RET_IF(nseg < 1 || nseg > 3, TLX_E_ARG);
+  for (int i = 0; i < nseg; ++i) {
+    const int rc = iq3_check(w[i], M, n[i], K, layout);
+    TLX_RET_IF(rc != TLX_OK, rc);
+  }
   TLX_RET_IF(!tlx_aligned(xh_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
   if (!launch) return TLX_OK;
   Iq3Launch a{};
-  const int tk = tiles_of(Nk), tv = tiles_of(Nv);
-  a.seg[0] = Iq3Seg{(const uint8_t*)wk, nullptr, krow_f16, nullptr, Nk, 0};
-  a.seg[1] = Iq3Seg{(const uint8_t*)wv, nullptr, vrow_f16, nullptr, Nv, tk};
-  a.nseg = 2;
+  int tiles = 0;
+  for (int i = 0; i < nseg; ++i) {
+    a.seg[i] = Iq3Seg{(const uint8_t*)w[i], nullptr, out[i], nullptr, n[i], tiles};
+    tiles += tiles_of(n[i]);
+  }
+  a.nseg = nseg;
   a.gridf = gridf;
   a.x = (const _Float16*)xh_f16;
   a.M = M;
   a.K = K;
-  return iq3_launch<1, EPI_F16>(a, tk + tv, (hipStream_t)stream);
+  a.raw = layout == TLX_LAYOUT_RAW;
+  return iq3_launch<1, EPI_F16>(a, tiles, (hipStream_t)stream);
 }

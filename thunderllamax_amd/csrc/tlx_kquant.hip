@@ -498,6 +498,14 @@ int k4_dequant(const void* w, void* out, int64_t rows, int64_t kdim, int out_f16
 
 }  // namespace
 
+int tlx_kq_gemv(int fmt, const void* w, const uint16_t* x_f16, uint16_t* out_f16, int M, int N,
+                int K, bool launch, void* stream) {
+  TLX_RET_IF(fmt < KF_Q6R || fmt > KF_Q5K, TLX_E_ARG);
+  const int rc = kq_check(fmt, w, x_f16, out_f16, M, N, K);
+  TLX_RET_IF(rc != TLX_OK || !launch, rc);
+  return kq_gemv16(fmt, w, x_f16, out_f16, M, N, K, (hipStream_t)stream);
+}
+
 extern "C" int tlx_q6k_gemv16(const void* w, const uint16_t* x_f16, uint16_t* out_f16, int M, int N,
                               int K, int layout, void* stream) {
   const int f = q6_fmt(layout);
@@ -524,23 +532,6 @@ extern "C" int tlx_q5k_gemv16(const void* w, const uint16_t* x_f16, uint16_t* ou
 extern "C" int tlx_head8(const void* wq5, const uint16_t* xh_f16, uint16_t* logits_f16, int M,
                          int vocab, int K, void* stream) {
   return tlx_q5k_gemv16(wq5, xh_f16, logits_f16, M, vocab, K, stream);
-}
-
-extern "C" int tlx_aq6k8(const void* wq, const void* wk, const void* wv, const float* gridf,
-                         const uint16_t* xh_f16, uint16_t* qrow_f16, uint16_t* krow_f16,
-                         uint16_t* vrow_f16, int M, int Nq, int Nk, int Nv, int K, int layout,
-                         void* stream) {
-  // q: Q6_K in the padded 212-B blocks (layout PACKED) or raw 210-B blocks; k and v: IQ3_XXS
-  // packed rows, through the IQ3 GEMV (two launches on the same stream).
-  const int f = q6_fmt(layout);
-  TLX_RET_IF(f < 0, TLX_E_ARG);
-  int rc = kq_check(f, wq, xh_f16, qrow_f16, M, Nq, K);
-  if (rc == TLX_OK)
-    rc = tlx_iq3_kv(wk, wv, gridf, xh_f16, krow_f16, vrow_f16, M, Nk, Nv, K, false, stream);
-  TLX_RET_IF(rc != TLX_OK, rc);
-  rc = tlx_iq3_kv(wk, wv, gridf, xh_f16, krow_f16, vrow_f16, M, Nk, Nv, K, true, stream);
-  TLX_RET_IF(rc != TLX_OK, rc);
-  return kq_gemv16(f, wq, xh_f16, qrow_f16, M, Nq, K, (hipStream_t)stream);
 }
 
 extern "C" int tlx_q4k_dequant(const void* w, void* out, int64_t rows, int64_t kdim, int out_f16,

@@ -8,7 +8,7 @@ allocated here.  Errors raise ``TlxError`` (the reference asserts in Python).
 """
 import torch
 
-from ._lib import LAYOUT_PACK7, LAYOUT_PACKED, LAYOUT_RAW, call
+from ._lib import LAYOUT_PACK7, LAYOUT_PACKED, LAYOUT_RAW, V_Q4K, call
 
 _F16 = torch.float16
 
@@ -115,17 +115,42 @@ def iq3_gemv(w, gridf, x, out, layout=LAYOUT_PACKED, stream=None):
     return out
 
 
-def aq3k8(wq, wk, wv, gridf, xh, qrow, krow, vrow, layout=LAYOUT_PACKED, stream=None):
-    """Fused q/k/v IQ3_XXS projections in one launch   (aq3k8 / aq3k8v{M})."""
+def _q4k_rows(n, k):
+    return n * 144 * (k // 256)
+
+
+def _attn(name, wq, wk, wv, gridf, xh, qrow, krow, vrow, qbytes, kbytes, vbytes, layout, stream):
     M, K = _mk(xh), xh.shape[-1]
-    for t, o, nm in ((wq, qrow, "wq"), (wk, krow, "wk"), (wv, vrow, "wv")):
-        _need(t, _iq3_rows(o.shape[-1], K), nm)
+    for t, o, nm, nbytes in ((wq, qrow, "wq", qbytes), (wk, krow, "wk", kbytes), (wv, vrow, "wv", vbytes)):
+        _need(t, nbytes(o.shape[-1], K), nm)
         _need(o, M * o.shape[-1] * 2, nm + " output")
     _need(gridf, 4096, "gridf")
     _dev(wq, wk, wv, gridf, xh, qrow, krow, vrow)
-    call("tlx_aq3k8", wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), gridf.data_ptr(), xh.data_ptr(),
-         qrow.data_ptr(), krow.data_ptr(), vrow.data_ptr(), M, qrow.shape[-1], krow.shape[-1],
-         vrow.shape[-1], K, layout, _stream(stream))
+    args = [wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), gridf.data_ptr(), xh.data_ptr(),
+            qrow.data_ptr(), krow.data_ptr(), vrow.data_ptr(), M, qrow.shape[-1], krow.shape[-1],
+            vrow.shape[-1], K]
+    if layout is not None:
+        args.append(layout)
+    call(name, *args, _stream(stream))
+
+
+def aq3k8(wq, wk, wv, gridf, xh, qrow, krow, vrow, layout=LAYOUT_PACKED, stream=None):
+    """Fused q/k/v projections (aq3k8 / aq3k8v{M}): q, k IQ3_XXS in ``layout`` (packed rows or
+    GGUF blocks); v IQ3_XXS too, or GGUF Q4_K when ``layout`` includes ``V_Q4K``."""
+    v = _q4k_rows if layout & V_Q4K else _iq3_rows
+    _attn("tlx_aq3k8", wq, wk, wv, gridf, xh, qrow, krow, vrow, _iq3_rows, _iq3_rows, v, layout, stream)
+
+
+def a_qkv_iq3(wq, wk, wv4, gridf, xh, qrow, krow, vrow, stream=None):
+    """Fused q/k/v projections on GGUF blocks (a_qkv_iq3): q, k IQ3_XXS, v Q4_K."""
+    _attn("tlx_a_qkv_iq3", wq, wk, wv4, gridf, xh, qrow, krow, vrow, _iq3_rows, _iq3_rows, _q4k_rows,
+          None, stream)
+
+
+def a_qkv_q6(wq, wk, wv4, gridf, xh, qrow, krow, vrow, stream=None):
+    """Fused q/k/v projections on GGUF blocks (a_qkv_q6): q Q6_K (210-B), k IQ3_XXS, v Q4_K."""
+    _attn("tlx_a_qkv_q6", wq, wk, wv4, gridf, xh, qrow, krow, vrow,
+          lambda n, k: _q6_rows(n, k, LAYOUT_RAW), _iq3_rows, _q4k_rows, None, stream)
 
 
 def h6k_gemv(w, x, y, layout=LAYOUT_RAW, stream=None):
@@ -197,18 +222,12 @@ def q5k_dequant(w, out, kdim, stream=None):
 
 def aq6k8(wq, wk, wv, gridf, xh, qrow, krow, vrow, layout=LAYOUT_PACKED, stream=None):
     """Fused attention projections with a Q6_K q (padded 212-B blocks for ``LAYOUT_PACKED``,
-    raw 210-B for ``LAYOUT_RAW``) and IQ3_XXS packed-row k and v."""
-    M, K = xh.shape
-    _need(wq, _q6_rows(qrow.shape[-1], K, layout), "wq")
-    _need(qrow, M * qrow.shape[-1] * 2, "wq output")
-    for t, o, nm in ((wk, krow, "wk"), (wv, vrow, "wv")):
-        _need(t, _iq3_rows(o.shape[-1], K), nm)
-        _need(o, M * o.shape[-1] * 2, nm + " output")
-    _need(gridf, 4096, "gridf")
-    _dev(wq, wk, wv, gridf, xh, qrow, krow, vrow)
-    call("tlx_aq6k8", wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), gridf.data_ptr(), xh.data_ptr(),
-         qrow.data_ptr(), krow.data_ptr(), vrow.data_ptr(), M, qrow.shape[-1], krow.shape[-1],
-         vrow.shape[-1], K, layout, _stream(stream))
+    raw 210-B for ``LAYOUT_RAW``), IQ3_XXS packed-row k, and v IQ3_XXS packed rows or (with
+    ``V_Q4K`` in ``layout``) GGUF Q4_K."""
+    base = layout & ~V_Q4K
+    v = _q4k_rows if layout & V_Q4K else _iq3_rows
+    _attn("tlx_aq6k8", wq, wk, wv, gridf, xh, qrow, krow, vrow,
+          lambda n, k: _q6_rows(n, k, base), _iq3_rows, v, layout, stream)
 
 
 # ------------------------------------------------------------------ prefill dequant-GEMMs
