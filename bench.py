@@ -19,6 +19,13 @@ an fp32 matmul) on a bounded sample of rows of the same workload, on this host's
 gate+up with SwiGLU (K=5120, N=2x17408) and down with the residual epilogue (K=17408,
 N=5120) -- in TFLOP/s (2*M*N*K per GEMM) and as a fraction of the dense fp16 MFMA peak.
 
+``sweep`` is config 3: one dense hybrid decode step at M=11 -- 48 gated-delta-net layers and 16
+attention layers (every fourth layer; Q6_K q on layers 3, 7, 19, 31, 43, 55, 59, 63) with their
+FFNs, then the Q6_K head -- as the sequence of GEMV launches a decode step makes (10.18 GB of
+weights, all resident, so every step streams them from HBM), captured once in a HIP graph and
+replayed.  Weights are seeded random bytes with sane d fields (the timing does not depend on the
+values; parity is the tests' business).  Reported as weight-streaming GB/s for the step.
+
 ``moe`` is config 5: the whole MoE layer (top-8 from N(0,1) logits, sort, grouped IQ4_XS
 gate+up and down, shared expert, combine) at M=11 and M=2048, seeded expert weights; at
 M=11 each step reads a different copy of the 257 expert slabs (3 copies, 1.3 GB), so the
@@ -46,6 +53,7 @@ def parse():
     ap.add_argument("--ms", default="1,4,8,11", help="activation widths to time")
     ap.add_argument("--gemm-m", type=int, default=2048, help="prefill rows for the GEMM leg (0: skip)")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE leg")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the decode-step sweep leg")
     return ap.parse_args()
 
 
@@ -165,6 +173,106 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
     return out
 
 
+def sweep_leg(ops, formats, torch, dev, steps, warmup):
+    """Config 3: the 64-layer dense decode step at M=11 plus the Q6_K head."""
+    from thunderllamax_amd._lib import LAYOUT_RAW
+    H, F, M = 5120, 17408, 11
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20261204)
+    dbits = 0x1419  # fp16 1.05e-3: a finite scale for every block
+
+    def iq3(rows, k):      # packed rows [qs 64NB][sw 32NB][d 2NB]
+        nb = k // 256
+        w = torch.randint(0, 256, (rows, 98 * nb), dtype=torch.uint8, device=dev, generator=gen)
+        w[:, 96 * nb:].view(torch.int16).fill_(dbits)
+        return w
+
+    def q6(rows, k):       # GGUF 210-B blocks, d at bytes 208..209
+        nb = k // 256
+        w = torch.randint(0, 256, (rows, nb, 210), dtype=torch.uint8, device=dev, generator=gen)
+        w[:, :, 208:210].view(torch.int16).fill_(dbits)
+        return w.view(rows, nb * 210)
+
+    gridf = formats.gridf_tensor(dev)
+    xs = {k: torch.randn(M, k, device=dev).half() for k in (H, 6144, F)}
+    o = {n: torch.empty(M, n, dtype=torch.float16, device=dev) for n in (10240, 6144, 48, 12288, 1024, H, F)}
+    vrow = torch.empty(M, 1024, dtype=torch.float16, device=dev)
+    hh = torch.randn(M, H, device=dev)
+    y = torch.empty(M, H, device=dev)
+    logits = torch.empty(M, 151936, dtype=torch.float16, device=dev)
+    q6_layers = {3, 7, 19, 31, 43, 55, 59, 63}
+    calls, nbytes = [], 0
+    kinds = {"gdn": [], "attn_iq3": [], "attn_q6": [], "head": []}
+    for layer in range(64):
+        c0 = len(calls)
+        if layer % 4 == 3:   # full attention
+            wk, wv, wo = iq3(1024, H), iq3(1024, H), iq3(H, 6144)
+            if layer in q6_layers:
+                wq = q6(12288, H)
+                calls.append(lambda s, wq=wq, wk=wk, wv=wv: ops.aq6k8(wq, wk, wv, gridf, xs[H], o[12288], o[1024], vrow, layout=LAYOUT_RAW, stream=s))
+                kind = "attn_q6"
+            else:
+                wq = iq3(12288, H)
+                calls.append(lambda s, wq=wq, wk=wk, wv=wv: ops.aq3k8(wq, wk, wv, gridf, xs[H], o[12288], o[1024], vrow, stream=s))
+                kind = "attn_iq3"
+            calls.append(lambda s, w=wo: ops.iq3_gemv(w, gridf, xs[6144], o[H], stream=s))
+            nbytes += wq.numel() + wk.numel() + wv.numel() + wo.numel()
+        else:                # gated delta net projections
+            ws = [(iq3(10240, H), H, 10240), (iq3(6144, H), H, 6144), (iq3(48, H), H, 48),
+                  (iq3(48, H), H, 48), (iq3(H, 6144), 6144, H)]
+            for w, k, n in ws:
+                calls.append(lambda s, w=w, k=k, n=n: ops.iq3_gemv(w, gridf, xs[k], o[n], stream=s))
+                nbytes += w.numel()
+            kind = "gdn"
+        wg, wu, wd = iq3(F, H), iq3(F, H), iq3(H, F)
+        calls.append(lambda s, wg=wg, wu=wu: ops.ffn8(wg, wu, gridf, xs[H], o[F], stream=s))
+        calls.append(lambda s, wd=wd: ops.down8(wd, gridf, xs[F], hh, y, stream=s))
+        nbytes += wg.numel() + wu.numel() + wd.numel()
+        kinds[kind].append((c0, len(calls)))
+    wh = q6(151936, H)
+    c0 = len(calls)
+    calls.append(lambda s: ops.q6k_gemv16(wh, xs[H], logits, LAYOUT_RAW, stream=s))
+    kinds["head"].append((c0, len(calls)))
+    nbytes += wh.numel()
+
+    def graph_ms(lo, hi, reps, warm):
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            for c in calls[lo:hi]:
+                c(st)          # eager first: one-time kernel attributes are set outside capture
+        torch.cuda.current_stream().wait_stream(st)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            for c in calls[lo:hi]:
+                c(st)
+        for _ in range(warm):
+            g.replay()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            g.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / reps
+
+    t_step = graph_ms(0, len(calls), steps, warmup)
+    per_kind = {}
+    for kind, spans in kinds.items():   # one layer of each kind, replayed
+        lo, hi = spans[0]
+        t = graph_ms(lo, hi, max(5, steps), 2)
+        per_kind[kind] = {"layers": len(spans), "ms_per_layer": round(t, 4)}
+    gbs = nbytes / (t_step * 1e-3) / 1e9
+    return {"workload": "dense hybrid decode step, M=11: 48 GDN + 16 attention layers (8 with a Q6_K q), "
+                        "FFN 17408, Q6_K head 151936x5120",
+            "M": M, "launches": len(calls), "weight_bytes": nbytes, "ms": round(t_step, 4),
+            "weight_gbs": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+            "per_layer_kind": per_kind}
+
+
 def cpu_baseline(N, K, M, seconds=10.0):
     """numpy restatement of the reference path on a sample of rows, scaled to GB/s."""
     from oracle import quants
@@ -260,6 +368,8 @@ def main():
     if args.gemm_m > 0:
         out["gemm"] = gemm_leg(ops, formats, synth, torch, dev, args.gemm_m, max(3, args.steps // 5),
                                max(1, args.warmup // 5))
+    if not args.no_sweep:
+        out["sweep"] = sweep_leg(ops, formats, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5))
     if not args.no_moe:
         out["moe"] = moe_leg(ops, formats, synth, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5))
     if not args.no_cpu:

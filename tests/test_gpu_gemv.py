@@ -136,30 +136,32 @@ def test_iq3_gemv_ragged_rows(gpu):
     assert view.numel() > 0 and torch.all(out[:, N:] == -7.0)
 
 
+@pytest.mark.parametrize("M", [3, 9])
 @pytest.mark.parametrize("N,K", [(48, 5120), (640, 512), (40, 1024), (9600, 1024)])
-def test_iq3_gemv_work_splits(gpu, N, K):
+def test_iq3_gemv_work_splits(gpu, N, K, M):
     """Tiles split across waves (48x5120), waves without items (640x512, 40x1024) and several
     tiles per workgroup (9600x1024)."""
-    print(f"[case] iq3_gemv split N={N} K={K}", flush=True)
+    print(f"[case] iq3_gemv split N={N} K={K} M={M}", flush=True)
     rng = np.random.default_rng(N + K)
     p, w = _iq3(rng, N, K, gpu)
-    x = synth.activations_f16(rng, 5, K)
-    out = torch.empty(5, N, dtype=torch.float16, device=gpu)
+    x = synth.activations_f16(rng, M, K)
+    out = torch.empty(M, N, dtype=torch.float16, device=gpu)
     ops.iq3_gemv(w, formats.gridf_tensor(gpu), torch.from_numpy(x).to(gpu), out)
     torch.cuda.synchronize()
     _, ref = gemv.gemv16_ref(quants.dequant_iq3xxs_packed(p, K), x)
     assert _rows_err(out.cpu().numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("N,K", [(40, 5120), (24, 1024)])
-def test_ffn8_work_splits(gpu, N, K):
-    """Gate/up tiles split across waves: both matrices' partial sums are combined."""
-    print(f"[case] ffn8 split N={N} K={K}", flush=True)
+@pytest.mark.parametrize("M", [3, 9])
+@pytest.mark.parametrize("N,K", [(40, 5120), (24, 1024), (200, 512)])
+def test_ffn8_work_splits(gpu, N, K, M):
+    """Gate/up pairs over several block ranges and a ragged row count (200)."""
+    print(f"[case] ffn8 split N={N} K={K} M={M}", flush=True)
     rng = np.random.default_rng(7 * N + K)
     pg, wg = _iq3(rng, N, K, gpu)
     pu, wu = _iq3(rng, N, K, gpu)
-    x = synth.activations_f16(rng, 3, K)
-    gact = torch.empty(3, N, dtype=torch.float16, device=gpu)
+    x = synth.activations_f16(rng, M, K)
+    gact = torch.empty(M, N, dtype=torch.float16, device=gpu)
     ops.ffn8(wg, wu, formats.gridf_tensor(gpu), torch.from_numpy(x).to(gpu), gact)
     torch.cuda.synchronize()
     Wg, Wu = quants.dequant_iq3xxs_packed(pg, K), quants.dequant_iq3xxs_packed(pu, K)

@@ -220,6 +220,7 @@ int iq3_launch(const Iq3Launch& a, int tiles, hipStream_t st) {
 }
 
 
+
 int iq3_check(const void* w, int M, int N, int K, int layout) {
   if (M < 1 || M > TLX_MAX_M || N < 1 || K < 256 || (K & 255)) return TLX_E_ARG;
   if (layout != TLX_LAYOUT_PACKED && layout != TLX_LAYOUT_RAW) return TLX_E_ARG;

@@ -257,20 +257,37 @@ __global__ __launch_bounds__(kWaves * TLX_WAVE) void kq_gemv16_kernel(const KqAr
   const int r = lane >> 2, c = lane & 3;      // load role: row r, 16-B piece c of each 64 B
   const int col = lane & 15, kq = lane >> 4;  // MFMA role
   const uint32_t rowb = (uint32_t)G.bs * nb;
-  auto blk_of = [&](int i) -> uint32_t {
-    const int t = t0 + i / nb, b = i - (i / nb) * nb;
-    const int n = min(16 * t + r, N - 1);  // tail tile: clamp the loads, mask the stores
-    return (uint32_t)n * rowb + (uint32_t)b * G.bs;
-  };
-
   // Every load, staging write and fragment read below is unconditional (item indices are
   // clamped to the wave's last item), so the loop body is straight-line and the compiler's
-  // wait counts stay exact.
+  // wait counts stay exact.  The load cursor (the next item to load, as a block offset that
+  // steps by one block and jumps to the next tile's rows) stops at the last item, whose loads
+  // then repeat.
   const int last = hi - 1;
+  uint32_t loff = 0;
+  int lb = 0, lt = 0, lleft = 0;
+  auto tile_off = [&](int t) {  // tail tile: clamp the loads, mask the stores
+    return (uint32_t)min(16 * t + r, N - 1) * rowb;
+  };
+  auto load_next = [&](KLd& L) {
+    k_load<F>(L, a.w, loff, c);
+    if (lleft > 0) {
+      --lleft;
+      if (++lb == nb) {
+        lb = 0;
+        loff = tile_off(++lt);
+      } else {
+        loff += G.bs;
+      }
+    }
+  };
   KLd g[kPrefetch];  // ring: item i sits in g[(i - lo) % kPrefetch] until it is staged
   if (lo < hi) {
+    lt = t0 + lo / nb;
+    lb = lo - (lo / nb) * nb;
+    lleft = last - lo;
+    loff = tile_off(lt) + (uint32_t)lb * G.bs;
 #pragma unroll
-    for (int p = 0; p < kPrefetch; ++p) k_load<F>(g[p], a.w, blk_of(min(lo + p, last)), c);
+    for (int p = 0; p < kPrefetch; ++p) load_next(g[p]);
   }
 
   // activations: 1-KB LDS-DMA pieces (row m, halves [512j, 512j + 512)), in flight together
@@ -323,15 +340,14 @@ __global__ __launch_bounds__(kWaves * TLX_WAVE) void kq_gemv16_kernel(const KqAr
   if (lo < hi) {
     k_stage<F>(stg, g[0], r, c);
     k_frag<F>(R[0], stg, col, kq);
-    k_load<F>(g[0], a.w, blk_of(min(lo + kPrefetch, last)), c);
+    load_next(g[0]);
   }
   int seg = lo;
+  int tl = lo / nb, b = lo - (lo / nb) * nb;  // compute cursor (tile local to the workgroup)
   for (int i0 = lo; i0 < hi; i0 += kPrefetch) {
 #pragma unroll
     for (int p = 0; p < kPrefetch; ++p) {
       const int i = i0 + p;  // i >= hi: padding steps of the last round, computed and discarded
-      const int ic = min(i, last);
-      const int tl = ic / nb, b = ic - tl * nb;
       h8_t A[8];
 #pragma unroll
       for (int o = 0; o < 8; ++o)
@@ -349,7 +365,7 @@ __global__ __launch_bounds__(kWaves * TLX_WAVE) void kq_gemv16_kernel(const KqAr
       f4_t D;
       if constexpr (is_q6(F)) D = q6_block(R[p & 1], A, kq);
       else D = k4_block<F>(R[p & 1], A, S, kq);
-      k_load<F>(g[(p + 1) % kPrefetch], a.w, blk_of(min(i + 1 + kPrefetch, last)), c);
+      load_next(g[(p + 1) % kPrefetch]);
       if (i < hi) {
         acc += D;
         if (b == nb - 1 || i == hi - 1) {  // end of a tile segment
@@ -358,6 +374,10 @@ __global__ __launch_bounds__(kWaves * TLX_WAVE) void kq_gemv16_kernel(const KqAr
           else accLast = acc;
           acc = f4_t{0.f, 0.f, 0.f, 0.f};
           seg = i + 1;
+        }
+        if (i + 1 < hi && ++b == nb) {
+          b = 0;
+          ++tl;
         }
       }
     }
