@@ -6,7 +6,12 @@
  *     hipStream_t passed as void*, NULL = the default stream);
  *   - keeps the reference kernel's positional argument order, then appends the sizes the
  *     reference bakes into kernel names / #defines (M, N, K) and a layout flag;
- *   - is asynchronous on `stream`, never allocates, never aborts;
+ *   - is asynchronous on `stream` and never aborts;
+ *   - allocates nothing per call.  The IQ3_XXS decode GEMVs (ffn8, down8, iq3_gemv and the
+ *     IQ3_XXS segments of the attention projections) with M >= 6 first write a tile-ordered
+ *     copy of the activations (K * 32 bytes) into a 4 MB workspace per device that the library
+ *     allocates on the first such call (make that call outside stream capture); two such
+ *     calls must not run concurrently on one device (order them on one stream);
  *   - returns TLX_OK, a negative TLX_E_* code for a rejected argument (nothing launched),
  *     or a positive hipError_t from the launch.
  *
@@ -25,6 +30,7 @@ extern "C" {
 #define TLX_E_ARG (-1)     /* size / M / layout out of range */
 #define TLX_E_ALIGN (-2)   /* a pointer or row stride is not aligned as the layout needs */
 #define TLX_E_NODEV (-3)   /* no usable gfx950 device */
+#define TLX_E_NOMEM (-4)   /* the library workspace could not be allocated */
 
 /* Weight layouts (row-major over output rows). */
 #define TLX_LAYOUT_RAW 0     /* GGUF blocks as stored in the file */

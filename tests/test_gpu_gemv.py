@@ -85,7 +85,7 @@ def test_ffn8_rows_invariant_and_deterministic(gpu):
     assert torch.equal(full.view(torch.int16), again.view(torch.int16))
 
 
-@pytest.mark.parametrize("M", [1, 11])
+@pytest.mark.parametrize("M", [1, 11, 16])
 def test_down8_parity(gpu, M):
     print(f"[case] down8 M={M} N=256 K=17408", flush=True)
     rng = np.random.default_rng(40 + M)
@@ -150,6 +150,33 @@ def test_iq3_gemv_work_splits(gpu, N, K, M):
     torch.cuda.synchronize()
     _, ref = gemv.gemv16_ref(quants.dequant_iq3xxs_packed(p, K), x)
     assert _rows_err(out.cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("N,K", [(5120, 17408), (16, 17408), (1000, 6144), (17408, 5120)])
+def test_rows_invariant_across_activation_paths(gpu, N, K):
+    """From M=6 on the activations are read from a tile-ordered copy in the library workspace,
+    below that straight from x: row r of an M=11 call equals an M=1 call bit for bit, and the
+    same call after a call of another shape (which rewrites the workspace) reproduces the first
+    bit for bit.  Sampled rows are checked against the oracle."""
+    print(f"[case] iq3_gemv activation-path invariance N={N} K={K}", flush=True)
+    rng = np.random.default_rng(N + 3 * K)
+    p, w = _iq3(rng, N, K, gpu)
+    x = torch.from_numpy(synth.activations_f16(rng, 11, K)).to(gpu)
+    g = formats.gridf_tensor(gpu)
+    full = torch.empty(11, N, dtype=torch.float16, device=gpu)
+    ops.iq3_gemv(w, g, x, full)
+    small = torch.empty(11, 48, dtype=torch.float16, device=gpu)
+    ops.iq3_gemv(w[:48] if N >= 48 else torch.cat([w] * 3), g, x, small)
+    again = torch.empty_like(full)
+    ops.iq3_gemv(w, g, x, again)
+    one = torch.empty(1, N, dtype=torch.float16, device=gpu)
+    for r in (0, 5, 10):
+        ops.iq3_gemv(w, g, x[r:r + 1].contiguous(), one)
+        assert torch.equal(one[0].view(torch.int16), full[r].view(torch.int16)), r
+    assert torch.equal(full.view(torch.int16), again.view(torch.int16))
+    rows = np.sort(np.random.default_rng(N).choice(N, min(N, 64), replace=False))
+    _, ref = gemv.gemv16_ref(quants.dequant_iq3xxs_packed(p[rows], K), x.cpu().numpy())
+    assert _rows_err(full.cpu().numpy()[:, rows], ref) <= TOL
 
 
 @pytest.mark.parametrize("M", [3, 9])

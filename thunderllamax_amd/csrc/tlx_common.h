@@ -77,6 +77,14 @@ static inline int tlx_cu_count() {
   return cache[dev];
 }
 
+// ---------------------------------------------------------------- workspace
+// Device memory the library holds per device (tlx_core.hip): scratch for the tile-ordered
+// activation copy of the IQ3_XXS decode GEMVs.  Allocated on the first call that needs it on a
+// device and kept until the process ends; calls that overlap in time on one device must not
+// both use it.
+constexpr size_t kWsBytes = size_t(4) << 20;
+int tlx_workspace(void** ws);
+
 // Internal entry points shared by the fused attention projections (tlx_attn.hip).  With
 // launch == false they validate the arguments only.
 //   IQ3_XXS: up to three matrices (packed rows or GGUF blocks) sharing the activations, one

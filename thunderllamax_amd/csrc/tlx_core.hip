@@ -1,5 +1,7 @@
-// Library-level entry points: version and error strings.
+// Library-level entry points (version, error strings) and the per-device workspace.
 #include "tlx_common.h"
+
+#include <mutex>
 
 extern "C" int tlx_version(void) { return 1; }
 
@@ -9,6 +11,22 @@ extern "C" const char* tlx_strerror(int code) {
     case TLX_E_ARG: return "argument out of range (M, sizes or layout)";
     case TLX_E_ALIGN: return "pointer or row stride misaligned for this layout";
     case TLX_E_NODEV: return "no usable gfx950 device";
+    case TLX_E_NOMEM: return "the library workspace could not be allocated";
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown tlx error";
   }
+}
+
+// One workspace of kWsBytes per device, allocated on the first call that needs it.
+int tlx_workspace(void** ws) {
+  static std::mutex mu;
+  static void* cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return TLX_E_NODEV;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[dev] == nullptr && hipMalloc(&cache[dev], kWsBytes) != hipSuccess) {
+    cache[dev] = nullptr;
+    return TLX_E_NOMEM;
+  }
+  *ws = cache[dev];
+  return TLX_OK;
 }

@@ -27,6 +27,7 @@ namespace {
 constexpr int kIq3BlockBytes = 98;
 constexpr int kTblEntries = 4096;
 constexpr int kTile = 16;
+constexpr int kXtMinM = 6;  // from this M on, activations are read from the tile-ordered copy
 
 enum Epi { EPI_F16 = 0, EPI_SWIGLU = 1, EPI_RESID = 2 };
 
@@ -74,7 +75,8 @@ struct Iq3Launch {
   Iq3Seg seg[3];
   int nseg;
   const float* gridf;
-  const _Float16* x;   // [M][K]
+  const _Float16* x;   // activations [M][K], or (xt) the tile-ordered copy [K/8][16][8]
+  int xt;
   int M, K;
   int raw;             // GGUF blocks [d][qs 64][sw 32] (1) or packed rows [qs][sw][d] (0)
 };
@@ -129,8 +131,11 @@ __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Lau
   if constexpr (NMAT == 2) base[1] = sg.w1;
 
   // Activation rows >= M only reach output rows that are never stored, so those lanes load a
-  // valid row instead of being masked: no branches, and the wait counters stay exact.
-  const _Float16* xr = a.x + (size_t)min(col, M - 1) * K + 64 * kq;
+  // valid row instead of being masked: no branches, and the wait counters stay exact.  From the
+  // tile-ordered copy (M >= kXtMinM) the 4 lanes of a quad read 64 contiguous bytes.
+  const _Float16* xr = a.xt ? a.x + (size_t)(1024 * kq + 8 * col)
+                            : a.x + (size_t)min(col, M - 1) * K + 64 * kq;
+  const int xbs = a.xt ? 4096 : 256, xcs = a.xt ? 128 : 8;  // halves per block / per chunk
 
   f4_t acc[NMAT];
 #pragma unroll
@@ -144,7 +149,7 @@ __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Lau
     // activations leaves the weight prefetch in flight
     h8_t X[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) X[t] = *reinterpret_cast<const h8_t*>(xr + 256 * b + 8 * t);
+    for (int t = 0; t < 8; ++t) X[t] = *reinterpret_cast<const h8_t*>(xr + xbs * b + xcs * t);
     Iq3Regs<NMAT> nxt;
     const bool more = b + WAVES < nb;
     if (more) iq3_load<NMAT>(nxt, base, qoff, soff, doff, qst, sst, dst, b + WAVES);
@@ -206,9 +211,32 @@ __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Lau
   }
 }
 
+// The tile-ordered activation copy: xt[kc][col][0..7] = x[min(col, M - 1)][8kc .. 8kc + 7].
+__global__ __launch_bounds__(256) void iq3_xt_kernel(const _Float16* __restrict__ x,
+                                                     _Float16* __restrict__ xt, int M, int K) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);  // (kc, col)
+  if (i >= (K >> 3) * 16) return;
+  const int kc = i >> 4, col = i & 15;
+  *reinterpret_cast<u4_t*>(xt + (size_t)i * 8) =
+      *reinterpret_cast<const u4_t*>(x + (size_t)min(col, M - 1) * K + 8 * kc);
+}
+
 template <int NMAT, int EPI>
-int iq3_launch(const Iq3Launch& a, int tiles, hipStream_t st) {
+int iq3_launch(Iq3Launch& a, int tiles, hipStream_t st) {
   const int nb = a.K >> 8;
+  a.xt = 0;
+  // same values, same arithmetic: only the activation loads change (larger K reads x directly)
+  if (a.M >= kXtMinM && (size_t)a.K * 16 * 2 <= kWsBytes) {
+    void* ws = nullptr;
+    const int rc = tlx_workspace(&ws);
+    if (rc != TLX_OK) return rc;
+    _Float16* xt = reinterpret_cast<_Float16*>(ws);
+    iq3_xt_kernel<<<(a.K / 8 * 16 + 255) / 256, 256, 0, st>>>(a.x, xt, a.M, a.K);
+    const int lrc = tlx_launch_status();
+    if (lrc != TLX_OK) return lrc;
+    a.x = xt;
+    a.xt = 1;
+  }
   int waves = 4;
   while (tiles * waves < 4096 && waves < 16 && nb >= 4 * waves) waves *= 2;
   switch (waves) {
