@@ -9,8 +9,10 @@ reported under ``per_m``.  A "step" is one ffn8 call over one batch of M activat
 Timing: weights are synthetic (seeded) and resident in HBM before timing starts; each step
 reads a different copy out of a rotation larger than the 256 MB Infinity Cache, so the
 figure is HBM bandwidth, not cache bandwidth.  W untimed warmup steps, then exactly K
-timed steps bracketed by device synchronization, timed with HIP events recorded on the
-stream the kernels are launched on.
+timed steps -- captured in one HIP graph, as a decode step replays its launches -- bracketed
+by device synchronization, timed with HIP events recorded on the stream the graph replays on
+(the current stream).
+From M=6 on a step is two launches (the tile-ordered activation copy, then the GEMV).
 
 ``cpu_baseline`` times the numpy restatement of the reference's CPU path (dequantize, then
 an fp32 matmul) on a bounded sample of rows of the same workload, on this host's cores.
@@ -40,6 +42,12 @@ import time
 import numpy as np
 
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per M=11 step (tile-ordered activation copy + ffn8), measured with two
+# `rocprofv3 --pmc` passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --ms 11 --steps 10 --warmup 2
+# --gemm-m 0 --no-sweep --no-moe --no-cpu --copy-mib 256`; the 256 MiB copy at the end reads
+# FETCH_SIZE = 131,089 KiB and WRITE_SIZE = 262,144 KiB, so fetches are scaled by 2.0, writes
+# by 1.0.  Re-measure when the kernel changes.
+FFN8_M11_TRAFFIC_BYTES = 75_608_191
 PEAK_F16_TFLOPS = 2500.0
 ROT_BYTES = 300 * 2**20
 
@@ -54,23 +62,37 @@ def parse():
     ap.add_argument("--gemm-m", type=int, default=2048, help="prefill rows for the GEMM leg (0: skip)")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the decode-step sweep leg")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="end with one device-to-device copy of this many MiB (a reference "
+                         "dispatch of known size for calibrating memory counters)")
     return ap.parse_args()
 
 
 def time_ffn(ops, wsets, gridf, x, gact, steps, warmup, torch):
+    """Average ms per ffn8 call over `steps` calls captured in one HIP graph (host launch gaps
+    excluded: a decode step replays its launches as a graph), after `warmup` eager calls and
+    one untimed replay; HIP events on the replay stream."""
     n = len(wsets)
-    for i in range(warmup):
-        wg, wu = wsets[i % n]
-        ops.ffn8(wg, wu, gridf, x, gact)
-    stream = torch.cuda.current_stream()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        for i in range(max(warmup, 1)):   # eager: one-time set-up happens outside the capture
+            wg, wu = wsets[i % n]
+            ops.ffn8(wg, wu, gridf, x, gact, stream=st)
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        for i in range(steps):
+            wg, wu = wsets[i % n]
+            ops.ffn8(wg, wu, gridf, x, gact, stream=st)
+    g.replay()   # replays on the current stream
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for i in range(steps):
-        wg, wu = wsets[i % n]
-        ops.ffn8(wg, wu, gridf, x, gact, stream=stream)
-    t1.record(stream)
+    t0.record()
+    g.replay()
+    t1.record()
     torch.cuda.synchronize()
     return t0.elapsed_time(t1) / steps
 
@@ -363,7 +385,10 @@ def main():
                    "rotation_copies": ncopy, "parallelism": "single GPU"},
         "per_m": per_m,
         "roofline": {"bound": "hbm", "achieved": value, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(value / PEAK_HBM_GBS, 4), "traffic": None},
+                     "frac": round(value / PEAK_HBM_GBS, 4),
+                     "traffic": FFN8_M11_TRAFFIC_BYTES if head == "11" else None,
+                     "algorithmic_bytes": wbytes + int(head) * K * 2 + int(head) * N * 2,
+                     "kernel": "iq3_gemv_kernel<2,1,4> (+ iq3_xt_kernel for M >= 6)"},
     }
     if args.gemm_m > 0:
         out["gemm"] = gemm_leg(ops, formats, synth, torch, dev, args.gemm_m, max(3, args.steps // 5),
@@ -374,6 +399,11 @@ def main():
         out["moe"] = moe_leg(ops, formats, synth, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(N, K, int(head))
+    if args.copy_mib > 0:
+        src = torch.ones(args.copy_mib * 2**18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
     print(json.dumps(out), flush=True)
 
 

@@ -454,11 +454,11 @@ extern "C" int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const fl
   TLX_RET_IF(P < 1, TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(xs, 16) || !tlx_aligned(act, 16), TLX_E_ALIGN);
   const int chunks = (P + kTok - 1) / kTok;
-  moe_gemm_kernel<MOE_UP_DENSE><<<dim3(chunks, MoeShape<MOE_UP>::STRIPES), 256, 0, (hipStream_t)stream>>>(
+  moe_gemm_kernel<MOE_UP_DENSE><<<dim3(chunks, MoeShape<MOE_UP_DENSE>::STRIPES), 256, 0, (hipStream_t)stream>>>(
       ptbl_sh, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, act, P);
   int rc = tlx_launch_status();
   TLX_RET_IF(rc != TLX_OK, rc);
-  moe_gemm_kernel<MOE_DN_DENSE><<<dim3(chunks, MoeShape<MOE_DN>::STRIPES), 256, 0, (hipStream_t)stream>>>(
+  moe_gemm_kernel<MOE_DN_DENSE><<<dim3(chunks, MoeShape<MOE_DN_DENSE>::STRIPES), 256, 0, (hipStream_t)stream>>>(
       ptbl_sh + 1, nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
   return tlx_launch_status();
 }
