@@ -29,9 +29,9 @@ replayed.  Weights are seeded random bytes with sane d fields (the timing does n
 values; parity is the tests' business).  Reported as weight-streaming GB/s for the step.
 
 ``moe`` is config 5: the whole MoE layer (top-8 from N(0,1) logits, sort, grouped IQ4_XS
-gate+up and down, shared expert, combine) at M=11 and M=2048, seeded expert weights; at
-M=11 each step reads a different copy of the 257 expert slabs (3 copies, 1.3 GB), so the
-weights come from HBM.
+gate+up and down, shared expert, combine) at M=11 and M=2048, seeded expert weights, the
+layer's six launches per step captured in one HIP graph; each step reads a different copy of
+the 257 expert slabs (3 copies, 1.3 GB), so at M=11 the weights come from HBM.
 """
 import argparse
 import json
@@ -113,6 +113,31 @@ def time_call(fn, steps, warmup, torch):
     return t0.elapsed_time(t1) / steps
 
 
+def time_graph(fn, steps, warmup, torch):
+    """Average ms of fn(stream) over `steps` calls captured in one HIP graph (each call may pick
+    different buffers, e.g. rotated weights), after `warmup` eager calls and one untimed replay."""
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        for _ in range(max(warmup, 1)):
+            fn(st)
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        for _ in range(steps):
+            fn(st)
+    g.replay()   # replays on the current stream
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
 def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup):
     """Config 4: IQ3_XXS FFN prefill GEMMs at M rows, synthetic seeded weights."""
     rng = synth.config_rng(4)
@@ -186,7 +211,7 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
             ops.moe_shared(c["ptbl_sh"], x, iq4nl, sact, shared, stream=st)
             ops.moe_combine(parts, gates, sg, shared, hres, y, stream=st)
 
-        t = time_call(layer, steps, warmup, torch)
+        t = time_graph(layer, steps, warmup, torch)
         hit = int((torch.diff(eoff) > 0).sum().item())
         flops = 2.0 * 3 * F * H * (8 * P + P)
         wbytes = (hit + 1) * 1671168

@@ -215,6 +215,8 @@ struct __attribute__((aligned(16))) MoeLds {
   int orow[kTok];                // output row of token slot t
 };
 
+__device__ __forceinline__ h8_t splat8h(_Float16 v) { return h8_t{v, v, v, v, v, v, v, v}; }
+
 __device__ __forceinline__ int moe_frag(int R, int p) { return ((R >> 4) * 64 + p * 16 + (R & 15)) * 8; }
 
 // raw global data of one 32-k step for one thread (registers, prefetched two steps ahead)
@@ -379,6 +381,185 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const uint64_t* __restric
   }
 }
 
+// ------------------------------------------------------------------ grouped IQ4_XS GEMV
+// The small-batch (decode / verify) form of the same products.  With a few tokens per expert the
+// step-synchronous GEMM above waits on memory once per 32-k step; here a workgroup owns one
+// 16-row output tile (FFN: 16 gate + the matching 16 up rows; down: two tiles) of one work item,
+// its waves split the tile's K blocks, every wave issues all of its loads at once, and the waves
+// reduce through LDS in a fixed order.
+//   * lane (col, kq) of a wave holds weight row col's sub-blocks 2kq and 2kq + 1 of each of its
+//     blocks (32 quant bytes) and the block header; a sub-block's 4-byte chunk c gives the 8
+//     weights j = 4c..4c+3 (low nibbles) and 16 + 4c.. (high nibbles), decoded by 4 lookups of
+//     the byte -> (kv[lo], kv[hi]) fp16 table and scaled by fp16(d * (ls - 32)) -- the same
+//     operand values as the GEMM -- then one v_mfma_f32_16x16x32_f16 per chunk and 16-token group;
+//   * the A operand is the matching activations, interleaved the same way, in groups of 16 of the
+//     item's tokens (rows past the item repeat its last token and are never stored).
+constexpr int kGvGroups = kTok / 16;
+
+// waves per 16-row tile: the FFN tile (2 x 8 blocks per row) is split over 2 waves, a down tile
+// (2 blocks per row) is one wave's
+template <int KIND>
+constexpr int moe_gv_wpt() { return (KIND == MOE_UP || KIND == MOE_UP_DENSE) ? 2 : 1; }
+
+template <int KIND>
+__global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff,
+                                                     const uint16_t* __restrict__ plist,
+                                                     const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp,
+                                                     const float* __restrict__ xs, const float* __restrict__ iq4nl,
+                                                     void* __restrict__ out, int P) {
+  using S = MoeShape<KIND>;
+  constexpr bool kDense = KIND == MOE_DN_DENSE || KIND == MOE_UP_DENSE;
+  constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
+  constexpr int NMAT = kUp ? 2 : 1;
+  constexpr int kNb = S::K / 256;                 // IQ4_XS blocks per row
+  constexpr int kWpt = moe_gv_wpt<KIND>();        // waves per tile
+  constexpr int kBpw = kNb / kWpt;                // blocks per wave
+  constexpr int kTpw = 4 / kWpt;                  // tiles per workgroup
+  constexpr int kRowBytes = kNb * 136;
+  __shared__ uint32_t lut[256];
+  __shared__ int xrow[kTok], orow[kTok];
+  __shared__ f4_t red[4][kGvGroups][NMAT][64];
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int col = lane & 15, kq = lane >> 4;
+
+  using gbyte = const __attribute__((address_space(1))) uint8_t;
+  int m0, ntok;
+  gbyte* base;
+  if constexpr (kDense) {
+    m0 = (int)blockIdx.x * kTok;
+    ntok = min(kTok, P - m0);
+    base = (gbyte*)(ptbl[0]);
+  } else {
+    if (blockIdx.x >= *nitp) return;
+    const uint32_t it = items[blockIdx.x];
+    const int e = (int)(it >> 16);
+    m0 = (int)(it & 0xFFFFu);
+    const int eb0 = eoff[e];
+    ntok = min(kTok, eoff[e + 1] - eb0 - m0);
+    m0 += eb0;
+    base = (gbyte*)(ptbl[e]);
+  }
+  if (t < kTok) {
+    const int slot = min(t, ntok - 1);
+    if constexpr (kDense) {
+      xrow[t] = m0 + slot;
+      orow[t] = m0 + slot;
+    } else {
+      const int pair = plist[m0 + slot];
+      xrow[t] = kUp ? (pair >> 3) : pair;
+      orow[t] = pair;
+    }
+  }
+  {
+    const _Float16 lo = (_Float16)iq4nl[t & 15], hi = (_Float16)iq4nl[t >> 4];
+    lut[t] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+  }
+  __syncthreads();
+  const int ngroups = (ntok + 15) >> 4;
+
+  const int tile = (int)blockIdx.y * kTpw + wave / kWpt;   // 16-row output tile
+  const int kb0 = (wave % kWpt) * kBpw;
+  gbyte* wrow[NMAT];
+  wrow[0] = base + (size_t)(16 * tile + col) * kRowBytes;
+  if constexpr (NMAT == 2) wrow[1] = wrow[0] + kGateBytes;
+
+  // all of the wave's weight loads first
+  u2_t hdr[kBpw][NMAT];
+  u4_t qv[kBpw][NMAT][2];
+#pragma unroll
+  for (int bb = 0; bb < kBpw; ++bb)
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi) {
+      gbyte* blk = wrow[mi] + 136 * (kb0 + bb);
+      hdr[bb][mi] = *(const __attribute__((address_space(1))) u2_t*)(blk);
+      qv[bb][mi][0] = *(const __attribute__((address_space(1))) u4_t*)(blk + 8 + 32 * kq);
+      qv[bb][mi][1] = *(const __attribute__((address_space(1))) u4_t*)(blk + 24 + 32 * kq);
+    }
+
+  f4_t acc[kGvGroups][NMAT];
+#pragma unroll
+  for (int g = 0; g < kGvGroups; ++g)
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi) acc[g][mi] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int bb = 0; bb < kBpw; ++bb) {
+    const int kbase = 256 * (kb0 + bb) + 64 * kq;   // the lane's sub-blocks 2kq, 2kq + 1
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const int ib = 2 * kq + sb;
+      _Float16 dh[NMAT];
+#pragma unroll
+      for (int mi = 0; mi < NMAT; ++mi) {
+        const uint32_t sh = hdr[bb][mi].x >> 16;
+        const uint32_t ls = ((hdr[bb][mi].y >> (4 * ib)) & 0xFu) | (((sh >> (2 * ib)) & 3u) << 4);
+        dh[mi] = (_Float16)(tlx_h2f((uint16_t)hdr[bb][mi].x) * (float)((int)ls - 32));
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        h8_t B[NMAT];
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi) {
+          const uint32_t qw = qv[bb][mi][sb][c];
+          const u4_t w4 = {lut[qw & 0xFF], lut[(qw >> 8) & 0xFF], lut[(qw >> 16) & 0xFF], lut[qw >> 24]};
+          B[mi] = __builtin_bit_cast(h8_t, w4) * splat8h(dh[mi]);
+        }
+        const int k0 = kbase + 32 * sb + 4 * c;
+#pragma unroll
+        for (int g = 0; g < kGvGroups; ++g) {
+          if (g < ngroups) {
+            const float* xr = xs + (size_t)xrow[16 * g + col] * S::K + k0;
+            const float4 x0 = *reinterpret_cast<const float4*>(xr);
+            const float4 x1 = *reinterpret_cast<const float4*>(xr + 16);
+            const h8_t A = {(_Float16)x0.x, (_Float16)x1.x, (_Float16)x0.y, (_Float16)x1.y,
+                            (_Float16)x0.z, (_Float16)x1.z, (_Float16)x0.w, (_Float16)x1.w};
+#pragma unroll
+            for (int mi = 0; mi < NMAT; ++mi)
+              acc[g][mi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[mi], acc[g][mi], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+  // fixed-order reduction over the waves of a tile
+  if constexpr (kWpt > 1) {
+    if (wave % kWpt != 0) {
+#pragma unroll
+      for (int g = 0; g < kGvGroups; ++g)
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi) red[wave][g][mi][lane] = acc[g][mi];
+    }
+    __syncthreads();
+    if (wave % kWpt != 0) return;
+    for (int w = wave + 1; w < wave + kWpt; ++w)
+#pragma unroll
+      for (int g = 0; g < kGvGroups; ++g)
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi) acc[g][mi] += red[w][g][mi][lane];
+  }
+
+  // lane (col, kq) holds tokens 16g + 4kq + r of row 16 * tile + col
+  const int n = 16 * tile + col;
+#pragma unroll
+  for (int g = 0; g < kGvGroups; ++g) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int slot = 16 * g + 4 * kq + r;
+      if (slot >= ntok) continue;
+      const int o = orow[slot];
+      if constexpr (kUp) {
+        const float gv = acc[g][0][r], uv = acc[g][1][r];
+        reinterpret_cast<float*>(out)[(size_t)o * kFf + n] = gv / (1.f + expf(-gv)) * uv;
+      } else if constexpr (KIND == MOE_DN) {
+        reinterpret_cast<uint16_t*>(out)[(size_t)o * kHid + n] = tlx_f2h_bits(acc[g][0][r]);
+      } else {
+        reinterpret_cast<float*>(out)[(size_t)o * kHid + n] = acc[g][0][r];
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ combine
 // y = hres + (sum_r g_r * part_r (r ascending) + sg * shared), fp32; 8 elements per thread.
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ parts, const float* __restrict__ gates,
@@ -430,10 +611,25 @@ extern "C" int tlx_moe_sort(const uint16_t* eids, int* eoff, uint16_t* plist, ui
 
 extern "C" int tlx_moe_max_items(int np) { return moe_max_items(np); }
 
+// pair counts up to this use the GEMV form (a few tokens per expert); larger ones the GEMM
+constexpr int kGvMaxPairs = 2048;
+
+template <int KIND>
+dim3 moe_gv_grid(int nx) {
+  constexpr int kWpt = moe_gv_wpt<KIND>(), kTpw = 4 / kWpt;
+  constexpr int kRows = (KIND == MOE_UP || KIND == MOE_UP_DENSE) ? kFf : kHid;
+  return dim3(nx, kRows / 16 / kTpw);
+}
+
 extern "C" int tlx_moe_up4(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const uint32_t* items,
                            const uint32_t* nitp, const float* xs, const float* iq4nl, float* ys, int np, void* stream) {
   TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(xs, 16), TLX_E_ALIGN);
+  if (np <= kGvMaxPairs) {
+    moe_gv_kernel<MOE_UP><<<moe_gv_grid<MOE_UP>(moe_max_items(np)), 256, 0, (hipStream_t)stream>>>(
+        ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, 0);
+    return tlx_launch_status();
+  }
   const dim3 grid(moe_max_items(np), MoeShape<MOE_UP>::STRIPES);
   moe_gemm_kernel<MOE_UP><<<grid, 256, 0, (hipStream_t)stream>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, 0);
   return tlx_launch_status();
@@ -444,6 +640,11 @@ extern "C" int tlx_moe_dn4(const uint64_t* ptbl_dn, const int* eoff, const uint1
                            void* stream) {
   TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(act, 16) || !tlx_aligned(parts, 16), TLX_E_ALIGN);
+  if (np <= kGvMaxPairs) {
+    moe_gv_kernel<MOE_DN><<<moe_gv_grid<MOE_DN>(moe_max_items(np)), 256, 0, (hipStream_t)stream>>>(
+        ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
+    return tlx_launch_status();
+  }
   const dim3 grid(moe_max_items(np), MoeShape<MOE_DN>::STRIPES);
   moe_gemm_kernel<MOE_DN><<<grid, 256, 0, (hipStream_t)stream>>>(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
   return tlx_launch_status();
@@ -454,6 +655,15 @@ extern "C" int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const fl
   TLX_RET_IF(P < 1, TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(xs, 16) || !tlx_aligned(act, 16), TLX_E_ALIGN);
   const int chunks = (P + kTok - 1) / kTok;
+  if (8 * P <= kGvMaxPairs) {
+    moe_gv_kernel<MOE_UP_DENSE><<<moe_gv_grid<MOE_UP_DENSE>(chunks), 256, 0, (hipStream_t)stream>>>(
+        ptbl_sh, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, act, P);
+    int rc = tlx_launch_status();
+    TLX_RET_IF(rc != TLX_OK, rc);
+    moe_gv_kernel<MOE_DN_DENSE><<<moe_gv_grid<MOE_DN_DENSE>(chunks), 256, 0, (hipStream_t)stream>>>(
+        ptbl_sh + 1, nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
+    return tlx_launch_status();
+  }
   moe_gemm_kernel<MOE_UP_DENSE><<<dim3(chunks, MoeShape<MOE_UP_DENSE>::STRIPES), 256, 0, (hipStream_t)stream>>>(
       ptbl_sh, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, act, P);
   int rc = tlx_launch_status();
