@@ -187,6 +187,26 @@ def test_moe_layer_prefill_m2048_sampled(gpu, experts):
     assert np.isfinite(out["y"]).all()
 
 
+@pytest.mark.parametrize("P", [64, 256])
+def test_moe_layer_small_batch_skewed(gpu, experts, P):
+    """Pair counts up to 2048 take the GEMV form: a router biased towards 12 experts gives them
+    2..4 groups of 16 tokens and several 64-pair items each (ragged last ones)."""
+    print(f"[case] moe layer skewed P={P}", flush=True)
+    rng = np.random.default_rng(24 + P)
+    x, logits, sg, hres = _inputs(rng, P)
+    logits[:, :12] += 3.0
+    out = _run_layer(gpu, experts, x, logits, sg, hres)
+    eids, _ = moe.topk_ref(logits)
+    cnt = np.bincount(eids.ravel(), minlength=moe.E)
+    assert cnt[:12].min() > 16   # every hot expert has more than one group
+    hot = [int(np.argmax(cnt[:12])), int(np.argmin(cnt[:12]))]
+    pairs = [8 * p + r for p in range(P) for r in range(8) if eids[p, r] in hot]
+    srng = np.random.default_rng(6)
+    pairs = sorted(set(pairs) | set(srng.choice(8 * P, 48, replace=False).tolist()))
+    positions = sorted(srng.choice(P, 12, replace=False).tolist())
+    _check_layer(experts, x, logits, sg, hres, out, pairs, positions)
+
+
 def test_moe_layer_deterministic(gpu, experts):
     print("[case] moe determinism P=256", flush=True)
     rng = np.random.default_rng(23)

@@ -148,6 +148,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const uint16_t* __restri
                                                         uint32_t* __restrict__ nitp, int np) {
   __shared__ uint16_t wcnt[kSortWaves][kE];   // this round: pairs of expert e in wave w
   __shared__ int run[kE];                     // pairs of expert e before this round (pass 2: + eoff)
+  __shared__ int wtot[kE / 64][2];            // per-wave totals of the count scans
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint64_t below = (1ull << lane) - 1ull;
   const int rounds = (np + 1023) / 1024;
@@ -178,18 +179,28 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const uint16_t* __restri
       }
       __syncthreads();
     }
-    if (pass == 0) {
-      if (t == 0) {   // totals -> bin offsets and work items; run[] becomes the bin starts
-        int sum = 0, b = 0;
-        for (int e = 0; e < kE; ++e) {
-          const int c = run[e];
-          eoff[e] = sum;
-          for (int k = 0; k < c; k += kTok) items[b++] = ((uint32_t)e << 16) | (uint32_t)k;
-          run[e] = sum;
-          sum += c;
+    if (pass == 0) {   // totals -> bin offsets and work items; run[] becomes the bin starts
+      // exclusive prefix sums over the 256 experts of the pair counts and of the item counts
+      // (ceil(count / 64)): wave-inclusive scans, then the totals of the waves before
+      const int c = t < kE ? run[t] : 0, ni = (c + kTok - 1) / kTok;
+      int sc = c, si = ni;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int pc = __shfl_up(sc, o, 64), pi = __shfl_up(si, o, 64);
+        if (lane >= o) { sc += pc; si += pi; }
+      }
+      if (t < kE && lane == 63) { wtot[wave][0] = sc; wtot[wave][1] = si; }
+      __syncthreads();
+      if (t < kE) {
+        int bc = sc - c, bi = si - ni;
+        for (int w = 0; w < wave; ++w) { bc += wtot[w][0]; bi += wtot[w][1]; }
+        eoff[t] = bc;
+        for (int j = 0; j < ni; ++j) items[bi + j] = ((uint32_t)t << 16) | (uint32_t)(kTok * j);
+        run[t] = bc;
+        if (t == kE - 1) {
+          eoff[kE] = bc + c;
+          *nitp = (uint32_t)(bi + ni);
         }
-        eoff[kE] = sum;
-        *nitp = (uint32_t)b;
       }
       __syncthreads();
     }
@@ -401,28 +412,141 @@ constexpr int kGvGroups = kTok / 16;
 template <int KIND>
 constexpr int moe_gv_wpt() { return (KIND == MOE_UP || KIND == MOE_UP_DENSE) ? 2 : 1; }
 
+using gbyte = const __attribute__((address_space(1))) uint8_t;
+
+// One wave's share of a 16-row output tile for NG groups of 16 tokens.  NG is a template
+// argument so that every activation load is unconditional: the compiler can then issue them
+// ahead of their MFMAs instead of waiting on each one in turn.  red: the workgroup's
+// [4 waves][kGvGroups][NMAT][64 lanes] reduction buffer.
+template <int KIND, int NG>
+__device__ __forceinline__ void moe_gv_tile(gbyte* base, const uint32_t* lut, const int* xrow, const int* orow,
+                                            f4_t* red, const float* __restrict__ xs, void* __restrict__ out,
+                                            int ntok, int tile, int wave, int lane) {
+  using S = MoeShape<KIND>;
+  constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
+  constexpr int NMAT = kUp ? 2 : 1;
+  constexpr int kNb = S::K / 256;                 // IQ4_XS blocks per row
+  constexpr int kWpt = moe_gv_wpt<KIND>();        // waves per tile
+  constexpr int kBpw = kNb / kWpt;                // blocks per wave
+  constexpr int kRowBytes = kNb * 136;
+  const int col = lane & 15, kq = lane >> 4;
+  const int kb0 = (wave % kWpt) * kBpw;
+  gbyte* wrow[NMAT];
+  wrow[0] = base + (size_t)(16 * tile + col) * kRowBytes;
+  if constexpr (NMAT == 2) wrow[1] = wrow[0] + kGateBytes;
+
+  // all of the wave's weight loads first
+  u2_t hdr[kBpw][NMAT];
+  u4_t qv[kBpw][NMAT][2];
+#pragma unroll
+  for (int bb = 0; bb < kBpw; ++bb)
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi) {
+      gbyte* blk = wrow[mi] + 136 * (kb0 + bb);
+      hdr[bb][mi] = *(const __attribute__((address_space(1))) u2_t*)(blk);
+      qv[bb][mi][0] = *(const __attribute__((address_space(1))) u4_t*)(blk + 8 + 32 * kq);
+      qv[bb][mi][1] = *(const __attribute__((address_space(1))) u4_t*)(blk + 24 + 32 * kq);
+    }
+  const float* xr[NG];   // lane's activation row in group g, at its first k of a block
+#pragma unroll
+  for (int g = 0; g < NG; ++g) xr[g] = xs + (size_t)xrow[16 * g + col] * S::K + 256 * kb0 + 64 * kq;
+
+  f4_t acc[NG][NMAT];
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi) acc[g][mi] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int bb = 0; bb < kBpw; ++bb) {
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const int ib = 2 * kq + sb;   // the lane's sub-blocks 2kq, 2kq + 1
+      _Float16 dh[NMAT];
+#pragma unroll
+      for (int mi = 0; mi < NMAT; ++mi) {
+        const uint32_t sh = hdr[bb][mi].x >> 16;
+        const uint32_t ls = ((hdr[bb][mi].y >> (4 * ib)) & 0xFu) | (((sh >> (2 * ib)) & 3u) << 4);
+        dh[mi] = (_Float16)(tlx_h2f((uint16_t)hdr[bb][mi].x) * (float)((int)ls - 32));
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        h8_t B[NMAT];
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi) {
+          const uint32_t qw = qv[bb][mi][sb][c];
+          const u4_t w4 = {lut[qw & 0xFF], lut[(qw >> 8) & 0xFF], lut[(qw >> 16) & 0xFF], lut[qw >> 24]};
+          B[mi] = __builtin_bit_cast(h8_t, w4) * splat8h(dh[mi]);
+        }
+        const int k0 = 256 * bb + 32 * sb + 4 * c;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const float4 x0 = *reinterpret_cast<const float4*>(xr[g] + k0);
+          const float4 x1 = *reinterpret_cast<const float4*>(xr[g] + k0 + 16);
+          const h8_t A = {(_Float16)x0.x, (_Float16)x1.x, (_Float16)x0.y, (_Float16)x1.y,
+                          (_Float16)x0.z, (_Float16)x1.z, (_Float16)x0.w, (_Float16)x1.w};
+#pragma unroll
+          for (int mi = 0; mi < NMAT; ++mi)
+            acc[g][mi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[mi], acc[g][mi], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // fixed-order reduction over the waves of a tile
+  auto rslot = [&](int w, int g, int mi) -> f4_t& { return red[((w * kGvGroups + g) * NMAT + mi) * 64 + lane]; };
+  if constexpr (kWpt > 1) {
+    if (wave % kWpt != 0) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi) rslot(wave, g, mi) = acc[g][mi];
+    }
+    __syncthreads();
+    if (wave % kWpt != 0) return;
+    for (int w = wave + 1; w < wave + kWpt; ++w)
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi) acc[g][mi] += rslot(w, g, mi);
+  }
+
+  // lane (col, kq) holds tokens 16g + 4kq + r of row 16 * tile + col
+  const int n = 16 * tile + col;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int slot = 16 * g + 4 * kq + r;
+      if (slot >= ntok) continue;
+      const int o = orow[slot];
+      if constexpr (kUp) {
+        const float gv = acc[g][0][r], uv = acc[g][1][r];
+        reinterpret_cast<float*>(out)[(size_t)o * kFf + n] = gv / (1.f + expf(-gv)) * uv;
+      } else if constexpr (KIND == MOE_DN) {
+        reinterpret_cast<uint16_t*>(out)[(size_t)o * kHid + n] = tlx_f2h_bits(acc[g][0][r]);
+      } else {
+        reinterpret_cast<float*>(out)[(size_t)o * kHid + n] = acc[g][0][r];
+      }
+    }
+  }
+}
+
 template <int KIND>
 __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff,
                                                      const uint16_t* __restrict__ plist,
                                                      const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp,
                                                      const float* __restrict__ xs, const float* __restrict__ iq4nl,
                                                      void* __restrict__ out, int P) {
-  using S = MoeShape<KIND>;
   constexpr bool kDense = KIND == MOE_DN_DENSE || KIND == MOE_UP_DENSE;
   constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
   constexpr int NMAT = kUp ? 2 : 1;
-  constexpr int kNb = S::K / 256;                 // IQ4_XS blocks per row
-  constexpr int kWpt = moe_gv_wpt<KIND>();        // waves per tile
-  constexpr int kBpw = kNb / kWpt;                // blocks per wave
-  constexpr int kTpw = 4 / kWpt;                  // tiles per workgroup
-  constexpr int kRowBytes = kNb * 136;
+  constexpr int kTpw = 4 / moe_gv_wpt<KIND>();    // tiles per workgroup
   __shared__ uint32_t lut[256];
   __shared__ int xrow[kTok], orow[kTok];
-  __shared__ f4_t red[4][kGvGroups][NMAT][64];
+  __shared__ f4_t red[4 * kGvGroups * NMAT * 64];
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  const int col = lane & 15, kq = lane >> 4;
 
-  using gbyte = const __attribute__((address_space(1))) uint8_t;
   int m0, ntok;
   gbyte* base;
   if constexpr (kDense) {
@@ -455,108 +579,12 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
     lut[t] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
   }
   __syncthreads();
-  const int ngroups = (ntok + 15) >> 4;
-
-  const int tile = (int)blockIdx.y * kTpw + wave / kWpt;   // 16-row output tile
-  const int kb0 = (wave % kWpt) * kBpw;
-  gbyte* wrow[NMAT];
-  wrow[0] = base + (size_t)(16 * tile + col) * kRowBytes;
-  if constexpr (NMAT == 2) wrow[1] = wrow[0] + kGateBytes;
-
-  // all of the wave's weight loads first
-  u2_t hdr[kBpw][NMAT];
-  u4_t qv[kBpw][NMAT][2];
-#pragma unroll
-  for (int bb = 0; bb < kBpw; ++bb)
-#pragma unroll
-    for (int mi = 0; mi < NMAT; ++mi) {
-      gbyte* blk = wrow[mi] + 136 * (kb0 + bb);
-      hdr[bb][mi] = *(const __attribute__((address_space(1))) u2_t*)(blk);
-      qv[bb][mi][0] = *(const __attribute__((address_space(1))) u4_t*)(blk + 8 + 32 * kq);
-      qv[bb][mi][1] = *(const __attribute__((address_space(1))) u4_t*)(blk + 24 + 32 * kq);
-    }
-
-  f4_t acc[kGvGroups][NMAT];
-#pragma unroll
-  for (int g = 0; g < kGvGroups; ++g)
-#pragma unroll
-    for (int mi = 0; mi < NMAT; ++mi) acc[g][mi] = f4_t{0.f, 0.f, 0.f, 0.f};
-
-#pragma unroll
-  for (int bb = 0; bb < kBpw; ++bb) {
-    const int kbase = 256 * (kb0 + bb) + 64 * kq;   // the lane's sub-blocks 2kq, 2kq + 1
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      const int ib = 2 * kq + sb;
-      _Float16 dh[NMAT];
-#pragma unroll
-      for (int mi = 0; mi < NMAT; ++mi) {
-        const uint32_t sh = hdr[bb][mi].x >> 16;
-        const uint32_t ls = ((hdr[bb][mi].y >> (4 * ib)) & 0xFu) | (((sh >> (2 * ib)) & 3u) << 4);
-        dh[mi] = (_Float16)(tlx_h2f((uint16_t)hdr[bb][mi].x) * (float)((int)ls - 32));
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        h8_t B[NMAT];
-#pragma unroll
-        for (int mi = 0; mi < NMAT; ++mi) {
-          const uint32_t qw = qv[bb][mi][sb][c];
-          const u4_t w4 = {lut[qw & 0xFF], lut[(qw >> 8) & 0xFF], lut[(qw >> 16) & 0xFF], lut[qw >> 24]};
-          B[mi] = __builtin_bit_cast(h8_t, w4) * splat8h(dh[mi]);
-        }
-        const int k0 = kbase + 32 * sb + 4 * c;
-#pragma unroll
-        for (int g = 0; g < kGvGroups; ++g) {
-          if (g < ngroups) {
-            const float* xr = xs + (size_t)xrow[16 * g + col] * S::K + k0;
-            const float4 x0 = *reinterpret_cast<const float4*>(xr);
-            const float4 x1 = *reinterpret_cast<const float4*>(xr + 16);
-            const h8_t A = {(_Float16)x0.x, (_Float16)x1.x, (_Float16)x0.y, (_Float16)x1.y,
-                            (_Float16)x0.z, (_Float16)x1.z, (_Float16)x0.w, (_Float16)x1.w};
-#pragma unroll
-            for (int mi = 0; mi < NMAT; ++mi)
-              acc[g][mi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[mi], acc[g][mi], 0, 0, 0);
-          }
-        }
-      }
-    }
-  }
-
-  // fixed-order reduction over the waves of a tile
-  if constexpr (kWpt > 1) {
-    if (wave % kWpt != 0) {
-#pragma unroll
-      for (int g = 0; g < kGvGroups; ++g)
-#pragma unroll
-        for (int mi = 0; mi < NMAT; ++mi) red[wave][g][mi][lane] = acc[g][mi];
-    }
-    __syncthreads();
-    if (wave % kWpt != 0) return;
-    for (int w = wave + 1; w < wave + kWpt; ++w)
-#pragma unroll
-      for (int g = 0; g < kGvGroups; ++g)
-#pragma unroll
-        for (int mi = 0; mi < NMAT; ++mi) acc[g][mi] += red[w][g][mi][lane];
-  }
-
-  // lane (col, kq) holds tokens 16g + 4kq + r of row 16 * tile + col
-  const int n = 16 * tile + col;
-#pragma unroll
-  for (int g = 0; g < kGvGroups; ++g) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int slot = 16 * g + 4 * kq + r;
-      if (slot >= ntok) continue;
-      const int o = orow[slot];
-      if constexpr (kUp) {
-        const float gv = acc[g][0][r], uv = acc[g][1][r];
-        reinterpret_cast<float*>(out)[(size_t)o * kFf + n] = gv / (1.f + expf(-gv)) * uv;
-      } else if constexpr (KIND == MOE_DN) {
-        reinterpret_cast<uint16_t*>(out)[(size_t)o * kHid + n] = tlx_f2h_bits(acc[g][0][r]);
-      } else {
-        reinterpret_cast<float*>(out)[(size_t)o * kHid + n] = acc[g][0][r];
-      }
-    }
+  const int tile = (int)blockIdx.y * kTpw + wave / moe_gv_wpt<KIND>();   // 16-row output tile
+  switch ((ntok + 15) >> 4) {   // workgroup-uniform
+    case 1: moe_gv_tile<KIND, 1>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
+    case 2: moe_gv_tile<KIND, 2>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
+    case 3: moe_gv_tile<KIND, 3>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
+    default: moe_gv_tile<KIND, 4>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
   }
 }
 
