@@ -187,10 +187,11 @@ def test_moe_layer_prefill_m2048_sampled(gpu, experts):
     assert np.isfinite(out["y"]).all()
 
 
-@pytest.mark.parametrize("P", [64, 256])
-def test_moe_layer_small_batch_skewed(gpu, experts, P):
-    """Pair counts up to 2048 take the GEMV form: a router biased towards 12 experts gives them
-    2..4 groups of 16 tokens and several 64-pair items each (ragged last ones)."""
+@pytest.mark.parametrize("P", [64, 256, 300])
+def test_moe_layer_skewed(gpu, experts, P):
+    """A router biased towards 12 experts gives them 2..4 groups of 16 tokens and several 64-pair
+    items each (ragged last ones).  Pair counts up to 2048 (P = 64, 256) take the GEMV form, more
+    (P = 300) the prefill GEMM, whose shared expert then ends on a 44-position chunk."""
     print(f"[case] moe layer skewed P={P}", flush=True)
     rng = np.random.default_rng(24 + P)
     x, logits, sg, hres = _inputs(rng, P)

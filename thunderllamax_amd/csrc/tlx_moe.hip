@@ -210,72 +210,215 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const uint16_t* __restri
 // ------------------------------------------------------------------ grouped IQ4_XS GEMM
 enum MoeKind { MOE_UP = 0, MOE_DN = 1, MOE_DN_DENSE = 2, MOE_UP_DENSE = 3 };
 
-// K: reduction length; TROWS: weight rows per workgroup tile (FFN: half gate, half up);
-// STRIPES: tiles per expert matrix
+// K: reduction length
 template <int KIND> struct MoeShape;
-template <> struct MoeShape<MOE_UP> { static constexpr int K = kHid, TROWS = 256, STRIPES = kFf / 128; };
-template <> struct MoeShape<MOE_UP_DENSE> { static constexpr int K = kHid, TROWS = 256, STRIPES = kFf / 128; };
-template <> struct MoeShape<MOE_DN> { static constexpr int K = kFf, TROWS = 128, STRIPES = kHid / 128; };
-template <> struct MoeShape<MOE_DN_DENSE> { static constexpr int K = kFf, TROWS = 128, STRIPES = kHid / 128; };
-
-struct __attribute__((aligned(16))) MoeLds {
-  _Float16 a[2][kTok * 32];      // activations, fragment order (16-B piece p of row R at ((R/16)*64 + p*16 + R%16))
-  _Float16 b[2][256 * 32];       // dequantized weights, same order
-  uint32_t lut[256];             // quant byte -> (kv[lo], kv[hi]) fp16
-  int xrow[kTok];                // activation row of token slot t
-  int orow[kTok];                // output row of token slot t
-};
+template <> struct MoeShape<MOE_UP> { static constexpr int K = kHid; };
+template <> struct MoeShape<MOE_UP_DENSE> { static constexpr int K = kHid; };
+template <> struct MoeShape<MOE_DN> { static constexpr int K = kFf; };
+template <> struct MoeShape<MOE_DN_DENSE> { static constexpr int K = kFf; };
 
 __device__ __forceinline__ h8_t splat8h(_Float16 v) { return h8_t{v, v, v, v, v, v, v, v}; }
 
-__device__ __forceinline__ int moe_frag(int R, int p) { return ((R >> 4) * 64 + p * 16 + (R & 15)) * 8; }
+using gbyte = const __attribute__((address_space(1))) uint8_t;
 
-// raw global data of one 32-k step for one thread (registers, prefetched two steps ahead)
-template <int TROWS>
-struct MoeRaw {
-  float4 x0, x1;                         // activations k 4j..4j+3 and 16+4j..19+4j
-  u2_t hdr;                              // block header: d | sh << 16, sl
-  std::conditional_t<TROWS == 256, u4_t, u2_t> q;   // quant bytes (16 or 8)
+// ------------------------------------------------------------------ grouped IQ4_XS GEMM (prefill)
+// Work unit: one 64-pair item (expert, chunk of its sorted pairs) x one stripe of weight rows
+// (FFN: 256 gate rows + the matching 256 up rows; down: 512 rows).  8 waves, two per SIMD; wave
+// w owns four 16-row tiles (FFN: gate tiles 2w, 2w + 1 of the stripe and the two matching up
+// tiles; down: tiles 4w..4w+3) over the whole K, so no reduction across waves.
+//   * weights go straight from HBM to registers and are decoded there, as in the GEMV form
+//     below: lane (col, kq) holds row col's sub-blocks kq, kq + 4 of each block (32 quant
+//     bytes + the 8-byte header);
+//   * activations: per 256-k block, the item's token rows are DMA'd (global -> LDS, 16 B a
+//     lane, one 1 KB row per wave-load) into a double-buffered fp32 tile, piece p of row t at
+//     slot p ^ (t & 7) so that the 8 lanes of a ds_read_b128 phase (rows col 0..7) hit distinct
+//     16-B slots; a wave converts each A fragment to fp16 once and uses it for its 4 tiles;
+//   * per block: wait for this block's data, one barrier, issue the next block's activation DMA
+//     and weight loads, then 8 x (NG groups x 4 tiles) MFMAs -- every load has a whole block of
+//     compute to land in;
+//   * blockIdx -> (item, stripe) keeps the stripes of an item on one XCD (workgroups are
+//     dispatched round-robin over the 8 XCDs), so its activations are read from that L2.
+constexpr int kPfTiles = 4;   // 16-row tiles per wave
+constexpr int kPfWaves = 8;
+constexpr int kPfThreads = kPfWaves * TLX_WAVE;
+
+struct __attribute__((aligned(16))) MoePfLds {
+  float a[2][kTok * 256];   // 256-k blocks of the item's activations, fp32, swizzled 16-B pieces
+  uint32_t lut[256];        // quant byte -> (kv[lo], kv[hi]) fp16
+  int xrow[kTok];           // activation row of token slot t
+  int orow[kTok];           // output row of token slot t
 };
 
 template <int KIND>
-__global__ __launch_bounds__(256) void moe_gemm_kernel(const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff,
-                                                       const uint16_t* __restrict__ plist,
-                                                       const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp,
-                                                       const float* __restrict__ xs, const float* __restrict__ iq4nl,
-                                                       void* __restrict__ out, int P) {
+constexpr int moe_pf_stripes() {
+  return (KIND == MOE_UP || KIND == MOE_UP_DENSE) ? kFf / (16 * 2 * kPfWaves) : kHid / (16 * kPfTiles * kPfWaves);
+}
+
+// DMA 256-k block kb of the item's token rows t < 16 * NG into buf: wave w moves rows 8w..8w+7
+// (xr: their activation rows, wave-uniform)
+template <int K, int NG>
+__device__ __forceinline__ void moe_pf_dma_a(float* buf, const int* xr, const float* __restrict__ xs, int kb,
+                                             int wave, int lane) {
+  if (8 * wave >= 16 * NG) return;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const float* src = xs + (size_t)xr[r] * K + 256 * kb + 4 * (lane ^ r);   // row 8w + r: r = t & 7
+    __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(buf + 256 * (8 * wave + r)),
+                                     16, 0, 0);
+  }
+}
+
+template <int KIND, int NG>
+__device__ __forceinline__ void moe_pf_tile(MoePfLds& L, gbyte* base, const float* __restrict__ xs,
+                                            void* __restrict__ out, int ntok, int stripe, int wave, int lane) {
   using S = MoeShape<KIND>;
+  constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
+  constexpr int kNb = S::K / 256;
+  constexpr int kRowBytes = kNb * 136;
+  const int col = lane & 15, kq = lane >> 4;
+  // the wave's tiles: FFN gate tiles 2 * (kPfWaves * stripe + wave) + {0, 1}, then the same up
+  // tiles; down tiles 4 * (kPfWaves * stripe + wave) + {0..3}
+  const int tb = kPfWaves * stripe + wave;
+  gbyte* wrow[kPfTiles];
+#pragma unroll
+  for (int j = 0; j < kPfTiles; ++j) {
+    if constexpr (kUp)
+      wrow[j] = base + (j >= 2 ? kGateBytes : 0) + (size_t)(16 * (2 * tb + (j & 1)) + col) * kRowBytes;
+    else
+      wrow[j] = base + (size_t)(16 * (4 * tb + j) + col) * kRowBytes;
+  }
+  u2_t hdr[2][kPfTiles];
+  u4_t qv[2][kPfTiles][2];
+  auto load_w = [&](int kb, int set) {
+#pragma unroll
+    for (int j = 0; j < kPfTiles; ++j) {
+      gbyte* blk = wrow[j] + 136 * kb;
+      hdr[set][j] = *(const __attribute__((address_space(1))) u2_t*)(blk);
+      qv[set][j][0] = *(const __attribute__((address_space(1))) u4_t*)(blk + 8 + 16 * kq);
+      qv[set][j][1] = *(const __attribute__((address_space(1))) u4_t*)(blk + 72 + 16 * kq);
+    }
+  };
+
+  f4_t acc[NG][kPfTiles];
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int j = 0; j < kPfTiles; ++j) acc[g][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int sw = col & 7;
+  int xr[8];   // the activation rows this wave stages (scalar registers: read from LDS once)
+#pragma unroll
+  for (int r = 0; r < 8; ++r) xr[r] = __builtin_amdgcn_readfirstlane(L.xrow[8 * wave + r]);
+
+  // block kb reads activation buffer / weight register set kb & 1 (= set)
+  auto block = [&](int kb, int set) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this block's activations and weights
+    __syncthreads();                      // ... for every wave; block kb - 1's buffer is free
+    if (kb + 1 < kNb) moe_pf_dma_a<S::K, NG>(L.a[set ^ 1], xr, xs, kb + 1, wave, lane);
+    load_w(min(kb + 1, kNb - 1), set ^ 1);   // clamped on the last block
+    const float* arow = L.a[set] + 256 * col;   // + 4096 * g: token row 16g + col
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const int ib = kq + 4 * sb;
+      _Float16 dh[kPfTiles];
+#pragma unroll
+      for (int j = 0; j < kPfTiles; ++j) {
+        const uint32_t sh = hdr[set][j].x >> 16;
+        const uint32_t ls = ((hdr[set][j].y >> (4 * ib)) & 0xFu) | (((sh >> (2 * ib)) & 3u) << 4);
+        dh[j] = (_Float16)(tlx_h2f((uint16_t)hdr[set][j].x) * (float)((int)ls - 32));
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        h8_t B[kPfTiles];
+#pragma unroll
+        for (int j = 0; j < kPfTiles; ++j) {
+          const uint32_t qw = qv[set][j][sb][c];
+          const u4_t w4 = {L.lut[qw & 0xFF], L.lut[(qw >> 8) & 0xFF], L.lut[(qw >> 16) & 0xFF], L.lut[qw >> 24]};
+          B[j] = __builtin_bit_cast(h8_t, w4) * splat8h(dh[j]);
+        }
+        const int pc = 8 * kq + 32 * sb + c;   // 16-B piece of k0 = 32kq + 128sb + 4c
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const float4 x0 = *reinterpret_cast<const float4*>(arow + 4096 * g + 4 * (pc ^ sw));
+          const float4 x1 = *reinterpret_cast<const float4*>(arow + 4096 * g + 4 * ((pc + 4) ^ sw));
+          const h8_t A = {(_Float16)x0.x, (_Float16)x1.x, (_Float16)x0.y, (_Float16)x1.y,
+                          (_Float16)x0.z, (_Float16)x1.z, (_Float16)x0.w, (_Float16)x1.w};
+#pragma unroll
+          for (int j = 0; j < kPfTiles; ++j)
+            acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], acc[g][j], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  moe_pf_dma_a<S::K, NG>(L.a[0], xr, xs, 0, wave, lane);
+  load_w(0, 0);
+  for (int kb = 0; kb < kNb; kb += 2) {
+    block(kb, 0);
+    block(kb + 1, 1);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // the clamped tail loads
+
+  // lane (col, kq) holds tokens 16g + 4kq + r of row 16 * tile + col
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int slot = 16 * g + 4 * kq + r;
+      if (slot >= ntok) continue;
+      const int o = L.orow[slot];
+      if constexpr (kUp) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float gv = acc[g][j][r], uv = acc[g][j + 2][r];
+          const int n = 16 * (2 * tb + j) + col;
+          reinterpret_cast<float*>(out)[(size_t)o * kFf + n] = gv / (1.f + expf(-gv)) * uv;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kPfTiles; ++j) {
+          const int n = 16 * (4 * tb + j) + col;
+          if constexpr (KIND == MOE_DN)
+            reinterpret_cast<uint16_t*>(out)[(size_t)o * kHid + n] = tlx_f2h_bits(acc[g][j][r]);
+          else
+            reinterpret_cast<float*>(out)[(size_t)o * kHid + n] = acc[g][j][r];
+        }
+      }
+    }
+  }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(kPfThreads, 1) void moe_pf_kernel(
+    const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff, const uint16_t* __restrict__ plist,
+    const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp, const float* __restrict__ xs,
+    const float* __restrict__ iq4nl, void* __restrict__ out, int P) {
   constexpr bool kDense = KIND == MOE_DN_DENSE || KIND == MOE_UP_DENSE;
   constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
-  constexpr int kRowBytes = (S::K / 256) * 136;
-  constexpr int kRG = S::TROWS / 64;     // 16-row groups per wave
-  __shared__ MoeLds L;
-  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  const int col = lane & 15, kq = lane >> 4;
+  constexpr int kS = moe_pf_stripes<KIND>();
+  __shared__ MoePfLds L;
+  const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
+  // XCD x = id % 8 runs the kS stripes of items x, x + 8, ... one item after another
+  const int id = (int)blockIdx.x, l = id >> 3;
+  const int stripe = l % kS, item = (l / kS) * 8 + (id & 7);
 
-  // work item: expert, first pair of the chunk, number of pairs; stripe from blockIdx.y
-  // the slab address is loaded from a table: give it the global address space explicitly, or the
-  // compiler falls back to flat loads, whose completion every LDS wait would then also wait for
-  using gbyte = const __attribute__((address_space(1))) uint8_t;
-  int e, m0, ntok;
+  int m0, ntok;
   gbyte* base;
   if constexpr (kDense) {
-    e = 0;
-    m0 = (int)blockIdx.x * kTok;
+    m0 = item * kTok;
+    if (m0 >= P) return;
     ntok = min(kTok, P - m0);
     base = (gbyte*)(ptbl[0]);
   } else {
-    if (blockIdx.x >= *nitp) return;
-    const uint32_t it = items[blockIdx.x];
-    e = (int)(it >> 16);
+    if (item >= (int)*nitp) return;
+    const uint32_t it = items[item];
+    const int e = (int)(it >> 16);
     m0 = (int)(it & 0xFFFFu);
     const int eb0 = eoff[e];
     ntok = min(kTok, eoff[e + 1] - eb0 - m0);
     m0 += eb0;
     base = (gbyte*)(ptbl[e]);
   }
-  const int s = blockIdx.y;
-
   if (t < kTok) {
     const int slot = min(t, ntok - 1);   // padded slots repeat the last pair; never stored
     if constexpr (kDense) {
@@ -287,119 +430,28 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const uint64_t* __restric
       L.orow[t] = pair;
     }
   }
-  {
-    const int v = t;   // 256 table entries, one per thread
-    const _Float16 lo = (_Float16)iq4nl[v & 15], hi = (_Float16)iq4nl[v >> 4];
-    L.lut[v] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+  if (t < 256) {
+    const _Float16 lo = (_Float16)iq4nl[t & 15], hi = (_Float16)iq4nl[t >> 4];
+    L.lut[t] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
   }
   __syncthreads();
-
-  // staging roles: activations -- token slot t/4, k-pieces {4j..4j+3} and {16+4j..} (j = t%4);
-  // weights -- FFN: tile row t (gate rows 128s.. for t < 128, then the up rows), all 16 quant
-  // bytes of the group; down: tile row t/2, quant bytes 8h..8h+7 (h = t%2)
-  const int at = t >> 2, aj = t & 3;
-  const float* xr = xs + (size_t)L.xrow[at] * S::K;
-  const int br = kUp ? t : (t >> 1), bh = kUp ? 0 : (t & 1);
-  gbyte* wrow;
-  if constexpr (kUp) wrow = base + (br >= 128 ? kGateBytes : 0) + (size_t)(128 * s + (br & 127)) * kRowBytes;
-  else wrow = base + (size_t)(128 * s + br) * kRowBytes;
-
-  auto load = [&](int g, MoeRaw<S::TROWS>& r) {
-    r.x0 = *reinterpret_cast<const float4*>(xr + 32 * g + 4 * aj);
-    r.x1 = *reinterpret_cast<const float4*>(xr + 32 * g + 16 + 4 * aj);
-    gbyte* blk = wrow + 136 * (g >> 3);
-    r.hdr = *(const __attribute__((address_space(1))) u2_t*)(blk);
-    if constexpr (kUp) r.q = *(const __attribute__((address_space(1))) u4_t*)(blk + 8 + 16 * (g & 7));
-    else r.q = *(const __attribute__((address_space(1))) u2_t*)(blk + 8 + 16 * (g & 7) + 8 * bh);
-  };
-  auto store = [&](int g, const MoeRaw<S::TROWS>& r, int buf) {
-    // activations, interleaved to pair with the weight bytes' low and high nibbles
-    const h8_t av = {(_Float16)r.x0.x, (_Float16)r.x1.x, (_Float16)r.x0.y, (_Float16)r.x1.y,
-                     (_Float16)r.x0.z, (_Float16)r.x1.z, (_Float16)r.x0.w, (_Float16)r.x1.w};
-    *reinterpret_cast<h8_t*>(L.a[buf] + moe_frag(at, aj)) = av;
-    const int ib = g & 7;
-    const uint32_t sh = r.hdr.x >> 16;
-    const uint32_t ls = ((r.hdr.y >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xFu) | (((sh >> (2 * ib)) & 3u) << 4);
-    const _Float16 dh = (_Float16)(tlx_h2f((uint16_t)r.hdr.x) * (float)((int)ls - 32));
-    const h8_t dv = {dh, dh, dh, dh, dh, dh, dh, dh};
-    constexpr int kChunks = kUp ? 4 : 2;
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
-      const uint32_t qw = r.q[c];
-      const u4_t w4 = {L.lut[qw & 0xFF], L.lut[(qw >> 8) & 0xFF], L.lut[(qw >> 16) & 0xFF], L.lut[qw >> 24]};
-      *reinterpret_cast<h8_t*>(L.b[buf] + moe_frag(br, (kUp ? 0 : 2 * bh) + c)) = __builtin_bit_cast(h8_t, w4) * dv;
-    }
-  };
-
-  // the wave's weight row groups: FFN gate groups 2w, 2w+1 and up groups 8+2w, 8+2w+1; down 2w, 2w+1
-  int bgrp[kRG];
-#pragma unroll
-  for (int j = 0; j < kRG; ++j) bgrp[j] = kUp ? ((j < 2) ? 2 * wave + j : 8 + 2 * wave + (j - 2)) : 2 * wave + j;
-
-  f4_t acc[4][kRG];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < kRG; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
-
-  constexpr int kSteps = S::K / 32;
-  MoeRaw<S::TROWS> r0, r1;
-  load(0, r0);
-  load(1, r1);
-  store(0, r0, 0);
-  __syncthreads();
-  for (int g = 0; g < kSteps; ++g) {
-    const int buf = g & 1;
-    if (g + 2 < kSteps) load(g + 2, r0);          // two steps ahead
-    if (g + 1 < kSteps) store(g + 1, r1, buf ^ 1);  // the step after this one (loaded last step)
-    h8_t af[4], bf[kRG];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const h8_t*>(L.a[buf] + 512 * i + 8 * lane);
-#pragma unroll
-    for (int j = 0; j < kRG; ++j) bf[j] = *reinterpret_cast<const h8_t*>(L.b[buf] + 512 * bgrp[j] + 8 * lane);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < kRG; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    __syncthreads();
-    r1 = r0;
-  }
-
-  // lane (col, kq) holds, for token tile i, tokens 16i + 4kq + r and row 16*bgrp[j] + col
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int slot = 16 * i + 4 * kq + r;
-      if (slot >= ntok) continue;
-      const int orow = L.orow[slot];
-      if constexpr (kUp) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const float gv = acc[i][j][r], uv = acc[i][j + 2][r];
-          reinterpret_cast<float*>(out)[(size_t)orow * kFf + 128 * s + 16 * bgrp[j] + col] = gv / (1.f + expf(-gv)) * uv;
-        }
-      } else if constexpr (KIND == MOE_DN) {
-#pragma unroll
-        for (int j = 0; j < kRG; ++j)
-          reinterpret_cast<uint16_t*>(out)[(size_t)orow * kHid + 128 * s + 16 * bgrp[j] + col] = tlx_f2h_bits(acc[i][j][r]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < kRG; ++j)
-          reinterpret_cast<float*>(out)[(size_t)orow * kHid + 128 * s + 16 * bgrp[j] + col] = acc[i][j][r];
-      }
-    }
+  switch ((ntok + 15) >> 4) {   // workgroup-uniform
+    case 1: moe_pf_tile<KIND, 1>(L, base, xs, out, ntok, stripe, wave, lane); break;
+    case 2: moe_pf_tile<KIND, 2>(L, base, xs, out, ntok, stripe, wave, lane); break;
+    case 3: moe_pf_tile<KIND, 3>(L, base, xs, out, ntok, stripe, wave, lane); break;
+    default: moe_pf_tile<KIND, 4>(L, base, xs, out, ntok, stripe, wave, lane); break;
   }
 }
 
 // ------------------------------------------------------------------ grouped IQ4_XS GEMV
-// The small-batch (decode / verify) form of the same products.  With a few tokens per expert the
-// step-synchronous GEMM above waits on memory once per 32-k step; here a workgroup owns one
-// 16-row output tile (FFN: 16 gate + the matching 16 up rows; down: two tiles) of one work item,
-// its waves split the tile's K blocks, every wave issues all of its loads at once, and the waves
-// reduce through LDS in a fixed order.
-//   * lane (col, kq) of a wave holds weight row col's sub-blocks 2kq and 2kq + 1 of each of its
-//     blocks (32 quant bytes) and the block header; a sub-block's 4-byte chunk c gives the 8
+// The small-batch (decode / verify) form of the same products.  With a few tokens per expert
+// there is too little work per weight to stage anything; here a workgroup owns one 16-row output
+// tile (FFN: 16 gate + the matching 16 up rows; down: two tiles) of one work item, its waves
+// split the tile's K blocks, every wave issues all of its loads at once, and the waves reduce
+// through LDS in a fixed order.
+//   * lane (col, kq) of a wave holds weight row col's sub-blocks kq and kq + 4 of each of its
+//     blocks (the 4 lanes of a row read 64 contiguous bytes per load) and the block header; a
+//     sub-block's 4-byte chunk c gives the 8
 //     weights j = 4c..4c+3 (low nibbles) and 16 + 4c.. (high nibbles), decoded by 4 lookups of
 //     the byte -> (kv[lo], kv[hi]) fp16 table and scaled by fp16(d * (ls - 32)) -- the same
 //     operand values as the GEMM -- then one v_mfma_f32_16x16x32_f16 per chunk and 16-token group;
@@ -411,8 +463,6 @@ constexpr int kGvGroups = kTok / 16;
 // (2 blocks per row) is one wave's
 template <int KIND>
 constexpr int moe_gv_wpt() { return (KIND == MOE_UP || KIND == MOE_UP_DENSE) ? 2 : 1; }
-
-using gbyte = const __attribute__((address_space(1))) uint8_t;
 
 // One wave's share of a 16-row output tile for NG groups of 16 tokens.  NG is a template
 // argument so that every activation load is unconditional: the compiler can then issue them
@@ -444,12 +494,12 @@ __device__ __forceinline__ void moe_gv_tile(gbyte* base, const uint32_t* lut, co
     for (int mi = 0; mi < NMAT; ++mi) {
       gbyte* blk = wrow[mi] + 136 * (kb0 + bb);
       hdr[bb][mi] = *(const __attribute__((address_space(1))) u2_t*)(blk);
-      qv[bb][mi][0] = *(const __attribute__((address_space(1))) u4_t*)(blk + 8 + 32 * kq);
-      qv[bb][mi][1] = *(const __attribute__((address_space(1))) u4_t*)(blk + 24 + 32 * kq);
+      qv[bb][mi][0] = *(const __attribute__((address_space(1))) u4_t*)(blk + 8 + 16 * kq);
+      qv[bb][mi][1] = *(const __attribute__((address_space(1))) u4_t*)(blk + 72 + 16 * kq);
     }
   const float* xr[NG];   // lane's activation row in group g, at its first k of a block
 #pragma unroll
-  for (int g = 0; g < NG; ++g) xr[g] = xs + (size_t)xrow[16 * g + col] * S::K + 256 * kb0 + 64 * kq;
+  for (int g = 0; g < NG; ++g) xr[g] = xs + (size_t)xrow[16 * g + col] * S::K + 256 * kb0 + 32 * kq;
 
   f4_t acc[NG][NMAT];
 #pragma unroll
@@ -461,7 +511,7 @@ __device__ __forceinline__ void moe_gv_tile(gbyte* base, const uint32_t* lut, co
   for (int bb = 0; bb < kBpw; ++bb) {
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
-      const int ib = 2 * kq + sb;   // the lane's sub-blocks 2kq, 2kq + 1
+      const int ib = kq + 4 * sb;   // the lane's sub-blocks kq, kq + 4
       _Float16 dh[NMAT];
 #pragma unroll
       for (int mi = 0; mi < NMAT; ++mi) {
@@ -478,7 +528,7 @@ __device__ __forceinline__ void moe_gv_tile(gbyte* base, const uint32_t* lut, co
           const u4_t w4 = {lut[qw & 0xFF], lut[(qw >> 8) & 0xFF], lut[(qw >> 16) & 0xFF], lut[qw >> 24]};
           B[mi] = __builtin_bit_cast(h8_t, w4) * splat8h(dh[mi]);
         }
-        const int k0 = 256 * bb + 32 * sb + 4 * c;
+        const int k0 = 256 * bb + 128 * sb + 4 * c;
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
           const float4 x0 = *reinterpret_cast<const float4*>(xr[g] + k0);
@@ -642,6 +692,10 @@ extern "C" int tlx_moe_max_items(int np) { return moe_max_items(np); }
 // pair counts up to this use the GEMV form (a few tokens per expert); larger ones the GEMM
 constexpr int kGvMaxPairs = 2048;
 
+// items (expert chunks) rounded up to a multiple of 8 (one per XCD), times the stripes
+template <int KIND>
+int moe_pf_grid(int nitems) { return (nitems + 7) / 8 * 8 * moe_pf_stripes<KIND>(); }
+
 template <int KIND>
 dim3 moe_gv_grid(int nx) {
   constexpr int kWpt = moe_gv_wpt<KIND>(), kTpw = 4 / kWpt;
@@ -658,8 +712,8 @@ extern "C" int tlx_moe_up4(const uint64_t* ptbl, const int* eoff, const uint16_t
         ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, 0);
     return tlx_launch_status();
   }
-  const dim3 grid(moe_max_items(np), MoeShape<MOE_UP>::STRIPES);
-  moe_gemm_kernel<MOE_UP><<<grid, 256, 0, (hipStream_t)stream>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, 0);
+  moe_pf_kernel<MOE_UP><<<moe_pf_grid<MOE_UP>(moe_max_items(np)), kPfThreads, 0, (hipStream_t)stream>>>(
+      ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, 0);
   return tlx_launch_status();
 }
 
@@ -673,8 +727,8 @@ extern "C" int tlx_moe_dn4(const uint64_t* ptbl_dn, const int* eoff, const uint1
         ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
     return tlx_launch_status();
   }
-  const dim3 grid(moe_max_items(np), MoeShape<MOE_DN>::STRIPES);
-  moe_gemm_kernel<MOE_DN><<<grid, 256, 0, (hipStream_t)stream>>>(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
+  moe_pf_kernel<MOE_DN><<<moe_pf_grid<MOE_DN>(moe_max_items(np)), kPfThreads, 0, (hipStream_t)stream>>>(
+      ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
   return tlx_launch_status();
 }
 
@@ -692,11 +746,11 @@ extern "C" int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const fl
         ptbl_sh + 1, nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
     return tlx_launch_status();
   }
-  moe_gemm_kernel<MOE_UP_DENSE><<<dim3(chunks, MoeShape<MOE_UP_DENSE>::STRIPES), 256, 0, (hipStream_t)stream>>>(
+  moe_pf_kernel<MOE_UP_DENSE><<<moe_pf_grid<MOE_UP_DENSE>(chunks), kPfThreads, 0, (hipStream_t)stream>>>(
       ptbl_sh, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, act, P);
   int rc = tlx_launch_status();
   TLX_RET_IF(rc != TLX_OK, rc);
-  moe_gemm_kernel<MOE_DN_DENSE><<<dim3(chunks, MoeShape<MOE_DN_DENSE>::STRIPES), 256, 0, (hipStream_t)stream>>>(
+  moe_pf_kernel<MOE_DN_DENSE><<<moe_pf_grid<MOE_DN_DENSE>(chunks), kPfThreads, 0, (hipStream_t)stream>>>(
       ptbl_sh + 1, nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
   return tlx_launch_status();
 }
