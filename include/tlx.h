@@ -166,6 +166,22 @@ int tlx_pfg3_iq3d(const void* w, const float* gridf, const uint16_t* x16, const 
 int tlx_pfg3_iq3o(const void* w, const float* gridf, const uint16_t* x16, uint16_t* out16,
                   int M, int N, int K, int layout, void* stream);
 
+/* ---- int8-activation (W4A8) prefill branch.
+ * Activation quantizer, replaces pfk_q8 (engine/pfk_q8.cu:25-59, kernel(x, xq, sx, rs)):
+ * per (row, 128-k chunk) s = max(absmax, 1e-6) * (1/127), xq = rint(x / s) clamped to
+ * +-127, rs = sum of the chunk's xq.  x16 [M][K] fp16, xq [M][K] int8, sx / rs [M][K/128];
+ * K % 128 == 0.  Bit-identical to the reference. */
+int tlx_p8_quant(const uint16_t* x16, int8_t* xq, float* sx, int32_t* rs, int M, int K, void* stream);
+
+/* Fused W4A8 gate+up + SwiGLU, replaces p8w4ffn7 (engine/p8_w4ffn7.cu:169-257,
+ * kernel(w1u, w2u, lut8, xq, sx, out16)): the packed7 IQ3_XXS weights (TLX_LAYOUT_PACK7)
+ * with each grid magnitude replaced by its linearized level lut8[4g + j] (int8[1024]: 1..15)
+ * and the sub-block scale d * ((sw >> 28) + 0.5) * 0.5 * 4.0507, times the int8 activations
+ * xq * sx of tlx_p8_quant; out16 = silu16(half(g)) * half(u).  M % 128 == 0, N % 64 == 0,
+ * K % 256 == 0. */
+int tlx_p8w4_ffn(const void* w1u, const void* w2u, const int8_t* lut8, const int8_t* xq, const float* sx,
+                 uint16_t* out16, int M, int N, int K, int layout, void* stream);
+
 /* ---- MoE grouped-expert path (256 routed experts + 1 shared, hidden 2048, expert FF 512,
  * top-8; IQ4_XS weights).  Pairs are position-major, rank ascending: pair = 8*pos + rank.
  * Expert e's gate/up slab at ptbl[e] (512 gate rows, then 512 up rows 557,056 B later; 1088 B

@@ -50,6 +50,8 @@ SIGNATURES = {
     "tlx_pfg3_ffn": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_pfg3_iq3d": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_pfg3_iq3o": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "tlx_p8_quant": [_p, _p, _p, _p, _i, _i, _p],
+    "tlx_p8w4_ffn": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_moe_topk": [_p, _p, _p, _i, _p],
     "tlx_moe_route": [_p, _p, _p, _p, _p, _p, _i, _p],
     "tlx_moe_sort": [_p, _p, _p, _p, _p, _i, _p],

@@ -13,7 +13,7 @@ All three are pure byte permutations of the GGUF data, computed here with array 
 """
 import numpy as np
 
-from .tables import iq3xxs_gridf, iq4nl_f32
+from .tables import iq3xxs_gridf, iq3xxs_lut8, iq4nl_f32
 
 IQ3XXS_BLOCK = 98
 Q6K_BLOCK = 210
@@ -63,6 +63,12 @@ def gridf_tensor(device="cuda"):
     """The ``gridf`` buffer (float32[1024]) every IQ3_XXS entry point takes."""
     import torch
     return torch.from_numpy(iq3xxs_gridf()).to(device)
+
+
+def lut8_tensor(device="cuda"):
+    """The ``lut8`` buffer (int8[1024]) of the W4A8 prefill branch."""
+    import torch
+    return torch.from_numpy(iq3xxs_lut8()).to(device)
 
 
 def iq4nl_tensor(device="cuda"):

@@ -247,6 +247,33 @@ def pfg3_ffn(wg, wu, gridf, x16, out16, layout=LAYOUT_PACK7, stream=None):
     return out16
 
 
+def p8_quant(x16, xq, sx, rs, stream=None):
+    """Per (row, 128-k chunk) int8 quantization of fp16 activations (pfk_q8: kernel(x, xq, sx, rs))."""
+    M, K = x16.shape
+    if K % 128:
+        raise ValueError("K must be a multiple of 128")
+    _need(xq, M * K, "xq")
+    _need(sx, M * (K // 128) * 4, "sx")
+    _need(rs, M * (K // 128) * 4, "rs")
+    _dev(x16, xq, sx, rs)
+    call("tlx_p8_quant", x16.data_ptr(), xq.data_ptr(), sx.data_ptr(), rs.data_ptr(), M, K, _stream(stream))
+    return xq, sx, rs
+
+
+def p8w4_ffn(w1u, w2u, lut8, xq, sx, out16, layout=LAYOUT_PACK7, stream=None):
+    """W4A8 gate+up + SwiGLU over int8 activations (p8w4ffn7: kernel(w1u, w2u, lut8, xq, sx, out16))."""
+    M, K, N = xq.shape[0], xq.shape[1], out16.shape[1]
+    _need(w1u, _pack7(N, K), "w1u (packed7)")
+    _need(w2u, _pack7(N, K), "w2u (packed7)")
+    _need(lut8, 1024, "lut8")
+    _need(sx, M * (K // 128) * 4, "sx")
+    _need(out16, M * N * 2, "out16")
+    _dev(w1u, w2u, lut8, xq, sx, out16)
+    call("tlx_p8w4_ffn", w1u.data_ptr(), w2u.data_ptr(), lut8.data_ptr(), xq.data_ptr(), sx.data_ptr(),
+         out16.data_ptr(), M, N, K, layout, _stream(stream))
+    return out16
+
+
 def pfg3_iq3d(w, gridf, x16, res16, out32, layout=LAYOUT_PACK7, stream=None):
     """out32[m] = res16[m] + W·x16[m]   (pf_gemm3 RES=1: kernel(w1, gridf, x16, res16, out32))."""
     M, K, N = x16.shape[0], x16.shape[1], out32.shape[1]

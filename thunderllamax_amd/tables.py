@@ -78,6 +78,15 @@ def iq3xxs_gridf() -> np.ndarray:
     return b.astype(np.float32).copy()
 
 
+def iq3xxs_lut8() -> np.ndarray:
+    """int8[1024]: the linearized IQ3_XXS codebook of the W4A8 branch, level of grid byte j of
+    grid word g at 4g + j: clip(rint(byte / 4.0507), 0, 15)
+    (/root/reference/engine/p8_w4ffn7_test.py:44-46; the 8 magnitudes 4..62 map to 1, 3, ..., 15).
+    """
+    b = IQ3XXS_GRID.astype("<u4").view(np.uint8).astype(np.float32)
+    return np.clip(np.rint(b / np.float32(4.0507)), 0, 15).astype(np.int8)
+
+
 def iq4nl_f32() -> np.ndarray:
     """float32[16]: the IQ4_NL non-linear levels (/root/reference/engine/mm/MM_P2_ports.py:112-114)."""
     return KVALUES_IQ4NL.astype(np.float32)
