@@ -19,7 +19,9 @@ an fp32 matmul) on a bounded sample of rows of the same workload, on this host's
 
 ``gemm`` is the metric's second half: the prefill dequant-GEMM of config 4 at M=2048 --
 gate+up with SwiGLU (K=5120, N=2x17408) and down with the residual epilogue (K=17408,
-N=5120) -- in TFLOP/s (2*M*N*K per GEMM) and as a fraction of the dense fp16 MFMA peak.
+N=5120) -- in TFLOP/s (2*M*N*K per GEMM) and as a fraction of the dense fp16 MFMA peak;
+``gemm.w4a8_ffn`` is the reference's int8-activation branch of the same gate+up (activation
+quantizer + W4A8 GEMM), in TOP/s against the dense int8 MFMA peak.
 
 ``sweep`` is config 3: one dense hybrid decode step at M=11 -- 48 gated-delta-net layers and 16
 attention layers (every fourth layer; Q6_K q on layers 3, 7, 19, 31, 43, 55, 59, 63) with their
@@ -49,6 +51,7 @@ PEAK_HBM_GBS = 8000.0
 # by 1.0.  Re-measure when the kernel changes.
 FFN8_M11_TRAFFIC_BYTES = 75_608_191
 PEAK_F16_TFLOPS = 2500.0
+PEAK_I8_TOPS = 5000.0
 ROT_BYTES = 300 * 2**20
 
 
@@ -156,6 +159,14 @@ def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup):
     tf_ffn = f_ffn / (t_ffn * 1e-3) / 1e12
     tf_down = f_down / (t_down * 1e-3) / 1e12
     tf_layer = (f_ffn + f_down) / ((t_ffn + t_down) * 1e-3) / 1e12
+    # the int8-activation branch of the same FFN: quantize the activations, then the W4A8 GEMM
+    xq = torch.empty(M, H, dtype=torch.int8, device=dev)
+    sx = torch.empty(M, H // 128, dtype=torch.float32, device=dev)
+    rs = torch.empty(M, H // 128, dtype=torch.int32, device=dev)
+    lut8 = formats.lut8_tensor(dev)
+    t_q8 = time_call(lambda s: ops.p8_quant(x, xq, sx, rs, stream=s), steps, warmup, torch)
+    t_w4 = time_call(lambda s: ops.p8w4_ffn(pg, pu, lut8, xq, sx, act, stream=s), steps, warmup, torch)
+    to_w4 = f_ffn / ((t_q8 + t_w4) * 1e-3) / 1e12
     return {
         "workload": f"IQ3_XXS prefill FFN, M={M}: gate+up+SwiGLU K={H} N=2x{F}; down+residual K={F} N={H}",
         "M": M,
@@ -165,6 +176,10 @@ def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup):
         "roofline": {"bound": "mfma", "achieved": round(tf_ffn, 1), "peak": PEAK_F16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf_ffn / PEAK_F16_TFLOPS, 4), "traffic": None,
                      "kernel": "pf_gemm_kernel<FFN> (gate+up)"},
+        "w4a8_ffn": {"quant_ms": round(t_q8, 4), "gemm_ms": round(t_w4, 4), "tops": round(to_w4, 1),
+                     "roofline": {"bound": "mfma", "achieved": round(to_w4, 1), "peak": PEAK_I8_TOPS,
+                                  "unit": "TOP/s", "frac": round(to_w4 / PEAK_I8_TOPS, 4),
+                                  "kernel": "p8_quant_kernel + p8w4_ffn_kernel"}},
     }
 
 

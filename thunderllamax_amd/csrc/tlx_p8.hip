@@ -16,9 +16,10 @@
 // per-step float rescale (engine/p8_w4ffn7.cu:123-167), regrouped.
 //   * workgroup tile 128 activation rows x 64 output columns (64 gate + 64 up weight rows);
 //     4 waves, wave (wm, wn) computes rows 64wm.. x columns 32wn.. of gate and up
-//     (16 MFMA tiles of 16 x 16); two workgroups per CU (68.6 KB LDS each);
-//   * per 128-k chunk: the chunk's activations (16 KB), packed7 units (8 KB) and activation
-//     scales are DMA'd into LDS a chunk ahead; the workgroup decodes the units once into an
+//     (16 MFMA tiles of 16 x 16); two workgroups per CU (75.8 KB LDS each);
+//   * per 128-k chunk: the chunk's activations (16 KB) and activation scales are DMA'd into
+//     LDS a chunk ahead, its packed7 units (8 KB) once the previous chunk's are decoded; the
+//     workgroup decodes the units once, one sign-folded table lookup per 4 weights, into an
 //     int8 B tile in MFMA fragment order (+ per row the 4 step factors and d'), then each
 //     wave runs 4 steps x 16 MFMAs;
 //   * activations are stored row-major with the 16-B pieces of row m XOR-swizzled by m & 7,
@@ -63,20 +64,25 @@ constexpr int kThreads = 256;
 
 struct __attribute__((aligned(16))) P8Lds {
   uint8_t a[2][kBM * kQch];   // int8 activations of one chunk, row m at 128m, pieces swizzled
-  u4_t w[2][16 * 32];         // packed7 units of one chunk: 8 gate groups, then 8 up groups
+  u4_t w[16 * 32];            // packed7 units of one chunk: 8 gate groups, then 8 up groups
   u2_t b[8][4][64];           // decoded weights: [16-row n-tile][32-k step][lane] (8 int8)
-  uint32_t lut[256];          // level bytes of grid word g
+  uint32_t lut[16 * 256];     // (sign nibble << 8 | grid word) -> 4 signed levels
   uint32_t fac[kBM];          // per tile row: 2s + 1 of the chunk's 4 sub-blocks, a byte each
   float dp[kBM];              // per tile row: d * 4.0507 / 4
   float sxs[2][kBM];          // the chunk's activation scales of the tile's rows
 };
 
-// 4 signed levels: the level bytes l (0..127) negated where bit i of the 4-bit field sg is set
-// (byte-wise two's complement without carries between bytes)
-__device__ __forceinline__ uint32_t p8_signed(uint32_t l, uint32_t sg) {
-  const uint32_t m = ((sg * 0x00204081u) & 0x01010101u) * 0xFFu;   // byte i = 0xFF if bit i
-  const uint32_t a = l ^ m;
-  return ((a & 0x7F7F7F7Fu) + (m & 0x01010101u)) ^ (a & 0x80808080u);
+// Sign-folded level table: entry (sg << 8 | g) = the 4 level bytes of grid word g (0..127),
+// byte i negated where bit i of sg is set (byte-wise two's complement, no carries between
+// bytes).  Built once per workgroup: thread t fills entries t, t + 256, ...
+__device__ __forceinline__ void p8_build_table(uint32_t* tbl, const uint32_t* __restrict__ lut8, int t) {
+  const uint32_t l = lut8[t];
+#pragma unroll
+  for (uint32_t sg = 0; sg < 16; ++sg) {
+    const uint32_t m = ((sg * 0x00204081u) & 0x01010101u) * 0xFFu;   // byte i = 0xFF if bit i
+    const uint32_t a = l ^ m;
+    tbl[(sg << 8) | (uint32_t)t] = ((a & 0x7F7F7F7Fu) + (m & 0x01010101u)) ^ (a & 0x80808080u);
+  }
 }
 
 struct P8Args {
@@ -103,8 +109,8 @@ __device__ __forceinline__ void p8_dma(P8Lds& L, const P8Args& g, int c, int buf
     const int j = 2 * wave + jj, G = 2 * j + (lane >> 5);
     const u4_t* base = G < 8 ? g.w1 : g.w2;
     const u4_t* src = base + ((size_t)(8 * g.nt + (G & 7)) * g.nch + c) * 32 + (lane & 31);
-    __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(L.w[buf] + 64 * j), 16,
-                                     0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(L.w + 64 * j), 16, 0,
+                                     0);
   }
   if (wave < 2) {
     const float* src = g.sx + (size_t)(g.m0 + 64 * wave + lane) * g.nch + c;
@@ -116,19 +122,19 @@ __device__ __forceinline__ void p8_dma(P8Lds& L, const P8Args& g, int c, int buf
 // Decode the chunk's 512 units (2 per thread): unit u = (group G, row r, sub-block c) of tile
 // row R = 8 (G & 7) + r (+ 64 for the up groups) -> B tile [R / 16][c][16 cc + R % 16] for
 // lane-chunk cc (8 weights: grid words q & 0xFF, q >> 8; signs sidx bits 0-3, 4-6 + parity)
-__device__ __forceinline__ void p8_decode(P8Lds& L, int buf, int t) {
+__device__ __forceinline__ void p8_decode(P8Lds& L, int t) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int u = t + kThreads * i, G = u >> 5, r = (u >> 2) & 7, c = u & 3;
     const int R = 8 * (G & 7) + r + (G >= 8 ? 64 : 0);
-    const u4_t unit = L.w[buf][u];
+    const u4_t unit = L.w[u];
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
       const uint32_t qv = ((cc < 2 ? unit.x : unit.y) >> (16 * (cc & 1))) & 0xFFFFu;
       const uint32_t sidx = (unit.z >> (7 * cc)) & 0x7Fu;
       const uint32_t par = __builtin_popcount(sidx) & 1u;
-      const uint32_t v0 = p8_signed(L.lut[qv & 0xFFu], sidx & 0xFu);
-      const uint32_t v1 = p8_signed(L.lut[qv >> 8], (sidx >> 4) | (par << 3));
+      const uint32_t v0 = L.lut[((sidx & 0xFu) << 8) | (qv & 0xFFu)];
+      const uint32_t v1 = L.lut[(((sidx >> 4) | (par << 3)) << 8) | (qv >> 8)];
       L.b[R >> 4][c][16 * cc + (R & 15)] = u2_t{v0, v1};
     }
     reinterpret_cast<uint8_t*>(L.fac)[4 * R + c] = (uint8_t)(2u * (unit.z >> 28) + 1u);
@@ -159,7 +165,7 @@ __global__ __launch_bounds__(kThreads, 2) void p8w4_ffn_kernel(const u4_t* __res
   g.w1 = w1; g.w2 = w2; g.xq = xq; g.sx = sx; g.K = K;
   g.nch = K / kQch; g.m0 = mt * kBM; g.nt = nt;
 
-  L.lut[t] = lut8[t];
+  p8_build_table(L.lut, lut8, t);
   p8_dma(L, g, 0, 0, wave, lane);
 
   // the wave's n-tiles: gate 2wn, 2wn + 1, then the matching up tiles
@@ -179,7 +185,7 @@ __global__ __launch_bounds__(kThreads, 2) void p8w4_ffn_kernel(const u4_t* __res
     const int buf = c & 1;
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this chunk's DMA
     __syncthreads();
-    p8_decode(L, buf, t);
+    p8_decode(L, t);
     __syncthreads();
     if (c + 1 < g.nch) p8_dma(L, g, c + 1, buf ^ 1, wave, lane);
 
@@ -204,19 +210,33 @@ __global__ __launch_bounds__(kThreads, 2) void p8w4_ffn_kernel(const u4_t* __res
         A[s] = *reinterpret_cast<const long*>(L.a[buf] + 128 * row + 16 * slot + 8 * (kq & 1));
       }
       const f4_t sv = *reinterpret_cast<const f4_t*>(&L.sxs[buf][64 * wm + 16 * i + 4 * kq]);
+      // step s's four MFMAs (one per n-tile) are issued while step s - 1's results are
+      // rescaled: a result is read four MFMAs after it was issued, with no wait states
+      i4_t acc[4], pr[2][4];
+#pragma unroll
+      for (int s = 0; s <= 4; ++s) {
+        if (s < 4) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) pr[s & 1][q] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[s], B[q][s], zero, 0, 0, 0);
+        }
+        if (s > 0) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int fs = (int)((f[q] >> (8 * (s - 1))) & 0xFFu);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int v = fs * ((pr[(s - 1) & 1][q][r] << 8) >> 8);   // 24-bit operands: v_mad_i32_i24
+              acc[q][r] = s == 1 ? v : acc[q][r] + v;
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        i4_t acc = zero;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int fs = (int)((f[q] >> (8 * s)) & 0xFFu);
-          const i4_t pr = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[s], B[q][s], zero, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[r] += fs * ((pr[r] << 8) >> 8);   // 24-bit operands: v_mad_i32_i24
-        }
         const float dq = L.dp[16 * jt[q] + col];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) facc[i][q][r] = __builtin_fmaf(sv[r] * dq, (float)acc[r], facc[i][q][r]);
+        for (int r = 0; r < 4; ++r) facc[i][q][r] = __builtin_fmaf(sv[r] * dq, (float)acc[q][r], facc[i][q][r]);
       }
     }
   }
