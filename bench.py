@@ -30,6 +30,9 @@ weights, all resident, so every step streams them from HBM), captured once in a 
 replayed.  Weights are seeded random bytes with sane d fields (the timing does not depend on the
 values; parity is the tests' business).  Reported as weight-streaming GB/s for the step.
 
+``formats`` times the load-time repacking on the GPU (raw GGUF IQ3_XXS rows of config 2's gate
+matrix -> packed rows -> packed7) in GB/s of bytes read + written.
+
 ``moe`` is config 5: the whole MoE layer (top-8 from N(0,1) logits, sort, grouped IQ4_XS
 gate+up and down, shared expert, combine) at M=11 and M=2048, seeded expert weights, the
 layer's six launches per step captured in one HIP graph; each step reads a different copy of
@@ -61,6 +64,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-formats", action="store_true", help="skip the load-time repacking leg")
     ap.add_argument("--ms", default="1,4,8,11", help="activation widths to time")
     ap.add_argument("--gemm-m", type=int, default=2048, help="prefill rows for the GEMM leg (0: skip)")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE leg")
@@ -181,6 +185,21 @@ def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup):
                                   "unit": "TOP/s", "frac": round(to_w4 / PEAK_I8_TOPS, 4),
                                   "kernel": "p8_quant_kernel + p8w4_ffn_kernel"}},
     }
+
+
+def formats_leg(ops, synth, torch, dev, steps, warmup):
+    """Load-time repacking of config 2's gate matrix on the GPU (raw GGUF rows -> packed rows
+    -> packed7): HBM bytes moved (read + write) per second."""
+    N, K = 17408, 5120
+    raw = torch.from_numpy(synth.iq3xxs_raw(synth.config_rng(2), N, K).reshape(-1)).to(dev)
+    packed = torch.empty_like(raw)
+    p7 = torch.empty(N * K // 2, dtype=torch.uint8, device=dev)
+    t_rows = time_call(lambda s: ops.pack_iq3_rows(raw, packed, N, K, stream=s), steps, warmup, torch)
+    t_p7 = time_call(lambda s: ops.pack_w7(packed, p7, N, K, stream=s), steps, warmup, torch)
+    nb = raw.numel()
+    return {"workload": f"IQ3_XXS {N}x{K} ({nb} B): raw rows -> packed rows -> packed7",
+            "pack_rows_ms": round(t_rows, 4), "pack_rows_gbs": round(2 * nb / (t_rows * 1e-3) / 1e9, 1),
+            "pack_w7_ms": round(t_p7, 4), "pack_w7_gbs": round((nb + p7.numel()) / (t_p7 * 1e-3) / 1e9, 1)}
 
 
 def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
@@ -435,6 +454,8 @@ def main():
                                max(1, args.warmup // 5))
     if not args.no_sweep:
         out["sweep"] = sweep_leg(ops, formats, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5))
+    if not args.no_formats:
+        out["formats"] = formats_leg(ops, synth, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5))
     if not args.no_moe:
         out["moe"] = moe_leg(ops, formats, synth, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5))
     if not args.no_cpu:

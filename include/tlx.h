@@ -31,6 +31,7 @@ extern "C" {
 #define TLX_E_ALIGN (-2)   /* a pointer or row stride is not aligned as the layout needs */
 #define TLX_E_NODEV (-3)   /* no usable gfx950 device */
 #define TLX_E_NOMEM (-4)   /* the library workspace could not be allocated */
+#define TLX_E_TRUNC (-5)   /* tlx_gguf_parse: the image ends inside the header; pass more bytes */
 
 /* Weight layouts (row-major over output rows). */
 #define TLX_LAYOUT_RAW 0     /* GGUF blocks as stored in the file */
@@ -181,6 +182,38 @@ int tlx_p8_quant(const uint16_t* x16, int8_t* xq, float* sx, int32_t* rs, int M,
  * K % 256 == 0. */
 int tlx_p8w4_ffn(const void* w1u, const void* w2u, const int8_t* lut8, const int8_t* xq, const float* sx,
                  uint16_t* out16, int M, int N, int K, int layout, void* stream);
+
+/* ---- On-disk formats.
+ * GGUF v3 tensor table, replaces parse_gguf (engine/engine0.py:25-51) and tnbytes (:53-55):
+ * parses the image head[0..len) of a file's start (magic, version, counts, the key/value
+ * section skipped, the tensor table).  Fills *n_tensors, *data_start (the end of the tensor
+ * table rounded up to 32 bytes, as the reference) and up to max_tensors entries of tensors
+ * (tensors may be NULL to count only).  dims are in GGUF order: dims[0] is the row length
+ * ("[in, out]").  nbytes is the reference's tnbytes, 0 for a type it does not know.  Host
+ * only; TLX_E_TRUNC when the image is too short (read more of the file and call again),
+ * TLX_E_ARG for a malformed file or a name longer than 127 bytes. */
+#define TLX_GGUF_MAX_DIMS 4
+typedef struct tlx_gguf_tensor {
+  char name[128];
+  int32_t type;       /* ggml type code (18 IQ3_XXS, 14 Q6_K, 13 Q5_K, 12 Q4_K, 23 IQ4_XS, ...) */
+  uint32_t n_dims;
+  uint64_t dims[TLX_GGUF_MAX_DIMS];
+  uint64_t offset;    /* bytes from data_start */
+  uint64_t nbytes;
+} tlx_gguf_tensor;
+int tlx_gguf_parse(const void* head, uint64_t len, uint64_t* data_start, int64_t* n_tensors,
+                   tlx_gguf_tensor* tensors, int64_t max_tensors);
+
+/* Repackers (device to device, byte permutations):
+ * raw IQ3_XXS rows [N][K/256][98] -> packed rows [qs 64NB][sw 32NB][d 2NB], replaces pack_iq3
+ * (engine/pack_w1c.py:20-31); */
+int tlx_pack_iq3_rows(const void* raw, void* packed, int N, int K, void* stream);
+/* raw Q6_K rows [N][K/256][210] -> padded blocks [pad2][d2][sc16][ql128][qh64], replaces pack_q6
+ * (engine/pack_w1c.py:33-45, which fixes K = 5120); */
+int tlx_pack_q6_pad(const void* raw, void* padded, int N, int K, void* stream);
+/* packed IQ3_XXS rows -> packed7 units [N/8][K/128][32][16 B], replaces pack_tensor
+ * (engine/pack_w7.py:40-75); N % 8 == 0. */
+int tlx_pack_w7(const void* packed, void* p7, int N, int K, void* stream);
 
 /* ---- MoE grouped-expert path (256 routed experts + 1 shared, hidden 2048, expert FF 512,
  * top-8; IQ4_XS weights).  Pairs are position-major, rank ascending: pair = 8*pos + rank.

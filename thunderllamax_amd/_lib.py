@@ -16,6 +16,8 @@ TLX_OK = 0
 TLX_E_ARG = -1
 TLX_E_ALIGN = -2
 TLX_E_NODEV = -3
+TLX_E_NOMEM = -4
+TLX_E_TRUNC = -5
 LAYOUT_RAW = 0
 LAYOUT_PACKED = 1
 LAYOUT_PACK7 = 2
@@ -51,6 +53,10 @@ SIGNATURES = {
     "tlx_pfg3_iq3d": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_pfg3_iq3o": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_p8_quant": [_p, _p, _p, _p, _i, _i, _p],
+    "tlx_gguf_parse": [_p, ctypes.c_uint64, _p, _p, _p, _i64],
+    "tlx_pack_iq3_rows": [_p, _p, _i, _i, _p],
+    "tlx_pack_q6_pad": [_p, _p, _i, _i, _p],
+    "tlx_pack_w7": [_p, _p, _i, _i, _p],
     "tlx_p8w4_ffn": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_moe_topk": [_p, _p, _p, _i, _p],
     "tlx_moe_route": [_p, _p, _p, _p, _p, _p, _i, _p],

@@ -12,6 +12,7 @@ extern "C" const char* tlx_strerror(int code) {
     case TLX_E_ALIGN: return "pointer or row stride misaligned for this layout";
     case TLX_E_NODEV: return "no usable gfx950 device";
     case TLX_E_NOMEM: return "the library workspace could not be allocated";
+    case TLX_E_TRUNC: return "the GGUF image ends inside the header";
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown tlx error";
   }
 }

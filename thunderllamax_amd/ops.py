@@ -247,6 +247,35 @@ def pfg3_ffn(wg, wu, gridf, x16, out16, layout=LAYOUT_PACK7, stream=None):
     return out16
 
 
+# ------------------------------------------------------------------ repackers (device to device)
+def pack_iq3_rows(raw, packed, N, K, stream=None):
+    """Raw IQ3_XXS rows [N][K/256][98 B] -> packed rows [qs][sw][d] (pack_w1c.pack_iq3)."""
+    nbytes = N * 98 * (K // 256)
+    _need(raw, nbytes, "raw")
+    _need(packed, nbytes, "packed")
+    _dev(raw, packed)
+    call("tlx_pack_iq3_rows", raw.data_ptr(), packed.data_ptr(), N, K, _stream(stream))
+    return packed
+
+
+def pack_q6_pad(raw, padded, N, K, stream=None):
+    """Raw Q6_K rows [N][K/256][210 B] -> padded 212-B blocks (pack_w1c.pack_q6)."""
+    _need(raw, N * 210 * (K // 256), "raw")
+    _need(padded, N * 212 * (K // 256), "padded")
+    _dev(raw, padded)
+    call("tlx_pack_q6_pad", raw.data_ptr(), padded.data_ptr(), N, K, _stream(stream))
+    return padded
+
+
+def pack_w7(packed, p7, N, K, stream=None):
+    """Packed IQ3_XXS rows -> packed7 units [N/8][K/128][32][16 B] (pack_w7.pack_tensor)."""
+    _need(packed, N * 98 * (K // 256), "packed")
+    _need(p7, _pack7(N, K), "p7")
+    _dev(packed, p7)
+    call("tlx_pack_w7", packed.data_ptr(), p7.data_ptr(), N, K, _stream(stream))
+    return p7
+
+
 def p8_quant(x16, xq, sx, rs, stream=None):
     """Per (row, 128-k chunk) int8 quantization of fp16 activations (pfk_q8: kernel(x, xq, sx, rs))."""
     M, K = x16.shape
