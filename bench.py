@@ -30,6 +30,9 @@ weights, all resident, so every step streams them from HBM), captured once in a 
 replayed.  Weights are seeded random bytes with sane d fields (the timing does not depend on the
 values; parity is the tests' business).  Reported as weight-streaming GB/s for the step.
 
+``producers`` times the residual-add + RMSNorm producer in front of ffn8 at M=11, alone, then
+followed by ffn8, and fused with it in one entry point (graph replays).
+
 ``formats`` times the load-time repacking on the GPU (raw GGUF IQ3_XXS rows of config 2's gate
 matrix -> packed rows -> packed7) in GB/s of bytes read + written.
 
@@ -64,7 +67,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-formats", action="store_true", help="skip the load-time repacking leg")
+    ap.add_argument("--no-formats", action="store_true", help="skip the producer and load-time repacking legs")
     ap.add_argument("--ms", default="1,4,8,11", help="activation widths to time")
     ap.add_argument("--gemm-m", type=int, default=2048, help="prefill rows for the GEMM leg (0: skip)")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE leg")
@@ -185,6 +188,45 @@ def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup):
                                   "unit": "TOP/s", "frac": round(to_w4 / PEAK_I8_TOPS, 4),
                                   "kernel": "p8_quant_kernel + p8w4_ffn_kernel"}},
     }
+
+
+def producers_leg(ops, formats, synth, torch, dev, steps, warmup, M=11):
+    """The activation producer before the FFN GEMV (hh{M}: residual add + RMSNorm -> fp16) at
+    config 2's D=5120, alone, followed by ffn8, and fused with it (tlx_ffn8_hh), as graph
+    replays over rotated FFN weights."""
+    K, N = 5120, 17408
+    rng = synth.config_rng(2)
+    copies = [(torch.from_numpy(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, N, K), K)).to(dev),
+               torch.from_numpy(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, N, K), K)).to(dev))
+              for _ in range(max(1, -(-ROT_BYTES // (2 * N * 98 * (K // 256)))))]
+    gridf = formats.gridf_tensor(dev)
+    x = torch.randn(M, K, device=dev)
+    a = torch.randn(M, K, device=dev).half()
+    nw = torch.ones(K, device=dev)
+    hh = torch.empty(M, K, device=dev)
+    hhx = torch.empty(M, K, dtype=torch.float16, device=dev)
+    g = torch.empty(M, N, dtype=torch.float16, device=dev)
+    it = [0]
+
+    def pick():
+        it[0] += 1
+        return copies[it[0] % len(copies)]
+
+    def sep(s):
+        wg, wu = pick()
+        ops.add_rms_f16(x, a, nw, hh, hhx, stream=s)
+        ops.ffn8(wg, wu, gridf, hhx, g, stream=s)
+
+    def fused(s):
+        wg, wu = pick()
+        ops.ffn8_hh(wg, wu, gridf, x, a, nw, hh, hhx, g, stream=s)
+
+    t_norm = time_graph(lambda s: ops.add_rms_f16(x, a, nw, hh, hhx, stream=s), steps, warmup, torch)
+    t_sep = time_graph(sep, steps, warmup, torch)
+    t_fused = time_graph(fused, steps, warmup, torch)
+    return {"workload": f"hh{{M}} producer (D={K}) + ffn8 (N=2x{N}), M={M}",
+            "add_rms_us": round(t_norm * 1e3, 2), "add_rms_then_ffn8_us": round(t_sep * 1e3, 2),
+            "ffn8_hh_us": round(t_fused * 1e3, 2)}
 
 
 def formats_leg(ops, synth, torch, dev, steps, warmup):
@@ -454,6 +496,9 @@ def main():
                                max(1, args.warmup // 5))
     if not args.no_sweep:
         out["sweep"] = sweep_leg(ops, formats, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5))
+    if not args.no_formats:
+        out["producers"] = producers_leg(ops, formats, synth, torch, dev, max(3, args.steps // 5),
+                                         max(1, args.warmup // 5))
     if not args.no_formats:
         out["formats"] = formats_leg(ops, synth, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5))
     if not args.no_moe:

@@ -183,6 +183,22 @@ int tlx_p8_quant(const uint16_t* x16, int8_t* xq, float* sx, int32_t* rs, int M,
 int tlx_p8w4_ffn(const void* w1u, const void* w2u, const int8_t* lut8, const int8_t* xq, const float* sx,
                  uint16_t* out16, int M, int N, int K, int layout, void* stream);
 
+/* ---- Activation producers either side of the GEMVs (fp32 residual stream, fp16 GEMV input).
+ * RMSNorm, replaces k0n{M} / k0_norm (engine/k0n11.cu:88-103, engine/gdn_block.cu:30-40):
+ * xh[m] = half((x[m] * r) * nw), r = rsqrt(sum(x[m]^2) / D + 1e-6).  D % 8 == 0. */
+int tlx_rms_f16(const float* x, const float* nw, uint16_t* xh, int M, int D, void* stream);
+/* Residual add + RMSNorm, replaces hh{M} / k3m_hh (engine/hh11.cu:88-107,
+ * engine/gdn_block.cu:258-276): hh = x + float(a) (fp32, exact), hhx = half((hh * r) * nw). */
+int tlx_add_rms_f16(const float* x, const uint16_t* a, const float* nw, float* hh, uint16_t* hhx, int M,
+                    int D, void* stream);
+/* hh{M} fused with ffn8: tlx_add_rms_f16(x, attn_out, nw2, hh, hhx) then tlx_ffn8(wg, wu, gridf,
+ * hhx, gact) with the same results bit for bit; from M = 6 on the producer also writes the
+ * GEMV's tile-ordered activation copy, so the call is two launches instead of three.  Same
+ * workspace rules as the IQ3_XXS GEMVs.  K is the model dimension D. */
+int tlx_ffn8_hh(const void* wg, const void* wu, const float* gridf, const float* x, const uint16_t* attn_out,
+                const float* nw2, float* hh, uint16_t* hhx_f16, uint16_t* gact_f16, int M, int N, int K,
+                int layout, void* stream);
+
 /* ---- On-disk formats.
  * GGUF v3 tensor table, replaces parse_gguf (engine/engine0.py:25-51) and tnbytes (:53-55):
  * parses the image head[0..len) of a file's start (magic, version, counts, the key/value

@@ -54,6 +54,9 @@ SIGNATURES = {
     "tlx_pfg3_iq3o": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_p8_quant": [_p, _p, _p, _p, _i, _i, _p],
     "tlx_gguf_parse": [_p, ctypes.c_uint64, _p, _p, _p, _i64],
+    "tlx_rms_f16": [_p, _p, _p, _i, _i, _p],
+    "tlx_add_rms_f16": [_p, _p, _p, _p, _p, _i, _i, _p],
+    "tlx_ffn8_hh": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_pack_iq3_rows": [_p, _p, _i, _i, _p],
     "tlx_pack_q6_pad": [_p, _p, _i, _i, _p],
     "tlx_pack_w7": [_p, _p, _i, _i, _p],

@@ -83,6 +83,12 @@ static inline int tlx_cu_count() {
 // device and kept until the process ends; calls that overlap in time on one device must not
 // both use it.
 constexpr size_t kWsBytes = size_t(4) << 20;
+
+// RMSNorm producer (tlx_norm.hip): add form (hh = x + a) when add; optionally also writes the
+// IQ3_XXS GEMVs' tile-ordered activation copy xt (M <= 16)
+int tlx_rms_launch(bool add, const float* x, const uint16_t* a, const float* nw, float* hh, uint16_t* xh,
+                   _Float16* xt, int M, int D, hipStream_t st);
+int tlx_rms_check(const float* x, const uint16_t* a, const float* nw, const float* hh, const uint16_t* xh, int M, int D);
 int tlx_workspace(void** ws);
 
 // Internal entry points shared by the fused attention projections (tlx_attn.hip).  With

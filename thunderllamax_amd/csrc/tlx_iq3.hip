@@ -224,9 +224,9 @@ __global__ __launch_bounds__(256) void iq3_xt_kernel(const _Float16* __restrict_
 template <int NMAT, int EPI>
 int iq3_launch(Iq3Launch& a, int tiles, hipStream_t st) {
   const int nb = a.K >> 8;
-  a.xt = 0;
-  // same values, same arithmetic: only the activation loads change (larger K reads x directly)
-  if (a.M >= kXtMinM && (size_t)a.K * 16 * 2 <= kWsBytes) {
+  // same values, same arithmetic: only the activation loads change (larger K reads x directly);
+  // a.xt set by the caller: a.x already is the tile-ordered copy (written by a producer)
+  if (!a.xt && a.M >= kXtMinM && (size_t)a.K * 16 * 2 <= kWsBytes) {
     void* ws = nullptr;
     const int rc = tlx_workspace(&ws);
     if (rc != TLX_OK) return rc;
@@ -342,6 +342,36 @@ extern "C" int tlx_ffn8(const void* wg, const void* wu, const float* gridf, cons
   a.x = (const _Float16*)hhx_f16;
   a.M = M;
   a.K = K;
+  return iq3_launch<2, EPI_SWIGLU>(a, tiles_of(N), (hipStream_t)stream);
+}
+
+extern "C" int tlx_ffn8_hh(const void* wg, const void* wu, const float* gridf, const float* x,
+                           const uint16_t* attn_out, const float* nw2, float* hh, uint16_t* hhx_f16,
+                           uint16_t* gact_f16, int M, int N, int K, int layout, void* stream) {
+  int rc = iq3_check(wg, M, N, K, layout);
+  if (rc == TLX_OK) rc = iq3_check(wu, M, N, K, layout);
+  if (rc == TLX_OK) rc = attn_out == nullptr || hh == nullptr ? TLX_E_ARG : tlx_rms_check(x, attn_out, nw2, hh, hhx_f16, M, K);
+  TLX_RET_IF(rc != TLX_OK, rc);
+  TLX_RET_IF(!tlx_aligned(gridf, 16), TLX_E_ALIGN);
+  Iq3Launch a{};
+  a.seg[0] = Iq3Seg{(const uint8_t*)wg, (const uint8_t*)wu, gact_f16, nullptr, N, 0};
+  a.raw = layout == TLX_LAYOUT_RAW;
+  a.nseg = 1;
+  a.gridf = gridf;
+  a.x = (const _Float16*)hhx_f16;
+  a.M = M;
+  a.K = K;
+  _Float16* xt = nullptr;
+  if (M >= kXtMinM && (size_t)K * 16 * 2 <= kWsBytes) {   // the producer writes the GEMV's copy
+    void* ws = nullptr;
+    rc = tlx_workspace(&ws);
+    TLX_RET_IF(rc != TLX_OK, rc);
+    xt = reinterpret_cast<_Float16*>(ws);
+    a.x = xt;
+    a.xt = 1;
+  }
+  rc = tlx_rms_launch(true, x, attn_out, nw2, hh, hhx_f16, xt, M, K, (hipStream_t)stream);
+  TLX_RET_IF(rc != TLX_OK, rc);
   return iq3_launch<2, EPI_SWIGLU>(a, tiles_of(N), (hipStream_t)stream);
 }
 

@@ -90,6 +90,46 @@ def ffn8(wg, wu, gridf, hhx, gact, layout=LAYOUT_PACKED, stream=None):
     return gact
 
 
+def rms_f16(x, nw, xh, stream=None):
+    """xh[m] = half((x[m] * r) * nw), r = rsqrt(mean(x[m]^2) + 1e-6)   (k0n{M} / k0_norm)."""
+    M, D = x.shape
+    _need(nw, D * 4, "nw")
+    _need(xh, M * D * 2, "xh")
+    _dev(x, nw, xh)
+    call("tlx_rms_f16", x.data_ptr(), nw.data_ptr(), xh.data_ptr(), M, D, _stream(stream))
+    return xh
+
+
+def add_rms_f16(x, a, nw, hh, hhx, stream=None):
+    """hh = x + float(a); hhx[m] = half((hh[m] * r) * nw)   (hh{M} / k3m_hh)."""
+    M, D = x.shape
+    _need(a, M * D * 2, "a")
+    _need(nw, D * 4, "nw")
+    _need(hh, M * D * 4, "hh")
+    _need(hhx, M * D * 2, "hhx")
+    _dev(x, a, nw, hh, hhx)
+    call("tlx_add_rms_f16", x.data_ptr(), a.data_ptr(), nw.data_ptr(), hh.data_ptr(), hhx.data_ptr(), M, D,
+         _stream(stream))
+    return hh, hhx
+
+
+def ffn8_hh(wg, wu, gridf, x, attn_out, nw2, hh, hhx, gact, layout=LAYOUT_PACKED, stream=None):
+    """hh{M} + ffn8 in one call: hh = x + float(attn_out), hhx = norm(hh), gact = ffn8(hhx)."""
+    M, K, N = x.shape[0], x.shape[1], gact.shape[-1]
+    _need(wg, _iq3_rows(N, K), "wg")
+    _need(wu, _iq3_rows(N, K), "wu")
+    _need(gridf, 4096, "gridf")
+    _need(attn_out, M * K * 2, "attn_out")
+    _need(nw2, K * 4, "nw2")
+    _need(hh, M * K * 4, "hh")
+    _need(hhx, M * K * 2, "hhx")
+    _need(gact, M * N * 2, "gact")
+    _dev(wg, wu, gridf, x, attn_out, nw2, hh, hhx, gact)
+    call("tlx_ffn8_hh", wg.data_ptr(), wu.data_ptr(), gridf.data_ptr(), x.data_ptr(), attn_out.data_ptr(),
+         nw2.data_ptr(), hh.data_ptr(), hhx.data_ptr(), gact.data_ptr(), M, N, K, layout, _stream(stream))
+    return gact
+
+
 def down8(wd, gridf, gact, hh, y, layout=LAYOUT_PACKED, stream=None):
     """y[m] = hh[m] + float(half(Wd·gact[m]))   (down8 / down8nw32_{M})."""
     M, K, N = _mk(gact), gact.shape[-1], y.shape[-1]
