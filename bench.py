@@ -38,7 +38,8 @@ matrix -> packed rows -> packed7) in GB/s of bytes read + written.
 
 ``moe`` is config 5: the whole MoE layer (top-8 from N(0,1) logits, sort, grouped IQ4_XS
 gate+up and down, shared expert, combine) at M=11 and M=2048, seeded expert weights, the
-layer's six launches per step captured in one HIP graph; each step reads a different copy of
+layer's launches per step captured in one HIP graph, the shared expert on a second stream
+(``ms_shared_not_overlapped``: the same layer with every launch on one stream); each step reads a different copy of
 the 257 expert slabs (3 copies, 1.3 GB), so at M=11 the weights come from HBM.
 """
 import argparse
@@ -264,35 +265,24 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
         logits = torch.from_numpy(rng.standard_normal((P, E)).astype(np.float32)).to(dev)
         sg = torch.rand(P, device=dev)
         hres = torch.randn(P, H, device=dev)
-        eids = torch.empty(P, 8, dtype=torch.int16, device=dev)
-        gates = torch.empty(P, 8, device=dev)
-        eoff = torch.empty(E + 1, dtype=torch.int32, device=dev)
-        plist = torch.empty(np_, dtype=torch.int16, device=dev)
-        items = torch.empty(ops.moe_max_items(np_), dtype=torch.int32, device=dev)
-        nitp = torch.empty(1, dtype=torch.int32, device=dev)
-        act = torch.empty(np_, F, device=dev)
-        parts = torch.empty(np_, H, dtype=torch.float16, device=dev)
-        sact = torch.empty(P, F, device=dev)
-        shared = torch.empty(P, H, device=dev)
+        sc = ops.MoeScratch(P, dev)
         y = torch.empty(P, H, device=dev)
         state = {"i": 0}
 
-        def layer(st):
+        def layer(st, overlap):
             c = copies[state["i"] % len(copies)]
             state["i"] += 1
-            ops.moe_topk(logits, eids, gates, stream=st)
-            ops.moe_sort(eids, eoff, plist, items, nitp, stream=st)
-            ops.moe_up4(c["ptbl"], eoff, plist, items, nitp, x, iq4nl, act, stream=st)
-            ops.moe_dn4(c["ptbl_dn"], eoff, plist, items, nitp, act, iq4nl, parts, stream=st)
-            ops.moe_shared(c["ptbl_sh"], x, iq4nl, sact, shared, stream=st)
-            ops.moe_combine(parts, gates, sg, shared, hres, y, stream=st)
+            ops.moe_layer(logits, sg, x, hres, y, c["ptbl"], c["ptbl_dn"], c["ptbl_sh"], iq4nl, sc, stream=st,
+                          overlap_shared=overlap)
 
-        t = time_graph(layer, steps, warmup, torch)
-        hit = int((torch.diff(eoff) > 0).sum().item())
+        t_seq = time_graph(lambda st: layer(st, False), steps, warmup, torch)
+        t = time_graph(lambda st: layer(st, True), steps, warmup, torch)
+        hit = int((torch.diff(sc.eoff) > 0).sum().item())
         flops = 2.0 * 3 * F * H * (8 * P + P)
         wbytes = (hit + 1) * 1671168
         out[f"M{P}"] = {"ms": round(t, 4), "tflops": round(flops / (t * 1e-3) / 1e12, 2),
-                        "experts_hit": hit, "weight_gbs": round(wbytes / (t * 1e-3) / 1e9, 1)}
+                        "experts_hit": hit, "weight_gbs": round(wbytes / (t * 1e-3) / 1e9, 1),
+                        "ms_shared_not_overlapped": round(t_seq, 4)}
     return out
 
 

@@ -235,3 +235,37 @@ def test_moe_bad_arguments(gpu, experts):
                     torch.zeros(ops.moe_max_items(8), dtype=torch.int32, device=gpu),
                     torch.zeros(1, dtype=torch.int32, device=gpu), torch.zeros(1, 2048, device=gpu),
                     experts["iq4nl"], torch.zeros(8, 512, device=gpu))
+
+
+def test_moe_layer_overlapped_equals_sequential(gpu, experts):
+    """ops.moe_layer with the shared expert on a second stream gives the sequential calls'
+    results bit for bit, eagerly and in every replay of a captured graph (eager work and
+    synchronizations between the replays)."""
+    print("[case] moe_layer overlapped vs sequential P=11 / 300", flush=True)
+    for P in (11, 300):
+        rng = np.random.default_rng(31 + P)
+        x, logits, sg, hres = _inputs(rng, P)
+        ref = _run_layer(gpu, experts, x, logits, sg, hres)
+        dx, dl = torch.from_numpy(x).to(gpu), torch.from_numpy(logits).to(gpu)
+        dsg, dh = torch.from_numpy(sg).to(gpu), torch.from_numpy(hres).to(gpu)
+        sc = ops.MoeScratch(P, gpu)
+        y = torch.empty(P, moe.HID, dtype=torch.float32, device=gpu)
+        args = (dl, dsg, dx, dh, y, experts["ptbl"], experts["ptbl_dn"], experts["ptbl_sh"], experts["iq4nl"], sc)
+        ops.moe_layer(*args)
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy(), ref["y"])
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            ops.moe_layer(*args, stream=st)
+        torch.cuda.current_stream().wait_stream(st)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            ops.moe_layer(*args, stream=st)
+        for _ in range(3):
+            y.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(y.cpu().numpy(), ref["y"])

@@ -692,6 +692,10 @@ extern "C" int tlx_moe_max_items(int np) { return moe_max_items(np); }
 // pair counts up to this use the GEMV form (a few tokens per expert); larger ones the GEMM
 constexpr int kGvMaxPairs = 2048;
 
+// work items the sort can produce for np pairs: at most ceil(np / 64) + 256 (one partial
+// chunk per expert), and at most np (every item holds a pair) -- the small-batch grids use both
+int moe_gv_items(int np) { return min(np, moe_max_items(np)); }
+
 // items (expert chunks) rounded up to a multiple of 8 (one per XCD), times the stripes
 template <int KIND>
 int moe_pf_grid(int nitems) { return (nitems + 7) / 8 * 8 * moe_pf_stripes<KIND>(); }
@@ -708,7 +712,7 @@ extern "C" int tlx_moe_up4(const uint64_t* ptbl, const int* eoff, const uint16_t
   TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(xs, 16), TLX_E_ALIGN);
   if (np <= kGvMaxPairs) {
-    moe_gv_kernel<MOE_UP><<<moe_gv_grid<MOE_UP>(moe_max_items(np)), 256, 0, (hipStream_t)stream>>>(
+    moe_gv_kernel<MOE_UP><<<moe_gv_grid<MOE_UP>(moe_gv_items(np)), 256, 0, (hipStream_t)stream>>>(
         ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, 0);
     return tlx_launch_status();
   }
@@ -723,7 +727,7 @@ extern "C" int tlx_moe_dn4(const uint64_t* ptbl_dn, const int* eoff, const uint1
   TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(act, 16) || !tlx_aligned(parts, 16), TLX_E_ALIGN);
   if (np <= kGvMaxPairs) {
-    moe_gv_kernel<MOE_DN><<<moe_gv_grid<MOE_DN>(moe_max_items(np)), 256, 0, (hipStream_t)stream>>>(
+    moe_gv_kernel<MOE_DN><<<moe_gv_grid<MOE_DN>(moe_gv_items(np)), 256, 0, (hipStream_t)stream>>>(
         ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
     return tlx_launch_status();
   }

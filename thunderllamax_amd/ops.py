@@ -466,3 +466,52 @@ def moe_combine(parts, gates, sg, shared, hres, y, stream=None):
     _dev(parts, gates, sg, shared, hres, y)
     call("tlx_moe_combine", parts.data_ptr(), gates.data_ptr(), sg.data_ptr(), shared.data_ptr(), hres.data_ptr(),
          y.data_ptr(), y.shape[0], _stream(stream))
+
+
+class MoeScratch:
+    """Per-call buffers of one MoE layer over P positions (allocated once, like the reference's
+    Bufs): router ids / gates, the sort's bins and items, routed and shared activations, parts."""
+
+    def __init__(self, P, device="cuda"):
+        np_ = 8 * P
+        self.P = P
+        self.eids = torch.empty(P, 8, dtype=torch.int16, device=device)
+        self.gates = torch.empty(P, 8, dtype=torch.float32, device=device)
+        self.eoff = torch.empty(257, dtype=torch.int32, device=device)
+        self.plist = torch.empty(np_, dtype=torch.int16, device=device)
+        self.items = torch.empty(moe_max_items(np_), dtype=torch.int32, device=device)
+        self.nitp = torch.empty(1, dtype=torch.int32, device=device)
+        self.act = torch.empty(np_, 512, dtype=torch.float32, device=device)
+        self.parts = torch.empty(np_, 2048, dtype=torch.float16, device=device)
+        self.sact = torch.empty(P, 512, dtype=torch.float32, device=device)
+        self.shared = torch.empty(P, 2048, dtype=torch.float32, device=device)
+
+
+_SIDE_STREAMS = {}
+
+
+def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, stream=None, overlap_shared=True):
+    """One MoE layer, the sequence of build_seq7 (engine/mm/MM_P7_lib.py:449-511): top-8 from
+    the router logits, sort, grouped gate+up, grouped down, shared expert, combine into y.
+    With overlap_shared the shared expert (which needs neither the routing nor the routed
+    experts) runs on a second stream, joined before the combine; the work and the results are
+    the same, and a graph captured from the call keeps the two branches concurrent."""
+    sc = scratch
+    cur = stream if isinstance(stream, torch.cuda.Stream) else torch.cuda.current_stream()
+    side = None
+    if overlap_shared:
+        side = _SIDE_STREAMS.get(cur.device)
+        if side is None:
+            side = _SIDE_STREAMS[cur.device] = torch.cuda.Stream(device=cur.device)
+        side.wait_stream(cur)
+        moe_shared(ptbl_sh, xs, iq4nl, sc.sact, sc.shared, stream=side)
+    moe_topk(logits, sc.eids, sc.gates, stream=cur)
+    moe_sort(sc.eids, sc.eoff, sc.plist, sc.items, sc.nitp, stream=cur)
+    moe_up4(ptbl, sc.eoff, sc.plist, sc.items, sc.nitp, xs, iq4nl, sc.act, stream=cur)
+    moe_dn4(ptbl_dn, sc.eoff, sc.plist, sc.items, sc.nitp, sc.act, iq4nl, sc.parts, stream=cur)
+    if side is None:
+        moe_shared(ptbl_sh, xs, iq4nl, sc.sact, sc.shared, stream=cur)
+    else:
+        cur.wait_stream(side)
+    moe_combine(sc.parts, sc.gates, sg, sc.shared, hres, y, stream=cur)
+    return y
