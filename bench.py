@@ -73,13 +73,16 @@ def parse():
     ap.add_argument("--gemm-m", type=int, default=2048, help="prefill rows for the GEMM leg (0: skip)")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the decode-step sweep leg")
+    ap.add_argument("--layout", default="tiled", choices=("tiled", "packed"),
+                    help="IQ3_XXS weight layout of the headline ffn8 leg (the other one is "
+                         "reported under per_m_other_layout)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="end with one device-to-device copy of this many MiB (a reference "
                          "dispatch of known size for calibrating memory counters)")
     return ap.parse_args()
 
 
-def time_ffn(ops, wsets, gridf, x, gact, steps, warmup, torch):
+def time_ffn(ops, wsets, gridf, x, gact, steps, warmup, torch, layout=1):
     """Average ms per ffn8 call over `steps` calls captured in one HIP graph (host launch gaps
     excluded: a decode step replays its launches as a graph), after `warmup` eager calls and
     one untimed replay; HIP events on the replay stream."""
@@ -89,14 +92,14 @@ def time_ffn(ops, wsets, gridf, x, gact, steps, warmup, torch):
     with torch.cuda.stream(st):
         for i in range(max(warmup, 1)):   # eager: one-time set-up happens outside the capture
             wg, wu = wsets[i % n]
-            ops.ffn8(wg, wu, gridf, x, gact, stream=st)
+            ops.ffn8(wg, wu, gridf, x, gact, layout=layout, stream=st)
     torch.cuda.current_stream().wait_stream(st)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=st):
         for i in range(steps):
             wg, wu = wsets[i % n]
-            ops.ffn8(wg, wu, gridf, x, gact, stream=st)
+            ops.ffn8(wg, wu, gridf, x, gact, layout=layout, stream=st)
     g.replay()   # replays on the current stream
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
@@ -445,17 +448,36 @@ def main():
         pu = formats.iq3_pack_rows(synth.iq3xxs_raw(rng, N, K), K)
         wsets.append((torch.from_numpy(pg).to(dev), torch.from_numpy(pu).to(dev)))
     gridf = formats.gridf_tensor(dev)
+    # the same weights as tile-major records (repacked on the GPU; same bytes per weight)
+    tsets = []
+    tbytes = (N + 15) // 16 * 16 * 102 * (K // 256)
+    for wg, wu in wsets:
+        tg = torch.empty(tbytes, dtype=torch.uint8, device=dev)
+        tu = torch.empty(tbytes, dtype=torch.uint8, device=dev)
+        ops.pack_iq3_tiled(wg, tg, N, K)
+        ops.pack_iq3_tiled(wu, tu, N, K)
+        tsets.append((tg, tu))
+    torch.cuda.synchronize()
+    from thunderllamax_amd._lib import LAYOUT_PACKED, LAYOUT_TILED
+    layouts = {"tiled": (tsets, LAYOUT_TILED), "packed": (wsets, LAYOUT_PACKED)}
+    other = "packed" if args.layout == "tiled" else "tiled"
 
-    per_m = {}
-    for M in ms:
-        x = torch.from_numpy(synth.activations_f16(rng, M, K)).to(dev)
-        gact = torch.empty(M, N, dtype=torch.float16, device=dev)
-        ms_step = time_ffn(ops, wsets, gridf, x, gact, args.steps, args.warmup, torch)
-        nbytes = wbytes + M * K * 2 + M * N * 2
-        gbs = nbytes / (ms_step * 1e-3) / 1e9
-        per_m[str(M)] = {"ms_per_step": round(ms_step, 5), "gbs": round(gbs, 1),
-                         "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
-                         "tflops": round(2 * M * 2 * N * K / (ms_step * 1e-3) / 1e12, 3)}
+    def per_m_of(name):
+        sets, lay = layouts[name]
+        res = {}
+        for M in ms:
+            x = torch.from_numpy(synth.activations_f16(np.random.default_rng(M), M, K)).to(dev)
+            gact = torch.empty(M, N, dtype=torch.float16, device=dev)
+            ms_step = time_ffn(ops, sets, gridf, x, gact, args.steps, args.warmup, torch, lay)
+            nbytes = wbytes + M * K * 2 + M * N * 2
+            gbs = nbytes / (ms_step * 1e-3) / 1e9
+            res[str(M)] = {"ms_per_step": round(ms_step, 5), "gbs": round(gbs, 1),
+                           "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+                           "tflops": round(2 * M * 2 * N * K / (ms_step * 1e-3) / 1e12, 3)}
+        return res
+
+    per_m = per_m_of(args.layout)
+    per_m_other = per_m_of(other)
     head = str(max(ms))
     value = per_m[head]["gbs"]
     out = {
@@ -473,13 +495,16 @@ def main():
         "data": "synthetic (seeded GGUF IQ3_XXS blocks, bf16->fp16 N(0,1) activations)",
         "config": {"workload": f"IQ3_XXS ffn8 gate+up+SwiGLU GEMV, K={K}, N=2x{N}, M={head}",
                    "M": int(head), "K": K, "N": 2 * N, "weight_bytes": wbytes,
-                   "rotation_copies": ncopy, "parallelism": "single GPU"},
+                   "layout": args.layout, "rotation_copies": ncopy, "parallelism": "single GPU"},
         "per_m": per_m,
+        "per_m_other_layout": {"layout": other, **per_m_other},
         "roofline": {"bound": "hbm", "achieved": value, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(value / PEAK_HBM_GBS, 4),
-                     "traffic": FFN8_M11_TRAFFIC_BYTES if head == "11" else None,
+                     "traffic": (FFN8_M11_TRAFFIC_BYTES if head == "11" and args.layout == "packed" else None),
                      "algorithmic_bytes": wbytes + int(head) * K * 2 + int(head) * N * 2,
-                     "kernel": "iq3_gemv_kernel<2,1,4> (+ iq3_xt_kernel for M >= 6)"},
+                     "kernel": ("iq3s_kernel<2,1,8,2> (tiled records, activations staged in LDS)"
+                                if args.layout == "tiled" else
+                                "iq3_gemv_kernel<2,1,4> (+ iq3_xt_kernel for M >= 6)")},
     }
     if args.gemm_m > 0:
         out["gemm"] = gemm_leg(ops, formats, synth, torch, dev, args.gemm_m, max(3, args.steps // 5),

@@ -39,6 +39,11 @@ extern "C" {
                                 Q6_K: pack_w1c 212-B blocks [pad2][d2][sc16][lo128][qh64] */
 #define TLX_LAYOUT_PACK7 2   /* IQ3_XXS packed7 (engine/pack_w7.py:7-21): [N/8 groups][K/128
                                 chunks][32 units r*4+c][16 B: q u16 x4, sw u32, d u16, pad] */
+#define TLX_LAYOUT_TILED 3   /* IQ3_XXS tile-major streaming layout of this library (no reference
+                                counterpart; built by tlx_pack_iq3_tiled): [ceil(N/16) tiles]
+                                [K/256 blocks] 1568-B records [qs 64 x 16 B][sw 64 x 8 B]
+                                [d 16 x 2 B]; slot L = 16*kq + r holds row r's grid bytes
+                                16kq..16kq+15 / scale words 2kq, 2kq+1; rows >= N are zero */
 
 #define TLX_MAX_M 16         /* decode GEMVs accept 1..16 activation rows */
 
@@ -69,7 +74,8 @@ int tlx_iq4xs_dequant(const void* w, const float* iq4nl, float* out, int64_t row
 /* Fused IQ3_XXS FFN gate+up GEMV + SwiGLU:
  *   gact[m][n] = silu16(half(Wg[n]·x[m])) * half(Wu[n]·x[m])
  * Replaces ffn8 / ffn8v{3..11} (engine/ffn8.cu:134-185, engine/ffn8v11.cu:88-133):
- * ffn8(wg, wu, gridf, hhx, gact).  wg, wu: N rows x 98*(K/256) B (layout PACKED);
+ * ffn8(wg, wu, gridf, hhx, gact).  wg, wu: N rows x 98*(K/256) B (layout PACKED rows,
+ * RAW blocks, or TILED records);
  * gridf: float[1024]; hhx_f16: [M][K]; gact_f16: [M][N]. */
 int tlx_ffn8(const void* wg, const void* wu, const float* gridf, const uint16_t* hhx_f16,
              uint16_t* gact_f16, int M, int N, int K, int layout, void* stream);
@@ -230,6 +236,12 @@ int tlx_pack_q6_pad(const void* raw, void* padded, int N, int K, void* stream);
 /* packed IQ3_XXS rows -> packed7 units [N/8][K/128][32][16 B], replaces pack_tensor
  * (engine/pack_w7.py:40-75); N % 8 == 0. */
 int tlx_pack_w7(const void* packed, void* p7, int N, int K, void* stream);
+/* IQ3_XXS rows (src_layout TLX_LAYOUT_RAW blocks or TLX_LAYOUT_PACKED rows) -> TLX_LAYOUT_TILED
+ * records, ceil(N/16) * (K/256) * 1568 B.  No reference counterpart: the decode GEMVs
+ * (tlx_ffn8, tlx_ffn8_hh, tlx_down8, tlx_iq3_gemv) read it with every wave load one contiguous
+ * run, the streaming form of the layout pack_w1c (engine/pack_w1c.py:20-31) makes for the
+ * reference's GEMVs.  The GEMV results are bit-identical to those of the source layout. */
+int tlx_pack_iq3_tiled(const void* src, void* tiled, int N, int K, int src_layout, void* stream);
 
 /* ---- MoE grouped-expert path (256 routed experts + 1 shared, hidden 2048, expert FF 512,
  * top-8; IQ4_XS weights).  Pairs are position-major, rank ascending: pair = 8*pos + rank.

@@ -4,6 +4,11 @@
 * ``pack_q6_pad``   -- /root/reference/engine/pack_w1c.py:33-45  raw Q6_K rows -> 212-B blocks
 * ``pack_w7``       -- /root/reference/engine/pack_w7.py:40-73   packed IQ3 rows -> packed7 units
 * ``unpack_w7``     -- /root/reference/engine/pack_w7.py:75-96   the inverse
+* ``pack_tiled`` / ``unpack_tiled`` -- this library's tile-major records for the IQ3_XXS
+  decode GEMVs (no reference counterpart): a lossless re-encoding of the pack_w1c rows above
+  with the per-chunk table indices precomputed.  Pinned by the inverse (which also checks the
+  one redundant bit, the sign parity), by a hand-decoded block, and, on the GPU, by the GEMVs
+  over the records against the dequantized rows.
 """
 import numpy as np
 
@@ -93,3 +98,86 @@ def unpack_w7(p7, kdim, n):
                 back[r::8, nb * 32 + 2 * w + 1] = u[:, chunk, 4 * r + c, 5]
                 back[r::8, nb * 48 + b] = u[:, chunk, 4 * r + c, 6]
     return back.view(np.uint8).reshape(n, 98 * nb)
+
+
+
+def _tiled_fields(full, nb):
+    """(qs u8[R, NB, 64], sw u32[R, NB, 8], d u16[R, NB]) of packed rows."""
+    r = len(full)
+    qs = full[:, :64 * nb].reshape(r, nb, 64)
+    sw = np.ascontiguousarray(full[:, 64 * nb:96 * nb]).view("<u4").reshape(r, nb, 8)
+    d = np.ascontiguousarray(full[:, 96 * nb:]).view("<u2").reshape(r, nb)
+    return qs, sw, d
+
+
+def pack_tiled(packed_rows, kdim):
+    """Packed IQ3 rows u8[N, 98*NB] -> tiled records u8[ceil(N/16), NB, 1632].
+
+    Record (tile t, block b): ``[A: slot 0..63 x 16 B][B: slot 0..63 x 8 B][scale word: row
+    0..15 x 4 B][d: row 0..15 x 2 B]``.  Slot ``L = 16*kq + r`` (row ``16t + r``) holds the 24-B
+    stream of lane-chunks ``lc = 8kq + c``, c = 0..7, 3 little-endian bytes each:
+    ``v = i0 | i1 << 12`` with ``i0 = (sidx & 15) << 8 | qs[2lc]``,
+    ``i1 = ((sidx >> 4) | parity(sidx) << 3) << 8 | qs[2lc + 1]`` and
+    ``sidx = (sw[lc >> 2] >> 7*(lc & 3)) & 127`` (the GGUF sign field of the chunk); its first 16
+    bytes go to A, the last 8 to B.  Scale word: nibble j = ``sw[j] >> 28``.  Rows past N are zero.
+    """
+    p = np.ascontiguousarray(packed_rows, dtype=np.uint8)
+    n, nb = len(p), kdim // 256
+    t = -(-n // 16)
+    full = np.zeros((16 * t, 98 * nb), dtype=np.uint8)
+    full[:n] = p
+    qs, sw, d = _tiled_fields(full, nb)
+    lc = np.arange(32)
+    sidx = (sw[:, :, lc >> 2] >> (7 * (lc & 3)).astype(np.uint32)) & 0x7F          # [R, NB, 32]
+    par = np.zeros_like(sidx)
+    for k in range(7):
+        par ^= (sidx >> k) & 1
+    i0 = ((sidx & 0xF) << 8) | qs[:, :, 0::2]
+    i1 = (((sidx >> 4) | (par << 3)) << 8) | qs[:, :, 1::2]
+    v = (i0 | (i1 << 12)).astype(np.uint32)                                          # 24-bit values
+    stream = np.stack([v & 0xFF, (v >> 8) & 0xFF, (v >> 16) & 0xFF], axis=-1).astype(np.uint8)
+    stream = stream.reshape(t, 16, nb, 4, 24)                                        # [tile, r, b, kq, 24 B]
+    A = stream[..., :16].transpose(0, 2, 3, 1, 4).reshape(t, nb, 1024)             # slot = 16kq + r
+    B = stream[..., 16:].transpose(0, 2, 3, 1, 4).reshape(t, nb, 512)
+    scw = np.zeros(sw.shape[:2], dtype=np.uint32)
+    for j in range(8):
+        scw |= (sw[:, :, j] >> 28) << (4 * j)
+    S = scw.astype("<u4").view(np.uint8).reshape(t, 16, nb, 4).transpose(0, 2, 1, 3).reshape(t, nb, 64)
+    D = d.astype("<u2").view(np.uint8).reshape(t, 16, nb, 2).transpose(0, 2, 1, 3).reshape(t, nb, 32)
+    return np.ascontiguousarray(np.concatenate([A, B, S, D], axis=2))
+
+
+def unpack_tiled(rec, kdim, n):
+    """Inverse of :func:`pack_tiled` -> packed IQ3 rows u8[n, 98*NB].  Raises if a stored parity
+    bit disagrees with its sign field (the one redundant bit of the record)."""
+    nb = kdim // 256
+    r = np.ascontiguousarray(rec, dtype=np.uint8).reshape(-1, nb, 1632)
+    t = len(r)
+    A = r[:, :, :1024].reshape(t, nb, 4, 16, 16)
+    B = r[:, :, 1024:1536].reshape(t, nb, 4, 16, 8)
+    stream = np.concatenate([A, B], axis=-1).transpose(0, 3, 1, 2, 4)               # [tile, r, b, kq, 24]
+    b3 = stream.reshape(16 * t, nb, 32, 3).astype(np.uint32)                        # lc = 8kq + c
+    v = b3[..., 0] | (b3[..., 1] << 8) | (b3[..., 2] << 16)
+    i0, i1 = v & 0xFFF, v >> 12
+    sidx = (i0 >> 8) | ((i1 >> 8) & 7) << 4
+    par = np.zeros_like(sidx)
+    for k in range(7):
+        par ^= (sidx >> k) & 1
+    if np.any(((i1 >> 11) & 1) != par):
+        raise ValueError("tiled record: parity bit does not match its sign field")
+    qs = np.empty((16 * t, nb, 64), dtype=np.uint8)
+    qs[:, :, 0::2] = i0 & 0xFF
+    qs[:, :, 1::2] = i1 & 0xFF
+    scw = r[:, :, 1536:1600].reshape(t, nb, 16, 4).transpose(0, 2, 1, 3).reshape(16 * t, nb, 4)
+    scw = np.ascontiguousarray(scw).view("<u4")[..., 0]
+    sw = np.zeros((16 * t, nb, 8), dtype=np.uint32)
+    for j in range(8):
+        w = (scw >> (4 * j)) & 0xF
+        sw[:, :, j] = w << 28
+        for f in range(4):
+            sw[:, :, j] |= sidx[:, :, 4 * j + f] << (7 * f)
+    d = r[:, :, 1600:].reshape(t, nb, 16, 2).transpose(0, 2, 1, 3).reshape(16 * t, nb, 2)
+    out = np.concatenate([qs.reshape(16 * t, 64 * nb),
+                          sw.astype("<u4").view(np.uint8).reshape(16 * t, 32 * nb),
+                          np.ascontiguousarray(d).reshape(16 * t, 2 * nb)], axis=1)
+    return out[:n]

@@ -1,0 +1,169 @@
+"""The tile-major records of the IQ3_XXS decode GEMVs (TLX_LAYOUT_TILED) and the balanced GEMV
+kernel that reads them.
+
+* The device repacker is byte-identical to the oracle's restatement (oracle/layouts.py
+  ``pack_tiled``), from GGUF blocks and from packed rows, tail tiles included.
+* Every GEMV entry point over the records stays within the path's rel-err 1e-3 of the oracle
+  (exact product of the dequantized weights and the fp16 activations, then the epilogue), on
+  shapes where tiles are split between waves of one workgroup and between two workgroups.
+* Rows of an M-row call are bit-identical to M=1 calls, and repeated calls agree bit for bit
+  (the cross-workgroup combine is ordered, not first-come).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemv, layouts, quants
+from thunderllamax_amd import formats, ops, synth
+from thunderllamax_amd._lib import LAYOUT_RAW, LAYOUT_TILED, TlxError
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _tiled(gpu, src, N, K, src_layout=None):
+    out = torch.empty(-(-N // 16) * 16 * 102 * (K // 256), dtype=torch.uint8, device=gpu)
+    if src_layout is None:
+        ops.pack_iq3_tiled(src, out, N, K)
+    else:
+        ops.pack_iq3_tiled(src, out, N, K, src_layout)
+    return out
+
+
+def _mat(gpu, rng, N, K):
+    packed = formats.iq3_pack_rows(synth.iq3xxs_raw(rng, N, K), K)
+    return packed, _tiled(gpu, torch.from_numpy(packed).to(gpu), N, K)
+
+
+def _rows_err(y, ref):
+    return max(gemv.rel_err(y[m], ref[m]) for m in range(ref.shape[0]))
+
+
+@pytest.mark.parametrize("N,K", [(16, 256), (37, 512), (64, 5120), (24, 17408)])
+def test_pack_tiled_bytes(gpu, N, K):
+    print(f"[case] pack_iq3_tiled N={N} K={K}", flush=True)
+    raw = synth.iq3xxs_raw(synth.config_rng(5), N, K)
+    packed = formats.iq3_pack_rows(raw, K)
+    ref = layouts.pack_tiled(packed, K).reshape(-1)
+    from_packed = _tiled(gpu, torch.from_numpy(packed).to(gpu), N, K)
+    from_raw = _tiled(gpu, torch.from_numpy(raw.reshape(-1)).to(gpu), N, K, LAYOUT_RAW)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_packed.cpu().numpy(), ref)
+    assert np.array_equal(from_raw.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M", [1, 5, 6, 11, 16])
+def test_ffn8_tiled_parity(gpu, M):
+    print(f"[case] ffn8 tiled M={M} N=1000 K=5120", flush=True)
+    rng = synth.config_rng(2)
+    N, K = 1000, 5120                       # 62.5 tiles: the tail tile has 8 zero rows
+    pg, tg = _mat(gpu, rng, N, K)
+    pu, tu = _mat(gpu, rng, N, K)
+    x = synth.activations_f16(rng, M, K)
+    out = torch.full((M, N), float("nan"), dtype=torch.float16, device=gpu)
+    ops.ffn8(tg, tu, formats.gridf_tensor(gpu), torch.from_numpy(x).to(gpu), out, layout=LAYOUT_TILED)
+    torch.cuda.synchronize()
+    _, _, ref = gemv.ffn8_ref(quants.dequant_iq3xxs_packed(pg, K), quants.dequant_iq3xxs_packed(pu, K), x)
+    err = _rows_err(out.cpu().numpy(), ref)
+    print(f"[ffn8 tiled M={M}] max row rel-err {err:.3e}")
+    assert err <= TOL
+
+
+def test_ffn8_tiled_full_size(gpu):
+    """Config 2 (N=17408, K=5120): tiles split between waves and between workgroups.  384 seeded
+    rows against the oracle at M=11; every row of the M=11 call equals an M=1 call on that
+    activation row bit for bit; two calls agree bit for bit."""
+    print("[case] ffn8 tiled full-size", flush=True)
+    rng = synth.config_rng(2)
+    N, K, M = 17408, 5120, 11
+    pg, tg = _mat(gpu, rng, N, K)
+    pu, tu = _mat(gpu, rng, N, K)
+    x = torch.from_numpy(synth.activations_f16(rng, M, K)).to(gpu)
+    g = formats.gridf_tensor(gpu)
+    full = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    again = torch.empty_like(full)
+    ops.ffn8(tg, tu, g, x, full, layout=LAYOUT_TILED)
+    ops.ffn8(tg, tu, g, x, again, layout=LAYOUT_TILED)
+    one = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    for m in range(M):
+        ops.ffn8(tg, tu, g, x[m:m + 1].contiguous(), one[m:m + 1], layout=LAYOUT_TILED)
+    torch.cuda.synchronize()
+    assert torch.equal(full.view(torch.int16), again.view(torch.int16))
+    assert torch.equal(full.view(torch.int16), one.view(torch.int16))
+    # every row (tiles shared between workgroups included) against the packed-row kernel, which
+    # sums the same block products in another order
+    ref_all = torch.empty_like(full)
+    ops.ffn8(torch.from_numpy(pg).to(gpu), torch.from_numpy(pu).to(gpu), g, x, ref_all)
+    torch.cuda.synchronize()
+    d = (full.float() - ref_all.float()).abs()
+    assert torch.isfinite(full.float()).all()
+    assert (d <= 2e-3 * ref_all.float().abs() + 1e-3).all(), float(d.max())
+    rows = np.sort(np.random.default_rng(1).choice(N, 384, replace=False))
+    _, _, ref = gemv.ffn8_ref(quants.dequant_iq3xxs_packed(pg[rows], K),
+                              quants.dequant_iq3xxs_packed(pu[rows], K), x.cpu().numpy())
+    err = _rows_err(full.cpu().numpy()[:, rows], ref)
+    print(f"[ffn8 tiled full] sampled max row rel-err {err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("M,N", [(1, 200), (11, 200), (11, 5120)])
+def test_down8_and_plain_tiled_parity(gpu, M, N):
+    print(f"[case] down8 / iq3_gemv tiled M={M} N={N} K=17408", flush=True)
+    rng = synth.config_rng(3)
+    K = 17408
+    pd, td = _mat(gpu, rng, N, K)
+    g = formats.gridf_tensor(gpu)
+    x = synth.activations_f16(rng, M, K)
+    hh = rng.standard_normal((M, N)).astype(np.float32)
+    y = torch.empty(M, N, device=gpu)
+    o = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    xd = torch.from_numpy(x).to(gpu)
+    ops.down8(td, g, xd, torch.from_numpy(hh).to(gpu), y, layout=LAYOUT_TILED)
+    ops.iq3_gemv(td, g, xd, o, layout=LAYOUT_TILED)
+    torch.cuda.synchronize()
+    rows = np.arange(N) if N <= 512 else np.sort(np.random.default_rng(2).choice(N, 256, replace=False))
+    W = quants.dequant_iq3xxs_packed(pd[rows], K)
+    _, yref = gemv.down8_ref(W, x, hh[:, rows])
+    _, oref = gemv.gemv16_ref(W, x)
+    ey = _rows_err(y.cpu().numpy()[:, rows], yref)
+    eo = _rows_err(o.cpu().numpy()[:, rows], oref)
+    print(f"[down8 tiled M={M} N={N}] rel-err {ey:.3e}; [iq3_gemv] {eo:.3e}")
+    assert ey <= TOL and eo <= TOL
+
+
+def test_ffn8_hh_tiled_equals_two_calls(gpu):
+    print("[case] ffn8_hh tiled M=11", flush=True)
+    rng = synth.config_rng(6)
+    M, N, K = 11, 256, 5120
+    _, tg = _mat(gpu, rng, N, K)
+    _, tu = _mat(gpu, rng, N, K)
+    g = formats.gridf_tensor(gpu)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(gpu)
+    ao = torch.from_numpy(synth.activations_f16(rng, M, K)).to(gpu)
+    nw = torch.from_numpy((1 + 0.1 * rng.standard_normal(K)).astype(np.float32)).to(gpu)
+    hh = torch.empty(M, K, device=gpu)
+    hhx = torch.empty(M, K, dtype=torch.float16, device=gpu)
+    fused = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    ops.ffn8_hh(tg, tu, g, x, ao, nw, hh, hhx, fused, layout=LAYOUT_TILED)
+    hh2, hhx2 = torch.empty_like(hh), torch.empty_like(hhx)
+    sep = torch.empty_like(fused)
+    ops.add_rms_f16(x, ao, nw, hh2, hhx2)
+    ops.ffn8(tg, tu, g, hhx2, sep, layout=LAYOUT_TILED)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int16), sep.view(torch.int16))
+
+
+def test_tiled_rejects_short_or_misaligned_buffers(gpu):
+    N, K = 20, 256                                  # two tiles: 32 rows of records
+    w = torch.zeros(20 * 98, dtype=torch.uint8, device=gpu)
+    x = torch.zeros(1, K, dtype=torch.float16, device=gpu)
+    out = torch.empty(1, N, dtype=torch.float16, device=gpu)
+    g = formats.gridf_tensor(gpu)
+    with pytest.raises(ValueError):
+        ops.iq3_gemv(w, g, x, out, layout=LAYOUT_TILED)     # 20 rows of bytes, 32 needed
+    big = torch.zeros(32 * 102 + 16, dtype=torch.uint8, device=gpu)
+    with pytest.raises(TlxError):
+        ops.iq3_gemv(big[8:], g, x, out, layout=LAYOUT_TILED)
+    q = torch.empty(1, 16, dtype=torch.float16, device=gpu)
+    with pytest.raises(TlxError):                   # the fused q/k/v projections take rows / blocks
+        ops.aq3k8(big, big, big, g, x, q, q, q, layout=LAYOUT_TILED)

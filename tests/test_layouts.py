@@ -25,6 +25,51 @@ def test_pack7_matches_reference_packer_and_inverts(rows, kdim):
     assert np.all(p7[..., 14:16] == 0)
 
 
+@pytest.mark.parametrize("rows,kdim", [(16, 256), (21, 512), (32, 5120)])
+def test_tiled_records_invert_and_place_fields(rows, kdim):
+    raw = synth.iq3xxs_raw(np.random.default_rng(rows), rows, kdim)
+    p = formats.iq3_pack_rows(raw, kdim)
+    rec = layouts.pack_tiled(p, kdim)
+    assert rec.shape == (-(-rows // 16), kdim // 256, 1632)
+    assert np.array_equal(layouts.unpack_tiled(rec, kdim, rows), p)
+    # rows past N (the tail tile) are zero
+    assert np.all(layouts.unpack_tiled(rec, kdim, 16 * len(rec))[rows:] == 0)
+
+
+def test_tiled_record_decodes_by_hand():
+    """One slot decoded with the GGUF rules written out: grid bytes, the 7-bit sign field of the
+    chunk, the 8th sign = parity, the sub-block scale nibble and d."""
+    kdim, rows = 256, 16
+    raw = synth.iq3xxs_raw(np.random.default_rng(5), rows, kdim)
+    rec = layouts.pack_tiled(formats.iq3_pack_rows(raw, kdim), kdim)[0, 0]
+    r, kq = 9, 2
+    blk = raw[r]
+    sw = blk[66:98].view("<u4")
+    stream = np.concatenate([rec[16 * (16 * kq + r):16 * (16 * kq + r) + 16],
+                             rec[1024 + 8 * (16 * kq + r):1024 + 8 * (16 * kq + r) + 8]])
+    for c in range(8):
+        lc = 8 * kq + c
+        sfield = int(sw[lc // 4] >> (7 * (lc % 4))) & 0x7F
+        signs = [(sfield >> k) & 1 for k in range(7)]
+        signs.append(sum(signs) % 2)
+        v = int(stream[3 * c]) | int(stream[3 * c + 1]) << 8 | int(stream[3 * c + 2]) << 16
+        i0, i1 = v & 0xFFF, v >> 12
+        assert i0 & 0xFF == blk[2 + 2 * lc] and i1 & 0xFF == blk[3 + 2 * lc]
+        assert [(i0 >> 8 >> k) & 1 for k in range(4)] == signs[:4]
+        assert [(i1 >> 8 >> k) & 1 for k in range(4)] == signs[4:]
+    scw = int(rec[1536 + 4 * r:1540 + 4 * r].view("<u4")[0])
+    assert [(scw >> (4 * j)) & 15 for j in range(8)] == [int(w >> 28) for w in sw]
+    assert bytes(rec[1600 + 2 * r:1602 + 2 * r]) == bytes(blk[0:2])
+
+
+def test_tiled_unpack_rejects_a_wrong_parity_bit():
+    kdim = 256
+    rec = layouts.pack_tiled(formats.iq3_pack_rows(synth.iq3xxs_raw(np.random.default_rng(1), 16, kdim), kdim), kdim)
+    rec[0, 0, 2] ^= 0x80            # slot 0, chunk 0: bit 23 of the stream = i1's parity bit
+    with pytest.raises(ValueError):
+        layouts.unpack_tiled(rec, kdim, 16)
+
+
 @pytest.mark.parametrize("rows,kdim", [(3, 256), (5, 1024)])
 def test_q6_padded_matches_reference_packer(rows, kdim):
     raw = synth.q6k_raw(np.random.default_rng(3), rows, kdim)

@@ -21,6 +21,7 @@ TLX_E_TRUNC = -5
 LAYOUT_RAW = 0
 LAYOUT_PACKED = 1
 LAYOUT_PACK7 = 2
+LAYOUT_TILED = 3
 V_Q4K = 0x100   # or-ed into the fused attention layout: v rows are GGUF Q4_K
 MAX_M = 16
 
@@ -60,6 +61,7 @@ SIGNATURES = {
     "tlx_pack_iq3_rows": [_p, _p, _i, _i, _p],
     "tlx_pack_q6_pad": [_p, _p, _i, _i, _p],
     "tlx_pack_w7": [_p, _p, _i, _i, _p],
+    "tlx_pack_iq3_tiled": [_p, _p, _i, _i, _i, _p],
     "tlx_p8w4_ffn": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_moe_topk": [_p, _p, _p, _i, _p],
     "tlx_moe_route": [_p, _p, _p, _p, _p, _p, _i, _p],

@@ -61,6 +61,28 @@ __device__ __forceinline__ uint16_t tlx_swiglu_bits(float g, float u) {
   return __builtin_bit_cast(uint16_t, __hmul(tlx_hsilu(hg), hu));
 }
 
+// IQ3_XXS sign-folded lookup table of the decode GEMVs, built by the workgroup in LDS from the
+// caller's gridf buffer (float[256][4]): entry (nib << 8 | g) = grid[g][j] with the sign of bit j
+// of nib, j = 0..3, as four fp16 values (grid magnitudes are exact in fp16).
+// Entries (nib << 8 | g) for nib = 4q .. 4q+3 of grid word g (values v).
+__device__ __forceinline__ void tlx_iq3_table_entries(u2_t* tbl, float4 v, int g, int q) {
+  const h2_t lo = {(_Float16)v.x, (_Float16)v.y};
+  const h2_t hi = {(_Float16)v.z, (_Float16)v.w};
+  const uint32_t l = __builtin_bit_cast(uint32_t, lo), h = __builtin_bit_cast(uint32_t, hi);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t nib = 4 * q + i;
+    const uint32_t ml = ((nib & 1u) << 15) | ((nib & 2u) << 30);
+    const uint32_t mh = ((nib & 4u) << 13) | ((nib & 8u) << 28);
+    tbl[(nib << 8) | g] = u2_t{l ^ ml, h ^ mh};
+  }
+}
+
+__device__ __forceinline__ void tlx_iq3_table(u2_t* tbl, const float* __restrict__ gridf) {
+  for (int e = threadIdx.x; e < 256 * 4; e += blockDim.x)
+    tlx_iq3_table_entries(tbl, reinterpret_cast<const float4*>(gridf)[e & 255], e & 255, e >> 8);
+}
+
 // ---------------------------------------------------------------- device properties
 // Compute-unit count of the current device (cached per device id; a benign race on first use
 // writes the same value twice).
@@ -83,6 +105,11 @@ static inline int tlx_cu_count() {
 // device and kept until the process ends; calls that overlap in time on one device must not
 // both use it.
 constexpr size_t kWsBytes = size_t(4) << 20;
+// regions: [0, 2 MB) the activation copy; [2 MB, 3 MB) partial tiles of the tiled-record GEMV;
+// [3 MB, +4 KB) its per-boundary arrival counters (zeroed at allocation, reset by each call)
+constexpr size_t kWsXtBytes = size_t(2) << 20;
+constexpr size_t kWsPartOff = size_t(2) << 20;
+constexpr size_t kWsCntOff = size_t(3) << 20;
 
 // RMSNorm producer (tlx_norm.hip): add form (hh = x + a) when add; optionally also writes the
 // IQ3_XXS GEMVs' tile-ordered activation copy xt (M <= 16)
@@ -98,6 +125,12 @@ int tlx_workspace(void** ws);
 int tlx_iq3_segments(const void* const* w, uint16_t* const* out, const int* n, int nseg,
                      const float* gridf, const uint16_t* xh_f16, int M, int K, int layout,
                      bool launch, void* stream);
+//   IQ3_XXS tiled records: the balanced GEMV (tlx_iq3s.hip); arguments already validated, x the
+//   activations or (xt != 0) their tile-ordered copy; nmat 2 = gate/up pair with epi SwiGLU,
+//   epi 0 = fp16 out, 2 = fp32 residual
+bool tlx_iq3s_stages_x(int M, int K);
+int tlx_iq3s_launch(int nmat, int epi, const void* w0, const void* w1, void* out, const float* res,
+                    const float* gridf, const _Float16* x, int xt, int M, int N, int K, hipStream_t st);
 //   k-quants: fmt 0 = Q6_K raw, 1 = Q6_K padded, 2 = Q4_K, 3 = Q5_K (tlx_kquant.hip).
 int tlx_kq_gemv(int fmt, const void* w, const uint16_t* x_f16, uint16_t* out_f16, int M, int N,
                 int K, bool launch, void* stream);

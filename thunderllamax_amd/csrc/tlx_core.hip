@@ -24,9 +24,13 @@ int tlx_workspace(void** ws) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return TLX_E_NODEV;
   std::lock_guard<std::mutex> lock(mu);
-  if (cache[dev] == nullptr && hipMalloc(&cache[dev], kWsBytes) != hipSuccess) {
-    cache[dev] = nullptr;
-    return TLX_E_NOMEM;
+  if (cache[dev] == nullptr) {
+    // zeroed once: the arrival counters of the tiled-record GEMV start (and end every call) at 0
+    if (hipMalloc(&cache[dev], kWsBytes) != hipSuccess || hipMemset(cache[dev], 0, kWsBytes) != hipSuccess) {
+      if (cache[dev] != nullptr) (void)hipFree(cache[dev]);
+      cache[dev] = nullptr;
+      return TLX_E_NOMEM;
+    }
   }
   *ws = cache[dev];
   return TLX_OK;

@@ -31,24 +31,6 @@ constexpr int kXtMinM = 6;  // from this M on, activations are read from the til
 
 enum Epi { EPI_F16 = 0, EPI_SWIGLU = 1, EPI_RESID = 2 };
 
-// entry (nib << 8 | g): grid[g][j] with the sign of bit j of nib, j = 0..3, as fp16.
-__device__ __forceinline__ void iq3_build_table(u2_t* tbl, const float* __restrict__ gridf) {
-  for (int e = threadIdx.x; e < 256 * 4; e += blockDim.x) {
-    const int g = e & 255, q = e >> 8;  // thread builds nibbles 4q..4q+3 of grid word g
-    const float4 v = reinterpret_cast<const float4*>(gridf)[g];
-    const h2_t lo = {(_Float16)v.x, (_Float16)v.y};
-    const h2_t hi = {(_Float16)v.z, (_Float16)v.w};
-    const uint32_t l = __builtin_bit_cast(uint32_t, lo), h = __builtin_bit_cast(uint32_t, hi);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t nib = 4 * q + i;
-      const uint32_t ml = ((nib & 1u) << 15) | ((nib & 2u) << 30);
-      const uint32_t mh = ((nib & 4u) << 13) | ((nib & 8u) << 28);
-      tbl[(nib << 8) | g] = u2_t{l ^ ml, h ^ mh};
-    }
-  }
-}
-
 // 8 signed grid magnitudes of one lane-chunk: q word = two grid indices, sidx = the 7-bit
 // sign field; the 8th sign is the parity of sidx.
 __device__ __forceinline__ h8_t iq3_chunk(const u2_t* tbl, uint32_t qw, uint32_t sidx) {
@@ -78,7 +60,7 @@ struct Iq3Launch {
   const _Float16* x;   // activations [M][K], or (xt) the tile-ordered copy [K/8][16][8]
   int xt;
   int M, K;
-  int raw;             // GGUF blocks [d][qs 64][sw 32] (1) or packed rows [qs][sw][d] (0)
+  int layout;          // TLX_LAYOUT_RAW or TLX_LAYOUT_PACKED
 };
 
 template <int NMAT>
@@ -107,7 +89,7 @@ __device__ __forceinline__ void iq3_load(Iq3Regs<NMAT>& r, const uint8_t* const*
 template <int NMAT, int EPI, int WAVES>
 __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Launch a) {
   __shared__ u2_t tbl[kTblEntries];
-  iq3_build_table(tbl, a.gridf);
+  tlx_iq3_table(tbl, a.gridf);
   __syncthreads();
 
   int s = 0;
@@ -118,13 +100,20 @@ __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Lau
   const int col = lane & 15, kq = lane >> 4;
   const int K = a.K, M = a.M, nb = K >> 8;
   const uint32_t rowb = (uint32_t)kIq3BlockBytes * nb;
-  const int row0 = ((int)blockIdx.x - sg.tile0) * kTile;
-  // tail tile: clamp the loads, mask the stores
-  const uint32_t roff = (uint32_t)min(row0 + col, sg.n - 1) * rowb;
-  const uint32_t qoff = roff + (a.raw ? 2u : 0u) + 16u * kq;
-  const uint32_t soff = roff + (a.raw ? 66u : 64u * nb) + 8u * kq;
-  const uint32_t doff = roff + (a.raw ? 0u : 96u * nb);
-  const uint32_t qst = a.raw ? 98u : 64u, sst = a.raw ? 98u : 32u, dst = a.raw ? 98u : 2u;
+  const int tile = (int)blockIdx.x - sg.tile0;
+  const int row0 = tile * kTile;
+  uint32_t qoff, soff, doff, qst, sst, dst;
+  {
+    // tail tile: clamp the loads, mask the stores
+    const bool raw = a.layout == TLX_LAYOUT_RAW;
+    const uint32_t roff = (uint32_t)min(row0 + col, sg.n - 1) * rowb;
+    qoff = roff + (raw ? 2u : 0u) + 16u * kq;
+    soff = roff + (raw ? 66u : 64u * nb) + 8u * kq;
+    doff = roff + (raw ? 0u : 96u * nb);
+    qst = raw ? 98u : 64u;
+    sst = raw ? 98u : 32u;
+    dst = raw ? 98u : 2u;
+  }
 
   const uint8_t* base[NMAT];
   base[0] = sg.w0;
@@ -226,7 +215,8 @@ int iq3_launch(Iq3Launch& a, int tiles, hipStream_t st) {
   const int nb = a.K >> 8;
   // same values, same arithmetic: only the activation loads change (larger K reads x directly);
   // a.xt set by the caller: a.x already is the tile-ordered copy (written by a producer)
-  if (!a.xt && a.M >= kXtMinM && (size_t)a.K * 16 * 2 <= kWsBytes) {
+  const bool staged = a.layout == TLX_LAYOUT_TILED && tlx_iq3s_stages_x(a.M, a.K);  // no copy needed
+  if (!a.xt && !staged && a.M >= kXtMinM && (size_t)a.K * 16 * 2 <= kWsXtBytes) {
     void* ws = nullptr;
     const int rc = tlx_workspace(&ws);
     if (rc != TLX_OK) return rc;
@@ -237,6 +227,9 @@ int iq3_launch(Iq3Launch& a, int tiles, hipStream_t st) {
     a.x = xt;
     a.xt = 1;
   }
+  if (a.layout == TLX_LAYOUT_TILED)
+    return tlx_iq3s_launch(NMAT, EPI, a.seg[0].w0, a.seg[0].w1, a.seg[0].out, a.seg[0].res, a.gridf, a.x,
+                           a.xt, a.M, a.seg[0].n, a.K, st);
   int waves = 4;
   while (tiles * waves < 4096 && waves < 16 && nb >= 4 * waves) waves *= 2;
   switch (waves) {
@@ -251,13 +244,16 @@ int iq3_launch(Iq3Launch& a, int tiles, hipStream_t st) {
 
 int iq3_check(const void* w, int M, int N, int K, int layout) {
   if (M < 1 || M > TLX_MAX_M || N < 1 || K < 256 || (K & 255)) return TLX_E_ARG;
-  if (layout != TLX_LAYOUT_PACKED && layout != TLX_LAYOUT_RAW) return TLX_E_ARG;
+  if (layout != TLX_LAYOUT_PACKED && layout != TLX_LAYOUT_RAW && layout != TLX_LAYOUT_TILED) return TLX_E_ARG;
   // packed rows: the operand loads are dword-aligned when the row bytes 98*NB are (NB even);
-  // GGUF blocks are 2-B aligned throughout
+  // tiled records are 1568 B (16-B aligned fields); GGUF blocks are 2-B aligned throughout
   if (layout == TLX_LAYOUT_PACKED && (((K >> 8) & 1) || !tlx_aligned(w, 4))) return TLX_E_ALIGN;
+  if (layout == TLX_LAYOUT_TILED && !tlx_aligned(w, 16)) return TLX_E_ALIGN;
   if (!tlx_aligned(w, 2)) return TLX_E_ALIGN;
-  // kernels address a matrix with 32-bit byte offsets
-  if ((size_t)N * kIq3BlockBytes * (K >> 8) > 0xFFFFFFFFull) return TLX_E_ARG;
+  // kernels address a matrix with 32-bit byte offsets (tiled: 102-B records of whole tiles)
+  const size_t bytes = layout == TLX_LAYOUT_TILED ? (size_t)(N + kTile - 1) / kTile * kTile * 102 * (K >> 8)
+                                                  : (size_t)N * kIq3BlockBytes * (K >> 8);
+  if (bytes > 0xFFFFFFFFull) return TLX_E_ARG;
   return TLX_OK;
 }
 
@@ -336,7 +332,7 @@ extern "C" int tlx_ffn8(const void* wg, const void* wu, const float* gridf, cons
   TLX_RET_IF(!tlx_aligned(hhx_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
   Iq3Launch a{};
   a.seg[0] = Iq3Seg{(const uint8_t*)wg, (const uint8_t*)wu, gact_f16, nullptr, N, 0};
-  a.raw = layout == TLX_LAYOUT_RAW;
+  a.layout = layout;
   a.nseg = 1;
   a.gridf = gridf;
   a.x = (const _Float16*)hhx_f16;
@@ -355,14 +351,15 @@ extern "C" int tlx_ffn8_hh(const void* wg, const void* wu, const float* gridf, c
   TLX_RET_IF(!tlx_aligned(gridf, 16), TLX_E_ALIGN);
   Iq3Launch a{};
   a.seg[0] = Iq3Seg{(const uint8_t*)wg, (const uint8_t*)wu, gact_f16, nullptr, N, 0};
-  a.raw = layout == TLX_LAYOUT_RAW;
+  a.layout = layout;
   a.nseg = 1;
   a.gridf = gridf;
   a.x = (const _Float16*)hhx_f16;
   a.M = M;
   a.K = K;
   _Float16* xt = nullptr;
-  if (M >= kXtMinM && (size_t)K * 16 * 2 <= kWsBytes) {   // the producer writes the GEMV's copy
+  const bool staged = layout == TLX_LAYOUT_TILED && tlx_iq3s_stages_x(M, K);
+  if (!staged && M >= kXtMinM && (size_t)K * 16 * 2 <= kWsXtBytes) {   // the producer writes the GEMV's copy
     void* ws = nullptr;
     rc = tlx_workspace(&ws);
     TLX_RET_IF(rc != TLX_OK, rc);
@@ -382,7 +379,7 @@ extern "C" int tlx_down8(const void* wd, const float* gridf, const uint16_t* gac
   TLX_RET_IF(!tlx_aligned(gact_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
   Iq3Launch a{};
   a.seg[0] = Iq3Seg{(const uint8_t*)wd, nullptr, y, hh, N, 0};
-  a.raw = layout == TLX_LAYOUT_RAW;
+  a.layout = layout;
   a.nseg = 1;
   a.gridf = gridf;
   a.x = (const _Float16*)gact_f16;
@@ -398,7 +395,7 @@ extern "C" int tlx_iq3_gemv(const void* w, const float* gridf, const uint16_t* x
   TLX_RET_IF(!tlx_aligned(x_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
   Iq3Launch a{};
   a.seg[0] = Iq3Seg{(const uint8_t*)w, nullptr, out_f16, nullptr, N, 0};
-  a.raw = layout == TLX_LAYOUT_RAW;
+  a.layout = layout;
   a.nseg = 1;
   a.gridf = gridf;
   a.x = (const _Float16*)x_f16;
@@ -412,7 +409,7 @@ extern "C" int tlx_iq3_gemv(const void* w, const float* gridf, const uint16_t* x
 int tlx_iq3_segments(const void* const* w, uint16_t* const* out, const int* n, int nseg,
                      const float* gridf, const uint16_t* xh_f16, int M, int K, int layout,
                      bool launch, void* stream) {
-  TLX_RET_IF(nseg < 1 || nseg > 3, TLX_E_ARG);
+  TLX_RET_IF(nseg < 1 || nseg > 3 || layout == TLX_LAYOUT_TILED, TLX_E_ARG);
   for (int i = 0; i < nseg; ++i) {
     const int rc = iq3_check(w[i], M, n[i], K, layout);
     TLX_RET_IF(rc != TLX_OK, rc);
@@ -430,6 +427,6 @@ int tlx_iq3_segments(const void* const* w, uint16_t* const* out, const int* n, i
   a.x = (const _Float16*)xh_f16;
   a.M = M;
   a.K = K;
-  a.raw = layout == TLX_LAYOUT_RAW;
+  a.layout = layout;
   return iq3_launch<1, EPI_F16>(a, tiles, (hipStream_t)stream);
 }

@@ -1,0 +1,504 @@
+// IQ3_XXS decode GEMVs over tile-major records (TLX_LAYOUT_TILED): the records, their device
+// repacker, and the balanced GEMV kernel that streams them.
+//
+// Record (16-row tile t, 256-k block b), 1632 B, records in (tile, block) order:
+//   [0, 1024)     slot L = 16*kq + r, 16 B: bits 0..127 of the slot's index stream
+//   [1024, 1536)  slot L, 8 B: bits 128..191
+//   [1536, 1600)  row r, u32: the 8 sub-block scales s_j = sw[j] >> 28 as nibbles 4j..4j+3
+//   [1600, 1632)  row r, u16: the block's d
+// Index stream of slot (kq, r): 8 lane-chunks c = 0..7 (GGUF lane-chunk 8kq + c = weights
+// 64kq + 8c .. +7 of row r), 24 bits each: two 12-bit lookup indices nib << 8 | g into the
+// sign-folded table (tlx_iq3_table), g = the chunk's grid bytes, nib = its sign bits 0..3 and
+// 4..6 + parity (the 8th sign).  The sign fields are recovered exactly from the indices, so the
+// record is a lossless re-encoding of the GGUF block (102 B per 256 weights against 98): the
+// parity the kernel would otherwise count per chunk is stored.
+//
+// Kernel: one workgroup per CU (persistent), W waves.  The T*NB records ("units") are split into
+// G*W equal contiguous ranges, one per wave, so every CU streams the same number of bytes and a
+// wave reads its range front to back (each record is 1632 contiguous bytes).  Lane (col, kq)
+// decodes row col's slot kq of each record into MFMA B operands exactly as the packed-row GEMV
+// does (same products, same per-block d scaling), so a block's contribution is bit-identical to
+// that kernel's; the sum over blocks is a fixed order of per-wave partials:
+//   * a wave's partial for a tile it does not cover completely goes to LDS; after the loop the
+//     lowest contributing wave adds the contributions in wave order;
+//   * a tile shared by two workgroups (at most two: a workgroup covers >= NB units) is finished
+//     by the second of them to arrive: both write their part to the library workspace, count
+//     on a per-boundary counter, and the last adds lower-range part + upper-range part and
+//     resets the counter.
+// The order depends only on (N, K, CU count): rows of an M-row call equal an M=1 call bit for bit.
+#include "tlx_common.h"
+
+#include <algorithm>
+
+namespace {
+
+constexpr int kTblEntries = 4096;
+constexpr uint32_t kRec = 1632;
+constexpr int kMaxG = 256;   // workgroups (boundaries) the workspace has slots for
+
+enum Epi { EPI_F16 = 0, EPI_SWIGLU = 1, EPI_RESID = 2 };
+
+// ------------------------------------------------------------------ repacker
+// One thread per (record, slot): the slot's 24 B of indices, and for kq == 0 the row's scale word
+// and d.  src: raw GGUF blocks (raw = 1) or packed rows [qs 64NB][sw 32NB][d 2NB]; rows >= N zero.
+__global__ __launch_bounds__(256) void pack_tiled_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ rec,
+                                                         long nslots, int N, int nb, int raw) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nslots) return;
+  const long u = i >> 6;                     // record = tile * nb + b
+  const int L = (int)(i & 63), r = L & 15, kq = L >> 4;
+  const long tile = u / nb;
+  const int b = (int)(u - tile * nb);
+  const long row = tile * 16 + r;
+  uint8_t* o = rec + u * kRec;
+  uint32_t st[6] = {0, 0, 0, 0, 0, 0};
+  uint32_t scw = 0, dbits = 0;
+  if (row < N) {
+    const uint8_t* rp = src + row * 98L * nb;
+    const uint8_t* qs = raw ? rp + 98L * b + 2 : rp + 64L * b;
+    const uint8_t* sw = raw ? rp + 98L * b + 66 : rp + 64L * nb + 32L * b;
+    dbits = raw ? tlx_ldu<uint16_t>(rp + 98L * b) : tlx_ldu<uint16_t>(rp + 96L * nb + 2L * b);
+    for (int j = 0; j < 8; ++j) scw |= (tlx_ldu<uint32_t>(sw + 4 * j) >> 28) << (4 * j);
+    for (int c = 0; c < 8; ++c) {
+      const int lc = 8 * kq + c;                      // GGUF lane-chunk: weights 8lc .. 8lc+7
+      const uint32_t w = tlx_ldu<uint32_t>(sw + 4 * (lc >> 2));
+      const uint32_t sidx = (w >> (7 * (lc & 3))) & 0x7Fu;
+      const uint32_t par = __builtin_popcount(sidx) & 1u;
+      const uint32_t i0 = ((sidx & 0xFu) << 8) | qs[2 * lc];
+      const uint32_t i1 = (((sidx >> 4) | (par << 3)) << 8) | qs[2 * lc + 1];
+      const uint32_t v = i0 | (i1 << 12);             // 24 bits at stream bit 24c
+      const int p = 24 * c, d = p >> 5, s = p & 31;
+      st[d] |= v << s;
+      if (s > 8) st[d + 1] |= v >> (32 - s);
+    }
+  }
+  *reinterpret_cast<u4_t*>(o + 16 * L) = u4_t{st[0], st[1], st[2], st[3]};
+  *reinterpret_cast<u2_t*>(o + 1024 + 8 * L) = u2_t{st[4], st[5]};
+  if (kq == 0) {
+    *reinterpret_cast<uint32_t*>(o + 1536 + 4 * r) = scw;
+    *reinterpret_cast<uint16_t*>(o + 1600 + 2 * r) = (uint16_t)dbits;
+  }
+}
+
+// ------------------------------------------------------------------ GEMV
+struct SkArgs {
+  const uint8_t* w0;
+  const uint8_t* w1;   // up matrix (SwiGLU), else null
+  void* out;
+  const float* res;    // residual (EPI_RESID)
+  const float* gridf;
+  const _Float16* x;   // [M][K], or (xt) the tile-ordered copy [K/8][16][8]
+  int xt;
+  int M, N, K, nb, U, G;
+  int ostride;         // output / residual row stride (elements)
+  f4_t* part;          // workspace: boundary g: [lo | hi][NMAT][64 lanes]
+  uint32_t* cnt;       // workspace: arrival counter per boundary (0 between calls)
+};
+
+template <int NMAT>
+struct Rec {
+  u4_t A[NMAT];
+  u2_t B[NMAT];
+  uint32_t sc[NMAT];
+  uint32_t d[NMAT];
+};
+
+// Buffer loads: the per-lane part of an address is a fixed VGPR, the per-record part a
+// wave-uniform SGPR (soff), the field offset an immediate -- no per-load vector address math.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
+}
+
+template <int NMAT>
+__device__ __forceinline__ void rec_load(Rec<NMAT>& r, const __amdgpu_buffer_rsrc_t* rs, int soff, int lane, int col) {
+#pragma unroll
+  for (int i = 0; i < NMAT; ++i) {
+    r.A[i] = __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(rs[i], 16 * lane, soff, 0));
+    r.B[i] = __builtin_bit_cast(u2_t, __builtin_amdgcn_raw_buffer_load_b64(rs[i], 8 * lane + 1024, soff, 0));
+    r.sc[i] = __builtin_amdgcn_raw_buffer_load_b32(rs[i], 4 * col + 1536, soff, 0);
+    r.d[i] = __builtin_amdgcn_raw_buffer_load_b16(rs[i], 2 * col + 1600, soff, 0);
+  }
+}
+
+// 12-bit field at bit P of the slot's 192-bit stream s[0..5], as a byte offset into the table
+// (8-B entries)
+template <int P>
+__device__ __forceinline__ uint32_t field_off(const uint32_t* s) {
+  constexpr int d = P >> 5, o = P & 31;
+  if constexpr (o < 3) {
+    return (s[d] << (3 - o)) & 0x7FF8u;
+  } else if constexpr (o <= 20) {
+    return (s[d] >> (o - 3)) & 0x7FF8u;
+  } else {
+    return __builtin_amdgcn_alignbit(s[d + 1], s[d], o - 3) & 0x7FF8u;
+  }
+}
+
+__device__ __forceinline__ h8_t splat8(_Float16 v) { return h8_t{v, v, v, v, v, v, v, v}; }
+
+template <int NMAT, int EPI>
+__device__ __forceinline__ void epilogue(const SkArgs& a, const f4_t* acc, int tile, int col, int kq) {
+  const int n = tile * 16 + col;
+  if (n >= a.N) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * kq + r;
+    if (m >= a.M) break;
+    const size_t o = (size_t)m * a.ostride + n;
+    if constexpr (EPI == EPI_SWIGLU) {
+      reinterpret_cast<uint16_t*>(a.out)[o] = tlx_swiglu_bits(acc[0][r], acc[1][r]);
+    } else if constexpr (EPI == EPI_RESID) {
+      reinterpret_cast<float*>(a.out)[o] = a.res[o] + (float)(_Float16)acc[0][r];
+    } else {
+      reinterpret_cast<uint16_t*>(a.out)[o] = tlx_f2h_bits(acc[0][r]);
+    }
+  }
+}
+
+// first unit of global wave gw (of GW): ranges are equal to within one unit
+__device__ __forceinline__ int unit_of(int gw, int GW, int U) { return (int)(((long)gw * U) / GW); }
+
+// Activations staged in LDS (rows of 2K + 16 bytes: the 16 rows one MFMA fragment reads are in
+// distinct 16-B slots) when they fit; the partial tiles reuse the space after the loop.
+constexpr int kXsBytes = 120 * 1024;
+constexpr int kXsWaves = 8;                                   // workgroup size of the staged form
+constexpr int kXsPer = kXsBytes / 16 / (kXsWaves * TLX_WAVE); // 16-B pieces per thread
+
+template <int NMAT, int W, bool XL>
+struct SkLds {
+  u2_t tbl[kTblEntries];                 // first: table byte offsets are LDS addresses
+  union {
+    f4_t part[W][2][NMAT][TLX_WAVE];     // partial tiles: [wave][first | last tile]
+    uint8_t xs[XL ? kXsBytes : 16];      // staged activations [M][2K + 16 B]
+  };
+};
+
+// Contribution of one record to the lane's MFMA fragment(s): d/4 * sum_c X[c] . B_c, with B_c
+// the chunk's 8 signed grid values times (2s+1) (exact fp16).
+template <int NMAT>
+__device__ __forceinline__ void rec_dot(f4_t* out, float* dq, const Rec<NMAT>& R, const h8_t* X, const uint8_t* tb,
+                                        int kq) {
+  // (2s+1) for the lane's two sub-blocks 2kq, 2kq+1; the 1/4 goes with d
+  _Float16 ks[NMAT][2];
+  uint32_t sv[NMAT][6];
+#pragma unroll
+  for (int i = 0; i < NMAT; ++i) {
+    const uint32_t s2 = R.sc[i] >> (8 * kq);
+    ks[i][0] = (_Float16)(float)(2u * (s2 & 15u) + 1u);
+    ks[i][1] = (_Float16)(float)(2u * ((s2 >> 4) & 15u) + 1u);
+    sv[i][0] = R.A[i].x; sv[i][1] = R.A[i].y; sv[i][2] = R.A[i].z; sv[i][3] = R.A[i].w;
+    sv[i][4] = R.B[i].x; sv[i][5] = R.B[i].y;
+    out[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  // chunk-major: the matrices' MFMA chains interleave, so consecutive MFMAs are independent
+#define TLX_CHUNK(c)                                                                                   \
+  _Pragma("unroll") for (int i = 0; i < NMAT; ++i) {                                                   \
+    const u2_t lo = *reinterpret_cast<const u2_t*>(tb + field_off<24 * (c)>(sv[i]));                   \
+    const u2_t hi = *reinterpret_cast<const u2_t*>(tb + field_off<24 * (c) + 12>(sv[i]));              \
+    const h8_t Bv = __builtin_bit_cast(h8_t, u4_t{lo.x, lo.y, hi.x, hi.y}) * splat8(ks[i][(c) >> 2]);   \
+    out[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(X[c], Bv, out[i], 0, 0, 0);                        \
+  }
+  TLX_CHUNK(0) TLX_CHUNK(1) TLX_CHUNK(2) TLX_CHUNK(3)
+  TLX_CHUNK(4) TLX_CHUNK(5) TLX_CHUNK(6) TLX_CHUNK(7)
+#undef TLX_CHUNK
+#pragma unroll
+  for (int i = 0; i < NMAT; ++i) dq[i] = tlx_h2f((uint16_t)R.d[i]) * 0.25f;
+}
+
+// first record of global wave gw: ranges are equal to within one record
+__device__ __forceinline__ int range_begin(int gw, int GW, int U) { return unit_of(gw, GW, U); }
+
+// XM: where the activations come from -- 0: x [M][K] in global memory, 1: the tile-ordered copy
+// [K/8][16][8] in global memory, 2: x staged into LDS by the workgroup (W == kXsWaves).
+template <int NMAT, int EPI, int W, int XM>
+__global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
+  __shared__ SkLds<NMAT, W, XM == 2> L;
+  constexpr bool XT = XM == 1;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int col = lane & 15, kq = lane >> 4;
+  const int nb = a.nb, GW = a.G * W, gw = (int)blockIdx.x * W + wave;
+  const int ubeg = range_begin(gw, GW, a.U), uend = range_begin(gw + 1, GW, a.U);
+  const bool empty = ubeg >= uend;   // only when there are fewer records than waves
+  const int last = max(min(uend, a.U) - 1, 0);
+  __amdgpu_buffer_rsrc_t rs[NMAT];
+  rs[0] = rsrc_of(a.w0, (uint32_t)a.U * kRec);
+  if constexpr (NMAT == 2) rs[1] = rsrc_of(a.w1, (uint32_t)a.U * kRec);
+  // activations: block b, chunk c of lane (col, kq) at byte xv + b * xbs + c * xcs
+  constexpr int xbs = XT ? 8192 : 512, xcs = XT ? 256 : 16;
+  const __amdgpu_buffer_rsrc_t rx = rsrc_of(a.x, XT ? (uint32_t)a.K * 32u : (uint32_t)(a.M * a.K) * 2u);
+  const int xv = XT ? 2 * (1024 * kq + 8 * col) : 2 * (min(col, a.M - 1) * a.K + 64 * kq);
+  const int xstr = 2 * a.K + 16;                                  // staged row bytes
+  const uint8_t* xsl = L.xs + min(col, a.M - 1) * xstr + 128 * kq;  // this lane's row, k = 64kq
+  auto xload = [&](h8_t* X, int u) {
+    const int b = u % nb;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      if constexpr (XM == 2)
+        X[c] = *reinterpret_cast<const h8_t*>(xsl + 512 * b + 16 * c);
+      else
+        X[c] = __builtin_bit_cast(h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, xv + xcs * c, xbs * b, 0));
+    }
+  };
+
+  // Record ring: record s is requested 3 records ahead of its use (4 buffers); activations one
+  // unit ahead (2 sets).  Issue order X(s+1), R(s+3), X(s+2), R(s+4), ...: the wait for record s
+  // and X(s) leaves the next three records and X(s+1) in flight.  The first loads are issued
+  // before the table is built (their latency covers it); the grid words the thread turns into
+  // table entries are loaded first, so waiting for them leaves the records in flight.
+  constexpr int kGw = 1024 / (W * TLX_WAVE);   // grid words (x 4 sign nibbles) per thread
+  float4 gv[kGw];
+  // staged activations: 16-B pieces p = thread + j * blockDim of x (clamped to the last piece:
+  // loads stay unconditional, a repeated piece is stored twice with the same bytes)
+  constexpr int kXp = XM == 2 ? kXsPer : 1;
+  u4_t xp[kXp];
+  const int npc = a.M * a.K / 8;
+  if constexpr (XM == 2) {
+#pragma unroll
+    for (int j = 0; j < kXp; ++j)
+      xp[j] = __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rx, 16 * min((int)threadIdx.x + j * W * TLX_WAVE, npc - 1), 0, 0));
+  }
+#pragma unroll
+  for (int j = 0; j < kGw; ++j) gv[j] = reinterpret_cast<const float4*>(a.gridf)[(threadIdx.x + j * W * TLX_WAVE) & 255];
+  // (scheduling barriers keep each record's loads together and the records in order: the wait
+  // counts in the loop assume that order on entry)
+  Rec<NMAT> R[4];
+  h8_t X[2][8];
+  __builtin_amdgcn_sched_barrier(0);
+  rec_load<NMAT>(R[0], rs, min(ubeg, last) * (int)kRec, lane, col);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (XM != 2) xload(X[0], min(ubeg, last));
+#pragma unroll
+  for (int j = 1; j < 4; ++j) {
+    __builtin_amdgcn_sched_barrier(0);
+    rec_load<NMAT>(R[j], rs, min(ubeg + j, last) * (int)kRec, lane, col);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (XM == 2) {
+    const int kp = a.K / 8;   // pieces per row
+#pragma unroll
+    for (int j = 0; j < kXp; ++j) {
+      const int p = min((int)threadIdx.x + j * W * TLX_WAVE, npc - 1);
+      *reinterpret_cast<u4_t*>(L.xs + (p / kp) * xstr + 16 * (p % kp)) = xp[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kGw; ++j) {
+    const int e = threadIdx.x + j * W * TLX_WAVE;   // grid word e & 255, sign nibbles 4(e >> 8) ..
+    tlx_iq3_table_entries(L.tbl, gv[j], e & 255, e >> 8);
+  }
+  __syncthreads();
+  if constexpr (XM == 2) xload(X[0], min(ubeg, last));
+  const uint8_t* tb = reinterpret_cast<const uint8_t*>(L.tbl);
+
+  // a wave touches at most two tiles: records < split belong to the first
+  const int tfirst = ubeg / nb, tlast = empty ? tfirst : (uend - 1) / nb;
+  const int split = min(uend, (tfirst + 1) * nb);
+  f4_t accA[NMAT], accB[NMAT];
+#pragma unroll
+  for (int i = 0; i < NMAT; ++i) accA[i] = accB[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+  auto accum = [&](const f4_t* D, const float* dq, int s) {
+    // wave-uniform 0/1 factors on the block scale pick the tile (no branch in the loop)
+    const float fA = s < split ? 1.f : 0.f;
+    const float fB = s >= split ? 1.f : 0.f;
+#pragma unroll
+    for (int i = 0; i < NMAT; ++i) {
+      accA[i] += (dq[i] * fA) * D[i];
+      accB[i] += (dq[i] * fB) * D[i];
+    }
+  };
+  // full rounds of 4 records: branch-free (a branch in the loop makes the wait counts conservative)
+  const int nfull = empty ? 0 : (uend - ubeg) & ~3;
+  for (int u = ubeg; u < ubeg + nfull; u += 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int s = u + j;
+      __builtin_amdgcn_sched_barrier(0);
+      xload(X[(j + 1) & 1], min(s + 1, last));
+      f4_t D[NMAT];
+      float dq[NMAT];
+      rec_dot<NMAT>(D, dq, R[j], X[j & 1], tb, kq);
+      accum(D, dq, s);
+      __builtin_amdgcn_sched_barrier(0);
+      rec_load<NMAT>(R[j], rs, min(s + 4, last) * (int)kRec, lane, col);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // the last 0..3 records: already in R[0..2] and X[0]; nothing more to load
+  const int rem = empty ? 0 : (uend - ubeg) & 3;
+  const int ut = ubeg + nfull;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    if (j < rem) {
+      f4_t D[NMAT];
+      float dq[NMAT];
+      if (j > 0) xload(X[j & 1], ut + j);
+      rec_dot<NMAT>(D, dq, R[j], X[j & 1], tb, kq);
+      accum(D, dq, ut + j);
+    }
+  }
+  if constexpr (XM == 2) __syncthreads();   // the parts overwrite the staged activations
+  if (!empty) {
+#pragma unroll
+    for (int i = 0; i < NMAT; ++i) {
+      L.part[wave][0][i][lane] = accA[i];
+      L.part[wave][1][i][lane] = accB[i];
+    }
+  }
+  __syncthreads();
+
+  // each tile is finished by the lowest wave of the workgroup that touches it: that wave adds
+  // the parts of the waves touching the tile in wave order
+  const int GWb = (int)blockIdx.x * W;
+  const int u0 = range_begin(GWb, GW, a.U), u1 = range_begin(GWb + W, GW, a.U);
+  for (int k = 0; k < (empty ? 0 : 2); ++k) {
+    const int t = k == 0 ? tfirst : tlast;
+    if (k == 1 && tlast == tfirst) break;
+    if (k == 0 && wave > 0 && ubeg % nb != 0) continue;   // a lower wave touches it
+    f4_t acc[NMAT];
+#pragma unroll
+    for (int i = 0; i < NMAT; ++i) acc[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+    for (int v = wave; v < W; ++v) {
+      const int vb = range_begin(GWb + v, GW, a.U);
+      if (vb >= (t + 1) * nb) break;
+      if (range_begin(GWb + v + 1, GW, a.U) == vb) continue;   // an empty range
+      const int slot = vb / nb == t ? 0 : 1;
+#pragma unroll
+      for (int i = 0; i < NMAT; ++i) acc[i] += L.part[v][slot][i][lane];
+    }
+    const bool lo_out = t * nb < u0, hi_out = (t + 1) * nb > u1;
+    if (!lo_out && !hi_out) {
+      epilogue<NMAT, EPI>(a, acc, t, col, kq);
+      continue;
+    }
+    // shared with the neighbouring workgroup: boundary g = the upper workgroup's index; part 0
+    // holds the lower workgroup's (earlier k) sum, part 1 the upper's
+    const int g = lo_out ? (int)blockIdx.x : (int)blockIdx.x + 1;
+    // Every access to the parts and the counter is an agent-scope atomic, coherent across the
+    // XCDs' L2s by itself, so no cache-wide write-back or invalidate is needed: the workgroup
+    // fence only waits for this wave's part stores to complete before the counter moves, and the
+    // part loads issue after the counter's value has returned.
+    uint64_t* pp = reinterpret_cast<uint64_t*>(a.part + (size_t)g * 2 * NMAT * TLX_WAVE);
+    const int mine = lo_out ? 1 : 0;
+#pragma unroll
+    for (int i = 0; i < NMAT; ++i) {
+      const u4_t v = __builtin_bit_cast(u4_t, acc[i]);
+      uint64_t* q = pp + 2 * ((mine * NMAT + i) * TLX_WAVE + lane);
+      __hip_atomic_store(q, (uint64_t)v.x | (uint64_t)v.y << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(q + 1, (uint64_t)v.z | (uint64_t)v.w << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    uint32_t prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(&a.cnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0);
+    if (prev != 1u) continue;                              // the other part is not there yet
+#pragma unroll
+    for (int i = 0; i < NMAT; ++i) {
+      uint64_t w[2][2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint64_t* q = pp + 2 * ((h * NMAT + i) * TLX_WAVE + lane);
+        w[h][0] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        w[h][1] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      const f4_t lo = __builtin_bit_cast(f4_t, u4_t{(uint32_t)w[0][0], (uint32_t)(w[0][0] >> 32),
+                                                    (uint32_t)w[0][1], (uint32_t)(w[0][1] >> 32)});
+      const f4_t hi = __builtin_bit_cast(f4_t, u4_t{(uint32_t)w[1][0], (uint32_t)(w[1][0] >> 32),
+                                                    (uint32_t)w[1][1], (uint32_t)(w[1][1] >> 32)});
+      acc[i] = lo + hi;                                    // lower range first: a fixed order
+    }
+    epilogue<NMAT, EPI>(a, acc, t, col, kq);
+    if (lane == 0) __hip_atomic_store(&a.cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+template <int NMAT, int EPI, int W>
+void sk_launch(const SkArgs& a, hipStream_t st) {
+  if constexpr (W == kXsWaves) {
+    if (!a.xt && a.M * (2 * a.K + 16) <= kXsBytes) {
+      iq3s_kernel<NMAT, EPI, W, 2><<<a.G, W * TLX_WAVE, 0, st>>>(a);
+      return;
+    }
+  }
+  if (a.xt) iq3s_kernel<NMAT, EPI, W, 1><<<a.G, W * TLX_WAVE, 0, st>>>(a);
+  else iq3s_kernel<NMAT, EPI, W, 0><<<a.G, W * TLX_WAVE, 0, st>>>(a);
+}
+
+template <int NMAT, int EPI>
+int sk_dispatch(int W, const SkArgs& a, hipStream_t st) {
+  switch (W) {
+    case 8: sk_launch<NMAT, EPI, 8>(a, st); break;
+    case 4: sk_launch<NMAT, EPI, 4>(a, st); break;
+    default: sk_launch<NMAT, EPI, 1>(a, st); break;
+  }
+  return tlx_launch_status();
+}
+
+}  // namespace
+
+// True when the tiled-record GEMV stages x [M][K] in LDS itself (no tile-ordered copy needed).
+bool tlx_iq3s_stages_x(int M, int K) { return M * (2 * K + 16) <= kXsBytes; }
+
+// Balanced GEMV over tiled records (called by the IQ3_XXS entry points of tlx_iq3.hip, which
+// have validated the arguments and prepared x / xt).  nmat 2 = SwiGLU pair, epi as Epi.
+int tlx_iq3s_launch(int nmat, int epi, const void* w0, const void* w1, void* out, const float* res,
+                    const float* gridf, const _Float16* x, int xt, int M, int N, int K, hipStream_t st) {
+  void* ws = nullptr;
+  const int rc = tlx_workspace(&ws);
+  TLX_RET_IF(rc != TLX_OK, rc);
+  SkArgs a{};
+  a.w0 = (const uint8_t*)w0;
+  a.w1 = (const uint8_t*)w1;
+  a.out = out;
+  a.res = res;
+  a.gridf = gridf;
+  a.x = x;
+  a.xt = xt;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.nb = K / 256;
+  a.part = reinterpret_cast<f4_t*>(static_cast<uint8_t*>(ws) + kWsPartOff);
+  a.cnt = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ws) + kWsCntOff);
+  const int T = (N + 15) / 16, nb = a.nb;
+  const int G0 = std::min(tlx_cu_count(), kMaxG);
+  constexpr int Wd = 8;   // 2 waves per SIMD, ~190 VGPRs each: the record ring and two activation sets
+  // A launch covers at most G0 * Wd tiles, so a wave's range (<= nb + 1 records) touches at most
+  // two tiles; larger matrices take several launches over consecutive tiles.
+  for (int t0 = 0; t0 < T; t0 += G0 * Wd) {
+    const int T1 = std::min(T - t0, G0 * Wd);
+    SkArgs b = a;
+    const size_t rec0 = (size_t)t0 * nb * kRec;
+    b.w0 = a.w0 + rec0;
+    b.w1 = a.w1 ? a.w1 + rec0 : nullptr;
+    b.N = std::min(N - t0 * 16, T1 * 16);
+    b.out = (uint8_t*)out + (size_t)t0 * 16 * (epi == EPI_RESID ? 4 : 2);
+    b.res = res ? res + (size_t)t0 * 16 : nullptr;
+    b.U = T1 * nb;
+    b.ostride = N;
+    // every wave gets >= 1 record; G <= T1 makes a workgroup cover >= nb records, so a tile
+    // spans at most two workgroups
+    int W = Wd;
+    int G = std::min(G0, T1);
+    if (b.U < G * W) G = std::max(1, b.U / W);
+    while (W > 1 && b.U < G * W) W = W > 4 ? W / 2 : 1;
+    b.G = G;
+    int rc;
+    if (nmat == 2) rc = sk_dispatch<2, EPI_SWIGLU>(W, b, st);
+    else if (epi == EPI_RESID) rc = sk_dispatch<1, EPI_RESID>(W, b, st);
+    else rc = sk_dispatch<1, EPI_F16>(W, b, st);
+    TLX_RET_IF(rc != TLX_OK, rc);
+  }
+  return TLX_OK;
+}
+
+extern "C" int tlx_pack_iq3_tiled(const void* src, void* tiled, int N, int K, int src_layout, void* stream) {
+  TLX_RET_IF(N < 1 || K < 256 || (K % 256), TLX_E_ARG);
+  TLX_RET_IF(src_layout != TLX_LAYOUT_RAW && src_layout != TLX_LAYOUT_PACKED, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(src, 2) || !tlx_aligned(tiled, 16), TLX_E_ALIGN);
+  const long nslots = (long)((N + 15) / 16) * (K / 256) * 64;
+  pack_tiled_kernel<<<(unsigned)((nslots + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      (const uint8_t*)src, (uint8_t*)tiled, nslots, N, K / 256, src_layout == TLX_LAYOUT_RAW);
+  return tlx_launch_status();
+}

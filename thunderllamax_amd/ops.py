@@ -8,7 +8,7 @@ allocated here.  Errors raise ``TlxError`` (the reference asserts in Python).
 """
 import torch
 
-from ._lib import LAYOUT_PACK7, LAYOUT_PACKED, LAYOUT_RAW, V_Q4K, call
+from ._lib import LAYOUT_PACK7, LAYOUT_PACKED, LAYOUT_RAW, LAYOUT_TILED, V_Q4K, call
 
 _F16 = torch.float16
 
@@ -40,6 +40,14 @@ def _need(t, nbytes, what):
 
 def _iq3_rows(n, k):
     return n * 98 * (k // 256)
+
+
+def _iq3_w(n, k, layout):
+    """Bytes of an IQ3_XXS matrix of n rows in `layout` (tiled: 102-B records of whole 16-row
+    tiles)."""
+    if layout == LAYOUT_TILED:
+        return (n + 15) // 16 * 16 * 102 * (k // 256)
+    return _iq3_rows(n, k)
 
 
 def _pack7(n, k):
@@ -80,8 +88,8 @@ def iq4xs_dequant(w, iq4nl, out, kdim, stream=None):
 def ffn8(wg, wu, gridf, hhx, gact, layout=LAYOUT_PACKED, stream=None):
     """gact[m] = silu16(half(Wg·hhx[m])) * half(Wu·hhx[m])   (ffn8 / ffn8v{M})."""
     M, K, N = _mk(hhx), hhx.shape[-1], gact.shape[-1]
-    _need(wg, _iq3_rows(N, K), "wg")
-    _need(wu, _iq3_rows(N, K), "wu")
+    _need(wg, _iq3_w(N, K, layout), "wg")
+    _need(wu, _iq3_w(N, K, layout), "wu")
     _need(gridf, 4096, "gridf")
     _need(gact, M * N * 2, "gact")
     _dev(wg, wu, gridf, hhx, gact)
@@ -116,8 +124,8 @@ def add_rms_f16(x, a, nw, hh, hhx, stream=None):
 def ffn8_hh(wg, wu, gridf, x, attn_out, nw2, hh, hhx, gact, layout=LAYOUT_PACKED, stream=None):
     """hh{M} + ffn8 in one call: hh = x + float(attn_out), hhx = norm(hh), gact = ffn8(hhx)."""
     M, K, N = x.shape[0], x.shape[1], gact.shape[-1]
-    _need(wg, _iq3_rows(N, K), "wg")
-    _need(wu, _iq3_rows(N, K), "wu")
+    _need(wg, _iq3_w(N, K, layout), "wg")
+    _need(wu, _iq3_w(N, K, layout), "wu")
     _need(gridf, 4096, "gridf")
     _need(attn_out, M * K * 2, "attn_out")
     _need(nw2, K * 4, "nw2")
@@ -133,7 +141,7 @@ def ffn8_hh(wg, wu, gridf, x, attn_out, nw2, hh, hhx, gact, layout=LAYOUT_PACKED
 def down8(wd, gridf, gact, hh, y, layout=LAYOUT_PACKED, stream=None):
     """y[m] = hh[m] + float(half(Wd·gact[m]))   (down8 / down8nw32_{M})."""
     M, K, N = _mk(gact), gact.shape[-1], y.shape[-1]
-    _need(wd, _iq3_rows(N, K), "wd")
+    _need(wd, _iq3_w(N, K, layout), "wd")
     _need(gridf, 4096, "gridf")
     _need(hh, M * N * 4, "hh")
     _need(y, M * N * 4, "y")
@@ -146,7 +154,7 @@ def down8(wd, gridf, gact, hh, y, layout=LAYOUT_PACKED, stream=None):
 def iq3_gemv(w, gridf, x, out, layout=LAYOUT_PACKED, stream=None):
     """out[m] = half(W·x[m])   (the IQ3ROWP segment body)."""
     M, K, N = _mk(x), x.shape[-1], out.shape[-1]
-    _need(w, _iq3_rows(N, K), "w")
+    _need(w, _iq3_w(N, K, layout), "w")
     _need(gridf, 4096, "gridf")
     _need(out, M * N * 2, "out")
     _dev(w, gridf, x, out)
@@ -314,6 +322,17 @@ def pack_w7(packed, p7, N, K, stream=None):
     _dev(packed, p7)
     call("tlx_pack_w7", packed.data_ptr(), p7.data_ptr(), N, K, _stream(stream))
     return p7
+
+
+def pack_iq3_tiled(src, tiled, N, K, src_layout=LAYOUT_PACKED, stream=None):
+    """IQ3_XXS rows (GGUF blocks or packed rows) -> the tile-major records the decode GEMVs read
+    with ``layout=LAYOUT_TILED`` (ceil(N/16) * K/256 * 1632 B: the GGUF bytes re-encoded with the
+    per-chunk table indices precomputed)."""
+    _need(src, _iq3_rows(N, K), "src")
+    _need(tiled, _iq3_w(N, K, LAYOUT_TILED), "tiled")
+    _dev(src, tiled)
+    call("tlx_pack_iq3_tiled", src.data_ptr(), tiled.data_ptr(), N, K, src_layout, _stream(stream))
+    return tiled
 
 
 def p8_quant(x16, xq, sx, rs, stream=None):
