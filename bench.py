@@ -12,7 +12,11 @@ figure is HBM bandwidth, not cache bandwidth.  W untimed warmup steps, then exac
 timed steps -- captured in one HIP graph, as a decode step replays its launches -- bracketed
 by device synchronization, timed with HIP events recorded on the stream the graph replays on
 (the current stream).
-From M=6 on a step is two launches (the tile-ordered activation copy, then the GEMV).
+The headline layout (``--layout``, default ``tiled``) is the library's tiled records (the GGUF
+blocks re-encoded with precomputed table indices, 102 B per 256 weights, repacked on the GPU);
+``value`` still counts the GGUF bytes (98 per 256 weights), so it is the rate at which the
+quantized model streams.  ``per_m_other_layout`` times the reference's packed rows (pack_w1c),
+where from M=6 on a step is two launches (the tile-ordered activation copy, then the GEMV).
 
 ``cpu_baseline`` times the numpy restatement of the reference's CPU path (dequantize, then
 an fp32 matmul) on a bounded sample of rows of the same workload, on this host's cores.
@@ -57,6 +61,9 @@ PEAK_HBM_GBS = 8000.0
 # FETCH_SIZE = 131,089 KiB and WRITE_SIZE = 262,144 KiB, so fetches are scaled by 2.0, writes
 # by 1.0.  Re-measure when the kernel changes.
 FFN8_M11_TRAFFIC_BYTES = 75_608_191
+# The same for the tiled-record kernel (one launch; FETCH_SIZE 35,970.3 KiB, WRITE_SIZE 1,928 KiB at
+# M=11 with the same calibration; profiles/iq3s_ffn8_tiled_k5120_n17408.md).
+FFN8_TILED_M11_TRAFFIC_BYTES = 75_641_446
 PEAK_F16_TFLOPS = 2500.0
 PEAK_I8_TOPS = 5000.0
 ROT_BYTES = 300 * 2**20
@@ -194,15 +201,24 @@ def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup):
     }
 
 
-def producers_leg(ops, formats, synth, torch, dev, steps, warmup, M=11):
+def producers_leg(ops, formats, synth, torch, dev, steps, warmup, M=11, tiled=True):
     """The activation producer before the FFN GEMV (hh{M}: residual add + RMSNorm -> fp16) at
     config 2's D=5120, alone, followed by ffn8, and fused with it (tlx_ffn8_hh), as graph
-    replays over rotated FFN weights."""
+    replays over rotated FFN weights (tiled records or packed rows)."""
+    from thunderllamax_amd._lib import LAYOUT_PACKED, LAYOUT_TILED
     K, N = 5120, 17408
     rng = synth.config_rng(2)
-    copies = [(torch.from_numpy(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, N, K), K)).to(dev),
-               torch.from_numpy(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, N, K), K)).to(dev))
-              for _ in range(max(1, -(-ROT_BYTES // (2 * N * 98 * (K // 256)))))]
+    lay = LAYOUT_TILED if tiled else LAYOUT_PACKED
+
+    def mat():
+        w = torch.from_numpy(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, N, K), K)).to(dev)
+        if not tiled:
+            return w
+        t = torch.empty(N * 102 * (K // 256), dtype=torch.uint8, device=dev)
+        ops.pack_iq3_tiled(w, t, N, K)
+        return t
+
+    copies = [(mat(), mat()) for _ in range(max(1, -(-ROT_BYTES // (2 * N * 98 * (K // 256)))))]
     gridf = formats.gridf_tensor(dev)
     x = torch.randn(M, K, device=dev)
     a = torch.randn(M, K, device=dev).half()
@@ -219,16 +235,17 @@ def producers_leg(ops, formats, synth, torch, dev, steps, warmup, M=11):
     def sep(s):
         wg, wu = pick()
         ops.add_rms_f16(x, a, nw, hh, hhx, stream=s)
-        ops.ffn8(wg, wu, gridf, hhx, g, stream=s)
+        ops.ffn8(wg, wu, gridf, hhx, g, layout=lay, stream=s)
 
     def fused(s):
         wg, wu = pick()
-        ops.ffn8_hh(wg, wu, gridf, x, a, nw, hh, hhx, g, stream=s)
+        ops.ffn8_hh(wg, wu, gridf, x, a, nw, hh, hhx, g, layout=lay, stream=s)
 
     t_norm = time_graph(lambda s: ops.add_rms_f16(x, a, nw, hh, hhx, stream=s), steps, warmup, torch)
     t_sep = time_graph(sep, steps, warmup, torch)
     t_fused = time_graph(fused, steps, warmup, torch)
     return {"workload": f"hh{{M}} producer (D={K}) + ffn8 (N=2x{N}), M={M}",
+            "iq3_layout": "tiled records" if tiled else "packed rows",
             "add_rms_us": round(t_norm * 1e3, 2), "add_rms_then_ffn8_us": round(t_sep * 1e3, 2),
             "ffn8_hh_us": round(t_fused * 1e3, 2)}
 
@@ -289,9 +306,12 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
     return out
 
 
-def sweep_leg(ops, formats, torch, dev, steps, warmup):
-    """Config 3: the 64-layer dense decode step at M=11 plus the Q6_K head."""
-    from thunderllamax_amd._lib import LAYOUT_RAW
+def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True):
+    """Config 3: the 64-layer dense decode step at M=11 plus the Q6_K head.  With ``tiled`` the
+    IQ3_XXS FFN and plain projections read tiled records (repacked on the GPU from the packed
+    rows); the fused q/k/v projections read packed rows either way."""
+    from thunderllamax_amd._lib import LAYOUT_PACKED, LAYOUT_RAW, LAYOUT_TILED
+    lay = LAYOUT_TILED if tiled else LAYOUT_PACKED
     H, F, M = 5120, 17408, 11
     gen = torch.Generator(device=dev)
     gen.manual_seed(20261204)
@@ -302,6 +322,14 @@ def sweep_leg(ops, formats, torch, dev, steps, warmup):
         w = torch.randint(0, 256, (rows, 98 * nb), dtype=torch.uint8, device=dev, generator=gen)
         w[:, 96 * nb:].view(torch.int16).fill_(dbits)
         return w
+
+    def iq3t(rows, k):     # the same, as tiled records when ``tiled``; bytes counted as GGUF
+        w = iq3(rows, k)
+        if not tiled:
+            return w, w.numel()
+        t = torch.empty((rows + 15) // 16 * 16 * 102 * (k // 256), dtype=torch.uint8, device=dev)
+        ops.pack_iq3_tiled(w, t, rows, k)
+        return t, w.numel()
 
     def q6(rows, k):       # GGUF 210-B blocks, d at bytes 208..209
         nb = k // 256
@@ -322,7 +350,8 @@ def sweep_leg(ops, formats, torch, dev, steps, warmup):
     for layer in range(64):
         c0 = len(calls)
         if layer % 4 == 3:   # full attention
-            wk, wv, wo = iq3(1024, H), iq3(1024, H), iq3(H, 6144)
+            wk, wv = iq3(1024, H), iq3(1024, H)
+            wo, nbo = iq3t(H, 6144)
             if layer in q6_layers:
                 wq = q6(12288, H)
                 calls.append(lambda s, wq=wq, wk=wk, wv=wv: ops.aq6k8(wq, wk, wv, gridf, xs[H], o[12288], o[1024], vrow, layout=LAYOUT_RAW, stream=s))
@@ -331,19 +360,19 @@ def sweep_leg(ops, formats, torch, dev, steps, warmup):
                 wq = iq3(12288, H)
                 calls.append(lambda s, wq=wq, wk=wk, wv=wv: ops.aq3k8(wq, wk, wv, gridf, xs[H], o[12288], o[1024], vrow, stream=s))
                 kind = "attn_iq3"
-            calls.append(lambda s, w=wo: ops.iq3_gemv(w, gridf, xs[6144], o[H], stream=s))
-            nbytes += wq.numel() + wk.numel() + wv.numel() + wo.numel()
+            calls.append(lambda s, w=wo: ops.iq3_gemv(w, gridf, xs[6144], o[H], layout=lay, stream=s))
+            nbytes += wq.numel() + wk.numel() + wv.numel() + nbo
         else:                # gated delta net projections
-            ws = [(iq3(10240, H), H, 10240), (iq3(6144, H), H, 6144), (iq3(48, H), H, 48),
-                  (iq3(48, H), H, 48), (iq3(H, 6144), 6144, H)]
-            for w, k, n in ws:
-                calls.append(lambda s, w=w, k=k, n=n: ops.iq3_gemv(w, gridf, xs[k], o[n], stream=s))
-                nbytes += w.numel()
+            ws = [(iq3t(10240, H), H, 10240), (iq3t(6144, H), H, 6144), (iq3t(48, H), H, 48),
+                  (iq3t(48, H), H, 48), (iq3t(H, 6144), 6144, H)]
+            for (w, nbw), k, n in ws:
+                calls.append(lambda s, w=w, k=k, n=n: ops.iq3_gemv(w, gridf, xs[k], o[n], layout=lay, stream=s))
+                nbytes += nbw
             kind = "gdn"
-        wg, wu, wd = iq3(F, H), iq3(F, H), iq3(H, F)
-        calls.append(lambda s, wg=wg, wu=wu: ops.ffn8(wg, wu, gridf, xs[H], o[F], stream=s))
-        calls.append(lambda s, wd=wd: ops.down8(wd, gridf, xs[F], hh, y, stream=s))
-        nbytes += wg.numel() + wu.numel() + wd.numel()
+        (wg, nbg), (wu, nbu), (wd, nbd) = iq3t(F, H), iq3t(F, H), iq3t(H, F)
+        calls.append(lambda s, wg=wg, wu=wu: ops.ffn8(wg, wu, gridf, xs[H], o[F], layout=lay, stream=s))
+        calls.append(lambda s, wd=wd: ops.down8(wd, gridf, xs[F], hh, y, layout=lay, stream=s))
+        nbytes += nbg + nbu + nbd
         kinds[kind].append((c0, len(calls)))
     wh = q6(151936, H)
     c0 = len(calls)
@@ -384,6 +413,7 @@ def sweep_leg(ops, formats, torch, dev, steps, warmup):
     gbs = nbytes / (t_step * 1e-3) / 1e9
     return {"workload": "dense hybrid decode step, M=11: 48 GDN + 16 attention layers (8 with a Q6_K q), "
                         "FFN 17408, Q6_K head 151936x5120",
+            "iq3_layout": "tiled records (FFN, plain projections)" if tiled else "packed rows",
             "M": M, "launches": len(calls), "weight_bytes": nbytes, "ms": round(t_step, 4),
             "weight_gbs": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
             "per_layer_kind": per_kind}
@@ -500,7 +530,8 @@ def main():
         "per_m_other_layout": {"layout": other, **per_m_other},
         "roofline": {"bound": "hbm", "achieved": value, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(value / PEAK_HBM_GBS, 4),
-                     "traffic": (FFN8_M11_TRAFFIC_BYTES if head == "11" and args.layout == "packed" else None),
+                     "traffic": (None if head != "11" else
+                                 FFN8_TILED_M11_TRAFFIC_BYTES if args.layout == "tiled" else FFN8_M11_TRAFFIC_BYTES),
                      "algorithmic_bytes": wbytes + int(head) * K * 2 + int(head) * N * 2,
                      "kernel": ("iq3s_kernel<2,1,8,2> (tiled records, activations staged in LDS)"
                                 if args.layout == "tiled" else
@@ -510,10 +541,11 @@ def main():
         out["gemm"] = gemm_leg(ops, formats, synth, torch, dev, args.gemm_m, max(3, args.steps // 5),
                                max(1, args.warmup // 5))
     if not args.no_sweep:
-        out["sweep"] = sweep_leg(ops, formats, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5))
+        out["sweep"] = sweep_leg(ops, formats, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5),
+                                 tiled=args.layout == "tiled")
     if not args.no_formats:
         out["producers"] = producers_leg(ops, formats, synth, torch, dev, max(3, args.steps // 5),
-                                         max(1, args.warmup // 5))
+                                         max(1, args.warmup // 5), tiled=args.layout == "tiled")
     if not args.no_formats:
         out["formats"] = formats_leg(ops, synth, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5))
     if not args.no_moe:
