@@ -307,9 +307,9 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
 
 
 def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True):
-    """Config 3: the 64-layer dense decode step at M=11 plus the Q6_K head.  With ``tiled`` the
-    IQ3_XXS FFN and plain projections read tiled records (repacked on the GPU from the packed
-    rows); the fused q/k/v projections read packed rows either way."""
+    """Config 3: the 64-layer dense decode step at M=11 plus the Q6_K head.  With ``tiled`` every
+    IQ3_XXS tensor except the k/v rows beside a Q6_K q reads tiled records (repacked on the GPU
+    from the packed rows).  The four GDN projections that read the same x share one launch."""
     from thunderllamax_amd._lib import LAYOUT_PACKED, LAYOUT_RAW, LAYOUT_TILED
     lay = LAYOUT_TILED if tiled else LAYOUT_PACKED
     H, F, M = 5120, 17408, 11
@@ -341,6 +341,7 @@ def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True):
     xs = {k: torch.randn(M, k, device=dev).half() for k in (H, 6144, F)}
     o = {n: torch.empty(M, n, dtype=torch.float16, device=dev) for n in (10240, 6144, 48, 12288, 1024, H, F)}
     vrow = torch.empty(M, 1024, dtype=torch.float16, device=dev)
+    ab48 = torch.empty(M, 48, dtype=torch.float16, device=dev)
     hh = torch.randn(M, H, device=dev)
     y = torch.empty(M, H, device=dev)
     logits = torch.empty(M, 151936, dtype=torch.float16, device=dev)
@@ -350,24 +351,27 @@ def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True):
     for layer in range(64):
         c0 = len(calls)
         if layer % 4 == 3:   # full attention
-            wk, wv = iq3(1024, H), iq3(1024, H)
             wo, nbo = iq3t(H, 6144)
             if layer in q6_layers:
-                wq = q6(12288, H)
+                wq, wk, wv = q6(12288, H), iq3(1024, H), iq3(1024, H)
                 calls.append(lambda s, wq=wq, wk=wk, wv=wv: ops.aq6k8(wq, wk, wv, gridf, xs[H], o[12288], o[1024], vrow, layout=LAYOUT_RAW, stream=s))
+                nbytes += wq.numel() + wk.numel() + wv.numel()
                 kind = "attn_q6"
             else:
-                wq = iq3(12288, H)
-                calls.append(lambda s, wq=wq, wk=wk, wv=wv: ops.aq3k8(wq, wk, wv, gridf, xs[H], o[12288], o[1024], vrow, stream=s))
+                (wq, nbq), (wk, nbk), (wv, nbv) = iq3t(12288, H), iq3t(1024, H), iq3t(1024, H)
+                calls.append(lambda s, wq=wq, wk=wk, wv=wv: ops.aq3k8(wq, wk, wv, gridf, xs[H], o[12288], o[1024], vrow, layout=lay, stream=s))
+                nbytes += nbq + nbk + nbv
                 kind = "attn_iq3"
             calls.append(lambda s, w=wo: ops.iq3_gemv(w, gridf, xs[6144], o[H], layout=lay, stream=s))
-            nbytes += wq.numel() + wk.numel() + wv.numel() + nbo
+            nbytes += nbo
         else:                # gated delta net projections
-            ws = [(iq3t(10240, H), H, 10240), (iq3t(6144, H), H, 6144), (iq3t(48, H), H, 48),
-                  (iq3t(48, H), H, 48), (iq3t(H, 6144), 6144, H)]
-            for (w, nbw), k, n in ws:
-                calls.append(lambda s, w=w, k=k, n=n: ops.iq3_gemv(w, gridf, xs[k], o[n], layout=lay, stream=s))
-                nbytes += nbw
+            # qkv, gate, alpha, beta read the same x: one launch (tlx_iq3_gemv_multi); then ssm_out
+            proj = [iq3t(10240, H), iq3t(6144, H), iq3t(48, H), iq3t(48, H)]
+            pw = [w for w, _ in proj]
+            calls.append(lambda s, pw=pw: ops.iq3_gemv_multi(pw, gridf, xs[H], [o[10240], o[6144], o[48], ab48], layout=lay, stream=s))
+            wso, nbso = iq3t(H, 6144)
+            calls.append(lambda s, w=wso: ops.iq3_gemv(w, gridf, xs[6144], o[H], layout=lay, stream=s))
+            nbytes += sum(nb for _, nb in proj) + nbso
             kind = "gdn"
         (wg, nbg), (wu, nbu), (wd, nbd) = iq3t(F, H), iq3t(F, H), iq3t(H, F)
         calls.append(lambda s, wg=wg, wu=wu: ops.ffn8(wg, wu, gridf, xs[H], o[F], layout=lay, stream=s))
@@ -413,7 +417,7 @@ def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True):
     gbs = nbytes / (t_step * 1e-3) / 1e9
     return {"workload": "dense hybrid decode step, M=11: 48 GDN + 16 attention layers (8 with a Q6_K q), "
                         "FFN 17408, Q6_K head 151936x5120",
-            "iq3_layout": "tiled records (FFN, plain projections)" if tiled else "packed rows",
+            "iq3_layout": "tiled records" if tiled else "packed rows",
             "M": M, "launches": len(calls), "weight_bytes": nbytes, "ms": round(t_step, 4),
             "weight_gbs": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
             "per_layer_kind": per_kind}

@@ -91,9 +91,17 @@ int tlx_down8(const void* wd, const float* gridf, const uint16_t* gact_f16, cons
 int tlx_iq3_gemv(const void* w, const float* gridf, const uint16_t* x_f16, uint16_t* out_f16,
                  int M, int N, int K, int layout, void* stream);
 
+/* Up to four IQ3_XXS matrices that share the activations, one launch: out[s][m][r] =
+ * half(W_s[r]·x[m]), W_s of n[s] rows (w, out, n: host arrays of nseg entries; layout PACKED rows,
+ * RAW blocks or TILED records, the same for all).  With GGUF IQ3_XXS tensors this replaces the
+ * GDN block's separate projection launches k1_q5 / k1_iq3 / k1_ab
+ * (engine/gdn_block.cu:44-148: qkv, gate, alpha, beta all read the same normed x). */
+int tlx_iq3_gemv_multi(const void* const* w, uint16_t* const* out, const int* n, int nseg,
+                       const float* gridf, const uint16_t* x_f16, int M, int K, int layout, void* stream);
+
 /* Fused attention q/k/v projections (one entry per reference kernel; one launch per quant
  * format on `stream`; all arguments are validated before any launch):
- *   tlx_aq3k8: q, k (and v) IQ3_XXS in `layout` (PACKED rows or RAW blocks); v is IQ3_XXS
+ *   tlx_aq3k8: q, k (and v) IQ3_XXS in `layout` (PACKED rows, RAW blocks or TILED records); v is IQ3_XXS
  *     (the benchmark's dense configuration) unless `layout` has TLX_V_Q4K, then GGUF Q4_K (the reference's
  *     wv4).  Replaces aq3k8 / aq3k8v{4..11} (engine/aq3k8.cu:134-145, engine/aq3k8v11.cu:88-180):
  *     aq3k8(wq, wk, wv4, gridf, xh, qrow, krow, vrow).

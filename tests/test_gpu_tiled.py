@@ -15,7 +15,7 @@ import torch
 
 from oracle import gemv, layouts, quants
 from thunderllamax_amd import formats, ops, synth
-from thunderllamax_amd._lib import LAYOUT_RAW, LAYOUT_TILED, TlxError
+from thunderllamax_amd._lib import LAYOUT_PACKED, LAYOUT_RAW, LAYOUT_TILED, TlxError
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -164,6 +164,52 @@ def test_tiled_rejects_short_or_misaligned_buffers(gpu):
     big = torch.zeros(32 * 102 + 16, dtype=torch.uint8, device=gpu)
     with pytest.raises(TlxError):
         ops.iq3_gemv(big[8:], g, x, out, layout=LAYOUT_TILED)
-    q = torch.empty(1, 16, dtype=torch.float16, device=gpu)
-    with pytest.raises(TlxError):                   # the fused q/k/v projections take rows / blocks
-        ops.aq3k8(big, big, big, g, x, q, q, q, layout=LAYOUT_TILED)
+    with pytest.raises(ValueError):                 # five matrices: one launch takes at most four
+        ops.iq3_gemv_multi([big] * 5, g, x, [out] * 5, layout=LAYOUT_TILED)
+
+
+@pytest.mark.parametrize("M", [1, 11])
+@pytest.mark.parametrize("tiled", [True, False])
+def test_multi_matrix_parity(gpu, M, tiled):
+    """Four matrices sharing x in one launch (the GDN projections' shape pattern: a large, a
+    medium and two 48-row matrices) against the oracle; tiled calls are deterministic."""
+    print(f"[case] iq3_gemv_multi M={M} tiled={tiled}", flush=True)
+    rng = synth.config_rng(7)
+    K, ns = 5120, (1000, 600, 48, 48)
+    packed = [formats.iq3_pack_rows(synth.iq3xxs_raw(rng, n, K), K) for n in ns]
+    ws = [torch.from_numpy(p).to(gpu) for p in packed]
+    lay = LAYOUT_TILED if tiled else LAYOUT_PACKED
+    if tiled:
+        ws = [_tiled(gpu, w, n, K) for w, n in zip(ws, ns)]
+    x = synth.activations_f16(rng, M, K)
+    xd = torch.from_numpy(x).to(gpu)
+    g = formats.gridf_tensor(gpu)
+    outs = [torch.full((M, n), float("nan"), dtype=torch.float16, device=gpu) for n in ns]
+    ops.iq3_gemv_multi(ws, g, xd, outs, layout=lay)
+    again = [torch.empty_like(o) for o in outs]
+    ops.iq3_gemv_multi(ws, g, xd, again, layout=lay)
+    torch.cuda.synchronize()
+    for p, o, o2 in zip(packed, outs, again):
+        _, ref = gemv.gemv16_ref(quants.dequant_iq3xxs_packed(p, K), x)
+        err = _rows_err(o.cpu().numpy(), ref)
+        print(f"[multi M={M} tiled={tiled} N={p.shape[0]}] rel-err {err:.3e}")
+        assert err <= TOL
+        assert torch.equal(o.view(torch.int16), o2.view(torch.int16))
+
+
+def test_aq3k8_tiled_parity(gpu):
+    print("[case] aq3k8 tiled M=11", flush=True)
+    rng = synth.config_rng(8)
+    M, K, Nq, Nk, Nv = 11, 5120, 768, 128, 128
+    pq, tq = _mat(gpu, rng, Nq, K)
+    pk, tk = _mat(gpu, rng, Nk, K)
+    pv, tv = _mat(gpu, rng, Nv, K)
+    x = synth.activations_f16(rng, M, K)
+    q = torch.empty(M, Nq, dtype=torch.float16, device=gpu)
+    k = torch.empty(M, Nk, dtype=torch.float16, device=gpu)
+    v = torch.empty(M, Nv, dtype=torch.float16, device=gpu)
+    ops.aq3k8(tq, tk, tv, formats.gridf_tensor(gpu), torch.from_numpy(x).to(gpu), q, k, v, layout=LAYOUT_TILED)
+    torch.cuda.synchronize()
+    for p, o in ((pq, q), (pk, k), (pv, v)):
+        _, ref = gemv.gemv16_ref(quants.dequant_iq3xxs_packed(p, K), x)
+        assert _rows_err(o.cpu().numpy(), ref) <= TOL

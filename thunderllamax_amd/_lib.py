@@ -61,6 +61,7 @@ SIGNATURES = {
     "tlx_pack_iq3_rows": [_p, _p, _i, _i, _p],
     "tlx_pack_q6_pad": [_p, _p, _i, _i, _p],
     "tlx_pack_w7": [_p, _p, _i, _i, _p],
+    "tlx_iq3_gemv_multi": [_p, _p, _p, _i, _p, _p, _i, _i, _i, _p],
     "tlx_pack_iq3_tiled": [_p, _p, _i, _i, _i, _p],
     "tlx_p8w4_ffn": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_moe_topk": [_p, _p, _p, _i, _p],

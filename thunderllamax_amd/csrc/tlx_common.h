@@ -127,10 +127,11 @@ int tlx_iq3_segments(const void* const* w, uint16_t* const* out, const int* n, i
                      bool launch, void* stream);
 //   IQ3_XXS tiled records: the balanced GEMV (tlx_iq3s.hip); arguments already validated, x the
 //   activations or (xt != 0) their tile-ordered copy; nmat 2 = gate/up pair with epi SwiGLU,
-//   epi 0 = fp16 out, 2 = fp32 residual
+//   epi 0 = fp16 out, 2 = fp32 residual; up to 4 fp16-out matrices (nseg) share one launch
 bool tlx_iq3s_stages_x(int M, int K);
-int tlx_iq3s_launch(int nmat, int epi, const void* w0, const void* w1, void* out, const float* res,
-                    const float* gridf, const _Float16* x, int xt, int M, int N, int K, hipStream_t st);
+int tlx_iq3s_launch(int nmat, int epi, int nseg, const void* const* w, const void* w1, void* const* out,
+                    const int* n, const float* res, const float* gridf, const _Float16* x, int xt, int M, int K,
+                    hipStream_t st);
 //   k-quants: fmt 0 = Q6_K raw, 1 = Q6_K padded, 2 = Q4_K, 3 = Q5_K (tlx_kquant.hip).
 int tlx_kq_gemv(int fmt, const void* w, const uint16_t* x_f16, uint16_t* out_f16, int M, int N,
                 int K, bool launch, void* stream);

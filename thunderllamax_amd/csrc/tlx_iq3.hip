@@ -54,7 +54,7 @@ struct Iq3Seg {
 };
 
 struct Iq3Launch {
-  Iq3Seg seg[3];
+  Iq3Seg seg[4];
   int nseg;
   const float* gridf;
   const _Float16* x;   // activations [M][K], or (xt) the tile-ordered copy [K/8][16][8]
@@ -227,9 +227,18 @@ int iq3_launch(Iq3Launch& a, int tiles, hipStream_t st) {
     a.x = xt;
     a.xt = 1;
   }
-  if (a.layout == TLX_LAYOUT_TILED)
-    return tlx_iq3s_launch(NMAT, EPI, a.seg[0].w0, a.seg[0].w1, a.seg[0].out, a.seg[0].res, a.gridf, a.x,
-                           a.xt, a.M, a.seg[0].n, a.K, st);
+  if (a.layout == TLX_LAYOUT_TILED) {
+    const void* w[4];
+    void* out[4];
+    int n[4];
+    for (int i = 0; i < a.nseg; ++i) {
+      w[i] = a.seg[i].w0;
+      out[i] = a.seg[i].out;
+      n[i] = a.seg[i].n;
+    }
+    return tlx_iq3s_launch(NMAT, EPI, a.nseg, w, a.seg[0].w1, out, n, a.seg[0].res, a.gridf, a.x, a.xt, a.M,
+                           a.K, st);
+  }
   int waves = 4;
   while (tiles * waves < 4096 && waves < 16 && nb >= 4 * waves) waves *= 2;
   switch (waves) {
@@ -409,7 +418,7 @@ extern "C" int tlx_iq3_gemv(const void* w, const float* gridf, const uint16_t* x
 int tlx_iq3_segments(const void* const* w, uint16_t* const* out, const int* n, int nseg,
                      const float* gridf, const uint16_t* xh_f16, int M, int K, int layout,
                      bool launch, void* stream) {
-  TLX_RET_IF(nseg < 1 || nseg > 3 || layout == TLX_LAYOUT_TILED, TLX_E_ARG);
+  TLX_RET_IF(nseg < 1 || nseg > 4, TLX_E_ARG);
   for (int i = 0; i < nseg; ++i) {
     const int rc = iq3_check(w[i], M, n[i], K, layout);
     TLX_RET_IF(rc != TLX_OK, rc);
@@ -429,4 +438,14 @@ int tlx_iq3_segments(const void* const* w, uint16_t* const* out, const int* n, i
   a.K = K;
   a.layout = layout;
   return iq3_launch<1, EPI_F16>(a, tiles, (hipStream_t)stream);
+}
+
+// Up to four IQ3_XXS matrices sharing the activations, fp16 out, one launch.
+extern "C" int tlx_iq3_gemv_multi(const void* const* w, uint16_t* const* out, const int* n, int nseg,
+                                  const float* gridf, const uint16_t* x_f16, int M, int K, int layout,
+                                  void* stream) {
+  TLX_RET_IF(w == nullptr || out == nullptr || n == nullptr, TLX_E_ARG);
+  const int rc = tlx_iq3_segments(w, out, n, nseg, gridf, x_f16, M, K, layout, false, stream);
+  TLX_RET_IF(rc != TLX_OK, rc);
+  return tlx_iq3_segments(w, out, n, nseg, gridf, x_f16, M, K, layout, true, stream);
 }

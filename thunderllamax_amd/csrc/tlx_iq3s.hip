@@ -81,19 +81,29 @@ __global__ __launch_bounds__(256) void pack_tiled_kernel(const uint8_t* __restri
 }
 
 // ------------------------------------------------------------------ GEMV
+constexpr int kMaxSeg = 4;   // matrices sharing the activations in one launch (NMAT == 1)
+
 struct SkArgs {
-  const uint8_t* w0;
-  const uint8_t* w1;   // up matrix (SwiGLU), else null
-  void* out;
-  const float* res;    // residual (EPI_RESID)
+  // segment s: records sw[s] (tiles sT0[s] .. sT0[s+1]-1 of the launch), output sout[s] with
+  // sN[s] valid rows and row stride sld[s]; unused segments have sT0 = INT_MAX
+  const uint8_t* sw[kMaxSeg];
+  void* sout[kMaxSeg];
+  int sN[kMaxSeg], sld[kMaxSeg], sT0[kMaxSeg + 1];
+  int nseg;
+  const uint8_t* w1;   // up matrix (SwiGLU, one segment), else null
+  const float* res;    // residual (EPI_RESID, one segment; row stride sld[0])
   const float* gridf;
   const _Float16* x;   // [M][K], or (xt) the tile-ordered copy [K/8][16][8]
   int xt;
-  int M, N, K, nb, U, G;
-  int ostride;         // output / residual row stride (elements)
+  int M, K, nb, U, G;
   f4_t* part;          // workspace: boundary g: [lo | hi][NMAT][64 lanes]
   uint32_t* cnt;       // workspace: arrival counter per boundary (0 between calls)
 };
+
+// segment of launch tile t (wave-uniform)
+__device__ __forceinline__ int seg_of(const SkArgs& a, int t) {
+  return (t >= a.sT0[1]) + (t >= a.sT0[2]) + (t >= a.sT0[3]);
+}
 
 template <int NMAT>
 struct Rec {
@@ -138,19 +148,22 @@ __device__ __forceinline__ h8_t splat8(_Float16 v) { return h8_t{v, v, v, v, v, 
 
 template <int NMAT, int EPI>
 __device__ __forceinline__ void epilogue(const SkArgs& a, const f4_t* acc, int tile, int col, int kq) {
-  const int n = tile * 16 + col;
-  if (n >= a.N) return;
+  const int sg = seg_of(a, tile);
+  const int n = (tile - a.sT0[sg]) * 16 + col;
+  if (n >= a.sN[sg]) return;
+  void* out = a.sout[sg];
+  const int ld = a.sld[sg];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int m = 4 * kq + r;
     if (m >= a.M) break;
-    const size_t o = (size_t)m * a.ostride + n;
+    const size_t o = (size_t)m * ld + n;
     if constexpr (EPI == EPI_SWIGLU) {
-      reinterpret_cast<uint16_t*>(a.out)[o] = tlx_swiglu_bits(acc[0][r], acc[1][r]);
+      reinterpret_cast<uint16_t*>(out)[o] = tlx_swiglu_bits(acc[0][r], acc[1][r]);
     } else if constexpr (EPI == EPI_RESID) {
-      reinterpret_cast<float*>(a.out)[o] = a.res[o] + (float)(_Float16)acc[0][r];
+      reinterpret_cast<float*>(out)[o] = a.res[o] + (float)(_Float16)acc[0][r];
     } else {
-      reinterpret_cast<uint16_t*>(a.out)[o] = tlx_f2h_bits(acc[0][r]);
+      reinterpret_cast<uint16_t*>(out)[o] = tlx_f2h_bits(acc[0][r]);
     }
   }
 }
@@ -221,9 +234,22 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
   const int ubeg = range_begin(gw, GW, a.U), uend = range_begin(gw + 1, GW, a.U);
   const bool empty = ubeg >= uend;   // only when there are fewer records than waves
   const int last = max(min(uend, a.U) - 1, 0);
-  __amdgpu_buffer_rsrc_t rs[NMAT];
-  rs[0] = rsrc_of(a.w0, (uint32_t)a.U * kRec);
-  if constexpr (NMAT == 2) rs[1] = rsrc_of(a.w1, (uint32_t)a.U * kRec);
+  // record u: segment, buffer resource(s) and offset (all wave-uniform, in SGPRs)
+  auto rload = [&](Rec<NMAT>& R, int u) {
+    __amdgpu_buffer_rsrc_t rs[NMAT];
+    int soff;
+    if constexpr (NMAT == 2) {
+      rs[0] = rsrc_of(a.sw[0], (uint32_t)a.U * kRec);
+      rs[1] = rsrc_of(a.w1, (uint32_t)a.U * kRec);
+      soff = u * (int)kRec;
+    } else {
+      const int sg = seg_of(a, u / nb);
+      const int u0 = a.sT0[sg] * nb, u1 = min(a.sT0[sg + 1], a.U / nb) * nb;
+      rs[0] = rsrc_of(a.sw[sg], (uint32_t)(u1 - u0) * kRec);
+      soff = (u - u0) * (int)kRec;
+    }
+    rec_load<NMAT>(R, rs, soff, lane, col);
+  };
   // activations: block b, chunk c of lane (col, kq) at byte xv + b * xbs + c * xcs
   constexpr int xbs = XT ? 8192 : 512, xcs = XT ? 256 : 16;
   const __amdgpu_buffer_rsrc_t rx = rsrc_of(a.x, XT ? (uint32_t)a.K * 32u : (uint32_t)(a.M * a.K) * 2u);
@@ -266,13 +292,13 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
   Rec<NMAT> R[4];
   h8_t X[2][8];
   __builtin_amdgcn_sched_barrier(0);
-  rec_load<NMAT>(R[0], rs, min(ubeg, last) * (int)kRec, lane, col);
+  rload(R[0], min(ubeg, last));
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (XM != 2) xload(X[0], min(ubeg, last));
 #pragma unroll
   for (int j = 1; j < 4; ++j) {
     __builtin_amdgcn_sched_barrier(0);
-    rec_load<NMAT>(R[j], rs, min(ubeg + j, last) * (int)kRec, lane, col);
+    rload(R[j], min(ubeg + j, last));
   }
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (XM == 2) {
@@ -321,7 +347,7 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
       rec_dot<NMAT>(D, dq, R[j], X[j & 1], tb, kq);
       accum(D, dq, s);
       __builtin_amdgcn_sched_barrier(0);
-      rec_load<NMAT>(R[j], rs, min(s + 4, last) * (int)kRec, lane, col);
+      rload(R[j], min(s + 4, last));
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -441,54 +467,87 @@ int sk_dispatch(int W, const SkArgs& a, hipStream_t st) {
 bool tlx_iq3s_stages_x(int M, int K) { return M * (2 * K + 16) <= kXsBytes; }
 
 // Balanced GEMV over tiled records (called by the IQ3_XXS entry points of tlx_iq3.hip, which
-// have validated the arguments and prepared x / xt).  nmat 2 = SwiGLU pair, epi as Epi.
-int tlx_iq3s_launch(int nmat, int epi, const void* w0, const void* w1, void* out, const float* res,
-                    const float* gridf, const _Float16* x, int xt, int M, int N, int K, hipStream_t st) {
+// have validated the arguments and prepared x / xt).  nmat 2 = SwiGLU pair (one segment), epi as
+// Epi; nseg matrices w[s] of n[s] rows (NMAT == 1, EPI_F16 when nseg > 1) share the activations.
+int tlx_iq3s_launch(int nmat, int epi, int nseg, const void* const* w, const void* w1, void* const* out,
+                    const int* n, const float* res, const float* gridf, const _Float16* x, int xt, int M, int K,
+                    hipStream_t st) {
   void* ws = nullptr;
   const int rc = tlx_workspace(&ws);
   TLX_RET_IF(rc != TLX_OK, rc);
+  TLX_RET_IF(nseg < 1 || nseg > kMaxSeg || (nseg > 1 && (nmat != 1 || epi != EPI_F16)), TLX_E_ARG);
   SkArgs a{};
-  a.w0 = (const uint8_t*)w0;
   a.w1 = (const uint8_t*)w1;
-  a.out = out;
   a.res = res;
   a.gridf = gridf;
   a.x = x;
   a.xt = xt;
   a.M = M;
-  a.N = N;
   a.K = K;
   a.nb = K / 256;
   a.part = reinterpret_cast<f4_t*>(static_cast<uint8_t*>(ws) + kWsPartOff);
   a.cnt = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ws) + kWsCntOff);
-  const int T = (N + 15) / 16, nb = a.nb;
+  const int nb = a.nb;
   const int G0 = std::min(tlx_cu_count(), kMaxG);
-  constexpr int Wd = 8;   // 2 waves per SIMD, ~190 VGPRs each: the record ring and two activation sets
-  // A launch covers at most G0 * Wd tiles, so a wave's range (<= nb + 1 records) touches at most
-  // two tiles; larger matrices take several launches over consecutive tiles.
-  for (int t0 = 0; t0 < T; t0 += G0 * Wd) {
-    const int T1 = std::min(T - t0, G0 * Wd);
-    SkArgs b = a;
-    const size_t rec0 = (size_t)t0 * nb * kRec;
-    b.w0 = a.w0 + rec0;
-    b.w1 = a.w1 ? a.w1 + rec0 : nullptr;
-    b.N = std::min(N - t0 * 16, T1 * 16);
-    b.out = (uint8_t*)out + (size_t)t0 * 16 * (epi == EPI_RESID ? 4 : 2);
-    b.res = res ? res + (size_t)t0 * 16 : nullptr;
-    b.U = T1 * nb;
-    b.ostride = N;
-    // every wave gets >= 1 record; G <= T1 makes a workgroup cover >= nb records, so a tile
+  constexpr int Wd = 8;   // 2 waves per SIMD, ~130-180 VGPRs each: the record ring and two activation sets
+  const int Tmax = G0 * Wd;   // a launch covers at most G0 * Wd tiles, so a wave touches <= 2 tiles
+
+  auto run = [&](SkArgs& b, int T) {
+    b.U = T * nb;
+    // every wave gets >= 1 record; G <= T makes a workgroup cover >= nb records, so a tile
     // spans at most two workgroups
     int W = Wd;
-    int G = std::min(G0, T1);
+    int G = std::min(G0, T);
     if (b.U < G * W) G = std::max(1, b.U / W);
     while (W > 1 && b.U < G * W) W = W > 4 ? W / 2 : 1;
     b.G = G;
-    int rc;
-    if (nmat == 2) rc = sk_dispatch<2, EPI_SWIGLU>(W, b, st);
-    else if (epi == EPI_RESID) rc = sk_dispatch<1, EPI_RESID>(W, b, st);
-    else rc = sk_dispatch<1, EPI_F16>(W, b, st);
-    TLX_RET_IF(rc != TLX_OK, rc);
+    if (nmat == 2) return sk_dispatch<2, EPI_SWIGLU>(W, b, st);
+    if (epi == EPI_RESID) return sk_dispatch<1, EPI_RESID>(W, b, st);
+    return sk_dispatch<1, EPI_F16>(W, b, st);
+  };
+  auto reset = [](SkArgs& b) {
+    for (int k = 0; k <= kMaxSeg; ++k) b.sT0[k] = 0x7fffffff;
+  };
+
+  int T = 0;
+  for (int k = 0; k < nseg; ++k) T += (n[k] + 15) / 16;
+  if (nseg > 1 && T <= Tmax) {   // one launch over the concatenated tiles
+    SkArgs b = a;
+    reset(b);
+    b.nseg = nseg;
+    int t0 = 0;
+    for (int k = 0; k < nseg; ++k) {
+      b.sw[k] = (const uint8_t*)w[k];
+      b.sout[k] = out[k];
+      b.sN[k] = n[k];
+      b.sld[k] = n[k];
+      b.sT0[k] = t0;
+      t0 += (n[k] + 15) / 16;
+    }
+    b.sT0[nseg] = t0;
+    return run(b, t0);
+  }
+  // one matrix at a time, each in launches of <= Tmax tiles
+  const size_t osz = epi == EPI_RESID ? 4 : 2;
+  for (int k = 0; k < nseg; ++k) {
+    const int Tk = (n[k] + 15) / 16;
+    for (int t0 = 0; t0 < Tk; t0 += Tmax) {
+      const int T1 = std::min(Tk - t0, Tmax);
+      const size_t rec0 = (size_t)t0 * nb * kRec;
+      SkArgs b = a;
+      reset(b);
+      b.nseg = 1;
+      b.sw[0] = (const uint8_t*)w[k] + rec0;
+      b.w1 = a.w1 ? a.w1 + rec0 : nullptr;
+      b.sout[0] = (uint8_t*)out[k] + (size_t)t0 * 16 * osz;
+      b.sN[0] = std::min(n[k] - t0 * 16, T1 * 16);
+      b.sld[0] = n[k];
+      b.sT0[0] = 0;
+      b.sT0[1] = T1;
+      b.res = res ? res + (size_t)t0 * 16 : nullptr;
+      const int r = run(b, T1);
+      TLX_RET_IF(r != TLX_OK, r);
+    }
   }
   return TLX_OK;
 }

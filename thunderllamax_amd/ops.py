@@ -163,6 +163,26 @@ def iq3_gemv(w, gridf, x, out, layout=LAYOUT_PACKED, stream=None):
     return out
 
 
+def iq3_gemv_multi(ws, gridf, x, outs, layout=LAYOUT_PACKED, stream=None):
+    """outs[s][m] = half(W_s·x[m]) for up to four IQ3_XXS matrices sharing x, one launch (the GDN
+    block's qkv / gate / alpha / beta projections, engine/gdn_block.cu:44-148)."""
+    import ctypes
+    if not 1 <= len(ws) == len(outs) <= 4:
+        raise ValueError("one to four matrices, one output each")
+    M, K = _mk(x), x.shape[-1]
+    for i, (w, o) in enumerate(zip(ws, outs)):
+        _need(w, _iq3_w(o.shape[-1], K, layout), f"w[{i}]")
+        _need(o, M * o.shape[-1] * 2, f"out[{i}]")
+    _need(gridf, 4096, "gridf")
+    _dev(*ws, *outs, gridf, x)
+    k = len(ws)
+    wp = (ctypes.c_void_p * k)(*[w.data_ptr() for w in ws])
+    op = (ctypes.c_void_p * k)(*[o.data_ptr() for o in outs])
+    n = (ctypes.c_int * k)(*[o.shape[-1] for o in outs])
+    call("tlx_iq3_gemv_multi", wp, op, n, k, gridf.data_ptr(), x.data_ptr(), M, K, layout, _stream(stream))
+    return outs
+
+
 def _q4k_rows(n, k):
     return n * 144 * (k // 256)
 
@@ -183,10 +203,12 @@ def _attn(name, wq, wk, wv, gridf, xh, qrow, krow, vrow, qbytes, kbytes, vbytes,
 
 
 def aq3k8(wq, wk, wv, gridf, xh, qrow, krow, vrow, layout=LAYOUT_PACKED, stream=None):
-    """Fused q/k/v projections (aq3k8 / aq3k8v{M}): q, k IQ3_XXS in ``layout`` (packed rows or
-    GGUF blocks); v IQ3_XXS too, or GGUF Q4_K when ``layout`` includes ``V_Q4K``."""
-    v = _q4k_rows if layout & V_Q4K else _iq3_rows
-    _attn("tlx_aq3k8", wq, wk, wv, gridf, xh, qrow, krow, vrow, _iq3_rows, _iq3_rows, v, layout, stream)
+    """Fused q/k/v projections (aq3k8 / aq3k8v{M}): q, k IQ3_XXS in ``layout`` (packed rows, GGUF
+    blocks or tiled records); v IQ3_XXS too, or GGUF Q4_K when ``layout`` includes ``V_Q4K``."""
+    base = layout & ~V_Q4K
+    iq3 = lambda n, k: _iq3_w(n, k, base)   # noqa: E731
+    v = _q4k_rows if layout & V_Q4K else iq3
+    _attn("tlx_aq3k8", wq, wk, wv, gridf, xh, qrow, krow, vrow, iq3, iq3, v, layout, stream)
 
 
 def a_qkv_iq3(wq, wk, wv4, gridf, xh, qrow, krow, vrow, stream=None):
