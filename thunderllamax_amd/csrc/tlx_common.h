@@ -117,6 +117,12 @@ int tlx_rms_launch(bool add, const float* x, const uint16_t* a, const float* nw,
                    _Float16* xt, int M, int D, hipStream_t st);
 int tlx_rms_check(const float* x, const uint16_t* a, const float* nw, const float* hh, const uint16_t* xh, int M, int D);
 int tlx_workspace(void** ws);
+// The prefill GEMM's split-tile workspace (tlx_core.hip, same lifetime rules): up to 512 fp32
+// parts of a 256 x 256 tile (256 KB each).
+constexpr int kPfMaxTiles = 65536;
+constexpr size_t kPfPartBytes = size_t(512) * 256 * 256 * 4;
+constexpr size_t kPfWsBytes = kPfPartBytes;
+int tlx_workspace_gemm(void** ws);
 
 // Internal entry points shared by the fused attention projections (tlx_attn.hip).  With
 // launch == false they validate the arguments only.

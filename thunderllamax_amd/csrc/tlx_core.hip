@@ -35,3 +35,21 @@ int tlx_workspace(void** ws) {
   *ws = cache[dev];
   return TLX_OK;
 }
+
+// The prefill GEMM's stream-K workspace, allocated and zeroed on first use per device.
+int tlx_workspace_gemm(void** ws) {
+  static std::mutex mu;
+  static void* cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return TLX_E_NODEV;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[dev] == nullptr) {
+    if (hipMalloc(&cache[dev], kPfWsBytes) != hipSuccess || hipMemset(cache[dev], 0, kPfWsBytes) != hipSuccess) {
+      if (cache[dev] != nullptr) (void)hipFree(cache[dev]);
+      cache[dev] = nullptr;
+      return TLX_E_NOMEM;
+    }
+  }
+  *ws = cache[dev];
+  return TLX_OK;
+}

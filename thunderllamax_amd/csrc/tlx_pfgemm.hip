@@ -151,7 +151,8 @@ struct PfArgs {
   const u4_t* w1;
   const u4_t* w2;
   const _Float16* x;
-  int K, steps, nch, m0, nt;
+  int K, nch, m0, nt;
+  int tlast, hlast;   // last k-step / 128-k chunk of the segment being computed (loads clamp there)
 };
 
 // One k-step t: operand loads of step t (written before the last barrier), then the producers
@@ -166,16 +167,16 @@ __device__ __forceinline__ void pf_step(PfLds& L, f4_t (&acc)[8][8], const PfArg
   // activations of step t+2 into the ring slot read at step t-1 (its reads completed before the
   // previous barrier; past the tail the source step is clamped and the slot is not read again)
   const int ra2 = ra == 0 ? 2 : ra - 1;
-  pf_dma_a(L.a[ra2], g.x, g.m0, g.K, min(t + 2, g.steps - 1), wave, lane);
+  pf_dma_a(L.a[ra2], g.x, g.m0, g.K, min(t + 2, g.tlast), wave, lane);
   // weights: at t = 4h-1 chunk h+1 goes into ring slot (h+1) & 1, whose chunk h-1 was last read
   // at step 4h-2; it is first read at step t+4.  Past the tail the source is clamped.
   const bool wstep = (t & 3) == 3;
   if (wstep) {
     const int h = ((t + 1) >> 2) + 1;
-    pf_dma_w(L, h & 1, g.w1, g.w2, kFfn, g.nt, g.nch, min(h, g.nch - 1), wave, lane);
+    pf_dma_w(L, h & 1, g.w1, g.w2, kFfn, g.nt, g.nch, min(h, g.hlast), wave, lane);
   }
   // sub-block t+1 into the other B buffer (clamped on the last step: not read again)
-  pf_dequant(L, L.b[(t + 1) & 1], threadIdx.x, min(t + 1, g.steps - 1));
+  pf_dequant(L, L.b[(t + 1) & 1], threadIdx.x, min(t + 1, g.tlast));
   pf_mfma<0, 8>(acc, f);
   // step t+1's activations (issued one step earlier) and every earlier chunk burst must have
   // landed; this step's loads (4, or 8 on a burst step) stay in flight.  Then a barrier without
@@ -187,68 +188,27 @@ __device__ __forceinline__ void pf_step(PfLds& L, f4_t (&acc)[8][8], const PfArg
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Schedule: `full` workgroups own one whole tile each (the complete rounds of one workgroup per
+// CU); the remaining r tiles are split into p chunk ranges (segments) whose workgroups fill the
+// last round(s).  Segments store their fp32 parts; pf_fix_kernel sums each split tile's parts in
+// segment order.  (Combining inside the kernel -- last arriver adds -- needs the parts visible
+// across the XCDs' L2s: per-access coherent atomics or agent-scope fences on ~1 MB per tile cost
+// more than the split saved.)  Tile index tau maps to (m-tile, n-tile) so that, when there are m-tiles for all 8
+// XCDs, workgroup tau runs on XCD tau % 8 and each XCD sweeps the n-tiles of its m-tiles, keeping
+// that activation slice in its L2.
+struct PfSk {
+  int full, r, p;      // whole-tile workgroups, split tiles, segments per split tile
+  float* part;         // workspace: one 256 KB fp32 slot per segment
+};
+
 template <int EPI>
-__global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
-    const u4_t* __restrict__ w1, const u4_t* __restrict__ w2, const float* __restrict__ gridf,
-    const _Float16* __restrict__ x, void* __restrict__ out, const float* __restrict__ res, int M, int N,
-    int K, int mtiles, int ntiles) {
-  __shared__ PfLds L;
-  constexpr bool kFfn = EPI == PF_FFN;
-  // wave index as a scalar: the per-wave DMA selection branches on SGPRs
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int col = lane & 15, kq = lane >> 4;
-  const int wm = wave >> 1, wn = wave & 1;
-  int mt, nt;
-  if ((mtiles & 7) == 0) {   // XCD x = w % 8 sweeps the n-tiles of m-tiles x, x+8, ... in turn
-    const int l = (int)blockIdx.x >> 3;
-    mt = ((int)blockIdx.x & 7) + 8 * (l / ntiles);
-    nt = l % ntiles;
-  } else {
-    mt = (int)blockIdx.x % mtiles;
-    nt = (int)blockIdx.x / mtiles;
-  }
-  PfArgs g;
-  g.w1 = w1; g.w2 = w2; g.x = x; g.K = K;
-  g.steps = K / kBK; g.nch = K / 128;
-  g.m0 = mt * kBM; g.nt = nt;
-
-  // prologue: activation steps 0, 1 and weight chunks 0, 1 in flight; table; sub-block 0
-  pf_dma_a(L.a[0], x, g.m0, K, 0, wave, lane);
-  pf_dma_a(L.a[1], x, g.m0, K, min(1, g.steps - 1), wave, lane);
-  pf_dma_w(L, 0, w1, w2, kFfn, nt, g.nch, 0, wave, lane);
-  pf_dma_w(L, 1, w1, w2, kFfn, nt, g.nch, min(1, g.nch - 1), wave, lane);
-  pf_build_table(L.tbl, gridf);
-  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-  __syncthreads();
-  pf_dequant(L, L.b[0], threadIdx.x, 0);
-  __syncthreads();
-
-  // the wave's eight 16-column n-tiles (row groups of the B tile); for FFN tiles 0..3 are gate
-  // columns [64wn, +64) and tiles 4..7 the up columns of the same range
-  int bg[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) bg[j] = kFfn ? (j < 4 ? 4 * wn + j : 8 + 4 * wn + (j - 4)) : 8 * wn + j;
-  const int aoff = 8 * (4 * col + (kq ^ ((col >> 1) & 3)));
-
-  f4_t acc[8][8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
-
-  int ra = 0;
-  for (int t = 0; t < g.steps; ++t) {
-    pf_step<kFfn>(L, acc, g, bg, aoff, t, ra, wave, wm, lane);
-    ra = ra == 2 ? 0 : ra + 1;
-  }
-  __builtin_amdgcn_s_waitcnt(0x0F70);   // drain the clamped tail loads before the block exits
-
-  // epilogue: lane (col, kq) of m-tile i, n-tile j holds rows 4kq + e, column col
+__device__ __forceinline__ void pf_epilogue(const f4_t (&acc)[8][8], const int* bg, int m0, int nt, int wm, int kq,
+                                            int col, void* __restrict__ out, const float* __restrict__ res, int N) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int m = g.m0 + 128 * wm + 16 * i + 4 * kq + e;
+      const int m = m0 + 128 * wm + 16 * i + 4 * kq + e;
       if constexpr (EPI == PF_FFN) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -270,11 +230,182 @@ __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
   }
 }
 
+template <int EPI>
+__global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
+    const u4_t* __restrict__ w1, const u4_t* __restrict__ w2, const float* __restrict__ gridf,
+    const _Float16* __restrict__ x, void* __restrict__ out, const float* __restrict__ res, int M, int N,
+    int K, int mtiles, int ntiles, const PfSk sk) {
+  __shared__ PfLds L;
+  constexpr bool kFfn = EPI == PF_FFN;
+  // wave index as a scalar: the per-wave DMA selection branches on SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int col = lane & 15, kq = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int nch = K / 128;
+  const int bx = (int)blockIdx.x;
+  int tau, h0 = 0, h1 = nch, seg = -1;
+  if (bx < sk.full) {
+    tau = bx;
+  } else {
+    seg = bx - sk.full;
+    const int q = seg % sk.p;
+    tau = sk.full + seg / sk.p;
+    h0 = q * nch / sk.p;
+    h1 = (q + 1) * nch / sk.p;
+  }
+  int mt, nt;
+  if ((mtiles & 7) == 0) {   // XCD x = tau % 8 sweeps the n-tiles of m-tiles x, x+8, ... in turn
+    const int l = tau >> 3;
+    mt = (tau & 7) + 8 * (l / ntiles);
+    nt = l % ntiles;
+  } else {
+    mt = tau % mtiles;
+    nt = tau / mtiles;
+  }
+  PfArgs g;
+  g.w1 = w1; g.w2 = w2; g.x = x; g.K = K; g.nch = nch;
+  g.m0 = mt * kBM; g.nt = nt;
+  g.tlast = 4 * h1 - 1; g.hlast = h1 - 1;
+  const int s0 = 4 * h0;
+
+  // prologue: activation steps s0, s0+1 and weight chunks h0, h0+1 in flight; table; sub-block s0
+  pf_dma_a(L.a[0], x, g.m0, K, s0, wave, lane);
+  pf_dma_a(L.a[1], x, g.m0, K, min(s0 + 1, g.tlast), wave, lane);
+  pf_dma_w(L, h0 & 1, w1, w2, kFfn, nt, nch, h0, wave, lane);
+  pf_dma_w(L, (h0 + 1) & 1, w1, w2, kFfn, nt, nch, min(h0 + 1, g.hlast), wave, lane);
+  pf_build_table(L.tbl, gridf);
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+  __syncthreads();
+  pf_dequant(L, L.b[s0 & 1], threadIdx.x, s0);
+  __syncthreads();
+
+  // the wave's eight 16-column n-tiles (row groups of the B tile); for FFN tiles 0..3 are gate
+  // columns [64wn, +64) and tiles 4..7 the up columns of the same range
+  int bg[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) bg[j] = kFfn ? (j < 4 ? 4 * wn + j : 8 + 4 * wn + (j - 4)) : 8 * wn + j;
+  const int aoff = 8 * (4 * col + (kq ^ ((col >> 1) & 3)));
+
+  f4_t acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  int ra = 0;
+  for (int t = s0; t <= g.tlast; ++t) {
+    pf_step<kFfn>(L, acc, g, bg, aoff, t, ra, wave, wm, lane);
+    ra = ra == 2 ? 0 : ra + 1;
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // drain the clamped tail loads before the block exits
+
+  if (seg >= 0) {
+    // a segment of a split tile: store the part (the register layout, 16 B a lane, coalesced);
+    // pf_fix_kernel, launched next on the stream, adds the parts in order and applies the epilogue
+    f4_t* mine = reinterpret_cast<f4_t*>(sk.part) + (size_t)seg * (kBM * kBN / 4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mine[(i * 8 + j) * kThreads + threadIdx.x] = acc[i][j];
+    return;
+  }
+  pf_epilogue<EPI>(acc, bg, g.m0, nt, wm, kq, col, out, res, N);
+}
+
 int pf_check(const void* w, const void* x, int M, int N, int K, int layout, int ntile) {
   if (M < kBM || (M % kBM) || N < ntile || (N % ntile) || K < 128 || (K % 128)) return TLX_E_ARG;
   if (layout != TLX_LAYOUT_PACK7) return TLX_E_ARG;
   if (!tlx_aligned(w, 16) || !tlx_aligned(x, 16)) return TLX_E_ALIGN;
   return TLX_OK;
+}
+
+// The split tiles' sums: workgroup (st, i) adds the p parts of row group i (16 rows per wave
+// row) of split tile st in segment order (fixed: the result does not depend on which segment
+// finished first) and applies the epilogue to them.  8 workgroups a tile keep the reads spread.
+template <int EPI>
+__global__ __launch_bounds__(kThreads) void pf_fix_kernel(const f4_t* __restrict__ part, void* __restrict__ out,
+                                                          const float* __restrict__ res, int N, int mtiles,
+                                                          int ntiles, int full, int p) {
+  constexpr bool kFfn = EPI == PF_FFN;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, kq = lane >> 4, wm = wave >> 1, wn = wave & 1;
+  const int st = (int)blockIdx.x >> 3, i = (int)blockIdx.x & 7, tau = full + st;
+  int mt, nt;
+  if ((mtiles & 7) == 0) {
+    const int l = tau >> 3;
+    mt = (tau & 7) + 8 * (l / ntiles);
+    nt = l % ntiles;
+  } else {
+    mt = tau % mtiles;
+    nt = tau / mtiles;
+  }
+  int bg[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) bg[j] = kFfn ? (j < 4 ? 4 * wn + j : 8 + 4 * wn + (j - 4)) : 8 * wn + j;
+  f4_t acc[8];
+  const f4_t* src = part + (size_t)st * p * (kBM * kBN / 4) + i * 8 * kThreads + threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    f4_t sum = src[j * kThreads];
+    for (int q = 1; q < p; ++q) sum += src[(size_t)q * (kBM * kBN / 4) + j * kThreads];
+    acc[j] = sum;
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int m = mt * kBM + 128 * wm + 16 * i + 4 * kq + e;
+    if constexpr (EPI == PF_FFN) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = nt * (kBN / 2) + 16 * bg[j] + col;
+        reinterpret_cast<uint16_t*>(out)[(size_t)m * N + n] = tlx_swiglu_bits(acc[j][e], acc[j + 4][e]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int n = nt * kBN + 16 * bg[j] + col;
+        const size_t o = (size_t)m * N + n;
+        if constexpr (EPI == PF_RES)
+          reinterpret_cast<float*>(out)[o] = res[o] + acc[j][e];
+        else
+          reinterpret_cast<uint16_t*>(out)[o] = tlx_f2h_bits(acc[j][e]);
+      }
+    }
+  }
+}
+
+// Launch shape: whole tiles for the complete rounds of one workgroup per CU; the r tiles left
+// over are split into p segments, p (<= 4) minimizing the chunks the busiest CU computes
+// (ties: fewer segments), when that beats one more round of whole tiles.
+template <int EPI>
+int pf_launch(const u4_t* w1, const u4_t* w2, const float* gridf, const _Float16* x, void* out, const float* res,
+              int M, int N, int K, int mtiles, int ntiles, hipStream_t st) {
+  const int tiles = mtiles * ntiles, G0 = tlx_cu_count(), nch = K / 128;
+  const int R = tiles / G0, r = tiles - R * G0;
+  PfSk sk{tiles, 0, 1, nullptr};
+  if (r > 0) {
+    int best_p = 1;
+    long best = (long)(R + 1) * nch;
+    for (int p = 2; p <= 4; ++p) {
+      if ((long)r * p * (kBM * kBN * 4) > (long)kPfPartBytes || r > kPfMaxTiles) break;
+      const long span = (long)R * nch + (long)((r * p + G0 - 1) / G0) * ((nch + p - 1) / p);
+      if (span < best) { best = span; best_p = p; }
+    }
+    if (best_p > 1) {
+      void* ws = nullptr;
+      const int rc = tlx_workspace_gemm(&ws);
+      TLX_RET_IF(rc != TLX_OK, rc);
+      sk = PfSk{R * G0, r, best_p, static_cast<float*>(ws)};
+    }
+  }
+  pf_gemm_kernel<EPI><<<sk.full + sk.r * sk.p, kThreads, 0, st>>>(w1, w2, gridf, x, out, res, M, N, K, mtiles,
+                                                                    ntiles, sk);
+  if (sk.p > 1) {
+    const int rc = tlx_launch_status();
+    TLX_RET_IF(rc != TLX_OK, rc);
+    pf_fix_kernel<EPI><<<sk.r * 8, kThreads, 0, st>>>(reinterpret_cast<const f4_t*>(sk.part), out, res, N, mtiles,
+                                                      ntiles, sk.full, sk.p);
+  }
+  return tlx_launch_status();
 }
 
 }  // namespace
@@ -285,10 +416,8 @@ extern "C" int tlx_pfg3_ffn(const void* wg, const void* wu, const float* gridf, 
   if (rc == TLX_OK) rc = pf_check(wu, x16, M, N, K, layout, kBN / 2);
   TLX_RET_IF(rc != TLX_OK, rc);
   TLX_RET_IF(!tlx_aligned(gridf, 16), TLX_E_ALIGN);
-  const int mtiles = M / kBM, ntiles = N / (kBN / 2);
-  pf_gemm_kernel<PF_FFN><<<mtiles * ntiles, kThreads, 0, (hipStream_t)stream>>>(
-      (const u4_t*)wg, (const u4_t*)wu, gridf, (const _Float16*)x16, out16, nullptr, M, N, K, mtiles, ntiles);
-  return tlx_launch_status();
+  return pf_launch<PF_FFN>((const u4_t*)wg, (const u4_t*)wu, gridf, (const _Float16*)x16, out16, nullptr, M, N, K,
+                           M / kBM, N / (kBN / 2), (hipStream_t)stream);
 }
 
 extern "C" int tlx_pfg3_iq3d(const void* w, const float* gridf, const uint16_t* x16, const float* res,
@@ -296,10 +425,8 @@ extern "C" int tlx_pfg3_iq3d(const void* w, const float* gridf, const uint16_t* 
   const int rc = pf_check(w, x16, M, N, K, layout, kBN);
   TLX_RET_IF(rc != TLX_OK, rc);
   TLX_RET_IF(!tlx_aligned(gridf, 16), TLX_E_ALIGN);
-  const int mtiles = M / kBM, ntiles = N / kBN;
-  pf_gemm_kernel<PF_RES><<<mtiles * ntiles, kThreads, 0, (hipStream_t)stream>>>(
-      (const u4_t*)w, nullptr, gridf, (const _Float16*)x16, out32, res, M, N, K, mtiles, ntiles);
-  return tlx_launch_status();
+  return pf_launch<PF_RES>((const u4_t*)w, nullptr, gridf, (const _Float16*)x16, out32, res, M, N, K, M / kBM,
+                           N / kBN, (hipStream_t)stream);
 }
 
 extern "C" int tlx_pfg3_iq3o(const void* w, const float* gridf, const uint16_t* x16, uint16_t* out16,
@@ -307,8 +434,6 @@ extern "C" int tlx_pfg3_iq3o(const void* w, const float* gridf, const uint16_t* 
   const int rc = pf_check(w, x16, M, N, K, layout, kBN);
   TLX_RET_IF(rc != TLX_OK, rc);
   TLX_RET_IF(!tlx_aligned(gridf, 16), TLX_E_ALIGN);
-  const int mtiles = M / kBM, ntiles = N / kBN;
-  pf_gemm_kernel<PF_F16><<<mtiles * ntiles, kThreads, 0, (hipStream_t)stream>>>(
-      (const u4_t*)w, nullptr, gridf, (const _Float16*)x16, out16, nullptr, M, N, K, mtiles, ntiles);
-  return tlx_launch_status();
+  return pf_launch<PF_F16>((const u4_t*)w, nullptr, gridf, (const _Float16*)x16, out16, nullptr, M, N, K, M / kBM,
+                           N / kBN, (hipStream_t)stream);
 }
