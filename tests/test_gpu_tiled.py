@@ -213,3 +213,20 @@ def test_aq3k8_tiled_parity(gpu):
     for p, o in ((pq, q), (pk, k), (pv, v)):
         _, ref = gemv.gemv16_ref(quants.dequant_iq3xxs_packed(p, K), x)
         assert _rows_err(o.cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("N,K,M", [(16, 256, 1), (20, 256, 4), (100, 512, 3), (300, 1024, 16), (64, 17408, 4)])
+def test_tiled_small_and_unstaged_shapes(gpu, N, K, M):
+    """Shapes with fewer records than waves (1- and 4-wave workgroups), a tail tile, M = 16 (the
+    tile-ordered copy) and M = 4 at K = 17408 (activations read from memory, too large to stage)."""
+    print(f"[case] iq3_gemv tiled N={N} K={K} M={M}", flush=True)
+    rng = synth.config_rng(9)
+    p, t = _mat(gpu, rng, N, K)
+    x = synth.activations_f16(rng, M, K)
+    o = torch.full((M, N), float("nan"), dtype=torch.float16, device=gpu)
+    ops.iq3_gemv(t, formats.gridf_tensor(gpu), torch.from_numpy(x).to(gpu), o, layout=LAYOUT_TILED)
+    torch.cuda.synchronize()
+    _, ref = gemv.gemv16_ref(quants.dequant_iq3xxs_packed(p, K), x)
+    err = _rows_err(o.cpu().numpy(), ref)
+    print(f"[tiled small N={N} K={K} M={M}] rel-err {err:.3e}")
+    assert err <= TOL
