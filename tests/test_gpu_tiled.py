@@ -131,6 +131,37 @@ def test_down8_and_plain_tiled_parity(gpu, M, N):
     assert ey <= TOL and eo <= TOL
 
 
+def test_odd_tile_count_parity(gpu):
+    """A matrix of 513 tiles, the last one half full, alone (fp16 out and the residual form) and
+    as the first of four matrices sharing x in one launch, against the oracle."""
+    print("[case] odd tile count N=8200 K=512 M=5", flush=True)
+    rng = synth.config_rng(9)
+    M, K, ns = 5, 512, (8200, 600, 48, 40)
+    packed = [formats.iq3_pack_rows(synth.iq3xxs_raw(rng, n, K), K) for n in ns]
+    ws = [_tiled(gpu, torch.from_numpy(p).to(gpu), n, K) for p, n in zip(packed, ns)]
+    g = formats.gridf_tensor(gpu)
+    x = synth.activations_f16(rng, M, K)
+    xd = torch.from_numpy(x).to(gpu)
+    N0 = ns[0]
+    hh = rng.standard_normal((M, N0)).astype(np.float32)
+    y = torch.empty(M, N0, device=gpu)
+    o = torch.full((M, N0), float("nan"), dtype=torch.float16, device=gpu)
+    ops.down8(ws[0], g, xd, torch.from_numpy(hh).to(gpu), y, layout=LAYOUT_TILED)
+    ops.iq3_gemv(ws[0], g, xd, o, layout=LAYOUT_TILED)
+    outs = [torch.full((M, n), float("nan"), dtype=torch.float16, device=gpu) for n in ns]
+    ops.iq3_gemv_multi(ws, g, xd, outs, layout=LAYOUT_TILED)
+    torch.cuda.synchronize()
+    refs = [gemv.gemv16_ref(quants.dequant_iq3xxs_packed(p, K), x)[1] for p in packed]
+    _, yref = gemv.down8_ref(quants.dequant_iq3xxs_packed(packed[0], K), x, hh)
+    ey, eo = _rows_err(y.cpu().numpy(), yref), _rows_err(o.cpu().numpy(), refs[0])
+    print(f"[N=8200 down8] rel-err {ey:.3e}; [iq3_gemv] {eo:.3e}")
+    assert ey <= TOL and eo <= TOL
+    for n, out, ref in zip(ns, outs, refs):
+        err = _rows_err(out.cpu().numpy(), ref)
+        print(f"[multi N={n}] rel-err {err:.3e}")
+        assert err <= TOL
+
+
 def test_ffn8_hh_tiled_equals_two_calls(gpu):
     print("[case] ffn8_hh tiled M=11", flush=True)
     rng = synth.config_rng(6)
