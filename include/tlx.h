@@ -7,11 +7,17 @@
  *   - keeps the reference kernel's positional argument order, then appends the sizes the
  *     reference bakes into kernel names / #defines (M, N, K) and a layout flag;
  *   - is asynchronous on `stream` and never aborts;
- *   - allocates nothing per call.  The IQ3_XXS decode GEMVs (ffn8, down8, iq3_gemv and the
- *     IQ3_XXS segments of the attention projections) with M >= 6 first write a tile-ordered
- *     copy of the activations (K * 32 bytes) into a 4 MB workspace per device that the library
- *     allocates on the first such call (make that call outside stream capture); two such
- *     calls must not run concurrently on one device (order them on one stream);
+ *   - allocates nothing, ever.  Scratch device memory is the caller's: query the sizes with
+ *     tlx_workspace_size and attach buffers per device with tlx_attach_workspace (the host owns
+ *     every buffer, as the reference's boot-time Bufs: engine/engine0.py:85-95).  The GEMV
+ *     workspace is required by the IQ3_XXS decode GEMVs over TLX_LAYOUT_TILED records (ffn8,
+ *     ffn8_hh, down8, iq3_gemv, iq3_gemv_multi and the IQ3_XXS segments of the attention
+ *     projections, at every M: shared partial tiles and arrival counters; TLX_E_NOWS without
+ *     one) and used by the packed-row forms at M >= 6 (the tile-ordered activation copy; without
+ *     a workspace they read the activations directly).  The GEMM workspace lets the prefill
+ *     GEMMs (tlx_pfg3_*) split the last partial round of tiles; without one they run whole tiles.
+ *     Calls that use a workspace must not overlap in time on one device (order them on one
+ *     stream); attach outside stream capture, after which every call is capture-safe;
  *   - returns TLX_OK, a negative TLX_E_* code for a rejected argument (nothing launched),
  *     or a positive hipError_t from the launch.
  *
@@ -30,8 +36,9 @@ extern "C" {
 #define TLX_E_ARG (-1)     /* size / M / layout out of range */
 #define TLX_E_ALIGN (-2)   /* a pointer or row stride is not aligned as the layout needs */
 #define TLX_E_NODEV (-3)   /* no usable gfx950 device */
-#define TLX_E_NOMEM (-4)   /* the library workspace could not be allocated */
+#define TLX_E_NOMEM (-4)   /* reserved (the library allocates no device memory) */
 #define TLX_E_TRUNC (-5)   /* tlx_gguf_parse: the image ends inside the header; pass more bytes */
+#define TLX_E_NOWS (-6)    /* the call needs the GEMV workspace and none is attached on this device */
 
 /* Weight layouts (row-major over output rows). */
 #define TLX_LAYOUT_RAW 0     /* GGUF blocks as stored in the file */
@@ -41,14 +48,31 @@ extern "C" {
                                 chunks][32 units r*4+c][16 B: q u16 x4, sw u32, d u16, pad] */
 #define TLX_LAYOUT_TILED 3   /* IQ3_XXS tile-major streaming layout of this library (no reference
                                 counterpart; built by tlx_pack_iq3_tiled): [ceil(N/16) tiles]
-                                [K/256 blocks] 1568-B records [qs 64 x 16 B][sw 64 x 8 B]
-                                [d 16 x 2 B]; slot L = 16*kq + r holds row r's grid bytes
-                                16kq..16kq+15 / scale words 2kq, 2kq+1; rows >= N are zero */
+                                [K/256 blocks] 1632-B records (tlx_iq3_tiled_bytes gives the size):
+                                [0,1024) slot L = 16*kq + r, 16 B: bits 0..127 of its index stream;
+                                [1024,1536) slot L, 8 B: bits 128..191; [1536,1600) row r, u32: the
+                                8 sub-block scale nibbles; [1600,1632) row r, u16: d.  The stream of
+                                slot (kq, r) holds weights 64kq..64kq+63 of row r as 16 12-bit table
+                                indices (sign nibble with the parity bit folded in, grid byte);
+                                rows >= N are zero */
 
 #define TLX_MAX_M 16         /* decode GEMVs accept 1..16 activation rows */
 
 int tlx_version(void);
 const char* tlx_strerror(int code);
+
+/* ------------------------------------------------------------------ workspaces
+ * No reference counterpart (the reference's GEMVs need no scratch; its host allocates every
+ * buffer once at boot: engine/engine0.py:85-95).  tlx_workspace_size reports the bytes of the
+ * GEMV workspace (a few MB) and of the prefill GEMM's split workspace (128 MB; smaller works,
+ * with fewer split tiles).  tlx_attach_workspace binds caller-owned device buffers (256-B
+ * aligned; either may be NULL) to the current device, replacing any earlier ones, zeroes the
+ * GEMV workspace's counters on `stream` with a kernel, and does the library's one-time set-up
+ * (kernel attributes), so that every later call may be made under stream capture.  The buffers
+ * must outlive every call that uses them. */
+int tlx_workspace_size(uint64_t* gemv_bytes, uint64_t* gemm_bytes);
+int tlx_attach_workspace(void* gemv_ws, uint64_t gemv_bytes, void* gemm_ws, uint64_t gemm_bytes,
+                         void* stream);
 
 /* ------------------------------------------------------------------ dequantization
  * Oracle-parity kernels: decode `rows` x `kdim` weights.  out_f16 = 0 writes float32 (the
@@ -245,11 +269,12 @@ int tlx_pack_q6_pad(const void* raw, void* padded, int N, int K, void* stream);
  * (engine/pack_w7.py:40-75); N % 8 == 0. */
 int tlx_pack_w7(const void* packed, void* p7, int N, int K, void* stream);
 /* IQ3_XXS rows (src_layout TLX_LAYOUT_RAW blocks or TLX_LAYOUT_PACKED rows) -> TLX_LAYOUT_TILED
- * records, ceil(N/16) * (K/256) * 1568 B.  No reference counterpart: the decode GEMVs
+ * records, ceil(N/16) * (K/256) * 1632 B (= tlx_iq3_tiled_bytes(N, K); 0 for invalid sizes).  No reference counterpart: the decode GEMVs
  * (tlx_ffn8, tlx_ffn8_hh, tlx_down8, tlx_iq3_gemv) read it with every wave load one contiguous
  * run, the streaming form of the layout pack_w1c (engine/pack_w1c.py:20-31) makes for the
  * reference's GEMVs.  The GEMV results are bit-identical to those of the source layout. */
 int tlx_pack_iq3_tiled(const void* src, void* tiled, int N, int K, int src_layout, void* stream);
+uint64_t tlx_iq3_tiled_bytes(int N, int K);
 
 /* ---- MoE grouped-expert path (256 routed experts + 1 shared, hidden 2048, expert FF 512,
  * top-8; IQ4_XS weights).  Pairs are position-major, rank ascending: pair = 8*pos + rank.

@@ -18,5 +18,9 @@ Pinning status (how each function is checked, see ``tests/test_oracle_*.py``):
   known-answer blocks; ``KVALUES_IQ4NL`` content pinned by invariants + SHA-256.
 * ``layouts``                  -- packers vs their own byte-exact inverses.
 * ``gemv``                     -- float64 matmul of the dequantized values (the math fixes
-  this); the fp16 SwiGLU epilogue is checked against float64 silu within fp16 rounding.
+  this); ``hsilu16`` over all 63,488 finite fp16 inputs against float64 silu within the
+  first-order bound of its five fp16 roundings, its exp2 overflow (-0) and underflow
+  (identity) branches exactly, and planted mistakes that the bound must catch;
+  ``swiglu16`` by its algebra (u = 0, 1, -u, 2u) and against float64 silu(g) * u
+  (tests/test_oracle_gemv.py).
 """

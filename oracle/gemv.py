@@ -16,8 +16,8 @@ def hsilu16(h):
     """fp16 SiLU chain of /root/reference/engine/ffn8.cu:22-24, every step rounded to fp16:
     ``h * rcp(1 + exp2(h * c))``."""
     h = np.asarray(h, dtype=np.float16)
-    t = (h.astype(np.float32) * np.float32(SILU_C16)).astype(np.float16)
-    with np.errstate(over="ignore"):          # exp2 overflowing fp16 -> inf, as on the GPU
+    with np.errstate(over="ignore"):          # h * c or exp2 overflowing fp16 -> inf, as on the GPU
+        t = (h.astype(np.float32) * np.float32(SILU_C16)).astype(np.float16)
         e = np.exp2(t.astype(np.float64)).astype(np.float16)
     den = (np.float32(1.0) + e.astype(np.float32)).astype(np.float16)
     r = (1.0 / den.astype(np.float64)).astype(np.float16)

@@ -66,3 +66,41 @@ def test_q6k_gemv_argument_validation():
     assert L.tlx_q6k_gemv(p, p, p, 0, 5120, 0, None) == _lib.TLX_E_ARG
     assert L.tlx_q6k_gemv(p, p, p, 16, 5120, 7, None) == _lib.TLX_E_ARG
     assert L.tlx_q6k_gemv(p + 1, p, p, 16, 5120, 0, None) == _lib.TLX_E_ALIGN
+
+
+def test_tiled_record_size_header_library_and_ops_agree():
+    """The record size the header states, tlx_iq3_tiled_bytes and the Python size check agree
+    (a caller sizing buffers from the header must not under-allocate)."""
+    from thunderllamax_amd import ops
+    src = open(HDR).read()
+    stated = {int(v) for v in re.findall(r"(\d+)-B records", src)}
+    assert stated == {1632}, stated
+    assert "1632 B (= tlx_iq3_tiled_bytes(N, K)" in src
+    L = _lib.lib()
+    for N, K in ((1, 256), (16, 256), (17, 5120), (17408, 5120), (5120, 17408), (48, 5120)):
+        want = -(-N // 16) * (K // 256) * 1632
+        assert L.tlx_iq3_tiled_bytes(N, K) == want
+        assert ops._iq3_w(N, K, _lib.LAYOUT_TILED) == want
+    assert L.tlx_iq3_tiled_bytes(0, 256) == 0 and L.tlx_iq3_tiled_bytes(16, 300) == 0
+
+
+def test_workspace_size_and_attach_validation():
+    """Workspace sizes are queryable on the host; attach rejects a short or misaligned GEMV
+    buffer before any device work."""
+    L = _lib.lib()
+    g, m = ctypes.c_uint64(), ctypes.c_uint64()
+    assert L.tlx_workspace_size(ctypes.byref(g), ctypes.byref(m)) == 0
+    assert 1 << 20 < g.value <= 4 << 20 and m.value == 128 << 20
+    assert L.tlx_attach_workspace(0x1000, g.value - 1, None, 0, None) == _lib.TLX_E_ARG
+    assert L.tlx_attach_workspace(0x1010, g.value, None, 0, None) == _lib.TLX_E_ALIGN
+    assert L.tlx_attach_workspace(None, 0, 0x1010, m.value, None) == _lib.TLX_E_ALIGN
+    assert b"workspace" in L.tlx_strerror(_lib.TLX_E_NOWS)
+
+
+def test_no_device_allocation_in_library_sources():
+    """The library allocates no device memory: no hipMalloc / hipFree / hipMemset in csrc/."""
+    csrc = os.path.join(os.path.dirname(_lib.LIB_PATH), "csrc")
+    for f in sorted(os.listdir(csrc)):
+        text = re.sub(r"//[^\n]*", "", open(os.path.join(csrc, f)).read())
+        for bad in ("hipMalloc", "hipFree", "hipMemset", "hipExtMalloc"):
+            assert bad not in text, (f, bad)

@@ -52,7 +52,7 @@ def test_pack_tiled_bytes(gpu, N, K):
     assert np.array_equal(from_raw.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("M", [1, 5, 6, 11, 16])
+@pytest.mark.parametrize("M", [1, 4, 5, 6, 8, 11, 16])
 def test_ffn8_tiled_parity(gpu, M):
     print(f"[case] ffn8 tiled M={M} N=1000 K=5120", flush=True)
     rng = synth.config_rng(2)

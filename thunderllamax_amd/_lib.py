@@ -18,6 +18,7 @@ TLX_E_ALIGN = -2
 TLX_E_NODEV = -3
 TLX_E_NOMEM = -4
 TLX_E_TRUNC = -5
+TLX_E_NOWS = -6
 LAYOUT_RAW = 0
 LAYOUT_PACKED = 1
 LAYOUT_PACK7 = 2
@@ -33,6 +34,9 @@ _i64 = ctypes.c_int64
 SIGNATURES = {
     "tlx_version": [],
     "tlx_strerror": [_i],
+    "tlx_workspace_size": [_p, _p],
+    "tlx_attach_workspace": [_p, ctypes.c_uint64, _p, ctypes.c_uint64, _p],
+    "tlx_iq3_tiled_bytes": [_i, _i],
     "tlx_iq3xxs_dequant": [_p, _p, _p, _i64, _i64, _i, _i, _p],
     "tlx_q6k_dequant": [_p, _p, _i64, _i64, _i, _i, _p],
     "tlx_iq4xs_dequant": [_p, _p, _p, _i64, _i64, _p],
@@ -96,7 +100,8 @@ def lib():
         for name, args in SIGNATURES.items():
             f = getattr(L, name)
             f.argtypes = args
-            f.restype = ctypes.c_char_p if name == "tlx_strerror" else ctypes.c_int
+            f.restype = (ctypes.c_char_p if name == "tlx_strerror" else
+                         ctypes.c_uint64 if name == "tlx_iq3_tiled_bytes" else ctypes.c_int)
         _LIB = L
     return _LIB
 

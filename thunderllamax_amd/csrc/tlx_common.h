@@ -84,32 +84,27 @@ __device__ __forceinline__ void tlx_iq3_table(u2_t* tbl, const float* __restrict
 }
 
 // ---------------------------------------------------------------- device properties
-// Compute-unit count of the current device (cached per device id; a benign race on first use
-// writes the same value twice).
-static inline int tlx_cu_count() {
-  static int cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cache[dev] = n;
-  }
-  return cache[dev];
-}
+// Compute-unit count of the current device (tlx_core.hip; cached per device, one cache for the
+// whole library, filled at the latest by tlx_attach_workspace).
+int tlx_cu_count();
 
 // ---------------------------------------------------------------- workspace
-// Device memory the library holds per device (tlx_core.hip): scratch for the tile-ordered
-// activation copy of the IQ3_XXS decode GEMVs.  Allocated on the first call that needs it on a
-// device and kept until the process ends; calls that overlap in time on one device must not
-// both use it.
-constexpr size_t kWsBytes = size_t(4) << 20;
-// regions: [0, 2 MB) the activation copy; [2 MB, 3 MB) partial tiles of the tiled-record GEMV;
-// [3 MB, +4 KB) its per-boundary arrival counters (zeroed at allocation, reset by each call)
+// Device memory the caller owns and attaches per device (tlx_attach_workspace, tlx_core.hip):
+// the IQ3_XXS decode GEMVs' scratch.  Calls that overlap in time on one device must not share it.
+//   [0, 1 MB)            partial tiles of the tiled-record GEMV (4 KB per workgroup boundary)
+//   [1 MB, 1 MB + 4 KB)  its per-boundary arrival counters (0 between calls; zeroed by attach)
+//   [1 MB + 64 KB, +2 MB) the tile-ordered activation copy of the packed-row GEMVs (K * 32 B)
+constexpr size_t kWsPartOff = 0;
+constexpr size_t kWsCntOff = size_t(1) << 20;
+constexpr size_t kWsCntBytes = 4096;
+constexpr size_t kWsXtOff = (size_t(1) << 20) + (size_t(64) << 10);
 constexpr size_t kWsXtBytes = size_t(2) << 20;
-constexpr size_t kWsPartOff = size_t(2) << 20;
-constexpr size_t kWsCntOff = size_t(3) << 20;
+constexpr size_t kWsBytes = kWsXtOff + kWsXtBytes;
+// The attached GEMV workspace of the current device (nullptr when none is attached).
+int tlx_workspace(void** ws);
+// Zeroes the arrival counters of a GEMV workspace with a fill kernel on `st` (no memset node:
+// safe inside stream capture).
+int tlx_ws_clear_counters(void* ws, hipStream_t st);
 
 // RMSNorm producer (tlx_norm.hip): add form (hh = x + a) when add; optionally also writes the
 // IQ3_XXS GEMVs' tile-ordered activation copy xt (M <= 16)
@@ -117,12 +112,13 @@ int tlx_rms_launch(bool add, const float* x, const uint16_t* a, const float* nw,
                    _Float16* xt, int M, int D, hipStream_t st);
 int tlx_rms_check(const float* x, const uint16_t* a, const float* nw, const float* hh, const uint16_t* xh, int M, int D);
 int tlx_workspace(void** ws);
-// The prefill GEMM's split-tile workspace (tlx_core.hip, same lifetime rules): up to 512 fp32
-// parts of a 256 x 256 tile (256 KB each).
+// The prefill GEMM's split-tile workspace: fp32 parts of 256 x 256 tiles (256 KB each), caller
+// owned and attached per device like the GEMV workspace; without one (or when it is too small for
+// a split) the GEMM runs whole tiles only.
 constexpr int kPfMaxTiles = 65536;
 constexpr size_t kPfPartBytes = size_t(512) * 256 * 256 * 4;
 constexpr size_t kPfWsBytes = kPfPartBytes;
-int tlx_workspace_gemm(void** ws);
+int tlx_workspace_gemm(void** ws, size_t* bytes);
 
 // Internal entry points shared by the fused attention projections (tlx_attn.hip).  With
 // launch == false they validate the arguments only.
@@ -135,9 +131,12 @@ int tlx_iq3_segments(const void* const* w, uint16_t* const* out, const int* n, i
 //   activations or (xt != 0) their tile-ordered copy; nmat 2 = gate/up pair with epi SwiGLU,
 //   epi 0 = fp16 out, 2 = fp32 residual; up to 4 fp16-out matrices (nseg) share one launch
 bool tlx_iq3s_stages_x(int M, int K);
+//   ws: the GEMV workspace (kWsBytes; required)
 int tlx_iq3s_launch(int nmat, int epi, int nseg, const void* const* w, const void* w1, void* const* out,
                     const int* n, const float* res, const float* gridf, const _Float16* x, int xt, int M, int K,
-                    hipStream_t st);
+                    void* ws, hipStream_t st);
 //   k-quants: fmt 0 = Q6_K raw, 1 = Q6_K padded, 2 = Q4_K, 3 = Q5_K (tlx_kquant.hip).
+//   one-time kernel set-up of the k-quant GEMVs (dynamic LDS limit), run by tlx_attach_workspace
+int tlx_kq_setup();
 int tlx_kq_gemv(int fmt, const void* w, const uint16_t* x_f16, uint16_t* out_f16, int M, int N,
                 int K, bool launch, void* stream);

@@ -60,7 +60,8 @@ struct Iq3Launch {
   const _Float16* x;   // activations [M][K], or (xt) the tile-ordered copy [K/8][16][8]
   int xt;
   int M, K;
-  int layout;          // TLX_LAYOUT_RAW or TLX_LAYOUT_PACKED
+  int layout;          // TLX_LAYOUT_RAW, TLX_LAYOUT_PACKED or TLX_LAYOUT_TILED
+  void* ws;            // GEMV workspace (kWsBytes) or nullptr: iq3_launch then takes the attached one
 };
 
 template <int NMAT>
@@ -213,14 +214,17 @@ __global__ __launch_bounds__(256) void iq3_xt_kernel(const _Float16* __restrict_
 template <int NMAT, int EPI>
 int iq3_launch(Iq3Launch& a, int tiles, hipStream_t st) {
   const int nb = a.K >> 8;
+  if (a.ws == nullptr) {
+    const int rc = tlx_workspace(&a.ws);
+    if (rc != TLX_OK) return rc;
+  }
+  if (a.layout == TLX_LAYOUT_TILED && a.ws == nullptr) return TLX_E_NOWS;   // parts and counters
   // same values, same arithmetic: only the activation loads change (larger K reads x directly);
   // a.xt set by the caller: a.x already is the tile-ordered copy (written by a producer)
   const bool staged = a.layout == TLX_LAYOUT_TILED && tlx_iq3s_stages_x(a.M, a.K);  // no copy needed
-  if (!a.xt && !staged && a.M >= kXtMinM && (size_t)a.K * 16 * 2 <= kWsXtBytes) {
-    void* ws = nullptr;
-    const int rc = tlx_workspace(&ws);
-    if (rc != TLX_OK) return rc;
-    _Float16* xt = reinterpret_cast<_Float16*>(ws);
+  // without a workspace the packed-row GEMV reads x directly (same values, slower loads)
+  if (!a.xt && !staged && a.ws != nullptr && a.M >= kXtMinM && (size_t)a.K * 16 * 2 <= kWsXtBytes) {
+    _Float16* xt = reinterpret_cast<_Float16*>(static_cast<uint8_t*>(a.ws) + kWsXtOff);
     iq3_xt_kernel<<<(a.K / 8 * 16 + 255) / 256, 256, 0, st>>>(a.x, xt, a.M, a.K);
     const int lrc = tlx_launch_status();
     if (lrc != TLX_OK) return lrc;
@@ -237,7 +241,7 @@ int iq3_launch(Iq3Launch& a, int tiles, hipStream_t st) {
       n[i] = a.seg[i].n;
     }
     return tlx_iq3s_launch(NMAT, EPI, a.nseg, w, a.seg[0].w1, out, n, a.seg[0].res, a.gridf, a.x, a.xt, a.M,
-                           a.K, st);
+                           a.K, a.ws, st);
   }
   int waves = 4;
   while (tiles * waves < 4096 && waves < 16 && nb >= 4 * waves) waves *= 2;
@@ -255,7 +259,7 @@ int iq3_check(const void* w, int M, int N, int K, int layout) {
   if (M < 1 || M > TLX_MAX_M || N < 1 || K < 256 || (K & 255)) return TLX_E_ARG;
   if (layout != TLX_LAYOUT_PACKED && layout != TLX_LAYOUT_RAW && layout != TLX_LAYOUT_TILED) return TLX_E_ARG;
   // packed rows: the operand loads are dword-aligned when the row bytes 98*NB are (NB even);
-  // tiled records are 1568 B (16-B aligned fields); GGUF blocks are 2-B aligned throughout
+  // tiled records are 1632 B (16-B aligned fields); GGUF blocks are 2-B aligned throughout
   if (layout == TLX_LAYOUT_PACKED && (((K >> 8) & 1) || !tlx_aligned(w, 4))) return TLX_E_ALIGN;
   if (layout == TLX_LAYOUT_TILED && !tlx_aligned(w, 16)) return TLX_E_ALIGN;
   if (!tlx_aligned(w, 2)) return TLX_E_ALIGN;
@@ -368,11 +372,11 @@ extern "C" int tlx_ffn8_hh(const void* wg, const void* wu, const float* gridf, c
   a.K = K;
   _Float16* xt = nullptr;
   const bool staged = layout == TLX_LAYOUT_TILED && tlx_iq3s_stages_x(M, K);
-  if (!staged && M >= kXtMinM && (size_t)K * 16 * 2 <= kWsXtBytes) {   // the producer writes the GEMV's copy
-    void* ws = nullptr;
-    rc = tlx_workspace(&ws);
-    TLX_RET_IF(rc != TLX_OK, rc);
-    xt = reinterpret_cast<_Float16*>(ws);
+  rc = tlx_workspace(&a.ws);
+  TLX_RET_IF(rc != TLX_OK, rc);
+  TLX_RET_IF(layout == TLX_LAYOUT_TILED && a.ws == nullptr, TLX_E_NOWS);
+  if (!staged && a.ws != nullptr && M >= kXtMinM && (size_t)K * 16 * 2 <= kWsXtBytes) {   // the producer writes the GEMV's copy
+    xt = reinterpret_cast<_Float16*>(static_cast<uint8_t*>(a.ws) + kWsXtOff);
     a.x = xt;
     a.xt = 1;
   }
@@ -424,6 +428,12 @@ int tlx_iq3_segments(const void* const* w, uint16_t* const* out, const int* n, i
     TLX_RET_IF(rc != TLX_OK, rc);
   }
   TLX_RET_IF(!tlx_aligned(xh_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
+  if (layout == TLX_LAYOUT_TILED) {   // checked before any launch of the fused projections
+    void* ws = nullptr;
+    const int rc = tlx_workspace(&ws);
+    TLX_RET_IF(rc != TLX_OK, rc);
+    TLX_RET_IF(ws == nullptr, TLX_E_NOWS);
+  }
   if (!launch) return TLX_OK;
   Iq3Launch a{};
   int tiles = 0;

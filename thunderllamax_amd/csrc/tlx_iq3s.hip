@@ -22,9 +22,9 @@
 //   * a wave's partial for a tile it does not cover completely goes to LDS; after the loop the
 //     lowest contributing wave adds the contributions in wave order;
 //   * a tile shared by two workgroups (at most two: a workgroup covers >= NB units) is finished
-//     by the second of them to arrive: both write their part to the library workspace, count
-//     on a per-boundary counter, and the last adds lower-range part + upper-range part and
-//     resets the counter.
+//     by the second of them to arrive: both write their part to the workspace, wait for those
+//     stores to complete, count on a per-boundary counter (self-resetting: 0 -> 1 -> 0), and the
+//     second adds lower-range part + upper-range part.
 // The order depends only on (N, K, CU count): rows of an M-row call equal an M=1 call bit for bit.
 #include "tlx_common.h"
 
@@ -97,7 +97,7 @@ struct SkArgs {
   int xt;
   int M, K, nb, U, G;
   f4_t* part;          // workspace: boundary g: [lo | hi][NMAT][64 lanes]
-  uint32_t* cnt;       // workspace: arrival counter per boundary (0 between calls)
+  uint32_t* cnt;       // workspace: arrival counter per boundary (0 between calls, self-resetting)
 };
 
 // segment of launch tile t (wave-uniform)
@@ -401,10 +401,15 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
     // shared with the neighbouring workgroup: boundary g = the upper workgroup's index; part 0
     // holds the lower workgroup's (earlier k) sum, part 1 the upper's
     const int g = lo_out ? (int)blockIdx.x : (int)blockIdx.x + 1;
-    // Every access to the parts and the counter is an agent-scope atomic, coherent across the
-    // XCDs' L2s by itself, so no cache-wide write-back or invalidate is needed: the workgroup
-    // fence only waits for this wave's part stores to complete before the counter moves, and the
-    // part loads issue after the counter's value has returned.
+    // Ordering argument.  Every access to the parts and the counter is an agent-scope atomic
+    // (coherent across the XCDs' L2s by itself), so no cache-wide write-back or invalidate is
+    // needed (an agent-scope release fence would write back each XCD's whole L2).  What is needed
+    // is that this wave's part stores have COMPLETED before the counter moves: the workgroup-scope
+    // fence orders them for the compiler only (it emits no wait on gfx950), so the wave waits for
+    // its outstanding vector-memory operations explicitly (vmcnt counts stores on gfx9).  The
+    // second arriver's part loads issue only after the counter's old value has come back (they
+    // sit behind the branch on it), i.e. after the first arriver's increment, which followed the
+    // completion of the first arriver's stores.
     uint64_t* pp = reinterpret_cast<uint64_t*>(a.part + (size_t)g * 2 * NMAT * TLX_WAVE);
     const int mine = lo_out ? 1 : 0;
 #pragma unroll
@@ -415,8 +420,11 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
       __hip_atomic_store(q + 1, (uint64_t)v.z | (uint64_t)v.w << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0x0F70);                    // vmcnt(0): the part stores are done
+    // Self-resetting arrival count: inc with limit 1 maps 0 -> 1 (first arriver) and 1 -> 0
+    // (second arriver), so every completed call leaves each counter at 0 without a reset store.
     uint32_t prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(&a.cnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) prev = __builtin_amdgcn_atomic_inc32(&a.cnt[g], 1u, __ATOMIC_RELAXED, "agent");
     prev = __shfl(prev, 0);
     if (prev != 1u) continue;                              // the other part is not there yet
 #pragma unroll
@@ -435,7 +443,6 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
       acc[i] = lo + hi;                                    // lower range first: a fixed order
     }
     epilogue<NMAT, EPI>(a, acc, t, col, kq);
-    if (lane == 0) __hip_atomic_store(&a.cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -471,10 +478,10 @@ bool tlx_iq3s_stages_x(int M, int K) { return M * (2 * K + 16) <= kXsBytes; }
 // Epi; nseg matrices w[s] of n[s] rows (NMAT == 1, EPI_F16 when nseg > 1) share the activations.
 int tlx_iq3s_launch(int nmat, int epi, int nseg, const void* const* w, const void* w1, void* const* out,
                     const int* n, const float* res, const float* gridf, const _Float16* x, int xt, int M, int K,
-                    hipStream_t st) {
-  void* ws = nullptr;
-  const int rc = tlx_workspace(&ws);
-  TLX_RET_IF(rc != TLX_OK, rc);
+                    void* ws, hipStream_t st) {
+  TLX_RET_IF(ws == nullptr, TLX_E_NOWS);
+  static_assert(size_t(kMaxG) * 2 * 2 * TLX_WAVE * sizeof(f4_t) <= kWsCntOff - kWsPartOff, "parts region");
+  static_assert(size_t(kMaxG) * 4 <= kWsCntBytes, "counter region");
   TLX_RET_IF(nseg < 1 || nseg > kMaxSeg || (nseg > 1 && (nmat != 1 || epi != EPI_F16)), TLX_E_ARG);
   SkArgs a{};
   a.w1 = (const uint8_t*)w1;
@@ -550,6 +557,11 @@ int tlx_iq3s_launch(int nmat, int epi, int nseg, const void* const* w, const voi
     }
   }
   return TLX_OK;
+}
+
+extern "C" uint64_t tlx_iq3_tiled_bytes(int N, int K) {
+  if (N < 1 || K < 256 || (K % 256)) return 0;
+  return (uint64_t)((N + 15) / 16) * (uint64_t)(K / 256) * kRec;
 }
 
 extern "C" int tlx_pack_iq3_tiled(const void* src, void* tiled, int N, int K, int src_layout, void* stream) {

@@ -412,15 +412,23 @@ inline int k_rows_per_pass(int F, int M, int K) {
   return mc;
 }
 
+// One-time kernel set-up: the dynamic LDS limit above 64 KB (done once per process, by the first
+// call or by tlx_attach_workspace, so that calls made under stream capture do no set-up).
 template <int F>
-int kq_gemv16_launch(const uint8_t* w, const _Float16* x, uint16_t* out, int M, int N, int K,
-                     hipStream_t st) {
+hipError_t kq_attr_once() {
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
     attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&kq_gemv16_kernel<F>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
   });
+  return attr;
+}
+
+template <int F>
+int kq_gemv16_launch(const uint8_t* w, const _Float16* x, uint16_t* out, int M, int N, int K,
+                     hipStream_t st) {
+  const hipError_t attr = kq_attr_once<F>();
   if (attr != hipSuccess) return (int)attr;
   const int T = (N + 15) / 16;
   const int mc = k_rows_per_pass(F, M, K);
@@ -436,6 +444,17 @@ int kq_gemv16_launch(const uint8_t* w, const _Float16* x, uint16_t* out, int M, 
   }
   return TLX_OK;
 }
+
+}  // namespace
+
+int tlx_kq_setup() {
+  const hipError_t e[4] = {kq_attr_once<0>(), kq_attr_once<1>(), kq_attr_once<2>(), kq_attr_once<3>()};
+  for (hipError_t x : e)
+    if (x != hipSuccess) return (int)x;
+  return TLX_OK;
+}
+
+namespace {
 
 int kq_check(int F, const void* w, const void* x, const void* out, int M, int N, int K) {
   if (M < 1 || M > TLX_MAX_M || N < 1 || K < 256 || (K & 255)) return TLX_E_ARG;

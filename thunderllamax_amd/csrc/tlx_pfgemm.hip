@@ -32,6 +32,8 @@
 //     of one m-tile at a time, so its L2 keeps that activation slice.
 #include "tlx_common.h"
 
+#include <algorithm>
+
 namespace {
 
 constexpr int kBM = 256, kBN = 256, kBK = 32;
@@ -383,19 +385,20 @@ int pf_launch(const u4_t* w1, const u4_t* w2, const float* gridf, const _Float16
   const int R = tiles / G0, r = tiles - R * G0;
   PfSk sk{tiles, 0, 1, nullptr};
   if (r > 0) {
+    // the split needs r * p parts of 256 KB in the attached workspace; without room, whole tiles
+    void* ws = nullptr;
+    size_t wsb = 0;
+    const int rc = tlx_workspace_gemm(&ws, &wsb);
+    TLX_RET_IF(rc != TLX_OK, rc);
+    const size_t cap = ws != nullptr ? std::min(wsb, kPfPartBytes) : 0;
     int best_p = 1;
     long best = (long)(R + 1) * nch;
     for (int p = 2; p <= 4; ++p) {
-      if ((long)r * p * (kBM * kBN * 4) > (long)kPfPartBytes || r > kPfMaxTiles) break;
+      if ((size_t)r * p * (kBM * kBN * 4) > cap || r > kPfMaxTiles) break;
       const long span = (long)R * nch + (long)((r * p + G0 - 1) / G0) * ((nch + p - 1) / p);
       if (span < best) { best = span; best_p = p; }
     }
-    if (best_p > 1) {
-      void* ws = nullptr;
-      const int rc = tlx_workspace_gemm(&ws);
-      TLX_RET_IF(rc != TLX_OK, rc);
-      sk = PfSk{R * G0, r, best_p, static_cast<float*>(ws)};
-    }
+    if (best_p > 1) sk = PfSk{R * G0, r, best_p, static_cast<float*>(ws)};
   }
   pf_gemm_kernel<EPI><<<sk.full + sk.r * sk.p, kThreads, 0, st>>>(w1, w2, gridf, x, out, res, M, N, K, mtiles,
                                                                     ntiles, sk);

@@ -12,6 +12,48 @@ from ._lib import LAYOUT_PACK7, LAYOUT_PACKED, LAYOUT_RAW, LAYOUT_TILED, V_Q4K, 
 
 _F16 = torch.float16
 
+# ------------------------------------------------------------------ workspaces
+# The library allocates no device memory: its scratch buffers are caller-owned and attached per
+# device (tlx_attach_workspace), as the reference's host allocates every buffer once at boot
+# (/root/reference/engine/engine0.py:85-95).  This module owns one pair per device.
+_WORKSPACES = {}
+
+
+def workspace_sizes():
+    """(GEMV workspace bytes, prefill-GEMM split workspace bytes) the library asks for."""
+    import ctypes
+    g, m = ctypes.c_uint64(), ctypes.c_uint64()
+    call("tlx_workspace_size", ctypes.byref(g), ctypes.byref(m))
+    return g.value, m.value
+
+
+def attach_workspace(device=None, gemm_bytes=None, stream=None):
+    """Allocate the library's scratch buffers on `device` (default: the current device) with torch
+    and attach them: the GEMV workspace (zeroed counters) and the prefill GEMM's split workspace
+    (``gemm_bytes``, default the library's full size; 0 = none, the GEMMs then run whole tiles).
+    Call it outside stream capture; the ops below attach on the first use of a device."""
+    dev = torch.device("cuda", torch.cuda.current_device() if device is None else torch.device(device).index)
+    gb, mb = workspace_sizes()
+    mb = mb if gemm_bytes is None else int(gemm_bytes)
+    with torch.cuda.device(dev):
+        g = torch.zeros(gb, dtype=torch.uint8, device=dev)
+        m = torch.empty(mb, dtype=torch.uint8, device=dev) if mb > 0 else None
+        call("tlx_attach_workspace", g.data_ptr(), gb, None if m is None else m.data_ptr(), mb,
+             _stream(stream))
+    _WORKSPACES[dev.index] = (g, m)
+    return g, m
+
+
+def _ws(t):
+    """Attach the workspaces of t's device on its first use there (never inside stream capture:
+    an allocation there would belong to the graph)."""
+    if t.device.index in _WORKSPACES:
+        return
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("libtlx workspace not attached on this device: call ops.attach_workspace() "
+                           "before capturing a graph")
+    attach_workspace(t.device)
+
 
 def _stream(stream):
     if stream is None:
@@ -93,6 +135,7 @@ def ffn8(wg, wu, gridf, hhx, gact, layout=LAYOUT_PACKED, stream=None):
     _need(gridf, 4096, "gridf")
     _need(gact, M * N * 2, "gact")
     _dev(wg, wu, gridf, hhx, gact)
+    _ws(wg)
     call("tlx_ffn8", wg.data_ptr(), wu.data_ptr(), gridf.data_ptr(), hhx.data_ptr(), gact.data_ptr(),
          M, N, K, layout, _stream(stream))
     return gact
@@ -133,6 +176,7 @@ def ffn8_hh(wg, wu, gridf, x, attn_out, nw2, hh, hhx, gact, layout=LAYOUT_PACKED
     _need(hhx, M * K * 2, "hhx")
     _need(gact, M * N * 2, "gact")
     _dev(wg, wu, gridf, x, attn_out, nw2, hh, hhx, gact)
+    _ws(wg)
     call("tlx_ffn8_hh", wg.data_ptr(), wu.data_ptr(), gridf.data_ptr(), x.data_ptr(), attn_out.data_ptr(),
          nw2.data_ptr(), hh.data_ptr(), hhx.data_ptr(), gact.data_ptr(), M, N, K, layout, _stream(stream))
     return gact
@@ -146,6 +190,7 @@ def down8(wd, gridf, gact, hh, y, layout=LAYOUT_PACKED, stream=None):
     _need(hh, M * N * 4, "hh")
     _need(y, M * N * 4, "y")
     _dev(wd, gridf, gact, hh, y)
+    _ws(wd)
     call("tlx_down8", wd.data_ptr(), gridf.data_ptr(), gact.data_ptr(), hh.data_ptr(), y.data_ptr(),
          M, N, K, layout, _stream(stream))
     return y
@@ -158,6 +203,7 @@ def iq3_gemv(w, gridf, x, out, layout=LAYOUT_PACKED, stream=None):
     _need(gridf, 4096, "gridf")
     _need(out, M * N * 2, "out")
     _dev(w, gridf, x, out)
+    _ws(w)
     call("tlx_iq3_gemv", w.data_ptr(), gridf.data_ptr(), x.data_ptr(), out.data_ptr(), M, N, K, layout,
          _stream(stream))
     return out
@@ -179,6 +225,7 @@ def iq3_gemv_multi(ws, gridf, x, outs, layout=LAYOUT_PACKED, stream=None):
     wp = (ctypes.c_void_p * k)(*[w.data_ptr() for w in ws])
     op = (ctypes.c_void_p * k)(*[o.data_ptr() for o in outs])
     n = (ctypes.c_int * k)(*[o.shape[-1] for o in outs])
+    _ws(x)
     call("tlx_iq3_gemv_multi", wp, op, n, k, gridf.data_ptr(), x.data_ptr(), M, K, layout, _stream(stream))
     return outs
 
@@ -199,6 +246,7 @@ def _attn(name, wq, wk, wv, gridf, xh, qrow, krow, vrow, qbytes, kbytes, vbytes,
             vrow.shape[-1], K]
     if layout is not None:
         args.append(layout)
+    _ws(xh)
     call(name, *args, _stream(stream))
 
 
@@ -312,6 +360,7 @@ def pfg3_ffn(wg, wu, gridf, x16, out16, layout=LAYOUT_PACK7, stream=None):
     _need(gridf, 4096, "gridf")
     _need(out16, M * N * 2, "out16")
     _dev(wg, wu, gridf, x16, out16)
+    _ws(x16)
     call("tlx_pfg3_ffn", wg.data_ptr(), wu.data_ptr(), gridf.data_ptr(), x16.data_ptr(), out16.data_ptr(),
          M, N, K, layout, _stream(stream))
     return out16
@@ -392,6 +441,7 @@ def pfg3_iq3d(w, gridf, x16, res16, out32, layout=LAYOUT_PACK7, stream=None):
     _need(res16, M * N * 4, "res16")
     _need(out32, M * N * 4, "out32")
     _dev(w, gridf, x16, res16, out32)
+    _ws(x16)
     call("tlx_pfg3_iq3d", w.data_ptr(), gridf.data_ptr(), x16.data_ptr(), res16.data_ptr(), out32.data_ptr(),
          M, N, K, layout, _stream(stream))
     return out32
@@ -404,6 +454,7 @@ def pfg3_iq3o(w, gridf, x16, out16, layout=LAYOUT_PACK7, stream=None):
     _need(gridf, 4096, "gridf")
     _need(out16, M * N * 2, "out16")
     _dev(w, gridf, x16, out16)
+    _ws(x16)
     call("tlx_pfg3_iq3o", w.data_ptr(), gridf.data_ptr(), x16.data_ptr(), out16.data_ptr(), M, N, K, layout,
          _stream(stream))
     return out16
