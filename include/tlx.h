@@ -229,6 +229,16 @@ int tlx_rms_f16(const float* x, const float* nw, uint16_t* xh, int M, int D, voi
  * engine/gdn_block.cu:258-276): hh = x + float(a) (fp32, exact), hhx = half((hh * r) * nw). */
 int tlx_add_rms_f16(const float* x, const uint16_t* a, const float* nw, float* hh, uint16_t* hhx, int M,
                     int D, void* stream);
+/* tlx_ffn8 that allocates nothing and needs no attached workspace.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments, kernels and results
+ * (bit for bit) as tlx_ffn8; the scratch is the library's own fixed device array (about 3 MB per
+ * device, held until the process ends), so K <= 65536 (larger K: TLX_E_ARG).  Every call on a
+ * device shares that device's scratch: calls that overlap in time on one device race (order them
+ * on one stream).  Each call first clears the scratch's counters with a small kernel. */
+int tlx_ffn8_noalloc(const void* wg, const void* wu, const float* gridf, const uint16_t* hhx_f16,
+                     uint16_t* gact_f16, int M, int N, int K, int layout, void* stream);
+
 /* hh{M} fused with ffn8: tlx_add_rms_f16(x, attn_out, nw2, hh, hhx) then tlx_ffn8(wg, wu, gridf,
  * hhx, gact) with the same results bit for bit; from M = 6 on the producer also writes the
  * GEMV's tile-ordered activation copy, so the call is two launches instead of three.  Same

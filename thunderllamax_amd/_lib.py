@@ -41,6 +41,7 @@ SIGNATURES = {
     "tlx_q6k_dequant": [_p, _p, _i64, _i64, _i, _i, _p],
     "tlx_iq4xs_dequant": [_p, _p, _p, _i64, _i64, _p],
     "tlx_ffn8": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "tlx_ffn8_noalloc": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_down8": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_iq3_gemv": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_aq3k8": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],

@@ -105,6 +105,8 @@ int tlx_workspace(void** ws);
 // Zeroes the arrival counters of a GEMV workspace with a fill kernel on `st` (no memset node:
 // safe inside stream capture).
 int tlx_ws_clear_counters(void* ws, hipStream_t st);
+// Device address of tlx_ffn8_noalloc's static scratch on the current device (tlx_iq3.hip).
+int tlx_scratch_init(void** ptr);
 
 // RMSNorm producer (tlx_norm.hip): add form (hh = x + a) when add; optionally also writes the
 // IQ3_XXS GEMVs' tile-ordered activation copy xt (M <= 16)

@@ -72,6 +72,8 @@ extern "C" int tlx_attach_workspace(void* gemv_ws, uint64_t gemv_bytes, void* ge
   (void)tlx_cu_count();
   const int src = tlx_kq_setup();
   TLX_RET_IF(src != TLX_OK, src);
+  const int scr = tlx_scratch_init(nullptr);   // tlx_ffn8_noalloc's scratch address on this device
+  TLX_RET_IF(scr != TLX_OK, scr);
   if (gemv_ws != nullptr) {   // the arrival counters start at 0 (every complete call leaves them at 0)
     const int rc = tlx_ws_clear_counters(gemv_ws, (hipStream_t)stream);
     TLX_RET_IF(rc != TLX_OK, rc);

@@ -22,6 +22,8 @@
 //     caller's gridf buffer.
 #include "tlx_common.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int kIq3BlockBytes = 98;
@@ -351,6 +353,62 @@ extern "C" int tlx_ffn8(const void* wg, const void* wu, const float* gridf, cons
   a.x = (const _Float16*)hhx_f16;
   a.M = M;
   a.K = K;
+  return iq3_launch<2, EPI_SWIGLU>(a, tiles_of(N), (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------ ffn8 that allocates nothing
+// tlx_ffn8_noalloc runs tlx_ffn8's kernels on this file's own scratch instead of an attached
+// workspace: `scratch` is a file-scope device array with the GEMV workspace's regions (kWsBytes,
+// about 3 MB), one copy per device, held until the process ends.  In host code the array's name
+// is not a device address: the address is looked up once per device (hipGetSymbolAddress, with
+// the device current) and only that pointer is passed to kernels.
+namespace {
+
+__device__ __align__(256) uint8_t scratch[kWsBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];   // per-device address of `scratch`
+
+}  // namespace
+
+// The current device's address of `scratch` (resolved on the first use on a device; also called
+// by tlx_attach_workspace, the library's set-up call).
+int tlx_scratch_init(void** ptr) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return TLX_E_NODEV;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* q = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || q == nullptr) return e != hipSuccess ? (int)e : TLX_E_NODEV;
+    g_scratch_ptr[dev] = q;
+  }
+  if (ptr != nullptr) *ptr = g_scratch_ptr[dev];
+  return TLX_OK;
+}
+
+extern "C" int tlx_ffn8_noalloc(const void* wg, const void* wu, const float* gridf, const uint16_t* hhx_f16,
+                                uint16_t* gact_f16, int M, int N, int K, int layout, void* stream) {
+  int rc = iq3_check(wg, M, N, K, layout);
+  if (rc == TLX_OK) rc = iq3_check(wu, M, N, K, layout);
+  TLX_RET_IF(rc != TLX_OK, rc);
+  // the scratch's activation-copy region holds K * 32 bytes: K <= 65536
+  TLX_RET_IF((size_t)K * 16 * 2 > kWsXtBytes, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(hhx_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
+  void* ws = nullptr;
+  rc = tlx_scratch_init(&ws);
+  TLX_RET_IF(rc != TLX_OK, rc);
+  // the scratch keeps the last call's contents: the arrival counters start this call at zero
+  rc = tlx_ws_clear_counters(ws, (hipStream_t)stream);
+  TLX_RET_IF(rc != TLX_OK, rc);
+  Iq3Launch a{};
+  a.seg[0] = Iq3Seg{(const uint8_t*)wg, (const uint8_t*)wu, gact_f16, nullptr, N, 0};
+  a.layout = layout;
+  a.nseg = 1;
+  a.gridf = gridf;
+  a.x = (const _Float16*)hhx_f16;
+  a.M = M;
+  a.K = K;
+  a.ws = ws;
   return iq3_launch<2, EPI_SWIGLU>(a, tiles_of(N), (hipStream_t)stream);
 }
 

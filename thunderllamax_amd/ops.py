@@ -141,6 +141,20 @@ def ffn8(wg, wu, gridf, hhx, gact, layout=LAYOUT_PACKED, stream=None):
     return gact
 
 
+def ffn8_noalloc(wg, wu, gridf, hhx, gact, layout=LAYOUT_PACKED, stream=None):
+    """ffn8 on the library's own fixed scratch: no workspace, no allocation (for callers that
+    cannot allocate; calls overlapping in time on one device race on that scratch)."""
+    M, K, N = _mk(hhx), hhx.shape[-1], gact.shape[-1]
+    _need(wg, _iq3_w(N, K, layout), "wg")
+    _need(wu, _iq3_w(N, K, layout), "wu")
+    _need(gridf, 4096, "gridf")
+    _need(gact, M * N * 2, "gact")
+    _dev(wg, wu, gridf, hhx, gact)
+    call("tlx_ffn8_noalloc", wg.data_ptr(), wu.data_ptr(), gridf.data_ptr(), hhx.data_ptr(), gact.data_ptr(),
+         M, N, K, layout, _stream(stream))
+    return gact
+
+
 def rms_f16(x, nw, xh, stream=None):
     """xh[m] = half((x[m] * r) * nw), r = rsqrt(mean(x[m]^2) + 1e-6)   (k0n{M} / k0_norm)."""
     M, D = x.shape
