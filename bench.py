@@ -19,9 +19,17 @@ quantized model streams.  ``per_m_other_layout`` times the reference's packed ro
 where from M=6 on a step is two launches (the tile-ordered activation copy, then the GEMV).
 
 ``cpu_baseline`` times the numpy restatement of the reference's CPU path (dequantize, then
-an fp32 matmul) on a bounded sample of rows of the same workload, on this host's cores.
+an fp32 matmul) on the same workload (config 2 at the headline M, timed in full: dequant and
+matmul separately, median of 5 after one warm-up) on this host's cores; ``cpu`` holds the same
+for every configuration (configs 3-5 on row / M slices, extrapolated linearly and labelled so).
 
-``gemm`` is the metric's second half: the prefill dequant-GEMM of config 4 at M=2048 --
+``config1`` is BASELINE config 1: the Q6_K 5120x5120 GEMV with fp32 activations and outputs
+(h6k2048's contract), weights rotated over more than 300 MB, graph replays, HBM roofline.
+``stream`` is the measured HBM ceiling: a read-only stream over 1 GiB buffers (rotated), the
+figure every GB/s roofline also states its fraction of (``frac_of_measured``) beside the 8 TB/s
+datasheet peak (``frac``).
+
+``gemm`` is the metric's second half: the prefill dequant-GEMM of config 4 at M=2048 and M=8192 --
 gate+up with SwiGLU (K=5120, N=2x17408) and down with the residual epilogue (K=17408,
 N=5120) -- in TFLOP/s (2*M*N*K per GEMM) and as a fraction of the dense fp16 MFMA peak;
 ``gemm.w4a8_ffn`` is the reference's int8-activation branch of the same gate+up (activation
@@ -67,6 +75,27 @@ FFN8_TILED_M11_TRAFFIC_BYTES = 75_641_446
 PEAK_F16_TFLOPS = 2500.0
 PEAK_I8_TOPS = 5000.0
 ROT_BYTES = 300 * 2**20
+MEASURED = {"hbm_gbs": None}   # the read-stream ceiling of this run (stream leg), once measured
+
+
+def hbm_roofline(achieved_gbs, kernel, traffic=None, **extra):
+    """Roofline object of an HBM-bound measurement: fraction of the datasheet peak and, when the
+    stream leg has run, of the measured read ceiling."""
+    r = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+         "frac": round(achieved_gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "kernel": kernel}
+    if MEASURED["hbm_gbs"]:
+        r["measured_peak"] = MEASURED["hbm_gbs"]
+        r["frac_of_measured"] = round(achieved_gbs / MEASURED["hbm_gbs"], 4)
+    r.update(extra)
+    return r
+
+
+def mfma_roofline(achieved, kernel, peak=None, unit="TFLOP/s", **extra):
+    peak = PEAK_F16_TFLOPS if peak is None else peak
+    r = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": unit,
+         "frac": round(achieved / peak, 4), "traffic": None, "kernel": kernel}
+    r.update(extra)
+    return r
 
 
 def parse():
@@ -77,7 +106,10 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-formats", action="store_true", help="skip the producer and load-time repacking legs")
     ap.add_argument("--ms", default="1,4,8,11", help="activation widths to time")
-    ap.add_argument("--gemm-m", type=int, default=2048, help="prefill rows for the GEMM leg (0: skip)")
+    ap.add_argument("--gemm-m", default="2048,8192", help="prefill row counts for the GEMM leg ('0': skip)")
+    ap.add_argument("--no-config1", action="store_true", help="skip the config-1 Q6_K fp32 GEMV leg")
+    ap.add_argument("--no-stream", action="store_true", help="skip the HBM read-stream ceiling leg")
+    ap.add_argument("--cpu-reps", type=int, default=5, help="timed repetitions of each CPU baseline (median)")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the decode-step sweep leg")
     ap.add_argument("--layout", default="tiled", choices=("tiled", "packed"),
@@ -159,46 +191,53 @@ def time_graph(fn, steps, warmup, torch):
     return t0.elapsed_time(t1) / steps
 
 
-def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup):
-    """Config 4: IQ3_XXS FFN prefill GEMMs at M rows, synthetic seeded weights."""
+def gemm_weights(formats, synth, torch, dev):
+    """Config 4's weights in the packed7 unit layout the prefill GEMMs read (seeded)."""
     rng = synth.config_rng(4)
     H, F = 5120, 17408
-    def pack7(rows, k):   # the prefill GEMMs read the packed7 unit layout
+    def pack7(rows, k):
         return torch.from_numpy(formats.iq3_pack7(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, rows, k), k), k)).to(dev)
-    pg, pu, pd = pack7(F, H), pack7(F, H), pack7(H, F)
+    return pack7(F, H), pack7(F, H), pack7(H, F)
+
+
+def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup, weights, w4a8=True):
+    """Config 4: IQ3_XXS FFN prefill GEMMs at M rows, synthetic seeded weights, graph replays."""
+    rng = synth.config_rng(4)
+    H, F = 5120, 17408
+    pg, pu, pd = weights
     gridf = formats.gridf_tensor(dev)
     x = torch.from_numpy(synth.activations_f16(rng, M, H)).to(dev)
     act = torch.empty(M, F, dtype=torch.float16, device=dev)
     res = torch.randn(M, H, device=dev)
     y = torch.empty(M, H, dtype=torch.float32, device=dev)
-    t_ffn = time_call(lambda s: ops.pfg3_ffn(pg, pu, gridf, x, act, stream=s), steps, warmup, torch)
-    t_down = time_call(lambda s: ops.pfg3_iq3d(pd, gridf, act, res, y, stream=s), steps, warmup, torch)
+    t_ffn = time_graph(lambda s: ops.pfg3_ffn(pg, pu, gridf, x, act, stream=s), steps, warmup, torch)
+    t_down = time_graph(lambda s: ops.pfg3_iq3d(pd, gridf, act, res, y, stream=s), steps, warmup, torch)
     f_ffn, f_down = 2.0 * M * H * 2 * F, 2.0 * M * F * H
     tf_ffn = f_ffn / (t_ffn * 1e-3) / 1e12
     tf_down = f_down / (t_down * 1e-3) / 1e12
     tf_layer = (f_ffn + f_down) / ((t_ffn + t_down) * 1e-3) / 1e12
-    # the int8-activation branch of the same FFN: quantize the activations, then the W4A8 GEMM
-    xq = torch.empty(M, H, dtype=torch.int8, device=dev)
-    sx = torch.empty(M, H // 128, dtype=torch.float32, device=dev)
-    rs = torch.empty(M, H // 128, dtype=torch.int32, device=dev)
-    lut8 = formats.lut8_tensor(dev)
-    t_q8 = time_call(lambda s: ops.p8_quant(x, xq, sx, rs, stream=s), steps, warmup, torch)
-    t_w4 = time_call(lambda s: ops.p8w4_ffn(pg, pu, lut8, xq, sx, act, stream=s), steps, warmup, torch)
-    to_w4 = f_ffn / ((t_q8 + t_w4) * 1e-3) / 1e12
-    return {
+    out = {
         "workload": f"IQ3_XXS prefill FFN, M={M}: gate+up+SwiGLU K={H} N=2x{F}; down+residual K={F} N={H}",
         "M": M,
         "ffn_ms": round(t_ffn, 4), "ffn_tflops": round(tf_ffn, 1),
         "down_ms": round(t_down, 4), "down_tflops": round(tf_down, 1),
         "tflops": round(tf_layer, 1),
-        "roofline": {"bound": "mfma", "achieved": round(tf_ffn, 1), "peak": PEAK_F16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tf_ffn / PEAK_F16_TFLOPS, 4), "traffic": None,
-                     "kernel": "pf_gemm_kernel<FFN> (gate+up)"},
-        "w4a8_ffn": {"quant_ms": round(t_q8, 4), "gemm_ms": round(t_w4, 4), "tops": round(to_w4, 1),
-                     "roofline": {"bound": "mfma", "achieved": round(to_w4, 1), "peak": PEAK_I8_TOPS,
-                                  "unit": "TOP/s", "frac": round(to_w4 / PEAK_I8_TOPS, 4),
-                                  "kernel": "p8_quant_kernel + p8w4_ffn_kernel"}},
+        "roofline": mfma_roofline(tf_ffn, "pf_gemm_kernel<FFN> (+ pf_fix_kernel) gate+up",
+                                  down=mfma_roofline(tf_down, "pf_gemm_kernel<RES> (+ pf_fix_kernel) down")),
     }
+    if not w4a8:
+        return out
+    # the int8-activation branch of the same FFN: quantize the activations, then the W4A8 GEMM
+    xq = torch.empty(M, H, dtype=torch.int8, device=dev)
+    sx = torch.empty(M, H // 128, dtype=torch.float32, device=dev)
+    rs = torch.empty(M, H // 128, dtype=torch.int32, device=dev)
+    lut8 = formats.lut8_tensor(dev)
+    t_q8 = time_graph(lambda s: ops.p8_quant(x, xq, sx, rs, stream=s), steps, warmup, torch)
+    t_w4 = time_graph(lambda s: ops.p8w4_ffn(pg, pu, lut8, xq, sx, act, stream=s), steps, warmup, torch)
+    to_w4 = f_ffn / ((t_q8 + t_w4) * 1e-3) / 1e12
+    out["w4a8_ffn"] = {"quant_ms": round(t_q8, 4), "gemm_ms": round(t_w4, 4), "tops": round(to_w4, 1),
+                       "roofline": mfma_roofline(to_w4, "p8_quant_kernel + p8w4_ffn_kernel", PEAK_I8_TOPS, "TOP/s")}
+    return out
 
 
 def producers_leg(ops, formats, synth, torch, dev, steps, warmup, M=11, tiled=True):
@@ -278,7 +317,8 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
                            ptbl_dn=formats.pointer_table(ddn[:E], dev),
                            ptbl_sh=formats.pointer_table([dgu[E], ddn[E]], dev)))
     iq4nl = formats.iq4nl_tensor(dev)
-    out = {"workload": "MoE layer, 256 IQ4_XS experts + 1 shared, hidden 2048, FF 512, top-8"}
+    out = {"workload": "MoE layer, 256 IQ4_XS experts + 1 shared, hidden 2048, FF 512, top-8; hidden states "
+                       "bf16(0.05 * N(0,1)) (N(0,1) overflows the fp16 parts for these weight statistics)"}
     for P in (11, 2048):
         np_ = 8 * P
         x = torch.from_numpy(synth.bf16_round(0.05 * rng.standard_normal((P, H)).astype(np.float32))).to(dev)
@@ -300,9 +340,14 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
         hit = int((torch.diff(sc.eoff) > 0).sum().item())
         flops = 2.0 * 3 * F * H * (8 * P + P)
         wbytes = (hit + 1) * 1671168
-        out[f"M{P}"] = {"ms": round(t, 4), "tflops": round(flops / (t * 1e-3) / 1e12, 2),
-                        "experts_hit": hit, "weight_gbs": round(wbytes / (t * 1e-3) / 1e9, 1),
-                        "ms_shared_not_overlapped": round(t_seq, 4)}
+        tflops = flops / (t * 1e-3) / 1e12
+        gbs = wbytes / (t * 1e-3) / 1e9
+        out[f"M{P}"] = {"ms": round(t, 4), "tflops": round(tflops, 2),
+                        "experts_hit": hit, "weight_gbs": round(gbs, 1),
+                        "ms_shared_not_overlapped": round(t_seq, 4),
+                        "roofline": (hbm_roofline(gbs, "MoE layer (7 launches, graph): expert weight bytes / layer time")
+                                     if P <= 64 else
+                                     mfma_roofline(tflops, "MoE layer (7 launches, graph): 2*3*512*2048*9*M / layer time"))}
     return out
 
 
@@ -420,45 +465,241 @@ def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True):
             "iq3_layout": "tiled records" if tiled else "packed rows",
             "M": M, "launches": len(calls), "weight_bytes": nbytes, "ms": round(t_step, 4),
             "weight_gbs": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
-            "per_layer_kind": per_kind}
+            "per_layer_kind": per_kind,
+            "roofline": hbm_roofline(gbs, f"decode step: {len(calls)} GEMV launches in one graph "
+                                          "(weight bytes per step / step time)")}
 
 
-def cpu_baseline(N, K, M, seconds=10.0):
-    """numpy restatement of the reference path on a sample of rows, scaled to GB/s."""
+def config1_leg(ops, synth, torch, dev, steps, warmup):
+    """Config 1: Q6_K 5120x5120 GEMV, fp32 x and y (tlx_q6k_gemv, the h6k2048 contract), weights
+    rotated over more than 300 MB so every step reads HBM."""
+    from thunderllamax_amd._lib import LAYOUT_RAW
+    rng = synth.config_rng(1)
+    N = K = 5120
+    wbytes = N * 210 * (K // 256)
+    copies = [torch.from_numpy(synth.q6k_raw(rng, N, K)).to(dev) for _ in range(-(-ROT_BYTES // wbytes))]
+    x = torch.from_numpy(rng.standard_normal(K).astype(np.float32)).to(dev)
+    y = torch.empty(N, dtype=torch.float32, device=dev)
+    it = [0]
+
+    def step(s):
+        it[0] += 1
+        ops.h6k_gemv(copies[it[0] % len(copies)], x, y, layout=LAYOUT_RAW, stream=s)
+
+    t = time_graph(step, steps, warmup, torch)
+    nbytes = wbytes + 4 * K + 4 * N
+    gbs = nbytes / (t * 1e-3) / 1e9
+    return {"workload": f"Q6_K GEMV {N}x{K}, fp32 x and y (M=1), raw 210-B blocks", "ms": round(t, 5),
+            "algorithmic_bytes": nbytes, "gbs": round(gbs, 1), "rotation_copies": len(copies),
+            "roofline": hbm_roofline(gbs, "q6k_gemv_f32_kernel")}
+
+
+def stream_leg(ops, torch, dev, steps, warmup):
+    """Measured HBM read ceiling: tlx_stream_read over two 1 GiB buffers in turn (each step reads
+    1 GiB; 2 GiB rotate past the 256 MB Infinity Cache)."""
+    nbytes = 1 << 30
+    bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device=dev) for _ in range(2)]
+    sink = torch.empty(4 * nbytes // ops.stream_chunk_bytes(), dtype=torch.int32, device=dev)
+    it = [0]
+
+    def step(s):
+        it[0] += 1
+        ops.stream_read(bufs[it[0] % 2], sink, stream=s)
+
+    t = time_graph(step, steps, warmup, torch)
+    gbs = nbytes / (t * 1e-3) / 1e9
+    MEASURED["hbm_gbs"] = round(gbs, 1)
+    return {"workload": "read-only stream, 1 GiB per step (2 buffers rotated), 16-B loads, 64 KB per workgroup",
+            "ms": round(t, 4), "gbs": round(gbs, 1), "frac_of_datasheet": round(gbs / PEAK_HBM_GBS, 4),
+            "kernel": "stream_read_kernel"}
+
+
+# ------------------------------------------------------------------ CPU baselines
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+class _Cpu:
+    """Numpy restatement of the reference's CPU path (the oracle's dequantizers, then fp32
+    matmuls): row chunks dequantized on a thread pool (numpy releases the interpreter lock in its
+    array loops), matmuls on the BLAS threads.  Times are medians of `reps` after one warm-up."""
+
+    def __init__(self, reps):
+        import concurrent.futures as cf
+        self.cores = os.cpu_count() or 1
+        self.blas = int(os.environ.get("OMP_NUM_THREADS", self.cores))
+        self.threads = max(1, min(8, self.cores // 2))
+        self.pool = cf.ThreadPoolExecutor(self.threads)
+        self.reps = reps
+
+    def dequant(self, fn, rows, kdim):
+        chunks = np.array_split(rows, min(len(rows), 4 * self.threads))
+        return np.concatenate(list(self.pool.map(lambda c: fn(c, kdim), chunks)))
+
+    def median(self, f):
+        f()
+        ts = []
+        for _ in range(self.reps):
+            a = time.perf_counter()
+            f()
+            ts.append(time.perf_counter() - a)
+        return float(np.median(ts))
+
+    def gemv(self, fn, rows, kdim, x, total_rows=None, m_scale=1.0):
+        """(dequant s, matmul s) for `rows` (a row slice scaled to total_rows when given) times
+        x [M, kdim] (an M slice scaled by m_scale)."""
+        box = {}
+        t_deq = self.median(lambda: box.__setitem__("W", self.dequant(fn, rows, kdim)))
+        W = box["W"]
+        t_mm = self.median(lambda: x @ W.T)
+        r = 1.0 if total_rows is None else total_rows / rows.shape[0]
+        return t_deq * r, t_mm * r * m_scale
+
+    def describe(self):
+        return {"cores": self.cores, "dequant_threads": self.threads, "blas_threads": self.blas,
+                "cpu_model": _cpu_model(), "reps": self.reps}
+
+
+def cpu_legs(reps, heads_m):
+    """CPU baselines of every configuration (BASELINE's plan): configs 1 and 2 and config 5 at
+    M=11 in full; config 3 one tensor per (format, shape) on a row slice, summed over the 64-layer
+    manifest; configs 4 and 5 at M=2048 (and config 4 at M=8192) on a 256-row M slice and weight-
+    row slices, extrapolated linearly."""
     from oracle import quants
     from thunderllamax_amd import formats, synth
-    rng = np.random.default_rng(12345)
-    sample = 256
-    raw_g = synth.iq3xxs_raw(rng, sample, K)
-    raw_u = synth.iq3xxs_raw(rng, sample, K)
-    pg, pu = formats.iq3_pack_rows(raw_g, K), formats.iq3_pack_rows(raw_u, K)
-    x = synth.activations_f16(rng, M, K).astype(np.float32)
-    t_deq, t_mm, reps = 0.0, 0.0, 0
-    t_start = time.perf_counter()
-    while reps < 2 or time.perf_counter() - t_start < seconds:
-        a = time.perf_counter()
-        Wg = quants.dequant_iq3xxs_packed(pg, K)
-        Wu = quants.dequant_iq3xxs_packed(pu, K)
-        b = time.perf_counter()
-        ag = x @ Wg.T
-        au = x @ Wu.T
-        c = time.perf_counter()
-        t_deq += b - a
-        t_mm += c - b
-        reps += 1
-    per_call = (t_deq + t_mm) / reps * (N / sample)     # both matrices, all N rows
-    bytes_call = 2 * N * 98 * (K // 256) + M * K * 2 + M * N * 2
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {
-        "value": round(bytes_call / per_call / 1e9, 4),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"numpy dequant (single thread) + fp32 matmul ({threads} BLAS threads) of "
-                   f"{sample} of {N} gate and up rows, K={K}, M={M}, {reps} reps; "
-                   f"dequant {t_deq / reps * 1e3:.1f} ms + matmul {t_mm / reps * 1e3:.1f} ms "
-                   f"per sample, scaled linearly to all {N} rows"),
-    }
+    cpu = _Cpu(reps)
+    iq3 = quants.dequant_iq3xxs_packed
+    q6 = quants.dequant_q6k
+    iq4 = quants.dequant_iq4xs
+    out = {"host": cpu.describe()}
+
+    # config 1: Q6_K 5120x5120, fp32 x, M=1, in full
+    rng = synth.config_rng(1)
+    raw = synth.q6k_raw(rng, 5120, 5120)
+    x1 = rng.standard_normal((1, 5120)).astype(np.float32)
+    td, tm = cpu.gemv(q6, raw, 5120, x1)
+    nb1 = 5120 * 210 * 20 + 2 * 4 * 5120
+    out["config1"] = {"dequant_s": round(td, 4), "matmul_s": round(tm, 5),
+                      "gbs": round(nb1 / (td + tm) / 1e9, 4), "sample": "full matrix"}
+
+    # config 2: IQ3_XXS gate + up 17408x5120 at the headline M, in full
+    rng = synth.config_rng(2)
+    K, N = 5120, 17408
+    pg = formats.iq3_pack_rows(synth.iq3xxs_raw(rng, N, K), K)
+    pu = formats.iq3_pack_rows(synth.iq3xxs_raw(rng, N, K), K)
+    M = heads_m
+    x2 = synth.activations_f16(rng, M, K).astype(np.float32)
+    tdg, tmg = cpu.gemv(iq3, pg, K, x2)
+    tdu, tmu = cpu.gemv(iq3, pu, K, x2)
+    nb2 = 2 * N * 98 * (K // 256) + M * K * 2 + M * N * 2
+    t2 = tdg + tdu + tmg + tmu
+    out["config2"] = {"M": M, "dequant_s": round(tdg + tdu, 4), "matmul_s": round(tmg + tmu, 4),
+                      "gbs": round(nb2 / t2 / 1e9, 4), "sample": "full gate and up matrices"}
+    del pg, pu
+
+    # config 3: every (format, shape) of the decode step on a 1024-row slice, x [11, K]
+    rng = synth.config_rng(3)
+    M3, S = 11, 1024
+    manifest = [("iq3", 10240, 5120, 48), ("iq3", 6144, 5120, 48), ("iq3", 48, 5120, 96),
+                ("iq3", 5120, 6144, 64), ("iq3", 17408, 5120, 128), ("iq3", 5120, 17408, 64),
+                ("iq3", 12288, 5120, 8), ("iq3", 1024, 5120, 32), ("q6", 12288, 5120, 8),
+                ("q6", 151936, 5120, 1)]
+    t3, w3, per = 0.0, 0, []
+    for fmt, n, k, count in manifest:
+        rows = min(n, S)
+        if fmt == "iq3":
+            w = formats.iq3_pack_rows(synth.iq3xxs_raw(rng, rows, k), k)
+            td, tm = cpu.gemv(iq3, w, k, synth.activations_f16(rng, M3, k).astype(np.float32), total_rows=n)
+            wb = n * 98 * (k // 256)
+        else:
+            w = synth.q6k_raw(rng, rows, k)
+            td, tm = cpu.gemv(q6, w, k, synth.activations_f16(rng, M3, k).astype(np.float32), total_rows=n)
+            wb = n * 210 * (k // 256)
+        t3 += count * (td + tm)
+        w3 += count * wb
+        per.append({"tensor": f"{fmt} {n}x{k}", "count": count, "s_each": round(td + tm, 5)})
+    out["config3"] = {"M": M3, "s": round(t3, 3), "weight_gbs": round(w3 / t3 / 1e9, 4),
+                      "weight_bytes": w3, "per_tensor": per,
+                      "sample": f"each tensor on min(rows, {S}) rows, scaled to all rows "
+                                "(extrapolated), summed over the 64-layer manifest"}
+
+    # config 4: gate/up and down on 1024-row weight slices, 256-row M slice, extrapolated
+    rng = synth.config_rng(4)
+    H, F = 5120, 17408
+    pg = formats.iq3_pack_rows(synth.iq3xxs_raw(rng, S, H), H)
+    pd = formats.iq3_pack_rows(synth.iq3xxs_raw(rng, S, F), F)
+    xa = synth.activations_f16(rng, 256, H).astype(np.float32)
+    xb = synth.activations_f16(rng, 256, F).astype(np.float32)
+    out["config4"] = {}
+    for M4 in (2048, 8192):
+        tdg, tmg = cpu.gemv(iq3, pg, H, xa, total_rows=2 * F, m_scale=M4 / 256)
+        tdd, tmd = cpu.gemv(iq3, pd, F, xb, total_rows=H, m_scale=M4 / 256)
+        t4 = tdg + tmg + tdd + tmd
+        flops = 2.0 * M4 * H * 2 * F + 2.0 * M4 * F * H
+        out["config4"][f"M{M4}"] = {"s": round(t4, 3), "dequant_s": round(tdg + tdd, 3),
+                                    "matmul_s": round(tmg + tmd, 3), "tflops": round(flops / t4 / 1e12, 5),
+                                    "sample": f"{S}-row weight slices and a 256-row M slice, extrapolated"}
+
+    # config 5: MoE; dequant of 8 experts' slabs scaled to the experts hit, per-pair matmuls
+    rng = synth.config_rng(5)
+    E, HID, FF = 256, 2048, 512
+    sl_gu = np.concatenate([synth.iq4xs_raw(rng, 2 * FF, HID) for _ in range(8)])
+    sl_dn = np.concatenate([synth.iq4xs_raw(rng, HID, FF) for _ in range(8)])
+    box = {}
+    t_deq8 = cpu.median(lambda: box.update(gu=cpu.dequant(iq4, sl_gu, HID), dn=cpu.dequant(iq4, sl_dn, FF)))
+    Wgu, Wdn = box["gu"].reshape(8, 2 * FF, HID), box["dn"].reshape(8, HID, FF)
+    out["config5"] = {}
+    for P in (11, 2048):
+        Ps = min(P, 256)
+        logits = rng.standard_normal((Ps, E)).astype(np.float32)
+        xs = rng.standard_normal((Ps, HID)).astype(np.float32)
+
+        def layer():
+            top = np.argsort(-logits, axis=1, kind="stable")[:, :8]
+            lg = np.take_along_axis(logits, top, 1)
+            g = np.exp(lg - lg[:, :1])
+            g /= g.sum(1, keepdims=True)
+            y = np.zeros((Ps, HID), dtype=np.float32)
+            for e in np.unique(top):
+                pos, rank = np.nonzero(top == e)
+                w = e % 8      # the 8 dequantized slabs stand for every expert (timing only)
+                a = xs[pos] @ Wgu[w].T
+                act = a[:, :FF] / (1 + np.exp(-a[:, :FF])) * a[:, FF:]
+                y[pos] += g[pos, rank][:, None] * (act @ Wdn[w].T)
+            a = xs @ Wgu[0].T                      # the shared expert
+            y += (a[:, :FF] / (1 + np.exp(-a[:, :FF])) * a[:, FF:]) @ Wdn[0].T
+            return len(np.unique(top))
+
+        with np.errstate(over="ignore"):   # silu of large gate values: exp overflow -> 0, as intended
+            hit = layer()
+            t_mm = cpu.median(layer) * (P / Ps)
+        hit_full = hit if P == Ps else E
+        t_deq = t_deq8 * (hit_full + 1) / 8
+        t5 = t_deq + t_mm
+        flops = 2.0 * 3 * FF * HID * 9 * P
+        out["config5"][f"M{P}"] = {"s": round(t5, 4), "dequant_s": round(t_deq, 4), "matmul_s": round(t_mm, 4),
+                                   "experts_hit": hit_full, "tflops": round(flops / t5 / 1e12, 5),
+                                   "weight_gbs": round((hit_full + 1) * 1671168 / t5 / 1e9, 4),
+                                   "sample": ("dequant timed on 8 experts' slabs, scaled to the experts hit + "
+                                              "shared; router, per-expert matmuls and combine timed" +
+                                              (" on a 256-token slice, extrapolated" if P != Ps else " in full"))}
+    return out, cpu
+
+
+def cpu_baseline_of(legs, cpu):
+    """The contract's cpu_baseline object: config 2 (the headline workload), in GB/s."""
+    c2 = legs["config2"]
+    return {"value": c2["gbs"], "unit": "GB/s", "cores": cpu.threads, "kind": "port",
+            "sample": (f"config 2 in full (both {17408}x5120 matrices, M={c2['M']}): numpy dequant on "
+                       f"{cpu.threads} threads {c2['dequant_s']:.3f} s + fp32 matmul on {cpu.blas} BLAS threads "
+                       f"{c2['matmul_s']:.4f} s, median of {cpu.reps} after one warm-up; host "
+                       f"{cpu.describe()['cpu_model']}, {cpu.cores} cores")}
 
 
 def main():
@@ -510,10 +751,23 @@ def main():
                            "tflops": round(2 * M * 2 * N * K / (ms_step * 1e-3) / 1e12, 3)}
         return res
 
+    def note(msg):   # progress on stderr: the JSON line stays the only stdout line
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    small_steps, small_warm = max(3, args.steps // 5), max(1, args.warmup // 5)
+    if not args.no_stream:
+        note("stream (HBM read ceiling)")
+        stream = stream_leg(ops, torch, dev, small_steps, small_warm)
+    note(f"ffn8 per M ({args.layout})")
     per_m = per_m_of(args.layout)
+    note(f"ffn8 per M ({other})")
     per_m_other = per_m_of(other)
     head = str(max(ms))
     value = per_m[head]["gbs"]
+    for res in (per_m, per_m_other):
+        for r in res.values():
+            if MEASURED["hbm_gbs"]:
+                r["frac_of_measured"] = round(r["gbs"] / MEASURED["hbm_gbs"], 4)
     out = {
         "metric": "Quant GEMV HBM GB/s (% of peak) at M=1/11; dequant-GEMM TFLOPS at M=2048",
         "value": value,
@@ -532,30 +786,46 @@ def main():
                    "layout": args.layout, "rotation_copies": ncopy, "parallelism": "single GPU"},
         "per_m": per_m,
         "per_m_other_layout": {"layout": other, **per_m_other},
-        "roofline": {"bound": "hbm", "achieved": value, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(value / PEAK_HBM_GBS, 4),
-                     "traffic": (None if head != "11" else
-                                 FFN8_TILED_M11_TRAFFIC_BYTES if args.layout == "tiled" else FFN8_M11_TRAFFIC_BYTES),
-                     "algorithmic_bytes": wbytes + int(head) * K * 2 + int(head) * N * 2,
-                     "kernel": ("iq3s_kernel<2,1,8,2> (tiled records, activations staged in LDS)"
-                                if args.layout == "tiled" else
-                                "iq3_gemv_kernel<2,1,4> (+ iq3_xt_kernel for M >= 6)")},
+        "roofline": hbm_roofline(
+            value,
+            ("iq3s_kernel<2,1,8,2> (tiled records, activations staged in LDS)" if args.layout == "tiled" else
+             "iq3_gemv_kernel<2,1,4> (+ iq3_xt_kernel for M >= 6)"),
+            traffic=(None if head != "11" else
+                     FFN8_TILED_M11_TRAFFIC_BYTES if args.layout == "tiled" else FFN8_M11_TRAFFIC_BYTES),
+            algorithmic_bytes=wbytes + int(head) * K * 2 + int(head) * N * 2),
     }
-    if args.gemm_m > 0:
-        out["gemm"] = gemm_leg(ops, formats, synth, torch, dev, args.gemm_m, max(3, args.steps // 5),
-                               max(1, args.warmup // 5))
+    if not args.no_stream:
+        out["stream"] = stream
+    if not args.no_config1:
+        note("config 1 (Q6_K fp32 GEMV)")
+        out["config1"] = config1_leg(ops, synth, torch, dev, args.steps, args.warmup)
+    gemm_ms = [int(m) for m in str(args.gemm_m).split(",") if int(m) > 0]
+    if gemm_ms:
+        weights = gemm_weights(formats, synth, torch, dev)
+        out["gemm"] = {}
+        for i, M in enumerate(gemm_ms):
+            note(f"gemm M={M}")
+            leg = gemm_leg(ops, formats, synth, torch, dev, M, small_steps, small_warm, weights, w4a8=i == 0)
+            if i == 0:   # the metric's M=2048 figures at the top of the object
+                out["gemm"].update(leg)
+            out["gemm"][f"M{M}"] = {k: v for k, v in leg.items() if k != "w4a8_ffn"}
+        del weights
     if not args.no_sweep:
-        out["sweep"] = sweep_leg(ops, formats, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5),
-                                 tiled=args.layout == "tiled")
+        note("sweep (config 3)")
+        out["sweep"] = sweep_leg(ops, formats, torch, dev, small_steps, small_warm, tiled=args.layout == "tiled")
     if not args.no_formats:
-        out["producers"] = producers_leg(ops, formats, synth, torch, dev, max(3, args.steps // 5),
-                                         max(1, args.warmup // 5), tiled=args.layout == "tiled")
-    if not args.no_formats:
-        out["formats"] = formats_leg(ops, synth, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5))
+        note("producers / formats")
+        out["producers"] = producers_leg(ops, formats, synth, torch, dev, small_steps, small_warm,
+                                         tiled=args.layout == "tiled")
+        out["formats"] = formats_leg(ops, synth, torch, dev, small_steps, small_warm)
     if not args.no_moe:
-        out["moe"] = moe_leg(ops, formats, synth, torch, dev, max(3, args.steps // 5), max(1, args.warmup // 5))
+        note("moe (config 5)")
+        out["moe"] = moe_leg(ops, formats, synth, torch, dev, small_steps, small_warm)
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(N, K, int(head))
+        note("CPU baselines")
+        legs, cpu = cpu_legs(args.cpu_reps, int(head))
+        out["cpu_baseline"] = cpu_baseline_of(legs, cpu)
+        out["cpu"] = legs
     if args.copy_mib > 0:
         src = torch.ones(args.copy_mib * 2**18, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)

@@ -334,6 +334,14 @@ int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const float* iq4nl,
 int tlx_moe_combine(const uint16_t* parts, const float* gates, const float* sg, const float* shared,
                     const float* hres, float* y, int P, void* stream);
 
+/* ---- Measurement.
+ * HBM read-stream probe (the measured bandwidth ceiling the benchmark states GEMV throughput
+ * against, beside the datasheet figure; the reference's counterpart is its read-stream tool
+ * tools/w0_e4_bw.cu, not a hot-path kernel): reads nbytes of src once (nbytes a multiple of
+ * tlx_stream_chunk_bytes()), writing 4 * nbytes / tlx_stream_chunk_bytes() words to sink. */
+uint64_t tlx_stream_chunk_bytes(void);
+int tlx_stream_read(const void* src, uint64_t nbytes, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -77,6 +77,8 @@ SIGNATURES = {
     "tlx_moe_dn4": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _p],
     "tlx_moe_shared": [_p, _p, _p, _p, _p, _i, _p],
     "tlx_moe_combine": [_p, _p, _p, _p, _p, _p, _i, _p],
+    "tlx_stream_chunk_bytes": [],
+    "tlx_stream_read": [_p, ctypes.c_uint64, _p, _p],
 }
 
 
@@ -102,7 +104,8 @@ def lib():
             f = getattr(L, name)
             f.argtypes = args
             f.restype = (ctypes.c_char_p if name == "tlx_strerror" else
-                         ctypes.c_uint64 if name == "tlx_iq3_tiled_bytes" else ctypes.c_int)
+                         ctypes.c_uint64 if name in ("tlx_iq3_tiled_bytes", "tlx_stream_chunk_bytes")
+                         else ctypes.c_int)
         _LIB = L
     return _LIB
 

@@ -621,3 +621,21 @@ def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, s
         cur.wait_stream(side)
     moe_combine(sc.parts, sc.gates, sg, sc.shared, hres, y, stream=cur)
     return y
+
+
+# ------------------------------------------------------------------ measurement
+def stream_read(src, sink, stream=None):
+    """Read all of ``src`` once (HBM read-stream probe); ``sink`` receives one uint32 per wave.
+    src's byte size must be a multiple of ``stream_chunk_bytes()``."""
+    from ._lib import lib
+    nbytes = src.numel() * src.element_size()
+    chunk = lib().tlx_stream_chunk_bytes()
+    _need(sink, 4 * 4 * (nbytes // chunk), "sink")
+    _dev(src, sink)
+    call("tlx_stream_read", src.data_ptr(), nbytes, sink.data_ptr(), _stream(stream))
+    return sink
+
+
+def stream_chunk_bytes():
+    from ._lib import lib
+    return lib().tlx_stream_chunk_bytes()
