@@ -222,10 +222,14 @@ __device__ __forceinline__ void rec_dot(f4_t* out, float* dq, const Rec<NMAT>& R
 __device__ __forceinline__ int range_begin(int gw, int GW, int U) { return unit_of(gw, GW, U); }
 
 // XM: where the activations come from -- 0: x [M][K] in global memory, 1: the tile-ordered copy
-// [K/8][16][8] in global memory, 2: x staged into LDS by the workgroup (W == kXsWaves).
+// [K/8][16][8] in global memory, 2: x staged into LDS by the workgroup (W == kXsWaves), every
+// thread loading kXsPer pieces, 3: the same when fewer pieces are needed (small M: the loads past
+// the end are skipped).  Staged activations are read from LDS at the point of use (no register
+// copy), which leaves room for the shallower record ring below.
 template <int NMAT, int EPI, int W, int XM>
 __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
-  __shared__ SkLds<NMAT, W, XM == 2> L;
+  constexpr bool XS = XM >= 2;   // staged in LDS
+  __shared__ SkLds<NMAT, W, XS> L;
   constexpr bool XT = XM == 1;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -259,52 +263,55 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
   auto xload = [&](h8_t* X, int u) {
     const int b = u % nb;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      if constexpr (XM == 2)
-        X[c] = *reinterpret_cast<const h8_t*>(xsl + 512 * b + 16 * c);
-      else
-        X[c] = __builtin_bit_cast(h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, xv + xcs * c, xbs * b, 0));
-    }
+    for (int c = 0; c < 8; ++c)
+      X[c] = __builtin_bit_cast(h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, xv + xcs * c, xbs * b, 0));
   };
 
-  // Record ring: record s is requested 3 records ahead of its use (4 buffers); activations one
-  // unit ahead (2 sets).  Issue order X(s+1), R(s+3), X(s+2), R(s+4), ...: the wait for record s
-  // and X(s) leaves the next three records and X(s+1) in flight.  The first loads are issued
-  // before the table is built (their latency covers it); the grid words the thread turns into
-  // table entries are loaded first, so waiting for them leaves the records in flight.
+  // Record ring of RING buffers: record s is requested RING - 1 records ahead of its use.  With
+  // activations from global memory (4 buffers) they are loaded one unit ahead (2 sets), issue order
+  // X(s+1), R(s+3), X(s+2), R(s+4), ...: the wait for record s and X(s) leaves the next three
+  // records and X(s+1) in flight.  With staged activations the ring is 2 deep: measured faster than
+  // 3, 4, 6 or 8 (each wave streams only ~10 records, and requesting more of them up front made
+  // the whole launch slower).  The first loads are issued before the table is built (their latency
+  // covers it); the grid words the thread turns into table entries are loaded first, so waiting for
+  // them leaves the records in flight.
   constexpr int kGw = 1024 / (W * TLX_WAVE);   // grid words (x 4 sign nibbles) per thread
   float4 gv[kGw];
   // staged activations: 16-B pieces p = thread + j * blockDim of x (clamped to the last piece:
   // loads stay unconditional, a repeated piece is stored twice with the same bytes)
-  constexpr int kXp = XM == 2 ? kXsPer : 1;
+  constexpr int kXp = XS ? kXsPer : 1;
   u4_t xp[kXp];
   const int npc = a.M * a.K / 8;
-  if constexpr (XM == 2) {
+  if constexpr (XS) {
 #pragma unroll
-    for (int j = 0; j < kXp; ++j)
+    for (int j = 0; j < kXp; ++j) {
+      if (XM == 3 && j * W * TLX_WAVE >= npc) break;   // (uniform) the rest is past the end
       xp[j] = __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                            rx, 16 * min((int)threadIdx.x + j * W * TLX_WAVE, npc - 1), 0, 0));
+    }
   }
 #pragma unroll
   for (int j = 0; j < kGw; ++j) gv[j] = reinterpret_cast<const float4*>(a.gridf)[(threadIdx.x + j * W * TLX_WAVE) & 255];
   // (scheduling barriers keep each record's loads together and the records in order: the wait
   // counts in the loop assume that order on entry)
-  Rec<NMAT> R[4];
-  h8_t X[2][8];
+  constexpr int RING = XS ? 2 : 4;
+  Rec<NMAT> R[RING];
+  h8_t X[XS ? 1 : 2][8];
   __builtin_amdgcn_sched_barrier(0);
   rload(R[0], min(ubeg, last));
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (XM != 2) xload(X[0], min(ubeg, last));
+  if constexpr (!XS) xload(X[0], min(ubeg, last));
 #pragma unroll
-  for (int j = 1; j < 4; ++j) {
+  for (int j = 1; j < RING; ++j) {
     __builtin_amdgcn_sched_barrier(0);
     rload(R[j], min(ubeg + j, last));
   }
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (XM == 2) {
+  if constexpr (XS) {
     const int kp = a.K / 8;   // pieces per row
 #pragma unroll
     for (int j = 0; j < kXp; ++j) {
+      if (XM == 3 && j * W * TLX_WAVE >= npc) break;
       const int p = min((int)threadIdx.x + j * W * TLX_WAVE, npc - 1);
       *reinterpret_cast<u4_t*>(L.xs + (p / kp) * xstr + 16 * (p % kp)) = xp[j];
     }
@@ -315,7 +322,6 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
     tlx_iq3_table_entries(L.tbl, gv[j], e & 255, e >> 8);
   }
   __syncthreads();
-  if constexpr (XM == 2) xload(X[0], min(ubeg, last));
   const uint8_t* tb = reinterpret_cast<const uint8_t*>(L.tbl);
 
   // a wave touches at most two tiles: records < split belong to the first
@@ -334,37 +340,44 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
       accB[i] += (dq[i] * fB) * D[i];
     }
   };
-  // full rounds of 4 records: branch-free (a branch in the loop makes the wait counts conservative)
-  const int nfull = empty ? 0 : (uend - ubeg) & ~3;
-  for (int u = ubeg; u < ubeg + nfull; u += 4) {
+  // activations of record s: staged rows in LDS (read at the point of use), else the register set
+  auto xsrc = [&](int s, int j) -> const h8_t* {
+    if constexpr (XS) return reinterpret_cast<const h8_t*>(xsl + 512 * (s % nb));
+    else return X[j & 1];
+  };
+  // full rounds of RING records: branch-free (a branch in the loop makes the wait counts conservative)
+  const int nfull = empty ? 0 : (uend - ubeg) / RING * RING;
+  for (int u = ubeg; u < ubeg + nfull; u += RING) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < RING; ++j) {
       const int s = u + j;
       __builtin_amdgcn_sched_barrier(0);
-      xload(X[(j + 1) & 1], min(s + 1, last));
+      if constexpr (!XS) xload(X[(j + 1) & 1], min(s + 1, last));
       f4_t D[NMAT];
       float dq[NMAT];
-      rec_dot<NMAT>(D, dq, R[j], X[j & 1], tb, kq);
+      rec_dot<NMAT>(D, dq, R[j], xsrc(s, j), tb, kq);
       accum(D, dq, s);
       __builtin_amdgcn_sched_barrier(0);
-      rload(R[j], min(s + 4, last));
+      rload(R[j], min(s + RING, last));
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  // the last 0..3 records: already in R[0..2] and X[0]; nothing more to load
-  const int rem = empty ? 0 : (uend - ubeg) & 3;
+  // the last 0..RING-1 records: already in R[0..RING-2] (and X[0]); nothing more to load
+  const int rem = empty ? 0 : (uend - ubeg) - nfull;
   const int ut = ubeg + nfull;
 #pragma unroll
-  for (int j = 0; j < 3; ++j) {
+  for (int j = 0; j < RING - 1; ++j) {
     if (j < rem) {
       f4_t D[NMAT];
       float dq[NMAT];
-      if (j > 0) xload(X[j & 1], ut + j);
-      rec_dot<NMAT>(D, dq, R[j], X[j & 1], tb, kq);
+      if constexpr (!XS) {
+        if (j > 0) xload(X[j & 1], ut + j);
+      }
+      rec_dot<NMAT>(D, dq, R[j], xsrc(ut + j, j), tb, kq);
       accum(D, dq, ut + j);
     }
   }
-  if constexpr (XM == 2) __syncthreads();   // the parts overwrite the staged activations
+  if constexpr (XS) __syncthreads();   // the parts overwrite the staged activations
   if (!empty) {
 #pragma unroll
     for (int i = 0; i < NMAT; ++i) {
@@ -450,7 +463,9 @@ template <int NMAT, int EPI, int W>
 void sk_launch(const SkArgs& a, hipStream_t st) {
   if constexpr (W == kXsWaves) {
     if (!a.xt && a.M * (2 * a.K + 16) <= kXsBytes) {
-      iq3s_kernel<NMAT, EPI, W, 2><<<a.G, W * TLX_WAVE, 0, st>>>(a);
+      // all kXsPer pieces per thread needed, or fewer (skip the loads past the end)
+      if (a.M * a.K / 8 > (kXsPer - 1) * W * TLX_WAVE) iq3s_kernel<NMAT, EPI, W, 2><<<a.G, W * TLX_WAVE, 0, st>>>(a);
+      else iq3s_kernel<NMAT, EPI, W, 3><<<a.G, W * TLX_WAVE, 0, st>>>(a);
       return;
     }
   }
