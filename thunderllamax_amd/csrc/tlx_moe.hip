@@ -7,14 +7,11 @@
 // k = 2048); its down slab at ptbl_dn[e] -- 2048 rows x 272 B (k = 512).  Pairs are
 // position-major, rank ascending: pair = 8 * pos + rank.
 //
-// Grouped GEMM design: a workgroup owns (expert, chunk of up to 64 of its pairs, stripe of 128
-// weight rows -- 64 gate + 64 up for the FFN, 128 rows for down); per 32-k step the 256
-// threads stage the 64 activation rows (gathered through the sorted pair list, converted to
-// fp16) and dequantize the 128 x 32 weights into LDS, then 4 waves run 16 pairs x 128 rows of
-// v_mfma_f32_16x16x32_f16 each.  IQ4_XS decode: a 256-entry LDS table maps a quant byte to
-// (kv[lo], kv[hi]) as fp16, so one lookup yields the two weights that byte holds (elements j
-// and j+16 of the group); the MFMA k order is chosen to pair them (A is staged in the same
-// order), and the group scale d*(ls-32) multiplies in fp16.
+// Grouped GEMMs: a GEMV form for small batches and a GEMM form for prefill (see each kernel).
+// IQ4_XS decode: a 256-entry table maps a quant byte to (kv[lo], kv[hi]) as fp16, so one lookup
+// yields the two weights that byte holds (elements j and j+16 of the group); the MFMA k order is
+// chosen to pair them (the activations follow the same order), and the group scale d*(ls-32)
+// multiplies in fp16.
 #include "tlx_common.h"
 
 #include <type_traits>
@@ -120,14 +117,15 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
 }
 
 // ------------------------------------------------------------------ sort
-// Stable counting sort of the pairs by expert, no atomics.  The pairs are taken in rounds of
-// 1024 (16 waves x 64 lanes, pair order = wave-major, lane-minor).  In a wave, 8 ballots over the
-// bits of the expert id give every lane the mask of lanes holding the same expert; its rank among
-// them is the popcount below it, and the lowest such lane writes the group's count.  Pass 1
-// accumulates the per-expert totals (-> eoff and the work items), pass 2 repeats the rounds and
-// scatters each pair to eoff[e] + (pairs of e in earlier rounds) + (in earlier waves of this
-// round) + (its rank in the wave).  Items: per expert, ceil(count / 64) chunks of its pairs,
-// expert ascending, item = expert << 16 | first pair offset in the bin.
+// Deterministic stable counting sort by expert, one workgroup of 16 waves.  Wave w owns the
+// contiguous pair range [w * span, (w + 1) * span); in each 64-pair step the 8 ballots over the id
+// bits give every lane the mask of lanes holding the same expert, its rank among them is the
+// popcount below it, and the lowest such lane updates the wave's private count for that expert
+// (distinct experts, distinct LDS words: no atomics, no barriers inside a pass).  Pass 1 counts;
+// one scan over (expert, wave) gives every wave its start in each bin -- bins are expert
+// ascending, inside a bin the waves in order, inside a wave the steps and lanes in order, i.e. pair
+// order (stable, as mmsort8); pass 2 repeats the steps and scatters.  Items: per expert
+// ceil(count / 64) chunks of its pairs, expert ascending, item = expert << 16 | first pair offset.
 constexpr int kMaxPairs = 16384;
 constexpr int kTok = 64;
 constexpr int kSortWaves = 16;
@@ -146,64 +144,80 @@ __device__ __forceinline__ uint64_t same_key_mask(uint32_t key) {
 __global__ __launch_bounds__(1024) void moe_sort_kernel(const uint16_t* __restrict__ eids, int* __restrict__ eoff,
                                                         uint16_t* __restrict__ plist, uint32_t* __restrict__ items,
                                                         uint32_t* __restrict__ nitp, int np) {
-  __shared__ uint16_t wcnt[kSortWaves][kE];   // this round: pairs of expert e in wave w
-  __shared__ int run[kE];                     // pairs of expert e before this round (pass 2: + eoff)
-  __shared__ int wtot[kE / 64][2];            // per-wave totals of the count scans
+  __shared__ int cnt[kSortWaves][kE];   // pass 1: pairs of expert e in wave w; then its running slot
+  __shared__ int wtot[kE / 64][2];      // per-wave totals of the expert scans
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint64_t below = (1ull << lane) - 1ull;
-  const int rounds = (np + 1023) / 1024;
-  if (t < kE) run[t] = 0;
-  for (int pass = 0; pass < 2; ++pass) {
-    for (int r = 0; r < rounds; ++r) {
-      for (int e = lane; e < kE; e += 64) wcnt[wave][e] = 0;
-      const int i = 1024 * r + t;
-      const bool valid = i < np;
-      const uint32_t key = valid ? (eids[i] & 0xFFu) : 0u;   // ids are < 256 by contract
-      uint64_t same = same_key_mask(key) & __ballot(valid);
-      if (!valid) same = 0;
-      const int rank = __builtin_popcountll(same & below);
-      __syncthreads();                                         // wcnt cleared
-      if (valid && rank == 0) wcnt[wave][key] = (uint16_t)__builtin_popcountll(same);
-      __syncthreads();
-      if (pass == 1 && valid) {
-        int pre = run[key];
-        for (int w = 0; w < wave; ++w) pre += wcnt[w][key];
-        plist[pre + rank] = (uint16_t)i;
-      }
-      __syncthreads();
-      if (t < kE) {
-        int s = 0;
+  const int span = ((np + kSortWaves - 1) / kSortWaves + 63) & ~63;
+  const int i0 = min(np, wave * span), i1 = min(np, i0 + span);
+  for (int e = lane; e < kE; e += 64) cnt[wave][e] = 0;   // the wave's own row (in-order LDS)
+  // the wave's expert ids, all requested at once (at most kSteps per lane), kept for both passes
+  constexpr int kSteps = kMaxPairs / kSortWaves / 64;
+  uint32_t keys[kSteps];
 #pragma unroll
-        for (int w = 0; w < kSortWaves; ++w) s += wcnt[w][t];
-        run[t] += s;
-      }
-      __syncthreads();
-    }
-    if (pass == 0) {   // totals -> bin offsets and work items; run[] becomes the bin starts
-      // exclusive prefix sums over the 256 experts of the pair counts and of the item counts
-      // (ceil(count / 64)): wave-inclusive scans, then the totals of the waves before
-      const int c = t < kE ? run[t] : 0, ni = (c + kTok - 1) / kTok;
-      int sc = c, si = ni;
+  for (int j = 0; j < kSteps; ++j) {
+    const int idx = i0 + 64 * j + lane;
+    keys[j] = idx < i1 ? (eids[idx] & 0xFFu) : 0u;   // ids are < 256 by contract
+  }
+  auto step = [&](int j, auto&& use) {
+    const int idx = i0 + 64 * j + lane;
+    const bool valid = idx < i1;
+    const uint32_t key = keys[j];
+    uint64_t same = same_key_mask(key) & __ballot(valid);   // every lane takes part in the ballots
+    if (!valid) same = 0;
+    if (valid) use(idx, key, __builtin_popcountll(same & below), __builtin_popcountll(same));
+  };
+  const int nsteps = (i1 - i0 + 63) / 64;   // <= kSteps
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int pc = __shfl_up(sc, o, 64), pi = __shfl_up(si, o, 64);
-        if (lane >= o) { sc += pc; si += pi; }
-      }
-      if (t < kE && lane == 63) { wtot[wave][0] = sc; wtot[wave][1] = si; }
-      __syncthreads();
-      if (t < kE) {
-        int bc = sc - c, bi = si - ni;
-        for (int w = 0; w < wave; ++w) { bc += wtot[w][0]; bi += wtot[w][1]; }
-        eoff[t] = bc;
-        for (int j = 0; j < ni; ++j) items[bi + j] = ((uint32_t)t << 16) | (uint32_t)(kTok * j);
-        run[t] = bc;
-        if (t == kE - 1) {
-          eoff[kE] = bc + c;
-          *nitp = (uint32_t)(bi + ni);
-        }
-      }
-      __syncthreads();
+  for (int j = 0; j < kSteps; ++j) {
+    if (j >= nsteps) break;
+    step(j, [&](int, uint32_t key, int rank, int n) {
+      if (rank == 0) cnt[wave][key] += n;
+    });
+  }
+  __syncthreads();
+  // expert e = t (t < 256): total over the waves; exclusive scans over the experts of the pair
+  // counts and of the item counts (wave-inclusive scans, then the totals of the waves before)
+  int c = 0, ni = 0, sc = 0, si = 0;
+  if (t < kE) {
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) c += cnt[w][t];
+    ni = (c + kTok - 1) / kTok;
+    sc = c;
+    si = ni;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int pc = __shfl_up(sc, o, 64), pi = __shfl_up(si, o, 64);
+      if (lane >= o) { sc += pc; si += pi; }
     }
+    if (lane == 63) { wtot[wave][0] = sc; wtot[wave][1] = si; }
+  }
+  __syncthreads();
+  if (t < kE) {
+    int bc = sc - c, bi = si - ni;
+    for (int w = 0; w < wave; ++w) { bc += wtot[w][0]; bi += wtot[w][1]; }
+    eoff[t] = bc;
+    for (int j = 0; j < ni; ++j) items[bi + j] = ((uint32_t)t << 16) | (uint32_t)(kTok * j);
+    if (t == kE - 1) {
+      eoff[kE] = bc + c;
+      *nitp = (uint32_t)(bi + ni);
+    }
+    // bin e: wave w's pairs start after the bin start and the earlier waves' pairs of e
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) {
+      const int n = cnt[w][t];
+      cnt[w][t] = bc;
+      bc += n;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kSteps; ++j) {
+    if (j >= nsteps) break;
+    step(j, [&](int idx, uint32_t key, int rank, int n) {
+      plist[cnt[wave][key] + rank] = (uint16_t)idx;
+      if (rank == 0) cnt[wave][key] += n;   // after every lane of the step has read it (in-order LDS)
+    });
   }
 }
 
@@ -226,16 +240,17 @@ using gbyte = const __attribute__((address_space(1))) uint8_t;
 // (FFN: 256 gate rows + the matching 256 up rows; down: 512 rows).  8 waves, two per SIMD; wave
 // w owns four 16-row tiles (FFN: gate tiles 2w, 2w + 1 of the stripe and the two matching up
 // tiles; down: tiles 4w..4w+3) over the whole K, so no reduction across waves.
-//   * weights go straight from HBM to registers and are decoded there, as in the GEMV form
-//     below: lane (col, kq) holds row col's sub-blocks kq, kq + 4 of each block (32 quant
-//     bytes + the 8-byte header);
-//   * activations: per 256-k block, the item's token rows are DMA'd (global -> LDS, 16 B a
-//     lane, one 1 KB row per wave-load) into a double-buffered fp32 tile, piece p of row t at
-//     slot p ^ (t & 7) so that the 8 lanes of a ds_read_b128 phase (rows col 0..7) hit distinct
-//     16-B slots; a wave converts each A fragment to fp16 once and uses it for its 4 tiles;
-//   * per block: wait for this block's data, one barrier, issue the next block's activation DMA
-//     and weight loads, then 8 x (NG groups x 4 tiles) MFMAs -- every load has a whole block of
-//     compute to land in;
+//   * weights go straight from HBM to registers (a block ahead) and are decoded there: lane
+//     (col, kq) holds row col's sub-blocks kq, kq + 4 of each block (32 quant bytes + the 8-byte
+//     header); each quant byte is looked up in a byte -> (kv[lo], kv[hi]) fp16 table kept once
+//     per lane (64 copies, copy l in bank l), so the wave's 64 lookups never collide in a bank;
+//   * activations: per 256-k block the item's token rows are loaded (a block ahead, through the
+//     sorted pair list), converted to fp16 once, and stored in LDS already in the MFMA k order
+//     (the 8 halves of piece p = 4 ib + c are x[32 ib + 4c + {0, 16, 1, 17, 2, 18, 3, 19}], the
+//     order the byte table pairs the weights in) with piece p of token row t at slot p ^ (t & 15):
+//     the 16 lanes of a fragment read hit 16 distinct 16-B slots;
+//   * per block: issue the next block's activation and weight loads, 8 x (NG groups x 4 tiles)
+//     MFMAs on this block, then store the next block's activations and one barrier;
 //   * blockIdx -> (item, stripe) keeps the stripes of an item on one XCD (workgroups are
 //     dispatched round-robin over the 8 XCDs), so its activations are read from that L2.
 constexpr int kPfTiles = 4;   // 16-row tiles per wave
@@ -243,10 +258,10 @@ constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * TLX_WAVE;
 
 struct __attribute__((aligned(16))) MoePfLds {
-  float a[2][kTok * 256];   // 256-k blocks of the item's activations, fp32, swizzled 16-B pieces
-  uint32_t lut[256];        // quant byte -> (kv[lo], kv[hi]) fp16
-  int xrow[kTok];           // activation row of token slot t
-  int orow[kTok];           // output row of token slot t
+  uint32_t lut[256 * TLX_WAVE];   // [quant byte][lane]: (kv[lo], kv[hi]) fp16
+  u4_t a[2][kTok * 32];           // 256-k blocks of the item's activations, fp16, [row][swizzled piece]
+  int xrow[kTok];                 // activation row of token slot t
+  int orow[kTok];                 // output row of token slot t
 };
 
 template <int KIND>
@@ -254,28 +269,33 @@ constexpr int moe_pf_stripes() {
   return (KIND == MOE_UP || KIND == MOE_UP_DENSE) ? kFf / (16 * 2 * kPfWaves) : kHid / (16 * kPfTiles * kPfWaves);
 }
 
-// DMA 256-k block kb of the item's token rows t < 16 * NG into buf: wave w moves rows 8w..8w+7
-// (xr: their activation rows, wave-uniform)
-template <int K, int NG>
-__device__ __forceinline__ void moe_pf_dma_a(float* buf, const int* xr, const float* __restrict__ xs, int kb,
-                                             int wave, int lane) {
-  if (8 * wave >= 16 * NG) return;
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const float* src = xs + (size_t)xr[r] * K + 256 * kb + 4 * (lane ^ r);   // row 8w + r: r = t & 7
-    __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(buf + 256 * (8 * wave + r)),
-                                     16, 0, 0);
-  }
+// token rows 16g..16g+15 of block kb: thread t loads piece p = t & 31 of row 16g + (t >> 5) --
+// x[row][256 kb + 32 ib + 4c .. + 3] and [.. + 16 .. + 19] with ib = p >> 2, c = p & 3
+template <int K>
+__device__ __forceinline__ void moe_pf_load_a(float4 (&v)[2], const MoePfLds& L, const float* __restrict__ xs, int kb,
+                                              int g, int t) {
+  const int row = 16 * g + (t >> 5), p = t & 31;
+  const float* src = xs + (size_t)L.xrow[row] * K + 256 * kb + 32 * (p >> 2) + 4 * (p & 3);
+  v[0] = *reinterpret_cast<const float4*>(src);
+  v[1] = *reinterpret_cast<const float4*>(src + 16);
+}
+
+__device__ __forceinline__ void moe_pf_store_a(u4_t* buf, const float4 (&v)[2], int g, int t) {
+  const int row = 16 * g + (t >> 5), p = t & 31;
+  const h8_t h = {(_Float16)v[0].x, (_Float16)v[1].x, (_Float16)v[0].y, (_Float16)v[1].y,
+                  (_Float16)v[0].z, (_Float16)v[1].z, (_Float16)v[0].w, (_Float16)v[1].w};
+  buf[row * 32 + (p ^ (row & 15))] = __builtin_bit_cast(u4_t, h);
 }
 
 template <int KIND, int NG>
 __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, gbyte* base, const float* __restrict__ xs,
-                                            void* __restrict__ out, int ntok, int stripe, int wave, int lane) {
+                                            const float* __restrict__ iq4nl, void* __restrict__ out, int ntok,
+                                            int stripe, int wave, int lane) {
   using S = MoeShape<KIND>;
   constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
   constexpr int kNb = S::K / 256;
   constexpr int kRowBytes = kNb * 136;
-  const int col = lane & 15, kq = lane >> 4;
+  const int col = lane & 15, kq = lane >> 4, t = threadIdx.x;
   // the wave's tiles: FFN gate tiles 2 * (kPfWaves * stripe + wave) + {0, 1}, then the same up
   // tiles; down tiles 4 * (kPfWaves * stripe + wave) + {0..3}
   const int tb = kPfWaves * stripe + wave;
@@ -298,6 +318,15 @@ __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, gbyte* base, const floa
       qv[set][j][1] = *(const __attribute__((address_space(1))) u4_t*)(blk + 72 + 16 * kq);
     }
   };
+  float4 xa[NG][2];   // the next block's activations, in flight during this block's MFMAs
+  auto load_a = [&](int kb) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) moe_pf_load_a<S::K>(xa[g], L, xs, kb, g, t);
+  };
+  auto store_a = [&](u4_t* buf) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) moe_pf_store_a(buf, xa[g], g, t);
+  };
 
   f4_t acc[NG][kPfTiles];
 #pragma unroll
@@ -305,18 +334,14 @@ __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, gbyte* base, const floa
 #pragma unroll
     for (int j = 0; j < kPfTiles; ++j) acc[g][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int sw = col & 7;
-  int xr[8];   // the activation rows this wave stages (scalar registers: read from LDS once)
-#pragma unroll
-  for (int r = 0; r < 8; ++r) xr[r] = __builtin_amdgcn_readfirstlane(L.xrow[8 * wave + r]);
+  const uint8_t* lutb = reinterpret_cast<const uint8_t*>(L.lut) + 4 * lane;   // this lane's copy
+  auto lut = [&](uint32_t byte_x256) { return *reinterpret_cast<const uint32_t*>(lutb + byte_x256); };
 
   // block kb reads activation buffer / weight register set kb & 1 (= set)
   auto block = [&](int kb, int set) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this block's activations and weights
-    __syncthreads();                      // ... for every wave; block kb - 1's buffer is free
-    if (kb + 1 < kNb) moe_pf_dma_a<S::K, NG>(L.a[set ^ 1], xr, xs, kb + 1, wave, lane);
+    if (kb + 1 < kNb) load_a(kb + 1);
     load_w(min(kb + 1, kNb - 1), set ^ 1);   // clamped on the last block
-    const float* arow = L.a[set] + 256 * col;   // + 4096 * g: token row 16g + col
+    const u4_t* arow = L.a[set] + 32 * col;   // + 512 * g: token row 16g + col (slot p ^ col)
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       const int ib = kq + 4 * sb;
@@ -333,26 +358,39 @@ __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, gbyte* base, const floa
 #pragma unroll
         for (int j = 0; j < kPfTiles; ++j) {
           const uint32_t qw = qv[set][j][sb][c];
-          const u4_t w4 = {L.lut[qw & 0xFF], L.lut[(qw >> 8) & 0xFF], L.lut[(qw >> 16) & 0xFF], L.lut[qw >> 24]};
+          // byte i of qw times 256: the row of the byte table
+          const u4_t w4 = {lut((qw << 8) & 0xFF00u), lut(qw & 0xFF00u), lut((qw >> 8) & 0xFF00u),
+                           lut((qw >> 16) & 0xFF00u)};
           B[j] = __builtin_bit_cast(h8_t, w4) * splat8h(dh[j]);
         }
-        const int pc = 8 * kq + 32 * sb + c;   // 16-B piece of k0 = 32kq + 128sb + 4c
+        const int pc = 4 * ib + c;   // 16-B piece: k0 = 32 ib + 4c (and + 16)
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-          const float4 x0 = *reinterpret_cast<const float4*>(arow + 4096 * g + 4 * (pc ^ sw));
-          const float4 x1 = *reinterpret_cast<const float4*>(arow + 4096 * g + 4 * ((pc + 4) ^ sw));
-          const h8_t A = {(_Float16)x0.x, (_Float16)x1.x, (_Float16)x0.y, (_Float16)x1.y,
-                          (_Float16)x0.z, (_Float16)x1.z, (_Float16)x0.w, (_Float16)x1.w};
+          const h8_t A = __builtin_bit_cast(h8_t, arow[512 * g + (pc ^ col)]);
 #pragma unroll
           for (int j = 0; j < kPfTiles; ++j)
             acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], acc[g][j], 0, 0, 0);
         }
       }
     }
+    if (kb + 1 < kNb) store_a(L.a[set ^ 1]);   // (waits for its loads) block kb - 1's buffer is free
+    __syncthreads();
   };
 
-  moe_pf_dma_a<S::K, NG>(L.a[0], xr, xs, 0, wave, lane);
+  // block 0's weights first: the byte table is built while they are in flight
   load_w(0, 0);
+  {   // the byte table, one copy per lane: entry b of copy l at [b][l]
+#pragma unroll 4
+    for (int b = t >> 6; b < 256; b += kPfWaves) {
+      const _Float16 lo = (_Float16)iq4nl[b & 15], hi = (_Float16)iq4nl[b >> 4];
+      L.lut[b * TLX_WAVE + lane] =
+          (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+  }
+  __syncthreads();   // xrow / orow (written by the kernel before the tile) are visible
+  load_a(0);
+  store_a(L.a[0]);
+  __syncthreads();   // block 0's activations and the byte table are visible
   for (int kb = 0; kb < kNb; kb += 2) {
     block(kb, 0);
     block(kb + 1, 1);
@@ -430,16 +468,11 @@ __global__ __launch_bounds__(kPfThreads, 1) void moe_pf_kernel(
       L.orow[t] = pair;
     }
   }
-  if (t < 256) {
-    const _Float16 lo = (_Float16)iq4nl[t & 15], hi = (_Float16)iq4nl[t >> 4];
-    L.lut[t] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-  }
-  __syncthreads();
-  switch ((ntok + 15) >> 4) {   // workgroup-uniform
-    case 1: moe_pf_tile<KIND, 1>(L, base, xs, out, ntok, stripe, wave, lane); break;
-    case 2: moe_pf_tile<KIND, 2>(L, base, xs, out, ntok, stripe, wave, lane); break;
-    case 3: moe_pf_tile<KIND, 3>(L, base, xs, out, ntok, stripe, wave, lane); break;
-    default: moe_pf_tile<KIND, 4>(L, base, xs, out, ntok, stripe, wave, lane); break;
+  switch ((ntok + 15) >> 4) {   // workgroup-uniform (the tile's first barrier publishes xrow / orow)
+    case 1: moe_pf_tile<KIND, 1>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
+    case 2: moe_pf_tile<KIND, 2>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
+    case 3: moe_pf_tile<KIND, 3>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
+    default: moe_pf_tile<KIND, 4>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
   }
 }
 
