@@ -63,15 +63,16 @@ import time
 import numpy as np
 
 PEAK_HBM_GBS = 8000.0
-# HBM bytes per M=11 step (tile-ordered activation copy + ffn8), measured with two
-# `rocprofv3 --pmc` passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --ms 11 --steps 10 --warmup 2
-# --gemm-m 0 --no-sweep --no-moe --no-cpu --copy-mib 256`; the 256 MiB copy at the end reads
-# FETCH_SIZE = 131,089 KiB and WRITE_SIZE = 262,144 KiB, so fetches are scaled by 2.0, writes
-# by 1.0.  Re-measure when the kernel changes.
-FFN8_M11_TRAFFIC_BYTES = 75_608_191
-# The same for the tiled-record kernel (one launch; FETCH_SIZE 35,970.3 KiB, WRITE_SIZE 1,928 KiB at
-# M=11 with the same calibration; profiles/iq3s_ffn8_tiled_k5120_n17408.md).
-FFN8_TILED_M11_TRAFFIC_BYTES = 75_641_446
+# HBM bytes per M=11 step (tile-ordered activation copy + ffn8 over packed rows), measured with two
+# `rocprofv3 --pmc` passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --ms 11 --gemm-m 2048 --no-sweep
+# --no-formats --no-cpu --no-config1 --no-stream --steps 10 --warmup 2 --copy-mib 256`; the 256 MiB
+# copy at the end reads FETCH_SIZE = 131,088 KiB and WRITE_SIZE = 262,144 KiB, so fetches are
+# scaled by 2.0, writes by 1.0: (36,276.0 + 65.0) KiB x 2 + (374.0 + 160.0) KiB.  Re-measure when
+# the kernel changes.
+FFN8_M11_TRAFFIC_BYTES = 74_973_184
+# The same for the tiled-record kernel (one launch; FETCH_SIZE 35,842.2 KiB, WRITE_SIZE 1,922.0 KiB
+# at M=11 with the same calibration; profiles/pmc_counters_ffn8_pfgemm_moe.md).
+FFN8_TILED_M11_TRAFFIC_BYTES = 75_372_953
 PEAK_F16_TFLOPS = 2500.0
 PEAK_I8_TOPS = 5000.0
 ROT_BYTES = 300 * 2**20
@@ -788,7 +789,7 @@ def main():
         "per_m_other_layout": {"layout": other, **per_m_other},
         "roofline": hbm_roofline(
             value,
-            ("iq3s_kernel<2,1,8,2> (tiled records, activations staged in LDS)" if args.layout == "tiled" else
+            ("iq3s_kernel<2,1,8,3> (tiled records, activations staged in LDS)" if args.layout == "tiled" else
              "iq3_gemv_kernel<2,1,4> (+ iq3_xt_kernel for M >= 6)"),
             traffic=(None if head != "11" else
                      FFN8_TILED_M11_TRAFFIC_BYTES if args.layout == "tiled" else FFN8_M11_TRAFFIC_BYTES),
