@@ -3,15 +3,19 @@
 //
 // GEMV design (fp32 x, fp32 y -- a VALU kernel; fp32 activations do not fit the fp16 MFMA
 // operand without rounding them):
-//   * a workgroup of 4 waves owns 4 consecutive rows; every wave covers all 4 rows (one per
-//     16-lane quarter) and the waves split the K blocks (block b -> wave b % 4);
+//   * a workgroup of W waves owns 4 consecutive rows; every wave covers all 4 rows (one per
+//     16-lane quarter) and the waves split the K blocks (block b -> wave b % W), W = ceil(NB / 4)
+//     up to 16, so a wave has at most 4 blocks a round and issues all their loads before the
+//     first use (one memory round trip per round instead of one per block);
 //   * within a quarter, lane i owns half h = i >> 3 and the l-quad p = i & 7 of a block,
 //     i.e. the 16 weights k = 128h + 32g + 4p + j (g, j = 0..3): one dword each of
 //     ql[64h+4p], ql[64h+32+4p], qh[32h+4p] decodes all 16 with byte-parallel masks;
 //   * per (lane, g) the four products x*(q-32) are summed, then scaled once by d*sc[g]
 //     (the 4 weights share one 16-element scale group);
-//   * a 16-lane butterfly then a fixed-order LDS sum over the 4 waves finish the row.
+//   * a 16-lane butterfly then a fixed-order LDS sum over the W waves finish the row.
 #include "tlx_common.h"
+
+#include <algorithm>
 
 namespace {
 
@@ -56,11 +60,17 @@ __global__ __launch_bounds__(256) void q6k_dequant_kernel(const uint8_t* __restr
 }
 
 // ------------------------------------------------------------------ fp32 GEMV
-__global__ __launch_bounds__(256) void q6k_gemv_f32_kernel(const uint8_t* __restrict__ w,
-                                                           const float* __restrict__ x,
-                                                           float* __restrict__ y, int rows,
-                                                           int K, int layout) {
-  __shared__ float red[3][64];
+constexpr int kQ6Waves = 4;
+constexpr int kQ6MaxU = 8;      // blocks per wave per round (all their loads in flight together)
+constexpr int kQ6MaxK = 16384;  // x staged in LDS: K floats (64 KB at most)
+
+template <int U>
+__global__ __launch_bounds__(kQ6Waves * 64) void q6k_gemv_f32_kernel(const uint8_t* __restrict__ w,
+                                                                    const float* __restrict__ x,
+                                                                    float* __restrict__ y, int rows,
+                                                                    int K, int layout) {
+  extern __shared__ __align__(16) float xs[];   // K floats (dynamic: occupancy follows K)
+  __shared__ float red[kQ6Waves][4];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int quarter = lane >> 4, i = lane & 15;
   const int h = i >> 3, p = i & 7;
@@ -70,38 +80,61 @@ __global__ __launch_bounds__(256) void q6k_gemv_f32_kernel(const uint8_t* __rest
   const int row = min((int)blockIdx.x * 4 + quarter, rows - 1);
   const uint8_t* rp = w + (size_t)row * bs * nb;
 
+  // x into LDS by DMA (1 KB a wave instruction), issued ahead of the first round's weight loads
+  for (int q = wave; q < nb; q += kQ6Waves)
+    __builtin_amdgcn_global_load_lds((const void*)(x + 256 * q + 4 * lane),
+                                     (__attribute__((address_space(3))) void*)(xs + 256 * q), 16, 0, 0);
   float acc = 0.f;
-  for (int b = wave; b < nb; b += 4) {
-    const uint8_t* blk = rp + (size_t)b * bs;
-    const uint32_t qla = tlx_ldu<uint32_t>(blk + o.ql + 64 * h + 4 * p);
-    const uint32_t qlb = tlx_ldu<uint32_t>(blk + o.ql + 64 * h + 32 + 4 * p);
-    const uint32_t qh = tlx_ldu<uint32_t>(blk + o.qh + 32 * h + 4 * p);
-    const uint64_t sc8 = tlx_ldu<uint64_t>(blk + o.sc + 8 * h);
-    const float d = tlx_h2f(tlx_ldu<uint16_t>(blk + o.d));
-    const float* xb = x + 256 * b + 128 * h + 4 * p;
+  int b0 = wave;
+  do {   // every wave runs the first round (it holds the staging barrier)
+    // the round's blocks b0 + 4 j (past the end: the last block, loaded and weighted 0)
+    uint32_t qla[U], qlb[U], qhv[U];
+    uint64_t sc8[U];
+    uint16_t dh[U];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float4 xv = *reinterpret_cast<const float4*>(xb + 32 * g);
-      const uint32_t lo = (((g & 1) ? qlb : qla) >> ((g >> 1) * 4)) & 0x0F0F0F0Fu;
-      const uint32_t q = lo | (((qh >> (2 * g)) & 0x03030303u) << 4);
-      float s = xv.x * (float)((int)(q & 0xFF) - 32);
-      s += xv.y * (float)((int)((q >> 8) & 0xFF) - 32);
-      s += xv.z * (float)((int)((q >> 16) & 0xFF) - 32);
-      s += xv.w * (float)((int)(q >> 24) - 32);
-      const float sc = (float)(int8_t)(uint8_t)(sc8 >> (8 * ((p >> 2) + 2 * g)));
-      acc += (d * sc) * s;
+    for (int j = 0; j < U; ++j) {
+      const int b = min(b0 + kQ6Waves * j, nb - 1);
+      const uint8_t* blk = rp + (size_t)b * bs;
+      qla[j] = tlx_ldu<uint32_t>(blk + o.ql + 64 * h + 4 * p);
+      qlb[j] = tlx_ldu<uint32_t>(blk + o.ql + 64 * h + 32 + 4 * p);
+      qhv[j] = tlx_ldu<uint32_t>(blk + o.qh + 32 * h + 4 * p);
+      sc8[j] = tlx_ldu<uint64_t>(blk + o.sc + 8 * h);
+      dh[j] = tlx_ldu<uint16_t>(blk + o.d);
     }
-  }
+    if (b0 == wave) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's DMA pieces have landed
+      __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int b = b0 + kQ6Waves * j;
+      const float d = b < nb ? tlx_h2f(dh[j]) : 0.f;
+      const float* xb = xs + 256 * min(b, nb - 1) + 128 * h + 4 * p;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 xv = *reinterpret_cast<const float4*>(xb + 32 * g);
+        const uint32_t lo = (((g & 1) ? qlb[j] : qla[j]) >> ((g >> 1) * 4)) & 0x0F0F0F0Fu;
+        const uint32_t q = lo | (((qhv[j] >> (2 * g)) & 0x03030303u) << 4);
+        float s = xv.x * (float)((int)(q & 0xFF) - 32);
+        s += xv.y * (float)((int)((q >> 8) & 0xFF) - 32);
+        s += xv.z * (float)((int)((q >> 16) & 0xFF) - 32);
+        s += xv.w * (float)((int)(q >> 24) - 32);
+        const float sc = (float)(int8_t)(uint8_t)(sc8[j] >> (8 * ((p >> 2) + 2 * g)));
+        acc += (d * sc) * s;
+      }
+    }
+    b0 += kQ6Waves * U;
+  } while (b0 < nb);
 #pragma unroll
   for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 16);
-  if (wave > 0 && i == 0) red[wave - 1][quarter] = acc;
+  if (i == 0) red[wave][quarter] = acc;
   __syncthreads();
   if (wave == 0 && i == 0) {
-    acc += red[0][quarter];
-    acc += red[1][quarter];
-    acc += red[2][quarter];
+    float sum = red[0][quarter];
+#pragma unroll
+    for (int v = 1; v < kQ6Waves; ++v) sum += red[v][quarter];
     const int r = (int)blockIdx.x * 4 + quarter;
-    if (r < rows) y[r] = acc;
+    if (r < rows) y[r] = sum;
   }
 }
 
@@ -125,7 +158,21 @@ extern "C" int tlx_q6k_gemv(const void* w, const float* x, float* y, int rows, i
   TLX_RET_IF(rows < 1 || K < 256 || (K & 255), TLX_E_ARG);
   TLX_RET_IF(layout != TLX_LAYOUT_RAW && layout != TLX_LAYOUT_PACKED, TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(w, 4) || !tlx_aligned(x, 16), TLX_E_ALIGN);
-  q6k_gemv_f32_kernel<<<(rows + 3) / 4, 256, 0, (hipStream_t)stream>>>((const uint8_t*)w, x, y,
-                                                                        rows, K, layout);
+  TLX_RET_IF(K > kQ6MaxK, TLX_E_ARG);
+  const int nb = K >> 8, U = std::min(kQ6MaxU, (nb + kQ6Waves - 1) / kQ6Waves);
+  const dim3 grid((rows + 3) / 4), block(kQ6Waves * 64);
+  const size_t lds = (size_t)K * sizeof(float);
+  const uint8_t* wp = (const uint8_t*)w;
+  hipStream_t st = (hipStream_t)stream;
+  switch (U) {
+    case 1: q6k_gemv_f32_kernel<1><<<grid, block, lds, st>>>(wp, x, y, rows, K, layout); break;
+    case 2: q6k_gemv_f32_kernel<2><<<grid, block, lds, st>>>(wp, x, y, rows, K, layout); break;
+    case 3: q6k_gemv_f32_kernel<3><<<grid, block, lds, st>>>(wp, x, y, rows, K, layout); break;
+    case 4: q6k_gemv_f32_kernel<4><<<grid, block, lds, st>>>(wp, x, y, rows, K, layout); break;
+    case 5: q6k_gemv_f32_kernel<5><<<grid, block, lds, st>>>(wp, x, y, rows, K, layout); break;
+    case 6: q6k_gemv_f32_kernel<6><<<grid, block, lds, st>>>(wp, x, y, rows, K, layout); break;
+    case 7: q6k_gemv_f32_kernel<7><<<grid, block, lds, st>>>(wp, x, y, rows, K, layout); break;
+    default: q6k_gemv_f32_kernel<8><<<grid, block, lds, st>>>(wp, x, y, rows, K, layout); break;
+  }
   return tlx_launch_status();
 }
