@@ -311,17 +311,33 @@ int tlx_moe_sort(const uint16_t* eids, int* eoff, uint16_t* plist, uint32_t* ite
                  int np, void* stream);
 int tlx_moe_max_items(int np);
 
-/* Grouped gate+up + SwiGLU: ys[pair][512] = silu(Wg_e . x[pos]) * (Wu_e . x[pos]), f32.
- * Replaces gx8e256up4 / gxu_gm (engine/mm/MM_P2_gx8e256up4.cu:8-14, engine/mm/MM_E_gxu_gm.cu:86-93):
- * (ptbl, eoff, plist, xs f32[P][2048], iq4nl f32[16], ys). */
-int tlx_moe_up4(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const uint32_t* items,
-                const uint32_t* nitp, const float* xs, const float* iq4nl, float* ys, int np, void* stream);
+/* Grouped gate+up + SwiGLU over the sorted pairs: ys[pair][512] = silu(Wg_e . x[pos]) * (Wu_e . x[pos]),
+ * f32, pos = pair >> 3.  Replaces gxm_up4 (engine/mm/MM_B_gxm_up4.cu:20-28): gxm_up4(ptbl, items, nitp,
+ * eoff, plist, xs f32[P][2048], iq4nlb f32[16], ys), same positional order; items / nitp are the
+ * ones tlx_moe_sort wrote.  The fp16-MMA prefill form gxu_gm (engine/mm/MM_E_gxu_gm.cu:86-93) is
+ * the same call: np > 2048 runs the MFMA grouped GEMM. */
+int tlx_moe_up4(const uint64_t* ptbl, const uint32_t* items, const uint32_t* nitp, const int* eoff,
+                const uint16_t* plist, const float* xs, const float* iq4nl, float* ys, int np, void* stream);
 
-/* Grouped down: parts[pair][2048] = fp16(Wd_e . act[pair]).
- * Replaces gx8e256dn / gxd_gm (engine/mm/MM_P2_gx8e256dn.cu:9-15, engine/mm/MM_E_gxd_gm.cu:91-174). */
-int tlx_moe_dn4(const uint64_t* ptbl_dn, const int* eoff, const uint16_t* plist, const uint32_t* items,
-                const uint32_t* nitp, const float* act, const float* iq4nl, uint16_t* parts, int np,
+/* Grouped down over the sorted pairs: parts[pair][2048] = fp16(Wd_e . act[pair]).
+ * Replaces gxm_dn / gxm_dnf (engine/mm/MM_B_gxm_dn.cu:15-23, engine/mm/MM_C_gxm_dnf.cu:22):
+ * gxm_dn(ptbl, items, nitp, eoff, plist, xs = act f32[NPAIR][512], iq4nlb, parts), same order;
+ * np > 2048 runs the MFMA form (gxd_gm, engine/mm/MM_E_gxd_gm.cu:91-97). */
+int tlx_moe_dn4(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
+                const uint16_t* plist, const float* act, const float* iq4nl, uint16_t* parts, int np,
                 void* stream);
+
+/* Pair-walk decode form of tlx_moe_up4 (no sort): pair p runs expert eids[p] on x[p >> 3].
+ * Replaces gx8e256up4 (engine/mm/MM_P2_gx8e256up4.cu:8-14): gx8e256up4(ptbl, eids, xs, iq4nlb, ys)
+ * launched over NPAIR = np blocks.  Bit-identical to tlx_moe_up4 on the same pairs. */
+int tlx_moe_up4_pairs(const uint64_t* ptbl, const uint16_t* eids, const float* xs, const float* iq4nl,
+                      float* ys, int np, void* stream);
+
+/* Pair-walk decode form of tlx_moe_dn4: pair p runs expert eids[p] on act[p].
+ * Replaces gx8e256dn (engine/mm/MM_P2_gx8e256dn.cu:8-14): gx8e256dn(ptbl, eids, xs, iq4nlb, parts).
+ * Bit-identical to tlx_moe_dn4 on the same pairs. */
+int tlx_moe_dn4_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, const float* iq4nl,
+                      uint16_t* parts, int np, void* stream);
 
 /* Shared expert over all P positions: act[P][512] (caller scratch) then out[P][2048] f32.
  * ptbl_sh = {gate/up slab, down slab}.  Replaces shgu32 / shdn32 (engine/mm/MM_P2_ports.py:195-201

@@ -51,9 +51,9 @@ def _run_layer(gpu, ex, x, logits, sg, hres):
     nitp = torch.empty(1, dtype=torch.int32, device=gpu)
     ops.moe_sort(eids, eoff, plist, items, nitp)
     act = torch.empty(np_, moe.FF, dtype=torch.float32, device=gpu)
-    ops.moe_up4(ex["ptbl"], eoff, plist, items, nitp, dx, ex["iq4nl"], act)
+    ops.moe_up4(ex["ptbl"], items, nitp, eoff, plist, dx, ex["iq4nl"], act)
     parts = torch.empty(np_, moe.HID, dtype=torch.float16, device=gpu)
-    ops.moe_dn4(ex["ptbl_dn"], eoff, plist, items, nitp, act, ex["iq4nl"], parts)
+    ops.moe_dn4(ex["ptbl_dn"], items, nitp, eoff, plist, act, ex["iq4nl"], parts)
     sact = torch.empty(P, moe.FF, dtype=torch.float32, device=gpu)
     shared = torch.empty(P, moe.HID, dtype=torch.float32, device=gpu)
     ops.moe_shared(ex["ptbl_sh"], dx, ex["iq4nl"], sact, shared)
@@ -230,11 +230,29 @@ def test_moe_bad_arguments(gpu, experts):
     with pytest.raises(TlxError):
         ops.moe_topk(torch.zeros(0, 256, dtype=torch.float32, device=gpu), z, z)
     with pytest.raises(ValueError):   # a pointer table shorter than 256 entries never reaches the library
-        ops.moe_up4(experts["ptbl"][:8], torch.zeros(257, dtype=torch.int32, device=gpu),
-                    torch.zeros(8, dtype=torch.int16, device=gpu),
-                    torch.zeros(ops.moe_max_items(8), dtype=torch.int32, device=gpu),
-                    torch.zeros(1, dtype=torch.int32, device=gpu), torch.zeros(1, 2048, device=gpu),
+        ops.moe_up4(experts["ptbl"][:8], torch.zeros(ops.moe_max_items(8), dtype=torch.int32, device=gpu),
+                    torch.zeros(1, dtype=torch.int32, device=gpu), torch.zeros(257, dtype=torch.int32, device=gpu),
+                    torch.zeros(8, dtype=torch.int16, device=gpu), torch.zeros(1, 2048, device=gpu),
                     experts["iq4nl"], torch.zeros(8, 512, device=gpu))
+
+
+@pytest.mark.parametrize("P", [1, 11])
+def test_moe_pair_walk_equals_grouped(gpu, experts, P):
+    """The pair-walk decode forms (gx8e256up4 / gx8e256dn: expert eids[p], no sort) give the
+    grouped forms' act and parts bit for bit, and the oracle's within tolerance."""
+    print(f"[case] moe pair walk P={P}", flush=True)
+    rng = np.random.default_rng(40 + P)
+    x, logits, sg, hres = _inputs(rng, P)
+    a = _run_layer(gpu, experts, x, logits, sg, hres)
+    np_ = 8 * P
+    eids = torch.from_numpy(a["eids"].reshape(-1)).to(gpu)
+    act = torch.empty(np_, moe.FF, dtype=torch.float32, device=gpu)
+    ops.moe_up4_pairs(experts["ptbl"], eids, torch.from_numpy(x).to(gpu), experts["iq4nl"], act)
+    parts = torch.empty(np_, moe.HID, dtype=torch.float16, device=gpu)
+    ops.moe_dn4_pairs(experts["ptbl_dn"], eids, act, experts["iq4nl"], parts)
+    torch.cuda.synchronize()
+    assert np.array_equal(act.cpu().numpy(), a["act"])
+    assert np.array_equal(parts.cpu().numpy(), a["parts"])
 
 
 def test_moe_layer_overlapped_equals_sequential(gpu, experts):

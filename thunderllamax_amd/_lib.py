@@ -75,6 +75,8 @@ SIGNATURES = {
     "tlx_moe_max_items": [_i],
     "tlx_moe_up4": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _p],
     "tlx_moe_dn4": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _p],
+    "tlx_moe_up4_pairs": [_p, _p, _p, _p, _p, _i, _p],
+    "tlx_moe_dn4_pairs": [_p, _p, _p, _p, _p, _i, _p],
     "tlx_moe_shared": [_p, _p, _p, _p, _p, _i, _p],
     "tlx_moe_combine": [_p, _p, _p, _p, _p, _p, _i, _p],
     "tlx_stream_chunk_bytes": [],

@@ -619,8 +619,8 @@ template <int KIND>
 __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff,
                                                      const uint16_t* __restrict__ plist,
                                                      const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp,
-                                                     const float* __restrict__ xs, const float* __restrict__ iq4nl,
-                                                     void* __restrict__ out, int P) {
+                                                     const uint16_t* __restrict__ eids, const float* __restrict__ xs,
+                                                     const float* __restrict__ iq4nl, void* __restrict__ out, int P) {
   constexpr bool kDense = KIND == MOE_DN_DENSE || KIND == MOE_UP_DENSE;
   constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
   constexpr int NMAT = kUp ? 2 : 1;
@@ -636,6 +636,10 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
     m0 = (int)blockIdx.x * kTok;
     ntok = min(kTok, P - m0);
     base = (gbyte*)(ptbl[0]);
+  } else if (eids) {   // pair walk: workgroup column x is pair x, expert eids[x], no sort
+    m0 = (int)blockIdx.x;
+    ntok = 1;
+    base = (gbyte*)(ptbl[eids[m0]]);
   } else {
     if (blockIdx.x >= *nitp) return;
     const uint32_t it = items[blockIdx.x];
@@ -651,6 +655,9 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
     if constexpr (kDense) {
       xrow[t] = m0 + slot;
       orow[t] = m0 + slot;
+    } else if (eids) {
+      xrow[t] = kUp ? (m0 >> 3) : m0;
+      orow[t] = m0;
     } else {
       const int pair = plist[m0 + slot];
       xrow[t] = kUp ? (pair >> 3) : pair;
@@ -740,13 +747,13 @@ dim3 moe_gv_grid(int nx) {
   return dim3(nx, kRows / 16 / kTpw);
 }
 
-extern "C" int tlx_moe_up4(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const uint32_t* items,
-                           const uint32_t* nitp, const float* xs, const float* iq4nl, float* ys, int np, void* stream) {
+extern "C" int tlx_moe_up4(const uint64_t* ptbl, const uint32_t* items, const uint32_t* nitp, const int* eoff,
+                           const uint16_t* plist, const float* xs, const float* iq4nl, float* ys, int np, void* stream) {
   TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(xs, 16), TLX_E_ALIGN);
   if (np <= kGvMaxPairs) {
     moe_gv_kernel<MOE_UP><<<moe_gv_grid<MOE_UP>(moe_gv_items(np)), 256, 0, (hipStream_t)stream>>>(
-        ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, 0);
+        ptbl, eoff, plist, items, nitp, nullptr, xs, iq4nl, ys, 0);
     return tlx_launch_status();
   }
   moe_pf_kernel<MOE_UP><<<moe_pf_grid<MOE_UP>(moe_max_items(np)), kPfThreads, 0, (hipStream_t)stream>>>(
@@ -754,18 +761,36 @@ extern "C" int tlx_moe_up4(const uint64_t* ptbl, const int* eoff, const uint16_t
   return tlx_launch_status();
 }
 
-extern "C" int tlx_moe_dn4(const uint64_t* ptbl_dn, const int* eoff, const uint16_t* plist, const uint32_t* items,
-                           const uint32_t* nitp, const float* act, const float* iq4nl, uint16_t* parts, int np,
+extern "C" int tlx_moe_dn4(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
+                           const uint16_t* plist, const float* act, const float* iq4nl, uint16_t* parts, int np,
                            void* stream) {
   TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(act, 16) || !tlx_aligned(parts, 16), TLX_E_ALIGN);
   if (np <= kGvMaxPairs) {
     moe_gv_kernel<MOE_DN><<<moe_gv_grid<MOE_DN>(moe_gv_items(np)), 256, 0, (hipStream_t)stream>>>(
-        ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
+        ptbl_dn, eoff, plist, items, nitp, nullptr, act, iq4nl, parts, 0);
     return tlx_launch_status();
   }
   moe_pf_kernel<MOE_DN><<<moe_pf_grid<MOE_DN>(moe_max_items(np)), kPfThreads, 0, (hipStream_t)stream>>>(
       ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_moe_up4_pairs(const uint64_t* ptbl, const uint16_t* eids, const float* xs, const float* iq4nl,
+                                 float* ys, int np, void* stream) {
+  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(xs, 16), TLX_E_ALIGN);
+  moe_gv_kernel<MOE_UP><<<moe_gv_grid<MOE_UP>(np), 256, 0, (hipStream_t)stream>>>(
+      ptbl, nullptr, nullptr, nullptr, nullptr, eids, xs, iq4nl, ys, 0);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_moe_dn4_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, const float* iq4nl,
+                                 uint16_t* parts, int np, void* stream) {
+  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(act, 16) || !tlx_aligned(parts, 16), TLX_E_ALIGN);
+  moe_gv_kernel<MOE_DN><<<moe_gv_grid<MOE_DN>(np), 256, 0, (hipStream_t)stream>>>(
+      ptbl_dn, nullptr, nullptr, nullptr, nullptr, eids, act, iq4nl, parts, 0);
   return tlx_launch_status();
 }
 
@@ -776,11 +801,11 @@ extern "C" int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const fl
   const int chunks = (P + kTok - 1) / kTok;
   if (8 * P <= kGvMaxPairs) {
     moe_gv_kernel<MOE_UP_DENSE><<<moe_gv_grid<MOE_UP_DENSE>(chunks), 256, 0, (hipStream_t)stream>>>(
-        ptbl_sh, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, act, P);
+        ptbl_sh, nullptr, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, act, P);
     int rc = tlx_launch_status();
     TLX_RET_IF(rc != TLX_OK, rc);
     moe_gv_kernel<MOE_DN_DENSE><<<moe_gv_grid<MOE_DN_DENSE>(chunks), 256, 0, (hipStream_t)stream>>>(
-        ptbl_sh + 1, nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
+        ptbl_sh + 1, nullptr, nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
     return tlx_launch_status();
   }
   moe_pf_kernel<MOE_UP_DENSE><<<moe_pf_grid<MOE_UP_DENSE>(chunks), kPfThreads, 0, (hipStream_t)stream>>>(

@@ -518,8 +518,9 @@ def moe_sort(eids, eoff, plist, items, nitp, stream=None):
          eids.numel(), _stream(stream))
 
 
-def moe_up4(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, stream=None):
-    """ys[pair][512] = silu(Wg_e . x[pos]) * (Wu_e . x[pos])   (gx8e256up4 / gxu_gm)."""
+def moe_up4(ptbl, items, nitp, eoff, plist, xs, iq4nl, ys, stream=None):
+    """gxm_up4(ptbl, items, nitp, eoff, plist, xs, iq4nlb, ys) over the sorted pairs:
+    ys[pair][512] = silu(Wg_e . x[pos]) * (Wu_e . x[pos]), pos = pair >> 3."""
     n = ys.shape[0]
     _need(ptbl, 256 * 8, "ptbl")
     _need(eoff, 257 * 4, "eoff")
@@ -529,12 +530,13 @@ def moe_up4(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, stream=None):
     _need(ys, n * 512 * 4, "ys")
     _need(iq4nl, 64, "iq4nl")
     _dev(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys)
-    call("tlx_moe_up4", ptbl.data_ptr(), eoff.data_ptr(), plist.data_ptr(), items.data_ptr(), nitp.data_ptr(),
+    call("tlx_moe_up4", ptbl.data_ptr(), items.data_ptr(), nitp.data_ptr(), eoff.data_ptr(), plist.data_ptr(),
          xs.data_ptr(), iq4nl.data_ptr(), ys.data_ptr(), ys.shape[0], _stream(stream))
 
 
-def moe_dn4(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, stream=None):
-    """parts[pair][2048] = fp16(Wd_e . act[pair])   (gx8e256dn / gxd_gm)."""
+def moe_dn4(ptbl_dn, items, nitp, eoff, plist, act, iq4nl, parts, stream=None):
+    """gxm_dn(ptbl, items, nitp, eoff, plist, act, iq4nlb, parts) over the sorted pairs:
+    parts[pair][2048] = fp16(Wd_e . act[pair])."""
     n = act.shape[0]
     _need(ptbl_dn, 256 * 8, "ptbl_dn")
     _need(eoff, 257 * 4, "eoff")
@@ -544,8 +546,34 @@ def moe_dn4(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, stream=None):
     _need(parts, n * 2048 * 2, "parts")
     _need(iq4nl, 64, "iq4nl")
     _dev(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts)
-    call("tlx_moe_dn4", ptbl_dn.data_ptr(), eoff.data_ptr(), plist.data_ptr(), items.data_ptr(), nitp.data_ptr(),
+    call("tlx_moe_dn4", ptbl_dn.data_ptr(), items.data_ptr(), nitp.data_ptr(), eoff.data_ptr(), plist.data_ptr(),
          act.data_ptr(), iq4nl.data_ptr(), parts.data_ptr(), act.shape[0], _stream(stream))
+
+
+def moe_up4_pairs(ptbl, eids, xs, iq4nl, ys, stream=None):
+    """gx8e256up4(ptbl, eids, xs, iq4nlb, ys): pair p runs expert eids[p] on x[p >> 3], no sort."""
+    n = ys.shape[0]
+    _need(ptbl, 256 * 8, "ptbl")
+    _need(eids, n * 2, "eids")
+    _need(xs, ((n + 7) // 8) * 2048 * 4, "xs")
+    _need(ys, n * 512 * 4, "ys")
+    _need(iq4nl, 64, "iq4nl")
+    _dev(ptbl, eids, xs, iq4nl, ys)
+    call("tlx_moe_up4_pairs", ptbl.data_ptr(), eids.data_ptr(), xs.data_ptr(), iq4nl.data_ptr(), ys.data_ptr(),
+         n, _stream(stream))
+
+
+def moe_dn4_pairs(ptbl_dn, eids, act, iq4nl, parts, stream=None):
+    """gx8e256dn(ptbl, eids, act, iq4nlb, parts): pair p runs expert eids[p] on act[p], no sort."""
+    n = act.shape[0]
+    _need(ptbl_dn, 256 * 8, "ptbl_dn")
+    _need(eids, n * 2, "eids")
+    _need(act, n * 512 * 4, "act")
+    _need(parts, n * 2048 * 2, "parts")
+    _need(iq4nl, 64, "iq4nl")
+    _dev(ptbl_dn, eids, act, iq4nl, parts)
+    call("tlx_moe_dn4_pairs", ptbl_dn.data_ptr(), eids.data_ptr(), act.data_ptr(), iq4nl.data_ptr(),
+         parts.data_ptr(), n, _stream(stream))
 
 
 def moe_shared(ptbl_sh, xs, iq4nl, act, out, stream=None):
@@ -613,8 +641,8 @@ def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, s
         moe_shared(ptbl_sh, xs, iq4nl, sc.sact, sc.shared, stream=side)
     moe_topk(logits, sc.eids, sc.gates, stream=cur)
     moe_sort(sc.eids, sc.eoff, sc.plist, sc.items, sc.nitp, stream=cur)
-    moe_up4(ptbl, sc.eoff, sc.plist, sc.items, sc.nitp, xs, iq4nl, sc.act, stream=cur)
-    moe_dn4(ptbl_dn, sc.eoff, sc.plist, sc.items, sc.nitp, sc.act, iq4nl, sc.parts, stream=cur)
+    moe_up4(ptbl, sc.items, sc.nitp, sc.eoff, sc.plist, xs, iq4nl, sc.act, stream=cur)
+    moe_dn4(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, iq4nl, sc.parts, stream=cur)
     if side is None:
         moe_shared(ptbl_sh, xs, iq4nl, sc.sact, sc.shared, stream=cur)
     else:
