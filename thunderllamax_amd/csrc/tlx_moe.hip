@@ -334,8 +334,14 @@ __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, gbyte* base, const floa
 #pragma unroll
     for (int j = 0; j < kPfTiles; ++j) acc[g][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  const uint8_t* lutb = reinterpret_cast<const uint8_t*>(L.lut) + 4 * lane;   // this lane's copy
-  auto lut = [&](uint32_t byte_x256) { return *reinterpret_cast<const uint32_t*>(lutb + byte_x256); };
+  // entry (quant byte i of qw) of this lane's copy: byte offset 256 * byte + 4 * lane, assembled by
+  // one byte permute (result bytes: [4 * lane, byte i, 0, 0])
+  const uint8_t* lut0 = reinterpret_cast<const uint8_t*>(L.lut);
+  const uint32_t lane4 = 4u * (uint32_t)lane;
+  auto lut = [&](uint32_t qw, int i) {
+    const uint32_t off = __builtin_amdgcn_perm(qw, lane4, 0x0C0C0000u | ((4u + (uint32_t)i) << 8));
+    return *reinterpret_cast<const uint32_t*>(lut0 + off);
+  };
 
   // block kb reads activation buffer / weight register set kb & 1 (= set)
   auto block = [&](int kb, int set) {
@@ -359,8 +365,7 @@ __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, gbyte* base, const floa
         for (int j = 0; j < kPfTiles; ++j) {
           const uint32_t qw = qv[set][j][sb][c];
           // byte i of qw times 256: the row of the byte table
-          const u4_t w4 = {lut((qw << 8) & 0xFF00u), lut(qw & 0xFF00u), lut((qw >> 8) & 0xFF00u),
-                           lut((qw >> 16) & 0xFF00u)};
+          const u4_t w4 = {lut(qw, 0), lut(qw, 1), lut(qw, 2), lut(qw, 3)};
           B[j] = __builtin_bit_cast(h8_t, w4) * splat8h(dh[j]);
         }
         const int pc = 4 * ib + c;   // 16-B piece: k0 = 32 ib + 4c (and + 16)
@@ -379,9 +384,11 @@ __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, gbyte* base, const floa
 
   // block 0's weights first: the byte table is built while they are in flight
   load_w(0, 0);
-  {   // the byte table, one copy per lane: entry b of copy l at [b][l]
-#pragma unroll 4
-    for (int b = t >> 6; b < 256; b += kPfWaves) {
+  {   // the byte table, one copy per lane: entry b of copy l at [b][l]; wave w writes the entries
+      // b = w + 8i, whose two table values are wave-uniform (scalar loads)
+#pragma unroll
+    for (int i = 0; i < 256 / kPfWaves; ++i) {
+      const int b = wave + kPfWaves * i;
       const _Float16 lo = (_Float16)iq4nl[b & 15], hi = (_Float16)iq4nl[b >> 4];
       L.lut[b * TLX_WAVE + lane] =
           (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
