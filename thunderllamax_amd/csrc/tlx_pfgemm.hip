@@ -10,9 +10,10 @@
 // Design:
 //   * workgroup tile 256 (m) x 256 (n) x 32 (k) per step; for FFN the 256 n are 128 gate + 128
 //     up rows of one n-range, so a lane holds g and u of the same output element;
-//   * 4 waves (one per SIMD, so each owns 512 registers); wave (wm, wn) computes m [128wm, +128)
-//     x 128 n (FFN: 64 gate + 64 up columns of one n-range) with v_mfma_f32_16x16x32_f16,
-//     64 MFMAs per step into 256 accumulator registers;
+//   * 8 waves, two per SIMD (256 registers each: while one waits at a dependency the other
+//     issues); wave (wm, wn) computes m [64wm, +64) x 128 n (FFN: 64 gate + 64 up columns of one
+//     n-range) with v_mfma_f32_16x16x32_f16, 32 MFMAs per step into 128 accumulator registers
+//     (measured against 4 waves of 128 x 128: +3-5% FFN, up to +10% down at M=8192);
 //   * every global->LDS load is a direct (LDS-DMA) 16-byte load in which each group of 4 lanes
 //     reads 64 contiguous bytes: that is what keeps the vector-memory path at full rate (a load
 //     whose 4-lane groups span 4 rows runs at a quarter of it);
@@ -37,8 +38,10 @@
 namespace {
 
 constexpr int kBM = 256, kBN = 256, kBK = 32;
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;                 // two per SIMD: one wave's stalls are the other's issue slots
 constexpr int kThreads = kWaves * TLX_WAVE;
+constexpr int kMI = kBM / (16 * (kWaves / 2));   // 16-row A fragments per wave (waves: kWaves/2 along m, 2 along n)
+constexpr int kLdW = 16 / kWaves;                // wave-loads per wave per 16-load burst
 constexpr int kTile = kBM * kBK;          // halfs per A or B tile
 
 enum PfEpi { PF_FFN = 0, PF_RES = 1, PF_F16 = 2 };
@@ -70,14 +73,14 @@ __device__ __forceinline__ void pf_build_table(uint32_t* tbl, const float* __res
 }
 
 // Stage chunk h (128 k) of the tile's 256 weight rows into ring slot `slot`: 32 groups x 512 B,
-// 16 wave-loads, wave w doing loads 4w..4w+3; load j moves tile groups 2j, 2j+1 (lane l: group
+// 16 wave-loads, wave w doing loads kLdW w .. kLdW w + kLdW - 1; load j moves tile groups 2j, 2j+1 (lane l: group
 // 2j + l / 32, unit l % 32).  FFN tiles take gate groups 16nt.. for tile groups 0-15 and the up
 // groups for 16-31.
 __device__ __forceinline__ void pf_dma_w(PfLds& L, int slot, const u4_t* __restrict__ w1, const u4_t* __restrict__ w2,
                                          bool ffn, int nt, int nch, int h, int wave, int lane) {
 #pragma unroll
-  for (int jj = 0; jj < 4; ++jj) {
-    const int j = 4 * wave + jj;
+  for (int jj = 0; jj < kLdW; ++jj) {
+    const int j = kLdW * wave + jj;
     const int G = 2 * j + (lane >> 5);
     const u4_t* base;
     int grp;
@@ -89,8 +92,10 @@ __device__ __forceinline__ void pf_dma_w(PfLds& L, int slot, const u4_t* __restr
   }
 }
 
-// Dequantize sub-block u (32 weights) of tile row r into the B tile.
-__device__ __forceinline__ void pf_dequant(const PfLds& L, _Float16* bt, int r, int u) {
+// Dequantize sub-block u (32 weights) of tile row r into the B tile: thread tid does row
+// tid % 256, pieces c of half tid / 256 (two threads a row).
+__device__ __forceinline__ void pf_dequant(const PfLds& L, _Float16* bt, int tid, int u) {
+  const int r = tid & (kBN - 1), c0 = (tid >> 8) * (4 * kBN / kThreads);
   const u4_t unit = L.w[(u >> 2) & 1][4 * r + (u & 3)];
   const uint32_t sw = unit.z;
   const _Float16 ks = (_Float16)((float)(2u * (sw >> 28) + 1u) * 0.25f);
@@ -98,7 +103,8 @@ __device__ __forceinline__ void pf_dequant(const PfLds& L, _Float16* bt, int r, 
   const h8_t kv = {ks, ks, ks, ks, ks, ks, ks, ks};
   const h8_t dv = {d, d, d, d, d, d, d, d};
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
+  for (int cc = 0; cc < 4 * kBN / kThreads; ++cc) {
+    const int c = c0 + cc;
     const uint32_t qd = (c >> 1) ? unit.y : unit.x;
     const uint32_t qw = (c & 1) ? (qd >> 16) : (qd & 0xFFFFu);
     const uint32_t sidx = (sw >> (7 * c)) & 0x7Fu;
@@ -113,14 +119,14 @@ __device__ __forceinline__ void pf_dequant(const PfLds& L, _Float16* bt, int r, 
   }
 }
 
-// Activations of k-step `step` (32 k) for the tile's 256 rows: 16 wave-loads, 4 per wave.  Load g
+// Activations of k-step `step` (32 k) for the tile's 256 rows: 16 wave-loads, kLdW per wave.  Load g
 // moves rows 16g..16g+15 x 64 B: lane l fills LDS piece l % 4 of row 16g + l / 4 with logical
 // piece (l % 4) ^ ((l / 8) % 4), the swizzle of row l / 4.
 __device__ __forceinline__ void pf_dma_a(_Float16* abuf, const _Float16* __restrict__ x, int m0, int K,
                                          int step, int wave, int lane) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int g = 4 * wave + j;
+  for (int j = 0; j < kLdW; ++j) {
+    const int g = kLdW * wave + j;
     const _Float16* src = x + (size_t)(m0 + 16 * g + (lane >> 2)) * K + kBK * step + 8 * ((lane & 3) ^ ((lane >> 3) & 3));
     __builtin_amdgcn_global_load_lds((const void*)src,
                                      (__attribute__((address_space(3))) void*)(abuf + 512 * g), 16, 0, 0);
@@ -128,7 +134,7 @@ __device__ __forceinline__ void pf_dma_a(_Float16* abuf, const _Float16* __restr
 }
 
 struct PfFrag {
-  h8_t a[8], b[8];
+  h8_t a[kMI], b[8];
 };
 
 // Operand loads of one step: A rows (group 8wm + i, row l % 16, piece l / 16 stored at
@@ -138,11 +144,11 @@ __device__ __forceinline__ void pf_load_frag(PfFrag& f, const _Float16* A, const
 #pragma unroll
   for (int j = 0; j < 8; ++j) f.b[j] = *reinterpret_cast<const h8_t*>(B + 512 * bg[j] + 8 * lane);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) f.a[i] = *reinterpret_cast<const h8_t*>(A + 512 * (8 * wm + i) + aoff);
+  for (int i = 0; i < kMI; ++i) f.a[i] = *reinterpret_cast<const h8_t*>(A + 512 * (kMI * wm + i) + aoff);
 }
 
 template <int I0, int I1>
-__device__ __forceinline__ void pf_mfma(f4_t (&acc)[8][8], const PfFrag& f) {
+__device__ __forceinline__ void pf_mfma(f4_t (&acc)[kMI][8], const PfFrag& f) {
 #pragma unroll
   for (int i = I0; i < I1; ++i)
 #pragma unroll
@@ -162,7 +168,7 @@ struct PfArgs {
 // of sub-block t+1 -- which the scheduler interleaves with the 64 MFMAs of step t, then the
 // barrier.
 template <bool kFfn>
-__device__ __forceinline__ void pf_step(PfLds& L, f4_t (&acc)[8][8], const PfArgs& g, const int* bg, int aoff,
+__device__ __forceinline__ void pf_step(PfLds& L, f4_t (&acc)[kMI][8], const PfArgs& g, const int* bg, int aoff,
                                         int t, int ra, int wave, int wm, int lane) {
   PfFrag f;
   pf_load_frag(f, L.a[ra], L.b[t & 1], bg, aoff, wm, lane);
@@ -179,14 +185,15 @@ __device__ __forceinline__ void pf_step(PfLds& L, f4_t (&acc)[8][8], const PfArg
   }
   // sub-block t+1 into the other B buffer (clamped on the last step: not read again)
   pf_dequant(L, L.b[(t + 1) & 1], threadIdx.x, min(t + 1, g.tlast));
-  pf_mfma<0, 8>(acc, f);
+  pf_mfma<0, kMI>(acc, f);
   // step t+1's activations (issued one step earlier) and every earlier chunk burst must have
   // landed; this step's loads (4, or 8 on a burst step) stay in flight.  Then a barrier without
   // a memory fence (a fence would also wait for those).  The scheduling fences keep every MFMA
   // of the step on its side of the barrier (MFMAs touch no memory, so the asm alone would not).
   __builtin_amdgcn_sched_barrier(0);
-  if (wstep) asm volatile("s_waitcnt vmcnt(8)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(4)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  static_assert(kLdW == 2, "the wait counts below assume 2 A loads (+2 weight loads) per wave per step");
+  if (wstep) asm volatile("s_waitcnt vmcnt(4)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(2)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -204,13 +211,13 @@ struct PfSk {
 };
 
 template <int EPI>
-__device__ __forceinline__ void pf_epilogue(const f4_t (&acc)[8][8], const int* bg, int m0, int nt, int wm, int kq,
+__device__ __forceinline__ void pf_epilogue(const f4_t (&acc)[kMI][8], const int* bg, int m0, int nt, int wm, int kq,
                                             int col, void* __restrict__ out, const float* __restrict__ res, int N) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kMI; ++i) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int m = m0 + 128 * wm + 16 * i + 4 * kq + e;
+      const int m = m0 + 16 * kMI * wm + 16 * i + 4 * kq + e;
       if constexpr (EPI == PF_FFN) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -288,9 +295,9 @@ __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
   for (int j = 0; j < 8; ++j) bg[j] = kFfn ? (j < 4 ? 4 * wn + j : 8 + 4 * wn + (j - 4)) : 8 * wn + j;
   const int aoff = 8 * (4 * col + (kq ^ ((col >> 1) & 3)));
 
-  f4_t acc[8][8];
+  f4_t acc[kMI][8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < kMI; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
@@ -306,7 +313,7 @@ __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
     // pf_fix_kernel, launched next on the stream, adds the parts in order and applies the epilogue
     f4_t* mine = reinterpret_cast<f4_t*>(sk.part) + (size_t)seg * (kBM * kBN / 4);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < kMI; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) mine[(i * 8 + j) * kThreads + threadIdx.x] = acc[i][j];
     return;
@@ -331,7 +338,7 @@ __global__ __launch_bounds__(kThreads) void pf_fix_kernel(const f4_t* __restrict
   constexpr bool kFfn = EPI == PF_FFN;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kq = lane >> 4, wm = wave >> 1, wn = wave & 1;
-  const int st = (int)blockIdx.x >> 3, i = (int)blockIdx.x & 7, tau = full + st;
+  const int st = (int)blockIdx.x / kMI, i = (int)blockIdx.x % kMI, tau = full + st;
   int mt, nt;
   if ((mtiles & 7) == 0) {
     const int l = tau >> 3;
@@ -354,7 +361,7 @@ __global__ __launch_bounds__(kThreads) void pf_fix_kernel(const f4_t* __restrict
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const int m = mt * kBM + 128 * wm + 16 * i + 4 * kq + e;
+    const int m = mt * kBM + 16 * kMI * wm + 16 * i + 4 * kq + e;
     if constexpr (EPI == PF_FFN) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -405,7 +412,7 @@ int pf_launch(const u4_t* w1, const u4_t* w2, const float* gridf, const _Float16
   if (sk.p > 1) {
     const int rc = tlx_launch_status();
     TLX_RET_IF(rc != TLX_OK, rc);
-    pf_fix_kernel<EPI><<<sk.r * 8, kThreads, 0, st>>>(reinterpret_cast<const f4_t*>(sk.part), out, res, N, mtiles,
+    pf_fix_kernel<EPI><<<sk.r * kMI, kThreads, 0, st>>>(reinterpret_cast<const f4_t*>(sk.part), out, res, N, mtiles,
                                                       ntiles, sk.full, sk.p);
   }
   return tlx_launch_status();
