@@ -355,7 +355,8 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
 def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True):
     """Config 3: the 64-layer dense decode step at M=11 plus the Q6_K head.  With ``tiled`` every
     IQ3_XXS tensor except the k/v rows beside a Q6_K q reads tiled records (repacked on the GPU
-    from the packed rows).  The four GDN projections that read the same x share one launch."""
+    from the packed rows).  The four GDN projections that read the same x share one launch, and
+    each FFN block hands ffn8's output to down8 in the tile-ordered form (no activation copy)."""
     from thunderllamax_amd._lib import LAYOUT_PACKED, LAYOUT_RAW, LAYOUT_TILED
     lay = LAYOUT_TILED if tiled else LAYOUT_PACKED
     H, F, M = 5120, 17408, 11
@@ -386,6 +387,7 @@ def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True):
     gridf = formats.gridf_tensor(dev)
     xs = {k: torch.randn(M, k, device=dev).half() for k in (H, 6144, F)}
     o = {n: torch.empty(M, n, dtype=torch.float16, device=dev) for n in (10240, 6144, 48, 12288, 1024, H, F)}
+    gt = ops.tileord_empty(F, dev)   # ffn8's output in the tile-ordered form (tiled records)
     vrow = torch.empty(M, 1024, dtype=torch.float16, device=dev)
     ab48 = torch.empty(M, 48, dtype=torch.float16, device=dev)
     hh = torch.randn(M, H, device=dev)
@@ -420,8 +422,13 @@ def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True):
             nbytes += sum(nb for _, nb in proj) + nbso
             kind = "gdn"
         (wg, nbg), (wu, nbu), (wd, nbd) = iq3t(F, H), iq3t(F, H), iq3t(H, F)
-        calls.append(lambda s, wg=wg, wu=wu: ops.ffn8(wg, wu, gridf, xs[H], o[F], layout=lay, stream=s))
-        calls.append(lambda s, wd=wd: ops.down8(wd, gridf, xs[F], hh, y, layout=lay, stream=s))
+        if tiled:   # the FFN block's hand-off: ffn8 writes the tile-ordered form down8 reads (no copy)
+            calls.append(lambda s, wg=wg, wu=wu: ops.ffn8(wg, wu, gridf, xs[H], gt, layout=lay, stream=s,
+                                                          out_tileord=True))
+            calls.append(lambda s, wd=wd: ops.down8(wd, gridf, gt, hh, y, layout=lay, stream=s, in_tileord=True))
+        else:
+            calls.append(lambda s, wg=wg, wu=wu: ops.ffn8(wg, wu, gridf, xs[H], o[F], layout=lay, stream=s))
+            calls.append(lambda s, wd=wd: ops.down8(wd, gridf, o[F], hh, y, layout=lay, stream=s))
         nbytes += nbg + nbu + nbd
         kinds[kind].append((c0, len(calls)))
     wh = q6(151936, H)

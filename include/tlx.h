@@ -137,6 +137,16 @@ int tlx_iq3_gemv_multi(const void* const* w, uint16_t* const* out, const int* n,
  *     (engine/a_qkv_q6.cu:88-125).
  * xh_f16: [M][K]; qrow/krow/vrow: fp16 [M][Nq|Nk|Nv]. */
 #define TLX_V_Q4K 0x100  /* or-ed into `layout`: v rows are GGUF Q4_K */
+/* Or-ed into the `layout` of tlx_ffn8 / tlx_iq3_gemv (TLX_LAYOUT_TILED only): the fp16 output is
+ * written in the tile-ordered activation form [N/8][16][8] (N * 32 bytes; slot r of column group
+ * n/8 holds row r, rows M..15 repeat row M-1) instead of [M][N] -- the form in which the next
+ * IQ3_XXS GEMV reads its activations without a copy launch.  No reference counterpart (the
+ * reference's GEMVs take row-major activations); the values are those of the row-major output. */
+#define TLX_OUT_TILEORD 0x200
+/* Or-ed into the `layout` of tlx_ffn8 / tlx_down8 / tlx_iq3_gemv: the activations are already in
+ * the tile-ordered form [K/8][16][8] (e.g. written by a TLX_OUT_TILEORD call); results are bit
+ * for bit those of the row-major activations. */
+#define TLX_IN_TILEORD 0x400
 int tlx_aq3k8(const void* wq, const void* wk, const void* wv, const float* gridf,
               const uint16_t* xh_f16, uint16_t* qrow_f16, uint16_t* krow_f16, uint16_t* vrow_f16,
               int M, int Nq, int Nk, int Nv, int K, int layout, void* stream);

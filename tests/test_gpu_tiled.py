@@ -261,3 +261,54 @@ def test_tiled_small_and_unstaged_shapes(gpu, N, K, M):
     err = _rows_err(o.cpu().numpy(), ref)
     print(f"[tiled small N={N} K={K} M={M}] rel-err {err:.3e}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 4, 11, 16])
+def test_tileord_handoff_ffn8_down8(gpu, M):
+    """ffn8 writing its output in the tile-ordered form (TLX_OUT_TILEORD) and down8 reading it
+    (TLX_IN_TILEORD) give the row-major calls' results bit for bit; the tile-ordered buffer holds
+    the row-major rows and repeats row M-1 in slots M..15.  Shapes of config 2/3's FFN block."""
+    print(f"[case] tile-ordered ffn8 -> down8 M={M} N=17408 K=5120", flush=True)
+    rng = synth.config_rng(3)
+    H, F = 5120, 17408
+    _, tg = _mat(gpu, rng, F, H)
+    _, tu = _mat(gpu, rng, F, H)
+    _, td = _mat(gpu, rng, H, F)
+    g = formats.gridf_tensor(gpu)
+    x = torch.from_numpy(synth.activations_f16(rng, M, H)).to(gpu)
+    hh = torch.randn(M, H, device=gpu)
+    gact = torch.empty(M, F, dtype=torch.float16, device=gpu)
+    ops.ffn8(tg, tu, g, x, gact, LAYOUT_TILED)
+    gt = ops.tileord_empty(F, gpu)
+    ops.ffn8(tg, tu, g, x, gt, LAYOUT_TILED, out_tileord=True)
+    y = torch.empty(M, H, device=gpu)
+    ops.down8(td, g, gact, hh, y, LAYOUT_TILED)
+    yt = torch.empty(M, H, device=gpu)
+    ops.down8(td, g, gt, hh, yt, LAYOUT_TILED, in_tileord=True)
+    # the plain GEMV form over the same hand-off (fp16 output, tile-ordered both ways)
+    o = torch.empty(M, H, dtype=torch.float16, device=gpu)
+    ops.iq3_gemv(td, g, gact, o, LAYOUT_TILED)
+    ot = ops.tileord_empty(H, gpu)
+    ops.iq3_gemv(td, g, gt, ot, LAYOUT_TILED, in_tileord=True, out_tileord=True, m=M)
+    torch.cuda.synchronize()
+    rows = ops.tileord_to_rows(gt, 16).cpu().numpy()
+    assert np.array_equal(rows[:M], gact.cpu().numpy())
+    assert all(np.array_equal(rows[m], rows[M - 1]) for m in range(M, 16))
+    assert np.array_equal(yt.cpu().numpy(), y.cpu().numpy())
+    assert np.array_equal(ops.tileord_to_rows(ot, M).cpu().numpy(), o.cpu().numpy())
+
+
+def test_tileord_flags_rejected(gpu):
+    """The tile-ordered output exists for the tiled records only, and down8 has no fp16 output."""
+    print("[case] tile-ordered flag checks", flush=True)
+    from thunderllamax_amd import _lib
+    rng = synth.config_rng(3)
+    pg, tg = _mat(gpu, rng, 64, 512)
+    g = formats.gridf_tensor(gpu)
+    x = torch.from_numpy(synth.activations_f16(rng, 2, 512)).to(gpu)
+    dp = torch.from_numpy(pg).to(gpu)
+    with pytest.raises(TlxError):
+        ops.ffn8(dp, dp, g, x, ops.tileord_empty(64, gpu), LAYOUT_PACKED, out_tileord=True)
+    with pytest.raises(TlxError):
+        _lib.call("tlx_down8", tg.data_ptr(), g.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(), 2, 64, 512,
+                  LAYOUT_TILED | _lib.OUT_TILEORD, None)

@@ -24,6 +24,8 @@ LAYOUT_PACKED = 1
 LAYOUT_PACK7 = 2
 LAYOUT_TILED = 3
 V_Q4K = 0x100   # or-ed into the fused attention layout: v rows are GGUF Q4_K
+OUT_TILEORD = 0x200   # or-ed into an IQ3_XXS GEMV layout: fp16 output in the tile-ordered form [N/8][16][8]
+IN_TILEORD = 0x400    # or-ed into an IQ3_XXS GEMV layout: activations in the tile-ordered form [K/8][16][8]
 MAX_M = 16
 
 _p = ctypes.c_void_p

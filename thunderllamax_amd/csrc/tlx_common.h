@@ -136,7 +136,7 @@ bool tlx_iq3s_stages_x(int M, int K);
 //   ws: the GEMV workspace (kWsBytes; required)
 int tlx_iq3s_launch(int nmat, int epi, int nseg, const void* const* w, const void* w1, void* const* out,
                     const int* n, const float* res, const float* gridf, const _Float16* x, int xt, int M, int K,
-                    void* ws, hipStream_t st);
+                    void* ws, bool out_tileord, hipStream_t st);
 //   k-quants: fmt 0 = Q6_K raw, 1 = Q6_K padded, 2 = Q4_K, 3 = Q5_K (tlx_kquant.hip).
 //   one-time kernel set-up of the k-quant GEMVs (dynamic LDS limit), run by tlx_attach_workspace
 int tlx_kq_setup();

@@ -61,6 +61,7 @@ struct Iq3Launch {
   const float* gridf;
   const _Float16* x;   // activations [M][K], or (xt) the tile-ordered copy [K/8][16][8]
   int xt;
+  int otile;           // TLX_OUT_TILEORD: outputs in the tile-ordered form (tiled records only)
   int M, K;
   int layout;          // TLX_LAYOUT_RAW, TLX_LAYOUT_PACKED or TLX_LAYOUT_TILED
   void* ws;            // GEMV workspace (kWsBytes) or nullptr: iq3_launch then takes the attached one
@@ -243,8 +244,9 @@ int iq3_launch(Iq3Launch& a, int tiles, hipStream_t st) {
       n[i] = a.seg[i].n;
     }
     return tlx_iq3s_launch(NMAT, EPI, a.nseg, w, a.seg[0].w1, out, n, a.seg[0].res, a.gridf, a.x, a.xt, a.M,
-                           a.K, a.ws, st);
+                           a.K, a.ws, a.otile != 0, st);
   }
+  if (a.otile) return TLX_E_ARG;   // the tile-ordered output exists for the tiled records only
   int waves = 4;
   while (tiles * waves < 4096 && waves < 16 && nb >= 4 * waves) waves *= 2;
   switch (waves) {
@@ -256,6 +258,16 @@ int iq3_launch(Iq3Launch& a, int tiles, hipStream_t st) {
 }
 
 
+
+// Splits the activation-form flags off `layout`; TLX_E_ARG for flags the entry point does not take.
+int iq3_flags(int& layout, int allowed, Iq3Launch& a) {
+  const int fl = layout & (TLX_OUT_TILEORD | TLX_IN_TILEORD);
+  if (fl & ~allowed) return TLX_E_ARG;
+  layout &= ~(TLX_OUT_TILEORD | TLX_IN_TILEORD);
+  a.otile = (fl & TLX_OUT_TILEORD) ? 1 : 0;
+  a.xt = (fl & TLX_IN_TILEORD) ? 1 : 0;
+  return TLX_OK;
+}
 
 int iq3_check(const void* w, int M, int N, int K, int layout) {
   if (M < 1 || M > TLX_MAX_M || N < 1 || K < 256 || (K & 255)) return TLX_E_ARG;
@@ -341,11 +353,13 @@ extern "C" int tlx_iq3xxs_dequant(const void* w, const float* gridf, void* out, 
 
 extern "C" int tlx_ffn8(const void* wg, const void* wu, const float* gridf, const uint16_t* hhx_f16,
                         uint16_t* gact_f16, int M, int N, int K, int layout, void* stream) {
-  int rc = iq3_check(wg, M, N, K, layout);
+  Iq3Launch a{};
+  int rc = iq3_flags(layout, TLX_OUT_TILEORD | TLX_IN_TILEORD, a);
+  if (rc == TLX_OK) rc = iq3_check(wg, M, N, K, layout);
   if (rc == TLX_OK) rc = iq3_check(wu, M, N, K, layout);
   TLX_RET_IF(rc != TLX_OK, rc);
+  TLX_RET_IF(a.otile && (layout != TLX_LAYOUT_TILED || (N & 7)), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(hhx_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
-  Iq3Launch a{};
   a.seg[0] = Iq3Seg{(const uint8_t*)wg, (const uint8_t*)wu, gact_f16, nullptr, N, 0};
   a.layout = layout;
   a.nseg = 1;
@@ -445,10 +459,11 @@ extern "C" int tlx_ffn8_hh(const void* wg, const void* wu, const float* gridf, c
 
 extern "C" int tlx_down8(const void* wd, const float* gridf, const uint16_t* gact_f16,
                          const float* hh, float* y, int M, int N, int K, int layout, void* stream) {
-  const int rc = iq3_check(wd, M, N, K, layout);
+  Iq3Launch a{};
+  int rc = iq3_flags(layout, TLX_IN_TILEORD, a);
+  if (rc == TLX_OK) rc = iq3_check(wd, M, N, K, layout);
   TLX_RET_IF(rc != TLX_OK, rc);
   TLX_RET_IF(!tlx_aligned(gact_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
-  Iq3Launch a{};
   a.seg[0] = Iq3Seg{(const uint8_t*)wd, nullptr, y, hh, N, 0};
   a.layout = layout;
   a.nseg = 1;
@@ -461,10 +476,12 @@ extern "C" int tlx_down8(const void* wd, const float* gridf, const uint16_t* gac
 
 extern "C" int tlx_iq3_gemv(const void* w, const float* gridf, const uint16_t* x_f16,
                             uint16_t* out_f16, int M, int N, int K, int layout, void* stream) {
-  const int rc = iq3_check(w, M, N, K, layout);
-  TLX_RET_IF(rc != TLX_OK, rc);
-  TLX_RET_IF(!tlx_aligned(x_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
   Iq3Launch a{};
+  int rc = iq3_flags(layout, TLX_OUT_TILEORD | TLX_IN_TILEORD, a);
+  if (rc == TLX_OK) rc = iq3_check(w, M, N, K, layout);
+  TLX_RET_IF(rc != TLX_OK, rc);
+  TLX_RET_IF(a.otile && (layout != TLX_LAYOUT_TILED || (N & 7)), TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(x_f16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
   a.seg[0] = Iq3Seg{(const uint8_t*)w, nullptr, out_f16, nullptr, N, 0};
   a.layout = layout;
   a.nseg = 1;

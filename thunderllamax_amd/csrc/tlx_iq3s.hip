@@ -95,6 +95,7 @@ struct SkArgs {
   const float* gridf;
   const _Float16* x;   // [M][K], or (xt) the tile-ordered copy [K/8][16][8]
   int xt;
+  int otile;           // 1: fp16 outputs in the tile-ordered form [N/8][16][8] (all 16 rows)
   int M, K, nb, U, G;
   f4_t* part;          // workspace: boundary g: [lo | hi][NMAT][64 lanes]
   uint32_t* cnt;       // workspace: arrival counter per boundary (0 between calls, self-resetting)
@@ -153,6 +154,17 @@ __device__ __forceinline__ void epilogue(const SkArgs& a, const f4_t* acc, int t
   if (n >= a.sN[sg]) return;
   void* out = a.sout[sg];
   const int ld = a.sld[sg];
+  if constexpr (EPI != EPI_RESID) {
+    if (a.otile) {   // slot m of column group n / 8, every m: rows >= M hold row M-1's value
+      uint16_t* o = reinterpret_cast<uint16_t*>(out) + (size_t)(n >> 3) * 128 + (n & 7);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 4 * kq + r;
+        o[8 * m] = EPI == EPI_SWIGLU ? tlx_swiglu_bits(acc[0][r], acc[NMAT - 1][r]) : tlx_f2h_bits(acc[0][r]);
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int m = 4 * kq + r;
@@ -493,8 +505,9 @@ bool tlx_iq3s_stages_x(int M, int K) { return M * (2 * K + 16) <= kXsBytes; }
 // Epi; nseg matrices w[s] of n[s] rows (NMAT == 1, EPI_F16 when nseg > 1) share the activations.
 int tlx_iq3s_launch(int nmat, int epi, int nseg, const void* const* w, const void* w1, void* const* out,
                     const int* n, const float* res, const float* gridf, const _Float16* x, int xt, int M, int K,
-                    void* ws, hipStream_t st) {
+                    void* ws, bool out_tileord, hipStream_t st) {
   TLX_RET_IF(ws == nullptr, TLX_E_NOWS);
+  TLX_RET_IF(out_tileord && (nseg != 1 || epi == EPI_RESID), TLX_E_ARG);
   static_assert(size_t(kMaxG) * 2 * 2 * TLX_WAVE * sizeof(f4_t) <= kWsCntOff - kWsPartOff, "parts region");
   static_assert(size_t(kMaxG) * 4 <= kWsCntBytes, "counter region");
   TLX_RET_IF(nseg < 1 || nseg > kMaxSeg || (nseg > 1 && (nmat != 1 || epi != EPI_F16)), TLX_E_ARG);
@@ -504,6 +517,7 @@ int tlx_iq3s_launch(int nmat, int epi, int nseg, const void* const* w, const voi
   a.gridf = gridf;
   a.x = x;
   a.xt = xt;
+  a.otile = out_tileord ? 1 : 0;
   a.M = M;
   a.K = K;
   a.nb = K / 256;
@@ -561,7 +575,8 @@ int tlx_iq3s_launch(int nmat, int epi, int nseg, const void* const* w, const voi
       b.nseg = 1;
       b.sw[0] = (const uint8_t*)w[k] + rec0;
       b.w1 = a.w1 ? a.w1 + rec0 : nullptr;
-      b.sout[0] = (uint8_t*)out[k] + (size_t)t0 * 16 * osz;
+      // row-major: column offset t0 * 16; tile-ordered: column groups 2 t0 of 256 B each
+      b.sout[0] = (uint8_t*)out[k] + (out_tileord ? (size_t)t0 * 512 : (size_t)t0 * 16 * osz);
       b.sN[0] = std::min(n[k] - t0 * 16, T1 * 16);
       b.sld[0] = n[k];
       b.sT0[0] = 0;

@@ -8,7 +8,7 @@ allocated here.  Errors raise ``TlxError`` (the reference asserts in Python).
 """
 import torch
 
-from ._lib import LAYOUT_PACK7, LAYOUT_PACKED, LAYOUT_RAW, LAYOUT_TILED, V_Q4K, call
+from ._lib import IN_TILEORD, LAYOUT_PACK7, LAYOUT_PACKED, LAYOUT_RAW, LAYOUT_TILED, OUT_TILEORD, V_Q4K, call
 
 _F16 = torch.float16
 
@@ -72,6 +72,27 @@ def _mk(x):
     return 1 if x.dim() == 1 else x.shape[0]
 
 
+def tileord_empty(n, device, dtype=torch.float16):
+    """A buffer for n activations in the tile-ordered form [n/8][16][8] (the form in which the
+    IQ3_XXS GEMVs read activations without a copy launch; slot r holds row r, rows M..15 repeat
+    row M-1), for TLX_OUT_TILEORD outputs / TLX_IN_TILEORD inputs."""
+    if n % 8:
+        raise ValueError("the tile-ordered form needs a multiple of 8 columns")
+    return torch.empty(n // 8, 16, 8, dtype=dtype, device=device)
+
+
+def tileord_to_rows(t, m):
+    """The first m rows of a tile-ordered [n/8][16][8] buffer as a row-major [m][n] tensor."""
+    return t.permute(1, 0, 2).reshape(16, -1)[:m]
+
+
+def _tileord_n(t):
+    """Columns of a tile-ordered [n/8][16][8] buffer."""
+    if t.dim() != 3 or t.shape[1:] != (16, 8):
+        raise ValueError("a tile-ordered buffer is [n/8][16][8]")
+    return t.shape[0] * 8
+
+
 def _need(t, nbytes, what):
     """Raise unless buffer `t` holds at least `nbytes` bytes: the library sees only pointers,
     so a buffer too small for the shape and layout it is described with must be caught here."""
@@ -127,17 +148,20 @@ def iq4xs_dequant(w, iq4nl, out, kdim, stream=None):
 
 
 # ------------------------------------------------------------------ decode GEMVs
-def ffn8(wg, wu, gridf, hhx, gact, layout=LAYOUT_PACKED, stream=None):
-    """gact[m] = silu16(half(Wg·hhx[m])) * half(Wu·hhx[m])   (ffn8 / ffn8v{M})."""
-    M, K, N = _mk(hhx), hhx.shape[-1], gact.shape[-1]
+def ffn8(wg, wu, gridf, hhx, gact, layout=LAYOUT_PACKED, stream=None, out_tileord=False):
+    """gact[m] = silu16(half(Wg·hhx[m])) * half(Wu·hhx[m])   (ffn8 / ffn8v{M}).  With
+    ``out_tileord`` (tiled records only) gact is a tile-ordered [N/8][16][8] buffer (tileord_empty),
+    which down8 / iq3_gemv read with ``in_tileord`` and no copy launch."""
+    M, K = _mk(hhx), hhx.shape[-1]
+    N = _tileord_n(gact) if out_tileord else gact.shape[-1]
     _need(wg, _iq3_w(N, K, layout), "wg")
     _need(wu, _iq3_w(N, K, layout), "wu")
     _need(gridf, 4096, "gridf")
-    _need(gact, M * N * 2, "gact")
+    _need(gact, (16 if out_tileord else M) * N * 2, "gact")
     _dev(wg, wu, gridf, hhx, gact)
     _ws(wg)
     call("tlx_ffn8", wg.data_ptr(), wu.data_ptr(), gridf.data_ptr(), hhx.data_ptr(), gact.data_ptr(),
-         M, N, K, layout, _stream(stream))
+         M, N, K, layout | (OUT_TILEORD if out_tileord else 0), _stream(stream))
     return gact
 
 
@@ -196,29 +220,42 @@ def ffn8_hh(wg, wu, gridf, x, attn_out, nw2, hh, hhx, gact, layout=LAYOUT_PACKED
     return gact
 
 
-def down8(wd, gridf, gact, hh, y, layout=LAYOUT_PACKED, stream=None):
-    """y[m] = hh[m] + float(half(Wd·gact[m]))   (down8 / down8nw32_{M})."""
-    M, K, N = _mk(gact), gact.shape[-1], y.shape[-1]
+def down8(wd, gridf, gact, hh, y, layout=LAYOUT_PACKED, stream=None, in_tileord=False):
+    """y[m] = hh[m] + float(half(Wd·gact[m]))   (down8 / down8nw32_{M}).  With ``in_tileord``
+    gact is a tile-ordered [K/8][16][8] buffer (e.g. ffn8's ``out_tileord`` output) and M = y's rows."""
+    if in_tileord:
+        M, K = _mk(y), _tileord_n(gact)
+    else:
+        M, K = _mk(gact), gact.shape[-1]
+    N = y.shape[-1]
     _need(wd, _iq3_w(N, K, layout), "wd")
     _need(gridf, 4096, "gridf")
+    _need(gact, (16 if in_tileord else M) * K * 2, "gact")
     _need(hh, M * N * 4, "hh")
     _need(y, M * N * 4, "y")
     _dev(wd, gridf, gact, hh, y)
     _ws(wd)
     call("tlx_down8", wd.data_ptr(), gridf.data_ptr(), gact.data_ptr(), hh.data_ptr(), y.data_ptr(),
-         M, N, K, layout, _stream(stream))
+         M, N, K, layout | (IN_TILEORD if in_tileord else 0), _stream(stream))
     return y
 
 
-def iq3_gemv(w, gridf, x, out, layout=LAYOUT_PACKED, stream=None):
-    """out[m] = half(W·x[m])   (the IQ3ROWP segment body)."""
-    M, K, N = _mk(x), x.shape[-1], out.shape[-1]
+def iq3_gemv(w, gridf, x, out, layout=LAYOUT_PACKED, stream=None, in_tileord=False, out_tileord=False, m=None):
+    """out[m] = half(W·x[m])   (the IQ3ROWP segment body).  ``in_tileord`` / ``out_tileord``: x / out
+    in the tile-ordered [n/8][16][8] form (then M is given by ``m`` or the row-major side)."""
+    K = _tileord_n(x) if in_tileord else x.shape[-1]
+    N = _tileord_n(out) if out_tileord else out.shape[-1]
+    M = m if m is not None else (_mk(x) if not in_tileord else _mk(out) if not out_tileord else None)
+    if M is None:
+        raise ValueError("both sides tile-ordered: pass m")
     _need(w, _iq3_w(N, K, layout), "w")
     _need(gridf, 4096, "gridf")
-    _need(out, M * N * 2, "out")
+    _need(x, (16 if in_tileord else M) * K * 2, "x")
+    _need(out, (16 if out_tileord else M) * N * 2, "out")
     _dev(w, gridf, x, out)
     _ws(w)
-    call("tlx_iq3_gemv", w.data_ptr(), gridf.data_ptr(), x.data_ptr(), out.data_ptr(), M, N, K, layout,
+    fl = (IN_TILEORD if in_tileord else 0) | (OUT_TILEORD if out_tileord else 0)
+    call("tlx_iq3_gemv", w.data_ptr(), gridf.data_ptr(), x.data_ptr(), out.data_ptr(), M, N, K, layout | fl,
          _stream(stream))
     return out
 
