@@ -67,12 +67,12 @@ PEAK_HBM_GBS = 8000.0
 # `rocprofv3 --pmc` passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --ms 11 --gemm-m 2048 --no-sweep
 # --no-formats --no-cpu --no-config1 --no-stream --steps 10 --warmup 2 --copy-mib 256`; the 256 MiB
 # copy at the end reads FETCH_SIZE = 131,088 KiB and WRITE_SIZE = 262,144 KiB, so fetches are
-# scaled by 2.0, writes by 1.0: (36,276.0 + 65.0) KiB x 2 + (374.0 + 160.0) KiB.  Re-measure when
+# scaled by 2.0, writes by 1.0: (36,300.9 + 65.0) KiB x 2 + (374.0 + 160.0) KiB.  Re-measure when
 # the kernel changes.
-FFN8_M11_TRAFFIC_BYTES = 74_973_184
-# The same for the tiled-record kernel (one launch; FETCH_SIZE 35,842.2 KiB, WRITE_SIZE 1,922.0 KiB
+FFN8_M11_TRAFFIC_BYTES = 75_024_128
+# The same for the tiled-record kernel (one launch; FETCH_SIZE 35,843.8 KiB, WRITE_SIZE 1,922.0 KiB
 # at M=11 with the same calibration; profiles/pmc_counters_ffn8_pfgemm_moe.md).
-FFN8_TILED_M11_TRAFFIC_BYTES = 75_372_953
+FFN8_TILED_M11_TRAFFIC_BYTES = 75_376_256
 PEAK_F16_TFLOPS = 2500.0
 PEAK_I8_TOPS = 5000.0
 ROT_BYTES = 300 * 2**20
