@@ -203,6 +203,14 @@ def test_tiled_more_than_2048_tiles(gpu):
         tail = _rows_err(got.cpu().numpy()[:, 32768:], ref[:, 32768:])
         print(f"[{name} N=33000] rel-err {err:.3e}, rows past the first launch {tail:.3e}")
         assert err <= TOL and tail <= TOL
+    # the tile-ordered outputs of both launches (the second starts at column group 4096)
+    ot = ops.tileord_empty(N, gpu)
+    ft = ops.tileord_empty(N, gpu)
+    ops.iq3_gemv(ta, g, xd, ot, layout=LAYOUT_TILED, out_tileord=True)
+    ops.ffn8(ta, tb, g, xd, ft, layout=LAYOUT_TILED, out_tileord=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(ops.tileord_to_rows(ot, M).cpu().numpy(), o.cpu().numpy())
+    assert np.array_equal(ops.tileord_to_rows(ft, M).cpu().numpy(), f.cpu().numpy())
 
 
 # ------------------------------------------------------------------ the SwiGLU epilogue
