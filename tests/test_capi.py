@@ -90,7 +90,7 @@ def test_workspace_size_and_attach_validation():
     L = _lib.lib()
     g, m = ctypes.c_uint64(), ctypes.c_uint64()
     assert L.tlx_workspace_size(ctypes.byref(g), ctypes.byref(m)) == 0
-    assert 1 << 20 < g.value <= 4 << 20 and m.value == 128 << 20
+    assert 1 << 20 < g.value <= 8 << 20 and m.value == 128 << 20
     assert L.tlx_attach_workspace(0x1000, g.value - 1, None, 0, None) == _lib.TLX_E_ARG
     assert L.tlx_attach_workspace(0x1010, g.value, None, 0, None) == _lib.TLX_E_ALIGN
     assert L.tlx_attach_workspace(None, 0, 0x1010, m.value, None) == _lib.TLX_E_ALIGN

@@ -92,14 +92,21 @@ int tlx_cu_count();
 // Device memory the caller owns and attaches per device (tlx_attach_workspace, tlx_core.hip):
 // the IQ3_XXS decode GEMVs' scratch.  Calls that overlap in time on one device must not share it.
 //   [0, 1 MB)            partial tiles of the tiled-record GEMV (4 KB per workgroup boundary)
-//   [1 MB, 1 MB + 4 KB)  its per-boundary arrival counters (0 between calls; zeroed by attach)
+//   [1 MB, +4 KB)        their arrival counters (0 between calls; zeroed by attach)
+//   [1 MB + 4 KB, +4 KB) per-tile arrival counters of the k-split form (0 between calls)
 //   [1 MB + 64 KB, +2 MB) the tile-ordered activation copy of the packed-row GEMVs (K * 32 B)
+//   [3 MB + 64 KB, +4 MB) the k-split form's range partials ([tile][range][64 lanes] f4)
 constexpr size_t kWsPartOff = 0;
 constexpr size_t kWsCntOff = size_t(1) << 20;
 constexpr size_t kWsCntBytes = 4096;
+constexpr size_t kWsKcntOff = kWsCntOff + kWsCntBytes;
+constexpr size_t kWsKcntBytes = 4096;
 constexpr size_t kWsXtOff = (size_t(1) << 20) + (size_t(64) << 10);
 constexpr size_t kWsXtBytes = size_t(2) << 20;
-constexpr size_t kWsBytes = kWsXtOff + kWsXtBytes;
+constexpr size_t kWsBaseBytes = kWsXtOff + kWsXtBytes;   // what the forms without the k-split use
+constexpr size_t kWsKpartOff = kWsBaseBytes;
+constexpr size_t kWsKpartBytes = size_t(4) << 20;
+constexpr size_t kWsBytes = kWsKpartOff + kWsKpartBytes;
 // The attached GEMV workspace of the current device (nullptr when none is attached).
 int tlx_workspace(void** ws);
 // Zeroes the arrival counters of a GEMV workspace with a fill kernel on `st` (no memset node:
@@ -132,11 +139,11 @@ int tlx_iq3_segments(const void* const* w, uint16_t* const* out, const int* n, i
 //   IQ3_XXS tiled records: the balanced GEMV (tlx_iq3s.hip); arguments already validated, x the
 //   activations or (xt != 0) their tile-ordered copy; nmat 2 = gate/up pair with epi SwiGLU,
 //   epi 0 = fp16 out, 2 = fp32 residual; up to 4 fp16-out matrices (nseg) share one launch
-bool tlx_iq3s_stages_x(int M, int K);
-//   ws: the GEMV workspace (kWsBytes; required)
+bool tlx_iq3s_stages_x(int nmat, int M, int N, int K, int nseg, bool ws_kparts);
+//   ws: the GEMV workspace (required; kWsBytes, or kWsBaseBytes with ws_kparts false: no k-split)
 int tlx_iq3s_launch(int nmat, int epi, int nseg, const void* const* w, const void* w1, void* const* out,
                     const int* n, const float* res, const float* gridf, const _Float16* x, int xt, int M, int K,
-                    void* ws, bool out_tileord, hipStream_t st);
+                    void* ws, bool ws_kparts, bool out_tileord, hipStream_t st);
 //   k-quants: fmt 0 = Q6_K raw, 1 = Q6_K padded, 2 = Q4_K, 3 = Q5_K (tlx_kquant.hip).
 //   one-time kernel set-up of the k-quant GEMVs (dynamic LDS limit), run by tlx_attach_workspace
 int tlx_kq_setup();

@@ -50,7 +50,8 @@ int tlx_cu_count() {
 }
 
 int tlx_ws_clear_counters(void* ws, hipStream_t st) {
-  const int n = (int)(kWsCntBytes / 4);
+  static_assert(kWsKcntOff == kWsCntOff + kWsCntBytes, "the two counter regions are cleared together");
+  const int n = (int)((kWsCntBytes + kWsKcntBytes) / 4);
   ws_zero_kernel<<<(n + 255) / 256, 256, 0, st>>>(reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ws) + kWsCntOff), n);
   return tlx_launch_status();
 }

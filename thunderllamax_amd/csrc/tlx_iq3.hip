@@ -65,6 +65,7 @@ struct Iq3Launch {
   int M, K;
   int layout;          // TLX_LAYOUT_RAW, TLX_LAYOUT_PACKED or TLX_LAYOUT_TILED
   void* ws;            // GEMV workspace (kWsBytes) or nullptr: iq3_launch then takes the attached one
+  int noks;            // 1: ws has only the base regions (kWsBaseBytes): no k-split form
 };
 
 template <int NMAT>
@@ -224,7 +225,8 @@ int iq3_launch(Iq3Launch& a, int tiles, hipStream_t st) {
   if (a.layout == TLX_LAYOUT_TILED && a.ws == nullptr) return TLX_E_NOWS;   // parts and counters
   // same values, same arithmetic: only the activation loads change (larger K reads x directly);
   // a.xt set by the caller: a.x already is the tile-ordered copy (written by a producer)
-  const bool staged = a.layout == TLX_LAYOUT_TILED && tlx_iq3s_stages_x(a.M, a.K);  // no copy needed
+  const bool staged = a.layout == TLX_LAYOUT_TILED &&
+                      tlx_iq3s_stages_x(NMAT, a.M, a.seg[0].n, a.K, a.nseg, !a.noks);  // no copy needed
   // without a workspace the packed-row GEMV reads x directly (same values, slower loads)
   if (!a.xt && !staged && a.ws != nullptr && a.M >= kXtMinM && (size_t)a.K * 16 * 2 <= kWsXtBytes) {
     _Float16* xt = reinterpret_cast<_Float16*>(static_cast<uint8_t*>(a.ws) + kWsXtOff);
@@ -244,7 +246,7 @@ int iq3_launch(Iq3Launch& a, int tiles, hipStream_t st) {
       n[i] = a.seg[i].n;
     }
     return tlx_iq3s_launch(NMAT, EPI, a.nseg, w, a.seg[0].w1, out, n, a.seg[0].res, a.gridf, a.x, a.xt, a.M,
-                           a.K, a.ws, a.otile != 0, st);
+                           a.K, a.ws, !a.noks, a.otile != 0, st);
   }
   if (a.otile) return TLX_E_ARG;   // the tile-ordered output exists for the tiled records only
   int waves = 4;
@@ -372,13 +374,14 @@ extern "C" int tlx_ffn8(const void* wg, const void* wu, const float* gridf, cons
 
 // ------------------------------------------------------------------ ffn8 that allocates nothing
 // tlx_ffn8_noalloc runs tlx_ffn8's kernels on this file's own scratch instead of an attached
-// workspace: `scratch` is a file-scope device array with the GEMV workspace's regions (kWsBytes,
-// about 3 MB), one copy per device, held until the process ends.  In host code the array's name
+// workspace: `scratch` is a file-scope device array with the GEMV workspace's base regions
+// (kWsBaseBytes, about 3 MB; no k-split region, which only single-matrix GEMVs use), one copy per
+// device, held until the process ends.  In host code the array's name
 // is not a device address: the address is looked up once per device (hipGetSymbolAddress, with
 // the device current) and only that pointer is passed to kernels.
 namespace {
 
-__device__ __align__(256) uint8_t scratch[kWsBytes];
+__device__ __align__(256) uint8_t scratch[kWsBaseBytes];
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[64];   // per-device address of `scratch`
 
@@ -423,6 +426,7 @@ extern "C" int tlx_ffn8_noalloc(const void* wg, const void* wu, const float* gri
   a.M = M;
   a.K = K;
   a.ws = ws;
+  a.noks = 1;
   return iq3_launch<2, EPI_SWIGLU>(a, tiles_of(N), (hipStream_t)stream);
 }
 
@@ -443,7 +447,7 @@ extern "C" int tlx_ffn8_hh(const void* wg, const void* wu, const float* gridf, c
   a.M = M;
   a.K = K;
   _Float16* xt = nullptr;
-  const bool staged = layout == TLX_LAYOUT_TILED && tlx_iq3s_stages_x(M, K);
+  const bool staged = layout == TLX_LAYOUT_TILED && tlx_iq3s_stages_x(2, M, N, K, 1, true);
   rc = tlx_workspace(&a.ws);
   TLX_RET_IF(rc != TLX_OK, rc);
   TLX_RET_IF(layout == TLX_LAYOUT_TILED && a.ws == nullptr, TLX_E_NOWS);

@@ -99,6 +99,12 @@ struct SkArgs {
   int M, K, nb, U, G;
   f4_t* part;          // workspace: boundary g: [lo | hi][NMAT][64 lanes]
   uint32_t* cnt;       // workspace: arrival counter per boundary (0 between calls, self-resetting)
+  // k-split form (ks > 1): the K blocks in ks equal ranges of nbk blocks, range r computed by the
+  // gk workgroups r*gk .. r*gk+gk-1 over every tile; a tile's range partials are added in range
+  // order by the last of its ks arrivals
+  int ks, nbk, gk;
+  f4_t* kpart;         // workspace: [tile][ks][NMAT][64 lanes]
+  uint32_t* kcnt;      // workspace: arrival counter per tile (0 between calls, self-resetting)
 };
 
 // segment of launch tile t (wave-uniform)
@@ -234,46 +240,98 @@ __device__ __forceinline__ void rec_dot(f4_t* out, float* dq, const Rec<NMAT>& R
 __device__ __forceinline__ int range_begin(int gw, int GW, int U) { return unit_of(gw, GW, U); }
 
 // XM: where the activations come from -- 0: x [M][K] in global memory, 1: the tile-ordered copy
-// [K/8][16][8] in global memory, 2: x staged into LDS by the workgroup (W == kXsWaves), every
-// thread loading kXsPer pieces, 3: the same when fewer pieces are needed (small M: the loads past
-// the end are skipped).  Staged activations are read from LDS at the point of use (no register
+// [K/8][16][8] in global memory, 2: x (or the copy's first M rows) staged into LDS by the
+// workgroup (W == kXsWaves), every thread loading kXsPer pieces, 3: the same when fewer pieces are
+// needed (small M: the loads past the end are skipped).  Staged activations are read from LDS at the point of use (no register
 // copy), which leaves room for the shallower record ring below.
-template <int NMAT, int EPI, int W, int XM>
+template <int NMAT, int EPI, int W, int XM, bool KS>
 __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
   constexpr bool XS = XM >= 2;   // staged in LDS
   __shared__ SkLds<NMAT, W, XS> L;
   constexpr bool XT = XM == 1;
+  static_assert(!KS || NMAT == 1, "the k-split form is for single matrices");
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int col = lane & 15, kq = lane >> 4;
-  const int nb = a.nb, GW = a.G * W, gw = (int)blockIdx.x * W + wave;
-  const int ubeg = range_begin(gw, GW, a.U), uend = range_begin(gw + 1, GW, a.U);
+  // KS: record indices below are local to the workgroup's k-range: local record u = tile * nbl +
+  // j is global record tile * nb + kr * nbl + j.  Without it they are the global records.
+  const int nb = a.nb, nbl = KS ? a.nbk : nb;
+  const int kr = KS ? (int)blockIdx.x / a.gk : 0, bx = (int)blockIdx.x - kr * a.gk;
+  const int Ul = KS ? a.U / a.ks : a.U, GW = a.gk * W, gw = bx * W + wave;
+  int ubeg = range_begin(gw, GW, Ul), uend = range_begin(gw + 1, GW, Ul);
+  int last = max(min(uend, Ul) - 1, 0);
+  if constexpr (KS) {
+    // (pinned to scalar registers: the loop's record positions derive from them and are buffer
+    // offsets, which must be scalar)
+    ubeg = __builtin_amdgcn_readfirstlane(ubeg);
+    uend = __builtin_amdgcn_readfirstlane(uend);
+    last = __builtin_amdgcn_readfirstlane(last);
+  }
   const bool empty = ubeg >= uend;   // only when there are fewer records than waves
-  const int last = max(min(uend, a.U) - 1, 0);
-  // record u: segment, buffer resource(s) and offset (all wave-uniform, in SGPRs)
-  auto rload = [&](Rec<NMAT>& R, int u) {
+  // Record positions: index u; with KS also its block j = u % nbl within tile t = u / nbl, which
+  // the loop advances one record at a time (no divisions there: the load addresses wait on them).
+  struct Pos { int u, j, t; };
+  auto pos_at = [&](int u) {
+    if constexpr (KS)
+      return Pos{__builtin_amdgcn_readfirstlane(u), __builtin_amdgcn_readfirstlane(u % nbl),
+                 __builtin_amdgcn_readfirstlane(u / nbl)};
+    else
+      return Pos{u, 0, 0};
+  };
+  auto advance = [&](Pos& p) {   // p + 1, held at the wave's last record
+    // integer forms of the two conditions (no booleans: the compiler keeps those in vector
+    // registers across the loop, which would make the record offsets per-lane)
+    const int adv = (int)((uint32_t)(p.u - last) >> 31);       // 1 while p.u < last
+    const int nj = p.j + adv;
+    const int wrap = (int)((uint32_t)(nbl - 1 - nj) >> 31);    // 1 when nj == nbl
+    p.u += adv;
+    p.j = nj - wrap * nbl;
+    p.t += wrap;
+  };
+  // KS: the loads cover records min(ubeg, last) .. last, at most two tiles (tA, tB), so at most
+  // two segments, whose buffer resources and first records are set up here.
+  int tA = 0, gA = 0, gB = 0;
+  __amdgpu_buffer_rsrc_t rsA, rsB;
+  if constexpr (KS) {
+    tA = min(ubeg, last) / nbl;
+    auto seg_rs = [&](int t, int& g0) {
+      const int sg = seg_of(a, t);
+      const int u0 = a.sT0[sg] * nb, u1 = min(a.sT0[sg + 1], a.U / nb) * nb;
+      g0 = u0;
+      return rsrc_of(a.sw[sg], (uint32_t)(u1 - u0) * kRec);
+    };
+    rsA = seg_rs(tA, gA);
+    rsB = seg_rs(last / nbl, gB);
+  }
+  // record at p: segment, buffer resource(s) and offset (all wave-uniform, in SGPRs)
+  auto rload = [&](Rec<NMAT>& R, const Pos& p) {
     __amdgpu_buffer_rsrc_t rs[NMAT];
     int soff;
-    if constexpr (NMAT == 2) {
+    if constexpr (KS) {
+      const int g = p.t * nb + kr * nbl + p.j;
+      const bool inA = p.t == tA;
+      rs[0] = inA ? rsA : rsB;
+      soff = (g - (inA ? gA : gB)) * (int)kRec;
+    } else if constexpr (NMAT == 2) {
       rs[0] = rsrc_of(a.sw[0], (uint32_t)a.U * kRec);
       rs[1] = rsrc_of(a.w1, (uint32_t)a.U * kRec);
-      soff = u * (int)kRec;
+      soff = p.u * (int)kRec;
     } else {
-      const int sg = seg_of(a, u / nb);
+      const int sg = seg_of(a, p.u / nb);
       const int u0 = a.sT0[sg] * nb, u1 = min(a.sT0[sg + 1], a.U / nb) * nb;
       rs[0] = rsrc_of(a.sw[sg], (uint32_t)(u1 - u0) * kRec);
-      soff = (u - u0) * (int)kRec;
+      soff = (p.u - u0) * (int)kRec;
     }
     rec_load<NMAT>(R, rs, soff, lane, col);
   };
   // activations: block b, chunk c of lane (col, kq) at byte xv + b * xbs + c * xcs
   constexpr int xbs = XT ? 8192 : 512, xcs = XT ? 256 : 16;
-  const __amdgpu_buffer_rsrc_t rx = rsrc_of(a.x, XT ? (uint32_t)a.K * 32u : (uint32_t)(a.M * a.K) * 2u);
+  const __amdgpu_buffer_rsrc_t rx = rsrc_of(a.x, a.xt ? (uint32_t)a.K * 32u : (uint32_t)(a.M * a.K) * 2u);
   const int xv = XT ? 2 * (1024 * kq + 8 * col) : 2 * (min(col, a.M - 1) * a.K + 64 * kq);
-  const int xstr = 2 * a.K + 16;                                  // staged row bytes
+  const int xstr = 512 * nbl + 16;                                // staged row bytes (the range's k)
   const uint8_t* xsl = L.xs + min(col, a.M - 1) * xstr + 128 * kq;  // this lane's row, k = 64kq
-  auto xload = [&](h8_t* X, int u) {
-    const int b = u % nb;
+  auto xload = [&](h8_t* X, const Pos& p) {
+    const int b = KS ? kr * nbl + p.j : p.u % nb;
 #pragma unroll
     for (int c = 0; c < 8; ++c)
       X[c] = __builtin_bit_cast(h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, xv + xcs * c, xbs * b, 0));
@@ -289,17 +347,44 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
   // them leaves the records in flight.
   constexpr int kGw = 1024 / (W * TLX_WAVE);   // grid words (x 4 sign nibbles) per thread
   float4 gv[kGw];
-  // staged activations: 16-B pieces p = thread + j * blockDim of x (clamped to the last piece:
+  // staged activations: 16-B pieces p = thread + j * blockDim of x (past the end: the last piece;
   // loads stay unconditional, a repeated piece is stored twice with the same bytes)
   constexpr int kXp = XS ? kXsPer : 1;
   u4_t xp[kXp];
-  const int npc = a.M * a.K / 8;
+  const int kp = 32 * nbl;   // 16-B pieces per staged row
+  const int npc = a.M * kp;
+  // Staged piece p (8 k of one row).  Row-major x is read row by row (p = row * kp + k8); the
+  // tile-ordered copy [K/8][16][8] k-group by k-group (p = k8 * M + row: consecutive threads read
+  // consecutive 16-B rows of a 256-B group).  With p = hi * D + lo, the source piece index and the
+  // LDS byte offset are linear in (hi, lo) with per-form coefficients, and a thread's pieces step
+  // by the workgroup size, so (hi, lo) advance by (qB, rB) with one carry: no divisions and no
+  // branches per piece.  xd: the pieces' LDS byte offsets, for the stores after the table build.
+  int xd[kXp];
   if constexpr (XS) {
+    const bool xt = a.xt != 0;
+    constexpr int B = W * TLX_WAVE;
+    const int D = xt ? a.M : kp, qB = B / D, rB = B - qB * D;
+    const int sH = xt ? 16 : a.K / 8, s0 = xt ? kr * kp * 16 : kr * kp;
+    const int dH = xt ? 16 : xstr, dL = xt ? xstr : 16;
+    // past the end: the last piece (row M - 1, k8 kp - 1)
+    const int srcL = xt ? 16 * ((kr * kp + kp - 1) * 16 + a.M - 1) : 16 * ((a.M - 1) * (a.K / 8) + kr * kp + kp - 1);
+    const int dstL = (a.M - 1) * xstr + 16 * (kp - 1);
+    int hi = (int)threadIdx.x / D, lo = (int)threadIdx.x - hi * D;
 #pragma unroll
     for (int j = 0; j < kXp; ++j) {
-      if (XM == 3 && j * W * TLX_WAVE >= npc) break;   // (uniform) the rest is past the end
-      xp[j] = __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                           rx, 16 * min((int)threadIdx.x + j * W * TLX_WAVE, npc - 1), 0, 0));
+      // (XM 3: the pieces past the end are skipped by a uniform test, not a break: with the
+      // loop-carried (hi, lo) a break keeps the loop from unrolling and xp / xd in registers)
+      if (XM != 3 || j * B < npc) {
+        const bool in = (int)threadIdx.x + j * B < npc;
+        xd[j] = in ? hi * dH + lo * dL : dstL;
+        xp[j] = __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rx, in ? 16 * (hi * sH + lo + s0) : srcL, 0, 0));
+      }
+      lo += rB;
+      hi += qB;
+      const int carry = lo >= D ? 1 : 0;
+      lo -= carry * D;
+      hi += carry;
     }
   }
 #pragma unroll
@@ -310,22 +395,21 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
   Rec<NMAT> R[RING];
   h8_t X[XS ? 1 : 2][8];
   __builtin_amdgcn_sched_barrier(0);
-  rload(R[0], min(ubeg, last));
+  rload(R[0], pos_at(min(ubeg, last)));
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (!XS) xload(X[0], min(ubeg, last));
+  if constexpr (!XS) xload(X[0], pos_at(min(ubeg, last)));
 #pragma unroll
   for (int j = 1; j < RING; ++j) {
     __builtin_amdgcn_sched_barrier(0);
-    rload(R[j], min(ubeg + j, last));
+    rload(R[j], pos_at(min(ubeg + j, last)));
   }
+  // the loop's positions: next record load, next activation load, record computed
+  Pos pr = pos_at(min(ubeg + RING, last)), px = pos_at(min(ubeg + 1, last)), ps = pos_at(min(ubeg, last));
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (XS) {
-    const int kp = a.K / 8;   // pieces per row
 #pragma unroll
     for (int j = 0; j < kXp; ++j) {
-      if (XM == 3 && j * W * TLX_WAVE >= npc) break;
-      const int p = min((int)threadIdx.x + j * W * TLX_WAVE, npc - 1);
-      *reinterpret_cast<u4_t*>(L.xs + (p / kp) * xstr + 16 * (p % kp)) = xp[j];
+      if (XM != 3 || j * W * TLX_WAVE < npc) *reinterpret_cast<u4_t*>(L.xs + xd[j]) = xp[j];
     }
   }
 #pragma unroll
@@ -337,8 +421,8 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
   const uint8_t* tb = reinterpret_cast<const uint8_t*>(L.tbl);
 
   // a wave touches at most two tiles: records < split belong to the first
-  const int tfirst = ubeg / nb, tlast = empty ? tfirst : (uend - 1) / nb;
-  const int split = min(uend, (tfirst + 1) * nb);
+  const int tfirst = ubeg / nbl, tlast = empty ? tfirst : (uend - 1) / nbl;
+  const int split = min(uend, (tfirst + 1) * nbl);
   f4_t accA[NMAT], accB[NMAT];
 #pragma unroll
   for (int i = 0; i < NMAT; ++i) accA[i] = accB[i] = f4_t{0.f, 0.f, 0.f, 0.f};
@@ -353,8 +437,8 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
     }
   };
   // activations of record s: staged rows in LDS (read at the point of use), else the register set
-  auto xsrc = [&](int s, int j) -> const h8_t* {
-    if constexpr (XS) return reinterpret_cast<const h8_t*>(xsl + 512 * (s % nb));
+  auto xsrc = [&](const Pos& p, int j) -> const h8_t* {
+    if constexpr (XS) return reinterpret_cast<const h8_t*>(xsl + 512 * (KS ? p.j : p.u % nb));
     else return X[j & 1];
   };
   // full rounds of RING records: branch-free (a branch in the loop makes the wait counts conservative)
@@ -364,13 +448,21 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
     for (int j = 0; j < RING; ++j) {
       const int s = u + j;
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (!XS) xload(X[(j + 1) & 1], min(s + 1, last));
+      if constexpr (!XS) {
+        if constexpr (!KS) px.u = min(s + 1, last);
+        xload(X[(j + 1) & 1], px);
+        if constexpr (KS) advance(px);
+      }
       f4_t D[NMAT];
       float dq[NMAT];
-      rec_dot<NMAT>(D, dq, R[j], xsrc(s, j), tb, kq);
+      if constexpr (!KS) ps.u = s;
+      rec_dot<NMAT>(D, dq, R[j], xsrc(ps, j), tb, kq);
+      if constexpr (XS && KS) advance(ps);   // (held only past the last record, where it is unused)
       accum(D, dq, s);
       __builtin_amdgcn_sched_barrier(0);
-      rload(R[j], min(s + RING, last));
+      if constexpr (!KS) pr.u = min(s + RING, last);
+      rload(R[j], pr);
+      if constexpr (KS) advance(pr);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -383,9 +475,9 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
       f4_t D[NMAT];
       float dq[NMAT];
       if constexpr (!XS) {
-        if (j > 0) xload(X[j & 1], ut + j);
+        if (j > 0) xload(X[j & 1], pos_at(ut + j));
       }
-      rec_dot<NMAT>(D, dq, R[j], xsrc(ut + j, j), tb, kq);
+      rec_dot<NMAT>(D, dq, R[j], xsrc(pos_at(ut + j), j), tb, kq);
       accum(D, dq, ut + j);
     }
   }
@@ -401,26 +493,64 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
 
   // each tile is finished by the lowest wave of the workgroup that touches it: that wave adds
   // the parts of the waves touching the tile in wave order
-  const int GWb = (int)blockIdx.x * W;
-  const int u0 = range_begin(GWb, GW, a.U), u1 = range_begin(GWb + W, GW, a.U);
+  // a tile's sum is final here without the k-split; with it, it is this range's partial: store it,
+  // count the arrival, and the last of the tile's ks ranges adds them in range order (same
+  // ordering argument as the boundary parts below)
+  auto finish = [&](f4_t* acc, int t) {
+    if constexpr (!KS) {
+      epilogue<NMAT, EPI>(a, acc, t, col, kq);
+      return;
+    }
+    uint64_t* kp = reinterpret_cast<uint64_t*>(a.kpart + (size_t)t * a.ks * NMAT * TLX_WAVE);
+#pragma unroll
+    for (int i = 0; i < NMAT; ++i) {
+      const u4_t v = __builtin_bit_cast(u4_t, acc[i]);
+      uint64_t* q = kp + 2 * ((kr * NMAT + i) * TLX_WAVE + lane);
+      __hip_atomic_store(q, (uint64_t)v.x | (uint64_t)v.y << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(q + 1, (uint64_t)v.z | (uint64_t)v.w << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0x0F70);                    // vmcnt(0): the partial's stores are done
+    uint32_t prev = 0;   // 0 -> 1 -> .. -> ks-1 -> 0: the last arrival leaves the counter at 0
+    if (lane == 0) prev = __builtin_amdgcn_atomic_inc32(&a.kcnt[t], (uint32_t)(a.ks - 1), __ATOMIC_RELAXED, "agent");
+    prev = __shfl(prev, 0);
+    if (prev != (uint32_t)(a.ks - 1)) return;
+    f4_t sum[NMAT];
+#pragma unroll
+    for (int i = 0; i < NMAT; ++i) sum[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < a.ks; ++r)
+#pragma unroll
+      for (int i = 0; i < NMAT; ++i) {
+        const uint64_t* q = kp + 2 * ((r * NMAT + i) * TLX_WAVE + lane);
+        const uint64_t w0 = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t w1 = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sum[i] += __builtin_bit_cast(f4_t, u4_t{(uint32_t)w0, (uint32_t)(w0 >> 32), (uint32_t)w1, (uint32_t)(w1 >> 32)});
+      }
+    epilogue<NMAT, EPI>(a, sum, t, col, kq);
+  };
+
+  const int GWb = bx * W;
+  const int u0 = range_begin(GWb, GW, Ul), u1 = range_begin(GWb + W, GW, Ul);
   for (int k = 0; k < (empty ? 0 : 2); ++k) {
     const int t = k == 0 ? tfirst : tlast;
     if (k == 1 && tlast == tfirst) break;
-    if (k == 0 && wave > 0 && ubeg % nb != 0) continue;   // a lower wave touches it
+    // a lower wave of the workgroup touches it (the one holding record ubeg - 1; waves between
+    // may be empty when the workgroup has fewer records than waves)
+    if (k == 0 && ubeg > u0 && ubeg % nbl != 0) continue;
     f4_t acc[NMAT];
 #pragma unroll
     for (int i = 0; i < NMAT; ++i) acc[i] = f4_t{0.f, 0.f, 0.f, 0.f};
     for (int v = wave; v < W; ++v) {
-      const int vb = range_begin(GWb + v, GW, a.U);
-      if (vb >= (t + 1) * nb) break;
-      if (range_begin(GWb + v + 1, GW, a.U) == vb) continue;   // an empty range
-      const int slot = vb / nb == t ? 0 : 1;
+      const int vb = range_begin(GWb + v, GW, Ul);
+      if (vb >= (t + 1) * nbl) break;
+      if (range_begin(GWb + v + 1, GW, Ul) == vb) continue;   // an empty range
+      const int slot = vb / nbl == t ? 0 : 1;
 #pragma unroll
       for (int i = 0; i < NMAT; ++i) acc[i] += L.part[v][slot][i][lane];
     }
-    const bool lo_out = t * nb < u0, hi_out = (t + 1) * nb > u1;
+    const bool lo_out = t * nbl < u0, hi_out = (t + 1) * nbl > u1;
     if (!lo_out && !hi_out) {
-      epilogue<NMAT, EPI>(a, acc, t, col, kq);
+      finish(acc, t);
       continue;
     }
     // shared with the neighbouring workgroup: boundary g = the upper workgroup's index; part 0
@@ -467,22 +597,33 @@ __global__ __launch_bounds__(W * TLX_WAVE) void iq3s_kernel(const SkArgs a) {
                                                     (uint32_t)w[1][1], (uint32_t)(w[1][1] >> 32)});
       acc[i] = lo + hi;                                    // lower range first: a fixed order
     }
-    epilogue<NMAT, EPI>(a, acc, t, col, kq);
+    finish(acc, t);
   }
+}
+
+// staged row bytes for nbk blocks of k per row
+__host__ __device__ constexpr int xs_row_bytes(int nbk) { return 512 * nbk + 16; }
+
+template <int NMAT, int EPI, int W, bool KS>
+void sk_launch_x(const SkArgs& a, hipStream_t st) {
+  if constexpr (W == kXsWaves) {
+    if (a.M * xs_row_bytes(a.nbk) <= kXsBytes) {   // from x or its tile-ordered copy
+      // all kXsPer pieces per thread needed, or fewer (skip the loads past the end)
+      if (a.M * 32 * a.nbk > (kXsPer - 1) * W * TLX_WAVE) iq3s_kernel<NMAT, EPI, W, 2, KS><<<a.G, W * TLX_WAVE, 0, st>>>(a);
+      else iq3s_kernel<NMAT, EPI, W, 3, KS><<<a.G, W * TLX_WAVE, 0, st>>>(a);
+      return;
+    }
+  }
+  if (a.xt) iq3s_kernel<NMAT, EPI, W, 1, KS><<<a.G, W * TLX_WAVE, 0, st>>>(a);
+  else iq3s_kernel<NMAT, EPI, W, 0, KS><<<a.G, W * TLX_WAVE, 0, st>>>(a);
 }
 
 template <int NMAT, int EPI, int W>
 void sk_launch(const SkArgs& a, hipStream_t st) {
-  if constexpr (W == kXsWaves) {
-    if (!a.xt && a.M * (2 * a.K + 16) <= kXsBytes) {
-      // all kXsPer pieces per thread needed, or fewer (skip the loads past the end)
-      if (a.M * a.K / 8 > (kXsPer - 1) * W * TLX_WAVE) iq3s_kernel<NMAT, EPI, W, 2><<<a.G, W * TLX_WAVE, 0, st>>>(a);
-      else iq3s_kernel<NMAT, EPI, W, 3><<<a.G, W * TLX_WAVE, 0, st>>>(a);
-      return;
-    }
+  if constexpr (NMAT == 1 && W == kXsWaves) {
+    if (a.ks > 1) return sk_launch_x<NMAT, EPI, W, true>(a, st);
   }
-  if (a.xt) iq3s_kernel<NMAT, EPI, W, 1><<<a.G, W * TLX_WAVE, 0, st>>>(a);
-  else iq3s_kernel<NMAT, EPI, W, 0><<<a.G, W * TLX_WAVE, 0, st>>>(a);
+  sk_launch_x<NMAT, EPI, W, false>(a, st);
 }
 
 template <int NMAT, int EPI>
@@ -495,17 +636,38 @@ int sk_dispatch(int W, const SkArgs& a, hipStream_t st) {
   return tlx_launch_status();
 }
 
+constexpr int kWd = 8;   // 2 waves per SIMD, ~130-180 VGPRs each: the record ring and two activation sets
+constexpr int kKs = 4;   // k-ranges of the k-split form
+
+// k-ranges of a launch.  Long-K single matrices (the down and output projections) have few tiles
+// for 256 workgroups and long per-wave record streams; splitting K into kKs ranges, each covered
+// by a quarter of the workgroups over every tile, shortens the streams and the activation slice
+// each workgroup stages.  It needs whole-block ranges, the workspace's range-partial region, and
+// no more tiles than a quarter of the grid keeps within two tiles per wave.  Depends on (N, K,
+// the CU count) only, so a row's summation order is the same for every M.
+int sk_ranges(int nmat, int nseg, int N, int K, bool kparts) {
+  const int G0 = std::min(tlx_cu_count(), kMaxG), gk = G0 / kKs, T = (N + 15) / 16, nb = K / 256;
+  if (!kparts || nmat != 1 || nseg != 1 || K < 5632 || nb % kKs != 0 || gk < 1) return 1;
+  if (T < gk || T > gk * kWd) return 1;
+  if ((size_t)T * 4 > kWsKcntBytes || (size_t)T * kKs * TLX_WAVE * sizeof(f4_t) > kWsKpartBytes) return 1;
+  return kKs;
+}
+
 }  // namespace
 
-// True when the tiled-record GEMV stages x [M][K] in LDS itself (no tile-ordered copy needed).
-bool tlx_iq3s_stages_x(int M, int K) { return M * (2 * K + 16) <= kXsBytes; }
+// True when the tiled-record GEMV stages x [M][K] (each workgroup its k-range) in LDS itself (no
+// tile-ordered copy needed).
+bool tlx_iq3s_stages_x(int nmat, int M, int N, int K, int nseg, bool ws_kparts) {
+  const int ks = sk_ranges(nmat, nseg, N, K, ws_kparts);
+  return M * xs_row_bytes(K / 256 / ks) <= kXsBytes;
+}
 
 // Balanced GEMV over tiled records (called by the IQ3_XXS entry points of tlx_iq3.hip, which
 // have validated the arguments and prepared x / xt).  nmat 2 = SwiGLU pair (one segment), epi as
 // Epi; nseg matrices w[s] of n[s] rows (NMAT == 1, EPI_F16 when nseg > 1) share the activations.
 int tlx_iq3s_launch(int nmat, int epi, int nseg, const void* const* w, const void* w1, void* const* out,
                     const int* n, const float* res, const float* gridf, const _Float16* x, int xt, int M, int K,
-                    void* ws, bool out_tileord, hipStream_t st) {
+                    void* ws, bool ws_kparts, bool out_tileord, hipStream_t st) {
   TLX_RET_IF(ws == nullptr, TLX_E_NOWS);
   TLX_RET_IF(out_tileord && (nseg != 1 || epi == EPI_RESID), TLX_E_ARG);
   static_assert(size_t(kMaxG) * 2 * 2 * TLX_WAVE * sizeof(f4_t) <= kWsCntOff - kWsPartOff, "parts region");
@@ -523,20 +685,34 @@ int tlx_iq3s_launch(int nmat, int epi, int nseg, const void* const* w, const voi
   a.nb = K / 256;
   a.part = reinterpret_cast<f4_t*>(static_cast<uint8_t*>(ws) + kWsPartOff);
   a.cnt = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ws) + kWsCntOff);
+  a.kpart = reinterpret_cast<f4_t*>(static_cast<uint8_t*>(ws) + kWsKpartOff);
+  a.kcnt = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ws) + kWsKcntOff);
   const int nb = a.nb;
   const int G0 = std::min(tlx_cu_count(), kMaxG);
-  constexpr int Wd = 8;   // 2 waves per SIMD, ~130-180 VGPRs each: the record ring and two activation sets
+  constexpr int Wd = kWd;
   const int Tmax = G0 * Wd;   // a launch covers at most G0 * Wd tiles, so a wave touches <= 2 tiles
+  const int ks = sk_ranges(nmat, nseg, n[0], K, ws_kparts);
 
   auto run = [&](SkArgs& b, int T) {
     b.U = T * nb;
-    // every wave gets >= 1 record; G <= T makes a workgroup cover >= nb records, so a tile
-    // spans at most two workgroups
     int W = Wd;
-    int G = std::min(G0, T);
-    if (b.U < G * W) G = std::max(1, b.U / W);
-    while (W > 1 && b.U < G * W) W = W > 4 ? W / 2 : 1;
-    b.G = G;
+    if (ks > 1) {
+      // kKs groups of G0 / kKs workgroups, group r over k-range r of every tile (gk <= T: a tile
+      // spans at most two workgroups of its group; T <= gk * Wd: a wave touches <= 2 tiles)
+      b.ks = ks;
+      b.nbk = nb / ks;
+      b.gk = G0 / ks;
+      b.G = b.gk * ks;
+    } else {
+      // every wave gets >= 1 record; G <= T makes a workgroup cover >= nb records, so a tile
+      // spans at most two workgroups
+      int G = std::min(G0, T);
+      if (b.U < G * W) G = std::max(1, b.U / W);
+      while (W > 1 && b.U < G * W) W = W > 4 ? W / 2 : 1;
+      b.ks = 1;
+      b.nbk = nb;
+      b.gk = b.G = G;
+    }
     if (nmat == 2) return sk_dispatch<2, EPI_SWIGLU>(W, b, st);
     if (epi == EPI_RESID) return sk_dispatch<1, EPI_RESID>(W, b, st);
     return sk_dispatch<1, EPI_F16>(W, b, st);
