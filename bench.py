@@ -307,19 +307,26 @@ def formats_leg(ops, synth, torch, dev, steps, warmup):
 
 def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
     """Config 5: the MoE layer at M=11 (HBM-bound) and M=2048 (MFMA-bound)."""
+    from thunderllamax_amd._lib import LAYOUT_RAW, LAYOUT_TILED
     rng = synth.config_rng(5)
     E, H, F = 256, 2048, 512
-    copies = []
+    copies = {LAYOUT_RAW: [], LAYOUT_TILED: []}   # GGUF rows, and the same slabs repacked as tiled records
+
+    def tables(dgu, ddn):
+        return dict(keep=(dgu, ddn), ptbl=formats.pointer_table(dgu[:E], dev),
+                    ptbl_dn=formats.pointer_table(ddn[:E], dev), ptbl_sh=formats.pointer_table([dgu[E], ddn[E]], dev))
+
     for _ in range(3):
         gu, dn = synth.moe_expert_slabs(rng, E + 1)
         dgu = [torch.from_numpy(a).to(dev) for a in gu]
         ddn = [torch.from_numpy(a).to(dev) for a in dn]
-        copies.append(dict(keep=(dgu, ddn), ptbl=formats.pointer_table(dgu[:E], dev),
-                           ptbl_dn=formats.pointer_table(ddn[:E], dev),
-                           ptbl_sh=formats.pointer_table([dgu[E], ddn[E]], dev)))
+        copies[LAYOUT_RAW].append(tables(dgu, ddn))
+        copies[LAYOUT_TILED].append(tables([ops.pack_iq4_tiled(a, torch.empty_like(a), 2 * F, H) for a in dgu],
+                                           [ops.pack_iq4_tiled(a, torch.empty_like(a), H, F) for a in ddn]))
     iq4nl = formats.iq4nl_tensor(dev)
     out = {"workload": "MoE layer, 256 IQ4_XS experts + 1 shared, hidden 2048, FF 512, top-8; hidden states "
-                       "bf16(0.05 * N(0,1)) (N(0,1) overflows the fp16 parts for these weight statistics)"}
+                       "bf16(0.05 * N(0,1)) (N(0,1) overflows the fp16 parts for these weight statistics); "
+                       "expert slabs as tiled records (tlx_pack_iq4_tiled, the GGUF bytes permuted into lane order)"}
     for P in (11, 2048):
         np_ = 8 * P
         x = torch.from_numpy(synth.bf16_round(0.05 * rng.standard_normal((P, H)).astype(np.float32))).to(dev)
@@ -330,13 +337,14 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
         y = torch.empty(P, H, device=dev)
         state = {"i": 0}
 
-        def layer(st, overlap):
-            c = copies[state["i"] % len(copies)]
+        def layer(st, overlap, layout=LAYOUT_TILED):
+            c = copies[layout][state["i"] % 3]
             state["i"] += 1
             ops.moe_layer(logits, sg, x, hres, y, c["ptbl"], c["ptbl_dn"], c["ptbl_sh"], iq4nl, sc, stream=st,
-                          overlap_shared=overlap)
+                          overlap_shared=overlap, layout=layout)
 
         t_seq = time_graph(lambda st: layer(st, False), steps, warmup, torch)
+        t_raw = time_graph(lambda st: layer(st, True, LAYOUT_RAW), steps, warmup, torch)
         t = time_graph(lambda st: layer(st, True), steps, warmup, torch)
         hit = int((torch.diff(sc.eoff) > 0).sum().item())
         flops = 2.0 * 3 * F * H * (8 * P + P)
@@ -345,7 +353,7 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
         gbs = wbytes / (t * 1e-3) / 1e9
         out[f"M{P}"] = {"ms": round(t, 4), "tflops": round(tflops, 2),
                         "experts_hit": hit, "weight_gbs": round(gbs, 1),
-                        "ms_shared_not_overlapped": round(t_seq, 4),
+                        "ms_shared_not_overlapped": round(t_seq, 4), "ms_gguf_row_slabs": round(t_raw, 4),
                         "roofline": (hbm_roofline(gbs, "MoE layer (7 launches, graph): expert weight bytes / layer time")
                                      if P <= 64 else
                                      mfma_roofline(tflops, "MoE layer (7 launches, graph): 2*3*512*2048*9*M / layer time"))}

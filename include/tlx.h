@@ -300,7 +300,18 @@ uint64_t tlx_iq3_tiled_bytes(int N, int K);
  * top-8; IQ4_XS weights).  Pairs are position-major, rank ascending: pair = 8*pos + rank.
  * Expert e's gate/up slab at ptbl[e] (512 gate rows, then 512 up rows 557,056 B later; 1088 B
  * a row), its down slab at ptbl_dn[e] (2048 rows x 272 B).  ptbl / ptbl_dn are device arrays
- * of 256 device addresses. */
+ * of 256 device addresses.  layout (the expert GEMMs' trailing argument): TLX_LAYOUT_RAW for
+ * slabs of GGUF rows as above, TLX_LAYOUT_TILED for slabs repacked by tlx_pack_iq4_tiled (same
+ * size, same results bit for bit; faster: every wave load is one contiguous run). */
+
+/* GGUF IQ4_XS rows u8[N][K/256*136] -> tiled records u8[N/16][K/256][2176] (N % 16 == 0,
+ * K % 256 == 0; 8-B aligned buffers): per (16-row tile, 256-k block) the 16 rows' block headers
+ * (8 B each, row order), then their quant bytes in MFMA lane order -- lane l = 16 kq + r holds row
+ * r's bytes 16 kq .. 16 kq + 15, then (a second 1024 B) its bytes 64 + 16 kq .. .  A pure byte
+ * permutation; an expert slab keeps its size and its up rows their offset.  No reference
+ * counterpart: the reference reads GGUF rows (engine/mm/MM_P2_gx8e256up4.cu:23-39); this is the
+ * load-time repack for the grouped GEMMs' layout argument. */
+int tlx_pack_iq4_tiled(const void* src, void* tiled, int N, int K, void* stream);
 
 /* Top-8 + renormalized softmax from router logits f32[P][256] (the router epilogue of
  * engine/mm/MM_P1_rt8e256.cu:41-60: strict >, ties to the lower id).  eids u16[P][8],
@@ -314,7 +325,8 @@ int tlx_moe_route(const float* wrt, const float* wsh, const float* h, uint16_t* 
 
 /* Deterministic stable sort of the np = 8P pairs by expert: eoff i32[257] (exclusive bin
  * offsets), plist u16[np] (pair ids, pair order inside a bin), items u32[tlx_moe_max_items(np)]
- * (expert << 16 | first pair in bin, one per 64 pairs), nitp u32[1] (item count).  np <= 16384.
+ * (expert << 16 | first pair in bin, one per 64 pairs for np <= 2048 and per 96 pairs above: the
+ * grouped GEMMs' forms), nitp u32[1] (item count).  np <= 16384.
  * Replaces mmsort8 (engine/mm/MM_B_mmsort8.cu:22-31): mmsort8(eids, eoff, plist, items, nitp, np);
  * eoff / plist are the reference's, the item granularity is this library's own. */
 int tlx_moe_sort(const uint16_t* eids, int* eoff, uint16_t* plist, uint32_t* items, uint32_t* nitp,
@@ -327,7 +339,8 @@ int tlx_moe_max_items(int np);
  * ones tlx_moe_sort wrote.  The fp16-MMA prefill form gxu_gm (engine/mm/MM_E_gxu_gm.cu:86-93) is
  * the same call: np > 2048 runs the MFMA grouped GEMM. */
 int tlx_moe_up4(const uint64_t* ptbl, const uint32_t* items, const uint32_t* nitp, const int* eoff,
-                const uint16_t* plist, const float* xs, const float* iq4nl, float* ys, int np, void* stream);
+                const uint16_t* plist, const float* xs, const float* iq4nl, float* ys, int np, int layout,
+                void* stream);
 
 /* Grouped down over the sorted pairs: parts[pair][2048] = fp16(Wd_e . act[pair]).
  * Replaces gxm_dn / gxm_dnf (engine/mm/MM_B_gxm_dn.cu:15-23, engine/mm/MM_C_gxm_dnf.cu:22):
@@ -335,25 +348,25 @@ int tlx_moe_up4(const uint64_t* ptbl, const uint32_t* items, const uint32_t* nit
  * np > 2048 runs the MFMA form (gxd_gm, engine/mm/MM_E_gxd_gm.cu:91-97). */
 int tlx_moe_dn4(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
                 const uint16_t* plist, const float* act, const float* iq4nl, uint16_t* parts, int np,
-                void* stream);
+                int layout, void* stream);
 
 /* Pair-walk decode form of tlx_moe_up4 (no sort): pair p runs expert eids[p] on x[p >> 3].
  * Replaces gx8e256up4 (engine/mm/MM_P2_gx8e256up4.cu:8-14): gx8e256up4(ptbl, eids, xs, iq4nlb, ys)
  * launched over NPAIR = np blocks.  Bit-identical to tlx_moe_up4 on the same pairs. */
 int tlx_moe_up4_pairs(const uint64_t* ptbl, const uint16_t* eids, const float* xs, const float* iq4nl,
-                      float* ys, int np, void* stream);
+                      float* ys, int np, int layout, void* stream);
 
 /* Pair-walk decode form of tlx_moe_dn4: pair p runs expert eids[p] on act[p].
  * Replaces gx8e256dn (engine/mm/MM_P2_gx8e256dn.cu:8-14): gx8e256dn(ptbl, eids, xs, iq4nlb, parts).
  * Bit-identical to tlx_moe_dn4 on the same pairs. */
 int tlx_moe_dn4_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, const float* iq4nl,
-                      uint16_t* parts, int np, void* stream);
+                      uint16_t* parts, int np, int layout, void* stream);
 
 /* Shared expert over all P positions: act[P][512] (caller scratch) then out[P][2048] f32.
  * ptbl_sh = {gate/up slab, down slab}.  Replaces shgu32 / shdn32 (engine/mm/MM_P2_ports.py:195-201
  * restates them) with the IQ4_XS weights of the benchmark's MoE configuration. */
 int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const float* iq4nl, float* act, float* out,
-                   int P, void* stream);
+                   int P, int layout, void* stream);
 
 /* y = hres + (sum_r gates[r] * parts[pos][r] + sg * shared), f32[P][2048].
  * Replaces cmbz2048 (engine/mm/MM_P34_cmbz2048.cu:6-13): cmbz2048(parts, gates, sg, shared, hres, y). */

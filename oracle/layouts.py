@@ -9,6 +9,11 @@
   with the per-chunk table indices precomputed.  Pinned by the inverse (which also checks the
   one redundant bit, the sign parity), by a hand-decoded block, and, on the GPU, by the GEMVs
   over the records against the dequantized rows.
+* ``pack_iq4_tiled`` / ``unpack_iq4_tiled`` -- this library's tiled IQ4_XS expert slabs for the
+  MoE GEMMs (no reference counterpart): a byte permutation of GGUF IQ4_XS rows
+  (/root/reference/engine/mm/MM_P0_d2_repack.py:78-93 gives the block: d, scales_h, scales_l,
+  qs) into MFMA lane order.  Pinned by the inverse, by hand-placed bytes, and, on the GPU, by
+  the GEMMs over tiled slabs equal to those over the GGUF rows bit for bit.
 """
 import numpy as np
 
@@ -181,3 +186,30 @@ def unpack_tiled(rec, kdim, n):
                           sw.astype("<u4").view(np.uint8).reshape(16 * t, 32 * nb),
                           np.ascontiguousarray(d).reshape(16 * t, 2 * nb)], axis=1)
     return out[:n]
+
+
+def pack_iq4_tiled(raw_rows, kdim):
+    """GGUF IQ4_XS rows u8[N, 136*NB] (N % 16 == 0) -> tiled records u8[N/16, NB, 2176].
+
+    Record (tile t, block b): ``[row r's 8-B header (d, scales_h, scales_l), r = 0..15]`` then two
+    1024-B lane regions; lane ``l = 16*kq + r`` of region h holds row ``16t + r``'s quant bytes
+    ``qs[64h + 16kq .. 64h + 16kq + 15]`` (sub-block ``4h + kq``; ``qs`` = block bytes 8..135).
+    """
+    x = np.ascontiguousarray(raw_rows, dtype=np.uint8)
+    n, nb = len(x), kdim // 256
+    assert n % 16 == 0 and x.shape[1] == 136 * nb
+    blk = x.reshape(n // 16, 16, nb, 136).transpose(0, 2, 1, 3)                     # [t, b, r, 136]
+    hdr = blk[..., :8].reshape(n // 16, nb, 128)
+    lanes = blk[..., 8:].reshape(n // 16, nb, 16, 2, 4, 16).transpose(0, 1, 3, 4, 2, 5)   # [t, b, h, kq, r, 16]
+    return np.ascontiguousarray(np.concatenate([hdr, lanes.reshape(n // 16, nb, 2048)], axis=2))
+
+
+def unpack_iq4_tiled(rec, kdim):
+    """Inverse of :func:`pack_iq4_tiled` -> GGUF IQ4_XS rows u8[16*T, 136*NB]."""
+    nb = kdim // 256
+    r = np.ascontiguousarray(rec, dtype=np.uint8).reshape(-1, nb, 2176)
+    t = len(r)
+    hdr = r[:, :, :128].reshape(t, nb, 16, 8)
+    qs = r[:, :, 128:].reshape(t, nb, 2, 4, 16, 16).transpose(0, 1, 4, 2, 3, 5).reshape(t, nb, 16, 128)
+    blk = np.concatenate([hdr, qs], axis=3).transpose(0, 2, 1, 3)                   # [t, r, b, 136]
+    return np.ascontiguousarray(blk.reshape(16 * t, 136 * nb))

@@ -11,9 +11,9 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import gemv, moe
+from oracle import gemv, layouts, moe
 from thunderllamax_amd import formats, ops, synth
-from thunderllamax_amd._lib import TlxError
+from thunderllamax_amd._lib import LAYOUT_RAW, LAYOUT_TILED, TlxError
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -34,11 +34,34 @@ def experts(gpu):
     }
 
 
+@pytest.fixture(scope="module")
+def experts_tiled(gpu, experts):
+    """The same experts as tiled slabs (tlx_pack_iq4_tiled on the GPU); two slabs of each kind
+    checked byte for byte against the oracle's restatement."""
+    def tile(slabs, n, k):
+        return [ops.pack_iq4_tiled(s, torch.empty_like(s), n, k) for s in slabs]
+    tgu = tile(experts["dgu"], 2 * moe.FF, moe.HID)
+    tdn = tile(experts["ddn"], moe.HID, moe.FF)
+    torch.cuda.synchronize()
+    for e in (0, moe.E):
+        assert np.array_equal(tgu[e].cpu().numpy(),
+                              layouts.pack_iq4_tiled(experts["gu"][e].reshape(2 * moe.FF, -1), moe.HID).ravel())
+        assert np.array_equal(tdn[e].cpu().numpy(),
+                              layouts.pack_iq4_tiled(experts["dn"][e].reshape(moe.HID, -1), moe.FF).ravel())
+    return {
+        "dgu": tgu, "ddn": tdn,
+        "ptbl": formats.pointer_table(tgu[:moe.E], gpu),
+        "ptbl_dn": formats.pointer_table(tdn[:moe.E], gpu),
+        "ptbl_sh": formats.pointer_table([tgu[moe.E], tdn[moe.E]], gpu),
+        "iq4nl": experts["iq4nl"],
+    }
+
+
 def _rows_err(y, ref):
     return max(gemv.rel_err(y[i], ref[i]) for i in range(ref.shape[0]))
 
 
-def _run_layer(gpu, ex, x, logits, sg, hres):
+def _run_layer(gpu, ex, x, logits, sg, hres, layout=LAYOUT_RAW):
     P = x.shape[0]
     np_ = 8 * P
     dx = torch.from_numpy(x).to(gpu)
@@ -51,12 +74,12 @@ def _run_layer(gpu, ex, x, logits, sg, hres):
     nitp = torch.empty(1, dtype=torch.int32, device=gpu)
     ops.moe_sort(eids, eoff, plist, items, nitp)
     act = torch.empty(np_, moe.FF, dtype=torch.float32, device=gpu)
-    ops.moe_up4(ex["ptbl"], items, nitp, eoff, plist, dx, ex["iq4nl"], act)
+    ops.moe_up4(ex["ptbl"], items, nitp, eoff, plist, dx, ex["iq4nl"], act, layout=layout)
     parts = torch.empty(np_, moe.HID, dtype=torch.float16, device=gpu)
-    ops.moe_dn4(ex["ptbl_dn"], items, nitp, eoff, plist, act, ex["iq4nl"], parts)
+    ops.moe_dn4(ex["ptbl_dn"], items, nitp, eoff, plist, act, ex["iq4nl"], parts, layout=layout)
     sact = torch.empty(P, moe.FF, dtype=torch.float32, device=gpu)
     shared = torch.empty(P, moe.HID, dtype=torch.float32, device=gpu)
-    ops.moe_shared(ex["ptbl_sh"], dx, ex["iq4nl"], sact, shared)
+    ops.moe_shared(ex["ptbl_sh"], dx, ex["iq4nl"], sact, shared, layout=layout)
     y = torch.empty(P, moe.HID, dtype=torch.float32, device=gpu)
     ops.moe_combine(parts, gates, torch.from_numpy(sg).to(gpu), shared, torch.from_numpy(hres).to(gpu), y)
     torch.cuda.synchronize()
@@ -134,7 +157,8 @@ def test_moe_sort(gpu, P):
     assert np.array_equal(eoff.cpu().numpy(), ref_off)
     assert np.array_equal(plist.cpu().numpy().view(np.uint16), ref_pl)
     cnt = np.diff(ref_off)
-    want = [(e << 16) | k for e in range(moe.E) for k in range(0, int(cnt[e]), 64)]
+    tok = 64 if np_ <= 2048 else 96   # pairs per item: the GEMV form's 64, the GEMM form's 96
+    want = [(e << 16) | k for e in range(moe.E) for k in range(0, int(cnt[e]), tok)]
     n = int(nitp.cpu().numpy()[0])
     assert n == len(want)
     assert np.array_equal(items.cpu().numpy().view(np.uint32)[:n], np.array(want, dtype=np.uint32))
@@ -189,8 +213,9 @@ def test_moe_layer_prefill_m2048_sampled(gpu, experts):
 
 @pytest.mark.parametrize("P", [64, 256, 300])
 def test_moe_layer_skewed(gpu, experts, P):
-    """A router biased towards 12 experts gives them 2..4 groups of 16 tokens and several 64-pair
-    items each (ragged last ones).  Pair counts up to 2048 (P = 64, 256) take the GEMV form, more
+    """A router biased towards 12 experts gives them 2..4 groups of 16 tokens and several items
+    each (64 pairs in the GEMV form, 96 in the GEMM form; ragged last ones).  Pair counts up to
+    2048 (P = 64, 256) take the GEMV form, more
     (P = 300) the prefill GEMM, whose shared expert then ends on a 44-position chunk."""
     print(f"[case] moe layer skewed P={P}", flush=True)
     rng = np.random.default_rng(24 + P)
@@ -287,3 +312,31 @@ def test_moe_layer_overlapped_equals_sequential(gpu, experts):
             g.replay()
             torch.cuda.synchronize()
             assert np.array_equal(y.cpu().numpy(), ref["y"])
+
+
+@pytest.mark.parametrize("P", [11, 300, 2048])
+def test_moe_tiled_slabs_equal_gguf_rows(gpu, experts, experts_tiled, P):
+    """Tiled expert slabs give the GGUF rows' router-to-combine results bit for bit: GEMV form
+    (P = 11), GEMM form with ragged items (P = 300, a biased router) and config 5's M = 2048;
+    at P = 11 also the pair-walk forms.  (The GGUF-row results are checked against the oracle by
+    the tests above.)"""
+    print(f"[case] moe tiled slabs P={P}", flush=True)
+    rng = np.random.default_rng(50 + P)
+    x, logits, sg, hres = _inputs(rng, P)
+    if P == 300:
+        logits[:, :12] += 3.0
+    a = _run_layer(gpu, experts, x, logits, sg, hres)
+    b = _run_layer(gpu, experts_tiled, x, logits, sg, hres, layout=LAYOUT_TILED)
+    for k in ("act", "parts", "shared", "y"):
+        assert np.array_equal(a[k], b[k]), k
+    if P == 11:
+        np_ = 8 * P
+        eids = torch.from_numpy(a["eids"].reshape(-1)).to(gpu)
+        act = torch.empty(np_, moe.FF, dtype=torch.float32, device=gpu)
+        ops.moe_up4_pairs(experts_tiled["ptbl"], eids, torch.from_numpy(x).to(gpu), experts["iq4nl"], act,
+                          layout=LAYOUT_TILED)
+        parts = torch.empty(np_, moe.HID, dtype=torch.float16, device=gpu)
+        ops.moe_dn4_pairs(experts_tiled["ptbl_dn"], eids, act, experts["iq4nl"], parts, layout=LAYOUT_TILED)
+        torch.cuda.synchronize()
+        assert np.array_equal(act.cpu().numpy(), a["act"])
+        assert np.array_equal(parts.cpu().numpy(), a["parts"])

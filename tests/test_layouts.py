@@ -87,3 +87,25 @@ def test_bf16_to_f16_activation_rule():
     assert synth.bf16_round(x)[2] == np.float32(1.0078125)
     f = synth.activations_f16(np.random.default_rng(0), 4, 256)
     assert f.dtype == np.float16 and np.all(np.isfinite(f))
+
+
+@pytest.mark.parametrize("rows,kdim", [(16, 256), (32, 512), (48, 2048)])
+def test_iq4_tiled_slab_inverts(rows, kdim):
+    raw = synth.iq4xs_raw(np.random.default_rng(rows + kdim), rows, kdim)
+    rec = layouts.pack_iq4_tiled(raw, kdim)
+    assert rec.shape == (rows // 16, kdim // 256, 2176)
+    assert np.array_equal(layouts.unpack_iq4_tiled(rec, kdim), raw)
+
+
+def test_iq4_tiled_slab_places_bytes_by_hand():
+    """Bytes placed by the record rules written out: header of row r at 8r, quant byte j of
+    sub-block ib of row r at 128 + 1024 (ib // 4) + 16 (16 (ib % 4) + r) + j."""
+    kdim = 512
+    raw = synth.iq4xs_raw(np.random.default_rng(3), 32, kdim)
+    rec = layouts.pack_iq4_tiled(raw, kdim)
+    for t, b, r in [(0, 0, 0), (0, 1, 5), (1, 0, 15), (1, 1, 9)]:
+        row = raw[16 * t + r, 136 * b:136 * (b + 1)]
+        assert np.array_equal(rec[t, b, 8 * r:8 * r + 8], row[:8])
+        for ib in range(8):
+            o = 128 + 1024 * (ib // 4) + 16 * (16 * (ib % 4) + r)
+            assert np.array_equal(rec[t, b, o:o + 16], row[8 + 16 * ib:8 + 16 * ib + 16])

@@ -75,11 +75,12 @@ SIGNATURES = {
     "tlx_moe_route": [_p, _p, _p, _p, _p, _p, _i, _p],
     "tlx_moe_sort": [_p, _p, _p, _p, _p, _i, _p],
     "tlx_moe_max_items": [_i],
-    "tlx_moe_up4": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _p],
-    "tlx_moe_dn4": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _p],
-    "tlx_moe_up4_pairs": [_p, _p, _p, _p, _p, _i, _p],
-    "tlx_moe_dn4_pairs": [_p, _p, _p, _p, _p, _i, _p],
-    "tlx_moe_shared": [_p, _p, _p, _p, _p, _i, _p],
+    "tlx_moe_up4": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _p],
+    "tlx_moe_dn4": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _p],
+    "tlx_moe_up4_pairs": [_p, _p, _p, _p, _p, _i, _i, _p],
+    "tlx_moe_dn4_pairs": [_p, _p, _p, _p, _p, _i, _i, _p],
+    "tlx_moe_shared": [_p, _p, _p, _p, _p, _i, _i, _p],
+    "tlx_pack_iq4_tiled": [_p, _p, _i, _i, _p],
     "tlx_moe_combine": [_p, _p, _p, _p, _p, _p, _i, _p],
     "tlx_stream_chunk_bytes": [],
     "tlx_stream_read": [_p, ctypes.c_uint64, _p, _p],

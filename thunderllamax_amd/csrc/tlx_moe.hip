@@ -6,6 +6,14 @@
 // 512 up rows (GATE_B4 = 557,056 bytes apart), 1088 B per row (8 IQ4_XS blocks of 136 B,
 // k = 2048); its down slab at ptbl_dn[e] -- 2048 rows x 272 B (k = 512).  Pairs are
 // position-major, rank ascending: pair = 8 * pos + rank.
+// Tiled slabs (TLX_LAYOUT_TILED, this library's own; tlx_pack_iq4_tiled): the same bytes per
+// (16-row tile t, 256-k block b) record of 2176 B, records in (t, b) order (so a slab keeps its
+// size and the up rows still start GATE_B4 bytes in):
+//   [0, 128)      row r's block header (d, scales_h, scales_l) at 8 r
+//   [128, 1152)   lane l = 16 kq + r: row r's quant bytes 16 kq .. 16 kq + 15 (sub-block kq)
+//   [1152, 2176)  lane l: row r's quant bytes 64 + 16 kq .. (sub-block kq + 4)
+// i.e. the bytes each MFMA lane decodes, in lane order: every wave load reads one contiguous run
+// (in GGUF rows the 4 lanes of a 64-B load request touch 4 rows).
 //
 // Grouped GEMMs: a GEMV form for small batches and a GEMM form for prefill (see each kernel).
 // IQ4_XS decode: a 256-entry table maps a quant byte to (kv[lo], kv[hi]) as fp16, so one lookup
@@ -125,10 +133,17 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
 // one scan over (expert, wave) gives every wave its start in each bin -- bins are expert
 // ascending, inside a bin the waves in order, inside a wave the steps and lanes in order, i.e. pair
 // order (stable, as mmsort8); pass 2 repeats the steps and scatters.  Items: per expert
-// ceil(count / 64) chunks of its pairs, expert ascending, item = expert << 16 | first pair offset.
+// ceil(count / tok) chunks of its pairs, expert ascending, item = expert << 16 | first pair offset,
+// tok = moe_item_tok(np).
 constexpr int kMaxPairs = 16384;
-constexpr int kTok = 64;
+constexpr int kTok = 64;         // item size of the GEMV form, and the dense (shared expert) chunk
+constexpr int kPfTok = 96;       // item size of the GEMM form: up to 6 groups of 16 tokens
+constexpr int kGvMaxPairs = 2048;   // pair counts up to this use the GEMV form, larger ones the GEMM
 constexpr int kSortWaves = 16;
+
+// pairs per work item: the GEMV form takes up to 64, the GEMM form 96 (at uniform routing over 256
+// experts an expert's count exceeds 96 with odds of ~1e-4, so its weights are streamed once)
+__host__ __device__ constexpr int moe_item_tok(int np) { return np <= kGvMaxPairs ? kTok : kPfTok; }
 
 // lanes of this wave holding the same 8-bit key as this lane
 __device__ __forceinline__ uint64_t same_key_mask(uint32_t key) {
@@ -148,6 +163,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const uint16_t* __restri
   __shared__ int wtot[kE / 64][2];      // per-wave totals of the expert scans
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint64_t below = (1ull << lane) - 1ull;
+  const int tok = moe_item_tok(np);
   const int span = ((np + kSortWaves - 1) / kSortWaves + 63) & ~63;
   const int i0 = min(np, wave * span), i1 = min(np, i0 + span);
   for (int e = lane; e < kE; e += 64) cnt[wave][e] = 0;   // the wave's own row (in-order LDS)
@@ -182,7 +198,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const uint16_t* __restri
   if (t < kE) {
 #pragma unroll
     for (int w = 0; w < kSortWaves; ++w) c += cnt[w][t];
-    ni = (c + kTok - 1) / kTok;
+    ni = (c + tok - 1) / tok;
     sc = c;
     si = ni;
 #pragma unroll
@@ -197,7 +213,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const uint16_t* __restri
     int bc = sc - c, bi = si - ni;
     for (int w = 0; w < wave; ++w) { bc += wtot[w][0]; bi += wtot[w][1]; }
     eoff[t] = bc;
-    for (int j = 0; j < ni; ++j) items[bi + j] = ((uint32_t)t << 16) | (uint32_t)(kTok * j);
+    for (int j = 0; j < ni; ++j) items[bi + j] = ((uint32_t)t << 16) | (uint32_t)(tok * j);
     if (t == kE - 1) {
       eoff[kE] = bc + c;
       *nitp = (uint32_t)(bi + ni);
@@ -236,21 +252,25 @@ __device__ __forceinline__ h8_t splat8h(_Float16 v) { return h8_t{v, v, v, v, v,
 using gbyte = const __attribute__((address_space(1))) uint8_t;
 
 // ------------------------------------------------------------------ grouped IQ4_XS GEMM (prefill)
-// Work unit: one 64-pair item (expert, chunk of its sorted pairs) x one stripe of weight rows
-// (FFN: 256 gate rows + the matching 256 up rows; down: 512 rows).  8 waves, two per SIMD; wave
-// w owns four 16-row tiles (FFN: gate tiles 2w, 2w + 1 of the stripe and the two matching up
-// tiles; down: tiles 4w..4w+3) over the whole K, so no reduction across waves.
-//   * weights go straight from HBM to registers (a block ahead) and are decoded there: lane
-//     (col, kq) holds row col's sub-blocks kq, kq + 4 of each block (32 quant bytes + the 8-byte
-//     header); each quant byte is looked up in a byte -> (kv[lo], kv[hi]) fp16 table kept once
-//     per lane (64 copies, copy l in bank l), so the wave's 64 lookups never collide in a bank;
-//   * activations: per 256-k block the item's token rows are loaded (a block ahead, through the
+// Work unit: one item (up to 96 of an expert's sorted pairs: at uniform routing all of them, so
+// the expert's weights are streamed once) x one stripe of weight rows (FFN: 256 gate rows + the
+// matching 256 up rows; down: 512 rows).  8 waves, two per SIMD; wave w owns four 16-row tiles
+// (FFN: gate tiles 2w, 2w + 1 of the stripe and the two matching up tiles; down: tiles 4w..4w+3)
+// over the whole K, so no reduction across waves.  K runs in stages of 128 (half an IQ4_XS
+// block): in stage h = 2 kb + sb, lane (col, kq) of a wave holds row col's sub-block 4 sb + kq of
+// block kb, i.e. 16 quant bytes and the block header.
+//   * weights go straight from memory to registers, RING - 1 stages ahead (buffer loads: the
+//     stage offset is a scalar, the lane's row offset a fixed register), and are decoded there:
+//     each quant byte is looked up in a byte -> (kv[lo], kv[hi]) fp16 table kept once per lane
+//     (64 copies, copy l in bank l), so the wave's 64 lookups never collide in a bank;
+//   * activations: per stage the item's token rows are loaded (a stage ahead, rows through the
 //     sorted pair list), converted to fp16 once, and stored in LDS already in the MFMA k order
-//     (the 8 halves of piece p = 4 ib + c are x[32 ib + 4c + {0, 16, 1, 17, 2, 18, 3, 19}], the
-//     order the byte table pairs the weights in) with piece p of token row t at slot p ^ (t & 15):
-//     the 16 lanes of a fragment read hit 16 distinct 16-B slots;
-//   * per block: issue the next block's activation and weight loads, 8 x (NG groups x 4 tiles)
-//     MFMAs on this block, then store the next block's activations and one barrier;
+//     (the 8 halves of piece p = 4 kq + c are x[k0 + 32 kq + 4c + {0, 16, 1, 17, 2, 18, 3, 19}],
+//     the order the byte table pairs the weights in) with piece p of token row t at slot
+//     p ^ (t & 15): the 16 lanes of a fragment read hit 16 distinct 16-B slots;
+//   * per stage: issue the next stage's activation loads and the weight loads RING - 1 stages
+//     ahead, 4 x (NG groups x 4 tiles) MFMAs on this stage, then store the next stage's
+//     activations and one barrier;
 //   * blockIdx -> (item, stripe) keeps the stripes of an item on one XCD (workgroups are
 //     dispatched round-robin over the 8 XCDs), so its activations are read from that L2.
 constexpr int kPfTiles = 4;   // 16-row tiles per wave
@@ -259,9 +279,9 @@ constexpr int kPfThreads = kPfWaves * TLX_WAVE;
 
 struct __attribute__((aligned(16))) MoePfLds {
   uint32_t lut[256 * TLX_WAVE];   // [quant byte][lane]: (kv[lo], kv[hi]) fp16
-  u4_t a[2][kTok * 32];           // 256-k blocks of the item's activations, fp16, [row][swizzled piece]
-  int xrow[kTok];                 // activation row of token slot t
-  int orow[kTok];                 // output row of token slot t
+  u4_t a[2][kPfTok * 16];         // 128-k stages of the item's activations, fp16, [row][swizzled piece]
+  int xrow[kPfTok];               // activation row of token slot t
+  int orow[kPfTok];               // output row of token slot t
 };
 
 template <int KIND>
@@ -269,63 +289,88 @@ constexpr int moe_pf_stripes() {
   return (KIND == MOE_UP || KIND == MOE_UP_DENSE) ? kFf / (16 * 2 * kPfWaves) : kHid / (16 * kPfTiles * kPfWaves);
 }
 
-// token rows 16g..16g+15 of block kb: thread t loads piece p = t & 31 of row 16g + (t >> 5) --
-// x[row][256 kb + 32 ib + 4c .. + 3] and [.. + 16 .. + 19] with ib = p >> 2, c = p & 3
-template <int K>
-__device__ __forceinline__ void moe_pf_load_a(float4 (&v)[2], const MoePfLds& L, const float* __restrict__ xs, int kb,
-                                              int g, int t) {
-  const int row = 16 * g + (t >> 5), p = t & 31;
-  const float* src = xs + (size_t)L.xrow[row] * K + 256 * kb + 32 * (p >> 2) + 4 * (p & 3);
-  v[0] = *reinterpret_cast<const float4*>(src);
-  v[1] = *reinterpret_cast<const float4*>(src + 16);
+// buffer resource over n bytes at p (raw dword-granular buffer; no format conversion)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t moe_rsrc(const void* p, uint32_t n) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)n, 0x00020000);
 }
 
-__device__ __forceinline__ void moe_pf_store_a(u4_t* buf, const float4 (&v)[2], int g, int t) {
-  const int row = 16 * g + (t >> 5), p = t & 31;
-  const h8_t h = {(_Float16)v[0].x, (_Float16)v[1].x, (_Float16)v[0].y, (_Float16)v[1].y,
-                  (_Float16)v[0].z, (_Float16)v[1].z, (_Float16)v[0].w, (_Float16)v[1].w};
-  buf[row * 32 + (p ^ (row & 15))] = __builtin_bit_cast(u4_t, h);
-}
+// weight registers of one stage: per tile the lane's 16 quant bytes and its row's block header
+struct MoeWs {
+  u4_t q[kPfTiles];
+  u2_t h[kPfTiles];
+};
 
-template <int KIND, int NG>
-__device__ __forceinline__ void moe_pf_tile(MoePfLds& L, gbyte* base, const float* __restrict__ xs,
+template <int KIND, int NG, bool TL>
+__device__ __forceinline__ void moe_pf_tile(MoePfLds& L, const void* base, const float* __restrict__ xs,
                                             const float* __restrict__ iq4nl, void* __restrict__ out, int ntok,
                                             int stripe, int wave, int lane) {
   using S = MoeShape<KIND>;
   constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
   constexpr int kNb = S::K / 256;
+  constexpr int kH = 2 * kNb;                       // 128-k stages
   constexpr int kRowBytes = kNb * 136;
+  constexpr uint32_t kSlab = kUp ? 2u * kGateBytes : (uint32_t)kHid * kRowBytes;
+  // weight ring depth (stages RING - 1 ahead) as the accumulators leave room: deeper rings at
+  // more groups spill
+  constexpr int RING = NG <= 2 ? 4 : 2;
+  constexpr int NI = (NG + 1) / 2;                  // activation pieces (x 2 float4) per thread
   const int col = lane & 15, kq = lane >> 4, t = threadIdx.x;
   // the wave's tiles: FFN gate tiles 2 * (kPfWaves * stripe + wave) + {0, 1}, then the same up
   // tiles; down tiles 4 * (kPfWaves * stripe + wave) + {0..3}
   const int tb = kPfWaves * stripe + wave;
-  gbyte* wrow[kPfTiles];
+  const __amdgpu_buffer_rsrc_t rw = moe_rsrc(base, kSlab);
+  // tile j's first byte in the slab (wave-uniform): GGUF rows and tiled records alike
+  int ts[kPfTiles];
 #pragma unroll
   for (int j = 0; j < kPfTiles; ++j) {
     if constexpr (kUp)
-      wrow[j] = base + (j >= 2 ? kGateBytes : 0) + (size_t)(16 * (2 * tb + (j & 1)) + col) * kRowBytes;
+      ts[j] = (j >= 2 ? kGateBytes : 0) + 16 * (2 * tb + (j & 1)) * kRowBytes;
     else
-      wrow[j] = base + (size_t)(16 * (4 * tb + j) + col) * kRowBytes;
+      ts[j] = 16 * (4 * tb + j) * kRowBytes;
   }
-  u2_t hdr[2][kPfTiles];
-  u4_t qv[2][kPfTiles][2];
-  auto load_w = [&](int kb, int set) {
+  // stage h's weights (block kb = h / 2, sub-block 4 (h & 1) + kq of row col): GGUF rows -- the
+  // header at row col's 136 kb, the quant bytes at + 8 + 64 (h & 1) + 16 kq; tiled -- the
+  // header at record (tile, kb) + 8 col, the quant bytes at + 128 + 1024 (h & 1) + 16 lane
+  const int vh = TL ? 8 * col : col * kRowBytes;
+  const int vq = TL ? 128 + 16 * lane : col * kRowBytes + 8 + 16 * kq;
+  auto load_w = [&](MoeWs& w, int h) {
+    const int so = TL ? 2176 * (h >> 1) : 136 * (h >> 1);
+    const int sq = so + (TL ? 1024 : 64) * (h & 1);
 #pragma unroll
     for (int j = 0; j < kPfTiles; ++j) {
-      gbyte* blk = wrow[j] + 136 * kb;
-      hdr[set][j] = *(const __attribute__((address_space(1))) u2_t*)(blk);
-      qv[set][j][0] = *(const __attribute__((address_space(1))) u4_t*)(blk + 8 + 16 * kq);
-      qv[set][j][1] = *(const __attribute__((address_space(1))) u4_t*)(blk + 72 + 16 * kq);
+      w.h[j] = __builtin_bit_cast(u2_t, __builtin_amdgcn_raw_buffer_load_b64(rw, vh, ts[j] + so, 0));
+      w.q[j] = __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, vq, ts[j] + sq, 0));
     }
   };
-  float4 xa[NG][2];   // the next block's activations, in flight during this block's MFMAs
-  auto load_a = [&](int kb) {
+  // activations: thread t, piece i covers row min(32 i + (t >> 4), 16 NG - 1), piece p = t & 15
+  // (a row past the item's groups repeats the last one: stored twice with the same bytes)
+  const __amdgpu_buffer_rsrc_t rx = moe_rsrc(xs, 0x7FFFFFFFu);
+  const int p = t & 15;
+  int xo[NI], ao[NI];   // the piece's source byte offset at k0 = 0, and its LDS slot
 #pragma unroll
-    for (int g = 0; g < NG; ++g) moe_pf_load_a<S::K>(xa[g], L, xs, kb, g, t);
+  for (int i = 0; i < NI; ++i) {
+    const int row = min(32 * i + (t >> 4), 16 * NG - 1);
+    xo[i] = 4 * (32 * (p >> 2) + 4 * (p & 3));   // + the row's offset once xrow is visible
+    ao[i] = row * 16 + (p ^ (row & 15));
+  }
+  // activations two stages ahead, in two register sets: stage h's are stored into LDS at the end
+  // of stage h - 1
+  float4 xa[2][NI][2];
+  auto load_a = [&](int set, int h) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      xa[set][i][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo[i], 512 * h, 0));
+      xa[set][i][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo[i] + 64, 512 * h, 0));
+    }
   };
-  auto store_a = [&](u4_t* buf) {
+  auto store_a = [&](int set, u4_t* buf) {
 #pragma unroll
-    for (int g = 0; g < NG; ++g) moe_pf_store_a(buf, xa[g], g, t);
+    for (int i = 0; i < NI; ++i) {
+      const float4 v0 = xa[set][i][0], v1 = xa[set][i][1];
+      const h8_t hv = {(_Float16)v0.x, (_Float16)v1.x, (_Float16)v0.y, (_Float16)v1.y,
+                       (_Float16)v0.z, (_Float16)v1.z, (_Float16)v0.w, (_Float16)v1.w};
+      buf[ao[i]] = __builtin_bit_cast(u4_t, hv);
+    }
   };
 
   f4_t acc[NG][kPfTiles];
@@ -343,47 +388,53 @@ __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, gbyte* base, const floa
     return *reinterpret_cast<const uint32_t*>(lut0 + off);
   };
 
-  // block kb reads activation buffer / weight register set kb & 1 (= set)
-  auto block = [&](int kb, int set) {
-    if (kb + 1 < kNb) load_a(kb + 1);
-    load_w(min(kb + 1, kNb - 1), set ^ 1);   // clamped on the last block
-    const u4_t* arow = L.a[set] + 32 * col;   // + 512 * g: token row 16g + col (slot p ^ col)
+  MoeWs W[RING];
+  // Stage h: weights from W[h % RING], activations from LDS buffer h & 1.  Loads are unconditional
+  // and clamped at the end (a load under a branch makes the wait counts assume the worst; the
+  // repeats past the end reload the last stage).  The memory counter completes in issue order, so
+  // the order of the stage's two requests keeps either wait from draining the other's prefetch:
+  // with RING > 2 the activations go first (the wait for stage h + 1's activations at the end of
+  // stage h then covers only weights up to stage h + 1), with RING == 2 the weights (the wait for
+  // stage h + 1's weights then covers only activations up to stage h + 1).
+  auto stage = [&](int h, MoeWs& w, MoeWs& wnext) {
+    if constexpr (RING > 2) load_a(h & 1, min(h + 2, kH - 1));
+    load_w(wnext, min(h + RING - 1, kH - 1));
+    if constexpr (RING == 2) load_a(h & 1, min(h + 2, kH - 1));
+    const u4_t* arow = L.a[h & 1] + 16 * col;   // + 256 * g: token row 16g + col (slot p ^ col)
+    const int ib = 4 * (h & 1) + kq;             // the lane's sub-block of block h / 2
+    _Float16 dh[kPfTiles];
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      const int ib = kq + 4 * sb;
-      _Float16 dh[kPfTiles];
+    for (int j = 0; j < kPfTiles; ++j) {
+      const uint32_t sh = w.h[j].x >> 16;
+      const uint32_t ls = ((w.h[j].y >> (4 * ib)) & 0xFu) | (((sh >> (2 * ib)) & 3u) << 4);
+      dh[j] = (_Float16)(tlx_h2f((uint16_t)w.h[j].x) * (float)((int)ls - 32));
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      h8_t B[kPfTiles];
 #pragma unroll
       for (int j = 0; j < kPfTiles; ++j) {
-        const uint32_t sh = hdr[set][j].x >> 16;
-        const uint32_t ls = ((hdr[set][j].y >> (4 * ib)) & 0xFu) | (((sh >> (2 * ib)) & 3u) << 4);
-        dh[j] = (_Float16)(tlx_h2f((uint16_t)hdr[set][j].x) * (float)((int)ls - 32));
+        const uint32_t qw = w.q[j][c];
+        const u4_t w4 = {lut(qw, 0), lut(qw, 1), lut(qw, 2), lut(qw, 3)};
+        B[j] = __builtin_bit_cast(h8_t, w4) * splat8h(dh[j]);
       }
+      const int pc = 4 * kq + c;   // 16-B piece: k0 = 128 h + 32 kq + 4c (and + 16)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        h8_t B[kPfTiles];
+      for (int g = 0; g < NG; ++g) {
+        const h8_t A = __builtin_bit_cast(h8_t, arow[256 * g + (pc ^ col)]);
 #pragma unroll
-        for (int j = 0; j < kPfTiles; ++j) {
-          const uint32_t qw = qv[set][j][sb][c];
-          // byte i of qw times 256: the row of the byte table
-          const u4_t w4 = {lut(qw, 0), lut(qw, 1), lut(qw, 2), lut(qw, 3)};
-          B[j] = __builtin_bit_cast(h8_t, w4) * splat8h(dh[j]);
-        }
-        const int pc = 4 * ib + c;   // 16-B piece: k0 = 32 ib + 4c (and + 16)
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          const h8_t A = __builtin_bit_cast(h8_t, arow[512 * g + (pc ^ col)]);
-#pragma unroll
-          for (int j = 0; j < kPfTiles; ++j)
-            acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], acc[g][j], 0, 0, 0);
-        }
+        for (int j = 0; j < kPfTiles; ++j)
+          acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], acc[g][j], 0, 0, 0);
       }
     }
-    if (kb + 1 < kNb) store_a(L.a[set ^ 1]);   // (waits for its loads) block kb - 1's buffer is free
+    // (waits for its loads; stage h - 1's buffer is free: every wave passed the last barrier)
+    store_a((h + 1) & 1, L.a[(h + 1) & 1]);
     __syncthreads();
   };
 
-  // block 0's weights first: the byte table is built while they are in flight
-  load_w(0, 0);
+  // the first stages' weights first: the byte table is built while they are in flight
+#pragma unroll
+  for (int r = 0; r < RING - 1; ++r) load_w(W[r], min(r, kH - 1));
   {   // the byte table, one copy per lane: entry b of copy l at [b][l]; wave w writes the entries
       // b = w + 8i, whose two table values are wave-uniform (scalar loads)
 #pragma unroll
@@ -395,13 +446,22 @@ __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, gbyte* base, const floa
     }
   }
   __syncthreads();   // xrow / orow (written by the kernel before the tile) are visible
-  load_a(0);
-  store_a(L.a[0]);
-  __syncthreads();   // block 0's activations and the byte table are visible
-  for (int kb = 0; kb < kNb; kb += 2) {
-    block(kb, 0);
-    block(kb + 1, 1);
+#pragma unroll
+  for (int i = 0; i < NI; ++i) xo[i] += L.xrow[min(32 * i + (t >> 4), 16 * NG - 1)] * (S::K * 4);
+  load_a(0, 0);
+  load_a(1, 1);
+  store_a(0, L.a[0]);
+  __syncthreads();   // stage 0's activations and the byte table are visible
+  // stages in rounds of U (a multiple of the ring depth and of the two activation sets), then the
+  // rest; stage h uses ring entry h % RING, a compile-time index in both loops
+  constexpr int U = RING % 2 ? 2 * RING : RING;
+  int h0 = 0;
+  for (; h0 + U <= kH; h0 += U) {
+#pragma unroll
+    for (int r = 0; r < U; ++r) stage(h0 + r, W[r % RING], W[(r + RING - 1) % RING]);
   }
+#pragma unroll
+  for (int r = 0; r < kH % U; ++r) stage(h0 + r, W[r % RING], W[(r + RING - 1) % RING]);
   __builtin_amdgcn_s_waitcnt(0x0F70);   // the clamped tail loads
 
   // lane (col, kq) holds tokens 16g + 4kq + r of row 16 * tile + col
@@ -433,7 +493,7 @@ __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, gbyte* base, const floa
   }
 }
 
-template <int KIND>
+template <int KIND, bool TL>
 __global__ __launch_bounds__(kPfThreads, 1) void moe_pf_kernel(
     const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff, const uint16_t* __restrict__ plist,
     const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp, const float* __restrict__ xs,
@@ -448,23 +508,23 @@ __global__ __launch_bounds__(kPfThreads, 1) void moe_pf_kernel(
   const int stripe = l % kS, item = (l / kS) * 8 + (id & 7);
 
   int m0, ntok;
-  gbyte* base;
-  if constexpr (kDense) {
+  const void* base;
+  if constexpr (kDense) {   // the shared expert: chunks of kTok positions
     m0 = item * kTok;
     if (m0 >= P) return;
     ntok = min(kTok, P - m0);
-    base = (gbyte*)(ptbl[0]);
+    base = (const void*)(ptbl[0]);
   } else {
     if (item >= (int)*nitp) return;
     const uint32_t it = items[item];
     const int e = (int)(it >> 16);
     m0 = (int)(it & 0xFFFFu);
     const int eb0 = eoff[e];
-    ntok = min(kTok, eoff[e + 1] - eb0 - m0);
+    ntok = min(kPfTok, eoff[e + 1] - eb0 - m0);
     m0 += eb0;
-    base = (gbyte*)(ptbl[e]);
+    base = (const void*)(ptbl[e]);
   }
-  if (t < kTok) {
+  if (t < kPfTok) {
     const int slot = min(t, ntok - 1);   // padded slots repeat the last pair; never stored
     if constexpr (kDense) {
       L.xrow[t] = m0 + slot;
@@ -475,11 +535,14 @@ __global__ __launch_bounds__(kPfThreads, 1) void moe_pf_kernel(
       L.orow[t] = pair;
     }
   }
-  switch ((ntok + 15) >> 4) {   // workgroup-uniform (the tile's first barrier publishes xrow / orow)
-    case 1: moe_pf_tile<KIND, 1>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
-    case 2: moe_pf_tile<KIND, 2>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
-    case 3: moe_pf_tile<KIND, 3>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
-    default: moe_pf_tile<KIND, 4>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
+  // workgroup-uniform (the tile's first barrier publishes xrow / orow); dense chunks have <= 64
+  switch ((ntok + 15) >> 4) {
+    case 1: moe_pf_tile<KIND, 1, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
+    case 2: moe_pf_tile<KIND, 2, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
+    case 3: moe_pf_tile<KIND, 3, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
+    case 4: moe_pf_tile<KIND, 4, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
+    case 5: if constexpr (!kDense) moe_pf_tile<KIND, 5, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
+    default: if constexpr (!kDense) moe_pf_tile<KIND, 6, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
   }
 }
 
@@ -508,7 +571,7 @@ constexpr int moe_gv_wpt() { return (KIND == MOE_UP || KIND == MOE_UP_DENSE) ? 2
 // argument so that every activation load is unconditional: the compiler can then issue them
 // ahead of their MFMAs instead of waiting on each one in turn.  red: the workgroup's
 // [4 waves][kGvGroups][NMAT][64 lanes] reduction buffer.
-template <int KIND, int NG>
+template <int KIND, int NG, bool TL>
 __device__ __forceinline__ void moe_gv_tile(gbyte* base, const uint32_t* lut, const int* xrow, const int* orow,
                                             f4_t* red, const float* __restrict__ xs, void* __restrict__ out,
                                             int ntok, int tile, int wave, int lane) {
@@ -532,10 +595,17 @@ __device__ __forceinline__ void moe_gv_tile(gbyte* base, const uint32_t* lut, co
   for (int bb = 0; bb < kBpw; ++bb)
 #pragma unroll
     for (int mi = 0; mi < NMAT; ++mi) {
-      gbyte* blk = wrow[mi] + 136 * (kb0 + bb);
-      hdr[bb][mi] = *(const __attribute__((address_space(1))) u2_t*)(blk);
-      qv[bb][mi][0] = *(const __attribute__((address_space(1))) u4_t*)(blk + 8 + 16 * kq);
-      qv[bb][mi][1] = *(const __attribute__((address_space(1))) u4_t*)(blk + 72 + 16 * kq);
+      if constexpr (TL) {   // record (tile, block): header at 8 col, quant bytes in lane order
+        gbyte* rec = wrow[mi] - (size_t)col * kRowBytes + 2176 * (kb0 + bb);
+        hdr[bb][mi] = *(const __attribute__((address_space(1))) u2_t*)(rec + 8 * col);
+        qv[bb][mi][0] = *(const __attribute__((address_space(1))) u4_t*)(rec + 128 + 16 * lane);
+        qv[bb][mi][1] = *(const __attribute__((address_space(1))) u4_t*)(rec + 1152 + 16 * lane);
+      } else {
+        gbyte* blk = wrow[mi] + 136 * (kb0 + bb);
+        hdr[bb][mi] = *(const __attribute__((address_space(1))) u2_t*)(blk);
+        qv[bb][mi][0] = *(const __attribute__((address_space(1))) u4_t*)(blk + 8 + 16 * kq);
+        qv[bb][mi][1] = *(const __attribute__((address_space(1))) u4_t*)(blk + 72 + 16 * kq);
+      }
     }
   const float* xr[NG];   // lane's activation row in group g, at its first k of a block
 #pragma unroll
@@ -622,7 +692,7 @@ __device__ __forceinline__ void moe_gv_tile(gbyte* base, const uint32_t* lut, co
   }
 }
 
-template <int KIND>
+template <int KIND, bool TL>
 __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff,
                                                      const uint16_t* __restrict__ plist,
                                                      const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp,
@@ -678,10 +748,10 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
   __syncthreads();
   const int tile = (int)blockIdx.y * kTpw + wave / moe_gv_wpt<KIND>();   // 16-row output tile
   switch ((ntok + 15) >> 4) {   // workgroup-uniform
-    case 1: moe_gv_tile<KIND, 1>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
-    case 2: moe_gv_tile<KIND, 2>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
-    case 3: moe_gv_tile<KIND, 3>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
-    default: moe_gv_tile<KIND, 4>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
+    case 1: moe_gv_tile<KIND, 1, TL>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
+    case 2: moe_gv_tile<KIND, 2, TL>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
+    case 3: moe_gv_tile<KIND, 3, TL>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
+    default: moe_gv_tile<KIND, 4, TL>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
   }
 }
 
@@ -709,7 +779,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   for (int k = 0; k < 8; ++k) yo[k] = hr[k] + __builtin_fmaf(sgp, sh[k], acc[k]);
 }
 
-int moe_max_items(int np) { return (np + kTok - 1) / kTok + kE; }
+int moe_max_items(int np) { return (np + moe_item_tok(np) - 1) / moe_item_tok(np) + kE; }
 
 }  // namespace
 
@@ -736,9 +806,6 @@ extern "C" int tlx_moe_sort(const uint16_t* eids, int* eoff, uint16_t* plist, ui
 
 extern "C" int tlx_moe_max_items(int np) { return moe_max_items(np); }
 
-// pair counts up to this use the GEMV form (a few tokens per expert); larger ones the GEMM
-constexpr int kGvMaxPairs = 2048;
-
 // work items the sort can produce for np pairs: at most ceil(np / 64) + 256 (one partial
 // chunk per expert), and at most np (every item holds a pair) -- the small-batch grids use both
 int moe_gv_items(int np) { return min(np, moe_max_items(np)); }
@@ -754,73 +821,130 @@ dim3 moe_gv_grid(int nx) {
   return dim3(nx, kRows / 16 / kTpw);
 }
 
+// launch helpers: the layout picks the kernel instantiation (GGUF rows or tiled records)
+template <int KIND>
+void moe_gv_launch(bool tl, dim3 grid, hipStream_t st, const uint64_t* ptbl, const int* eoff, const uint16_t* plist,
+                   const uint32_t* items, const uint32_t* nitp, const uint16_t* eids, const float* xs,
+                   const float* iq4nl, void* out, int P) {
+  if (tl)
+    moe_gv_kernel<KIND, true><<<grid, 256, 0, st>>>(ptbl, eoff, plist, items, nitp, eids, xs, iq4nl, out, P);
+  else
+    moe_gv_kernel<KIND, false><<<grid, 256, 0, st>>>(ptbl, eoff, plist, items, nitp, eids, xs, iq4nl, out, P);
+}
+
+template <int KIND>
+void moe_pf_launch(bool tl, int nitems, hipStream_t st, const uint64_t* ptbl, const int* eoff, const uint16_t* plist,
+                   const uint32_t* items, const uint32_t* nitp, const float* xs, const float* iq4nl, void* out, int P) {
+  const int grid = moe_pf_grid<KIND>(nitems);
+  if (tl)
+    moe_pf_kernel<KIND, true><<<grid, kPfThreads, 0, st>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, out, P);
+  else
+    moe_pf_kernel<KIND, false><<<grid, kPfThreads, 0, st>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, out, P);
+}
+
+bool moe_layout_ok(int layout) { return layout == TLX_LAYOUT_RAW || layout == TLX_LAYOUT_TILED; }
+
 extern "C" int tlx_moe_up4(const uint64_t* ptbl, const uint32_t* items, const uint32_t* nitp, const int* eoff,
-                           const uint16_t* plist, const float* xs, const float* iq4nl, float* ys, int np, void* stream) {
-  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+                           const uint16_t* plist, const float* xs, const float* iq4nl, float* ys, int np, int layout,
+                           void* stream) {
+  TLX_RET_IF(np < 1 || np > kMaxPairs || !moe_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(xs, 16), TLX_E_ALIGN);
-  if (np <= kGvMaxPairs) {
-    moe_gv_kernel<MOE_UP><<<moe_gv_grid<MOE_UP>(moe_gv_items(np)), 256, 0, (hipStream_t)stream>>>(
-        ptbl, eoff, plist, items, nitp, nullptr, xs, iq4nl, ys, 0);
-    return tlx_launch_status();
-  }
-  moe_pf_kernel<MOE_UP><<<moe_pf_grid<MOE_UP>(moe_max_items(np)), kPfThreads, 0, (hipStream_t)stream>>>(
-      ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, 0);
+  const bool tl = layout == TLX_LAYOUT_TILED;
+  const hipStream_t st = (hipStream_t)stream;
+  if (np <= kGvMaxPairs)
+    moe_gv_launch<MOE_UP>(tl, moe_gv_grid<MOE_UP>(moe_gv_items(np)), st, ptbl, eoff, plist, items, nitp, nullptr, xs,
+                          iq4nl, ys, 0);
+  else
+    moe_pf_launch<MOE_UP>(tl, moe_max_items(np), st, ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, 0);
   return tlx_launch_status();
 }
 
 extern "C" int tlx_moe_dn4(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
                            const uint16_t* plist, const float* act, const float* iq4nl, uint16_t* parts, int np,
-                           void* stream) {
-  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+                           int layout, void* stream) {
+  TLX_RET_IF(np < 1 || np > kMaxPairs || !moe_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(act, 16) || !tlx_aligned(parts, 16), TLX_E_ALIGN);
-  if (np <= kGvMaxPairs) {
-    moe_gv_kernel<MOE_DN><<<moe_gv_grid<MOE_DN>(moe_gv_items(np)), 256, 0, (hipStream_t)stream>>>(
-        ptbl_dn, eoff, plist, items, nitp, nullptr, act, iq4nl, parts, 0);
-    return tlx_launch_status();
-  }
-  moe_pf_kernel<MOE_DN><<<moe_pf_grid<MOE_DN>(moe_max_items(np)), kPfThreads, 0, (hipStream_t)stream>>>(
-      ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
+  const bool tl = layout == TLX_LAYOUT_TILED;
+  const hipStream_t st = (hipStream_t)stream;
+  if (np <= kGvMaxPairs)
+    moe_gv_launch<MOE_DN>(tl, moe_gv_grid<MOE_DN>(moe_gv_items(np)), st, ptbl_dn, eoff, plist, items, nitp, nullptr,
+                          act, iq4nl, parts, 0);
+  else
+    moe_pf_launch<MOE_DN>(tl, moe_max_items(np), st, ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
   return tlx_launch_status();
 }
 
 extern "C" int tlx_moe_up4_pairs(const uint64_t* ptbl, const uint16_t* eids, const float* xs, const float* iq4nl,
-                                 float* ys, int np, void* stream) {
-  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+                                 float* ys, int np, int layout, void* stream) {
+  TLX_RET_IF(np < 1 || np > kMaxPairs || !moe_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(xs, 16), TLX_E_ALIGN);
-  moe_gv_kernel<MOE_UP><<<moe_gv_grid<MOE_UP>(np), 256, 0, (hipStream_t)stream>>>(
-      ptbl, nullptr, nullptr, nullptr, nullptr, eids, xs, iq4nl, ys, 0);
+  moe_gv_launch<MOE_UP>(layout == TLX_LAYOUT_TILED, moe_gv_grid<MOE_UP>(np), (hipStream_t)stream, ptbl, nullptr,
+                        nullptr, nullptr, nullptr, eids, xs, iq4nl, ys, 0);
   return tlx_launch_status();
 }
 
 extern "C" int tlx_moe_dn4_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, const float* iq4nl,
-                                 uint16_t* parts, int np, void* stream) {
-  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+                                 uint16_t* parts, int np, int layout, void* stream) {
+  TLX_RET_IF(np < 1 || np > kMaxPairs || !moe_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(act, 16) || !tlx_aligned(parts, 16), TLX_E_ALIGN);
-  moe_gv_kernel<MOE_DN><<<moe_gv_grid<MOE_DN>(np), 256, 0, (hipStream_t)stream>>>(
-      ptbl_dn, nullptr, nullptr, nullptr, nullptr, eids, act, iq4nl, parts, 0);
+  moe_gv_launch<MOE_DN>(layout == TLX_LAYOUT_TILED, moe_gv_grid<MOE_DN>(np), (hipStream_t)stream, ptbl_dn, nullptr,
+                        nullptr, nullptr, nullptr, eids, act, iq4nl, parts, 0);
   return tlx_launch_status();
 }
 
 extern "C" int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const float* iq4nl, float* act, float* out,
-                              int P, void* stream) {
-  TLX_RET_IF(P < 1, TLX_E_ARG);
+                              int P, int layout, void* stream) {
+  TLX_RET_IF(P < 1 || !moe_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(xs, 16) || !tlx_aligned(act, 16), TLX_E_ALIGN);
+  const bool tl = layout == TLX_LAYOUT_TILED;
+  const hipStream_t st = (hipStream_t)stream;
   const int chunks = (P + kTok - 1) / kTok;
   if (8 * P <= kGvMaxPairs) {
-    moe_gv_kernel<MOE_UP_DENSE><<<moe_gv_grid<MOE_UP_DENSE>(chunks), 256, 0, (hipStream_t)stream>>>(
-        ptbl_sh, nullptr, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, act, P);
+    moe_gv_launch<MOE_UP_DENSE>(tl, moe_gv_grid<MOE_UP_DENSE>(chunks), st, ptbl_sh, nullptr, nullptr, nullptr, nullptr,
+                                nullptr, xs, iq4nl, act, P);
     int rc = tlx_launch_status();
     TLX_RET_IF(rc != TLX_OK, rc);
-    moe_gv_kernel<MOE_DN_DENSE><<<moe_gv_grid<MOE_DN_DENSE>(chunks), 256, 0, (hipStream_t)stream>>>(
-        ptbl_sh + 1, nullptr, nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
+    moe_gv_launch<MOE_DN_DENSE>(tl, moe_gv_grid<MOE_DN_DENSE>(chunks), st, ptbl_sh + 1, nullptr, nullptr, nullptr,
+                                nullptr, nullptr, act, iq4nl, out, P);
     return tlx_launch_status();
   }
-  moe_pf_kernel<MOE_UP_DENSE><<<moe_pf_grid<MOE_UP_DENSE>(chunks), kPfThreads, 0, (hipStream_t)stream>>>(
-      ptbl_sh, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, act, P);
+  moe_pf_launch<MOE_UP_DENSE>(tl, chunks, st, ptbl_sh, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, act, P);
   int rc = tlx_launch_status();
   TLX_RET_IF(rc != TLX_OK, rc);
-  moe_pf_kernel<MOE_DN_DENSE><<<moe_pf_grid<MOE_DN_DENSE>(chunks), kPfThreads, 0, (hipStream_t)stream>>>(
-      ptbl_sh + 1, nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
+  moe_pf_launch<MOE_DN_DENSE>(tl, chunks, st, ptbl_sh + 1, nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
+  return tlx_launch_status();
+}
+
+// ------------------------------------------------------------------ tiled slab repacker
+// One thread per 8 output bytes: record u = (tile, block) word w -- w < 16: row 16 tile + w's
+// block header; else lane region (w - 16) / 128 (sub-blocks kq, then kq + 4), lane l, half q:
+// row 16 tile + (l & 15)'s quant bytes 64 region + 16 (l >> 4) + 8 q.  All reads are 8-B aligned
+// (block starts are multiples of 8 bytes).
+__global__ __launch_bounds__(256) void pack_iq4_tiled_kernel(const uint8_t* __restrict__ src,
+                                                             uint8_t* __restrict__ dst, long nwords, int nb) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nwords) return;
+  const long u = i / 272;
+  const int w = (int)(i - u * 272);
+  const long tile = u / nb;
+  const int b = (int)(u - tile * nb);
+  const long rb = 136L * nb;
+  long off;
+  if (w < 16) {
+    off = (tile * 16 + w) * rb + 136L * b;
+  } else {
+    const int o = 8 * (w - 16), reg = o >> 10, l = (o & 1023) >> 4, q = (o >> 3) & 1;
+    off = (tile * 16 + (l & 15)) * rb + 136L * b + 8 + 64 * reg + 16 * (l >> 4) + 8 * q;
+  }
+  reinterpret_cast<u2_t*>(dst)[i] = *reinterpret_cast<const u2_t*>(src + off);
+}
+
+extern "C" int tlx_pack_iq4_tiled(const void* src, void* tiled, int N, int K, void* stream) {
+  TLX_RET_IF(N < 16 || (N % 16) || K < 256 || (K % 256), TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(src, 8) || !tlx_aligned(tiled, 8), TLX_E_ALIGN);
+  const long nwords = (long)(N / 16) * (K / 256) * 272;
+  pack_iq4_tiled_kernel<<<(unsigned)((nwords + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      (const uint8_t*)src, (uint8_t*)tiled, nwords, K / 256);
   return tlx_launch_status();
 }
 

@@ -457,6 +457,17 @@ def pack_iq3_tiled(src, tiled, N, K, src_layout=LAYOUT_PACKED, stream=None):
     return tiled
 
 
+def pack_iq4_tiled(src, tiled, N, K, stream=None):
+    """IQ4_XS GGUF rows u8[N][K/256*136] -> the tiled records the MoE expert GEMMs read with
+    ``layout=LAYOUT_TILED`` (same size: a byte permutation per 16-row tile and 256-k block)."""
+    nbytes = N * (K // 256) * 136
+    _need(src, nbytes, "src")
+    _need(tiled, nbytes, "tiled")
+    _dev(src, tiled)
+    call("tlx_pack_iq4_tiled", src.data_ptr(), tiled.data_ptr(), N, K, _stream(stream))
+    return tiled
+
+
 def p8_quant(x16, xq, sx, rs, stream=None):
     """Per (row, 128-k chunk) int8 quantization of fp16 activations (pfk_q8: kernel(x, xq, sx, rs))."""
     M, K = x16.shape
@@ -555,9 +566,10 @@ def moe_sort(eids, eoff, plist, items, nitp, stream=None):
          eids.numel(), _stream(stream))
 
 
-def moe_up4(ptbl, items, nitp, eoff, plist, xs, iq4nl, ys, stream=None):
+def moe_up4(ptbl, items, nitp, eoff, plist, xs, iq4nl, ys, stream=None, layout=LAYOUT_RAW):
     """gxm_up4(ptbl, items, nitp, eoff, plist, xs, iq4nlb, ys) over the sorted pairs:
-    ys[pair][512] = silu(Wg_e . x[pos]) * (Wu_e . x[pos]), pos = pair >> 3."""
+    ys[pair][512] = silu(Wg_e . x[pos]) * (Wu_e . x[pos]), pos = pair >> 3.  layout: the slabs'
+    (LAYOUT_RAW GGUF rows, LAYOUT_TILED records from ``pack_iq4_tiled``)."""
     n = ys.shape[0]
     _need(ptbl, 256 * 8, "ptbl")
     _need(eoff, 257 * 4, "eoff")
@@ -568,10 +580,10 @@ def moe_up4(ptbl, items, nitp, eoff, plist, xs, iq4nl, ys, stream=None):
     _need(iq4nl, 64, "iq4nl")
     _dev(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys)
     call("tlx_moe_up4", ptbl.data_ptr(), items.data_ptr(), nitp.data_ptr(), eoff.data_ptr(), plist.data_ptr(),
-         xs.data_ptr(), iq4nl.data_ptr(), ys.data_ptr(), ys.shape[0], _stream(stream))
+         xs.data_ptr(), iq4nl.data_ptr(), ys.data_ptr(), ys.shape[0], layout, _stream(stream))
 
 
-def moe_dn4(ptbl_dn, items, nitp, eoff, plist, act, iq4nl, parts, stream=None):
+def moe_dn4(ptbl_dn, items, nitp, eoff, plist, act, iq4nl, parts, stream=None, layout=LAYOUT_RAW):
     """gxm_dn(ptbl, items, nitp, eoff, plist, act, iq4nlb, parts) over the sorted pairs:
     parts[pair][2048] = fp16(Wd_e . act[pair])."""
     n = act.shape[0]
@@ -584,10 +596,10 @@ def moe_dn4(ptbl_dn, items, nitp, eoff, plist, act, iq4nl, parts, stream=None):
     _need(iq4nl, 64, "iq4nl")
     _dev(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts)
     call("tlx_moe_dn4", ptbl_dn.data_ptr(), items.data_ptr(), nitp.data_ptr(), eoff.data_ptr(), plist.data_ptr(),
-         act.data_ptr(), iq4nl.data_ptr(), parts.data_ptr(), act.shape[0], _stream(stream))
+         act.data_ptr(), iq4nl.data_ptr(), parts.data_ptr(), act.shape[0], layout, _stream(stream))
 
 
-def moe_up4_pairs(ptbl, eids, xs, iq4nl, ys, stream=None):
+def moe_up4_pairs(ptbl, eids, xs, iq4nl, ys, stream=None, layout=LAYOUT_RAW):
     """gx8e256up4(ptbl, eids, xs, iq4nlb, ys): pair p runs expert eids[p] on x[p >> 3], no sort."""
     n = ys.shape[0]
     _need(ptbl, 256 * 8, "ptbl")
@@ -597,10 +609,10 @@ def moe_up4_pairs(ptbl, eids, xs, iq4nl, ys, stream=None):
     _need(iq4nl, 64, "iq4nl")
     _dev(ptbl, eids, xs, iq4nl, ys)
     call("tlx_moe_up4_pairs", ptbl.data_ptr(), eids.data_ptr(), xs.data_ptr(), iq4nl.data_ptr(), ys.data_ptr(),
-         n, _stream(stream))
+         n, layout, _stream(stream))
 
 
-def moe_dn4_pairs(ptbl_dn, eids, act, iq4nl, parts, stream=None):
+def moe_dn4_pairs(ptbl_dn, eids, act, iq4nl, parts, stream=None, layout=LAYOUT_RAW):
     """gx8e256dn(ptbl, eids, act, iq4nlb, parts): pair p runs expert eids[p] on act[p], no sort."""
     n = act.shape[0]
     _need(ptbl_dn, 256 * 8, "ptbl_dn")
@@ -610,10 +622,10 @@ def moe_dn4_pairs(ptbl_dn, eids, act, iq4nl, parts, stream=None):
     _need(iq4nl, 64, "iq4nl")
     _dev(ptbl_dn, eids, act, iq4nl, parts)
     call("tlx_moe_dn4_pairs", ptbl_dn.data_ptr(), eids.data_ptr(), act.data_ptr(), iq4nl.data_ptr(),
-         parts.data_ptr(), n, _stream(stream))
+         parts.data_ptr(), n, layout, _stream(stream))
 
 
-def moe_shared(ptbl_sh, xs, iq4nl, act, out, stream=None):
+def moe_shared(ptbl_sh, xs, iq4nl, act, out, stream=None, layout=LAYOUT_RAW):
     """Shared expert over all positions: act [P][512] (scratch), out [P][2048] f32."""
     P = xs.shape[0]
     _need(ptbl_sh, 2 * 8, "ptbl_sh")
@@ -623,7 +635,7 @@ def moe_shared(ptbl_sh, xs, iq4nl, act, out, stream=None):
     _need(iq4nl, 64, "iq4nl")
     _dev(ptbl_sh, xs, iq4nl, act, out)
     call("tlx_moe_shared", ptbl_sh.data_ptr(), xs.data_ptr(), iq4nl.data_ptr(), act.data_ptr(), out.data_ptr(),
-         xs.shape[0], _stream(stream))
+         xs.shape[0], layout, _stream(stream))
 
 
 def moe_combine(parts, gates, sg, shared, hres, y, stream=None):
@@ -661,12 +673,14 @@ class MoeScratch:
 _SIDE_STREAMS = {}
 
 
-def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, stream=None, overlap_shared=True):
+def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, stream=None, overlap_shared=True,
+              layout=LAYOUT_RAW):
     """One MoE layer, the sequence of build_seq7 (engine/mm/MM_P7_lib.py:449-511): top-8 from
     the router logits, sort, grouped gate+up, grouped down, shared expert, combine into y.
     With overlap_shared the shared expert (which needs neither the routing nor the routed
     experts) runs on a second stream, joined before the combine; the work and the results are
-    the same, and a graph captured from the call keeps the two branches concurrent."""
+    the same, and a graph captured from the call keeps the two branches concurrent.  layout: the
+    expert slabs' (all of them, shared expert included)."""
     sc = scratch
     cur = stream if isinstance(stream, torch.cuda.Stream) else torch.cuda.current_stream()
     side = None
@@ -675,13 +689,13 @@ def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, s
         if side is None:
             side = _SIDE_STREAMS[cur.device] = torch.cuda.Stream(device=cur.device)
         side.wait_stream(cur)
-        moe_shared(ptbl_sh, xs, iq4nl, sc.sact, sc.shared, stream=side)
+        moe_shared(ptbl_sh, xs, iq4nl, sc.sact, sc.shared, stream=side, layout=layout)
     moe_topk(logits, sc.eids, sc.gates, stream=cur)
     moe_sort(sc.eids, sc.eoff, sc.plist, sc.items, sc.nitp, stream=cur)
-    moe_up4(ptbl, sc.items, sc.nitp, sc.eoff, sc.plist, xs, iq4nl, sc.act, stream=cur)
-    moe_dn4(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, iq4nl, sc.parts, stream=cur)
+    moe_up4(ptbl, sc.items, sc.nitp, sc.eoff, sc.plist, xs, iq4nl, sc.act, stream=cur, layout=layout)
+    moe_dn4(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, iq4nl, sc.parts, stream=cur, layout=layout)
     if side is None:
-        moe_shared(ptbl_sh, xs, iq4nl, sc.sact, sc.shared, stream=cur)
+        moe_shared(ptbl_sh, xs, iq4nl, sc.sact, sc.shared, stream=cur, layout=layout)
     else:
         cur.wait_stream(side)
     moe_combine(sc.parts, sc.gates, sg, sc.shared, hres, y, stream=cur)
