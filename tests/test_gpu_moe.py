@@ -216,7 +216,7 @@ def test_moe_layer_skewed(gpu, experts, P):
     """A router biased towards 12 experts gives them 2..4 groups of 16 tokens and several items
     each (64 pairs in the GEMV form, 96 in the GEMM form; ragged last ones).  Pair counts up to
     2048 (P = 64, 256) take the GEMV form, more
-    (P = 300) the prefill GEMM, whose shared expert then ends on a 44-position chunk."""
+    (P = 300) the prefill GEMM, whose shared expert then ends on a 12-position chunk."""
     print(f"[case] moe layer skewed P={P}", flush=True)
     rng = np.random.default_rng(24 + P)
     x, logits, sg, hres = _inputs(rng, P)

@@ -136,7 +136,9 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
 // ceil(count / tok) chunks of its pairs, expert ascending, item = expert << 16 | first pair offset,
 // tok = moe_item_tok(np).
 constexpr int kMaxPairs = 16384;
-constexpr int kTok = 64;         // item size of the GEMV form, and the dense (shared expert) chunk
+constexpr int kTok = 64;         // item size of the GEMV form, and its dense (shared expert) chunk
+constexpr int kDenseTok = 32;    // the GEMM form's dense chunk: 2 groups, so the shared expert's
+                                 // grids fill the GPU beside the router and the sort
 constexpr int kPfTok = 96;       // item size of the GEMM form: up to 6 groups of 16 tokens
 constexpr int kGvMaxPairs = 2048;   // pair counts up to this use the GEMV form, larger ones the GEMM
 constexpr int kSortWaves = 16;
@@ -397,9 +399,14 @@ __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, const void* base, const
   // stage h then covers only weights up to stage h + 1), with RING == 2 the weights (the wait for
   // stage h + 1's weights then covers only activations up to stage h + 1).
   auto stage = [&](int h, MoeWs& w, MoeWs& wnext) {
+    // (with the deep ring the requests are fenced at the stage's start: the scheduler would
+    // otherwise sink them to its end, and a small-NG stage is too short to cover their latency;
+    // measured: P = 512, 1-2 groups, 150 -> 81 us.  At 3+ groups the fences cost 7%.)
+    if constexpr (RING > 2) __builtin_amdgcn_sched_barrier(0);
     if constexpr (RING > 2) load_a(h & 1, min(h + 2, kH - 1));
     load_w(wnext, min(h + RING - 1, kH - 1));
     if constexpr (RING == 2) load_a(h & 1, min(h + 2, kH - 1));
+    if constexpr (RING > 2) __builtin_amdgcn_sched_barrier(0);
     const u4_t* arow = L.a[h & 1] + 16 * col;   // + 256 * g: token row 16g + col (slot p ^ col)
     const int ib = 4 * (h & 1) + kq;             // the lane's sub-block of block h / 2
     _Float16 dh[kPfTiles];
@@ -422,9 +429,11 @@ __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, const void* base, const
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         const h8_t A = __builtin_bit_cast(h8_t, arow[256 * g + (pc ^ col)]);
+        // weights as the MFMA's first operand: the output lane (col, kq) then holds weight rows
+        // 4 kq .. 4 kq + 3 of the tile for token col (4 consecutive outputs, one wide store)
 #pragma unroll
         for (int j = 0; j < kPfTiles; ++j)
-          acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], acc[g][j], 0, 0, 0);
+          acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(B[j], A, acc[g][j], 0, 0, 0);
       }
     }
     // (waits for its loads; stage h - 1's buffer is free: every wave passed the last barrier)
@@ -464,31 +473,23 @@ __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, const void* base, const
   for (int r = 0; r < kH % U; ++r) stage(h0 + r, W[r % RING], W[(r + RING - 1) % RING]);
   __builtin_amdgcn_s_waitcnt(0x0F70);   // the clamped tail loads
 
-  // lane (col, kq) holds tokens 16g + 4kq + r of row 16 * tile + col
+  // lane (col, kq) holds rows 16 tile + 4 kq + r of token 16 g + col
+  static_assert(kUp, "the down projection runs moe_pd_kernel");
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
+    const int slot = 16 * g + col;
+    if (slot >= ntok) continue;
+    const int o = L.orow[slot];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int slot = 16 * g + 4 * kq + r;
-      if (slot >= ntok) continue;
-      const int o = L.orow[slot];
-      if constexpr (kUp) {
+    for (int j = 0; j < 2; ++j) {
+      f4_t v;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const float gv = acc[g][j][r], uv = acc[g][j + 2][r];
-          const int n = 16 * (2 * tb + j) + col;
-          reinterpret_cast<float*>(out)[(size_t)o * kFf + n] = gv / (1.f + expf(-gv)) * uv;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < kPfTiles; ++j) {
-          const int n = 16 * (4 * tb + j) + col;
-          if constexpr (KIND == MOE_DN)
-            reinterpret_cast<uint16_t*>(out)[(size_t)o * kHid + n] = tlx_f2h_bits(acc[g][j][r]);
-          else
-            reinterpret_cast<float*>(out)[(size_t)o * kHid + n] = acc[g][j][r];
-        }
+      for (int r = 0; r < 4; ++r) {
+        const float gv = acc[g][j][r], uv = acc[g][j + 2][r];
+        v[r] = gv / (1.f + expf(-gv)) * uv;
       }
+      const int n = 16 * (2 * tb + j) + 4 * kq;
+      *reinterpret_cast<f4_t*>(reinterpret_cast<float*>(out) + (size_t)o * kFf + n) = v;
     }
   }
 }
@@ -509,10 +510,10 @@ __global__ __launch_bounds__(kPfThreads, 1) void moe_pf_kernel(
 
   int m0, ntok;
   const void* base;
-  if constexpr (kDense) {   // the shared expert: chunks of kTok positions
-    m0 = item * kTok;
+  if constexpr (kDense) {   // the shared expert: chunks of kDenseTok positions
+    m0 = item * kDenseTok;
     if (m0 >= P) return;
-    ntok = min(kTok, P - m0);
+    ntok = min(kDenseTok, P - m0);
     base = (const void*)(ptbl[0]);
   } else {
     if (item >= (int)*nitp) return;
@@ -535,14 +536,214 @@ __global__ __launch_bounds__(kPfThreads, 1) void moe_pf_kernel(
       L.orow[t] = pair;
     }
   }
-  // workgroup-uniform (the tile's first barrier publishes xrow / orow); dense chunks have <= 64
+  // workgroup-uniform (the tile's first barrier publishes xrow / orow); dense chunks have <= 32
   switch ((ntok + 15) >> 4) {
     case 1: moe_pf_tile<KIND, 1, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
     case 2: moe_pf_tile<KIND, 2, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
-    case 3: moe_pf_tile<KIND, 3, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
-    case 4: moe_pf_tile<KIND, 4, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
+    case 3: if constexpr (!kDense) moe_pf_tile<KIND, 3, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
+    case 4: if constexpr (!kDense) moe_pf_tile<KIND, 4, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
     case 5: if constexpr (!kDense) moe_pf_tile<KIND, 5, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
     default: if constexpr (!kDense) moe_pf_tile<KIND, 6, TL>(L, base, xs, iq4nl, out, ntok, stripe, wave, lane); break;
+  }
+}
+
+// ------------------------------------------------------------------ grouped IQ4_XS down GEMM (prefill)
+// The down projection's K (512) is short enough for an item's activations to stay in LDS: a
+// workgroup stages its item's act rows once (fp16, MFMA k order, 96 KB at 96 tokens) and then
+// streams all 2048 weight rows as 4 stripes of 512 -- wave w owns tiles 4 (8 s + w) .. + 3 of
+// stripe s -- with no barrier after the staging: the 16 (stripe, stage) steps of a wave are one
+// weight stream, loaded 3 steps ahead.  Stage h (128 k) of block h / 2: lane (col, kq) holds row
+// col's sub-block 4 (h & 1) + kq, decoded as in the gate/up kernel.  One workgroup per item, so
+// an expert's down weights are read once and its activations once.
+constexpr int kPdPieces = kFf / 8;   // 16-B pieces per staged row (64)
+
+struct __attribute__((aligned(16))) MoePdLds {
+  uint32_t lut[256 * TLX_WAVE];   // [quant byte][lane]: (kv[lo], kv[hi]) fp16
+  u4_t a[kPfTok * kPdPieces];     // the item's activations, fp16, [row][swizzled piece]
+};
+
+template <int KIND, int NG, bool TL>
+__device__ __forceinline__ void moe_pd_tile(MoePdLds& L, const void* base, const float* __restrict__ xs,
+                                            const float* __restrict__ iq4nl, void* __restrict__ out,
+                                            const uint16_t* __restrict__ plist, int m0, int ntok, int wave,
+                                            int lane) {
+  constexpr bool kDense = KIND == MOE_DN_DENSE;
+  constexpr int kNb = kFf / 256;                     // blocks per row (2)
+  constexpr int kRowBytes = kNb * 136;
+  constexpr int RING = NG <= 4 ? 4 : 2;               // weight steps in the ring (RING - 1 ahead)
+  const int col = lane & 15, kq = lane >> 4, t = threadIdx.x;
+  // slot s's pair (row of act / parts): the sorted pair list, or the dense chunk's position
+  auto pair_of = [&](int slot) { return kDense ? m0 + slot : (int)plist[m0 + slot]; };
+
+  const __amdgpu_buffer_rsrc_t rw = moe_rsrc(base, (uint32_t)kHid * kRowBytes);
+  const int vh = TL ? 8 * col : col * kRowBytes;
+  const int vq = TL ? 128 + 16 * lane : col * kRowBytes + 8 + 16 * kq;
+  // step i = 4 s + h: stripe s, stage h; tile j of the wave: 4 (8 s + wave) + j
+  auto load_w = [&](MoeWs& w, int i) {
+    const int s = i >> 2, h = i & 3;
+    const int t0 = 16 * 4 * (kPfWaves * s + wave) * kRowBytes;   // first tile's first byte
+    const int so = t0 + (TL ? 2176 * (h >> 1) : 136 * (h >> 1));
+    const int sq = so + (TL ? 1024 : 64) * (h & 1);
+#pragma unroll
+    for (int j = 0; j < kPfTiles; ++j) {
+      w.h[j] = __builtin_bit_cast(u2_t, __builtin_amdgcn_raw_buffer_load_b64(rw, vh, so + 16 * j * kRowBytes, 0));
+      w.q[j] = __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, vq, sq + 16 * j * kRowBytes, 0));
+    }
+  };
+
+  // the stripes of this workgroup: all 4 (routed items), or blockIdx.y (dense chunks)
+  const int s0 = kDense ? (int)blockIdx.y : 0, s1 = kDense ? s0 + 1 : 4;
+  MoeWs W[RING];
+#pragma unroll
+  for (int r = 0; r < RING - 1; ++r) load_w(W[r], 4 * s0 + r);   // first: in flight during the staging and the table
+  // ---- stage the item's activations: piece p of row r (x[r][8 (p & ~3) + ...]: sub-block p / 4,
+  // chunk p % 4, the halves k0 + {0, 16, 1, 17, 2, 18, 3, 19}) at slot p ^ (r & 15) of row r.
+  // All of a thread's pieces are requested at once; the byte table is built while they (and the
+  // first weights) are in flight.
+  {
+    const __amdgpu_buffer_rsrc_t rx = moe_rsrc(xs, 0x7FFFFFFFu);
+    constexpr int kPer = 16 * NG * kPdPieces / kPfThreads;   // pieces per thread (2 NG)
+    float4 v[kPer][2];
+    int dst[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int q = j * kPfThreads + t;   // piece index q = row * 64 + p
+      const int row = q >> 6, p = q & 63;
+      const int src = pair_of(min(row, ntok - 1)) * (kFf * 4) + 4 * (32 * (p >> 2) + 4 * (p & 3));
+      v[j][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, src, 0, 0));
+      v[j][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, src + 64, 0, 0));
+      dst[j] = row * kPdPieces + (p ^ (row & 15));
+    }
+    // the byte table, one copy per lane (as the gate/up kernel)
+#pragma unroll
+    for (int i = 0; i < 256 / kPfWaves; ++i) {
+      const int b = wave + kPfWaves * i;
+      const _Float16 lo = (_Float16)iq4nl[b & 15], hi = (_Float16)iq4nl[b >> 4];
+      L.lut[b * TLX_WAVE + lane] =
+          (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const h8_t hv = {(_Float16)v[j][0].x, (_Float16)v[j][1].x, (_Float16)v[j][0].y, (_Float16)v[j][1].y,
+                       (_Float16)v[j][0].z, (_Float16)v[j][1].z, (_Float16)v[j][0].w, (_Float16)v[j][1].w};
+      L.a[dst[j]] = __builtin_bit_cast(u4_t, hv);
+    }
+  }
+  __syncthreads();   // activations and table visible; no barrier after this
+
+  const uint8_t* lut0 = reinterpret_cast<const uint8_t*>(L.lut);
+  const uint32_t lane4 = 4u * (uint32_t)lane;
+  auto lut = [&](uint32_t qw, int i) {
+    const uint32_t off = __builtin_amdgcn_perm(qw, lane4, 0x0C0C0000u | ((4u + (uint32_t)i) << 8));
+    return *reinterpret_cast<const uint32_t*>(lut0 + off);
+  };
+  const u4_t* arow = L.a + kPdPieces * col;   // + 1024 g: token row 16 g + col
+
+  f4_t acc[NG][kPfTiles];
+  static_assert(4 % RING == 0, "stage h of a stripe uses ring entry h % RING");
+#pragma nounroll
+  for (int s = s0; s < s1; ++s) {
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int j = 0; j < kPfTiles; ++j) acc[g][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const int i = 4 * s + h;
+    // (scheduling fences: one per stage -- with no barrier in the loop the scheduler would
+    // otherwise interleave the stages' table lookups and decodes and run out of registers -- and
+    // one after the stage's weight requests, which it would otherwise sink to the stage's end,
+    // where the next stage waits for them at once)
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(W[(h + RING - 1) % RING], min(i + RING - 1, 4 * s1 - 1));   // clamped: repeats the last step
+    __builtin_amdgcn_sched_barrier(0);
+    const MoeWs& w = W[h % RING];
+    const int ib = 4 * (h & 1) + kq;
+    _Float16 dh[kPfTiles];
+#pragma unroll
+    for (int j = 0; j < kPfTiles; ++j) {
+      const uint32_t sh = w.h[j].x >> 16;
+      const uint32_t ls = ((w.h[j].y >> (4 * ib)) & 0xFu) | (((sh >> (2 * ib)) & 3u) << 4);
+      dh[j] = (_Float16)(tlx_h2f((uint16_t)w.h[j].x) * (float)((int)ls - 32));
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      h8_t B[kPfTiles];
+#pragma unroll
+      for (int j = 0; j < kPfTiles; ++j) {
+        const uint32_t qw = w.q[j][c];
+        const u4_t w4 = {lut(qw, 0), lut(qw, 1), lut(qw, 2), lut(qw, 3)};
+        B[j] = __builtin_bit_cast(h8_t, w4) * splat8h(dh[j]);
+      }
+      const int pc = 16 * h + 4 * kq + c;   // piece of k = 128 h + 32 kq + 4 c
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const h8_t A = __builtin_bit_cast(h8_t, arow[1024 * g + (pc ^ col)]);
+        // weights as the MFMA's first operand: the output lane (col, kq) then holds weight rows
+        // 4 kq .. 4 kq + 3 of the tile for token col (4 consecutive outputs, one wide store)
+#pragma unroll
+        for (int j = 0; j < kPfTiles; ++j)
+          acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(B[j], A, acc[g][j], 0, 0, 0);
+      }
+    }
+    if (h == 3) {   // stripe s done: lane (col, kq) holds rows 16 tile + 4 kq + r of token 16 g + col
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const int slot = 16 * g + col;
+        if (slot >= ntok) continue;
+        const int o = pair_of(slot);
+#pragma unroll
+        for (int j = 0; j < kPfTiles; ++j) {
+          const int n = 16 * (4 * (kPfWaves * s + wave) + j) + 4 * kq;
+          const f4_t v = acc[g][j];
+          if constexpr (KIND == MOE_DN) {
+            const h4_t hv = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+            *reinterpret_cast<h4_t*>(reinterpret_cast<uint16_t*>(out) + (size_t)o * kHid + n) = hv;
+          } else {
+            *reinterpret_cast<f4_t*>(reinterpret_cast<float*>(out) + (size_t)o * kHid + n) = v;
+          }
+        }
+      }
+    }
+  }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // the clamped tail loads
+}
+
+// one workgroup per item (routed: all 4 stripes) or per (kDenseTok-position chunk, stripe) (dense)
+template <int KIND, bool TL>
+__global__ __launch_bounds__(kPfThreads, 1) void moe_pd_kernel(
+    const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff, const uint16_t* __restrict__ plist,
+    const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp, const float* __restrict__ xs,
+    const float* __restrict__ iq4nl, void* __restrict__ out, int P) {
+  constexpr bool kDense = KIND == MOE_DN_DENSE;
+  __shared__ MoePdLds L;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int item = (int)blockIdx.x;
+  int m0, ntok;
+  const void* base;
+  if constexpr (kDense) {
+    m0 = item * kDenseTok;
+    if (m0 >= P) return;
+    ntok = min(kDenseTok, P - m0);
+    base = (const void*)(ptbl[0]);
+  } else {
+    if (item >= (int)*nitp) return;
+    const uint32_t it = items[item];
+    const int e = (int)(it >> 16);
+    m0 = (int)(it & 0xFFFFu);
+    const int eb0 = eoff[e];
+    ntok = min(kPfTok, eoff[e + 1] - eb0 - m0);
+    m0 += eb0;
+    base = (const void*)(ptbl[e]);
+  }
+  switch ((ntok + 15) >> 4) {   // workgroup-uniform; dense chunks have <= 32 positions
+    case 1: moe_pd_tile<KIND, 1, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane); break;
+    case 2: moe_pd_tile<KIND, 2, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane); break;
+    case 3: if constexpr (!kDense) moe_pd_tile<KIND, 3, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane); break;
+    case 4: if constexpr (!kDense) moe_pd_tile<KIND, 4, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane); break;
+    case 5: if constexpr (!kDense) moe_pd_tile<KIND, 5, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane); break;
+    default: if constexpr (!kDense) moe_pd_tile<KIND, 6, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane); break;
   }
 }
 
@@ -842,13 +1043,23 @@ void moe_pf_launch(bool tl, int nitems, hipStream_t st, const uint64_t* ptbl, co
     moe_pf_kernel<KIND, false><<<grid, kPfThreads, 0, st>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, out, P);
 }
 
+template <int KIND>
+void moe_pd_launch(bool tl, int nitems, hipStream_t st, const uint64_t* ptbl, const int* eoff, const uint16_t* plist,
+                   const uint32_t* items, const uint32_t* nitp, const float* xs, const float* iq4nl, void* out, int P) {
+  const dim3 grid(nitems, KIND == MOE_DN_DENSE ? 4 : 1);   // dense: one stripe per workgroup
+  if (tl)
+    moe_pd_kernel<KIND, true><<<grid, kPfThreads, 0, st>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, out, P);
+  else
+    moe_pd_kernel<KIND, false><<<grid, kPfThreads, 0, st>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, out, P);
+}
+
 bool moe_layout_ok(int layout) { return layout == TLX_LAYOUT_RAW || layout == TLX_LAYOUT_TILED; }
 
 extern "C" int tlx_moe_up4(const uint64_t* ptbl, const uint32_t* items, const uint32_t* nitp, const int* eoff,
                            const uint16_t* plist, const float* xs, const float* iq4nl, float* ys, int np, int layout,
                            void* stream) {
   TLX_RET_IF(np < 1 || np > kMaxPairs || !moe_layout_ok(layout), TLX_E_ARG);
-  TLX_RET_IF(!tlx_aligned(xs, 16), TLX_E_ALIGN);
+  TLX_RET_IF(!tlx_aligned(xs, 16) || !tlx_aligned(ys, 16), TLX_E_ALIGN);
   const bool tl = layout == TLX_LAYOUT_TILED;
   const hipStream_t st = (hipStream_t)stream;
   if (np <= kGvMaxPairs)
@@ -870,7 +1081,7 @@ extern "C" int tlx_moe_dn4(const uint64_t* ptbl_dn, const uint32_t* items, const
     moe_gv_launch<MOE_DN>(tl, moe_gv_grid<MOE_DN>(moe_gv_items(np)), st, ptbl_dn, eoff, plist, items, nitp, nullptr,
                           act, iq4nl, parts, 0);
   else
-    moe_pf_launch<MOE_DN>(tl, moe_max_items(np), st, ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
+    moe_pd_launch<MOE_DN>(tl, moe_max_items(np), st, ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
   return tlx_launch_status();
 }
 
@@ -895,7 +1106,7 @@ extern "C" int tlx_moe_dn4_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, 
 extern "C" int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const float* iq4nl, float* act, float* out,
                               int P, int layout, void* stream) {
   TLX_RET_IF(P < 1 || !moe_layout_ok(layout), TLX_E_ARG);
-  TLX_RET_IF(!tlx_aligned(xs, 16) || !tlx_aligned(act, 16), TLX_E_ALIGN);
+  TLX_RET_IF(!tlx_aligned(xs, 16) || !tlx_aligned(act, 16) || !tlx_aligned(out, 16), TLX_E_ALIGN);
   const bool tl = layout == TLX_LAYOUT_TILED;
   const hipStream_t st = (hipStream_t)stream;
   const int chunks = (P + kTok - 1) / kTok;
@@ -908,10 +1119,11 @@ extern "C" int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const fl
                                 nullptr, nullptr, act, iq4nl, out, P);
     return tlx_launch_status();
   }
-  moe_pf_launch<MOE_UP_DENSE>(tl, chunks, st, ptbl_sh, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, act, P);
+  const int dchunks = (P + kDenseTok - 1) / kDenseTok;
+  moe_pf_launch<MOE_UP_DENSE>(tl, dchunks, st, ptbl_sh, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, act, P);
   int rc = tlx_launch_status();
   TLX_RET_IF(rc != TLX_OK, rc);
-  moe_pf_launch<MOE_DN_DENSE>(tl, chunks, st, ptbl_sh + 1, nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
+  moe_pd_launch<MOE_DN_DENSE>(tl, dchunks, st, ptbl_sh + 1, nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
   return tlx_launch_status();
 }
 
