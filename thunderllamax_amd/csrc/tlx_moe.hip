@@ -772,10 +772,10 @@ constexpr int moe_gv_wpt() { return (KIND == MOE_UP || KIND == MOE_UP_DENSE) ? 2
 // argument so that every activation load is unconditional: the compiler can then issue them
 // ahead of their MFMAs instead of waiting on each one in turn.  red: the workgroup's
 // [4 waves][kGvGroups][NMAT][64 lanes] reduction buffer.
-template <int KIND, int NG, bool TL>
+template <int KIND, int NG, bool TL, bool XS>
 __device__ __forceinline__ void moe_gv_tile(gbyte* base, const uint32_t* lut, const int* xrow, const int* orow,
-                                            f4_t* red, const float* __restrict__ xs, void* __restrict__ out,
-                                            int ntok, int tile, int wave, int lane) {
+                                            f4_t* red, const u4_t* xst, const float* __restrict__ xs,
+                                            void* __restrict__ out, int ntok, int tile, int wave, int lane) {
   using S = MoeShape<KIND>;
   constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
   constexpr int NMAT = kUp ? 2 : 1;
@@ -811,6 +811,8 @@ __device__ __forceinline__ void moe_gv_tile(gbyte* base, const uint32_t* lut, co
   const float* xr[NG];   // lane's activation row in group g, at its first k of a block
 #pragma unroll
   for (int g = 0; g < NG; ++g) xr[g] = xs + (size_t)xrow[16 * g + col] * S::K + 256 * kb0 + 32 * kq;
+  // staged (NG == 1): the lane's token row min(col, ntok - 1) of the staged copy
+  const int xsrow = min(col, ntok - 1) * (S::K / 8 + 1);
 
   f4_t acc[NG][NMAT];
 #pragma unroll
@@ -842,10 +844,15 @@ __device__ __forceinline__ void moe_gv_tile(gbyte* base, const uint32_t* lut, co
         const int k0 = 256 * bb + 128 * sb + 4 * c;
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-          const float4 x0 = *reinterpret_cast<const float4*>(xr[g] + k0);
-          const float4 x1 = *reinterpret_cast<const float4*>(xr[g] + k0 + 16);
-          const h8_t A = {(_Float16)x0.x, (_Float16)x1.x, (_Float16)x0.y, (_Float16)x1.y,
-                          (_Float16)x0.z, (_Float16)x1.z, (_Float16)x0.w, (_Float16)x1.w};
+          h8_t A;
+          if constexpr (XS) {   // staged: piece 32 (kb0 + bb) + 4 ib + c of the lane's token row
+            A = __builtin_bit_cast(h8_t, xst[xsrow + 32 * (kb0 + bb) + 4 * ib + c]);
+          } else {
+            const float4 x0 = *reinterpret_cast<const float4*>(xr[g] + k0);
+            const float4 x1 = *reinterpret_cast<const float4*>(xr[g] + k0 + 16);
+            A = h8_t{(_Float16)x0.x, (_Float16)x1.x, (_Float16)x0.y, (_Float16)x1.y,
+                     (_Float16)x0.z, (_Float16)x1.z, (_Float16)x0.w, (_Float16)x1.w};
+          }
 #pragma unroll
           for (int mi = 0; mi < NMAT; ++mi)
             acc[g][mi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[mi], acc[g][mi], 0, 0, 0);
@@ -906,6 +913,12 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
   __shared__ uint32_t lut[256];
   __shared__ int xrow[kTok], orow[kTok];
   __shared__ f4_t red[4 * kGvGroups * NMAT * 64];
+  // Items of at most kGvStageRows tokens (decode: one or two) stage their token rows once, fp16
+  // in the MFMA k order, row stride K / 8 + 1 pieces: read from global inside the decode loop,
+  // each chunk's activations cost a serialized L2 round trip.
+  constexpr int kK = MoeShape<KIND>::K, kPr = kK / 8 + 1;
+  constexpr int kGvStageRows = 1024 / kPr;   // rows in 16 KB: 3 (gate+up, K = 2048), 15 (down)
+  __shared__ u4_t xst[kGvStageRows * kPr];
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
 
   int m0, ntok;
@@ -947,12 +960,29 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
     lut[t] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
   }
   __syncthreads();
+  const bool staged = ntok <= kGvStageRows;   // workgroup-uniform
+  if (staged) {
+    // piece q = row * (K / 8) + p: sub-block p / 4, chunk p % 4 -- x[32 (p / 4) + 4 (p % 4) + {0, 16, 1,
+    // 17, 2, 18, 3, 19}]
+    for (int q = t; q < ntok * (kK / 8); q += 256) {
+      const int row = q / (kK / 8), p = q - row * (kK / 8);
+      const float* src = xs + (size_t)xrow[row] * kK + 32 * (p >> 2) + 4 * (p & 3);
+      const float4 v0 = *reinterpret_cast<const float4*>(src), v1 = *reinterpret_cast<const float4*>(src + 16);
+      const h8_t hv = {(_Float16)v0.x, (_Float16)v1.x, (_Float16)v0.y, (_Float16)v1.y,
+                       (_Float16)v0.z, (_Float16)v1.z, (_Float16)v0.w, (_Float16)v1.w};
+      xst[row * kPr + p] = __builtin_bit_cast(u4_t, hv);
+    }
+    __syncthreads();
+  }
   const int tile = (int)blockIdx.y * kTpw + wave / moe_gv_wpt<KIND>();   // 16-row output tile
   switch ((ntok + 15) >> 4) {   // workgroup-uniform
-    case 1: moe_gv_tile<KIND, 1, TL>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
-    case 2: moe_gv_tile<KIND, 2, TL>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
-    case 3: moe_gv_tile<KIND, 3, TL>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
-    default: moe_gv_tile<KIND, 4, TL>(base, lut, xrow, orow, red, xs, out, ntok, tile, wave, lane); break;
+    case 1:
+      if (staged) moe_gv_tile<KIND, 1, TL, true>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane);
+      else moe_gv_tile<KIND, 1, TL, false>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane);
+      break;
+    case 2: moe_gv_tile<KIND, 2, TL, false>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane); break;
+    case 3: moe_gv_tile<KIND, 3, TL, false>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane); break;
+    default: moe_gv_tile<KIND, 4, TL, false>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane); break;
   }
 }
 
