@@ -313,7 +313,7 @@ uint64_t tlx_iq3_tiled_bytes(int N, int K);
  * load-time repack for the grouped GEMMs' layout argument. */
 int tlx_pack_iq4_tiled(const void* src, void* tiled, int N, int K, void* stream);
 
-/* Top-8 + renormalized softmax from router logits f32[P][256] (the router epilogue of
+/* Top-8 + renormalized softmax from router logits f32[P][256], 16-B aligned (the router epilogue of
  * engine/mm/MM_P1_rt8e256.cu:41-60: strict >, ties to the lower id).  eids u16[P][8],
  * gates f32[P][8].  No reference counterpart on its own: the benchmark's MoE configuration feeds logits. */
 int tlx_moe_topk(const float* logits, uint16_t* eids, float* gates, int P, void* stream);
@@ -323,7 +323,7 @@ int tlx_moe_topk(const float* logits, uint16_t* eids, float* gates, int P, void*
 int tlx_moe_route(const float* wrt, const float* wsh, const float* h, uint16_t* eids, float* gates,
                   float* sg, int P, void* stream);
 
-/* Deterministic stable sort of the np = 8P pairs by expert: eoff i32[257] (exclusive bin
+/* Deterministic stable sort of the np = 8P pairs by expert (eids 8-B aligned): eoff i32[257] (exclusive bin
  * offsets), plist u16[np] (pair ids, pair order inside a bin), items u32[tlx_moe_max_items(np)]
  * (expert << 16 | first pair in bin, one per 64 pairs for np <= 2048 and per 96 pairs above: the
  * grouped GEMMs' forms), nitp u32[1] (item count).  np <= 16384.

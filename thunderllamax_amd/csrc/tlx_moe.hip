@@ -67,15 +67,62 @@ __device__ __forceinline__ void topk8_wave(float v[4], int lane, uint16_t* eids,
   }
 }
 
-// one wave per position, 4 positions per 256-thread workgroup
+// The same 8 passes with a position per 16-lane row (lane l: experts 16 l .. 16 l + 15): the row's
+// argmax is 4 DPP exchange steps inside the row (quad swaps, half-row and row mirrors) instead of
+// 6 cross-lane shuffles over the wave, which go through the LDS crossbar and serialize 96 round
+// trips per position.  Same comparisons, same order of the softmax sums: the same results.
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp_step(float& bv, int& bi) {
+  const float ov = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, bv), CTRL, 0xF, 0xF, true));
+  const int oi = __builtin_amdgcn_update_dpp(0, bi, CTRL, 0xF, 0xF, true);
+  if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+
+__device__ __forceinline__ void topk8_row16(const float4 (&in)[4], int l, uint16_t* eids, float* gates) {
+  float v[16];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) { v[4 * q] = in[q].x; v[4 * q + 1] = in[q].y; v[4 * q + 2] = in[q].z; v[4 * q + 3] = in[q].w; }
+  float m = -3.402823466e38f, ex[kTopK], s8 = 0.f;
+  int ids[kTopK];
+#pragma unroll
+  for (int r = 0; r < kTopK; ++r) {
+    float bv = v[0];
+    int bi = 16 * l;
+#pragma unroll
+    for (int j = 1; j < 16; ++j)
+      if (v[j] > bv) { bv = v[j]; bi = 16 * l + j; }
+    argmax_dpp_step<0xB1>(bv, bi);    // quad_perm [1, 0, 3, 2]
+    argmax_dpp_step<0x4E>(bv, bi);    // quad_perm [2, 3, 0, 1]
+    argmax_dpp_step<0x141>(bv, bi);   // row_half_mirror: quad q with quad 1 - q of each half
+    argmax_dpp_step<0x140>(bv, bi);   // row_mirror: half with half
+    if (r == 0) m = bv;
+    ids[r] = bi;
+    ex[r] = expf(bv - m);
+    s8 += ex[r];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (bi == 16 * l + j) v[j] = -3.402823466e38f;
+  }
+  if (l < kTopK) {
+    int id = ids[0];
+    float e = ex[0];
+#pragma unroll
+    for (int r = 1; r < kTopK; ++r)
+      if (l == r) { id = ids[r]; e = ex[r]; }
+    eids[l] = (uint16_t)id;
+    gates[l] = e / s8;
+  }
+}
+
+// a position per 16-lane row, 16 positions per 256-thread workgroup
 __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__ logits, uint16_t* __restrict__ eids,
                                                        float* __restrict__ gates, int P) {
-  const int p = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (p >= P) return;
-  float v[4];
+  const int p = blockIdx.x * 16 + (threadIdx.x >> 4), l = threadIdx.x & 15;
+  if (p >= P) return;   // whole 16-lane rows: the exchanges stay inside a row
+  float4 in[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] = logits[(size_t)p * kE + lane + 64 * j];
-  topk8_wave(v, lane, eids + (size_t)p * kTopK, gates + (size_t)p * kTopK);
+  for (int q = 0; q < 4; ++q) in[q] = reinterpret_cast<const float4*>(logits + (size_t)p * kE + 16 * l)[q];
+  topk8_row16(in, l, eids + (size_t)p * kTopK, gates + (size_t)p * kTopK);
 }
 
 // rt8e256: logits = wrt . h, shared gate sg = sigmoid(wsh . h), then the top-8.  One 256-thread
@@ -125,23 +172,23 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
 }
 
 // ------------------------------------------------------------------ sort
-// Deterministic stable counting sort by expert, one workgroup of 16 waves.  Wave w owns the
-// contiguous pair range [w * span, (w + 1) * span); in each 64-pair step the 8 ballots over the id
-// bits give every lane the mask of lanes holding the same expert, its rank among them is the
-// popcount below it, and the lowest such lane updates the wave's private count for that expert
-// (distinct experts, distinct LDS words: no atomics, no barriers inside a pass).  Pass 1 counts;
-// one scan over (expert, wave) gives every wave its start in each bin -- bins are expert
-// ascending, inside a bin the waves in order, inside a wave the steps and lanes in order, i.e. pair
-// order (stable, as mmsort8); pass 2 repeats the steps and scatters.  Items: per expert
-// ceil(count / tok) chunks of its pairs, expert ascending, item = expert << 16 | first pair offset,
-// tok = moe_item_tok(np).
+// Deterministic stable counting sort by expert over many workgroups, one launch: workgroup c
+// owns pairs [256 c, 256 c + 256).  Every workgroup reads all np keys and counts them per expert
+// twice in LDS -- all pairs, and the pairs before its chunk -- with atomic increments (a count does
+// not depend on their order); a scan over the experts of the totals gives the bins (expert
+// ascending), and bin e's slots for this chunk start after the bin start and the earlier chunks'
+// pairs of e.  Inside the chunk, wave w ranks its 64 pairs by 8 ballots over the key bits (the
+// lanes holding the same key; rank = those below), after the earlier waves' pairs of each key.
+// Bins are therefore in pair order, stable like mmsort8.  Workgroup 0 writes eoff, the items and
+// their count.  Items: per expert ceil(count / tok) chunks of its pairs, expert ascending, item =
+// expert << 16 | first pair offset, tok = moe_item_tok(np).
 constexpr int kMaxPairs = 16384;
 constexpr int kTok = 64;         // item size of the GEMV form, and its dense (shared expert) chunk
 constexpr int kDenseTok = 32;    // the GEMM form's dense chunk: 2 groups, so the shared expert's
                                  // grids fill the GPU beside the router and the sort
 constexpr int kPfTok = 96;       // item size of the GEMM form: up to 6 groups of 16 tokens
 constexpr int kGvMaxPairs = 2048;   // pair counts up to this use the GEMV form, larger ones the GEMM
-constexpr int kSortWaves = 16;
+constexpr int kSortChunk = 256;     // pairs per sort workgroup (4 waves of 64)
 
 // pairs per work item: the GEMV form takes up to 64, the GEMM form 96 (at uniform routing over 256
 // experts an expert's count exceeds 96 with odds of ~1e-4, so its weights are streamed once)
@@ -158,85 +205,76 @@ __device__ __forceinline__ uint64_t same_key_mask(uint32_t key) {
   return m;
 }
 
-__global__ __launch_bounds__(1024) void moe_sort_kernel(const uint16_t* __restrict__ eids, int* __restrict__ eoff,
-                                                        uint16_t* __restrict__ plist, uint32_t* __restrict__ items,
-                                                        uint32_t* __restrict__ nitp, int np) {
-  __shared__ int cnt[kSortWaves][kE];   // pass 1: pairs of expert e in wave w; then its running slot
-  __shared__ int wtot[kE / 64][2];      // per-wave totals of the expert scans
+__global__ __launch_bounds__(kSortChunk) void moe_sort_kernel(const uint16_t* __restrict__ eids, int* __restrict__ eoff,
+                                                              uint16_t* __restrict__ plist, uint32_t* __restrict__ items,
+                                                              uint32_t* __restrict__ nitp, int np) {
+  __shared__ int tot[kE];         // pairs of expert e, all chunks
+  __shared__ int pre[kE];         // pairs of expert e in the chunks before this one
+  __shared__ int cw[4][kE];       // pairs of expert e in each wave of this chunk
+  __shared__ int wsum[4][2];      // per-wave totals of the expert scans
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  const uint64_t below = (1ull << lane) - 1ull;
-  const int tok = moe_item_tok(np);
-  const int span = ((np + kSortWaves - 1) / kSortWaves + 63) & ~63;
-  const int i0 = min(np, wave * span), i1 = min(np, i0 + span);
-  for (int e = lane; e < kE; e += 64) cnt[wave][e] = 0;   // the wave's own row (in-order LDS)
-  // the wave's expert ids, all requested at once (at most kSteps per lane), kept for both passes
-  constexpr int kSteps = kMaxPairs / kSortWaves / 64;
-  uint32_t keys[kSteps];
+  const int c0 = (int)blockIdx.x * kSortChunk;
+  tot[t] = 0;
+  pre[t] = 0;
 #pragma unroll
-  for (int j = 0; j < kSteps; ++j) {
-    const int idx = i0 + 64 * j + lane;
-    keys[j] = idx < i1 ? (eids[idx] & 0xFFu) : 0u;   // ids are < 256 by contract
-  }
-  auto step = [&](int j, auto&& use) {
-    const int idx = i0 + 64 * j + lane;
-    const bool valid = idx < i1;
-    const uint32_t key = keys[j];
-    uint64_t same = same_key_mask(key) & __ballot(valid);   // every lane takes part in the ballots
-    if (!valid) same = 0;
-    if (valid) use(idx, key, __builtin_popcountll(same & below), __builtin_popcountll(same));
-  };
-  const int nsteps = (i1 - i0 + 63) / 64;   // <= kSteps
-#pragma unroll
-  for (int j = 0; j < kSteps; ++j) {
-    if (j >= nsteps) break;
-    step(j, [&](int, uint32_t key, int rank, int n) {
-      if (rank == 0) cnt[wave][key] += n;
-    });
-  }
+  for (int w = 0; w < 4; ++w) cw[w][t] = 0;
   __syncthreads();
-  // expert e = t (t < 256): total over the waves; exclusive scans over the experts of the pair
-  // counts and of the item counts (wave-inclusive scans, then the totals of the waves before)
-  int c = 0, ni = 0, sc = 0, si = 0;
-  if (t < kE) {
+  // ---- count all keys (4 per thread and step; the tail key by key)
+  const int nq = np >> 2;
+  for (int q = t; q < nq; q += kSortChunk) {
+    const uint2 k4 = reinterpret_cast<const uint2*>(eids)[q];
+    const uint32_t ks[4] = {k4.x & 0xFFu, (k4.x >> 16) & 0xFFu, k4.y & 0xFFu, (k4.y >> 16) & 0xFFu};
 #pragma unroll
-    for (int w = 0; w < kSortWaves; ++w) c += cnt[w][t];
-    ni = (c + tok - 1) / tok;
-    sc = c;
-    si = ni;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int pc = __shfl_up(sc, o, 64), pi = __shfl_up(si, o, 64);
-      if (lane >= o) { sc += pc; si += pi; }
+    for (int j = 0; j < 4; ++j) {
+      atomicAdd(&tot[ks[j]], 1);
+      if (4 * q + j < c0) atomicAdd(&pre[ks[j]], 1);
     }
-    if (lane == 63) { wtot[wave][0] = sc; wtot[wave][1] = si; }
   }
+  for (int i = 4 * nq + t; i < np; i += kSortChunk) {
+    const uint32_t k = eids[i] & 0xFFu;
+    atomicAdd(&tot[k], 1);
+    if (i < c0) atomicAdd(&pre[k], 1);
+  }
+  // ---- this chunk's pairs: wave w's step, the lanes of each key and their ranks
+  const int idx = c0 + t;
+  const bool valid = idx < np;
+  const uint32_t key = valid ? (eids[idx] & 0xFFu) : 0u;   // ids are < 256 by contract
+  uint64_t same = same_key_mask(key) & __ballot(valid);      // every lane takes part in the ballots
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int rank = __builtin_popcountll(same & below);
+  if (valid && rank == 0) cw[wave][key] = __builtin_popcountll(same);
   __syncthreads();
-  if (t < kE) {
-    int bc = sc - c, bi = si - ni;
-    for (int w = 0; w < wave; ++w) { bc += wtot[w][0]; bi += wtot[w][1]; }
+  // ---- expert e = t: exclusive scans over the experts of the pair counts and of the item counts
+  const int tok = moe_item_tok(np);
+  const int c = tot[t], ni = (c + tok - 1) / tok;
+  int sc = c, si = ni;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int pc = __shfl_up(sc, o, 64), pi = __shfl_up(si, o, 64);
+    if (lane >= o) { sc += pc; si += pi; }
+  }
+  if (lane == 63) { wsum[wave][0] = sc; wsum[wave][1] = si; }
+  __syncthreads();
+  int bc = sc - c, bi = si - ni;
+  for (int w = 0; w < wave; ++w) { bc += wsum[w][0]; bi += wsum[w][1]; }
+  if (blockIdx.x == 0) {
     eoff[t] = bc;
     for (int j = 0; j < ni; ++j) items[bi + j] = ((uint32_t)t << 16) | (uint32_t)(tok * j);
     if (t == kE - 1) {
       eoff[kE] = bc + c;
       *nitp = (uint32_t)(bi + ni);
     }
-    // bin e: wave w's pairs start after the bin start and the earlier waves' pairs of e
+  }
+  // bin e's slots for this chunk's waves: after the bin start, the earlier chunks and waves
+  int run = bc + pre[t];
 #pragma unroll
-    for (int w = 0; w < kSortWaves; ++w) {
-      const int n = cnt[w][t];
-      cnt[w][t] = bc;
-      bc += n;
-    }
+  for (int w = 0; w < 4; ++w) {
+    const int n = cw[w][t];
+    cw[w][t] = run;
+    run += n;
   }
   __syncthreads();
-#pragma unroll
-  for (int j = 0; j < kSteps; ++j) {
-    if (j >= nsteps) break;
-    step(j, [&](int idx, uint32_t key, int rank, int n) {
-      plist[cnt[wave][key] + rank] = (uint16_t)idx;
-      if (rank == 0) cnt[wave][key] += n;   // after every lane of the step has read it (in-order LDS)
-    });
-  }
+  if (valid) plist[cw[wave][key] + rank] = (uint16_t)idx;
 }
 
 // ------------------------------------------------------------------ grouped IQ4_XS GEMM
@@ -1016,7 +1054,8 @@ int moe_max_items(int np) { return (np + moe_item_tok(np) - 1) / moe_item_tok(np
 
 extern "C" int tlx_moe_topk(const float* logits, uint16_t* eids, float* gates, int P, void* stream) {
   TLX_RET_IF(P < 1, TLX_E_ARG);
-  moe_topk_kernel<<<(P + 3) / 4, 256, 0, (hipStream_t)stream>>>(logits, eids, gates, P);
+  TLX_RET_IF(!tlx_aligned(logits, 16), TLX_E_ALIGN);
+  moe_topk_kernel<<<(P + 15) / 16, 256, 0, (hipStream_t)stream>>>(logits, eids, gates, P);
   return tlx_launch_status();
 }
 
@@ -1031,7 +1070,9 @@ extern "C" int tlx_moe_route(const float* wrt, const float* wsh, const float* h,
 extern "C" int tlx_moe_sort(const uint16_t* eids, int* eoff, uint16_t* plist, uint32_t* items, uint32_t* nitp,
                             int np, void* stream) {
   TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
-  moe_sort_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(eids, eoff, plist, items, nitp, np);
+  TLX_RET_IF(!tlx_aligned(eids, 8), TLX_E_ALIGN);
+  moe_sort_kernel<<<(np + kSortChunk - 1) / kSortChunk, kSortChunk, 0, (hipStream_t)stream>>>(eids, eoff, plist,
+                                                                                            items, nitp, np);
   return tlx_launch_status();
 }
 
