@@ -900,7 +900,10 @@ __device__ __forceinline__ void moe_gv_tile(gbyte* base, const uint32_t* lut, co
   }
 
   // fixed-order reduction over the waves of a tile
-  auto rslot = [&](int w, int g, int mi) -> f4_t& { return red[((w * kGvGroups + g) * NMAT + mi) * 64 + lane]; };
+  // slot of writer wave w (w % kWpt != 0): w / kWpt -- one per tile shared by two waves
+  auto rslot = [&](int w, int g, int mi) -> f4_t& {
+    return red[(((w / kWpt) * kGvGroups + g) * NMAT + mi) * 64 + lane];
+  };
   if constexpr (kWpt > 1) {
     if (wave % kWpt != 0) {
 #pragma unroll
@@ -950,7 +953,9 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
   constexpr int kTpw = 4 / moe_gv_wpt<KIND>();    // tiles per workgroup
   __shared__ uint32_t lut[256];
   __shared__ int xrow[kTok], orow[kTok];
-  __shared__ f4_t red[4 * kGvGroups * NMAT * 64];
+  // reduction slots: one per tile shared by two waves (gate+up); the down tiles are one wave's
+  // (16 KB, so 5 workgroups fit a CU: a decode step's ~1200 workgroups run in one round)
+  __shared__ f4_t red[(moe_gv_wpt<KIND>() > 1 ? 4 / moe_gv_wpt<KIND>() : 1) * kGvGroups * NMAT * 64];
   // Items of at most kGvStageRows tokens (decode: one or two) stage their token rows once, fp16
   // in the MFMA k order, row stride K / 8 + 1 pieces: read from global inside the decode loop,
   // each chunk's activations cost a serialized L2 round trip.
