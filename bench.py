@@ -48,11 +48,14 @@ followed by ffn8, and fused with it in one entry point (graph replays).
 ``formats`` times the load-time repacking on the GPU (raw GGUF IQ3_XXS rows of config 2's gate
 matrix -> packed rows -> packed7) in GB/s of bytes read + written.
 
-``moe`` is config 5: the whole MoE layer (top-8 from N(0,1) logits, sort, grouped IQ4_XS
-gate+up and down, shared expert, combine) at M=11 and M=2048, seeded expert weights, the
-layer's launches per step captured in one HIP graph, the shared expert on a second stream
-(``ms_shared_not_overlapped``: the same layer with every launch on one stream); each step reads a different copy of
-the 257 expert slabs (3 copies, 1.3 GB), so at M=11 the weights come from HBM.
+``moe`` is config 5: the whole MoE layer at M=11 and M=2048 as ``ops.moe_layer`` runs it by
+default -- M=11: top-8 from N(0,1) logits, the pair-walk IQ4_XS gate+up and down (no sort),
+shared expert, combine, all on one stream; M=2048: top-8, sort, grouped gate+up and down, the
+shared expert on a second stream, combine -- seeded expert weights, the layer's launches per
+step captured in one HIP graph (``ms_other_shared_stream``: the shared expert on the other
+choice of stream; ``ms_sorted_grouped`` at M=11: the grouped route); each step reads a
+different copy of the 257 expert slabs (3 copies, 1.3 GB), so at M=11 the weights come from
+HBM.
 """
 import argparse
 import json
@@ -337,26 +340,33 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
         y = torch.empty(P, H, device=dev)
         state = {"i": 0}
 
-        def layer(st, overlap, layout=LAYOUT_TILED):
+        def layer(st, overlap=None, layout=LAYOUT_TILED, pair_walk=None):
             c = copies[layout][state["i"] % 3]
             state["i"] += 1
             ops.moe_layer(logits, sg, x, hres, y, c["ptbl"], c["ptbl_dn"], c["ptbl_sh"], iq4nl, sc, stream=st,
-                          overlap_shared=overlap, layout=layout)
+                          overlap_shared=overlap, layout=layout, pair_walk=pair_walk)
 
-        t_seq = time_graph(lambda st: layer(st, False), steps, warmup, torch)
-        t_raw = time_graph(lambda st: layer(st, True, LAYOUT_RAW), steps, warmup, torch)
-        t = time_graph(lambda st: layer(st, True), steps, warmup, torch)
-        hit = int((torch.diff(sc.eoff) > 0).sum().item())
+        walk = P <= ops.MOE_PAIR_WALK_MAX_P   # the layer's defaults: pair walk, shared expert on one stream
+        t_other = time_graph(lambda st: layer(st, walk), steps, warmup, torch)
+        t_raw = time_graph(lambda st: layer(st, None, LAYOUT_RAW), steps, warmup, torch)
+        t_grouped = time_graph(lambda st: layer(st, False, pair_walk=False), steps, warmup, torch) if walk else None
+        t = time_graph(lambda st: layer(st), steps, warmup, torch)
+        hit = int(torch.unique(sc.eids).numel())
         flops = 2.0 * 3 * F * H * (8 * P + P)
         wbytes = (hit + 1) * 1671168
         tflops = flops / (t * 1e-3) / 1e12
         gbs = wbytes / (t * 1e-3) / 1e9
-        out[f"M{P}"] = {"ms": round(t, 4), "tflops": round(tflops, 2),
+        route = ("top-8, pair walk (no sort), shared expert on the same stream" if walk else
+                 "top-8, sort, grouped expert GEMMs, shared expert on a second stream")
+        out[f"M{P}"] = {"ms": round(t, 4), "tflops": round(tflops, 2), "route": route,
                         "experts_hit": hit, "weight_gbs": round(gbs, 1),
-                        "ms_shared_not_overlapped": round(t_seq, 4), "ms_gguf_row_slabs": round(t_raw, 4),
-                        "roofline": (hbm_roofline(gbs, "MoE layer (7 launches, graph): expert weight bytes / layer time")
+                        "ms_other_shared_stream": round(t_other, 4), "ms_gguf_row_slabs": round(t_raw, 4),
+                        **({"ms_sorted_grouped": round(t_grouped, 4)} if walk else {}),
+                        "roofline": (hbm_roofline(gbs, f"MoE layer ({route}, combine; graph): "
+                                                       "expert weight bytes / layer time")
                                      if P <= 64 else
-                                     mfma_roofline(tflops, "MoE layer (7 launches, graph): 2*3*512*2048*9*M / layer time"))}
+                                     mfma_roofline(tflops, f"MoE layer ({route}, combine; graph): "
+                                                           "2*3*512*2048*9*M / layer time"))}
     return out
 
 

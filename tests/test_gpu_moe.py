@@ -283,9 +283,12 @@ def test_moe_pair_walk_equals_grouped(gpu, experts, P):
 def test_moe_layer_overlapped_equals_sequential(gpu, experts):
     """ops.moe_layer with the shared expert on a second stream gives the sequential calls'
     results bit for bit, eagerly and in every replay of a captured graph (eager work and
-    synchronizations between the replays)."""
+    synchronizations between the replays); at P = 11 with its defaults there (the pair walk, one
+    stream) and with the shared expert on the second stream beside the pair walk and beside the
+    sorted, grouped forms; at P = 300 with its defaults there (grouped, second stream)."""
     print("[case] moe_layer overlapped vs sequential P=11 / 300", flush=True)
-    for P in (11, 300):
+    for P, pw, ov in ((11, None, None), (11, True, True), (11, False, True), (300, None, None)):
+        print(f"[case] moe_layer P={P} pair_walk={pw} overlap={ov}", flush=True)
         rng = np.random.default_rng(31 + P)
         x, logits, sg, hres = _inputs(rng, P)
         ref = _run_layer(gpu, experts, x, logits, sg, hres)
@@ -294,18 +297,18 @@ def test_moe_layer_overlapped_equals_sequential(gpu, experts):
         sc = ops.MoeScratch(P, gpu)
         y = torch.empty(P, moe.HID, dtype=torch.float32, device=gpu)
         args = (dl, dsg, dx, dh, y, experts["ptbl"], experts["ptbl_dn"], experts["ptbl_sh"], experts["iq4nl"], sc)
-        ops.moe_layer(*args)
+        ops.moe_layer(*args, pair_walk=pw, overlap_shared=ov)
         torch.cuda.synchronize()
         assert np.array_equal(y.cpu().numpy(), ref["y"])
         st = torch.cuda.Stream()
         st.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(st):
-            ops.moe_layer(*args, stream=st)
+            ops.moe_layer(*args, stream=st, pair_walk=pw, overlap_shared=ov)
         torch.cuda.current_stream().wait_stream(st)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=st):
-            ops.moe_layer(*args, stream=st)
+            ops.moe_layer(*args, stream=st, pair_walk=pw, overlap_shared=ov)
         for _ in range(3):
             y.zero_()
             torch.cuda.synchronize()

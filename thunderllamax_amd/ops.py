@@ -672,16 +672,31 @@ class MoeScratch:
 
 _SIDE_STREAMS = {}
 
+# Largest batch the MoE layer routes with the pair-walk forms by default: up to here the sort
+# launch it skips costs more than the expert slabs that two pairs of the batch share and the
+# pair walk reads twice.
+MOE_PAIR_WALK_MAX_P = 16
 
-def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, stream=None, overlap_shared=True,
-              layout=LAYOUT_RAW):
+
+def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, stream=None, overlap_shared=None,
+              layout=LAYOUT_RAW, pair_walk=None):
     """One MoE layer, the sequence of build_seq7 (engine/mm/MM_P7_lib.py:449-511): top-8 from
-    the router logits, sort, grouped gate+up, grouped down, shared expert, combine into y.
-    With overlap_shared the shared expert (which needs neither the routing nor the routed
-    experts) runs on a second stream, joined before the combine; the work and the results are
-    the same, and a graph captured from the call keeps the two branches concurrent.  layout: the
-    expert slabs' (all of them, shared expert included)."""
+    the router logits, then either the grouped path (sort, grouped gate+up, grouped down:
+    the reference's prefill sequence, :451-499) or the pair walk (gate+up and down per pair on
+    the router's ids, no sort: its decode sequence, :501-507), the shared expert, and the
+    combine into y.  Both give the same bits.  pair_walk None picks the pair walk for
+    P <= MOE_PAIR_WALK_MAX_P.  With overlap_shared the shared expert (which needs neither the
+    routing nor the routed experts) runs on a second stream, joined before the combine; the work
+    and the results are the same, and a graph captured from the call keeps the two branches
+    concurrent.  overlap_shared None overlaps on the grouped path only: at pair-walk sizes the
+    shared expert's two small launches take less time than the fork and join of the second
+    stream add to a graph replay.  layout: the expert slabs' (all of them, shared expert
+    included)."""
     sc = scratch
+    if pair_walk is None:
+        pair_walk = xs.shape[0] <= MOE_PAIR_WALK_MAX_P
+    if overlap_shared is None:
+        overlap_shared = not pair_walk
     cur = stream if isinstance(stream, torch.cuda.Stream) else torch.cuda.current_stream()
     side = None
     if overlap_shared:
@@ -691,9 +706,14 @@ def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, s
         side.wait_stream(cur)
         moe_shared(ptbl_sh, xs, iq4nl, sc.sact, sc.shared, stream=side, layout=layout)
     moe_topk(logits, sc.eids, sc.gates, stream=cur)
-    moe_sort(sc.eids, sc.eoff, sc.plist, sc.items, sc.nitp, stream=cur)
-    moe_up4(ptbl, sc.items, sc.nitp, sc.eoff, sc.plist, xs, iq4nl, sc.act, stream=cur, layout=layout)
-    moe_dn4(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, iq4nl, sc.parts, stream=cur, layout=layout)
+    if pair_walk:
+        eids = sc.eids.view(-1)
+        moe_up4_pairs(ptbl, eids, xs, iq4nl, sc.act, stream=cur, layout=layout)
+        moe_dn4_pairs(ptbl_dn, eids, sc.act, iq4nl, sc.parts, stream=cur, layout=layout)
+    else:
+        moe_sort(sc.eids, sc.eoff, sc.plist, sc.items, sc.nitp, stream=cur)
+        moe_up4(ptbl, sc.items, sc.nitp, sc.eoff, sc.plist, xs, iq4nl, sc.act, stream=cur, layout=layout)
+        moe_dn4(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, iq4nl, sc.parts, stream=cur, layout=layout)
     if side is None:
         moe_shared(ptbl_sh, xs, iq4nl, sc.sact, sc.shared, stream=cur, layout=layout)
     else:
