@@ -49,8 +49,8 @@ followed by ffn8, and fused with it in one entry point (graph replays).
 matrix -> packed rows -> packed7) in GB/s of bytes read + written.
 
 ``moe`` is config 5: the whole MoE layer at M=11 and M=2048 as ``ops.moe_layer`` runs it by
-default -- M=11: top-8 from N(0,1) logits, the pair-walk IQ4_XS gate+up and down (no sort),
-shared expert, combine, all on one stream; M=2048: top-8, sort, grouped gate+up and down, the
+default -- M=11: top-8 from N(0,1) logits, the pair-walk IQ4_XS gate+up and down (no sort)
+with the shared expert's chunks in the same two launches, combine, all on one stream; M=2048: top-8, sort, grouped gate+up and down, the
 shared expert on a second stream, combine -- seeded expert weights, the layer's launches per
 step captured in one HIP graph (``ms_other_shared_stream``: the shared expert on the other
 choice of stream; ``ms_sorted_grouped`` at M=11: the grouped route); each step reads a
@@ -356,7 +356,7 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
         wbytes = (hit + 1) * 1671168
         tflops = flops / (t * 1e-3) / 1e12
         gbs = wbytes / (t * 1e-3) / 1e9
-        route = ("top-8, pair walk (no sort), shared expert on the same stream" if walk else
+        route = ("top-8, pair walk (no sort) with the shared expert in its two launches" if walk else
                  "top-8, sort, grouped expert GEMMs, shared expert on a second stream")
         out[f"M{P}"] = {"ms": round(t, 4), "tflops": round(tflops, 2), "route": route,
                         "experts_hit": hit, "weight_gbs": round(gbs, 1),

@@ -362,6 +362,19 @@ int tlx_moe_up4_pairs(const uint64_t* ptbl, const uint16_t* eids, const float* x
 int tlx_moe_dn4_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, const float* iq4nl,
                       uint16_t* parts, int np, int layout, void* stream);
 
+/* The pair walk with the shared expert in the same launch (decode sizes: one launch per
+ * projection instead of two).  No counterpart among the reference's entry points: its fused
+ * decode sequence (engine/mm/MM_P7_lib.py:436-448, MM_FUSE2) merges launches of this layer the
+ * same way.  P positions, 8 P pairs: tlx_moe_up4_pairs over the pairs plus tlx_moe_shared's
+ * gate+up (ptbl_sh[0], into sact[P][512]); tlx_moe_dn4_pairs over the pairs plus the shared
+ * down projection (ptbl_sh_dn[0] = the shared down slab, sact into shared[P][2048] f32).  The
+ * outputs are those of the separate calls bit for bit.  sact and shared 16-B aligned. */
+int tlx_moe_up4_pairs_sh(const uint64_t* ptbl, const uint16_t* eids, const float* xs, const float* iq4nl,
+                         float* ys, const uint64_t* ptbl_sh, float* sact, int P, int layout, void* stream);
+int tlx_moe_dn4_pairs_sh(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, const float* iq4nl,
+                         uint16_t* parts, const uint64_t* ptbl_sh_dn, const float* sact, float* shared, int P,
+                         int layout, void* stream);
+
 /* Shared expert over all P positions: act[P][512] (caller scratch) then out[P][2048] f32.
  * ptbl_sh = {gate/up slab, down slab}.  Replaces shgu32 / shdn32 (engine/mm/MM_P2_ports.py:195-201
  * restates them) with the IQ4_XS weights of the benchmark's MoE configuration. */

@@ -84,7 +84,8 @@ def _run_layer(gpu, ex, x, logits, sg, hres, layout=LAYOUT_RAW):
     ops.moe_combine(parts, gates, torch.from_numpy(sg).to(gpu), shared, torch.from_numpy(hres).to(gpu), y)
     torch.cuda.synchronize()
     return {k: v.cpu().numpy() for k, v in dict(eids=eids, gates=gates, eoff=eoff, plist=plist, items=items,
-                                                   nitp=nitp, act=act, parts=parts, shared=shared, y=y).items()}
+                                                   nitp=nitp, act=act, parts=parts, sact=sact, shared=shared,
+                                                   y=y).items()}
 
 
 def _inputs(rng, P):
@@ -278,6 +279,34 @@ def test_moe_pair_walk_equals_grouped(gpu, experts, P):
     torch.cuda.synchronize()
     assert np.array_equal(act.cpu().numpy(), a["act"])
     assert np.array_equal(parts.cpu().numpy(), a["parts"])
+
+
+@pytest.mark.parametrize("P", [1, 11, 70])
+@pytest.mark.parametrize("lay", ["raw", "tiled"])
+def test_moe_pair_walk_with_shared_expert(gpu, experts, experts_tiled, P, lay):
+    """The fused decode launches (pair walk + the shared expert's chunks in one grid) give the
+    separate calls' act, parts, shared activations and shared output bit for bit (P = 70: two
+    shared chunks of 64 and 6 positions)."""
+    print(f"[case] moe pair walk + shared P={P} {lay}", flush=True)
+    ex, layout = (experts, LAYOUT_RAW) if lay == "raw" else (experts_tiled, LAYOUT_TILED)
+    rng = np.random.default_rng(60 + P)
+    x, logits, sg, hres = _inputs(rng, P)
+    a = _run_layer(gpu, ex, x, logits, sg, hres, layout=layout)
+    np_ = 8 * P
+    eids = torch.from_numpy(a["eids"].reshape(-1)).to(gpu)
+    act = torch.full((np_, moe.FF), float("nan"), dtype=torch.float32, device=gpu)
+    sact = torch.full((P, moe.FF), float("nan"), dtype=torch.float32, device=gpu)
+    ops.moe_up4_pairs_sh(ex["ptbl"], eids, torch.from_numpy(x).to(gpu), ex["iq4nl"], act, ex["ptbl_sh"][0:1], sact,
+                         layout=layout)
+    parts = torch.full((np_, moe.HID), float("nan"), dtype=torch.float16, device=gpu)
+    shared = torch.full((P, moe.HID), float("nan"), dtype=torch.float32, device=gpu)
+    ops.moe_dn4_pairs_sh(ex["ptbl_dn"], eids, act, ex["iq4nl"], parts, ex["ptbl_sh"][1:2], sact, shared,
+                         layout=layout)
+    torch.cuda.synchronize()
+    assert np.array_equal(act.cpu().numpy(), a["act"])
+    assert np.array_equal(sact.cpu().numpy(), a["sact"])
+    assert np.array_equal(parts.cpu().numpy(), a["parts"])
+    assert np.array_equal(shared.cpu().numpy(), a["shared"])
 
 
 def test_moe_layer_overlapped_equals_sequential(gpu, experts):

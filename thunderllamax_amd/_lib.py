@@ -80,6 +80,8 @@ SIGNATURES = {
     "tlx_moe_up4_pairs": [_p, _p, _p, _p, _p, _i, _i, _p],
     "tlx_moe_dn4_pairs": [_p, _p, _p, _p, _p, _i, _i, _p],
     "tlx_moe_shared": [_p, _p, _p, _p, _p, _i, _i, _p],
+    "tlx_moe_up4_pairs_sh": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _p],
+    "tlx_moe_dn4_pairs_sh": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _p],
     "tlx_pack_iq4_tiled": [_p, _p, _i, _i, _p],
     "tlx_moe_combine": [_p, _p, _p, _p, _p, _p, _i, _p],
     "tlx_stream_chunk_bytes": [],

@@ -941,13 +941,20 @@ __device__ __forceinline__ void moe_gv_tile(gbyte* base, const uint32_t* lut, co
   }
 }
 
+// Modes: dense (the shared expert, KIND *_DENSE: chunks of kTok positions); pair walk (eids:
+// workgroup column x is pair x); pair walk fused with the shared expert (eids and ptbl_sh: columns
+// x < 8 P are pairs, the rest the shared expert's chunks, which read xs_sh and write out_sh with
+// the dense kind's epilogue); grouped (the sort's items).
 template <int KIND, bool TL>
 __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff,
                                                      const uint16_t* __restrict__ plist,
                                                      const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp,
                                                      const uint16_t* __restrict__ eids, const float* __restrict__ xs,
-                                                     const float* __restrict__ iq4nl, void* __restrict__ out, int P) {
+                                                     const float* __restrict__ iq4nl, void* __restrict__ out, int P,
+                                                     const uint64_t* __restrict__ ptbl_sh, const float* __restrict__ xs_sh,
+                                                     void* __restrict__ out_sh) {
   constexpr bool kDense = KIND == MOE_DN_DENSE || KIND == MOE_UP_DENSE;
+  constexpr int KD = KIND == MOE_UP ? MOE_UP_DENSE : KIND == MOE_DN ? MOE_DN_DENSE : KIND;   // the dense kind
   constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
   constexpr int NMAT = kUp ? 2 : 1;
   constexpr int kTpw = 4 / moe_gv_wpt<KIND>();    // tiles per workgroup
@@ -966,7 +973,15 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
 
   int m0, ntok;
   gbyte* base;
-  if constexpr (kDense) {
+  // a shared-expert chunk of the fused pair walk (workgroup-uniform)
+  const bool shc = !kDense && eids && ptbl_sh && (int)blockIdx.x >= 8 * P;
+  if (shc) {
+    m0 = ((int)blockIdx.x - 8 * P) * kTok;
+    ntok = min(kTok, P - m0);
+    base = (gbyte*)(ptbl_sh[0]);
+    xs = xs_sh;
+    out = out_sh;
+  } else if constexpr (kDense) {
     m0 = (int)blockIdx.x * kTok;
     ntok = min(kTok, P - m0);
     base = (gbyte*)(ptbl[0]);
@@ -986,7 +1001,7 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
   }
   if (t < kTok) {
     const int slot = min(t, ntok - 1);
-    if constexpr (kDense) {
+    if (kDense || shc) {
       xrow[t] = m0 + slot;
       orow[t] = m0 + slot;
     } else if (eids) {
@@ -1018,6 +1033,20 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
     __syncthreads();
   }
   const int tile = (int)blockIdx.y * kTpw + wave / moe_gv_wpt<KIND>();   // 16-row output tile
+  if constexpr (KD != KIND) {
+    if (shc) {   // the dense kind's tile (the down projection's epilogue differs: f32 out)
+      switch ((ntok + 15) >> 4) {
+        case 1:
+          if (staged) moe_gv_tile<KD, 1, TL, true>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane);
+          else moe_gv_tile<KD, 1, TL, false>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane);
+          break;
+        case 2: moe_gv_tile<KD, 2, TL, false>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane); break;
+        case 3: moe_gv_tile<KD, 3, TL, false>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane); break;
+        default: moe_gv_tile<KD, 4, TL, false>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane); break;
+      }
+      return;
+    }
+  }
   switch ((ntok + 15) >> 4) {   // workgroup-uniform
     case 1:
       if (staged) moe_gv_tile<KIND, 1, TL, true>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane);
@@ -1102,11 +1131,14 @@ dim3 moe_gv_grid(int nx) {
 template <int KIND>
 void moe_gv_launch(bool tl, dim3 grid, hipStream_t st, const uint64_t* ptbl, const int* eoff, const uint16_t* plist,
                    const uint32_t* items, const uint32_t* nitp, const uint16_t* eids, const float* xs,
-                   const float* iq4nl, void* out, int P) {
+                   const float* iq4nl, void* out, int P, const uint64_t* ptbl_sh = nullptr,
+                   const float* xs_sh = nullptr, void* out_sh = nullptr) {
   if (tl)
-    moe_gv_kernel<KIND, true><<<grid, 256, 0, st>>>(ptbl, eoff, plist, items, nitp, eids, xs, iq4nl, out, P);
+    moe_gv_kernel<KIND, true><<<grid, 256, 0, st>>>(ptbl, eoff, plist, items, nitp, eids, xs, iq4nl, out, P, ptbl_sh,
+                                                     xs_sh, out_sh);
   else
-    moe_gv_kernel<KIND, false><<<grid, 256, 0, st>>>(ptbl, eoff, plist, items, nitp, eids, xs, iq4nl, out, P);
+    moe_gv_kernel<KIND, false><<<grid, 256, 0, st>>>(ptbl, eoff, plist, items, nitp, eids, xs, iq4nl, out, P, ptbl_sh,
+                                                      xs_sh, out_sh);
 }
 
 template <int KIND>
@@ -1176,6 +1208,28 @@ extern "C" int tlx_moe_dn4_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, 
   TLX_RET_IF(!tlx_aligned(act, 16) || !tlx_aligned(parts, 16), TLX_E_ALIGN);
   moe_gv_launch<MOE_DN>(layout == TLX_LAYOUT_TILED, moe_gv_grid<MOE_DN>(np), (hipStream_t)stream, ptbl_dn, nullptr,
                         nullptr, nullptr, nullptr, eids, act, iq4nl, parts, 0);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_moe_up4_pairs_sh(const uint64_t* ptbl, const uint16_t* eids, const float* xs, const float* iq4nl,
+                                    float* ys, const uint64_t* ptbl_sh, float* sact, int P, int layout, void* stream) {
+  TLX_RET_IF(P < 1 || 8 * P > kMaxPairs || !moe_layout_ok(layout), TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(xs, 16) || !tlx_aligned(sact, 16), TLX_E_ALIGN);
+  const dim3 g = moe_gv_grid<MOE_UP>(8 * P + (P + kTok - 1) / kTok);
+  moe_gv_launch<MOE_UP>(layout == TLX_LAYOUT_TILED, g, (hipStream_t)stream, ptbl, nullptr, nullptr, nullptr, nullptr,
+                        eids, xs, iq4nl, ys, P, ptbl_sh, xs, sact);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_moe_dn4_pairs_sh(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act,
+                                    const float* iq4nl, uint16_t* parts, const uint64_t* ptbl_sh_dn, const float* sact,
+                                    float* shared, int P, int layout, void* stream) {
+  TLX_RET_IF(P < 1 || 8 * P > kMaxPairs || !moe_layout_ok(layout), TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(act, 16) || !tlx_aligned(parts, 16) || !tlx_aligned(sact, 16) || !tlx_aligned(shared, 16),
+             TLX_E_ALIGN);
+  const dim3 g = moe_gv_grid<MOE_DN>(8 * P + (P + kTok - 1) / kTok);
+  moe_gv_launch<MOE_DN>(layout == TLX_LAYOUT_TILED, g, (hipStream_t)stream, ptbl_dn, nullptr, nullptr, nullptr, nullptr,
+                        eids, act, iq4nl, parts, P, ptbl_sh_dn, sact, shared);
   return tlx_launch_status();
 }
 

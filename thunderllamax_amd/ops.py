@@ -625,6 +625,41 @@ def moe_dn4_pairs(ptbl_dn, eids, act, iq4nl, parts, stream=None, layout=LAYOUT_R
          parts.data_ptr(), n, layout, _stream(stream))
 
 
+def moe_up4_pairs_sh(ptbl, eids, xs, iq4nl, ys, ptbl_sh, sact, stream=None, layout=LAYOUT_RAW):
+    """moe_up4_pairs and the shared expert's gate+up (ptbl_sh[0] into sact [P][512]) in one
+    launch; P = xs.shape[0], eids / ys over the 8 P pairs."""
+    P = xs.shape[0]
+    n = 8 * P
+    _need(ptbl, 256 * 8, "ptbl")
+    _need(ptbl_sh, 8, "ptbl_sh")
+    _need(eids, n * 2, "eids")
+    _need(xs, P * 2048 * 4, "xs")
+    _need(ys, n * 512 * 4, "ys")
+    _need(sact, P * 512 * 4, "sact")
+    _need(iq4nl, 64, "iq4nl")
+    _dev(ptbl, ptbl_sh, eids, xs, iq4nl, ys, sact)
+    call("tlx_moe_up4_pairs_sh", ptbl.data_ptr(), eids.data_ptr(), xs.data_ptr(), iq4nl.data_ptr(), ys.data_ptr(),
+         ptbl_sh.data_ptr(), sact.data_ptr(), P, layout, _stream(stream))
+
+
+def moe_dn4_pairs_sh(ptbl_dn, eids, act, iq4nl, parts, ptbl_sh_dn, sact, shared, stream=None, layout=LAYOUT_RAW):
+    """moe_dn4_pairs and the shared expert's down projection (ptbl_sh_dn[0], sact [P][512] into
+    shared [P][2048] f32) in one launch; P = sact.shape[0], act / parts over the 8 P pairs."""
+    P = sact.shape[0]
+    n = 8 * P
+    _need(ptbl_dn, 256 * 8, "ptbl_dn")
+    _need(ptbl_sh_dn, 8, "ptbl_sh_dn")
+    _need(eids, n * 2, "eids")
+    _need(act, n * 512 * 4, "act")
+    _need(parts, n * 2048 * 2, "parts")
+    _need(sact, P * 512 * 4, "sact")
+    _need(shared, P * 2048 * 4, "shared")
+    _need(iq4nl, 64, "iq4nl")
+    _dev(ptbl_dn, ptbl_sh_dn, eids, act, iq4nl, parts, sact, shared)
+    call("tlx_moe_dn4_pairs_sh", ptbl_dn.data_ptr(), eids.data_ptr(), act.data_ptr(), iq4nl.data_ptr(),
+         parts.data_ptr(), ptbl_sh_dn.data_ptr(), sact.data_ptr(), shared.data_ptr(), P, layout, _stream(stream))
+
+
 def moe_shared(ptbl_sh, xs, iq4nl, act, out, stream=None, layout=LAYOUT_RAW):
     """Shared expert over all positions: act [P][512] (scratch), out [P][2048] f32."""
     P = xs.shape[0]
@@ -689,9 +724,10 @@ def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, s
     routing nor the routed experts) runs on a second stream, joined before the combine; the work
     and the results are the same, and a graph captured from the call keeps the two branches
     concurrent.  overlap_shared None overlaps on the grouped path only: at pair-walk sizes the
-    shared expert's two small launches take less time than the fork and join of the second
-    stream add to a graph replay.  layout: the expert slabs' (all of them, shared expert
-    included)."""
+    shared expert's work is small against what the fork and join of the second stream add to a
+    graph replay, and on one stream it rides in the pair walk's two launches
+    (moe_up4_pairs_sh / moe_dn4_pairs_sh).  layout: the expert slabs' (all of them, shared
+    expert included)."""
     sc = scratch
     if pair_walk is None:
         pair_walk = xs.shape[0] <= MOE_PAIR_WALK_MAX_P
@@ -706,6 +742,13 @@ def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, s
         side.wait_stream(cur)
         moe_shared(ptbl_sh, xs, iq4nl, sc.sact, sc.shared, stream=side, layout=layout)
     moe_topk(logits, sc.eids, sc.gates, stream=cur)
+    if pair_walk and side is None:   # the shared expert rides in the pair walk's launches
+        eids = sc.eids.view(-1)
+        moe_up4_pairs_sh(ptbl, eids, xs, iq4nl, sc.act, ptbl_sh[0:1], sc.sact, stream=cur, layout=layout)
+        moe_dn4_pairs_sh(ptbl_dn, eids, sc.act, iq4nl, sc.parts, ptbl_sh[1:2], sc.sact, sc.shared, stream=cur,
+                         layout=layout)
+        moe_combine(sc.parts, sc.gates, sg, sc.shared, hres, y, stream=cur)
+        return y
     if pair_walk:
         eids = sc.eids.view(-1)
         moe_up4_pairs(ptbl, eids, xs, iq4nl, sc.act, stream=cur, layout=layout)
