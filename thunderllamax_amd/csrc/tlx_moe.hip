@@ -187,7 +187,8 @@ constexpr int kTok = 64;         // item size of the GEMV form, and its dense (s
 constexpr int kDenseTok = 32;    // the GEMM form's dense chunk: 2 groups, so the shared expert's
                                  // grids fill the GPU beside the router and the sort
 constexpr int kPfTok = 96;       // item size of the GEMM form: up to 6 groups of 16 tokens
-constexpr int kGvMaxPairs = 2048;   // pair counts up to this use the GEMV form, larger ones the GEMM
+constexpr int kGvMaxPairs = 2048;
+constexpr int kShTok = 16;          // positions per shared-expert chunk of the fused pair walk   // pair counts up to this use the GEMV form, larger ones the GEMM
 constexpr int kSortChunk = 256;     // pairs per sort workgroup (4 waves of 64)
 
 // pairs per work item: the GEMV form takes up to 64, the GEMM form 96 (at uniform routing over 256
@@ -975,9 +976,9 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
   gbyte* base;
   // a shared-expert chunk of the fused pair walk (workgroup-uniform)
   const bool shc = !kDense && eids && ptbl_sh && (int)blockIdx.x >= 8 * P;
-  if (shc) {
-    m0 = ((int)blockIdx.x - 8 * P) * kTok;
-    ntok = min(kTok, P - m0);
+  if (shc) {   // chunks of kShTok positions: one token group, the pair walk's register budget
+    m0 = ((int)blockIdx.x - 8 * P) * kShTok;
+    ntok = min(kShTok, P - m0);
     base = (gbyte*)(ptbl_sh[0]);
     xs = xs_sh;
     out = out_sh;
@@ -1033,17 +1034,10 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
     __syncthreads();
   }
   const int tile = (int)blockIdx.y * kTpw + wave / moe_gv_wpt<KIND>();   // 16-row output tile
-  if constexpr (KD != KIND) {
+  if constexpr (KIND == MOE_DN) {   // gate+up: the dense kind's tile is the routed one's code
     if (shc) {   // the dense kind's tile (the down projection's epilogue differs: f32 out)
-      switch ((ntok + 15) >> 4) {
-        case 1:
-          if (staged) moe_gv_tile<KD, 1, TL, true>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane);
-          else moe_gv_tile<KD, 1, TL, false>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane);
-          break;
-        case 2: moe_gv_tile<KD, 2, TL, false>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane); break;
-        case 3: moe_gv_tile<KD, 3, TL, false>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane); break;
-        default: moe_gv_tile<KD, 4, TL, false>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane); break;
-      }
+      if (staged) moe_gv_tile<KD, 1, TL, true>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane);
+      else moe_gv_tile<KD, 1, TL, false>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane);
       return;
     }
   }
@@ -1215,7 +1209,7 @@ extern "C" int tlx_moe_up4_pairs_sh(const uint64_t* ptbl, const uint16_t* eids, 
                                     float* ys, const uint64_t* ptbl_sh, float* sact, int P, int layout, void* stream) {
   TLX_RET_IF(P < 1 || 8 * P > kMaxPairs || !moe_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(xs, 16) || !tlx_aligned(sact, 16), TLX_E_ALIGN);
-  const dim3 g = moe_gv_grid<MOE_UP>(8 * P + (P + kTok - 1) / kTok);
+  const dim3 g = moe_gv_grid<MOE_UP>(8 * P + (P + kShTok - 1) / kShTok);
   moe_gv_launch<MOE_UP>(layout == TLX_LAYOUT_TILED, g, (hipStream_t)stream, ptbl, nullptr, nullptr, nullptr, nullptr,
                         eids, xs, iq4nl, ys, P, ptbl_sh, xs, sact);
   return tlx_launch_status();
@@ -1227,7 +1221,7 @@ extern "C" int tlx_moe_dn4_pairs_sh(const uint64_t* ptbl_dn, const uint16_t* eid
   TLX_RET_IF(P < 1 || 8 * P > kMaxPairs || !moe_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(act, 16) || !tlx_aligned(parts, 16) || !tlx_aligned(sact, 16) || !tlx_aligned(shared, 16),
              TLX_E_ALIGN);
-  const dim3 g = moe_gv_grid<MOE_DN>(8 * P + (P + kTok - 1) / kTok);
+  const dim3 g = moe_gv_grid<MOE_DN>(8 * P + (P + kShTok - 1) / kShTok);
   moe_gv_launch<MOE_DN>(layout == TLX_LAYOUT_TILED, g, (hipStream_t)stream, ptbl_dn, nullptr, nullptr, nullptr, nullptr,
                         eids, act, iq4nl, parts, P, ptbl_sh_dn, sact, shared);
   return tlx_launch_status();
