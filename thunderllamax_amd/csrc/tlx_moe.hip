@@ -953,7 +953,10 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
                                                      const uint16_t* __restrict__ eids, const float* __restrict__ xs,
                                                      const float* __restrict__ iq4nl, void* __restrict__ out, int P,
                                                      const uint64_t* __restrict__ ptbl_sh, const float* __restrict__ xs_sh,
-                                                     void* __restrict__ out_sh) {
+                                                     void* __restrict__ out_sh, int swap) {
+  // workgroup column (item, pair or chunk) and row (output tile group): swapped grids dispatch an
+  // item's tile groups one after another (consecutive workgroups stream one expert slab)
+  const uint32_t bx = swap ? blockIdx.y : blockIdx.x, by = swap ? blockIdx.x : blockIdx.y;
   constexpr bool kDense = KIND == MOE_DN_DENSE || KIND == MOE_UP_DENSE;
   constexpr int KD = KIND == MOE_UP ? MOE_UP_DENSE : KIND == MOE_DN ? MOE_DN_DENSE : KIND;   // the dense kind
   constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
@@ -975,24 +978,24 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
   int m0, ntok;
   gbyte* base;
   // a shared-expert chunk of the fused pair walk (workgroup-uniform)
-  const bool shc = !kDense && eids && ptbl_sh && (int)blockIdx.x >= 8 * P;
+  const bool shc = !kDense && eids && ptbl_sh && (int)bx >= 8 * P;
   if (shc) {   // chunks of kShTok positions: one token group, the pair walk's register budget
-    m0 = ((int)blockIdx.x - 8 * P) * kShTok;
+    m0 = ((int)bx - 8 * P) * kShTok;
     ntok = min(kShTok, P - m0);
     base = (gbyte*)(ptbl_sh[0]);
     xs = xs_sh;
     out = out_sh;
   } else if constexpr (kDense) {
-    m0 = (int)blockIdx.x * kTok;
+    m0 = (int)bx * kTok;
     ntok = min(kTok, P - m0);
     base = (gbyte*)(ptbl[0]);
   } else if (eids) {   // pair walk: workgroup column x is pair x, expert eids[x], no sort
-    m0 = (int)blockIdx.x;
+    m0 = (int)bx;
     ntok = 1;
     base = (gbyte*)(ptbl[eids[m0]]);
   } else {
-    if (blockIdx.x >= *nitp) return;
-    const uint32_t it = items[blockIdx.x];
+    if (bx >= *nitp) return;
+    const uint32_t it = items[bx];
     const int e = (int)(it >> 16);
     m0 = (int)(it & 0xFFFFu);
     const int eb0 = eoff[e];
@@ -1033,7 +1036,7 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
     }
     __syncthreads();
   }
-  const int tile = (int)blockIdx.y * kTpw + wave / moe_gv_wpt<KIND>();   // 16-row output tile
+  const int tile = (int)by * kTpw + wave / moe_gv_wpt<KIND>();   // 16-row output tile
   if constexpr (KIND == MOE_DN) {   // gate+up: the dense kind's tile is the routed one's code
     if (shc) {   // the dense kind's tile (the down projection's epilogue differs: f32 out)
       if (staged) moe_gv_tile<KD, 1, TL, true>(base, lut, xrow, orow, red, xst, xs, out, ntok, tile, wave, lane);
@@ -1114,11 +1117,14 @@ int moe_gv_items(int np) { return min(np, moe_max_items(np)); }
 template <int KIND>
 int moe_pf_grid(int nitems) { return (nitems + 7) / 8 * 8 * moe_pf_stripes<KIND>(); }
 
+// Grids of at least kGvSwapCols columns run swapped (measured: at 2048 pairs both projections
+// 17% faster; at decode widths the column-major order is as fast or faster).
+constexpr int kGvSwapCols = 128;
 template <int KIND>
 dim3 moe_gv_grid(int nx) {
   constexpr int kWpt = moe_gv_wpt<KIND>(), kTpw = 4 / kWpt;
   constexpr int kRows = (KIND == MOE_UP || KIND == MOE_UP_DENSE) ? kFf : kHid;
-  return dim3(nx, kRows / 16 / kTpw);
+  return nx >= kGvSwapCols ? dim3(kRows / 16 / kTpw, nx) : dim3(nx, kRows / 16 / kTpw);
 }
 
 // launch helpers: the layout picks the kernel instantiation (GGUF rows or tiled records)
@@ -1127,12 +1133,14 @@ void moe_gv_launch(bool tl, dim3 grid, hipStream_t st, const uint64_t* ptbl, con
                    const uint32_t* items, const uint32_t* nitp, const uint16_t* eids, const float* xs,
                    const float* iq4nl, void* out, int P, const uint64_t* ptbl_sh = nullptr,
                    const float* xs_sh = nullptr, void* out_sh = nullptr) {
+  constexpr int kTiles = ((KIND == MOE_UP || KIND == MOE_UP_DENSE) ? kFf : kHid) / 16 / (4 / moe_gv_wpt<KIND>());
+  const int swap = grid.x == (unsigned)kTiles && grid.y >= (unsigned)kGvSwapCols;
   if (tl)
     moe_gv_kernel<KIND, true><<<grid, 256, 0, st>>>(ptbl, eoff, plist, items, nitp, eids, xs, iq4nl, out, P, ptbl_sh,
-                                                     xs_sh, out_sh);
+                                                     xs_sh, out_sh, swap);
   else
     moe_gv_kernel<KIND, false><<<grid, 256, 0, st>>>(ptbl, eoff, plist, items, nitp, eids, xs, iq4nl, out, P, ptbl_sh,
-                                                      xs_sh, out_sh);
+                                                      xs_sh, out_sh, swap);
 }
 
 template <int KIND>
