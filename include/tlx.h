@@ -325,7 +325,7 @@ int tlx_moe_route(const float* wrt, const float* wsh, const float* h, uint16_t* 
 
 /* Deterministic stable sort of the np = 8P pairs by expert (eids 8-B aligned): eoff i32[257] (exclusive bin
  * offsets), plist u16[np] (pair ids, pair order inside a bin), items u32[tlx_moe_max_items(np)]
- * (expert << 16 | first pair in bin, one per 64 pairs for np <= 2048 and per 96 pairs above: the
+ * (expert << 16 | first pair in bin, one per 64 pairs for np <= 512 and per 96 pairs above: the
  * grouped GEMMs' forms), nitp u32[1] (item count).  np <= 16384.
  * Replaces mmsort8 (engine/mm/MM_B_mmsort8.cu:22-31): mmsort8(eids, eoff, plist, items, nitp, np);
  * eoff / plist are the reference's, the item granularity is this library's own. */
@@ -337,7 +337,7 @@ int tlx_moe_max_items(int np);
  * f32, pos = pair >> 3.  Replaces gxm_up4 (engine/mm/MM_B_gxm_up4.cu:20-28): gxm_up4(ptbl, items, nitp,
  * eoff, plist, xs f32[P][2048], iq4nlb f32[16], ys), same positional order; items / nitp are the
  * ones tlx_moe_sort wrote.  The fp16-MMA prefill form gxu_gm (engine/mm/MM_E_gxu_gm.cu:86-93) is
- * the same call: np > 2048 runs the MFMA grouped GEMM. */
+ * the same call: np > 512 runs the MFMA grouped GEMM. */
 int tlx_moe_up4(const uint64_t* ptbl, const uint32_t* items, const uint32_t* nitp, const int* eoff,
                 const uint16_t* plist, const float* xs, const float* iq4nl, float* ys, int np, int layout,
                 void* stream);
@@ -345,7 +345,7 @@ int tlx_moe_up4(const uint64_t* ptbl, const uint32_t* items, const uint32_t* nit
 /* Grouped down over the sorted pairs: parts[pair][2048] = fp16(Wd_e . act[pair]).
  * Replaces gxm_dn / gxm_dnf (engine/mm/MM_B_gxm_dn.cu:15-23, engine/mm/MM_C_gxm_dnf.cu:22):
  * gxm_dn(ptbl, items, nitp, eoff, plist, xs = act f32[NPAIR][512], iq4nlb, parts), same order;
- * np > 2048 runs the MFMA form (gxd_gm, engine/mm/MM_E_gxd_gm.cu:91-97). */
+ * np > 160 runs the MFMA form (gxd_gm, engine/mm/MM_E_gxd_gm.cu:91-97). */
 int tlx_moe_dn4(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
                 const uint16_t* plist, const float* act, const float* iq4nl, uint16_t* parts, int np,
                 int layout, void* stream);

@@ -158,7 +158,7 @@ def test_moe_sort(gpu, P):
     assert np.array_equal(eoff.cpu().numpy(), ref_off)
     assert np.array_equal(plist.cpu().numpy().view(np.uint16), ref_pl)
     cnt = np.diff(ref_off)
-    tok = 64 if np_ <= 2048 else 96   # pairs per item: the GEMV form's 64, the GEMM form's 96
+    tok = 64 if np_ <= 512 else 96   # pairs per item: 64 up to 512 pairs, 96 above
     want = [(e << 16) | k for e in range(moe.E) for k in range(0, int(cnt[e]), tok)]
     n = int(nitp.cpu().numpy()[0])
     assert n == len(want)
@@ -214,10 +214,11 @@ def test_moe_layer_prefill_m2048_sampled(gpu, experts):
 
 @pytest.mark.parametrize("P", [64, 256, 300])
 def test_moe_layer_skewed(gpu, experts, P):
-    """A router biased towards 12 experts gives them 2..4 groups of 16 tokens and several items
-    each (64 pairs in the GEMV form, 96 in the GEMM form; ragged last ones).  Pair counts up to
-    2048 (P = 64, 256) take the GEMV form, more
-    (P = 300) the prefill GEMM, whose shared expert then ends on a 12-position chunk."""
+    """A router biased towards 12 experts gives them 2..4 groups of 16 tokens, and from 96 pairs
+    on several items each (ragged last ones).  P = 64 (512 pairs): the gate+up GEMV form on 64-pair
+    items and the down projection's MFMA form on the same items; P = 256 and 300: the MFMA forms on
+    96-pair items, the shared expert in the GEMV form (P = 256) and in 32-position MFMA chunks
+    ending on a 12-position one (P = 300)."""
     print(f"[case] moe layer skewed P={P}", flush=True)
     rng = np.random.default_rng(24 + P)
     x, logits, sg, hres = _inputs(rng, P)
@@ -284,9 +285,10 @@ def test_moe_pair_walk_equals_grouped(gpu, experts, P):
 @pytest.mark.parametrize("P", [1, 11, 70])
 @pytest.mark.parametrize("lay", ["raw", "tiled"])
 def test_moe_pair_walk_with_shared_expert(gpu, experts, experts_tiled, P, lay):
-    """The fused decode launches (pair walk + the shared expert's chunks in one grid) give the
-    separate calls' act, parts, shared activations and shared output bit for bit (P = 70: two
-    shared chunks of 64 and 6 positions)."""
+    """The fused decode launches (pair walk + the shared expert's 16-position chunks in one grid)
+    give the separate calls' act, parts (the pair-walk calls), shared activations and shared
+    output (tlx_moe_shared: 64-position chunks) bit for bit (P = 70: five shared chunks, the last
+    of 6 positions)."""
     print(f"[case] moe pair walk + shared P={P} {lay}", flush=True)
     ex, layout = (experts, LAYOUT_RAW) if lay == "raw" else (experts_tiled, LAYOUT_TILED)
     rng = np.random.default_rng(60 + P)
@@ -294,6 +296,11 @@ def test_moe_pair_walk_with_shared_expert(gpu, experts, experts_tiled, P, lay):
     a = _run_layer(gpu, ex, x, logits, sg, hres, layout=layout)
     np_ = 8 * P
     eids = torch.from_numpy(a["eids"].reshape(-1)).to(gpu)
+    dx = torch.from_numpy(x).to(gpu)
+    ract = torch.empty(np_, moe.FF, dtype=torch.float32, device=gpu)
+    ops.moe_up4_pairs(ex["ptbl"], eids, dx, ex["iq4nl"], ract, layout=layout)
+    rparts = torch.empty(np_, moe.HID, dtype=torch.float16, device=gpu)
+    ops.moe_dn4_pairs(ex["ptbl_dn"], eids, ract, ex["iq4nl"], rparts, layout=layout)
     act = torch.full((np_, moe.FF), float("nan"), dtype=torch.float32, device=gpu)
     sact = torch.full((P, moe.FF), float("nan"), dtype=torch.float32, device=gpu)
     ops.moe_up4_pairs_sh(ex["ptbl"], eids, torch.from_numpy(x).to(gpu), ex["iq4nl"], act, ex["ptbl_sh"][0:1], sact,
@@ -303,9 +310,9 @@ def test_moe_pair_walk_with_shared_expert(gpu, experts, experts_tiled, P, lay):
     ops.moe_dn4_pairs_sh(ex["ptbl_dn"], eids, act, ex["iq4nl"], parts, ex["ptbl_sh"][1:2], sact, shared,
                          layout=layout)
     torch.cuda.synchronize()
-    assert np.array_equal(act.cpu().numpy(), a["act"])
+    assert np.array_equal(act.cpu().numpy(), ract.cpu().numpy())
     assert np.array_equal(sact.cpu().numpy(), a["sact"])
-    assert np.array_equal(parts.cpu().numpy(), a["parts"])
+    assert np.array_equal(parts.cpu().numpy(), rparts.cpu().numpy())
     assert np.array_equal(shared.cpu().numpy(), a["shared"])
 
 

@@ -187,13 +187,19 @@ constexpr int kTok = 64;         // item size of the GEMV form, and its dense (s
 constexpr int kDenseTok = 32;    // the GEMM form's dense chunk: 2 groups, so the shared expert's
                                  // grids fill the GPU beside the router and the sort
 constexpr int kPfTok = 96;       // item size of the GEMM form: up to 6 groups of 16 tokens
-constexpr int kGvMaxPairs = 2048;
+// Form per projection by pair count (measured over 4..2048 pairs, tiled slabs): the gate+up GEMV
+// form up to 512 pairs (items of 64 pairs), the MFMA form above (items of 96); the down GEMV form
+// up to 160 pairs, the act-resident MFMA form above (on the same items).  The shared expert runs
+// its GEMV form up to 256 positions.
+constexpr int kGvUpMaxPairs = 512;
+constexpr int kGvDnMaxPairs = 160;
+constexpr int kGvSharedMaxP = 256;
 constexpr int kShTok = 16;          // positions per shared-expert chunk of the fused pair walk   // pair counts up to this use the GEMV form, larger ones the GEMM
 constexpr int kSortChunk = 256;     // pairs per sort workgroup (4 waves of 64)
 
 // pairs per work item: the GEMV form takes up to 64, the GEMM form 96 (at uniform routing over 256
 // experts an expert's count exceeds 96 with odds of ~1e-4, so its weights are streamed once)
-__host__ __device__ constexpr int moe_item_tok(int np) { return np <= kGvMaxPairs ? kTok : kPfTok; }
+__host__ __device__ constexpr int moe_item_tok(int np) { return np <= kGvUpMaxPairs ? kTok : kPfTok; }
 
 // lanes of this wave holding the same 8-bit key as this lane
 __device__ __forceinline__ uint64_t same_key_mask(uint32_t key) {
@@ -754,7 +760,7 @@ template <int KIND, bool TL>
 __global__ __launch_bounds__(kPfThreads, 1) void moe_pd_kernel(
     const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff, const uint16_t* __restrict__ plist,
     const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp, const float* __restrict__ xs,
-    const float* __restrict__ iq4nl, void* __restrict__ out, int P) {
+    const float* __restrict__ iq4nl, void* __restrict__ out, int P, int tok) {
   constexpr bool kDense = KIND == MOE_DN_DENSE;
   __shared__ MoePdLds L;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -772,7 +778,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void moe_pd_kernel(
     const int e = (int)(it >> 16);
     m0 = (int)(it & 0xFFFFu);
     const int eb0 = eoff[e];
-    ntok = min(kPfTok, eoff[e + 1] - eb0 - m0);
+    ntok = min(tok, eoff[e + 1] - eb0 - m0);   // tok: the sort's item size (64 or 96 pairs)
     m0 += eb0;
     base = (const void*)(ptbl[e]);
   }
@@ -1117,8 +1123,8 @@ int moe_gv_items(int np) { return min(np, moe_max_items(np)); }
 template <int KIND>
 int moe_pf_grid(int nitems) { return (nitems + 7) / 8 * 8 * moe_pf_stripes<KIND>(); }
 
-// Grids of at least kGvSwapCols columns run swapped (measured: at 2048 pairs both projections
-// 17% faster; at decode widths the column-major order is as fast or faster).
+// Grids of at least kGvSwapCols columns run swapped (measured: 2% faster at 512 pairs, 17% at
+// 2048; at decode widths the column-major order is as fast or faster).
 constexpr int kGvSwapCols = 128;
 template <int KIND>
 dim3 moe_gv_grid(int nx) {
@@ -1155,12 +1161,13 @@ void moe_pf_launch(bool tl, int nitems, hipStream_t st, const uint64_t* ptbl, co
 
 template <int KIND>
 void moe_pd_launch(bool tl, int nitems, hipStream_t st, const uint64_t* ptbl, const int* eoff, const uint16_t* plist,
-                   const uint32_t* items, const uint32_t* nitp, const float* xs, const float* iq4nl, void* out, int P) {
+                   const uint32_t* items, const uint32_t* nitp, const float* xs, const float* iq4nl, void* out, int P,
+                   int tok = kPfTok) {
   const dim3 grid(nitems, KIND == MOE_DN_DENSE ? 4 : 1);   // dense: one stripe per workgroup
   if (tl)
-    moe_pd_kernel<KIND, true><<<grid, kPfThreads, 0, st>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, out, P);
+    moe_pd_kernel<KIND, true><<<grid, kPfThreads, 0, st>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, out, P, tok);
   else
-    moe_pd_kernel<KIND, false><<<grid, kPfThreads, 0, st>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, out, P);
+    moe_pd_kernel<KIND, false><<<grid, kPfThreads, 0, st>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, out, P, tok);
 }
 
 bool moe_layout_ok(int layout) { return layout == TLX_LAYOUT_RAW || layout == TLX_LAYOUT_TILED; }
@@ -1172,7 +1179,7 @@ extern "C" int tlx_moe_up4(const uint64_t* ptbl, const uint32_t* items, const ui
   TLX_RET_IF(!tlx_aligned(xs, 16) || !tlx_aligned(ys, 16), TLX_E_ALIGN);
   const bool tl = layout == TLX_LAYOUT_TILED;
   const hipStream_t st = (hipStream_t)stream;
-  if (np <= kGvMaxPairs)
+  if (np <= kGvUpMaxPairs)
     moe_gv_launch<MOE_UP>(tl, moe_gv_grid<MOE_UP>(moe_gv_items(np)), st, ptbl, eoff, plist, items, nitp, nullptr, xs,
                           iq4nl, ys, 0);
   else
@@ -1187,11 +1194,12 @@ extern "C" int tlx_moe_dn4(const uint64_t* ptbl_dn, const uint32_t* items, const
   TLX_RET_IF(!tlx_aligned(act, 16) || !tlx_aligned(parts, 16), TLX_E_ALIGN);
   const bool tl = layout == TLX_LAYOUT_TILED;
   const hipStream_t st = (hipStream_t)stream;
-  if (np <= kGvMaxPairs)
+  if (np <= kGvDnMaxPairs)
     moe_gv_launch<MOE_DN>(tl, moe_gv_grid<MOE_DN>(moe_gv_items(np)), st, ptbl_dn, eoff, plist, items, nitp, nullptr,
                           act, iq4nl, parts, 0);
   else
-    moe_pd_launch<MOE_DN>(tl, moe_max_items(np), st, ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0);
+    moe_pd_launch<MOE_DN>(tl, moe_max_items(np), st, ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts, 0,
+                          moe_item_tok(np));
   return tlx_launch_status();
 }
 
@@ -1242,7 +1250,7 @@ extern "C" int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const fl
   const bool tl = layout == TLX_LAYOUT_TILED;
   const hipStream_t st = (hipStream_t)stream;
   const int chunks = (P + kTok - 1) / kTok;
-  if (8 * P <= kGvMaxPairs) {
+  if (P <= kGvSharedMaxP) {
     moe_gv_launch<MOE_UP_DENSE>(tl, moe_gv_grid<MOE_UP_DENSE>(chunks), st, ptbl_sh, nullptr, nullptr, nullptr, nullptr,
                                 nullptr, xs, iq4nl, act, P);
     int rc = tlx_launch_status();
