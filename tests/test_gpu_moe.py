@@ -199,6 +199,17 @@ def test_moe_layer_decode_m11(gpu, experts):
     _check_layer(experts, x, logits, sg, hres, out, list(range(8 * P)), list(range(P)))
 
 
+@pytest.mark.parametrize("P", [16, 20])
+def test_moe_layer_gemv_forms_swapped_grid(gpu, experts, P):
+    """128 and 160 pairs: both GEMV forms on grids of 128+ columns, which run swapped (an
+    item's row-tile groups dispatched one after another), every pair and position checked."""
+    print(f"[case] moe layer P={P} (swapped GEMV grids)", flush=True)
+    rng = np.random.default_rng(70 + P)
+    x, logits, sg, hres = _inputs(rng, P)
+    out = _run_layer(gpu, experts, x, logits, sg, hres)
+    _check_layer(experts, x, logits, sg, hres, out, list(range(8 * P)), list(range(P)))
+
+
 def test_moe_layer_prefill_m2048_sampled(gpu, experts):
     print("[case] moe layer P=2048", flush=True)
     rng = np.random.default_rng(22)
