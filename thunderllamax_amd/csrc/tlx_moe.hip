@@ -194,11 +194,12 @@ constexpr int kPfTok = 96;       // item size of the GEMM form: up to 6 groups o
 constexpr int kGvUpMaxPairs = 512;
 constexpr int kGvDnMaxPairs = 160;
 constexpr int kGvSharedMaxP = 256;
-constexpr int kShTok = 16;          // positions per shared-expert chunk of the fused pair walk   // pair counts up to this use the GEMV form, larger ones the GEMM
+constexpr int kShTok = 16;          // positions per shared-expert chunk of the fused pair walk
 constexpr int kSortChunk = 256;     // pairs per sort workgroup (4 waves of 64)
 
-// pairs per work item: the GEMV form takes up to 64, the GEMM form 96 (at uniform routing over 256
-// experts an expert's count exceeds 96 with odds of ~1e-4, so its weights are streamed once)
+// pairs per work item: 64 up to kGvUpMaxPairs pairs (the gate+up GEMV form's limit; the down
+// projection's MFMA form takes the same items), 96 above (at uniform routing over 256 experts an
+// expert's count exceeds 96 with odds of ~1e-4, so its weights are streamed once)
 __host__ __device__ constexpr int moe_item_tok(int np) { return np <= kGvUpMaxPairs ? kTok : kPfTok; }
 
 // lanes of this wave holding the same 8-bit key as this lane
@@ -971,7 +972,7 @@ __global__ __launch_bounds__(256) void moe_gv_kernel(const uint64_t* __restrict_
   __shared__ uint32_t lut[256];
   __shared__ int xrow[kTok], orow[kTok];
   // reduction slots: one per tile shared by two waves (gate+up); the down tiles are one wave's
-  // (16 KB, so 5 workgroups fit a CU: a decode step's ~1200 workgroups run in one round)
+  // (16 KB: the workgroup's 30 KB of LDS leave residency to the register budget, 3 waves/SIMD)
   __shared__ f4_t red[(moe_gv_wpt<KIND>() > 1 ? 4 / moe_gv_wpt<KIND>() : 1) * kGvGroups * NMAT * 64];
   // Items of at most kGvStageRows tokens (decode: one or two) stage their token rows once, fp16
   // in the MFMA k order, row stride K / 8 + 1 pieces: read from global inside the decode loop,
