@@ -13,7 +13,7 @@ import torch
 
 from oracle import gemv, layouts, moe
 from thunderllamax_amd import formats, ops, synth
-from thunderllamax_amd._lib import LAYOUT_RAW, LAYOUT_TILED, TlxError
+from thunderllamax_amd._lib import LAYOUT_RAW, LAYOUT_TILED, TlxError, call
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -267,6 +267,17 @@ def test_moe_bad_arguments(gpu, experts):
     z = torch.zeros(16, dtype=torch.int32, device=gpu)
     with pytest.raises(TlxError):
         ops.moe_topk(torch.zeros(0, 256, dtype=torch.float32, device=gpu), z, z)
+    # the fused decode launches: no positions, and a shared-activation buffer off 16-B alignment
+    x1 = torch.zeros(1, 2048, device=gpu)
+    e8 = torch.zeros(8, dtype=torch.int16, device=gpu)
+    a8 = torch.zeros(8, 512, device=gpu)
+    sa = torch.zeros(2 * 512 + 4, device=gpu)
+    with pytest.raises(TlxError):
+        call("tlx_moe_up4_pairs_sh", experts["ptbl"].data_ptr(), e8.data_ptr(), x1.data_ptr(), experts["iq4nl"].data_ptr(),
+             a8.data_ptr(), experts["ptbl_sh"].data_ptr(), sa.data_ptr(), 0, LAYOUT_RAW, 0)
+    with pytest.raises(TlxError):
+        call("tlx_moe_up4_pairs_sh", experts["ptbl"].data_ptr(), e8.data_ptr(), x1.data_ptr(), experts["iq4nl"].data_ptr(),
+             a8.data_ptr(), experts["ptbl_sh"].data_ptr(), sa[1:].data_ptr(), 1, LAYOUT_RAW, 0)
     with pytest.raises(ValueError):   # a pointer table shorter than 256 entries never reaches the library
         ops.moe_up4(experts["ptbl"][:8], torch.zeros(ops.moe_max_items(8), dtype=torch.int32, device=gpu),
                     torch.zeros(1, dtype=torch.int32, device=gpu), torch.zeros(257, dtype=torch.int32, device=gpu),
