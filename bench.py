@@ -76,6 +76,12 @@ FFN8_M11_TRAFFIC_BYTES = 75_024_128
 # The same for the tiled-record kernel (one launch; FETCH_SIZE 35,843.8 KiB, WRITE_SIZE 1,922.0 KiB
 # at M=11 with the same calibration; profiles/pmc_counters_ffn8_pfgemm_moe.md).
 FFN8_TILED_M11_TRAFFIC_BYTES = 75_376_256
+# The M=11 MoE layer's launches (top-8, the pair walk's gate+up and down with the shared expert,
+# combine; tiled slabs), same passes and calibration (`--gemm-m 0 --no-sweep --no-formats --no-cpu
+# --no-config1 --no-stream --ms 11 --steps 10 --warmup 2 --copy-mib 256`; medians per dispatch):
+# FETCH_SIZE 13.6 + 48,697.1 + 24,097.0 + 275.7 KiB x 2, WRITE_SIZE 0.5 + 176.0 + 352.0 + 88.0 KiB
+# (profiles/moe_layer_config5.md).
+MOE_M11_TRAFFIC_BYTES = 150_306_099
 PEAK_F16_TFLOPS = 2500.0
 PEAK_I8_TOPS = 5000.0
 ROT_BYTES = 300 * 2**20
@@ -363,7 +369,8 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
                         "ms_other_shared_stream": round(t_other, 4), "ms_gguf_row_slabs": round(t_raw, 4),
                         **({"ms_sorted_grouped": round(t_grouped, 4)} if walk else {}),
                         "roofline": (hbm_roofline(gbs, f"MoE layer ({route}, combine; graph): "
-                                                       "expert weight bytes / layer time")
+                                                       "expert weight bytes / layer time",
+                                                  traffic=MOE_M11_TRAFFIC_BYTES if P == 11 else None)
                                      if P <= 64 else
                                      mfma_roofline(tflops, f"MoE layer ({route}, combine; graph): "
                                                            "2*3*512*2048*9*M / layer time"))}
