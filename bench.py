@@ -82,6 +82,14 @@ FFN8_TILED_M11_TRAFFIC_BYTES = 75_376_256
 # FETCH_SIZE 13.6 + 48,697.1 + 24,097.0 + 275.7 KiB x 2, WRITE_SIZE 0.5 + 176.0 + 352.0 + 88.0 KiB
 # (profiles/moe_layer_config5.md).
 MOE_M11_TRAFFIC_BYTES = 150_306_099
+# Config 1 (q6k_gemv_f32_kernel, one launch) and the prefill GEMMs at M=2048 (kernel + fix-up
+# launch), same calibration (`--gemm-m 2048 --no-stream --no-sweep --no-moe --no-cpu --no-formats
+# --ms 11 --steps 10 --warmup 2 --copy-mib 256`; profiles/pmc_counters_ffn8_pfgemm_moe.md):
+# config 1 FETCH_SIZE 10,682.0 KiB x 2 + WRITE_SIZE 40.0 KiB; gate+up (384,170.0 + 32,795.5) KiB x 2
+# + (131,072.0 + 4,096.0) KiB; down (244,708.8 + 81,948.0) KiB x 2 + (122,880.0 + 40,973.3) KiB.
+CONFIG1_TRAFFIC_BYTES = 21_917_696
+GEMM_FFN_M2048_TRAFFIC_BYTES = 992_357_376
+GEMM_DOWN_M2048_TRAFFIC_BYTES = 836_778_905
 PEAK_F16_TFLOPS = 2500.0
 PEAK_I8_TOPS = 5000.0
 ROT_BYTES = 300 * 2**20
@@ -100,10 +108,10 @@ def hbm_roofline(achieved_gbs, kernel, traffic=None, **extra):
     return r
 
 
-def mfma_roofline(achieved, kernel, peak=None, unit="TFLOP/s", **extra):
+def mfma_roofline(achieved, kernel, peak=None, unit="TFLOP/s", traffic=None, **extra):
     peak = PEAK_F16_TFLOPS if peak is None else peak
     r = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": unit,
-         "frac": round(achieved / peak, 4), "traffic": None, "kernel": kernel}
+         "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": kernel}
     r.update(extra)
     return r
 
@@ -233,7 +241,9 @@ def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup, weights, w4a8=Tr
         "down_ms": round(t_down, 4), "down_tflops": round(tf_down, 1),
         "tflops": round(tf_layer, 1),
         "roofline": mfma_roofline(tf_ffn, "pf_gemm_kernel<FFN> (+ pf_fix_kernel) gate+up",
-                                  down=mfma_roofline(tf_down, "pf_gemm_kernel<RES> (+ pf_fix_kernel) down")),
+                                  traffic=GEMM_FFN_M2048_TRAFFIC_BYTES if M == 2048 else None,
+                                  down=mfma_roofline(tf_down, "pf_gemm_kernel<RES> (+ pf_fix_kernel) down",
+                                                     traffic=GEMM_DOWN_M2048_TRAFFIC_BYTES if M == 2048 else None)),
     }
     if not w4a8:
         return out
@@ -524,7 +534,7 @@ def config1_leg(ops, synth, torch, dev, steps, warmup):
     gbs = nbytes / (t * 1e-3) / 1e9
     return {"workload": f"Q6_K GEMV {N}x{K}, fp32 x and y (M=1), raw 210-B blocks", "ms": round(t, 5),
             "algorithmic_bytes": nbytes, "gbs": round(gbs, 1), "rotation_copies": len(copies),
-            "roofline": hbm_roofline(gbs, "q6k_gemv_f32_kernel")}
+            "roofline": hbm_roofline(gbs, "q6k_gemv_f32_kernel", traffic=CONFIG1_TRAFFIC_BYTES)}
 
 
 def stream_leg(ops, torch, dev, steps, warmup):
