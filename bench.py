@@ -76,12 +76,14 @@ FFN8_M11_TRAFFIC_BYTES = 75_024_128
 # The same for the tiled-record kernel (one launch; FETCH_SIZE 35,843.8 KiB, WRITE_SIZE 1,922.0 KiB
 # at M=11 with the same calibration; profiles/pmc_counters_ffn8_pfgemm_moe.md).
 FFN8_TILED_M11_TRAFFIC_BYTES = 75_376_256
-# The M=11 MoE layer's launches (top-8, the pair walk's gate+up and down with the shared expert,
-# combine; tiled slabs), same passes and calibration (`--gemm-m 0 --no-sweep --no-formats --no-cpu
-# --no-config1 --no-stream --ms 11 --steps 10 --warmup 2 --copy-mib 256`; medians per dispatch):
-# FETCH_SIZE 13.6 + 48,697.1 + 24,097.0 + 275.7 KiB x 2, WRITE_SIZE 0.5 + 176.0 + 352.0 + 88.0 KiB
-# (profiles/moe_layer_config5.md).
-MOE_M11_TRAFFIC_BYTES = 150_306_099
+# The MoE layer's launches (tiled slabs), same passes and calibration (`--gemm-m 0 --no-sweep
+# --no-formats --no-cpu --no-config1 --no-stream --ms 11 --steps 10 --warmup 2 --copy-mib 256`;
+# medians per dispatch, split by launch shape; profiles/moe_layer_config5.md): M=11 (top-8, the
+# pair walk's gate+up and down with the shared expert, combine) FETCH_SIZE 13.5 + 49,375.3 +
+# 25,116.1 + 275.7 KiB x 2, WRITE_SIZE 0.5 + 198.0 + 440.0 + 88.0 KiB; M=2048 (top-8, sort, gate+up,
+# down, the shared expert's two, combine) FETCH_SIZE 349,499.7 KiB x 2, WRITE_SIZE 135,654.7 KiB.
+MOE_M11_TRAFFIC_BYTES = 153_894_605
+MOE_M2048_TRAFFIC_BYTES = 854_685_798
 # Config 1 (q6k_gemv_f32_kernel, one launch) and the prefill GEMMs at M=2048 (kernel + fix-up
 # launch), same calibration (`--gemm-m 2048 --no-stream --no-sweep --no-moe --no-cpu --no-formats
 # --ms 11 --steps 10 --warmup 2 --copy-mib 256`; profiles/pmc_counters_ffn8_pfgemm_moe.md):
@@ -383,7 +385,8 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
                                                   traffic=MOE_M11_TRAFFIC_BYTES if P == 11 else None)
                                      if P <= 64 else
                                      mfma_roofline(tflops, f"MoE layer ({route}, combine; graph): "
-                                                           "2*3*512*2048*9*M / layer time"))}
+                                                           "2*3*512*2048*9*M / layer time",
+                                                   traffic=MOE_M2048_TRAFFIC_BYTES if P == 2048 else None))}
     return out
 
 
