@@ -16,7 +16,12 @@ The headline layout (``--layout``, default ``tiled``) is the library's tiled rec
 blocks re-encoded with precomputed table indices, 102 B per 256 weights, repacked on the GPU);
 ``value`` still counts the GGUF bytes (98 per 256 weights), so it is the rate at which the
 quantized model streams.  ``per_m_other_layout`` times the reference's packed rows (pack_w1c),
-where from M=6 on a step is two launches (the tile-ordered activation copy, then the GEMV).
+where from M=6 on a step is two launches (the tile-ordered activation copy, then the GEMV), and
+``per_m_pack7`` the packed7 units (/root/reference/engine/pack_w7.py), the plane the prefill GEMM
+reads, on which the decode GEMVs run too (the reference's PF_DR7 mode).
+
+Every figure (every leg) is the median of 5 graph replays, each of >= 20 calls and timed by its own
+HIP events, after >= 3 eager warm-up calls and one untimed replay (``timing``).
 
 ``cpu_baseline`` times the numpy restatement of the reference's CPU path (dequantize, then
 an fp32 matmul) on the same workload (config 2 at the headline M, timed in full: dequant and
@@ -141,74 +146,82 @@ def parse():
     return ap.parse_args()
 
 
-def time_ffn(ops, wsets, gridf, x, gact, steps, warmup, torch, layout=1):
-    """Average ms per ffn8 call over `steps` calls captured in one HIP graph (host launch gaps
-    excluded: a decode step replays its launches as a graph), after `warmup` eager calls and
-    one untimed replay; HIP events on the replay stream."""
-    n = len(wsets)
-    st = torch.cuda.Stream()
-    st.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(st):
-        for i in range(max(warmup, 1)):   # eager: one-time set-up happens outside the capture
-            wg, wu = wsets[i % n]
-            ops.ffn8(wg, wu, gridf, x, gact, layout=layout, stream=st)
-    torch.cuda.current_stream().wait_stream(st)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=st):
-        for i in range(steps):
-            wg, wu = wsets[i % n]
-            ops.ffn8(wg, wu, gridf, x, gact, layout=layout, stream=st)
-    g.replay()   # replays on the current stream
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record()
-    g.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / steps
+# Every timed figure: a HIP graph of `calls` (>= MIN_CALLS) calls -- each may read a different
+# rotated weight copy -- captured after >= MIN_WARM eager warm-up calls and replayed once untimed;
+# then NREP replays, each bracketed by its own HIP events on the replay stream; the figure is the
+# median over those replays of (replay time / calls).
+MIN_CALLS, MIN_WARM, NREP = 20, 3, 5
+TIMING = (f"median of {NREP} graph replays of >= {MIN_CALLS} calls each (HIP events around each replay), "
+          f"after >= {MIN_WARM} eager warm-up calls and one untimed replay")
 
 
-def time_call(fn, steps, warmup, torch):
-    """Average ms of fn(stream) over `steps` calls after `warmup`, HIP events on its stream."""
-    stream = torch.cuda.current_stream()
-    for _ in range(warmup):
-        fn(stream)
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for _ in range(steps):
-        fn(stream)
-    t1.record(stream)
-    torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / steps
+def _timed_replays(g, calls, torch):
+    ts = []
+    for _ in range(NREP):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        g.replay()   # replays on the current stream
+        t1.record()
+        torch.cuda.synchronize()
+        ts.append(t0.elapsed_time(t1) / calls)
+    return float(np.median(ts))
 
 
 def time_graph(fn, steps, warmup, torch):
-    """Average ms of fn(stream) over `steps` calls captured in one HIP graph (each call may pick
-    different buffers, e.g. rotated weights), after `warmup` eager calls and one untimed replay."""
+    """Median ms of fn(stream) per call (see TIMING): max(steps, MIN_CALLS) calls captured in one
+    HIP graph (host launch gaps excluded: a decode step replays its launches as a graph; each call
+    may pick different buffers, e.g. rotated weights), after max(warmup, MIN_WARM) eager calls --
+    the one-time set-up happens outside the capture."""
+    calls = max(steps, MIN_CALLS)
     st = torch.cuda.Stream()
     st.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(st):
-        for _ in range(max(warmup, 1)):
+        for _ in range(max(warmup, MIN_WARM)):
             fn(st)
     torch.cuda.current_stream().wait_stream(st)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=st):
-        for _ in range(steps):
+        for _ in range(calls):
             fn(st)
-    g.replay()   # replays on the current stream
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record()
     g.replay()
-    t1.record()
     torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / steps
+    return _timed_replays(g, calls, torch)
+
+
+def time_ffn(ops, wsets, gridf, x, gact, steps, warmup, torch, layout=1):
+    """Median ms per ffn8 call (time_graph), each call on the next rotated weight copy."""
+    n = len(wsets)
+    it = [0]
+
+    def call(st):
+        wg, wu = wsets[it[0] % n]
+        it[0] += 1
+        ops.ffn8(wg, wu, gridf, x, gact, layout=layout, stream=st)
+
+    return time_graph(call, steps, warmup, torch)
+
+
+def time_call(fn, steps, warmup, torch):
+    """Median ms of fn(stream) over NREP timings of max(steps, MIN_CALLS) eager calls each, after
+    max(warmup, MIN_WARM) warm-up calls, HIP events on its stream."""
+    stream = torch.cuda.current_stream()
+    calls = max(steps, MIN_CALLS)
+    for _ in range(max(warmup, MIN_WARM)):
+        fn(stream)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(NREP):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(calls):
+            fn(stream)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ts.append(t0.elapsed_time(t1) / calls)
+    return float(np.median(ts))
 
 
 def gemm_weights(formats, synth, torch, dev):
@@ -476,34 +489,37 @@ def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True):
     nbytes += wh.numel()
 
     def graph_ms(lo, hi, reps, warm):
+        """Median ms of one replay of calls[lo:hi] (each replay timed by its own events)."""
         st = torch.cuda.Stream()
         st.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(st):
-            for c in calls[lo:hi]:
-                c(st)          # eager first: one-time kernel attributes are set outside capture
+            for _ in range(max(warm, MIN_WARM)):
+                for c in calls[lo:hi]:
+                    c(st)      # eager first: one-time kernel attributes are set outside capture
         torch.cuda.current_stream().wait_stream(st)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=st):
             for c in calls[lo:hi]:
                 c(st)
-        for _ in range(warm):
-            g.replay()
+        g.replay()
         torch.cuda.synchronize()
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        t0.record()
-        for _ in range(reps):
+        ts = []
+        for _ in range(max(reps, MIN_CALLS)):
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record()
             g.replay()
-        t1.record()
-        torch.cuda.synchronize()
-        return t0.elapsed_time(t1) / reps
+            t1.record()
+            torch.cuda.synchronize()
+            ts.append(t0.elapsed_time(t1))
+        return float(np.median(ts))
 
     t_step = graph_ms(0, len(calls), steps, warmup)
     per_kind = {}
     for kind, spans in kinds.items():   # one layer of each kind, replayed
         lo, hi = spans[0]
-        t = graph_ms(lo, hi, max(5, steps), 2)
+        t = graph_ms(lo, hi, steps, warmup)
         per_kind[kind] = {"layers": len(spans), "ms_per_layer": round(t, 4)}
     gbs = nbytes / (t_step * 1e-3) / 1e9
     return {"workload": "dense hybrid decode step, M=11: 48 GDN + 16 attention layers (8 with a Q6_K q), "
@@ -778,9 +794,17 @@ def main():
         ops.pack_iq3_tiled(wg, tg, N, K)
         ops.pack_iq3_tiled(wu, tu, N, K)
         tsets.append((tg, tu))
+    # and as packed7 units (the prefill GEMM's plane, which the decode GEMVs also read)
+    psets = []
+    for wg, wu in wsets:
+        pg7 = torch.empty(N * K // 2, dtype=torch.uint8, device=dev)
+        pu7 = torch.empty(N * K // 2, dtype=torch.uint8, device=dev)
+        ops.pack_w7(wg, pg7, N, K)
+        ops.pack_w7(wu, pu7, N, K)
+        psets.append((pg7, pu7))
     torch.cuda.synchronize()
-    from thunderllamax_amd._lib import LAYOUT_PACKED, LAYOUT_TILED
-    layouts = {"tiled": (tsets, LAYOUT_TILED), "packed": (wsets, LAYOUT_PACKED)}
+    from thunderllamax_amd._lib import LAYOUT_PACK7, LAYOUT_PACKED, LAYOUT_TILED
+    layouts = {"tiled": (tsets, LAYOUT_TILED), "packed": (wsets, LAYOUT_PACKED), "pack7": (psets, LAYOUT_PACK7)}
     other = "packed" if args.layout == "tiled" else "tiled"
 
     def per_m_of(name):
@@ -800,7 +824,7 @@ def main():
     def note(msg):   # progress on stderr: the JSON line stays the only stdout line
         print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
-    small_steps, small_warm = max(3, args.steps // 5), max(1, args.warmup // 5)
+    small_steps, small_warm = args.steps, args.warmup   # every leg: >= MIN_CALLS calls, >= MIN_WARM warm-ups
     if not args.no_stream:
         note("stream (HBM read ceiling)")
         stream = stream_leg(ops, torch, dev, small_steps, small_warm)
@@ -808,9 +832,11 @@ def main():
     per_m = per_m_of(args.layout)
     note(f"ffn8 per M ({other})")
     per_m_other = per_m_of(other)
+    note("ffn8 per M (pack7)")
+    per_m_p7 = per_m_of("pack7")
     head = str(max(ms))
     value = per_m[head]["gbs"]
-    for res in (per_m, per_m_other):
+    for res in (per_m, per_m_other, per_m_p7):
         for r in res.values():
             if MEASURED["hbm_gbs"]:
                 r["frac_of_measured"] = round(r["gbs"] / MEASURED["hbm_gbs"], 4)
@@ -832,6 +858,9 @@ def main():
                    "layout": args.layout, "rotation_copies": ncopy, "parallelism": "single GPU"},
         "per_m": per_m,
         "per_m_other_layout": {"layout": other, **per_m_other},
+        "per_m_pack7": {"layout": "packed7 units (the prefill GEMM's plane; GGUF bytes counted, the plane "
+                                  "holds 128 B per 256 weights)", **per_m_p7},
+        "timing": TIMING,
         "roofline": hbm_roofline(
             value,
             ("iq3s_kernel<2,1,8,3> (tiled records, activations staged in LDS)" if args.layout == "tiled" else

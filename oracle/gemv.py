@@ -4,8 +4,7 @@ The reference kernels compute ``acc_f32 += f32(f16(x) * f16(w))`` -- fp16-rounde
 and products, fp32 sums (/root/reference/engine/ffn8.cu:155-184).  The accuracy contract
 for matmul outputs is a relative error of at most 1e-3 against the exact product of the
 dequantized weights and the fp16 activations; ``*_ref`` below compute that exact product in
-float64 and then apply each kernel's output epilogue.  ``iq3_gemv_fp16_products`` restates
-the reference's own fp16-product arithmetic (for showing where its error sits).
+float64 and then apply each kernel's output epilogue.
 """
 import numpy as np
 
@@ -57,29 +56,6 @@ def gemv16_ref(W, x16):
 def q6k_gemv_ref(W, x32):
     """h6k2048 contract: fp32 W (dequantized) times fp32 x, exact in float64 -> [rows]."""
     return np.asarray(W, dtype=np.float64) @ np.asarray(x32, dtype=np.float64)
-
-
-def iq3_gemv_fp16_products(W16, x16):
-    """The reference kernels' arithmetic, lane order and warp-32 tree included
-    (/root/reference/engine/aq3k8.cu:125-130): lane l sums ``f32(f16(x*w))`` over
-    ``k = 256b + 8l + j`` (b asc, j asc), then a shfl_down tree 16, 8, 4, 2, 1."""
-    W16 = np.asarray(W16, dtype=np.float16)
-    x16 = np.asarray(x16, dtype=np.float16)
-    N, K = W16.shape
-    nb = K // 256
-    out = np.empty((x16.shape[0], N), dtype=np.float32)
-    Wl = W16.reshape(N, nb, 32, 8)
-    for m in range(x16.shape[0]):
-        xl = x16[m].reshape(nb, 32, 8)
-        p = (Wl.astype(np.float32) * xl[None].astype(np.float32)).astype(np.float16).astype(np.float32)
-        lane = np.zeros((N, 32), dtype=np.float32)
-        for b in range(nb):
-            for j in range(8):
-                lane = (lane + p[:, b, :, j]).astype(np.float32)
-        for o in (16, 8, 4, 2, 1):
-            lane[:, :32 - o] = (lane[:, :32 - o] + lane[:, o:]).astype(np.float32)
-        out[m] = lane[:, 0]
-    return out
 
 
 def pf_ffn_ref(Wg, Wu, x16):

@@ -97,16 +97,3 @@ def combine_ref(parts, gates, sg, shared, hres):
     acc = np.einsum("pr,prk->pk", np.asarray(gates, np.float64), np.asarray(parts, np.float64))
     acc += np.asarray(sg, np.float64)[:, None] * np.asarray(shared, np.float64)
     return np.asarray(hres, np.float64) + acc
-
-
-def moe_layer_ref(slabs, slabs_dn, shared_slab, shared_dn, x, logits, sg, hres):
-    """Whole layer in float64 from logits: top-8 -> per-pair expert FFN -> combine."""
-    eids, gates = topk_ref(logits)
-    P = x.shape[0]
-    parts = np.zeros((P, TOPK, HID))
-    for p in range(P):
-        for r in range(TOPK):
-            e = int(eids[p, r])
-            parts[p, r] = down_ref(slabs_dn[e], up_ref(slabs[e], x[p:p + 1]))[0]
-    shared = down_ref(shared_dn, up_ref(shared_slab, x))
-    return eids, gates, parts, shared, combine_ref(parts, gates, sg, shared, hres)

@@ -47,7 +47,8 @@ def test_version_and_strerror():
     (0, 64, 5120, 1, _lib.TLX_E_ARG),        # M below range
     (17, 64, 5120, 1, _lib.TLX_E_ARG),       # M above TLX_MAX_M
     (1, 64, 5000, 1, _lib.TLX_E_ARG),        # K not a multiple of 256
-    (1, 64, 5120, 2, _lib.TLX_E_ARG),        # packed7 is a prefill-GEMM layout only
+    (1, 60, 5120, 2, _lib.TLX_E_ARG),        # packed7 units come in 8-row groups
+    (1, 64, 5120, 5, _lib.TLX_E_ARG),        # no such layout
     (1, 64, 256 * 21, 1, _lib.TLX_E_ALIGN),  # odd block count -> rows not dword aligned
 ])
 def test_ffn8_argument_validation(M, N, K, layout, code):

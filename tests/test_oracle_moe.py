@@ -58,13 +58,17 @@ def _const_iq4_rows(rows, kdim, qbyte):
 
 
 def test_expert_ffn_closed_form():
-    # kv[8] = 1: every gate/up weight is 1, so g = u = sum(x); every down weight kv[9] = 13
-    gu = np.concatenate([_const_iq4_rows(moe.FF, moe.HID, 0x88).ravel(), _const_iq4_rows(moe.FF, moe.HID, 0x88).ravel()])
+    # gate weights kv[8] = 1 (g = s = sum(x)), up weights kv[9] = 13 (u = 13 s): act = silu(s) * 13 s.
+    # The halves differ, so reading the up rows as gate (silu(13 s) * s) or a wrong GATE_B4 offset
+    # (/root/reference/engine/mm/MM_P2_gx8e256up4.cu:22) fails.  Every down weight kv[9] = 13.
+    gu = np.concatenate([_const_iq4_rows(moe.FF, moe.HID, 0x88).ravel(), _const_iq4_rows(moe.FF, moe.HID, 0x99).ravel()])
     dn = _const_iq4_rows(moe.HID, moe.FF, 0x99).ravel()
-    x = np.random.default_rng(2).standard_normal((4, moe.HID))
+    x = 0.02 * np.random.default_rng(2).standard_normal((4, moe.HID))   # s = sum(x) of order 1
     s = x.sum(axis=1)
     act = moe.up_ref(gu, x)
-    np.testing.assert_allclose(act, np.repeat((s / (1 + np.exp(-s)) * s)[:, None], moe.FF, axis=1), rtol=1e-12)
+    np.testing.assert_allclose(act, np.repeat((s / (1 + np.exp(-s)) * 13.0 * s)[:, None], moe.FF, axis=1), rtol=1e-12)
+    swapped = (13.0 * s / (1 + np.exp(-13.0 * s))) * s
+    assert np.all(np.abs(act[:, 0] - swapped) > 1e-3 * np.abs(swapped))
     part = moe.down_ref(dn, act)
     np.testing.assert_allclose(part, np.repeat(13.0 * act.sum(axis=1)[:, None], moe.HID, axis=1), rtol=1e-12)
 

@@ -91,7 +91,25 @@ __device__ __forceinline__ void iq3_load(Iq3Regs<NMAT>& r, const uint8_t* const*
   }
 }
 
-template <int NMAT, int EPI, int WAVES>
+// The same registers from the packed7 units (TLX_LAYOUT_PACK7, engine/pack_w7.py:7-21): the lane's
+// 64 k of block b are sub-blocks c0, c0 + 1 of chunk 2b + (kq >> 1) (c0 = 2 (kq & 1)), two adjacent
+// 16-B units [q u16 x4][sw][d][pad] of its row: q words 0..3 then 4..7, the two scale/sign words,
+// the block's d.  The values are those the packed rows give, so the GEMV results are bit-identical.
+template <int NMAT>
+__device__ __forceinline__ void iq3_load7(Iq3Regs<NMAT>& r, const uint8_t* const* base, uint32_t off, int b) {
+#pragma unroll
+  for (int i = 0; i < NMAT; ++i) {
+    const uint8_t* p = base[i] + (off + 1024u * (uint32_t)b);
+    const u4_t u0 = *reinterpret_cast<const u4_t*>(p);
+    const u4_t u1 = *reinterpret_cast<const u4_t*>(p + 16);
+    r.qs[i] = u4_t{u0.x, u0.y, u1.x, u1.y};
+    r.sw[i] = u2_t{u0.z, u1.z};
+    r.d[i] = u0.w;
+  }
+}
+
+// P7: 0 = packed rows / GGUF blocks (strided fields), 1 = packed7 units
+template <int NMAT, int EPI, int WAVES, int P7>
 __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Launch a) {
   __shared__ u2_t tbl[kTblEntries];
   tlx_iq3_table(tbl, a.gridf);
@@ -111,13 +129,16 @@ __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Lau
   {
     // tail tile: clamp the loads, mask the stores
     const bool raw = a.layout == TLX_LAYOUT_RAW;
-    const uint32_t roff = (uint32_t)min(row0 + col, sg.n - 1) * rowb;
+    const int row = min(row0 + col, sg.n - 1);
+    const uint32_t roff = (uint32_t)row * rowb;
     qoff = roff + (raw ? 2u : 0u) + 16u * kq;
     soff = roff + (raw ? 66u : 64u * nb) + 8u * kq;
     doff = roff + (raw ? 0u : 96u * nb);
     qst = raw ? 98u : 64u;
     sst = raw ? 98u : 32u;
     dst = raw ? 98u : 2u;
+    if constexpr (P7)   // unit (row & 7, c0) of chunk kq >> 1 in group row >> 3 (2 * nb chunks a group)
+      qoff = ((uint32_t)((row >> 3) * 2 * nb + (kq >> 1)) * 32u + 4u * (uint32_t)(row & 7) + 2u * (kq & 1)) * 16u;
   }
 
   const uint8_t* base[NMAT];
@@ -135,9 +156,13 @@ __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Lau
 #pragma unroll
   for (int i = 0; i < NMAT; ++i) acc[i] = f4_t{0.f, 0.f, 0.f, 0.f};
 
+  auto load = [&](Iq3Regs<NMAT>& r, int blk) {
+    if constexpr (P7) iq3_load7<NMAT>(r, base, qoff, blk);
+    else iq3_load<NMAT>(r, base, qoff, soff, doff, qst, sst, dst, blk);
+  };
   int b = wave;
   Iq3Regs<NMAT> cur;
-  if (b < nb) iq3_load<NMAT>(cur, base, qoff, soff, doff, qst, sst, dst, b);
+  if (b < nb) load(cur, b);
   for (; b < nb; b += WAVES) {
     // this block's activations first, then the next block's weights: waiting for the
     // activations leaves the weight prefetch in flight
@@ -146,7 +171,7 @@ __global__ __launch_bounds__(WAVES * TLX_WAVE) void iq3_gemv_kernel(const Iq3Lau
     for (int t = 0; t < 8; ++t) X[t] = *reinterpret_cast<const h8_t*>(xr + xbs * b + xcs * t);
     Iq3Regs<NMAT> nxt;
     const bool more = b + WAVES < nb;
-    if (more) iq3_load<NMAT>(nxt, base, qoff, soff, doff, qst, sst, dst, b + WAVES);
+    if (more) load(nxt, b + WAVES);
 
 #pragma unroll
     for (int i = 0; i < NMAT; ++i) {
@@ -251,10 +276,20 @@ int iq3_launch(Iq3Launch& a, int tiles, hipStream_t st) {
   if (a.otile) return TLX_E_ARG;   // the tile-ordered output exists for the tiled records only
   int waves = 4;
   while (tiles * waves < 4096 && waves < 16 && nb >= 4 * waves) waves *= 2;
+  const bool p7 = a.layout == TLX_LAYOUT_PACK7;
   switch (waves) {
-    case 4: iq3_gemv_kernel<NMAT, EPI, 4><<<tiles, 4 * TLX_WAVE, 0, st>>>(a); break;
-    case 8: iq3_gemv_kernel<NMAT, EPI, 8><<<tiles, 8 * TLX_WAVE, 0, st>>>(a); break;
-    default: iq3_gemv_kernel<NMAT, EPI, 16><<<tiles, 16 * TLX_WAVE, 0, st>>>(a); break;
+    case 4:
+      if (p7) iq3_gemv_kernel<NMAT, EPI, 4, 1><<<tiles, 4 * TLX_WAVE, 0, st>>>(a);
+      else iq3_gemv_kernel<NMAT, EPI, 4, 0><<<tiles, 4 * TLX_WAVE, 0, st>>>(a);
+      break;
+    case 8:
+      if (p7) iq3_gemv_kernel<NMAT, EPI, 8, 1><<<tiles, 8 * TLX_WAVE, 0, st>>>(a);
+      else iq3_gemv_kernel<NMAT, EPI, 8, 0><<<tiles, 8 * TLX_WAVE, 0, st>>>(a);
+      break;
+    default:
+      if (p7) iq3_gemv_kernel<NMAT, EPI, 16, 1><<<tiles, 16 * TLX_WAVE, 0, st>>>(a);
+      else iq3_gemv_kernel<NMAT, EPI, 16, 0><<<tiles, 16 * TLX_WAVE, 0, st>>>(a);
+      break;
   }
   return tlx_launch_status();
 }
@@ -273,15 +308,21 @@ int iq3_flags(int& layout, int allowed, Iq3Launch& a) {
 
 int iq3_check(const void* w, int M, int N, int K, int layout) {
   if (M < 1 || M > TLX_MAX_M || N < 1 || K < 256 || (K & 255)) return TLX_E_ARG;
-  if (layout != TLX_LAYOUT_PACKED && layout != TLX_LAYOUT_RAW && layout != TLX_LAYOUT_TILED) return TLX_E_ARG;
+  if (layout != TLX_LAYOUT_PACKED && layout != TLX_LAYOUT_RAW && layout != TLX_LAYOUT_TILED &&
+      layout != TLX_LAYOUT_PACK7)
+    return TLX_E_ARG;
+  // packed7 units come in 8-row groups (N % 8 == 0) and are read as 16-B vectors
+  if (layout == TLX_LAYOUT_PACK7 && (N & 7)) return TLX_E_ARG;
+  if (layout == TLX_LAYOUT_PACK7 && !tlx_aligned(w, 16)) return TLX_E_ALIGN;
   // packed rows: the operand loads are dword-aligned when the row bytes 98*NB are (NB even);
   // tiled records are 1632 B (16-B aligned fields); GGUF blocks are 2-B aligned throughout
   if (layout == TLX_LAYOUT_PACKED && (((K >> 8) & 1) || !tlx_aligned(w, 4))) return TLX_E_ALIGN;
   if (layout == TLX_LAYOUT_TILED && !tlx_aligned(w, 16)) return TLX_E_ALIGN;
   if (!tlx_aligned(w, 2)) return TLX_E_ALIGN;
   // kernels address a matrix with 32-bit byte offsets (tiled: 102-B records of whole tiles)
-  const size_t bytes = layout == TLX_LAYOUT_TILED ? (size_t)(N + kTile - 1) / kTile * kTile * 102 * (K >> 8)
-                                                  : (size_t)N * kIq3BlockBytes * (K >> 8);
+  const size_t bytes = layout == TLX_LAYOUT_TILED  ? (size_t)(N + kTile - 1) / kTile * kTile * 102 * (K >> 8)
+                      : layout == TLX_LAYOUT_PACK7 ? (size_t)N * 128 * (K >> 8)
+                                                   : (size_t)N * kIq3BlockBytes * (K >> 8);
   if (bytes > 0xFFFFFFFFull) return TLX_E_ARG;
   return TLX_OK;
 }

@@ -40,13 +40,18 @@ def attach_workspace(device=None, gemm_bytes=None, stream=None):
         m = torch.empty(mb, dtype=torch.uint8, device=dev) if mb > 0 else None
         call("tlx_attach_workspace", g.data_ptr(), gb, None if m is None else m.data_ptr(), mb,
              _stream(stream))
+        # the fill (torch's current stream) and the counter clear (`stream`) complete before any
+        # call on any stream can use the workspace: a call on another stream that overlapped the
+        # clear could leave an arrival counter at 1 for every later call on the device
+        torch.cuda.synchronize(dev)
     _WORKSPACES[dev.index] = (g, m)
     return g, m
 
 
 def _ws(t):
     """Attach the workspaces of t's device on its first use there (never inside stream capture:
-    an allocation there would belong to the graph)."""
+    an allocation there would belong to the graph).  Every wrapper calls it before its first
+    launch, so the library's one-time set-up (kernel attributes) also runs outside capture."""
     if t.device.index in _WORKSPACES:
         return
     if torch.cuda.is_current_stream_capturing():
@@ -107,9 +112,11 @@ def _iq3_rows(n, k):
 
 def _iq3_w(n, k, layout):
     """Bytes of an IQ3_XXS matrix of n rows in `layout` (tiled: 102-B records of whole 16-row
-    tiles)."""
+    tiles; packed7: 16-B units, 128 B per 256 weights)."""
     if layout == LAYOUT_TILED:
         return (n + 15) // 16 * 16 * 102 * (k // 256)
+    if layout == LAYOUT_PACK7:
+        return _pack7(n, k)
     return _iq3_rows(n, k)
 
 
@@ -148,20 +155,27 @@ def iq4xs_dequant(w, iq4nl, out, kdim, stream=None):
 
 
 # ------------------------------------------------------------------ decode GEMVs
-def ffn8(wg, wu, gridf, hhx, gact, layout=LAYOUT_PACKED, stream=None, out_tileord=False):
+def ffn8(wg, wu, gridf, hhx, gact, layout=LAYOUT_PACKED, stream=None, out_tileord=False, in_tileord=False,
+         m=None):
     """gact[m] = silu16(half(Wg·hhx[m])) * half(Wu·hhx[m])   (ffn8 / ffn8v{M}).  With
     ``out_tileord`` (tiled records only) gact is a tile-ordered [N/8][16][8] buffer (tileord_empty),
-    which down8 / iq3_gemv read with ``in_tileord`` and no copy launch."""
-    M, K = _mk(hhx), hhx.shape[-1]
+    which down8 / iq3_gemv read with ``in_tileord`` and no copy launch; with ``in_tileord`` hhx is
+    such a buffer (then M is given by ``m`` or gact's rows)."""
+    K = _tileord_n(hhx) if in_tileord else hhx.shape[-1]
     N = _tileord_n(gact) if out_tileord else gact.shape[-1]
+    M = m if m is not None else (_mk(hhx) if not in_tileord else _mk(gact) if not out_tileord else None)
+    if M is None:
+        raise ValueError("both sides tile-ordered: pass m")
     _need(wg, _iq3_w(N, K, layout), "wg")
     _need(wu, _iq3_w(N, K, layout), "wu")
     _need(gridf, 4096, "gridf")
+    _need(hhx, (16 if in_tileord else M) * K * 2, "hhx")
     _need(gact, (16 if out_tileord else M) * N * 2, "gact")
     _dev(wg, wu, gridf, hhx, gact)
     _ws(wg)
+    fl = (IN_TILEORD if in_tileord else 0) | (OUT_TILEORD if out_tileord else 0)
     call("tlx_ffn8", wg.data_ptr(), wu.data_ptr(), gridf.data_ptr(), hhx.data_ptr(), gact.data_ptr(),
-         M, N, K, layout | (OUT_TILEORD if out_tileord else 0), _stream(stream))
+         M, N, K, layout | fl, _stream(stream))
     return gact
 
 
@@ -326,6 +340,7 @@ def h6k_gemv(w, x, y, layout=LAYOUT_RAW, stream=None):
     """y = W·x, Q6_K weights, fp32 x and y   (h6k2048 contract)."""
     _need(w, y.numel() * (210 if layout == LAYOUT_RAW else 212) * (x.numel() // 256), "w")
     _dev(w, x, y)
+    _ws(w)
     call("tlx_q6k_gemv", w.data_ptr(), x.data_ptr(), y.data_ptr(), y.numel(), x.numel(), layout,
          _stream(stream))
     return y
@@ -343,6 +358,7 @@ def q6k_gemv16(w, x, out, layout=LAYOUT_PACKED, stream=None):
     _need(w, _q6_rows(N, K, layout), "w")
     _need(out, M * N * 2, "out")
     _dev(w, x, out)
+    _ws(w)
     call("tlx_q6k_gemv16", w.data_ptr(), x.data_ptr(), out.data_ptr(), M, N, K, layout,
          _stream(stream))
     return out
@@ -354,6 +370,7 @@ def _k4_gemv(name, nbytes, w, x, out, stream):
     _need(w, N * nbytes * (K // 256), "w")
     _need(out, M * N * 2, "out")
     _dev(w, x, out)
+    _ws(w)
     call(name, w.data_ptr(), x.data_ptr(), out.data_ptr(), M, N, K, _stream(stream))
     return out
 
