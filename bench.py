@@ -275,6 +275,47 @@ def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup, weights, w4a8=Tr
     return out
 
 
+def merged_gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup):
+    """The merged multi-class prefill GEMM (pf_gemm3m) at M rows, K=5120, on the reference's three
+    configurations (/root/reference/engine/build_p7b.py:58-77): attention q/k/v with an IQ3_XXS or a
+    Q6_K q (IQ3_XXS k, Q4_K v) and the GDN qkv (Q5_K) with its IQ3_XXS gate.  Seeded weights, graph
+    replays, TFLOP/s of 2*M*N*K summed over the segments."""
+    from thunderllamax_amd._lib import (LAYOUT_PACK7, LAYOUT_PACKED, LAYOUT_RAW, TYPE_IQ3_XXS, TYPE_Q4_K,
+                                        TYPE_Q5_K, TYPE_Q6_K)
+    K = 5120
+    rng = synth.config_rng(4)
+
+    def mat(cls, n):
+        if cls == "iq3":
+            a = formats.iq3_pack7(formats.iq3_pack_rows(synth.iq3xxs_raw(rng, n, K), K), K)
+            t, lay = TYPE_IQ3_XXS, LAYOUT_PACK7
+        elif cls == "q6k":
+            a, t, lay = formats.q6_pad_rows(synth.q6k_raw(rng, n, K), K), TYPE_Q6_K, LAYOUT_PACKED
+        else:
+            a = synth.k4_raw(rng, n, K, cls == "q5k")
+            t, lay = (TYPE_Q5_K if cls == "q5k" else TYPE_Q4_K), LAYOUT_RAW
+        return torch.from_numpy(np.ascontiguousarray(a).reshape(-1)).to(dev), t, lay, n
+
+    configs = {"attnqkv_i3": [("iq3", 12288), ("iq3", 1024), ("q4k", 1024)],
+               "attnqkv_q6": [("q6k", 12288), ("iq3", 1024), ("q4k", 1024)],
+               "gdnqg": [("q5k", 10240), ("iq3", 6144)]}
+    gridf = formats.gridf_tensor(dev)
+    x = torch.from_numpy(synth.activations_f16(rng, M, K)).to(dev)
+    out = {"workload": f"merged prefill GEMM (pf_gemm3m), M={M}, K={K}: segments of different weight classes "
+                       "sharing x, one launch, fp16 out"}
+    for name, segs in configs.items():
+        mats = [mat(c, n) for c, n in segs]
+        outs = [torch.empty(M, n, dtype=torch.float16, device=dev) for *_, n in mats]
+        t = time_graph(lambda s: ops.pfg3m([m[0] for m in mats], outs, [m[1] for m in mats], [m[2] for m in mats],
+                                           gridf, x, stream=s), steps, warmup, torch)
+        flops = 2.0 * M * K * sum(n for *_, n in mats)
+        tf = flops / (t * 1e-3) / 1e12
+        out[name] = {"segments": [f"{c} {n}x{K}" for c, n in segs], "ms": round(t, 4), "tflops": round(tf, 1),
+                     "roofline": mfma_roofline(tf, "pfm_gemm_kernel (one launch over the segments)")}
+        del mats, outs
+    return out
+
+
 def producers_leg(ops, formats, synth, torch, dev, steps, warmup, M=11, tiled=True):
     """The activation producer before the FFN GEMV (hh{M}: residual add + RMSNorm -> fp16) at
     config 2's D=5120, alone, followed by ffn8, and fused with it (tlx_ffn8_hh), as graph
@@ -885,6 +926,8 @@ def main():
                 out["gemm"].update(leg)
             out["gemm"][f"M{M}"] = {k: v for k, v in leg.items() if k != "w4a8_ffn"}
         del weights
+        note(f"merged gemm M={gemm_ms[0]}")
+        out["gemm"]["merged"] = merged_gemm_leg(ops, formats, synth, torch, dev, gemm_ms[0], small_steps, small_warm)
     if not args.no_sweep:
         note("sweep (config 3)")
         out["sweep"] = sweep_leg(ops, formats, torch, dev, small_steps, small_warm, tiled=args.layout == "tiled")

@@ -215,6 +215,25 @@ int tlx_pfg3_iq3d(const void* w, const float* gridf, const uint16_t* x16, const 
 int tlx_pfg3_iq3o(const void* w, const float* gridf, const uint16_t* x16, uint16_t* out16,
                   int M, int N, int K, int layout, void* stream);
 
+/* Merged multi-segment prefill GEMM: up to three weight matrices of different formats that share
+ * the activations, one launch, plain fp16 epilogue: out_s[m][r] = half(sum_k x16[m][k] * half(W_s[r][k])),
+ * half(W) the reference's fp16 operand (IQ3_XXS fp16(db*g); Q4_K / Q5_K fp16((d*sc)*q - dmin*m);
+ * Q6_K fp16((d*sc)*(q-32)), each computed in fp32 and rounded once).  Replaces pf_gemm3m
+ * (engine/pf_gemm3m.cu:1-16,229; its builds engine/build_p7b.py:58-77: attention q/k/v with an
+ * IQ3_XXS or Q6_K q, IQ3_XXS k and Q4_K v; GDN qkv Q5_K with the IQ3_XXS gate):
+ * kernel(wA, wB[, wC], gridf, x16, outA, outB[, outC]) as arrays of nseg entries.  Per segment
+ * (w, out, n rows, type, layout): type a ggml type code, with its layout
+ *   TLX_TYPE_IQ3_XXS + TLX_LAYOUT_PACK7 (the packed7 units the IQ3_XXS GEMMs read),
+ *   TLX_TYPE_Q4_K / TLX_TYPE_Q5_K + TLX_LAYOUT_RAW (GGUF 144-B / 176-B blocks),
+ *   TLX_TYPE_Q6_K + TLX_LAYOUT_PACKED (the padded 212-B blocks of engine/pack_w1c.py:33-45);
+ * n % 256 == 0, M % 256 == 0, K % 256 == 0, 16-byte aligned buffers.  out_s is fp16 [M][n_s]. */
+#define TLX_TYPE_Q4_K 12
+#define TLX_TYPE_Q5_K 13
+#define TLX_TYPE_Q6_K 14
+#define TLX_TYPE_IQ3_XXS 18
+int tlx_pfg3m(const void* const* w, uint16_t* const* out, const int* n, const int* type, const int* layout,
+              int nseg, const float* gridf, const uint16_t* x16, int M, int K, void* stream);
+
 /* ---- int8-activation (W4A8) prefill branch.
  * Activation quantizer, replaces pfk_q8 (engine/pfk_q8.cu:25-59, kernel(x, xq, sx, rs)):
  * per (row, 128-k chunk) s = max(absmax, 1e-6) * (1/127), xq = rint(x / s) clamped to

@@ -105,3 +105,27 @@ def test_no_device_allocation_in_library_sources():
         text = re.sub(r"//[^\n]*", "", open(os.path.join(csrc, f)).read())
         for bad in ("hipMalloc", "hipFree", "hipMemset", "hipExtMalloc"):
             assert bad not in text, (f, bad)
+
+
+def test_pfg3m_argument_validation():
+    """The merged prefill GEMM rejects unsupported weight classes and shapes before any launch."""
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(64)
+    p = (ctypes.addressof(buf) + 15) & ~15
+    P = ctypes.c_void_p * 3
+    I = ctypes.c_int * 3
+    w, o = P(p, p, p), P(p, p, p)
+
+    def rc(n, types, layouts, nseg=3, M=256, K=512, x=p):
+        return L.tlx_pfg3m(w, o, I(*n), I(*types), I(*layouts), nseg, p, x, M, K, None)
+
+    ok_t, ok_l = (_lib.TYPE_IQ3_XXS, _lib.TYPE_Q6_K, _lib.TYPE_Q4_K), (_lib.LAYOUT_PACK7, _lib.LAYOUT_PACKED, _lib.LAYOUT_RAW)
+    assert rc((256, 256, 256), ok_t, ok_l, nseg=0) == _lib.TLX_E_ARG
+    assert rc((256, 256, 256), ok_t, ok_l, nseg=4) == _lib.TLX_E_ARG
+    assert rc((256, 256, 128), ok_t, ok_l) == _lib.TLX_E_ARG                      # n % 256
+    assert rc((256, 256, 256), ok_t, ok_l, M=128) == _lib.TLX_E_ARG               # M % 256
+    assert rc((256, 256, 256), ok_t, ok_l, K=384) == _lib.TLX_E_ARG               # K % 256
+    assert rc((256, 256, 256), ok_t, (_lib.LAYOUT_PACKED,) * 3) == _lib.TLX_E_ARG   # IQ3_XXS must be packed7
+    assert rc((256, 256, 256), (_lib.TYPE_Q6_K,) * 3, (_lib.LAYOUT_RAW,) * 3) == _lib.TLX_E_ARG  # Q6_K: padded
+    assert rc((256, 256, 256), (23,) * 3, (_lib.LAYOUT_RAW,) * 3) == _lib.TLX_E_ARG  # IQ4_XS: not a class
+    assert rc((256, 256, 256), ok_t, ok_l, x=p + 2) == _lib.TLX_E_ALIGN

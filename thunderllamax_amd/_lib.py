@@ -27,6 +27,11 @@ V_Q4K = 0x100   # or-ed into the fused attention layout: v rows are GGUF Q4_K
 OUT_TILEORD = 0x200   # or-ed into an IQ3_XXS GEMV layout: fp16 output in the tile-ordered form [N/8][16][8]
 IN_TILEORD = 0x400    # or-ed into an IQ3_XXS GEMV layout: activations in the tile-ordered form [K/8][16][8]
 MAX_M = 16
+# ggml type codes of the weight classes the merged prefill GEMM (tlx_pfg3m) takes
+TYPE_Q4_K = 12
+TYPE_Q5_K = 13
+TYPE_Q6_K = 14
+TYPE_IQ3_XXS = 18
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
@@ -60,6 +65,7 @@ SIGNATURES = {
     "tlx_pfg3_ffn": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_pfg3_iq3d": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "tlx_pfg3_iq3o": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "tlx_pfg3m": [_p, _p, _p, _p, _p, _i, _p, _p, _i, _i, _p],
     "tlx_p8_quant": [_p, _p, _p, _p, _i, _i, _p],
     "tlx_gguf_parse": [_p, ctypes.c_uint64, _p, _p, _p, _i64],
     "tlx_rms_f16": [_p, _p, _p, _i, _i, _p],

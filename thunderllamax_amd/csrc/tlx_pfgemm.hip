@@ -31,6 +31,19 @@
 //     steps, which the compiler interleaves with the step's MFMAs;
 //   * workgroup w runs on XCD w % 8; when M is a multiple of 2048 each XCD sweeps the n-tiles
 //     of one m-tile at a time, so its L2 keeps that activation slice.
+//
+// The merged form (pf_gemm3m, engine/pf_gemm3m.cu:1-16,229): up to three weight matrices of
+// different formats that share the activations, one launch, plain fp16 epilogue; a workgroup's
+// n-tile selects its segment.  Besides packed7 IQ3_XXS a segment may be GGUF Q4_K (144-B
+// blocks), GGUF Q5_K (176-B blocks) or Q6_K in the padded 212-B blocks of pack_w1c
+// (engine/pack_w1c.py:33-45), the classes the reference's merged twins mix (attention q/k/v:
+// engine/build_p7b.py:64-77; GDN qkv + gate: :58-63).  For those, thread (row tid / 2, half
+// tid % 2) decodes its 16 weights of sub-block t + 1 during step t into the other B tile, from
+// 16-B pieces each wave staged in LDS by DMA at step t - 1 (aligned covers of the fields its rows
+// need; the ring takes the place of the IQ3_XXS table): each weight becomes the reference's operand
+// fp16 of the GGUF value computed in fp32 -- Q4_K / Q5_K fp16((d*sc)*q - dmin*m) (one fma:
+// (d*sc)*q is exact in fp32), Q6_K fp16((d*sc)*(q - 32)) -- the dequantizers of
+// engine/pf_gemm3m.cu:84-136 (dq_c2 / dq_c3 / dq_c4).
 #include "tlx_common.h"
 
 #include <algorithm>
@@ -47,10 +60,15 @@ constexpr int kTile = kBM * kBK;          // halfs per A or B tile
 enum PfEpi { PF_FFN = 0, PF_RES = 1, PF_F16 = 2 };
 
 struct __attribute__((aligned(16))) PfLds {
-  uint32_t tbl[4096 * 2];                 // sign-folded grid table, 4 fp16 per entry
   _Float16 a[3][kTile];                   // activation ring: 16-row groups, row-major, swizzled
   _Float16 b[2][kTile];                   // dequantized weights, fragment order
-  u4_t w[2][kBN * 4];                     // packed7 units of one 128-k chunk: [group][r*4+c]
+  union {
+    struct {
+      uint32_t tbl[4096 * 2];             // IQ3_XXS: sign-folded grid table, 4 fp16 per entry
+      u4_t w[2][kBN * 4];                 // IQ3_XXS: packed7 units of one 128-k chunk: [group][r*4+c]
+    };
+    u4_t kq[2][kWaves][4][TLX_WAVE];      // k-quants: two stages of each wave's 16-B weight pieces
+  };
 };
 
 // B tile: fragment-order offset (halfs) of piece p of tile row R
@@ -161,7 +179,156 @@ struct PfArgs {
   const _Float16* x;
   int K, nch, m0, nt;
   int tlast, hlast;   // last k-step / 128-k chunk of the segment being computed (loads clamp there)
+  const uint8_t* wkq;    // k-quant formats: the tile's first weight row
+  uint32_t rowb;         // k-quant formats: bytes per weight row
 };
+
+// Weight formats of a GEMM segment: packed7 IQ3_XXS units, GGUF Q4_K / Q5_K blocks, Q6_K padded
+// 212-B blocks ([pad 2][d 2][sc 16][ql 128][qh 64]).
+enum PfFmt { PF_IQ3 = 0, PF_Q4K = 1, PF_Q5K = 2, PF_Q6P = 3 };
+
+__host__ __device__ constexpr int pf_block_bytes(int f) {
+  return f == PF_Q4K ? 144 : f == PF_Q5K ? 176 : f == PF_Q6P ? 212 : 128;
+}
+
+// K-quant weights reach the B tile through LDS: at step t each wave DMAs (16-B LDS-DMA loads, one
+// 1 KB slab per instruction) the aligned 16-B pieces that cover what its 32 tile rows need for
+// sub-block t + 2 into a two-stage ring; at step t + 1 the thread pair of each row decodes
+// sub-block t + 2 from there.  Pieces per row (P): Q4_K the 16-B header and the 32 qs bytes of the
+// sub-block pair (3); Q5_K the header, the 32 qh bytes and the 32 qs bytes (5); Q6_K (4-B aligned
+// fields) the 48-B aligned covers of its 32 ql bytes and of its 32 qh bytes and the 32-B cover of
+// d and the scales (8).  Piece p of a wave's sub-block goes to slab byte 16 p (row p / P, piece
+// p % P); lanes past 32 P re-load the last piece.
+template <int FMT> constexpr int pf_kq_pieces() { return FMT == PF_Q4K ? 3 : FMT == PF_Q5K ? 5 : 8; }
+template <int FMT> constexpr int pf_kq_dmas() { return (32 * pf_kq_pieces<FMT>() + TLX_WAVE - 1) / TLX_WAVE; }
+
+// Byte offset from the row start of piece q (0 .. P-1) of sub-block j.
+template <int FMT>
+__device__ __forceinline__ uint32_t pf_kq_piece_off(int j, int q) {
+  const uint32_t b = (uint32_t)(j >> 3), s = (uint32_t)(j & 7);
+  const uint32_t blk = (uint32_t)pf_block_bytes(FMT) * b;
+  if constexpr (FMT == PF_Q4K) {
+    return blk + (q == 0 ? 0u : 16u * (uint32_t)q + 32u * (s >> 1));
+  } else if constexpr (FMT == PF_Q5K) {
+    return blk + (q < 3 ? 16u * (uint32_t)q : 16u * (uint32_t)q + 32u * (s >> 1));
+  } else {
+    // ql bytes start at blk + 20 + 64 h' + 32 (g & 1), qh bytes at blk + 148 + 32 h': both 4 (b + 1)
+    // mod 16 past a 16-B boundary (blk = 212 b is 4 b mod 16); the header cover starts at blk rounded
+    // down.  A cover that starts on a boundary needs 2 pieces: its third re-loads the second.
+    const uint32_t hp = s >> 2, g = s & 3, m = 4u * ((b + 1u) & 3u), mh = 4u * (b & 3u);
+    const uint32_t need = m == 0 ? 2u : 3u;
+    if (q < 3) return blk + 20u + 64u * hp + 32u * (g & 1u) - m + 16u * min((uint32_t)q, need - 1u);
+    if (q < 6) return blk + 148u + 32u * hp - m + 16u * min((uint32_t)q - 3u, need - 1u);
+    return blk - mh + 16u * ((uint32_t)q - 6u);
+  }
+}
+
+// Stage the pieces of sub-block j into ring stage `stage` (wave-uniform; pf_kq_dmas loads).
+template <int FMT>
+__device__ __forceinline__ void pf_kq_dma(PfLds& L, int stage, const uint8_t* __restrict__ wt, uint32_t rowb,
+                                          int j, int wave, int lane) {
+  constexpr int P = pf_kq_pieces<FMT>();
+#pragma unroll
+  for (int i = 0; i < pf_kq_dmas<FMT>(); ++i) {
+    const int p = min(TLX_WAVE * i + lane, 32 * P - 1);
+    const int r = p / P, q = p - r * P;
+    const uint8_t* src = wt + (size_t)(32 * wave + r) * rowb + pf_kq_piece_off<FMT>(j, q);
+    __builtin_amdgcn_global_load_lds((const void*)src,
+                                     (__attribute__((address_space(3))) void*)(&L.kq[stage][wave][i][0]), 16, 0, 0);
+  }
+}
+
+// One thread's bytes of a sub-block, read back from its wave's slab.
+struct PfKq {
+  u4_t q;      // Q4_K / Q5_K: 16 qs bytes (nibble s & 1); Q6_K: 16 ql bytes (nibble g >= 2)
+  u4_t hb;     // Q5_K: qh bytes 16h .. 16h + 15 (bit s); Q6_K: qh bytes (bits 2g, 2g + 1)
+  u4_t hdr;    // Q4_K / Q5_K: d, dmin, the 12 packed scale bytes; Q6_K: .x = d
+  uint32_t sc; // Q6_K: the scale dword holding sc[8 h' + h + 2 g]
+};
+
+template <int FMT>
+__device__ __forceinline__ void pf_kq_read(PfKq& r, const PfLds& L, int stage, int j, int wave, int lane) {
+  constexpr int P = pf_kq_pieces<FMT>();
+  const int h = lane & 1;
+  const uint8_t* cb = reinterpret_cast<const uint8_t*>(&L.kq[stage][wave][0][0]) + 16 * P * (lane >> 1);
+  if constexpr (FMT == PF_Q4K) {
+    r.hdr = *reinterpret_cast<const u4_t*>(cb);
+    r.q = *reinterpret_cast<const u4_t*>(cb + 16 + 16 * h);
+  } else if constexpr (FMT == PF_Q5K) {
+    r.hdr = *reinterpret_cast<const u4_t*>(cb);
+    r.hb = *reinterpret_cast<const u4_t*>(cb + 16 + 16 * h);
+    r.q = *reinterpret_cast<const u4_t*>(cb + 48 + 16 * h);
+  } else {
+    const uint32_t b = (uint32_t)(j >> 3), s = (uint32_t)(j & 7);
+    const uint32_t m = 4u * ((b + 1u) & 3u), mh = 4u * (b & 3u);
+    const uint32_t* ql = reinterpret_cast<const uint32_t*>(cb + m + 16 * h);
+    const uint32_t* qh = reinterpret_cast<const uint32_t*>(cb + 48 + m + 16 * h);
+    r.q = u4_t{ql[0], ql[1], ql[2], ql[3]};
+    r.hb = u4_t{qh[0], qh[1], qh[2], qh[3]};
+    r.hdr.x = *reinterpret_cast<const uint16_t*>(cb + 96 + mh + 2);
+    const uint32_t i = 8u * (s >> 2) + (uint32_t)h + 2u * (s & 3u);
+    r.sc = *reinterpret_cast<const uint32_t*>(cb + 96 + mh + 4 + (i & ~3u));
+  }
+}
+
+// fp16 of an fp32 value, round to nearest even (the reference's __float2half)
+__device__ __forceinline__ uint32_t pf_pack2(float a, float b) {
+  const h2_t v = {(_Float16)a, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// The 16 operand values of sub-block j for half h into pieces 2h, 2h + 1 of tile row r.
+template <int FMT>
+__device__ __forceinline__ void pf_kq_dequant(const PfKq& r, _Float16* bt, int row, int j, int h) {
+  const int s = j & 7;
+  uint32_t w[8];
+  if constexpr (FMT == PF_Q4K || FMT == PF_Q5K) {
+    const uint32_t hx = r.hdr.x;
+    const float d = tlx_h2f((uint16_t)(hx & 0xFFFFu)), dmin = tlx_h2f((uint16_t)(hx >> 16));
+    // 6-bit scale and min of sub-block s from the 12 packed bytes (ggml get_scale_min_k4)
+    const uint32_t q03 = r.hdr.y, q47 = r.hdr.z, q811 = r.hdr.w;
+    auto byte = [](uint32_t v, int i) { return (v >> (8 * i)) & 0xFFu; };
+    uint32_t sc, mn;
+    if (s < 4) {
+      sc = byte(q03, s) & 63u;
+      mn = byte(q47, s) & 63u;
+    } else {
+      sc = (byte(q811, s - 4) & 0xFu) | ((byte(q03, s - 4) >> 6) << 4);
+      mn = (byte(q811, s - 4) >> 4) | ((byte(q47, s - 4) >> 6) << 4);
+    }
+    const float A = d * (float)sc, B = dmin * (float)mn;   // exact in fp32
+    const uint32_t sh = 4u * (uint32_t)(s & 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v = (r.q[i] >> sh) & 0x0F0F0F0Fu;
+      uint32_t hi = 0;
+      if constexpr (FMT == PF_Q5K) hi = ((r.hb[i] >> s) & 0x01010101u) << 4;
+      const uint32_t qv = v | hi;
+      float f[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) f[e] = __builtin_fmaf(A, (float)((qv >> (8 * e)) & 0xFFu), -B);
+      w[2 * i] = pf_pack2(f[0], f[1]);
+      w[2 * i + 1] = pf_pack2(f[2], f[3]);
+    }
+  } else {
+    const int hp = s >> 2, g = s & 3;
+    const float d = tlx_h2f((uint16_t)r.hdr.x);
+    const int sci = (8 * hp + h + 2 * g) & 3;
+    const float A = d * (float)(int8_t)((r.sc >> (8 * sci)) & 0xFFu);
+    const uint32_t nsh = g >= 2 ? 4u : 0u, hsh = 2u * (uint32_t)g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t qv = ((r.q[i] >> nsh) & 0x0F0F0F0Fu) | (((r.hb[i] >> hsh) & 0x03030303u) << 4);
+      float f[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) f[e] = A * (float)((int)((qv >> (8 * e)) & 0xFFu) - 32);
+      w[2 * i] = pf_pack2(f[0], f[1]);
+      w[2 * i + 1] = pf_pack2(f[2], f[3]);
+    }
+  }
+  *reinterpret_cast<u4_t*>(bt + pf_frag(row, 2 * h)) = u4_t{w[0], w[1], w[2], w[3]};
+  *reinterpret_cast<u4_t*>(bt + pf_frag(row, 2 * h + 1)) = u4_t{w[4], w[5], w[6], w[7]};
+}
 
 // One k-step t: operand loads of step t (written before the last barrier), then the producers
 // -- activations of step t+2, on every 4th step the burst staging the next chunk, the dequant
@@ -194,6 +361,34 @@ __device__ __forceinline__ void pf_step(PfLds& L, f4_t (&acc)[kMI][8], const PfA
   static_assert(kLdW == 2, "the wait counts below assume 2 A loads (+2 weight loads) per wave per step");
   if (wstep) asm volatile("s_waitcnt vmcnt(4)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   else asm volatile("s_waitcnt vmcnt(2)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// One k-step of a k-quant segment: the operand loads of step t; the decode of sub-block t + 1
+// (staged at step t - 1: the two activation loads issued after it may still be in flight); the
+// weight pieces of sub-block t + 2 into the stage sub-block t used; the activations of step t + 2;
+// the MFMAs, which the scheduler interleaves with the decode; the barrier.
+template <int FMT>
+__device__ __forceinline__ void pf_kq_step(PfLds& L, f4_t (&acc)[kMI][8], const PfArgs& g, const int* bg, int aoff,
+                                           int t, int ra, int wave, int wm, int lane) {
+  PfFrag f;
+  pf_load_frag(f, L.a[ra], L.b[t & 1], bg, aoff, wm, lane);
+  const int j1 = min(t + 1, g.tlast);
+  asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+  PfKq kr;
+  pf_kq_read<FMT>(kr, L, (t + 1) & 1, j1, wave, lane);
+  pf_kq_dequant<FMT>(kr, L.b[(t + 1) & 1], (int)threadIdx.x >> 1, j1, lane & 1);
+  pf_kq_dma<FMT>(L, t & 1, g.wkq, g.rowb, min(t + 2, g.tlast), wave, lane);
+  const int ra2 = ra == 0 ? 2 : ra - 1;
+  pf_dma_a(L.a[ra2], g.x, g.m0, g.K, min(t + 2, g.tlast), wave, lane);
+  pf_mfma<0, kMI>(acc, f);
+  // step t+1's activations (issued at step t-1) must have landed; this step's weight pieces and
+  // activations stay in flight
+  __builtin_amdgcn_sched_barrier(0);
+  static_assert(kLdW == 2, "the wait counts below assume 2 A loads per wave per step");
+  if constexpr (pf_kq_dmas<FMT>() == 2) asm volatile("s_waitcnt vmcnt(4)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (pf_kq_dmas<FMT>() == 3) asm volatile("s_waitcnt vmcnt(5)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(6)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -239,31 +434,10 @@ __device__ __forceinline__ void pf_epilogue(const f4_t (&acc)[kMI][8], const int
   }
 }
 
-template <int EPI>
-__global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
-    const u4_t* __restrict__ w1, const u4_t* __restrict__ w2, const float* __restrict__ gridf,
-    const _Float16* __restrict__ x, void* __restrict__ out, const float* __restrict__ res, int M, int N,
-    int K, int mtiles, int ntiles, const PfSk sk) {
-  __shared__ PfLds L;
-  constexpr bool kFfn = EPI == PF_FFN;
-  // wave index as a scalar: the per-wave DMA selection branches on SGPRs
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int col = lane & 15, kq = lane >> 4;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int nch = K / 128;
-  const int bx = (int)blockIdx.x;
-  int tau, h0 = 0, h1 = nch, seg = -1;
-  if (bx < sk.full) {
-    tau = bx;
-  } else {
-    seg = bx - sk.full;
-    const int q = seg % sk.p;
-    tau = sk.full + seg / sk.p;
-    h0 = q * nch / sk.p;
-    h1 = (q + 1) * nch / sk.p;
-  }
-  int mt, nt;
-  if ((mtiles & 7) == 0) {   // XCD x = tau % 8 sweeps the n-tiles of m-tiles x, x+8, ... in turn
+// (m-tile, n-tile) of tile index tau: when there are m-tiles for all 8 XCDs, workgroup tau runs
+// on XCD tau % 8 and that XCD sweeps the n-tiles of m-tiles x, x+8, ... in turn
+__device__ __forceinline__ void pf_tile_of(int tau, int mtiles, int ntiles, int& mt, int& nt) {
+  if ((mtiles & 7) == 0) {
     const int l = tau >> 3;
     mt = (tau & 7) + 8 * (l / ntiles);
     nt = l % ntiles;
@@ -271,22 +445,58 @@ __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
     mt = tau % mtiles;
     nt = tau / mtiles;
   }
+}
+
+// One workgroup's tile (or k-range segment of a split tile: seg >= 0, chunks [h0, h1)): the
+// prologue, the k-steps, then the epilogue or the part store.  nt: the tile's n-tile within its
+// matrix (or matrix pair); wkq: k-quant formats, the matrix.
+template <int EPI, int FMT>
+__device__ __forceinline__ void pf_tile(PfLds& L, const u4_t* __restrict__ w1, const u4_t* __restrict__ w2,
+                                        const uint8_t* __restrict__ wkq, const float* __restrict__ gridf,
+                                        const _Float16* __restrict__ x, void* __restrict__ out,
+                                        const float* __restrict__ res, int N, int K, int mt, int nt, int h0, int h1,
+                                        int seg, const PfSk& sk) {
+  constexpr bool kFfn = EPI == PF_FFN;
+  // wave index as a scalar: the per-wave DMA selection branches on SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int col = lane & 15, kq = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int nch = K / 128;
   PfArgs g;
   g.w1 = w1; g.w2 = w2; g.x = x; g.K = K; g.nch = nch;
   g.m0 = mt * kBM; g.nt = nt;
   g.tlast = 4 * h1 - 1; g.hlast = h1 - 1;
+  g.wkq = nullptr;
+  g.rowb = 0;
   const int s0 = 4 * h0;
 
-  // prologue: activation steps s0, s0+1 and weight chunks h0, h0+1 in flight; table; sub-block s0
-  pf_dma_a(L.a[0], x, g.m0, K, s0, wave, lane);
-  pf_dma_a(L.a[1], x, g.m0, K, min(s0 + 1, g.tlast), wave, lane);
-  pf_dma_w(L, h0 & 1, w1, w2, kFfn, nt, nch, h0, wave, lane);
-  pf_dma_w(L, (h0 + 1) & 1, w1, w2, kFfn, nt, nch, min(h0 + 1, g.hlast), wave, lane);
-  pf_build_table(L.tbl, gridf);
-  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-  __syncthreads();
-  pf_dequant(L, L.b[s0 & 1], threadIdx.x, s0);
-  __syncthreads();
+  if constexpr (FMT == PF_IQ3) {
+    // prologue: activation steps s0, s0+1 and weight chunks h0, h0+1 in flight; table; sub-block s0
+    pf_dma_a(L.a[0], x, g.m0, K, s0, wave, lane);
+    pf_dma_a(L.a[1], x, g.m0, K, min(s0 + 1, g.tlast), wave, lane);
+    pf_dma_w(L, h0 & 1, w1, w2, kFfn, nt, nch, h0, wave, lane);
+    pf_dma_w(L, (h0 + 1) & 1, w1, w2, kFfn, nt, nch, min(h0 + 1, g.hlast), wave, lane);
+    pf_build_table(L.tbl, gridf);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();
+    pf_dequant(L, L.b[s0 & 1], threadIdx.x, s0);
+    __syncthreads();
+  } else {
+    // prologue: activation steps s0, s0+1 and the weight pieces of sub-blocks s0, s0+1; sub-block s0
+    // decoded (every segment starts on a 128-k chunk)
+    g.rowb = (uint32_t)(pf_block_bytes(FMT) * (K >> 8));
+    g.wkq = wkq + (size_t)(nt * kBN) * g.rowb;
+    pf_kq_dma<FMT>(L, s0 & 1, g.wkq, g.rowb, s0, wave, lane);
+    pf_kq_dma<FMT>(L, (s0 + 1) & 1, g.wkq, g.rowb, s0 + 1, wave, lane);
+    pf_dma_a(L.a[0], x, g.m0, K, s0, wave, lane);
+    pf_dma_a(L.a[1], x, g.m0, K, s0 + 1, wave, lane);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();
+    PfKq kr;
+    pf_kq_read<FMT>(kr, L, s0 & 1, s0, wave, lane);
+    pf_kq_dequant<FMT>(kr, L.b[s0 & 1], threadIdx.x >> 1, s0, lane & 1);
+    __syncthreads();
+  }
 
   // the wave's eight 16-column n-tiles (row groups of the B tile); for FFN tiles 0..3 are gate
   // columns [64wn, +64) and tiles 4..7 the up columns of the same range
@@ -302,9 +512,16 @@ __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
     for (int j = 0; j < 8; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
   int ra = 0;
-  for (int t = s0; t <= g.tlast; ++t) {
-    pf_step<kFfn>(L, acc, g, bg, aoff, t, ra, wave, wm, lane);
-    ra = ra == 2 ? 0 : ra + 1;
+  if constexpr (FMT == PF_IQ3) {
+    for (int t = s0; t <= g.tlast; ++t) {
+      pf_step<kFfn>(L, acc, g, bg, aoff, t, ra, wave, wm, lane);
+      ra = ra == 2 ? 0 : ra + 1;
+    }
+  } else {
+    for (int t = s0; t <= g.tlast; ++t) {
+      pf_kq_step<FMT>(L, acc, g, bg, aoff, t, ra, wave, wm, lane);
+      ra = ra == 2 ? 0 : ra + 1;
+    }
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);   // drain the clamped tail loads before the block exits
 
@@ -319,6 +536,64 @@ __global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
     return;
   }
   pf_epilogue<EPI>(acc, bg, g.m0, nt, wm, kq, col, out, res, N);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads, 1) void pf_gemm_kernel(
+    const u4_t* __restrict__ w1, const u4_t* __restrict__ w2, const float* __restrict__ gridf,
+    const _Float16* __restrict__ x, void* __restrict__ out, const float* __restrict__ res, int M, int N,
+    int K, int mtiles, int ntiles, const PfSk sk) {
+  __shared__ PfLds L;
+  const int nch = K / 128;
+  const int bx = (int)blockIdx.x;
+  int tau, h0 = 0, h1 = nch, seg = -1;
+  if (bx < sk.full) {
+    tau = bx;
+  } else {
+    seg = bx - sk.full;
+    const int q = seg % sk.p;
+    tau = sk.full + seg / sk.p;
+    h0 = q * nch / sk.p;
+    h1 = (q + 1) * nch / sk.p;
+  }
+  int mt, nt;
+  pf_tile_of(tau, mtiles, ntiles, mt, nt);
+  pf_tile<EPI, PF_IQ3>(L, w1, w2, nullptr, gridf, x, out, res, N, K, mt, nt, h0, h1, seg, sk);
+}
+
+// The merged form: up to three segments (matrices of any PfFmt sharing x), fp16 outputs; the
+// n-tiles of all segments form one tile range, a workgroup's n-tile selects its segment.
+struct PfSeg {
+  const void* w;
+  uint16_t* out;
+  int n;        // rows (output columns)
+  int fmt;      // PfFmt
+  int nt0;      // first n-tile of the segment in the merged range
+};
+struct PfMulti {
+  PfSeg seg[3];
+  int nseg;
+};
+
+__global__ __launch_bounds__(kThreads, 1) void pfm_gemm_kernel(const PfMulti mseg, const float* __restrict__ gridf,
+                                                               const _Float16* __restrict__ x, int K, int mtiles,
+                                                               int ntiles) {
+  __shared__ PfLds L;
+  int mt, ntg;
+  pf_tile_of((int)blockIdx.x, mtiles, ntiles, mt, ntg);
+  int s = 0;
+  while (s + 1 < mseg.nseg && ntg >= mseg.seg[s + 1].nt0) ++s;
+  const PfSeg sg = mseg.seg[s];
+  const int nt = ntg - sg.nt0, nch = K / 128;
+  const PfSk none{0, 0, 1, nullptr};
+  const u4_t* w = static_cast<const u4_t*>(sg.w);
+  const uint8_t* wb = static_cast<const uint8_t*>(sg.w);
+  switch (sg.fmt) {
+    case PF_IQ3: pf_tile<PF_F16, PF_IQ3>(L, w, nullptr, nullptr, gridf, x, sg.out, nullptr, sg.n, K, mt, nt, 0, nch, -1, none); break;
+    case PF_Q4K: pf_tile<PF_F16, PF_Q4K>(L, nullptr, nullptr, wb, gridf, x, sg.out, nullptr, sg.n, K, mt, nt, 0, nch, -1, none); break;
+    case PF_Q5K: pf_tile<PF_F16, PF_Q5K>(L, nullptr, nullptr, wb, gridf, x, sg.out, nullptr, sg.n, K, mt, nt, 0, nch, -1, none); break;
+    default: pf_tile<PF_F16, PF_Q6P>(L, nullptr, nullptr, wb, gridf, x, sg.out, nullptr, sg.n, K, mt, nt, 0, nch, -1, none); break;
+  }
 }
 
 int pf_check(const void* w, const void* x, int M, int N, int K, int layout, int ntile) {
@@ -340,14 +615,7 @@ __global__ __launch_bounds__(kThreads) void pf_fix_kernel(const f4_t* __restrict
   const int col = lane & 15, kq = lane >> 4, wm = wave >> 1, wn = wave & 1;
   const int st = (int)blockIdx.x / kMI, i = (int)blockIdx.x % kMI, tau = full + st;
   int mt, nt;
-  if ((mtiles & 7) == 0) {
-    const int l = tau >> 3;
-    mt = (tau & 7) + 8 * (l / ntiles);
-    nt = l % ntiles;
-  } else {
-    mt = tau % mtiles;
-    nt = tau / mtiles;
-  }
+  pf_tile_of(tau, mtiles, ntiles, mt, nt);
   int bg[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) bg[j] = kFfn ? (j < 4 ? 4 * wn + j : 8 + 4 * wn + (j - 4)) : 8 * wn + j;
@@ -446,4 +714,33 @@ extern "C" int tlx_pfg3_iq3o(const void* w, const float* gridf, const uint16_t* 
   TLX_RET_IF(!tlx_aligned(gridf, 16), TLX_E_ALIGN);
   return pf_launch<PF_F16>((const u4_t*)w, nullptr, gridf, (const _Float16*)x16, out16, nullptr, M, N, K, M / kBM,
                            N / kBN, (hipStream_t)stream);
+}
+
+extern "C" int tlx_pfg3m(const void* const* w, uint16_t* const* out, const int* n, const int* type,
+                         const int* layout, int nseg, const float* gridf, const uint16_t* x16, int M, int K,
+                         void* stream) {
+  TLX_RET_IF(w == nullptr || out == nullptr || n == nullptr || type == nullptr || layout == nullptr, TLX_E_ARG);
+  TLX_RET_IF(nseg < 1 || nseg > 3, TLX_E_ARG);
+  // k-quant blocks are 256 wide and every segment starts its k-loop on a 128-k chunk
+  TLX_RET_IF(M < kBM || (M % kBM) || K < 256 || (K % 256), TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(x16, 16) || !tlx_aligned(gridf, 16), TLX_E_ALIGN);
+  PfMulti ms{};
+  int ntiles = 0;
+  for (int s = 0; s < nseg; ++s) {
+    TLX_RET_IF(n[s] < kBN || (n[s] % kBN), TLX_E_ARG);
+    int f;
+    if (type[s] == TLX_TYPE_IQ3_XXS && layout[s] == TLX_LAYOUT_PACK7) f = PF_IQ3;
+    else if (type[s] == TLX_TYPE_Q4_K && layout[s] == TLX_LAYOUT_RAW) f = PF_Q4K;
+    else if (type[s] == TLX_TYPE_Q5_K && layout[s] == TLX_LAYOUT_RAW) f = PF_Q5K;
+    else if (type[s] == TLX_TYPE_Q6_K && layout[s] == TLX_LAYOUT_PACKED) f = PF_Q6P;
+    else return TLX_E_ARG;
+    TLX_RET_IF(!tlx_aligned(w[s], 16) || !tlx_aligned(out[s], 16), TLX_E_ALIGN);
+    ms.seg[s] = PfSeg{w[s], out[s], n[s], f, ntiles};
+    ntiles += n[s] / kBN;
+  }
+  ms.nseg = nseg;
+  const int mtiles = M / kBM;
+  pfm_gemm_kernel<<<mtiles * ntiles, kThreads, 0, (hipStream_t)stream>>>(ms, gridf, (const _Float16*)x16, K, mtiles,
+                                                                         ntiles);
+  return tlx_launch_status();
 }

@@ -434,6 +434,43 @@ def pfg3_ffn(wg, wu, gridf, x16, out16, layout=LAYOUT_PACK7, stream=None):
     return out16
 
 
+# The merged form (pf_gemm3m): segments of different weight classes sharing x16, one launch.
+_PFM_CLASSES = {   # (ggml type, layout) -> bytes of an n x k matrix
+    (18, LAYOUT_PACK7): lambda n, k: _pack7(n, k),
+    (12, LAYOUT_RAW): lambda n, k: n * 144 * (k // 256),
+    (13, LAYOUT_RAW): lambda n, k: n * 176 * (k // 256),
+    (14, LAYOUT_PACKED): lambda n, k: n * 212 * (k // 256),
+}
+
+
+def pfg3m(ws, outs, types, layouts, gridf, x16, stream=None):
+    """outs[s][m] = half(W_s·x16[m]) for up to three matrices of different weight classes in one
+    launch (pf_gemm3m: kernel(wA, wB[, wC], gridf, x16, outA, outB[, outC])).  types: ggml type codes
+    (18 IQ3_XXS with LAYOUT_PACK7, 12 Q4_K / 13 Q5_K with LAYOUT_RAW, 14 Q6_K with LAYOUT_PACKED, the
+    padded 212-B blocks)."""
+    import ctypes
+    nseg = len(ws)
+    if not 1 <= nseg == len(outs) == len(types) == len(layouts) <= 3:
+        raise ValueError("one to three segments: a weight, output, type and layout each")
+    M, K = x16.shape
+    for w, o, t, lay in zip(ws, outs, types, layouts):
+        size = _PFM_CLASSES.get((int(t), int(lay)))
+        if size is None:
+            raise ValueError(f"weight class (type {t}, layout {lay}) is not a merged-GEMM segment class")
+        _need(w, size(o.shape[-1], K), "w")
+        _need(o, M * o.shape[-1] * 2, "out")
+        _dev(w, o)
+    _need(gridf, 4096, "gridf")
+    _dev(gridf, x16)
+    _ws(x16)
+    P = ctypes.c_void_p * nseg
+    I = ctypes.c_int * nseg
+    call("tlx_pfg3m", P(*[w.data_ptr() for w in ws]), P(*[o.data_ptr() for o in outs]),
+         I(*[o.shape[-1] for o in outs]), I(*[int(t) for t in types]), I(*[int(lay) for lay in layouts]), nseg,
+         gridf.data_ptr(), x16.data_ptr(), M, K, _stream(stream))
+    return outs
+
+
 # ------------------------------------------------------------------ repackers (device to device)
 def pack_iq3_rows(raw, packed, N, K, stream=None):
     """Raw IQ3_XXS rows [N][K/256][98 B] -> packed rows [qs][sw][d] (pack_w1c.pack_iq3)."""
