@@ -137,6 +137,9 @@ def parse():
     ap.add_argument("--cpu-reps", type=int, default=5, help="timed repetitions of each CPU baseline (median)")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the decode-step sweep leg")
+    ap.add_argument("--sweep-only", action="store_true",
+                    help="run only the decode-step sweep (no per-layer-kind graphs) and print its object: "
+                         "the form a counter pass over one step's dispatches uses")
     ap.add_argument("--layout", default="tiled", choices=("tiled", "packed"),
                     help="IQ3_XXS weight layout of the headline ffn8 leg (the other one is "
                          "reported under per_m_other_layout)")
@@ -444,7 +447,7 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
     return out
 
 
-def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True):
+def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True, per_kind_graphs=True):
     """Config 3: the 64-layer dense decode step at M=11 plus the Q6_K head.  With ``tiled`` every
     IQ3_XXS tensor except the k/v rows beside a Q6_K q reads tiled records (repacked on the GPU
     from the packed rows).  The four GDN projections that read the same x share one launch, and
@@ -558,7 +561,7 @@ def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True):
 
     t_step = graph_ms(0, len(calls), steps, warmup)
     per_kind = {}
-    for kind, spans in kinds.items():   # one layer of each kind, replayed
+    for kind, spans in (kinds.items() if per_kind_graphs else ()):   # one layer of each kind, replayed
         lo, hi = spans[0]
         t = graph_ms(lo, hi, steps, warmup)
         per_kind[kind] = {"layers": len(spans), "ms_per_layer": round(t, 4)}
@@ -815,6 +818,10 @@ def main():
     from thunderllamax_amd import formats, ops, synth
 
     dev = torch.device("cuda:0")
+    if args.sweep_only:
+        print(json.dumps({"sweep": sweep_leg(ops, formats, torch, dev, args.steps, args.warmup,
+                                             tiled=args.layout == "tiled", per_kind_graphs=False)}), flush=True)
+        return
     N, K = 17408, 5120
     ms = [int(m) for m in args.ms.split(",")]
     rng = synth.config_rng(2)

@@ -162,7 +162,8 @@ int tlx_a_qkv_q6(const void* wq, const void* wk, const void* wv4, const float* g
 
 /* Q6_K GEMV, fp32 activations and outputs: y[n] = sum_k ((d*sc)*(q-32))[n][k] * x[k].
  * The contract of h6k2048 (engine/mm/MM_P34_h6k2048.cu:8-52): h6k2048(w, x, y, rows),
- * generalised to any K (multiple of 256) and to the raw 210-B / padded 212-B layouts. */
+ * generalised to any K (multiple of 256, at most 15360: x is staged in 64 KB of LDS) and to the
+ * raw 210-B / padded 212-B layouts. */
 int tlx_q6k_gemv(const void* w, const float* x, float* y, int rows, int K, int layout,
                  void* stream);
 

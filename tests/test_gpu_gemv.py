@@ -231,6 +231,36 @@ def test_q6k_gemv_config1(gpu, layout):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("rows,K,layout", [(1000, 2304, LAYOUT_RAW), (37, 12288, LAYOUT_PACKED),
+                                            (333, 15360, LAYOUT_RAW), (5, 256, LAYOUT_PACKED), (4099, 5120, LAYOUT_RAW)])
+def test_q6k_gemv_shapes(gpu, rows, K, layout):
+    """The fp32 GEMV's other paths: a block count that is not a multiple of 4 (blocks past the end
+    weighted 0), several rounds of steps (K > 6144), the largest K (15360: x and its group sums
+    fill 64 KB of LDS), odd row counts (a workgroup's last rows masked) and tiny matrices."""
+    print(f"[case] q6k_gemv rows={rows} K={K} layout={layout}", flush=True)
+    rng = np.random.default_rng(rows + K)
+    raw = synth.q6k_raw(rng, rows, K)
+    x = rng.standard_normal(K).astype(np.float32)
+    host = raw if layout == LAYOUT_RAW else formats.q6_pad_rows(raw, K)
+    y = torch.full((rows + 3,), 7.0, dtype=torch.float32, device=gpu)
+    ops.h6k_gemv(torch.from_numpy(host).to(gpu), torch.from_numpy(x).to(gpu), y[:rows], layout)
+    torch.cuda.synchronize()
+    ref = gemv.q6k_gemv_ref(quants.dequant_q6k(raw, K), x)
+    yy = y.cpu().numpy()
+    assert np.all(yy[rows:] == 7.0)   # nothing past the output
+    err = gemv.rel_err(yy[:rows], ref)
+    print(f"[q6k rows={rows} K={K}] rel-err {err:.3e}")
+    assert err <= TOL
+
+
+def test_q6k_gemv_rejects_k_beyond_lds(gpu):
+    """K = 15616 would need more than 64 KB of staged activations: rejected before any launch."""
+    K = 15616
+    with pytest.raises(TlxError):
+        ops.h6k_gemv(torch.zeros(210 * (K // 256), dtype=torch.uint8, device=gpu), torch.zeros(K, device=gpu),
+                     torch.zeros(1, device=gpu), LAYOUT_RAW)
+
+
 def test_bad_arguments_raise(gpu):
     g = formats.gridf_tensor(gpu)
     w = torch.zeros(16 * 1960, dtype=torch.uint8, device=gpu)

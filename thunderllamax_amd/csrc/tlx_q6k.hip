@@ -62,7 +62,7 @@ __global__ __launch_bounds__(256) void q6k_dequant_kernel(const uint8_t* __restr
 // ------------------------------------------------------------------ fp32 GEMV
 constexpr int kQ6Waves = 4;
 constexpr int kQ6MaxU = 8;      // blocks per wave per round (all their loads in flight together)
-constexpr int kQ6MaxK = 16384;  // x staged in LDS: K floats (64 KB at most)
+constexpr int kQ6MaxK = 15360;  // x staged in LDS: K floats (60 KB at most)
 
 template <int U>
 __global__ __launch_bounds__(kQ6Waves * 64) void q6k_gemv_f32_kernel(const uint8_t* __restrict__ w,
@@ -80,10 +80,15 @@ __global__ __launch_bounds__(kQ6Waves * 64) void q6k_gemv_f32_kernel(const uint8
   const int row = min((int)blockIdx.x * 4 + quarter, rows - 1);
   const uint8_t* rp = w + (size_t)row * bs * nb;
 
-  // x into LDS by DMA (1 KB a wave instruction), issued ahead of the first round's weight loads
-  for (int q = wave; q < nb; q += kQ6Waves)
-    __builtin_amdgcn_global_load_lds((const void*)(x + 256 * q + 4 * lane),
-                                     (__attribute__((address_space(3))) void*)(xs + 256 * q), 16, 0, 0);
+  // x into LDS by DMA (1 KB a wave instruction), issued ahead of the first round's weight loads.
+  // Written out as assembly: the compiler cannot count a loop of DMA loads, so before the first LDS
+  // read of x it would drain every load in flight, the round's weights included; the explicit wait
+  // before the staging barrier below is the one these loads need.
+  for (int q = wave; q < nb; q += kQ6Waves) {
+    const float* src = x + 256 * q + 4 * lane;
+    const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(xs + 256 * q));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(dst) : "memory", "m0");
+  }
   float acc = 0.f;
   int b0 = wave;
   do {   // every wave runs the first round (it holds the staging barrier)
@@ -93,6 +98,7 @@ __global__ __launch_bounds__(kQ6Waves * 64) void q6k_gemv_f32_kernel(const uint8
     uint16_t dh[U];
 #pragma unroll
     for (int j = 0; j < U; ++j) {
+      __builtin_amdgcn_sched_barrier(0);   // block by block, in order: the waits below count them
       const int b = min(b0 + kQ6Waves * j, nb - 1);
       const uint8_t* blk = rp + (size_t)b * bs;
       qla[j] = tlx_ldu<uint32_t>(blk + o.ql + 64 * h + 4 * p);
@@ -101,9 +107,15 @@ __global__ __launch_bounds__(kQ6Waves * 64) void q6k_gemv_f32_kernel(const uint8
       sc8[j] = tlx_ldu<uint64_t>(blk + o.sc + 8 * h);
       dh[j] = tlx_ldu<uint16_t>(blk + o.d);
     }
+    __builtin_amdgcn_sched_barrier(0);
     if (b0 == wave) {
-      __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's DMA pieces have landed
-      __syncthreads();
+      // this wave's DMA pieces have landed; the round's 5U weight loads issued after them need not
+      // have (the barrier is written out without the fence __syncthreads carries, which would drain
+      // them): each block's arithmetic then waits only for that block's loads
+      constexpr int N = 5 * U;
+      static_assert(N <= 63, "vmcnt range");
+      __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+      asm volatile("s_barrier" ::: "memory");
     }
 #pragma unroll
     for (int j = 0; j < U; ++j) {
