@@ -99,19 +99,23 @@ int tlx_iq4xs_dequant(const void* w, const float* iq4nl, float* out, int64_t row
  *   gact[m][n] = silu16(half(Wg[n]·x[m])) * half(Wu[n]·x[m])
  * Replaces ffn8 / ffn8v{3..11} (engine/ffn8.cu:134-185, engine/ffn8v11.cu:88-133):
  * ffn8(wg, wu, gridf, hhx, gact).  wg, wu: N rows x 98*(K/256) B (layout PACKED rows,
- * RAW blocks, or TILED records);
+ * RAW blocks, or TILED records), or the prefill GEMM's PACK7 units (N % 8 == 0, 16-B aligned):
+ * then it replaces the r7 twins ffn8r7 / ffn8v{3,8,11}r7 that read the packed7 plane
+ * (engine/ffn8v11r7.cu:4-16,261; engine/trunk_w1c.py:20-25), bit for bit the packed-row results;
  * gridf: float[1024]; hhx_f16: [M][K]; gact_f16: [M][N]. */
 int tlx_ffn8(const void* wg, const void* wu, const float* gridf, const uint16_t* hhx_f16,
              uint16_t* gact_f16, int M, int N, int K, int layout, void* stream);
 
 /* IQ3_XXS down GEMV + residual:  y[m][n] = hh[m][n] + float(half(Wd[n]·gact[m]))
  * Replaces down8 / down8nw32_{3..11} (engine/down8.cu:134-144,
- * engine/down8nw32_11.cu:88-125): down8(wd, gridf, gact, hh, y). */
+ * engine/down8nw32_11.cu:88-125): down8(wd, gridf, gact, hh, y); with TLX_LAYOUT_PACK7 the r7
+ * twins down8r7 / down8nw32v{3,8,11}r7 (engine/down8nw32v11r7.cu:261).  Layouts as tlx_ffn8. */
 int tlx_down8(const void* wd, const float* gridf, const uint16_t* gact_f16, const float* hh,
               float* y, int M, int N, int K, int layout, void* stream);
 
 /* Plain IQ3_XXS GEMV with fp16 output: out[m][n] = half(W[n]·x[m]).  The per-segment body
- * of the fused attention / GDN projections (IQ3ROWP, engine/aq3k8.cu:99-131). */
+ * of the fused attention / GDN projections (IQ3ROWP, engine/aq3k8.cu:99-131).  Layouts as
+ * tlx_ffn8 (PACKED, RAW, PACK7 or TILED). */
 int tlx_iq3_gemv(const void* w, const float* gridf, const uint16_t* x_f16, uint16_t* out_f16,
                  int M, int N, int K, int layout, void* stream);
 
