@@ -8,10 +8,12 @@ reported under ``per_m``.  A "step" is one ffn8 call over one batch of M activat
 
 Timing: weights are synthetic (seeded) and resident in HBM before timing starts; each step
 reads a different copy out of a rotation larger than the 256 MB Infinity Cache, so the
-figure is HBM bandwidth, not cache bandwidth.  W untimed warmup steps, then exactly K
-timed steps -- captured in one HIP graph, as a decode step replays its launches -- bracketed
-by device synchronization, timed with HIP events recorded on the stream the graph replays on
-(the current stream).
+figure is HBM bandwidth, not cache bandwidth.  W untimed warmup steps, then K timed steps
+(at least 20) captured in one HIP graph, as a decode step replays its launches, and the graph
+replayed 5 times, each replay bracketed by device synchronization and timed with HIP events
+recorded on the stream the graph replays on; ``ms_per_step`` is the median replay / K.
+``roofline.traffic`` (and every leg's) is the HBM bytes per launch measured by rocprofv3
+counters (the ``TRAFFIC`` table below, with the command that measured it).
 The headline layout (``--layout``, default ``tiled``) is the library's tiled records (the GGUF
 blocks re-encoded with precomputed table indices, 102 B per 256 weights, repacked on the GPU);
 ``value`` still counts the GGUF bytes (98 per 256 weights), so it is the rate at which the
@@ -71,32 +73,33 @@ import time
 import numpy as np
 
 PEAK_HBM_GBS = 8000.0
-# HBM bytes per M=11 step (tile-ordered activation copy + ffn8 over packed rows), measured with two
-# `rocprofv3 --pmc` passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --ms 11 --gemm-m 2048 --no-sweep
-# --no-formats --no-cpu --no-config1 --no-stream --steps 10 --warmup 2 --copy-mib 256`; the 256 MiB
-# copy at the end reads FETCH_SIZE = 131,088 KiB and WRITE_SIZE = 262,144 KiB, so fetches are
-# scaled by 2.0, writes by 1.0: (36,300.9 + 65.0) KiB x 2 + (374.0 + 160.0) KiB.  Re-measure when
-# the kernel changes.
-FFN8_M11_TRAFFIC_BYTES = 75_024_128
-# The same for the tiled-record kernel (one launch; FETCH_SIZE 35,843.8 KiB, WRITE_SIZE 1,922.0 KiB
-# at M=11 with the same calibration; profiles/pmc_counters_ffn8_pfgemm_moe.md).
-FFN8_TILED_M11_TRAFFIC_BYTES = 75_376_256
-# The MoE layer's launches (tiled slabs), same passes and calibration (`--gemm-m 0 --no-sweep
-# --no-formats --no-cpu --no-config1 --no-stream --ms 11 --steps 10 --warmup 2 --copy-mib 256`;
-# medians per dispatch, split by launch shape; profiles/moe_layer_config5.md): M=11 (top-8, the
-# pair walk's gate+up and down with the shared expert, combine) FETCH_SIZE 13.5 + 49,375.3 +
-# 25,116.1 + 275.7 KiB x 2, WRITE_SIZE 0.5 + 198.0 + 440.0 + 88.0 KiB; M=2048 (top-8, sort, gate+up,
-# down, the shared expert's two, combine) FETCH_SIZE 349,499.7 KiB x 2, WRITE_SIZE 135,654.7 KiB.
-MOE_M11_TRAFFIC_BYTES = 153_894_605
-MOE_M2048_TRAFFIC_BYTES = 854_685_798
-# Config 1 (q6k_gemv_f32_kernel, one launch) and the prefill GEMMs at M=2048 (kernel + fix-up
-# launch), same calibration (`--gemm-m 2048 --no-stream --no-sweep --no-moe --no-cpu --no-formats
-# --ms 11 --steps 10 --warmup 2 --copy-mib 256`; profiles/pmc_counters_ffn8_pfgemm_moe.md):
-# config 1 FETCH_SIZE 10,682.0 KiB x 2 + WRITE_SIZE 40.0 KiB; gate+up (384,170.0 + 32,795.5) KiB x 2
-# + (131,072.0 + 4,096.0) KiB; down (244,708.8 + 81,948.0) KiB x 2 + (122,880.0 + 40,973.3) KiB.
-CONFIG1_TRAFFIC_BYTES = 21_917_696
-GEMM_FFN_M2048_TRAFFIC_BYTES = 992_357_376
-GEMM_DOWN_M2048_TRAFFIC_BYTES = 836_778_905
+# HBM bytes per launch (roofline.traffic), measured with two `rocprofv3 --pmc` passes over one
+# command, FETCH_SIZE then WRITE_SIZE (KiB per dispatch, medians over each workload's dispatches):
+#   bench.py --ms 11 --gemm-m 2048,8192 --no-sweep --no-formats --no-cpu --no-stream --steps 20
+#            --warmup 3 --copy-mib 256
+# and for the decode step `bench.py --sweep-only --steps 20 --warmup 3` (FETCH_SIZE and WRITE_SIZE
+# summed over the 273 dispatches of one step, median over steps).  The 256 MiB device copy that ends
+# the first command reads FETCH_SIZE = 131,094 KiB and WRITE_SIZE = 262,144 KiB, so fetched bytes =
+# 2 x FETCH_SIZE x 1024 and written bytes = WRITE_SIZE x 1024.  Kernel + its helper launches (the
+# tile-ordered activation copy of the packed-row GEMVs, the prefill GEMM's split-tile fix-up, the
+# int8 quantizer, the MoE layer's router / sort / combine).  Re-measure when a kernel changes.
+TRAFFIC = {
+    "ffn8_m11_tiled": 75_370_291,       # iq3s_kernel<2,1,8,3>: F 35,840.9  W 1,922.0
+    "ffn8_m11_packed": 74_799_514,      # iq3_xt_kernel + iq3_gemv_kernel<2,1,4,0>: F 65.0 + 36,191.2  W 160 + 374
+    "ffn8_m11_pack7": 91_283_251,       # iq3_xt_kernel + iq3_gemv_kernel<2,1,4,1>: F 65.0 + 44,239.9  W 160 + 374
+    "config1": 21_917_696,              # q6k_gemv_f32_kernel<5>: F 10,682.0  W 40.0
+    "gemm_ffn_m2048": 992_334_848,      # pf_gemm<FFN> + pf_fix: F 384,159.0 + 32,795.5  W 131,072 + 4,096
+    "gemm_down_m2048": 836_998_349,     # pf_gemm<RES> + pf_fix: F 244,813.4 + 81,948.0  W 122,880 + 40,978.4
+    "gemm_ffn_m8192": 3_557_484_339,    # pf_gemm<FFN> (no split tiles): F 1,597,788.9  W 278,528
+    "gemm_down_m8192": 1_753_614_131,   # pf_gemm<RES> + pf_fix: F 692,386.6 + 49,180.0  W 196,611.9 + 32,768.7
+    "w4a8_ffn_m2048": 1_595_100_365,    # p8_quant + p8w4_ffn: F 10,256 + 728,025.6  W 11,520 + 69,632
+    "merged_attnqkv_i3": 398_215_168,   # pfm_gemm_kernel: F 165,769.0  W 57,344
+    "merged_attnqkv_q6": 875_961_139,   # pfm_gemm_kernel: F 399,043.4  W 57,344
+    "merged_gdnqg": 568_197_120,        # pfm_gemm_kernel: F 244,672.0  W 65,536
+    "moe_m11": 153_883_750,             # topk + pair-walk gate+up and down (shared inside) + combine: F 74,775.3  W 726.5
+    "moe_m2048": 854_722_048,           # topk, sort, grouped gate+up / down, shared two, combine: F 349,518.3  W 135,652.9
+    "sweep": 12_030_388_122,            # one decode step: F 5,591,363.3  W 565,699.3
+}
 PEAK_F16_TFLOPS = 2500.0
 PEAK_I8_TOPS = 5000.0
 ROT_BYTES = 300 * 2**20
@@ -259,9 +262,9 @@ def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup, weights, w4a8=Tr
         "down_ms": round(t_down, 4), "down_tflops": round(tf_down, 1),
         "tflops": round(tf_layer, 1),
         "roofline": mfma_roofline(tf_ffn, "pf_gemm_kernel<FFN> (+ pf_fix_kernel) gate+up",
-                                  traffic=GEMM_FFN_M2048_TRAFFIC_BYTES if M == 2048 else None,
+                                  traffic=TRAFFIC.get(f"gemm_ffn_m{M}"),
                                   down=mfma_roofline(tf_down, "pf_gemm_kernel<RES> (+ pf_fix_kernel) down",
-                                                     traffic=GEMM_DOWN_M2048_TRAFFIC_BYTES if M == 2048 else None)),
+                                                     traffic=TRAFFIC.get(f"gemm_down_m{M}"))),
     }
     if not w4a8:
         return out
@@ -274,7 +277,8 @@ def gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup, weights, w4a8=Tr
     t_w4 = time_graph(lambda s: ops.p8w4_ffn(pg, pu, lut8, xq, sx, act, stream=s), steps, warmup, torch)
     to_w4 = f_ffn / ((t_q8 + t_w4) * 1e-3) / 1e12
     out["w4a8_ffn"] = {"quant_ms": round(t_q8, 4), "gemm_ms": round(t_w4, 4), "tops": round(to_w4, 1),
-                       "roofline": mfma_roofline(to_w4, "p8_quant_kernel + p8w4_ffn_kernel", PEAK_I8_TOPS, "TOP/s")}
+                       "roofline": mfma_roofline(to_w4, "p8_quant_kernel + p8w4_ffn_kernel", PEAK_I8_TOPS, "TOP/s",
+                                                 traffic=TRAFFIC.get(f"w4a8_ffn_m{M}"))}
     return out
 
 
@@ -314,7 +318,8 @@ def merged_gemm_leg(ops, formats, synth, torch, dev, M, steps, warmup):
         flops = 2.0 * M * K * sum(n for *_, n in mats)
         tf = flops / (t * 1e-3) / 1e12
         out[name] = {"segments": [f"{c} {n}x{K}" for c, n in segs], "ms": round(t, 4), "tflops": round(tf, 1),
-                     "roofline": mfma_roofline(tf, "pfm_gemm_kernel (one launch over the segments)")}
+                     "roofline": mfma_roofline(tf, "pfm_gemm_kernel (one launch over the segments)",
+                                                  traffic=TRAFFIC.get(f"merged_{name}") if M == 2048 else None)}
         del mats, outs
     return out
 
@@ -439,11 +444,11 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
                         **({"ms_sorted_grouped": round(t_grouped, 4)} if walk else {}),
                         "roofline": (hbm_roofline(gbs, f"MoE layer ({route}, combine; graph): "
                                                        "expert weight bytes / layer time",
-                                                  traffic=MOE_M11_TRAFFIC_BYTES if P == 11 else None)
+                                                  traffic=TRAFFIC.get(f"moe_m{P}"))
                                      if P <= 64 else
                                      mfma_roofline(tflops, f"MoE layer ({route}, combine; graph): "
                                                            "2*3*512*2048*9*M / layer time",
-                                                   traffic=MOE_M2048_TRAFFIC_BYTES if P == 2048 else None))}
+                                                   traffic=TRAFFIC.get(f"moe_m{P}")))}
     return out
 
 
@@ -573,7 +578,8 @@ def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True, per_kind_grap
             "weight_gbs": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
             "per_layer_kind": per_kind,
             "roofline": hbm_roofline(gbs, f"decode step: {len(calls)} GEMV launches in one graph "
-                                          "(weight bytes per step / step time)")}
+                                          "(weight bytes per step / step time)",
+                                     traffic=TRAFFIC["sweep"] if tiled else None)}
 
 
 def config1_leg(ops, synth, torch, dev, steps, warmup):
@@ -597,7 +603,7 @@ def config1_leg(ops, synth, torch, dev, steps, warmup):
     gbs = nbytes / (t * 1e-3) / 1e9
     return {"workload": f"Q6_K GEMV {N}x{K}, fp32 x and y (M=1), raw 210-B blocks", "ms": round(t, 5),
             "algorithmic_bytes": nbytes, "gbs": round(gbs, 1), "rotation_copies": len(copies),
-            "roofline": hbm_roofline(gbs, "q6k_gemv_f32_kernel", traffic=CONFIG1_TRAFFIC_BYTES)}
+            "roofline": hbm_roofline(gbs, "q6k_gemv_f32_kernel", traffic=TRAFFIC["config1"])}
 
 
 def stream_leg(ops, torch, dev, steps, warmup):
@@ -905,16 +911,16 @@ def main():
                    "M": int(head), "K": K, "N": 2 * N, "weight_bytes": wbytes,
                    "layout": args.layout, "rotation_copies": ncopy, "parallelism": "single GPU"},
         "per_m": per_m,
-        "per_m_other_layout": {"layout": other, **per_m_other},
+        "per_m_other_layout": {"layout": other, **per_m_other, "traffic_m11": TRAFFIC.get(f"ffn8_m11_{other}")},
         "per_m_pack7": {"layout": "packed7 units (the prefill GEMM's plane; GGUF bytes counted, the plane "
-                                  "holds 128 B per 256 weights)", **per_m_p7},
+                                  "holds 128 B per 256 weights)", **per_m_p7,
+                        "traffic_m11": TRAFFIC["ffn8_m11_pack7"]},
         "timing": TIMING,
         "roofline": hbm_roofline(
             value,
             ("iq3s_kernel<2,1,8,3> (tiled records, activations staged in LDS)" if args.layout == "tiled" else
              "iq3_gemv_kernel<2,1,4> (+ iq3_xt_kernel for M >= 6)"),
-            traffic=(None if head != "11" else
-                     FFN8_TILED_M11_TRAFFIC_BYTES if args.layout == "tiled" else FFN8_M11_TRAFFIC_BYTES),
+            traffic=TRAFFIC.get(f"ffn8_m{head}_{args.layout}"),
             algorithmic_bytes=wbytes + int(head) * K * 2 + int(head) * N * 2),
     }
     if not args.no_stream:
