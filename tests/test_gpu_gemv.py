@@ -236,7 +236,7 @@ def test_q6k_gemv_config1(gpu, layout):
 def test_q6k_gemv_shapes(gpu, rows, K, layout):
     """The fp32 GEMV's other paths: a block count that is not a multiple of 4 (blocks past the end
     weighted 0), several rounds of steps (K > 6144), the largest K (15360: x and its group sums
-    fill 64 KB of LDS), odd row counts (a workgroup's last rows masked) and tiny matrices."""
+    fill 75 KB of LDS, past the 64 KB default limit), odd row counts (a workgroup's last rows masked) and tiny matrices."""
     print(f"[case] q6k_gemv rows={rows} K={K} layout={layout}", flush=True)
     rng = np.random.default_rng(rows + K)
     raw = synth.q6k_raw(rng, rows, K)
@@ -254,7 +254,7 @@ def test_q6k_gemv_shapes(gpu, rows, K, layout):
 
 
 def test_q6k_gemv_rejects_k_beyond_lds(gpu):
-    """K = 15616 would need more than 64 KB of staged activations: rejected before any launch."""
+    """K = 15616 is past the largest K the staged activations are sized for: rejected before any launch."""
     K = 15616
     with pytest.raises(TlxError):
         ops.h6k_gemv(torch.zeros(210 * (K // 256), dtype=torch.uint8, device=gpu), torch.zeros(K, device=gpu),
