@@ -410,6 +410,50 @@ int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const float* iq4nl,
 int tlx_moe_combine(const uint16_t* parts, const float* gates, const float* sg, const float* shared,
                     const float* hres, float* y, int P, void* stream);
 
+/* ---- The MoE weight classes of the reference's real checkpoint (Qwen3.6-35B-A3B): IQ3_S routed
+ * gate/up, Q6_K routed down (3 of 40 layers), Q8_0 shared expert.  Operands are fp16 of the fp32
+ * GGUF values, f32 accumulation (results within rel-err 1e-3 of the float64 products; the
+ * reference's decode forms accumulate in fp32 FMA-free, its prefill forms in fp16 MMA).  Slabs as
+ * the reference's: IQ3_S gate/up slab = 512 gate rows, then 512 up rows from byte 450,560, 880 B a
+ * row (k = 2048); Q6_K down slab = 2048 rows of 420 B (raw 210-B blocks, k = 512); slab addresses
+ * 2-B aligned.  gridf: the IQ3_S grid as float[512][4], passed at run time as by the reference.
+ * np = number of pairs (8 per position), <= 16384; the sorted forms take tlx_moe_sort's eoff / plist. */
+
+/* IQ3_S dequant (dq_iq3_s, engine/mm/MM_P0_d2_repack.py:95-120): 110-B blocks
+ * [d f16][qs 64][qh 8][signs 32][scales 4]; out f32 or (out_f16) fp16 [rows][kdim], kdim % 256. */
+int tlx_iq3s_dequant(const void* w, const float* gridf, void* out, int64_t rows, int64_t kdim, int out_f16,
+                     void* stream);
+/* Q8_0 dequant (dq_q8_0, engine/mm/MM_P2_ports.py:47-54): 34-B blocks [d f16][q i8 32], y = d * q;
+ * kdim % 256. */
+int tlx_q8_0_dequant(const void* w, void* out, int64_t rows, int64_t kdim, int out_f16, void* stream);
+
+/* IQ3_S grouped gate+up + SwiGLU over the sorted pairs: ys[pair][512] f32 =
+ * silu(Wg_e . x[pair >> 3]) * (Wu_e . x[pair >> 3]).  Replaces gxu_gm
+ * (engine/mm/MM_E_gxu_gm.cu:86-93): gxu_gm(ptbl, eoff, plist, xs f32[P][2048], gridf, ys). */
+int tlx_moe_up3s(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const float* xs,
+                 const float* gridf, float* ys, int np, void* stream);
+/* Pair-walk form (no sort): pair p runs expert eids[p].  Replaces gx8e256up
+ * (engine/mm/MM_P1_gx8e256up.cu:15-20): gx8e256up(ptbl, eids, xs, gridf, ys).  Bit-identical to
+ * tlx_moe_up3s on the same pairs. */
+int tlx_moe_up3s_pairs(const uint64_t* ptbl, const uint16_t* eids, const float* xs, const float* gridf,
+                       float* ys, int np, void* stream);
+/* Q6_K grouped down over the sorted pairs: parts[pair][2048] = fp16(Wd_e . act[pair]).  Replaces
+ * gxm_dn6 (engine/mm/MM_B_gxm_dn6.cu:18-25): gxm_dn6(ptbl, items, nitp, eoff, plist,
+ * xs = act f32[NPAIR][512], parts), same positional order; items / nitp are accepted (may be null)
+ * and not read: this form walks eoff / plist. */
+int tlx_moe_dn6(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
+                const uint16_t* plist, const float* act, uint16_t* parts, int np, void* stream);
+/* Pair-walk form: replaces gx8e256dn6 (engine/mm/MM_P2_gx8e256dn6.cu:9-13):
+ * gx8e256dn6(ptbl, eids, xs = act, parts).  Bit-identical to tlx_moe_dn6 on the same pairs. */
+int tlx_moe_dn6_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, uint16_t* parts,
+                      int np, void* stream);
+/* The Q8_0 shared expert over P positions: y[P][2048] f32 = Wd . (silu(Wg . x) * (Wu . x)), with act
+ * f32[P][512] caller scratch (two launches on the stream).  Replaces shexp8
+ * (engine/mm/MM_P2_shexp8.cu:8-13): shexp8(wg [512][2176], wu [512][2176], wd [2048][544], x, y).
+ * x and act 16-B aligned. */
+int tlx_moe_shared8(const void* wg, const void* wu, const void* wd, const float* x, float* y, float* act, int P,
+                    void* stream);
+
 /* ---- Measurement.
  * HBM read-stream probe (the measured bandwidth ceiling the benchmark states GEMV throughput
  * against, beside the datasheet figure; the reference's counterpart is its read-stream tool

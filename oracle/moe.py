@@ -78,8 +78,14 @@ def up_ref(slab_gate_up, x):
     slab = np.ascontiguousarray(slab_gate_up, dtype=np.uint8)
     Wg = quants.dequant_iq4xs(slab[:GATE_BYTES].reshape(FF, IQ4_ROW_UP), HID)
     Wu = quants.dequant_iq4xs(slab[GATE_BYTES:2 * GATE_BYTES].reshape(FF, IQ4_ROW_UP), HID)
+    return swiglu_ref(Wg, Wu, x)
+
+
+def swiglu_ref(Wg, Wu, x):
+    """``silu(Wg . x) * (Wu . x)`` in float64 on dequantized gate / up rows of any weight class
+    (the gate+up body every expert kernel shares; up_ref is this on IQ4_XS slabs)."""
     x = np.asarray(x, np.float64)
-    return silu64(x @ Wg.astype(np.float64).T) * (x @ Wu.astype(np.float64).T)
+    return silu64(x @ np.asarray(Wg, np.float64).T) * (x @ np.asarray(Wu, np.float64).T)
 
 
 def down_ref(slab_down, act):
@@ -88,6 +94,39 @@ def down_ref(slab_down, act):
     [T, 2048]."""
     Wd = quants.dequant_iq4xs(np.ascontiguousarray(slab_down, dtype=np.uint8).reshape(HID, IQ4_ROW_DN), FF)
     return np.asarray(act, np.float64) @ Wd.astype(np.float64).T
+
+
+# The checkpoint's classes (the same math on other dequantizers): IQ3_S gate/up slabs of
+# 2 x 512 rows x 880 B (gxu_gm / gx8e256up, /root/reference/engine/mm/MM_E_gxu_gm.cu:86-93,
+# GATE_B = 450560), Q6_K down slabs of 2048 rows x 420 B (gxm_dn6 / gx8e256dn6,
+# /root/reference/engine/mm/MM_B_gxm_dn6.cu:18-25), the Q8_0 shared expert (shexp8,
+# /root/reference/engine/mm/MM_P2_shexp8.cu:8-13).
+IQ3S_ROW_UP = 8 * quants.IQ3S_BYTES
+IQ3S_GATE_BYTES = FF * IQ3S_ROW_UP
+Q6K_ROW_DN = 2 * quants.Q6K_BYTES
+
+
+def up3s_ref(slab_gate_up, grid, x):
+    """One IQ3_S expert's gate+up + SwiGLU, float64: x [T, 2048] -> act [T, 512]."""
+    slab = np.ascontiguousarray(slab_gate_up, dtype=np.uint8)
+    Wg = quants.dequant_iq3s(slab[:IQ3S_GATE_BYTES].reshape(FF, IQ3S_ROW_UP), HID, grid)
+    Wu = quants.dequant_iq3s(slab[IQ3S_GATE_BYTES:2 * IQ3S_GATE_BYTES].reshape(FF, IQ3S_ROW_UP), HID, grid)
+    return swiglu_ref(Wg, Wu, x)
+
+
+def down6_ref(slab_down, act):
+    """One Q6_K expert's down projection, float64: act [T, 512] -> [T, 2048]."""
+    Wd = quants.dequant_q6k(np.ascontiguousarray(slab_down, dtype=np.uint8).reshape(HID, Q6K_ROW_DN), FF)
+    return np.asarray(act, np.float64) @ Wd.astype(np.float64).T
+
+
+def shared8_ref(wg, wu, wd, x):
+    """The Q8_0 shared expert over positions x [P, 2048]: ``y = Wd . (silu(Wg . x) * (Wu . x))``,
+    float64 -> [P, 2048]."""
+    Wg = quants.dequant_q8_0(wg, HID)
+    Wu = quants.dequant_q8_0(wu, HID)
+    Wd = quants.dequant_q8_0(wd, FF)
+    return swiglu_ref(Wg, Wu, x) @ Wd.astype(np.float64).T
 
 
 def combine_ref(parts, gates, sg, shared, hres):

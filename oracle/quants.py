@@ -15,6 +15,8 @@ Q6K_PAD_BYTES = 212              # pad[2] | d f16 | sc[16] | ql[128] | qh[64]
 IQ4XS_BYTES = 136                # d f16 | scales_h u16 | scales_l[4] | qs[128]
 Q4K_BYTES = 144                  # d f16 | dmin f16 | scales[12] | qs[128]
 Q5K_BYTES = 176                  # d f16 | dmin f16 | scales[12] | qh[32] | qs[128]
+IQ3S_BYTES = 110                 # d f16 | qs[64] | qh[8] | signs[32] | scales[4]
+Q80_BYTES = 34                   # d f16 | q i8[32]  (32 weights per block)
 
 
 def _grid_f32():
@@ -385,3 +387,88 @@ def dequant_q5k_lanes(raw, kdim):
     """Q5_K rows -> float32 via the per-lane form of Q5ROW (/root/reference/engine/head8.cu:
     68-90): as Q4_K with qs at byte 48, plus bit (l>>2) of qh byte 16 + 8(l&3) + j as q's bit 4."""
     return _kq_dequant_lanes(raw, kdim, True)
+
+
+# --------------------------------------------------------------------------- IQ3_S
+# The MoE checkpoint's routed gate/up class.  Its 512-entry grid is a third-party table (ggml's
+# iq3s_grid, which the reference reaches through tinygrad's ggml bindings and passes to its
+# kernels at run time as gridf float[512][4]); it is absent here, so every function takes the
+# grid as an argument and the tests run on synthetic grids.
+def dequant_iq3s(raw, kdim, grid):
+    """IQ3_S rows u8[N, 110*NB] -> float32[N, kdim], grid float32[512, 4].
+
+    Restates ``dq_iq3_s`` of /root/reference/engine/mm/MM_P0_d2_repack.py:95-120: sub-block pair
+    ``p`` has ``db1 = d*(1 + 2*(sc[p] & 0xF))``, ``db2 = d*(1 + 2*(sc[p] >> 4))``; half ``h`` of it
+    (sub-block 2p+h, 32 weights) reads index bytes ``qs[16p + 8h ..]``, high-bit byte
+    ``qh[2p+h]`` and sign bytes ``signs[8p + 4h ..]``; group ``l`` (8 weights) takes indices
+    ``ia = qs[2l] | ((qh << (8-2l)) & 256)``, ``ib = qs[2l+1] | ((qh << (7-2l)) & 256)`` and
+    ``y = db * grid[ia] | db * grid[ib]``, negated where bit j of ``signs[l]`` is set.
+    """
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    G = np.asarray(grid, np.float32).reshape(512, 4)
+    n = raw.shape[0]
+    nb = kdim >> 8
+    assert raw.shape[1] == IQ3S_BYTES * nb, raw.shape
+    blk = raw.reshape(n, nb, IQ3S_BYTES)
+    d = _f16(blk[:, :, 0:2])
+    qs, qh, signs, sc = blk[:, :, 2:66], blk[:, :, 66:74], blk[:, :, 74:106], blk[:, :, 106:110]
+    km = (1 << np.arange(8)).astype(np.uint8)
+    y = np.empty((n, nb, 8, 32), dtype=np.float32)
+    l = np.arange(4)
+    for p in range(4):
+        for h in range(2):
+            db = d * (1 + 2 * ((sc[:, :, p] >> (4 * h)) & 0xF)).astype(np.float32)
+            hb = qh[:, :, 2 * p + h].astype(np.int64)
+            q = qs[:, :, 16 * p + 8 * h:16 * p + 8 * h + 8].astype(np.int64)
+            sg = signs[:, :, 8 * p + 4 * h:8 * p + 4 * h + 4]
+            ia = q[:, :, 0:8:2] | ((hb[:, :, None] << (8 - 2 * l)) & 256)
+            ib = q[:, :, 1:8:2] | ((hb[:, :, None] << (7 - 2 * l)) & 256)
+            neg = (sg[:, :, :, None] & km[None, None, None, :]) != 0
+            sgn = np.where(neg, np.float32(-1.0), np.float32(1.0))
+            yy = np.empty((n, nb, 4, 8), dtype=np.float32)
+            yy[:, :, :, 0:4] = db[:, :, None, None] * G[ia] * sgn[:, :, :, 0:4]
+            yy[:, :, :, 4:8] = db[:, :, None, None] * G[ib] * sgn[:, :, :, 4:8]
+            y[:, :, 2 * p + h] = yy.reshape(n, nb, 32)
+    return y.reshape(n, kdim)
+
+
+def dequant_iq3s_lanes(raw, kdim, grid):
+    """IQ3_S rows -> float32 via the per-weight form of ``gxu_gm``'s tile staging
+    (/root/reference/engine/mm/MM_E_gxu_gm.cu:57-84): weight k of a block (kib = k & 255) uses
+    index byte ``g = kib >> 2``: ``qb = qs[g] + (((qh[g >> 3] >> (g & 7)) & 1) << 8)``, grid entry
+    ``grid[qb][kib & 3]``, scale nibble ``(sc[kib >> 6] >> 4((kib >> 5) & 1)) & 0xF`` as
+    ``ds = d * (1 + 2*nib)``, and sign bit ``kib & 7`` of ``signs[kib >> 3]``: ``w = +-ds * g``."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    G = np.asarray(grid, np.float32).reshape(512, 4)
+    n = raw.shape[0]
+    nb = kdim >> 8
+    out = np.empty((n, kdim), dtype=np.float32)
+    for r in range(n):
+        for b in range(nb):
+            blk = raw[r, b * IQ3S_BYTES:(b + 1) * IQ3S_BYTES]
+            d = np.float32(blk[0:2].view(np.float16)[0])
+            for kib in range(256):
+                g = kib >> 2
+                qb = int(blk[2 + g]) + (((int(blk[66 + (g >> 3)]) >> (g & 7)) & 1) << 8)
+                s_ = kib >> 5
+                nib = (int(blk[106 + (s_ >> 1)]) >> (4 * (s_ & 1))) & 0xF
+                ds = np.float32(d * np.float32(1.0 + 2.0 * nib))
+                w = np.float32(ds * G[qb, kib & 3])
+                if (int(blk[74 + (kib >> 3)]) >> (kib & 7)) & 1:
+                    w = -w
+                out[r, 256 * b + kib] = w
+    return out
+
+
+# --------------------------------------------------------------------------- Q8_0
+def dequant_q8_0(raw, kdim):
+    """Q8_0 rows u8[N, 34*(kdim/32)] -> float32[N, kdim]: ``y = d * q`` per 32-weight block
+    (``dq_q8_0``, /root/reference/engine/mm/MM_P2_ports.py:47-54; the shared expert's class)."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    n = raw.shape[0]
+    nb = kdim >> 5
+    assert raw.shape[1] == Q80_BYTES * nb, raw.shape
+    blk = raw.reshape(n, nb, Q80_BYTES)
+    d = _f16(blk[:, :, 0:2])
+    q = blk[:, :, 2:34].astype(np.int8).astype(np.float32)
+    return (d[:, :, None] * q).reshape(n, kdim)

@@ -129,3 +129,21 @@ def test_pfg3m_argument_validation():
     assert rc((256, 256, 256), (_lib.TYPE_Q6_K,) * 3, (_lib.LAYOUT_RAW,) * 3) == _lib.TLX_E_ARG  # Q6_K: padded
     assert rc((256, 256, 256), (23,) * 3, (_lib.LAYOUT_RAW,) * 3) == _lib.TLX_E_ARG  # IQ4_XS: not a class
     assert rc((256, 256, 256), ok_t, ok_l, x=p + 2) == _lib.TLX_E_ALIGN
+
+
+def test_moe_checkpoint_classes_argument_validation():
+    """The IQ3_S / Q6_K / Q8_0 expert entry points and dequantizers reject bad sizes and alignment
+    before any launch."""
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(64)
+    p = (ctypes.addressof(buf) + 15) & ~15
+    assert L.tlx_moe_up3s(p, p, p, p, p, p, 0, None) == _lib.TLX_E_ARG          # no pairs
+    assert L.tlx_moe_up3s(p, p, p, p, p, p, 16385, None) == _lib.TLX_E_ARG      # more than the sort supports
+    assert L.tlx_moe_up3s(p, p, p, p + 4, p, p, 8, None) == _lib.TLX_E_ALIGN    # xs 16-B aligned
+    assert L.tlx_moe_up3s_pairs(p, p, p, p + 8, p, 8, None) == _lib.TLX_E_ALIGN # gridf 16-B aligned
+    assert L.tlx_moe_dn6(p, None, None, p, p, p, p, 0, None) == _lib.TLX_E_ARG
+    assert L.tlx_moe_dn6_pairs(p, p, p + 4, p, 8, None) == _lib.TLX_E_ALIGN
+    assert L.tlx_moe_shared8(p, p, p, p, p, p, 0, None) == _lib.TLX_E_ARG
+    assert L.tlx_moe_shared8(p, p, p, p, p, p + 4, 4, None) == _lib.TLX_E_ALIGN  # act 16-B aligned
+    assert L.tlx_iq3s_dequant(p, p, p, 1, 384, 0, None) == _lib.TLX_E_ARG        # kdim % 256
+    assert L.tlx_q8_0_dequant(p + 1, p, 1, 256, 0, None) == _lib.TLX_E_ALIGN

@@ -1,0 +1,166 @@
+"""The MoE weight classes of the reference's real checkpoint on the GPU against the oracle: IQ3_S
+routed gate/up (gxu_gm / gx8e256up), Q6_K routed down (gxm_dn6 / gx8e256dn6), the Q8_0 shared
+expert (shexp8), and the IQ3_S / Q8_0 dequantizers.
+
+* Dequantizers: bit for bit against quants.dequant_iq3s / dequant_q8_0 (f32), and the f16 outputs
+  against the same values rounded by numpy (round to nearest even).
+* Expert GEMMs: norm-wise rel-err <= 1e-3 per output row against the float64 products of the
+  dequantized weights (moe.up3s_ref / down6_ref / shared8_ref); the pair walk and the sorted form
+  bit for bit equal; two calls bit for bit equal.
+* The IQ3_S grid is synthetic (synth.iq3s_grid: ggml's level set, random entries): the real table
+  is a third-party constant absent here, and the kernels take it at run time as the reference's do.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemv, moe, quants
+from thunderllamax_amd import formats, ops, synth
+from thunderllamax_amd._lib import TlxError, call
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _rows_err(y, ref):
+    return max(gemv.rel_err(y[i], ref[i]) for i in range(ref.shape[0]))
+
+
+@pytest.fixture(scope="module")
+def ckpt(gpu):
+    rng = np.random.default_rng(20261205)
+    gu, dn, shared = synth.moe_ckpt_slabs(rng, moe.E)
+    grid = synth.iq3s_grid(rng)
+    dgu = [torch.from_numpy(s).to(gpu) for s in gu]
+    ddn = [torch.from_numpy(s).to(gpu) for s in dn]
+    return {
+        "gu": gu, "dn": dn, "shared": shared, "grid": grid, "dgu": dgu, "ddn": ddn,
+        "ptbl": formats.pointer_table(dgu, gpu), "ptbl_dn": formats.pointer_table(ddn, gpu),
+        "gridf": torch.from_numpy(grid.reshape(-1)).to(gpu),
+        "dsh": [torch.from_numpy(np.ascontiguousarray(a).reshape(-1)).to(gpu) for a in shared],
+    }
+
+
+def test_iq3s_dequant_bit_exact(gpu):
+    print("[case] iq3s dequant 37 x 2048", flush=True)
+    rng = np.random.default_rng(41)
+    raw = synth.iq3s_raw(rng, 37, 2048)
+    grid = synth.iq3s_grid(rng)
+    want = quants.dequant_iq3s(raw, 2048, grid)
+    w = torch.from_numpy(raw.reshape(-1)).to(gpu)
+    g = torch.from_numpy(grid.reshape(-1)).to(gpu)
+    o32 = ops.iq3s_dequant(w, g, torch.empty(37, 2048, dtype=torch.float32, device=gpu), 2048)
+    o16 = ops.iq3s_dequant(w, g, torch.empty(37, 2048, dtype=torch.float16, device=gpu), 2048)
+    torch.cuda.synchronize()
+    assert np.array_equal(o32.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(o16.cpu().numpy().view(np.uint16), want.astype(np.float16).view(np.uint16))
+
+
+def test_q80_dequant_bit_exact(gpu):
+    print("[case] q8_0 dequant 29 x 512", flush=True)
+    raw = synth.q80_raw(np.random.default_rng(42), 29, 512)
+    want = quants.dequant_q8_0(raw, 512)
+    w = torch.from_numpy(raw.reshape(-1)).to(gpu)
+    o32 = ops.q8_0_dequant(w, torch.empty(29, 512, dtype=torch.float32, device=gpu), 512)
+    o16 = ops.q8_0_dequant(w, torch.empty(29, 512, dtype=torch.float16, device=gpu), 512)
+    torch.cuda.synchronize()
+    assert np.array_equal(o32.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(o16.cpu().numpy().view(np.uint16), want.astype(np.float16).view(np.uint16))
+
+
+def _route(gpu, rng, P):
+    x = synth.bf16_round(0.05 * rng.standard_normal((P, moe.HID)).astype(np.float32))
+    eids_ref, _ = moe.topk_ref(rng.standard_normal((P, moe.E)).astype(np.float32))
+    np_ = 8 * P
+    eids = torch.from_numpy(eids_ref.reshape(-1).view(np.int16)).to(gpu)
+    eoff = torch.empty(257, dtype=torch.int32, device=gpu)
+    plist = torch.empty(np_, dtype=torch.int16, device=gpu)
+    items = torch.empty(ops.moe_max_items(np_), dtype=torch.int32, device=gpu)
+    nitp = torch.empty(1, dtype=torch.int32, device=gpu)
+    ops.moe_sort(eids, eoff, plist, items, nitp)
+    return x, eids_ref.reshape(-1), eids, eoff, plist, items, nitp
+
+
+def _run(gpu, ck, x, eids, eoff, plist, items, nitp, np_):
+    dx = torch.from_numpy(x).to(gpu)
+    act = torch.empty(np_, moe.FF, dtype=torch.float32, device=gpu)
+    act_w = torch.empty_like(act)
+    ops.moe_up3s(ck["ptbl"], eoff, plist, dx, ck["gridf"], act)
+    ops.moe_up3s_pairs(ck["ptbl"], eids, dx, ck["gridf"], act_w)
+    parts = torch.empty(np_, moe.HID, dtype=torch.float16, device=gpu)
+    parts_w = torch.empty_like(parts)
+    ops.moe_dn6(ck["ptbl_dn"], items, nitp, eoff, plist, act, parts)
+    ops.moe_dn6_pairs(ck["ptbl_dn"], eids, act, parts_w)
+    torch.cuda.synchronize()
+    return act.cpu().numpy(), act_w.cpu().numpy(), parts.cpu().numpy(), parts_w.cpu().numpy()
+
+
+def _check_pairs(ck, x, eids, act, parts, pairs):
+    by_e = {}
+    for p in pairs:
+        by_e.setdefault(int(eids[p]), []).append(p)
+    for e, prs in by_e.items():
+        ref = moe.up3s_ref(ck["gu"][e], ck["grid"], x[[p // 8 for p in prs]])
+        assert _rows_err(act[prs], ref) <= TOL, e
+        part = moe.down6_ref(ck["dn"][e], act[prs])
+        assert _rows_err(parts[prs].astype(np.float64), part) <= TOL, e
+
+
+def test_ckpt_experts_decode_m11(gpu, ckpt):
+    print("[case] IQ3_S up + Q6_K down, P=11, every pair", flush=True)
+    rng = np.random.default_rng(43)
+    P = 11
+    x, eids, deids, eoff, plist, items, nitp = _route(gpu, rng, P)
+    act, act_w, parts, parts_w = _run(gpu, ckpt, x, deids, eoff, plist, items, nitp, 8 * P)
+    assert np.array_equal(act.view(np.uint32), act_w.view(np.uint32))
+    assert np.array_equal(parts.view(np.uint16), parts_w.view(np.uint16))
+    _check_pairs(ckpt, x, eids, act, parts, list(range(8 * P)))
+
+
+def test_ckpt_experts_prefill_m2048(gpu, ckpt):
+    print("[case] IQ3_S up + Q6_K down, P=2048, sampled pairs", flush=True)
+    rng = np.random.default_rng(44)
+    P = 2048
+    x, eids, deids, eoff, plist, items, nitp = _route(gpu, rng, P)
+    act, act_w, parts, parts_w = _run(gpu, ckpt, x, deids, eoff, plist, items, nitp, 8 * P)
+    assert np.array_equal(act.view(np.uint32), act_w.view(np.uint32))
+    assert np.array_equal(parts.view(np.uint16), parts_w.view(np.uint16))
+    again = _run(gpu, ckpt, x, deids, eoff, plist, items, nitp, 8 * P)
+    assert np.array_equal(again[0].view(np.uint32), act.view(np.uint32))
+    assert np.array_equal(again[2].view(np.uint16), parts.view(np.uint16))
+    # the largest bins (several 64-token passes) and a spread of others
+    cnt = np.bincount(eids, minlength=moe.E)
+    big = np.argsort(-cnt)[:2]
+    pairs = [int(p) for e in big for p in np.nonzero(eids == e)[0][::7]]
+    pairs += [int(p) for p in np.random.default_rng(5).choice(8 * P, 48, replace=False)]
+    _check_pairs(ckpt, x, eids, act, parts, sorted(set(pairs)))
+
+
+@pytest.mark.parametrize("P", [11, 300])
+def test_ckpt_shared_q80(gpu, ckpt, P):
+    print(f"[case] Q8_0 shared expert P={P}", flush=True)
+    rng = np.random.default_rng(45 + P)
+    x = synth.bf16_round(0.05 * rng.standard_normal((P, moe.HID)).astype(np.float32))
+    dx = torch.from_numpy(x).to(gpu)
+    act = torch.empty(P, moe.FF, dtype=torch.float32, device=gpu)
+    y = torch.empty(P, moe.HID, dtype=torch.float32, device=gpu)
+    ops.moe_shared8(*ckpt["dsh"], dx, y, act)
+    torch.cuda.synchronize()
+    wg, wu, wd = ckpt["shared"]
+    ref = moe.shared8_ref(wg, wu, wd, x)
+    assert _rows_err(y.cpu().numpy(), ref) <= TOL
+
+
+def test_ckpt_argument_validation(gpu, ckpt):
+    dx = torch.zeros(2, moe.HID, device=gpu)
+    act = torch.empty(16, moe.FF, dtype=torch.float32, device=gpu)
+    eids = torch.zeros(16, dtype=torch.int16, device=gpu)
+    with pytest.raises(ValueError):   # xs too small for 24 pairs (3 positions)
+        ops.moe_up3s_pairs(ckpt["ptbl"], torch.zeros(24, dtype=torch.int16, device=gpu), dx, ckpt["gridf"],
+                           torch.empty(24, moe.FF, dtype=torch.float32, device=gpu))
+    with pytest.raises(TlxError):     # xs not 16-B aligned
+        call("tlx_moe_up3s_pairs", ckpt["ptbl"].data_ptr(), eids.data_ptr(), dx.data_ptr() + 8,
+             ckpt["gridf"].data_ptr(), act.data_ptr(), 16, None)
+    with pytest.raises(TlxError):     # more pairs than the sort supports
+        call("tlx_moe_dn6_pairs", ckpt["ptbl_dn"].data_ptr(), eids.data_ptr(), act.data_ptr(), act.data_ptr(),
+             16385, None)

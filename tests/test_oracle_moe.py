@@ -73,6 +73,48 @@ def test_expert_ffn_closed_form():
     np.testing.assert_allclose(part, np.repeat(13.0 * act.sum(axis=1)[:, None], moe.HID, axis=1), rtol=1e-12)
 
 
+def _const_iq3s_rows(rows, kdim, nib):
+    """IQ3_S rows whose weights are all d (1 + 2 nib) * grid[0][c] with d = 1/64 and no signs."""
+    blk = np.zeros(110, np.uint8)
+    blk[0:2] = np.array([1 / 64], np.float16).view(np.uint8)
+    blk[106:110] = nib | (nib << 4)
+    return np.tile(blk, (rows, kdim // 256))
+
+
+def _const_q80_rows(rows, kdim, q):
+    blk = np.zeros(34, np.uint8)
+    blk[0:2] = np.array([1 / 64], np.float16).view(np.uint8)
+    blk[2:34] = np.int8(q).view(np.uint8)
+    return np.tile(blk, (rows, kdim // 32))
+
+
+def test_checkpoint_classes_closed_form():
+    """IQ3_S gate+up (grid all ones: gate nibble 0 -> d, up nibble 1 -> 3d, so act = silu(ds) * 3ds
+    and a swap of the halves or a wrong 450,560-B offset fails), Q6_K down (q = 33, sc = 1,
+    d = 1/16: every weight 1/16), the Q8_0 shared expert (q = 2, 3, 5 for gate, up, down)."""
+    grid = np.ones((512, 4), np.float32)
+    gu = np.concatenate([_const_iq3s_rows(moe.FF, moe.HID, 0).ravel(), _const_iq3s_rows(moe.FF, moe.HID, 1).ravel()])
+    x = 0.5 * np.random.default_rng(4).standard_normal((3, moe.HID))
+    s = x.sum(axis=1) / 64
+    act = moe.up3s_ref(gu, grid, x)
+    np.testing.assert_allclose(act, np.repeat((s / (1 + np.exp(-s)) * 3 * s)[:, None], moe.FF, axis=1), rtol=1e-12)
+    swapped = (3 * s / (1 + np.exp(-3 * s))) * s
+    assert np.all(np.abs(act[:, 0] - swapped) > 1e-3 * np.abs(swapped))
+    q6 = np.zeros(210, np.uint8)
+    q6[0:128] = 0x11            # ql nibbles 1
+    q6[128:192] = 0xAA          # qh: 2 in every 2-bit field -> q = 1 | 32 = 33
+    q6[192:208] = 1             # sc = 1
+    q6[208:210] = np.array([1 / 16], np.float16).view(np.uint8)
+    dn = np.tile(q6, (moe.HID, moe.FF // 256))
+    part = moe.down6_ref(dn, act)
+    np.testing.assert_allclose(part, np.repeat(act.sum(axis=1)[:, None] / 16, moe.HID, axis=1), rtol=1e-12)
+    wg, wu, wd = _const_q80_rows(moe.FF, moe.HID, 2), _const_q80_rows(moe.FF, moe.HID, 3), _const_q80_rows(moe.HID, moe.FF, 5)
+    g, u = 2 * x.sum(axis=1) / 64, 3 * x.sum(axis=1) / 64
+    y = moe.shared8_ref(wg, wu, wd, x)
+    np.testing.assert_allclose(y, np.repeat((5 / 64 * moe.FF * g / (1 + np.exp(-g)) * u)[:, None], moe.HID, axis=1),
+                               rtol=1e-12)
+
+
 def test_combine_one_hot_gates():
     rng = np.random.default_rng(3)
     P = 5

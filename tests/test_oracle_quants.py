@@ -222,3 +222,78 @@ def test_k4_two_restatements_agree(five, rows, kdim):
     a = (quants.dequant_q5k if five else quants.dequant_q4k)(raw, kdim)
     b = (quants.dequant_q5k_lanes if five else quants.dequant_q4k_lanes)(raw, kdim)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ----------------------------------------------------------------------------- IQ3_S
+def _grid_ramp():
+    """grid[i] = (i, i+0.25, i+0.5, i+0.75) / 4: every entry and lane distinct, so a wrong index,
+    lane or high bit shows up as a wrong value."""
+    i = np.arange(512, dtype=np.float32)[:, None]
+    return (i + np.array([0, 0.25, 0.5, 0.75], np.float32)) / 4
+
+
+def _iq3s_block():
+    b = np.zeros(110, np.uint8)
+    b[0:2] = F16_ONE
+    return b
+
+
+def test_iq3s_known_answer_index_high_bit_sign_scale():
+    g = _grid_ramp()
+    b = _iq3s_block()
+    b[2] = 5            # sub-block 0, index byte 0 -> weights 0..3: grid[5]
+    b[3] = 7            # index byte 1 -> weights 4..7: grid[7 | 256] (qh bit 1 below)
+    b[66] = 0b10        # qh[0]: bit 1 -> index byte 1 gains 256
+    b[74] = 0b0110_0001  # signs[0]: weights 0, 5, 6 negative
+    b[106] = 0x3 | (0x7 << 4)   # scales[0]: sub-block 0 nibble 3 -> db = 7; sub-block 1 nibble 7 -> 15
+    b[2 + 8] = 9        # sub-block 1 index byte 0 -> weights 32..35: grid[9] * 15
+    w = quants.dequant_iq3s(b[None], 256, g)[0]
+    assert np.array_equal(w[0:4], 7 * g[5] * np.array([-1, 1, 1, 1], np.float32))
+    assert np.array_equal(w[4:8], 7 * g[7 + 256] * np.array([1, -1, -1, 1], np.float32))
+    assert np.array_equal(w[8:32], np.tile(7 * g[0], 6))   # index bytes 2..7 are 0
+    assert np.array_equal(w[32:36], 15 * g[9])
+    assert np.array_equal(w[64:96], np.tile(g[0], 8))   # pair 1: scales[1] = 0 -> db = 1
+
+
+def test_iq3s_all_signs_and_high_bits():
+    """Each of the 256 sign bits flips exactly its own weight; each of the 64 high bits moves exactly
+    its own index byte's 4 weights to the upper half of the grid."""
+    g = _grid_ramp()
+    base = quants.dequant_iq3s(_iq3s_block()[None], 256, g)[0]
+    for bit in range(256):
+        b = _iq3s_block()
+        b[74 + bit // 8] = 1 << (bit % 8)
+        w = quants.dequant_iq3s(b[None], 256, g)[0]
+        want = base.copy()
+        want[bit] = -want[bit]
+        assert np.array_equal(w, want), bit
+    for q in range(64):
+        b = _iq3s_block()
+        b[66 + q // 8] = 1 << (q % 8)
+        w = quants.dequant_iq3s(b[None], 256, g)[0]
+        want = base.copy()
+        want[4 * q:4 * q + 4] = g[256]
+        assert np.array_equal(w, want), q
+
+
+@pytest.mark.parametrize("rows,kdim", [(3, 512), (1, 2048)])
+def test_iq3s_two_restatements_agree(rows, kdim):
+    rng = np.random.default_rng(31 + rows)
+    raw = synth.iq3s_raw(rng, rows, kdim)
+    g = synth.iq3s_grid(rng)
+    a, b = quants.dequant_iq3s(raw, kdim, g), quants.dequant_iq3s_lanes(raw, kdim, g)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ----------------------------------------------------------------------------- Q8_0
+def test_q80_known_answer_every_int8():
+    """Block k holds d = 2^-k (k = 0..7) and q = all 256 int8 values in order: y = d * q exactly."""
+    q = np.arange(-128, 128, dtype=np.int8)
+    raw = np.zeros((1, 8 * 34), np.uint8)
+    for k in range(8):
+        blk = raw[0, 34 * k:34 * (k + 1)]
+        blk[0:2] = np.array([2.0 ** -k], np.float16).view(np.uint8)
+        blk[2:34] = q[32 * k:32 * (k + 1)].view(np.uint8)
+    w = quants.dequant_q8_0(raw, 256)[0]
+    want = np.concatenate([q[32 * k:32 * (k + 1)].astype(np.float64) * 2.0 ** -k for k in range(8)])
+    assert np.array_equal(w.astype(np.float64), want)

@@ -1,0 +1,382 @@
+// MoE expert GEMMs for the weight classes of the reference's real checkpoint (its Qwen3.6-35B-A3B
+// GGUF mix): IQ3_S routed gate/up (gxu_gm, engine/mm/MM_E_gxu_gm.cu:86-93; pair walk gx8e256up,
+// engine/mm/MM_P1_gx8e256up.cu:15-20), Q6_K routed down (gxm_dn6, engine/mm/MM_B_gxm_dn6.cu:18-25;
+// pair walk gx8e256dn6, engine/mm/MM_P2_gx8e256dn6.cu:9-13), the Q8_0 shared expert (shexp8,
+// engine/mm/MM_P2_shexp8.cu:8-13), and bit-exact IQ3_S / Q8_0 dequantizers.
+//
+// Slabs as the reference's: expert e's IQ3_S gate/up slab at ptbl[e] -- 512 gate rows, then 512 up
+// rows 450,560 B in (GATE_B), 880 B a row (8 blocks of 110 B, k = 2048); its Q6_K down slab at
+// ptbl_dn[e] -- 2048 rows of 420 B (2 raw 210-B blocks, k = 512); the shared expert's Q8_0 gate and
+// up rows (512 x 2176 B, k = 2048) and down rows (2048 x 544 B, k = 512).
+//
+// One kernel for all of them.  A workgroup (4 waves) owns 64 output columns of one expert -- for
+// gate+up 64 gate rows and the matching 64 up rows, so the SwiGLU pairs meet in one lane; for down
+// 64 rows -- and up to 64 token rows at a time (a pass).  K runs in chunks of 256: the pass's
+// activations (f32 -> fp16, round to nearest even) and the column block's weight rows, dequantized
+// to the reference's operands -- fp16 of the fp32 GGUF value, as gxu_gm stages them -- go to LDS
+// (rows padded to 264 halfs: the 16 rows of a fragment read fall in distinct banks); then wave w
+// runs v_mfma_f32_16x16x32_f16 over its 16 columns for every 16-token group of the pass.  Token
+// lists: sorted (the expert's bin from eoff / plist, in passes of 64), pair walk (one pair per
+// workgroup: pair p runs expert eids[p]) or dense (every position: the shared expert).  The k
+// order and the per-token arithmetic do not depend on which other tokens share a pass, so the pair
+// walk and the sorted form give the same bits for the same pair.
+//
+// IQ3_S's 512-entry grid is a run-time argument (float[512][4]), as in the reference.
+#include "tlx_common.h"
+
+namespace {
+
+constexpr int kHid = 2048, kFf = 512, kE = 256, kMaxPairs = 16384;
+constexpr int kGxCols = 64;         // output columns per workgroup
+constexpr int kGxTok = 64;          // token rows per pass
+constexpr int kGxKc = 256;          // k per chunk
+constexpr int kGxLd = kGxKc + 8;    // LDS row stride (halfs)
+constexpr int kGxThreads = 256;
+constexpr uint32_t kIq3sGate = kFf * 880;   // GATE_B: the up rows' offset in an IQ3_S slab
+
+enum GxCls { GX_IQ3S = 0, GX_Q6K = 1, GX_Q80 = 2 };
+enum GxForm { GX_SORTED = 0, GX_PAIRS = 1, GX_DENSE = 2 };
+
+template <int CLS> struct GxFmt;   // bytes per block, weights per block
+template <> struct GxFmt<GX_IQ3S> { static constexpr int kBlk = 110, kPer = 256; };
+template <> struct GxFmt<GX_Q6K> { static constexpr int kBlk = 210, kPer = 256; };
+template <> struct GxFmt<GX_Q80> { static constexpr int kBlk = 34, kPer = 32; };
+
+struct GxArgs {
+  const uint64_t* ptbl;    // routed: slab address per expert
+  const uint8_t* w0;       // dense: gate rows (gate+up) or down rows
+  const uint8_t* w1;       // dense gate+up: up rows
+  const uint16_t* eids;    // pair walk: expert of each pair
+  const int* eoff;         // sorted: bin offsets [E + 1]
+  const uint16_t* plist;   // sorted: pair ids in bin order
+  const float* x;          // gate+up: f32 [P][2048] (routed: row pair >> 3); down: f32 [pairs or P][512]
+  const float* grid;       // IQ3_S grid f32 [512][4]
+  void* out;               // gate+up: f32 [pairs or P][512]; down: f16 [pairs][2048] or (dense) f32 [P][2048]
+  int P;
+};
+
+template <bool UP, bool GRID>
+struct GxLds {
+  _Float16 x[kGxTok * kGxLd];
+  _Float16 w[(UP ? 2 : 1) * kGxCols * kGxLd];
+  float4 grid[GRID ? 512 : 1];
+  int xrow[kGxTok];
+  int orow[kGxTok];
+};
+
+__device__ __forceinline__ float gx_h2f(const uint8_t* p) { return tlx_h2f(tlx_ldu<uint16_t>(p)); }
+
+__device__ __forceinline__ void gx_store32(_Float16* dst, const float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h8_t h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = (_Float16)v[8 * i + j];
+    *reinterpret_cast<h8_t*>(dst + 8 * i) = h;
+  }
+}
+
+// The 32 weights of 32-weight group j of a 256-k chunk (kc) of one row, as f32 GGUF values.
+// IQ3_S (MM_P0_d2_repack.py:95-120): sub-block j: db = d (1 + 2 nib), index bytes qs[8j ..],
+// high bits qh[j], signs[4j ..].
+__device__ __forceinline__ void gx_dq_iq3s(float* v, const uint8_t* row, int kc, int j, const float4* grid) {
+  const uint8_t* b = row + (size_t)kc * 110;
+  const float d = gx_h2f(b);
+  const int nib = (b[106 + (j >> 1)] >> (4 * (j & 1))) & 15;
+  const float db = d * (float)(1 + 2 * nib);   // exact: an fp16 times an odd integer <= 31
+  const uint64_t qs = tlx_ldu<uint64_t>(b + 2 + 8 * j);
+  const uint32_t qh = b[66 + j];
+  const uint32_t sg = tlx_ldu<uint32_t>(b + 74 + 4 * j);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {   // index byte i: weights 4i .. 4i+3
+    const uint32_t idx = (uint32_t)((qs >> (8 * i)) & 255u) | (((qh >> i) & 1u) << 8);
+    const float4 g = grid[idx];
+    const uint32_t s = sg >> (4 * i);
+    const float gv[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float w = db * gv[c];
+      v[4 * i + c] = ((s >> c) & 1u) ? -w : w;
+    }
+  }
+}
+
+// Q6_K raw block kc (210 B: ql[128] qh[64] sc[16] d), weights 32j .. 32j+31: half h = j >> 2,
+// quarter g = j & 3: (d * sc[8h + l/16 + 2g]) * (q - 32), q = ql nibble | 2 qh bits << 4
+// (MM_P2_ports.py:21-45).
+__device__ __forceinline__ void gx_dq_q6k(float* v, const uint8_t* row, int kc, int j) {
+  const uint8_t* b = row + (size_t)kc * 210;
+  const int h = j >> 2, g = j & 3;
+  const float d = gx_h2f(b + 208);
+  const float t0 = d * (float)(int8_t)b[192 + 8 * h + 2 * g];
+  const float t1 = d * (float)(int8_t)b[192 + 8 * h + 1 + 2 * g];
+  const uint8_t* ql = b + 64 * h + 32 * (g & 1);
+  const uint8_t* qh = b + 128 + 32 * h;
+#pragma unroll
+  for (int l = 0; l < 32; ++l) {
+    const int lo = (g >> 1) ? (ql[l] >> 4) : (ql[l] & 15);
+    const int q = lo | (((qh[l] >> (2 * g)) & 3) << 4);
+    v[l] = (l < 16 ? t0 : t1) * (float)(q - 32);
+  }
+}
+
+// Q8_0 block (34 B: d, q i8[32]): d * q (exact in fp32).
+__device__ __forceinline__ void gx_dq_q80(float* v, const uint8_t* blk) {
+  const float d = gx_h2f(blk);
+#pragma unroll
+  for (int l = 0; l < 32; ++l) v[l] = d * (float)(int8_t)blk[2 + l];
+}
+
+template <int CLS>
+__device__ __forceinline__ void gx_dequant32(float* v, const uint8_t* row, int kc, int j, const float4* grid) {
+  if constexpr (CLS == GX_IQ3S) gx_dq_iq3s(v, row, kc, j, grid);
+  else if constexpr (CLS == GX_Q6K) gx_dq_q6k(v, row, kc, j);
+  else gx_dq_q80(v, row + (size_t)(8 * kc + j) * 34);
+}
+
+template <int CLS, bool UP, int FORM>
+__global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
+  constexpr int K = UP ? kHid : kFf;
+  constexpr int NR = (UP ? 2 : 1) * kGxCols;              // staged weight rows
+  constexpr int RB = (UP ? kFf : kHid) / kGxCols;         // column blocks per matrix
+  constexpr int ROWB = K / GxFmt<CLS>::kPer * GxFmt<CLS>::kBlk;
+  constexpr bool GRID = CLS == GX_IQ3S;
+  __shared__ GxLds<UP, GRID> L;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 15, kq = lane >> 4;
+  const int rb = (int)blockIdx.x % RB, item = (int)blockIdx.x / RB;
+
+  // the work item: token list, weight matrices
+  int beg = 0, ntot = 0;
+  const uint8_t* wg = nullptr;
+  const uint8_t* wu = nullptr;
+  if constexpr (FORM == GX_SORTED) {
+    beg = a.eoff[item];
+    ntot = a.eoff[item + 1] - beg;
+    if (ntot <= 0) return;   // uniform per workgroup
+    wg = reinterpret_cast<const uint8_t*>(a.ptbl[item]);
+  } else if constexpr (FORM == GX_PAIRS) {
+    beg = item;
+    ntot = 1;
+    wg = reinterpret_cast<const uint8_t*>(a.ptbl[a.eids[item]]);
+  } else {
+    beg = item * kGxTok;
+    ntot = min(kGxTok, a.P - beg);
+    wg = a.w0;
+  }
+  if constexpr (UP) wu = FORM == GX_DENSE ? a.w1 : wg + kIq3sGate;
+  if constexpr (GRID) {
+    for (int i = t; i < 512; i += kGxThreads) L.grid[i] = reinterpret_cast<const float4*>(a.grid)[i];
+  }
+
+  for (int p0 = 0; p0 < ntot; p0 += kGxTok) {
+    const int nt = min(kGxTok, ntot - p0);
+    const int ng = (nt + 15) >> 4;
+    __syncthreads();   // the previous pass is done with the token rows
+    if (t < kGxTok) {
+      int xr = -1, orw = -1;
+      if (t < nt) {
+        const int pr = FORM == GX_SORTED ? (int)a.plist[beg + p0 + t] : beg + p0 + t;   // pair or position
+        orw = pr;
+        xr = (UP && FORM != GX_DENSE) ? (pr >> 3) : pr;
+      }
+      L.xrow[t] = xr;
+      L.orow[t] = orw;
+    }
+    f4_t acc[4][UP ? 2 : 1];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int m = 0; m < (UP ? 2 : 1); ++m) acc[g][m] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int kc = 0; kc < K / kGxKc; ++kc) {
+      __syncthreads();   // the previous chunk's fragment reads are done; the token rows are visible
+      {   // activations: thread t covers token t >> 2, k (t & 3) * 64 .. + 63 (zeros past the pass)
+        const int tt = t >> 2, k0 = (t & 3) * 64;
+        const int xr = L.xrow[tt];
+        _Float16* dst = L.x + tt * kGxLd + k0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float f[8];
+          if (xr >= 0) {
+            const float4* src = reinterpret_cast<const float4*>(a.x + (size_t)xr * K + kc * kGxKc + k0 + 8 * i);
+            const float4 u = src[0], w = src[1];
+            f[0] = u.x; f[1] = u.y; f[2] = u.z; f[3] = u.w; f[4] = w.x; f[5] = w.y; f[6] = w.z; f[7] = w.w;
+          } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) f[j] = 0.f;
+          }
+          h8_t h;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) h[j] = (_Float16)f[j];
+          *reinterpret_cast<h8_t*>(dst + 8 * i) = h;
+        }
+      }
+      // weights: units (staged row R, 32-weight group j), NR * 8 of them
+#pragma unroll 1
+      for (int u = t; u < NR * 8; u += kGxThreads) {
+        const int R = u >> 3, j = u & 7;
+        const int r = rb * kGxCols + (R & (kGxCols - 1));
+        const uint8_t* row = ((UP && R >= kGxCols) ? wu : wg) + (size_t)r * ROWB;
+        float v[32];
+        gx_dequant32<CLS>(v, row, kc, j, L.grid);
+        gx_store32(L.w + R * kGxLd + 32 * j, v);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int s = 0; s < kGxKc / 32; ++s) {
+        const int ko = 32 * s + 8 * kq;
+        const h8_t bg = *reinterpret_cast<const h8_t*>(L.w + (16 * wave + col) * kGxLd + ko);
+        h8_t bu;
+        if constexpr (UP) bu = *reinterpret_cast<const h8_t*>(L.w + (kGxCols + 16 * wave + col) * kGxLd + ko);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          if (g < ng) {
+            const h8_t ax = *reinterpret_cast<const h8_t*>(L.x + (16 * g + col) * kGxLd + ko);
+            acc[g][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, bg, acc[g][0], 0, 0, 0);
+            if constexpr (UP) acc[g][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, bu, acc[g][1], 0, 0, 0);
+          }
+        }
+      }
+    }
+    // lane (col, kq) holds tokens 16 g + 4 kq + r of output column rb * 64 + 16 wave + col
+    const int n = rb * kGxCols + 16 * wave + col;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      if (g >= ng) break;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tk = 16 * g + 4 * kq + r;
+        if (tk >= nt) continue;
+        const size_t o = (size_t)L.orow[tk];
+        if constexpr (UP) {
+          const float gv = acc[g][0][r], uv = acc[g][1][r];
+          reinterpret_cast<float*>(a.out)[o * kFf + n] = gv / (1.f + expf(-gv)) * uv;
+        } else if constexpr (FORM == GX_DENSE) {
+          reinterpret_cast<float*>(a.out)[o * kHid + n] = acc[g][0][r];
+        } else {
+          reinterpret_cast<_Float16*>(a.out)[o * kHid + n] = (_Float16)acc[g][0][r];
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ dequantizers (bit-exact)
+// One thread per (row, 32-weight group).
+template <int CLS>
+__global__ __launch_bounds__(256) void gx_dequant_kernel(const uint8_t* __restrict__ w, const float* __restrict__ gridf,
+                                                         void* __restrict__ out, int64_t rows, int kdim, int out_f16) {
+  __shared__ float4 grid[CLS == GX_IQ3S ? 512 : 1];
+  if constexpr (CLS == GX_IQ3S) {
+    for (int i = threadIdx.x; i < 512; i += blockDim.x) grid[i] = reinterpret_cast<const float4*>(gridf)[i];
+    __syncthreads();
+  }
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int ng = kdim >> 5;
+  if (u >= rows * ng) return;
+  const int64_t r = u / ng;
+  const int gi = (int)(u - r * ng);
+  const int64_t rowb = (int64_t)kdim / GxFmt<CLS>::kPer * GxFmt<CLS>::kBlk;
+  const uint8_t* row = w + r * rowb;
+  float v[32];
+  gx_dequant32<CLS>(v, row, gi >> 3, gi & 7, grid);
+  const int64_t o = r * kdim + 32 * gi;
+  if (out_f16) {
+#pragma unroll
+    for (int l = 0; l < 32; ++l) reinterpret_cast<uint16_t*>(out)[o + l] = tlx_f2h_bits(v[l]);
+  } else {
+#pragma unroll
+    for (int l = 0; l < 32; ++l) reinterpret_cast<float*>(out)[o + l] = v[l];
+  }
+}
+
+template <int CLS, bool UP, int FORM>
+int gx_launch(const GxArgs& a, int items, hipStream_t st) {
+  constexpr int RB = (UP ? kFf : kHid) / kGxCols;
+  gx_kernel<CLS, UP, FORM><<<(unsigned)(items * RB), kGxThreads, 0, st>>>(a);
+  return tlx_launch_status();
+}
+
+}  // namespace
+
+extern "C" int tlx_iq3s_dequant(const void* w, const float* gridf, void* out, int64_t rows, int64_t kdim, int out_f16,
+                                void* stream) {
+  TLX_RET_IF(w == nullptr || gridf == nullptr || out == nullptr, TLX_E_ARG);
+  TLX_RET_IF(rows < 1 || kdim < 256 || (kdim & 255) || kdim > (1 << 24), TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(w, 2) || !tlx_aligned(gridf, 16) || !tlx_aligned(out, 4), TLX_E_ALIGN);
+  const int64_t units = rows * (kdim >> 5), grid = (units + 255) / 256;
+  TLX_RET_IF(grid > 0x7fffffff, TLX_E_ARG);
+  gx_dequant_kernel<GX_IQ3S><<<(unsigned)grid, 256, 0, (hipStream_t)stream>>>((const uint8_t*)w, gridf, out, rows,
+                                                                              (int)kdim, out_f16);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_q8_0_dequant(const void* w, void* out, int64_t rows, int64_t kdim, int out_f16, void* stream) {
+  TLX_RET_IF(w == nullptr || out == nullptr, TLX_E_ARG);
+  TLX_RET_IF(rows < 1 || kdim < 256 || (kdim & 255) || kdim > (1 << 24), TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(w, 2) || !tlx_aligned(out, 4), TLX_E_ALIGN);
+  const int64_t units = rows * (kdim >> 5), grid = (units + 255) / 256;
+  TLX_RET_IF(grid > 0x7fffffff, TLX_E_ARG);
+  gx_dequant_kernel<GX_Q80><<<(unsigned)grid, 256, 0, (hipStream_t)stream>>>((const uint8_t*)w, nullptr, out, rows,
+                                                                             (int)kdim, out_f16);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_moe_up3s(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const float* xs,
+                            const float* gridf, float* ys, int np, void* stream) {
+  TLX_RET_IF(!ptbl || !eoff || !plist || !xs || !gridf || !ys, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(ptbl, 8) || !tlx_aligned(xs, 16) || !tlx_aligned(gridf, 16) || !tlx_aligned(ys, 4), TLX_E_ALIGN);
+  GxArgs a{};
+  a.ptbl = ptbl; a.eoff = eoff; a.plist = plist; a.x = xs; a.grid = gridf; a.out = ys;
+  return gx_launch<GX_IQ3S, true, GX_SORTED>(a, kE, (hipStream_t)stream);
+}
+
+extern "C" int tlx_moe_up3s_pairs(const uint64_t* ptbl, const uint16_t* eids, const float* xs, const float* gridf,
+                                  float* ys, int np, void* stream) {
+  TLX_RET_IF(!ptbl || !eids || !xs || !gridf || !ys, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(ptbl, 8) || !tlx_aligned(xs, 16) || !tlx_aligned(gridf, 16) || !tlx_aligned(ys, 4), TLX_E_ALIGN);
+  GxArgs a{};
+  a.ptbl = ptbl; a.eids = eids; a.x = xs; a.grid = gridf; a.out = ys;
+  return gx_launch<GX_IQ3S, true, GX_PAIRS>(a, np, (hipStream_t)stream);
+}
+
+extern "C" int tlx_moe_dn6(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
+                           const uint16_t* plist, const float* act, uint16_t* parts, int np, void* stream) {
+  (void)items;   // the reference's slots; this form walks eoff / plist itself
+  (void)nitp;
+  TLX_RET_IF(!ptbl_dn || !eoff || !plist || !act || !parts, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(ptbl_dn, 8) || !tlx_aligned(act, 16) || !tlx_aligned(parts, 2), TLX_E_ALIGN);
+  GxArgs a{};
+  a.ptbl = ptbl_dn; a.eoff = eoff; a.plist = plist; a.x = act; a.out = parts;
+  return gx_launch<GX_Q6K, false, GX_SORTED>(a, kE, (hipStream_t)stream);
+}
+
+extern "C" int tlx_moe_dn6_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, uint16_t* parts,
+                                 int np, void* stream) {
+  TLX_RET_IF(!ptbl_dn || !eids || !act || !parts, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(ptbl_dn, 8) || !tlx_aligned(act, 16) || !tlx_aligned(parts, 2), TLX_E_ALIGN);
+  GxArgs a{};
+  a.ptbl = ptbl_dn; a.eids = eids; a.x = act; a.out = parts;
+  return gx_launch<GX_Q6K, false, GX_PAIRS>(a, np, (hipStream_t)stream);
+}
+
+extern "C" int tlx_moe_shared8(const void* wg, const void* wu, const void* wd, const float* x, float* y, float* act,
+                               int P, void* stream) {
+  TLX_RET_IF(!wg || !wu || !wd || !x || !y || !act, TLX_E_ARG);
+  TLX_RET_IF(P < 1 || P > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(wg, 2) || !tlx_aligned(wu, 2) || !tlx_aligned(wd, 2), TLX_E_ALIGN);
+  TLX_RET_IF(!tlx_aligned(x, 16) || !tlx_aligned(act, 16) || !tlx_aligned(y, 4), TLX_E_ALIGN);
+  hipStream_t st = (hipStream_t)stream;
+  const int items = (P + kGxTok - 1) / kGxTok;
+  GxArgs a{};
+  a.w0 = (const uint8_t*)wg; a.w1 = (const uint8_t*)wu; a.x = x; a.out = act; a.P = P;
+  int r = gx_launch<GX_Q80, true, GX_DENSE>(a, items, st);
+  TLX_RET_IF(r != TLX_OK, r);
+  GxArgs b{};
+  b.w0 = (const uint8_t*)wd; b.x = act; b.out = y; b.P = P;
+  return gx_launch<GX_Q80, false, GX_DENSE>(b, items, st);
+}

@@ -154,6 +154,27 @@ def iq4xs_dequant(w, iq4nl, out, kdim, stream=None):
     return out
 
 
+def iq3s_dequant(w, gridf, out, kdim, stream=None):
+    """IQ3_S rows (110 B per 256 weights) -> f32 or f16 ``out`` (bit-exact GGUF values); gridf:
+    the 512-entry grid as float[512][4] (a run-time table, as the reference passes it)."""
+    rows = w.numel() * w.element_size() // (110 * (kdim // 256))
+    _need(out, rows * kdim * out.element_size(), "out")
+    _need(gridf, 512 * 16, "gridf")
+    _dev(w, gridf, out)
+    call("tlx_iq3s_dequant", w.data_ptr(), gridf.data_ptr(), out.data_ptr(), rows, kdim, int(out.dtype == _F16),
+         _stream(stream))
+    return out
+
+
+def q8_0_dequant(w, out, kdim, stream=None):
+    """Q8_0 rows (34 B per 32 weights) -> f32 or f16 ``out`` (bit-exact d * q)."""
+    rows = w.numel() * w.element_size() // (34 * (kdim // 32))
+    _need(out, rows * kdim * out.element_size(), "out")
+    _dev(w, out)
+    call("tlx_q8_0_dequant", w.data_ptr(), out.data_ptr(), rows, kdim, int(out.dtype == _F16), _stream(stream))
+    return out
+
+
 # ------------------------------------------------------------------ decode GEMVs
 def ffn8(wg, wu, gridf, hhx, gact, layout=LAYOUT_PACKED, stream=None, out_tileord=False, in_tileord=False,
          m=None):
@@ -738,6 +759,77 @@ def moe_combine(parts, gates, sg, shared, hres, y, stream=None):
     _dev(parts, gates, sg, shared, hres, y)
     call("tlx_moe_combine", parts.data_ptr(), gates.data_ptr(), sg.data_ptr(), shared.data_ptr(), hres.data_ptr(),
          y.data_ptr(), y.shape[0], _stream(stream))
+
+
+# ---- the checkpoint's classes: IQ3_S routed gate/up, Q6_K routed down, Q8_0 shared expert
+def moe_up3s(ptbl, eoff, plist, xs, gridf, ys, stream=None):
+    """gxu_gm(ptbl, eoff, plist, xs, gridf, ys) over the sorted pairs (IQ3_S slabs: 512 gate rows
+    then 512 up rows 450,560 B in, 880 B a row): ys[pair][512] = silu(Wg_e . x[pos]) * (Wu_e . x[pos])."""
+    n = ys.shape[0]
+    _need(ptbl, 256 * 8, "ptbl")
+    _need(eoff, 257 * 4, "eoff")
+    _need(plist, n * 2, "plist")
+    _need(xs, ((n + 7) // 8) * 2048 * 4, "xs")
+    _need(ys, n * 512 * 4, "ys")
+    _need(gridf, 512 * 16, "gridf")
+    _dev(ptbl, eoff, plist, xs, gridf, ys)
+    call("tlx_moe_up3s", ptbl.data_ptr(), eoff.data_ptr(), plist.data_ptr(), xs.data_ptr(), gridf.data_ptr(),
+         ys.data_ptr(), n, _stream(stream))
+
+
+def moe_up3s_pairs(ptbl, eids, xs, gridf, ys, stream=None):
+    """gx8e256up(ptbl, eids, xs, gridf, ys): pair p runs IQ3_S expert eids[p] on x[p >> 3], no sort."""
+    n = ys.shape[0]
+    _need(ptbl, 256 * 8, "ptbl")
+    _need(eids, n * 2, "eids")
+    _need(xs, ((n + 7) // 8) * 2048 * 4, "xs")
+    _need(ys, n * 512 * 4, "ys")
+    _need(gridf, 512 * 16, "gridf")
+    _dev(ptbl, eids, xs, gridf, ys)
+    call("tlx_moe_up3s_pairs", ptbl.data_ptr(), eids.data_ptr(), xs.data_ptr(), gridf.data_ptr(), ys.data_ptr(),
+         n, _stream(stream))
+
+
+def moe_dn6(ptbl_dn, items, nitp, eoff, plist, act, parts, stream=None):
+    """gxm_dn6(ptbl, items, nitp, eoff, plist, act, parts) over the sorted pairs (Q6_K slabs of
+    2048 rows x 420 B): parts[pair][2048] = fp16(Wd_e . act[pair])."""
+    n = act.shape[0]
+    _need(ptbl_dn, 256 * 8, "ptbl_dn")
+    _need(eoff, 257 * 4, "eoff")
+    _need(plist, n * 2, "plist")
+    _need(act, n * 512 * 4, "act")
+    _need(parts, n * 2048 * 2, "parts")
+    _dev(ptbl_dn, eoff, plist, act, parts)
+    call("tlx_moe_dn6", ptbl_dn.data_ptr(), 0 if items is None else items.data_ptr(),
+         0 if nitp is None else nitp.data_ptr(), eoff.data_ptr(), plist.data_ptr(), act.data_ptr(), parts.data_ptr(),
+         n, _stream(stream))
+
+
+def moe_dn6_pairs(ptbl_dn, eids, act, parts, stream=None):
+    """gx8e256dn6(ptbl, eids, act, parts): pair p runs Q6_K expert eids[p] on act[p], no sort."""
+    n = act.shape[0]
+    _need(ptbl_dn, 256 * 8, "ptbl_dn")
+    _need(eids, n * 2, "eids")
+    _need(act, n * 512 * 4, "act")
+    _need(parts, n * 2048 * 2, "parts")
+    _dev(ptbl_dn, eids, act, parts)
+    call("tlx_moe_dn6_pairs", ptbl_dn.data_ptr(), eids.data_ptr(), act.data_ptr(), parts.data_ptr(), n,
+         _stream(stream))
+
+
+def moe_shared8(wg, wu, wd, x, y, act, stream=None):
+    """shexp8(wg, wu, wd, x, y): the Q8_0 shared expert over P = x.shape[0] positions,
+    y[P][2048] f32 = Wd . (silu(Wg . x) * (Wu . x)); act: caller scratch f32 [P][512]."""
+    P = x.shape[0]
+    _need(wg, 512 * 2176, "wg")
+    _need(wu, 512 * 2176, "wu")
+    _need(wd, 2048 * 544, "wd")
+    _need(x, P * 2048 * 4, "x")
+    _need(y, P * 2048 * 4, "y")
+    _need(act, P * 512 * 4, "act")
+    _dev(wg, wu, wd, x, y, act)
+    call("tlx_moe_shared8", wg.data_ptr(), wu.data_ptr(), wd.data_ptr(), x.data_ptr(), y.data_ptr(), act.data_ptr(),
+         P, _stream(stream))
 
 
 class MoeScratch:

@@ -97,3 +97,37 @@ def moe_expert_slabs(rng, n_experts):
           for _ in range(n_experts)]
     dn = [iq4xs_raw(rng, 2048, 512).ravel() for _ in range(n_experts)]
     return gu, dn
+
+
+def iq3s_raw(rng, rows, kdim):
+    """GGUF IQ3_S rows u8[rows, 110*NB]: d, then index / high-bit / sign / scale bytes uniform."""
+    nb = kdim // 256
+    blk = rng.integers(0, 256, size=(rows, nb, 110), dtype=np.uint8)
+    blk[:, :, 0:2] = _d16(rng, (rows, nb)).view(np.uint8).reshape(rows, nb, 2)
+    return blk.reshape(rows, nb * 110)
+
+
+def iq3s_grid(rng):
+    """A synthetic IQ3_S grid float32[512, 4] with ggml's level set (odd 1..15).  The real table
+    is a third-party constant absent here; the kernels take the grid at run time."""
+    return rng.choice(np.arange(1, 16, 2), size=(512, 4)).astype(np.float32)
+
+
+def q80_raw(rng, rows, kdim):
+    """GGUF Q8_0 rows u8[rows, 34*(kdim/32)]: d, then 32 int8 uniform."""
+    nb = kdim // 32
+    blk = np.empty((rows, nb, 34), dtype=np.uint8)
+    blk[:, :, 2:34] = rng.integers(0, 256, size=(rows, nb, 32), dtype=np.uint8)
+    blk[:, :, 0:2] = _d16(rng, (rows, nb)).view(np.uint8).reshape(rows, nb, 2)
+    return blk.reshape(rows, nb * 34)
+
+
+def moe_ckpt_slabs(rng, n_experts):
+    """The checkpoint's MoE classes: per routed expert an IQ3_S gate/up slab u8[2*512*880] (512
+    gate rows, then 512 up rows, k = 2048) and a Q6_K down slab u8[2048*420] (k = 512); the shared
+    expert's Q8_0 gate, up (512 x 2176 B) and down (2048 x 544 B) rows."""
+    gu = [np.concatenate([iq3s_raw(rng, 512, 2048).ravel(), iq3s_raw(rng, 512, 2048).ravel()])
+          for _ in range(n_experts)]
+    dn = [q6k_raw(rng, 2048, 512).ravel() for _ in range(n_experts)]
+    shared = (q80_raw(rng, 512, 2048), q80_raw(rng, 512, 2048), q80_raw(rng, 2048, 512))
+    return gu, dn, shared
