@@ -452,6 +452,53 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
     return out
 
 
+def moe_ckpt_leg(ops, formats, synth, torch, dev, steps, warmup):
+    """The MoE layer with the reference checkpoint's weight classes (IQ3_S routed gate/up, Q6_K
+    routed down, Q8_0 shared expert; ops.moe_layer_ckpt) at M=11 and M=2048, config 5's shapes,
+    seeded weights (a synthetic IQ3_S grid), two copies of the slabs rotated (906 MB), graph
+    replays; FLOPs and expert bytes counted as for config 5."""
+    rng = np.random.default_rng(20261205)
+    E, H, F = 256, 2048, 512
+    sets = []
+    for _ in range(2):
+        gu, dn, shared = synth.moe_ckpt_slabs(rng, E)
+        dgu = [torch.from_numpy(a).to(dev) for a in gu]
+        ddn = [torch.from_numpy(a).to(dev) for a in dn]
+        sets.append(dict(keep=(dgu, ddn), ptbl=formats.pointer_table(dgu, dev), ptbl_dn=formats.pointer_table(ddn, dev),
+                         sh=[torch.from_numpy(np.ascontiguousarray(a).reshape(-1)).to(dev) for a in shared]))
+    gridf = torch.from_numpy(synth.iq3s_grid(rng).reshape(-1)).to(dev)
+    out = {"workload": "MoE layer with the checkpoint's classes: 256 IQ3_S gate/up + Q6_K down experts, Q8_0 shared "
+                       "expert, hidden 2048, FF 512, top-8; hidden states bf16(0.05 * N(0,1))"}
+    for P in (11, 2048):
+        x = torch.from_numpy(synth.bf16_round(0.05 * rng.standard_normal((P, H)).astype(np.float32))).to(dev)
+        logits = torch.from_numpy(rng.standard_normal((P, E)).astype(np.float32)).to(dev)
+        sg = torch.rand(P, device=dev)
+        hres = torch.randn(P, H, device=dev)
+        sc = ops.MoeScratch(P, dev)
+        y = torch.empty(P, H, device=dev)
+        state = {"i": 0}
+
+        def layer(st):
+            c = sets[state["i"] % 2]
+            state["i"] += 1
+            ops.moe_layer_ckpt(logits, sg, x, hres, y, c["ptbl"], c["ptbl_dn"], c["sh"], gridf, sc, stream=st)
+
+        t = time_graph(layer, steps, warmup, torch)
+        hit = int(torch.unique(sc.eids).numel())
+        flops = 2.0 * 3 * F * H * (8 * P + P)
+        wbytes = hit * (2 * F * 880 + H * 420) + 2 * F * 2176 + H * 544
+        tflops = flops / (t * 1e-3) / 1e12
+        gbs = wbytes / (t * 1e-3) / 1e9
+        route = "pair walk" if P <= ops.MOE_PAIR_WALK_MAX_P else "sort + grouped forms"
+        out[f"M{P}"] = {"ms": round(t, 4), "tflops": round(tflops, 2), "experts_hit": hit, "weight_gbs": round(gbs, 1),
+                        "route": route,
+                        "roofline": (hbm_roofline(gbs, f"checkpoint-class MoE layer ({route}; graph): expert bytes / "
+                                                       "layer time") if P <= 64 else
+                                     mfma_roofline(tflops, f"checkpoint-class MoE layer ({route}; graph): "
+                                                           "2*3*512*2048*9*M / layer time"))}
+    return out
+
+
 def sweep_leg(ops, formats, torch, dev, steps, warmup, tiled=True, per_kind_graphs=True):
     """Config 3: the 64-layer dense decode step at M=11 plus the Q6_K head.  With ``tiled`` every
     IQ3_XXS tensor except the k/v rows beside a Q6_K q reads tiled records (repacked on the GPU
@@ -952,6 +999,8 @@ def main():
     if not args.no_moe:
         note("moe (config 5)")
         out["moe"] = moe_leg(ops, formats, synth, torch, dev, small_steps, small_warm)
+        note("MoE layer, checkpoint classes")
+        out["moe"]["ckpt"] = moe_ckpt_leg(ops, formats, synth, torch, dev, small_steps, small_warm)
     if not args.no_cpu:
         note("CPU baselines")
         legs, cpu = cpu_legs(args.cpu_reps, int(head))

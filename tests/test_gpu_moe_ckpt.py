@@ -164,3 +164,33 @@ def test_ckpt_argument_validation(gpu, ckpt):
     with pytest.raises(TlxError):     # more pairs than the sort supports
         call("tlx_moe_dn6_pairs", ckpt["ptbl_dn"].data_ptr(), eids.data_ptr(), act.data_ptr(), act.data_ptr(),
              16385, None)
+
+
+@pytest.mark.parametrize("P", [11, 300])
+def test_ckpt_layer(gpu, ckpt, P):
+    """ops.moe_layer_ckpt (top-8, pair walk at P=11 / sort + grouped forms at P=300, IQ3_S up,
+    Q6_K down, Q8_0 shared, combine): every pair's act / parts and the shared expert against the
+    oracle, y against the combine of the GPU's own parts and shared output."""
+    print(f"[case] checkpoint-class MoE layer P={P}", flush=True)
+    rng = np.random.default_rng(47 + P)
+    x = synth.bf16_round(0.05 * rng.standard_normal((P, moe.HID)).astype(np.float32))
+    logits = rng.standard_normal((P, moe.E)).astype(np.float32)
+    sg = (1.0 / (1.0 + np.exp(-rng.standard_normal(P)))).astype(np.float32)
+    hres = rng.standard_normal((P, moe.HID)).astype(np.float32)
+    sc = ops.MoeScratch(P, gpu)
+    y = torch.empty(P, moe.HID, dtype=torch.float32, device=gpu)
+    ops.moe_layer_ckpt(torch.from_numpy(logits).to(gpu), torch.from_numpy(sg).to(gpu), torch.from_numpy(x).to(gpu),
+                       torch.from_numpy(hres).to(gpu), y, ckpt["ptbl"], ckpt["ptbl_dn"], ckpt["dsh"], ckpt["gridf"], sc)
+    torch.cuda.synchronize()
+    eids, gates = moe.topk_ref(logits)
+    assert np.array_equal(sc.eids.cpu().numpy().view(np.uint16), eids)
+    act, parts, shared = sc.act.cpu().numpy(), sc.parts.cpu().numpy(), sc.shared.cpu().numpy()
+    pairs = list(range(8 * P)) if P <= 16 else sorted(np.random.default_rng(6).choice(8 * P, 40, replace=False))
+    _check_pairs(ckpt, x, eids.reshape(-1), act, parts, pairs)
+    wg, wu, wd = ckpt["shared"]
+    assert _rows_err(shared, moe.shared8_ref(wg, wu, wd, x)) <= TOL
+    pp = parts.reshape(P, 8, moe.HID)
+    g = sc.gates.cpu().numpy()
+    yref = moe.combine_ref(pp, g, sg, shared, hres)
+    scale = np.abs(hres) + np.einsum("pr,prk->pk", np.abs(g), np.abs(pp.astype(np.float64))) + np.abs(sg)[:, None] * np.abs(shared)
+    assert np.all(np.abs(y.cpu().numpy() - yref) <= 4e-6 * scale + 1e-30)

@@ -28,9 +28,8 @@ namespace {
 
 constexpr int kHid = 2048, kFf = 512, kE = 256, kMaxPairs = 16384;
 constexpr int kGxCols = 64;         // output columns per workgroup
-constexpr int kGxTok = 64;          // token rows per pass
-constexpr int kGxKc = 256;          // k per chunk
-constexpr int kGxLd = kGxKc + 8;    // LDS row stride (halfs)
+constexpr int kGxKc = 64;           // k per chunk (LDS stage)
+constexpr int kGxLd = kGxKc + 8;    // LDS row stride (halfs): fragment reads of 16 rows hit 16 distinct 16-B slots
 constexpr int kGxThreads = 256;
 constexpr uint32_t kIq3sGate = kFf * 880;   // GATE_B: the up rows' offset in an IQ3_S slab
 
@@ -41,6 +40,9 @@ template <int CLS> struct GxFmt;   // bytes per block, weights per block
 template <> struct GxFmt<GX_IQ3S> { static constexpr int kBlk = 110, kPer = 256; };
 template <> struct GxFmt<GX_Q6K> { static constexpr int kBlk = 210, kPer = 256; };
 template <> struct GxFmt<GX_Q80> { static constexpr int kBlk = 34, kPer = 32; };
+
+// token rows per pass: one 16-row MFMA group for the pair walk, four otherwise
+template <int FORM> constexpr int gx_tok() { return FORM == GX_PAIRS ? 16 : 64; }
 
 struct GxArgs {
   const uint64_t* ptbl;    // routed: slab address per expert
@@ -55,20 +57,20 @@ struct GxArgs {
   int P;
 };
 
-template <bool UP, bool GRID>
+template <bool UP, bool GRID, int TOK>
 struct GxLds {
-  _Float16 x[kGxTok * kGxLd];
+  _Float16 x[TOK * kGxLd];
   _Float16 w[(UP ? 2 : 1) * kGxCols * kGxLd];
   float4 grid[GRID ? 512 : 1];
-  int xrow[kGxTok];
-  int orow[kGxTok];
+  int xrow[TOK];
+  int orow[TOK];
 };
 
 __device__ __forceinline__ float gx_h2f(const uint8_t* p) { return tlx_h2f(tlx_ldu<uint16_t>(p)); }
 
-__device__ __forceinline__ void gx_store32(_Float16* dst, const float* v) {
+__device__ __forceinline__ void gx_store16(_Float16* dst, const float* v) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 2; ++i) {
     h8_t h;
 #pragma unroll
     for (int j = 0; j < 8; ++j) h[j] = (_Float16)v[8 * i + j];
@@ -76,62 +78,78 @@ __device__ __forceinline__ void gx_store32(_Float16* dst, const float* v) {
   }
 }
 
-// The 32 weights of 32-weight group j of a 256-k chunk (kc) of one row, as f32 GGUF values.
-// IQ3_S (MM_P0_d2_repack.py:95-120): sub-block j: db = d (1 + 2 nib), index bytes qs[8j ..],
-// high bits qh[j], signs[4j ..].
-__device__ __forceinline__ void gx_dq_iq3s(float* v, const uint8_t* row, int kc, int j, const float4* grid) {
-  const uint8_t* b = row + (size_t)kc * 110;
-  const float d = gx_h2f(b);
-  const int nib = (b[106 + (j >> 1)] >> (4 * (j & 1))) & 15;
-  const float db = d * (float)(1 + 2 * nib);   // exact: an fp16 times an odd integer <= 31
-  const uint64_t qs = tlx_ldu<uint64_t>(b + 2 + 8 * j);
-  const uint32_t qh = b[66 + j];
-  const uint32_t sg = tlx_ldu<uint32_t>(b + 74 + 4 * j);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {   // index byte i: weights 4i .. 4i+3
-    const uint32_t idx = (uint32_t)((qs >> (8 * i)) & 255u) | (((qh >> i) & 1u) << 8);
-    const float4 g = grid[idx];
-    const uint32_t s = sg >> (4 * i);
-    const float gv[4] = {g.x, g.y, g.z, g.w};
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float w = db * gv[c];
-      v[4 * i + c] = ((s >> c) & 1u) ? -w : w;
-    }
-  }
-}
+// The 16 weights k0 .. k0 + 15 (k0 % 16 == 0) of one row as f32 GGUF values, in two steps: fetch
+// (the raw bytes into registers, so a chunk's loads can be issued a chunk ahead) and decode.
+// IQ3_S (MM_P0_d2_repack.py:95-120): sub-block j = kib / 32 (db = d (1 + 2 nib)), half hf: index
+// bytes qs[8j + 4hf ..], high bits 4hf .. of qh[j], sign bytes signs[4j + 2hf ..].
+// Q6_K raw block (210 B: ql[128] qh[64] sc[16] d): half h = kib / 128, quarter g, l0 = 0 or 16:
+// (d * sc[8h + l0/16 + 2g]) * (q - 32), q = ql nibble | 2 qh bits << 4 (MM_P2_ports.py:21-45).
+// Q8_0 block (34 B: d, q i8[32]), half (k0 / 16) & 1: d * q (exact in fp32).
+template <int CLS> struct GxRaw;
+template <> struct GxRaw<GX_IQ3S> { uint32_t dn, qs, hs; };   // d | nib << 16, index bytes, qh nibble | signs << 8
+template <> struct GxRaw<GX_Q6K> { uint32_t ds; u4_t ql, qh; };   // d | sc << 16 | (kib & 255) << 24
+template <> struct GxRaw<GX_Q80> { uint32_t d; u4_t q; };
 
-// Q6_K raw block kc (210 B: ql[128] qh[64] sc[16] d), weights 32j .. 32j+31: half h = j >> 2,
-// quarter g = j & 3: (d * sc[8h + l/16 + 2g]) * (q - 32), q = ql nibble | 2 qh bits << 4
-// (MM_P2_ports.py:21-45).
-__device__ __forceinline__ void gx_dq_q6k(float* v, const uint8_t* row, int kc, int j) {
-  const uint8_t* b = row + (size_t)kc * 210;
-  const int h = j >> 2, g = j & 3;
-  const float d = gx_h2f(b + 208);
-  const float t0 = d * (float)(int8_t)b[192 + 8 * h + 2 * g];
-  const float t1 = d * (float)(int8_t)b[192 + 8 * h + 1 + 2 * g];
-  const uint8_t* ql = b + 64 * h + 32 * (g & 1);
-  const uint8_t* qh = b + 128 + 32 * h;
-#pragma unroll
-  for (int l = 0; l < 32; ++l) {
-    const int lo = (g >> 1) ? (ql[l] >> 4) : (ql[l] & 15);
-    const int q = lo | (((qh[l] >> (2 * g)) & 3) << 4);
-    v[l] = (l < 16 ? t0 : t1) * (float)(q - 32);
+template <int CLS>
+__device__ __forceinline__ GxRaw<CLS> gx_fetch(const uint8_t* row, int k0) {
+  GxRaw<CLS> r;
+  if constexpr (CLS == GX_IQ3S) {
+    const uint8_t* b = row + (size_t)(k0 >> 8) * 110;
+    const int kib = k0 & 255, j = kib >> 5, hf = (kib >> 4) & 1;
+    const uint32_t nib = (b[106 + (j >> 1)] >> (4 * (j & 1))) & 15u;
+    r.dn = tlx_ldu<uint16_t>(b) | (nib << 16);
+    r.qs = tlx_ldu<uint32_t>(b + 2 + 8 * j + 4 * hf);
+    r.hs = ((uint32_t)(b[66 + j] >> (4 * hf)) & 15u) | ((uint32_t)tlx_ldu<uint16_t>(b + 74 + 4 * j + 2 * hf) << 8);
+  } else if constexpr (CLS == GX_Q6K) {
+    const uint8_t* b = row + (size_t)(k0 >> 8) * 210;
+    const int kib = k0 & 255, h = kib >> 7, g = (kib >> 5) & 3, l0 = kib & 31;
+    r.ds = tlx_ldu<uint16_t>(b + 208) | ((uint32_t)b[192 + 8 * h + (l0 >> 4) + 2 * g] << 16) | ((uint32_t)kib << 24);
+    r.ql = tlx_ldu<u4_t>(b + 64 * h + 32 * (g & 1) + l0);
+    r.qh = tlx_ldu<u4_t>(b + 128 + 32 * h + l0);
+  } else {
+    const uint8_t* b = row + (size_t)(k0 >> 5) * 34;
+    r.d = tlx_ldu<uint16_t>(b);
+    r.q = tlx_ldu<u4_t>(b + 2 + 16 * ((k0 >> 4) & 1));
   }
-}
-
-// Q8_0 block (34 B: d, q i8[32]): d * q (exact in fp32).
-__device__ __forceinline__ void gx_dq_q80(float* v, const uint8_t* blk) {
-  const float d = gx_h2f(blk);
-#pragma unroll
-  for (int l = 0; l < 32; ++l) v[l] = d * (float)(int8_t)blk[2 + l];
+  return r;
 }
 
 template <int CLS>
-__device__ __forceinline__ void gx_dequant32(float* v, const uint8_t* row, int kc, int j, const float4* grid) {
-  if constexpr (CLS == GX_IQ3S) gx_dq_iq3s(v, row, kc, j, grid);
-  else if constexpr (CLS == GX_Q6K) gx_dq_q6k(v, row, kc, j);
-  else gx_dq_q80(v, row + (size_t)(8 * kc + j) * 34);
+__device__ __forceinline__ void gx_decode(float* v, const GxRaw<CLS>& r, const float4* grid) {
+  if constexpr (CLS == GX_IQ3S) {
+    const float db = tlx_h2f((uint16_t)(r.dn & 0xFFFFu)) * (float)(1u + 2u * (r.dn >> 16));   // exact
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {   // index byte i: weights 4i .. 4i+3
+      const uint32_t idx = ((r.qs >> (8 * i)) & 255u) | (((r.hs >> i) & 1u) << 8);
+      const float4 g = grid[idx];
+      const uint32_t sg = r.hs >> (8 + 4 * i);
+      const float gv[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float w = db * gv[c];
+        v[4 * i + c] = ((sg >> c) & 1u) ? -w : w;
+      }
+    }
+  } else if constexpr (CLS == GX_Q6K) {
+    const float t = tlx_h2f((uint16_t)(r.ds & 0xFFFFu)) * (float)(int8_t)(uint8_t)(r.ds >> 16);
+    const int g = (int)(r.ds >> 29) & 3;   // (kib >> 5) & 3
+#pragma unroll
+    for (int l = 0; l < 16; ++l) {
+      const uint32_t lb = (r.ql[l >> 2] >> (8 * (l & 3))) & 255u, hb = (r.qh[l >> 2] >> (8 * (l & 3))) & 255u;
+      const int lo = (g >> 1) ? (int)(lb >> 4) : (int)(lb & 15u);
+      const int q = lo | (int)(((hb >> (2 * g)) & 3u) << 4);
+      v[l] = t * (float)(q - 32);
+    }
+  } else {
+    const float d = tlx_h2f((uint16_t)r.d);
+#pragma unroll
+    for (int l = 0; l < 16; ++l) v[l] = d * (float)(int8_t)(uint8_t)(r.q[l >> 2] >> (8 * (l & 3)));
+  }
+}
+
+template <int CLS>
+__device__ __forceinline__ void gx_dequant16(float* v, const uint8_t* row, int k0, const float4* grid) {
+  gx_decode<CLS>(v, gx_fetch<CLS>(row, k0), grid);
 }
 
 template <int CLS, bool UP, int FORM>
@@ -141,7 +159,9 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
   constexpr int RB = (UP ? kFf : kHid) / kGxCols;         // column blocks per matrix
   constexpr int ROWB = K / GxFmt<CLS>::kPer * GxFmt<CLS>::kBlk;
   constexpr bool GRID = CLS == GX_IQ3S;
-  __shared__ GxLds<UP, GRID> L;
+  constexpr int TOK = gx_tok<FORM>();
+  constexpr int NG = TOK / 16;                            // 16-token MFMA groups per pass
+  __shared__ GxLds<UP, GRID, TOK> L;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 15, kq = lane >> 4;
   const int rb = (int)blockIdx.x % RB, item = (int)blockIdx.x / RB;
 
@@ -159,8 +179,8 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
     ntot = 1;
     wg = reinterpret_cast<const uint8_t*>(a.ptbl[a.eids[item]]);
   } else {
-    beg = item * kGxTok;
-    ntot = min(kGxTok, a.P - beg);
+    beg = item * TOK;
+    ntot = min(TOK, a.P - beg);
     wg = a.w0;
   }
   if constexpr (UP) wu = FORM == GX_DENSE ? a.w1 : wg + kIq3sGate;
@@ -168,11 +188,11 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
     for (int i = t; i < 512; i += kGxThreads) L.grid[i] = reinterpret_cast<const float4*>(a.grid)[i];
   }
 
-  for (int p0 = 0; p0 < ntot; p0 += kGxTok) {
-    const int nt = min(kGxTok, ntot - p0);
+  for (int p0 = 0; p0 < ntot; p0 += TOK) {
+    const int nt = min(TOK, ntot - p0);
     const int ng = (nt + 15) >> 4;
     __syncthreads();   // the previous pass is done with the token rows
-    if (t < kGxTok) {
+    if (t < TOK) {
       int xr = -1, orw = -1;
       if (t < nt) {
         const int pr = FORM == GX_SORTED ? (int)a.plist[beg + p0 + t] : beg + p0 + t;   // pair or position
@@ -182,44 +202,73 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
       L.xrow[t] = xr;
       L.orow[t] = orw;
     }
-    f4_t acc[4][UP ? 2 : 1];
+    f4_t acc[NG][UP ? 2 : 1];
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
+    for (int g = 0; g < NG; ++g)
 #pragma unroll
       for (int m = 0; m < (UP ? 2 : 1); ++m) acc[g][m] = f4_t{0.f, 0.f, 0.f, 0.f};
 
+    // the thread's weight units (staged row R, 16-weight piece q) and activation pieces
+    constexpr int NU = NR * (kGxKc / 16) / kGxThreads;       // units per thread (1 or 2)
+    constexpr int NX = (TOK * kGxKc / 8 + kGxThreads - 1) / kGxThreads;   // activation pieces per thread
+    static_assert(NR * (kGxKc / 16) % kGxThreads == 0, "units");
+    const uint8_t* urow[NU];
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+      const int R = (t + i * kGxThreads) >> 2;
+      urow[i] = ((UP && R >= kGxCols) ? wu : wg) + (size_t)(rb * kGxCols + (R & (kGxCols - 1))) * ROWB;
+    }
+    GxRaw<CLS> raw[NU];
+    float4 xv[NX][2];
+    // the activations' source rows for this thread's pieces (row 0 stands in past the pass: loaded,
+    // then replaced by zeros, so the loads stay unconditional)
+    int xo[NX];
+    bool xz[NX];
+    __syncthreads();   // the token rows are visible
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+      const int pc = t + i * kGxThreads;
+      const int xr = pc < TOK * kGxKc / 8 ? L.xrow[pc >> 3] : -1;
+      xz[i] = xr < 0;
+      xo[i] = (xr < 0 ? 0 : xr) * K + 8 * (pc & 7);
+    }
+#define GX_FETCH(KC)                                                                                 \
+  {                                                                                                  \
+    _Pragma("unroll") for (int i = 0; i < NU; ++i)                                                   \
+      raw[i] = gx_fetch<CLS>(urow[i], (KC) * kGxKc + 16 * ((t + i * kGxThreads) & 3));               \
+    _Pragma("unroll") for (int i = 0; i < NX; ++i) {                                                 \
+      const float4* src = reinterpret_cast<const float4*>(a.x + (size_t)xo[i] + (KC) * kGxKc);       \
+      xv[i][0] = src[0];                                                                             \
+      xv[i][1] = src[1];                                                                             \
+    }                                                                                                \
+  }
+    // gate+up (32 chunks): the next chunk's loads are issued before this chunk's MFMAs; down (8
+    // chunks): measured faster without (the prefetch registers cost occupancy)
+    constexpr bool PIPE = K / kGxKc > 8;
+    if constexpr (PIPE) GX_FETCH(0)
     for (int kc = 0; kc < K / kGxKc; ++kc) {
-      __syncthreads();   // the previous chunk's fragment reads are done; the token rows are visible
-      {   // activations: thread t covers token t >> 2, k (t & 3) * 64 .. + 63 (zeros past the pass)
-        const int tt = t >> 2, k0 = (t & 3) * 64;
-        const int xr = L.xrow[tt];
-        _Float16* dst = L.x + tt * kGxLd + k0;
+      if constexpr (!PIPE) GX_FETCH(kc)
+      __syncthreads();   // the previous chunk's fragment reads are done
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float f[8];
-          if (xr >= 0) {
-            const float4* src = reinterpret_cast<const float4*>(a.x + (size_t)xr * K + kc * kGxKc + k0 + 8 * i);
-            const float4 u = src[0], w = src[1];
-            f[0] = u.x; f[1] = u.y; f[2] = u.z; f[3] = u.w; f[4] = w.x; f[5] = w.y; f[6] = w.z; f[7] = w.w;
-          } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) f[j] = 0.f;
-          }
-          h8_t h;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) h[j] = (_Float16)f[j];
-          *reinterpret_cast<h8_t*>(dst + 8 * i) = h;
+      for (int i = 0; i < NX; ++i) {
+        const int pc = t + i * kGxThreads;
+        if (pc < TOK * kGxKc / 8) {
+          const float4 z = float4{0.f, 0.f, 0.f, 0.f};
+          const float4 u = xz[i] ? z : xv[i][0], w = xz[i] ? z : xv[i][1];
+          const h8_t h = {(_Float16)u.x, (_Float16)u.y, (_Float16)u.z, (_Float16)u.w,
+                          (_Float16)w.x, (_Float16)w.y, (_Float16)w.z, (_Float16)w.w};
+          *reinterpret_cast<h8_t*>(L.x + (pc >> 3) * kGxLd + 8 * (pc & 7)) = h;
         }
       }
-      // weights: units (staged row R, 32-weight group j), NR * 8 of them
-#pragma unroll 1
-      for (int u = t; u < NR * 8; u += kGxThreads) {
-        const int R = u >> 3, j = u & 7;
-        const int r = rb * kGxCols + (R & (kGxCols - 1));
-        const uint8_t* row = ((UP && R >= kGxCols) ? wu : wg) + (size_t)r * ROWB;
-        float v[32];
-        gx_dequant32<CLS>(v, row, kc, j, L.grid);
-        gx_store32(L.w + R * kGxLd + 32 * j, v);
+#pragma unroll
+      for (int i = 0; i < NU; ++i) {
+        const int u = t + i * kGxThreads;
+        float v[16];
+        gx_decode<CLS>(v, raw[i], L.grid);
+        gx_store16(L.w + (u >> 2) * kGxLd + 16 * (u & 3), v);
+      }
+      if constexpr (PIPE) {
+        if (kc + 1 < K / kGxKc) GX_FETCH(kc + 1)   // in flight over this chunk's MFMAs
       }
       __syncthreads();
 #pragma unroll
@@ -229,7 +278,7 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
         h8_t bu;
         if constexpr (UP) bu = *reinterpret_cast<const h8_t*>(L.w + (kGxCols + 16 * wave + col) * kGxLd + ko);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
+        for (int g = 0; g < NG; ++g) {
           if (g < ng) {
             const h8_t ax = *reinterpret_cast<const h8_t*>(L.x + (16 * g + col) * kGxLd + ko);
             acc[g][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, bg, acc[g][0], 0, 0, 0);
@@ -241,7 +290,7 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
     // lane (col, kq) holds tokens 16 g + 4 kq + r of output column rb * 64 + 16 wave + col
     const int n = rb * kGxCols + 16 * wave + col;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < NG; ++g) {
       if (g >= ng) break;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -261,8 +310,10 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
   }
 }
 
+#undef GX_FETCH
+
 // ------------------------------------------------------------------ dequantizers (bit-exact)
-// One thread per (row, 32-weight group).
+// One thread per (row, 16-weight piece).
 template <int CLS>
 __global__ __launch_bounds__(256) void gx_dequant_kernel(const uint8_t* __restrict__ w, const float* __restrict__ gridf,
                                                          void* __restrict__ out, int64_t rows, int kdim, int out_f16) {
@@ -272,21 +323,20 @@ __global__ __launch_bounds__(256) void gx_dequant_kernel(const uint8_t* __restri
     __syncthreads();
   }
   const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int ng = kdim >> 5;
-  if (u >= rows * ng) return;
-  const int64_t r = u / ng;
-  const int gi = (int)(u - r * ng);
+  const int np = kdim >> 4;
+  if (u >= rows * np) return;
+  const int64_t r = u / np;
+  const int pi = (int)(u - r * np);
   const int64_t rowb = (int64_t)kdim / GxFmt<CLS>::kPer * GxFmt<CLS>::kBlk;
-  const uint8_t* row = w + r * rowb;
-  float v[32];
-  gx_dequant32<CLS>(v, row, gi >> 3, gi & 7, grid);
-  const int64_t o = r * kdim + 32 * gi;
+  float v[16];
+  gx_dequant16<CLS>(v, w + r * rowb, 16 * pi, grid);
+  const int64_t o = r * kdim + 16 * pi;
   if (out_f16) {
 #pragma unroll
-    for (int l = 0; l < 32; ++l) reinterpret_cast<uint16_t*>(out)[o + l] = tlx_f2h_bits(v[l]);
+    for (int l = 0; l < 16; ++l) reinterpret_cast<uint16_t*>(out)[o + l] = tlx_f2h_bits(v[l]);
   } else {
 #pragma unroll
-    for (int l = 0; l < 32; ++l) reinterpret_cast<float*>(out)[o + l] = v[l];
+    for (int l = 0; l < 16; ++l) reinterpret_cast<float*>(out)[o + l] = v[l];
   }
 }
 
@@ -304,7 +354,7 @@ extern "C" int tlx_iq3s_dequant(const void* w, const float* gridf, void* out, in
   TLX_RET_IF(w == nullptr || gridf == nullptr || out == nullptr, TLX_E_ARG);
   TLX_RET_IF(rows < 1 || kdim < 256 || (kdim & 255) || kdim > (1 << 24), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(w, 2) || !tlx_aligned(gridf, 16) || !tlx_aligned(out, 4), TLX_E_ALIGN);
-  const int64_t units = rows * (kdim >> 5), grid = (units + 255) / 256;
+  const int64_t units = rows * (kdim >> 4), grid = (units + 255) / 256;
   TLX_RET_IF(grid > 0x7fffffff, TLX_E_ARG);
   gx_dequant_kernel<GX_IQ3S><<<(unsigned)grid, 256, 0, (hipStream_t)stream>>>((const uint8_t*)w, gridf, out, rows,
                                                                               (int)kdim, out_f16);
@@ -315,7 +365,7 @@ extern "C" int tlx_q8_0_dequant(const void* w, void* out, int64_t rows, int64_t 
   TLX_RET_IF(w == nullptr || out == nullptr, TLX_E_ARG);
   TLX_RET_IF(rows < 1 || kdim < 256 || (kdim & 255) || kdim > (1 << 24), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(w, 2) || !tlx_aligned(out, 4), TLX_E_ALIGN);
-  const int64_t units = rows * (kdim >> 5), grid = (units + 255) / 256;
+  const int64_t units = rows * (kdim >> 4), grid = (units + 255) / 256;
   TLX_RET_IF(grid > 0x7fffffff, TLX_E_ARG);
   gx_dequant_kernel<GX_Q80><<<(unsigned)grid, 256, 0, (hipStream_t)stream>>>((const uint8_t*)w, nullptr, out, rows,
                                                                              (int)kdim, out_f16);
@@ -371,7 +421,7 @@ extern "C" int tlx_moe_shared8(const void* wg, const void* wu, const void* wd, c
   TLX_RET_IF(!tlx_aligned(wg, 2) || !tlx_aligned(wu, 2) || !tlx_aligned(wd, 2), TLX_E_ALIGN);
   TLX_RET_IF(!tlx_aligned(x, 16) || !tlx_aligned(act, 16) || !tlx_aligned(y, 4), TLX_E_ALIGN);
   hipStream_t st = (hipStream_t)stream;
-  const int items = (P + kGxTok - 1) / kGxTok;
+  const int items = (P + gx_tok<GX_DENSE>() - 1) / gx_tok<GX_DENSE>();
   GxArgs a{};
   a.w0 = (const uint8_t*)wg; a.w1 = (const uint8_t*)wu; a.x = x; a.out = act; a.P = P;
   int r = gx_launch<GX_Q80, true, GX_DENSE>(a, items, st);

@@ -911,6 +911,37 @@ def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, s
     return y
 
 
+def moe_layer_ckpt(logits, sg, xs, hres, y, ptbl, ptbl_dn, shared8, gridf, scratch, stream=None, down="q6k",
+                   iq4nl=None, pair_walk=None):
+    """One MoE layer with the reference checkpoint's classes, the same sequence as moe_layer:
+    top-8, then the pair walk (P <= MOE_PAIR_WALK_MAX_P by default) or sort + grouped forms for
+    the IQ3_S gate+up, the down projection -- ``down`` "q6k" (Q6_K slabs, the checkpoint's layers
+    34/38/39) or "iq4" (IQ4_XS GGUF-row slabs, iq4nl given) -- the Q8_0 shared expert
+    (shared8 = (wg, wu, wd) rows), and the combine into y."""
+    sc = scratch
+    if pair_walk is None:
+        pair_walk = xs.shape[0] <= MOE_PAIR_WALK_MAX_P
+    cur = stream if isinstance(stream, torch.cuda.Stream) else torch.cuda.current_stream()
+    moe_topk(logits, sc.eids, sc.gates, stream=cur)
+    eids = sc.eids.view(-1)
+    if pair_walk:
+        moe_up3s_pairs(ptbl, eids, xs, gridf, sc.act, stream=cur)
+        if down == "q6k":
+            moe_dn6_pairs(ptbl_dn, eids, sc.act, sc.parts, stream=cur)
+        else:
+            moe_dn4_pairs(ptbl_dn, eids, sc.act, iq4nl, sc.parts, stream=cur)
+    else:
+        moe_sort(sc.eids, sc.eoff, sc.plist, sc.items, sc.nitp, stream=cur)
+        moe_up3s(ptbl, sc.eoff, sc.plist, xs, gridf, sc.act, stream=cur)
+        if down == "q6k":
+            moe_dn6(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, sc.parts, stream=cur)
+        else:
+            moe_dn4(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, iq4nl, sc.parts, stream=cur)
+    moe_shared8(*shared8, xs, sc.shared, sc.sact, stream=cur)
+    moe_combine(sc.parts, sc.gates, sg, sc.shared, hres, y, stream=cur)
+    return y
+
+
 # ------------------------------------------------------------------ measurement
 def stream_read(src, sink, stream=None):
     """Read all of ``src`` once (HBM read-stream probe); ``sink`` receives one uint32 per wave.
