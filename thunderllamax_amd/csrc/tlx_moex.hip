@@ -55,6 +55,7 @@ struct GxArgs {
   const float* grid;       // IQ3_S grid f32 [512][4]
   void* out;               // gate+up: f32 [pairs or P][512]; down: f16 [pairs][2048] or (dense) f32 [P][2048]
   int P;
+  int items;               // work items: experts (sorted), pairs (pair walk) or 64-position passes (dense)
 };
 
 template <bool UP, bool GRID, int TOK>
@@ -163,7 +164,12 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
   constexpr int NG = TOK / 16;                            // 16-token MFMA groups per pass
   __shared__ GxLds<UP, GRID, TOK> L;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 15, kq = lane >> 4;
-  const int rb = (int)blockIdx.x % RB, item = (int)blockIdx.x / RB;
+  // Workgroups go to the 8 XCDs round robin (block b to XCD b % 8), each XCD with its own L2.  The RB
+  // column blocks of one item are all placed on one XCD, so the item's activation rows -- read by
+  // every column block -- come from HBM once and from that XCD's L2 after.
+  const int slot = (int)blockIdx.x >> 3;
+  const int rb = slot % RB, item = slot / RB * 8 + ((int)blockIdx.x & 7);
+  if (item >= a.items) return;   // the grid is padded to a multiple of 8 items
 
   // the work item: token list, weight matrices
   int beg = 0, ntot = 0;
@@ -343,7 +349,9 @@ __global__ __launch_bounds__(256) void gx_dequant_kernel(const uint8_t* __restri
 template <int CLS, bool UP, int FORM>
 int gx_launch(const GxArgs& a, int items, hipStream_t st) {
   constexpr int RB = (UP ? kFf : kHid) / kGxCols;
-  gx_kernel<CLS, UP, FORM><<<(unsigned)(items * RB), kGxThreads, 0, st>>>(a);
+  GxArgs b = a;
+  b.items = items;
+  gx_kernel<CLS, UP, FORM><<<(unsigned)((items + 7) / 8 * 8 * RB), kGxThreads, 0, st>>>(b);
   return tlx_launch_status();
 }
 
