@@ -5,8 +5,10 @@ expert (shexp8), and the IQ3_S / Q8_0 dequantizers.
 * Dequantizers: bit for bit against quants.dequant_iq3s / dequant_q8_0 (f32), and the f16 outputs
   against the same values rounded by numpy (round to nearest even).
 * Expert GEMMs: norm-wise rel-err <= 1e-3 per output row against the float64 products of the
-  dequantized weights (moe.up3s_ref / down6_ref / shared8_ref); the pair walk and the sorted form
-  bit for bit equal; two calls bit for bit equal.
+  dequantized weights (moe.up3s_ref / down6_ref / shared8_ref), for the sorted form and the pair
+  walk each; the two forms within 1e-5 of each other (f32 act; the pair walk's k-steps take the
+  same products in another order) and within half an fp16 ulp norm-wise (parts); two calls bit for
+  bit equal.
 * The IQ3_S grid is synthetic (synth.iq3s_grid: ggml's level set, random entries): the real table
   is a third-party constant absent here, and the kernels take it at run time as the reference's do.
 """
@@ -95,15 +97,25 @@ def _run(gpu, ck, x, eids, eoff, plist, items, nitp, np_):
     return act.cpu().numpy(), act_w.cpu().numpy(), parts.cpu().numpy(), parts_w.cpu().numpy()
 
 
-def _check_pairs(ck, x, eids, act, parts, pairs):
+def _check_pairs(ck, x, eids, act, parts, pairs, act_in=None):
+    """act against the oracle's gate+up of x, parts against its down projection of act_in (the
+    activations the down kernel read; act by default)."""
+    act_in = act if act_in is None else act_in
     by_e = {}
     for p in pairs:
         by_e.setdefault(int(eids[p]), []).append(p)
     for e, prs in by_e.items():
         ref = moe.up3s_ref(ck["gu"][e], ck["grid"], x[[p // 8 for p in prs]])
         assert _rows_err(act[prs], ref) <= TOL, e
-        part = moe.down6_ref(ck["dn"][e], act[prs])
+        part = moe.down6_ref(ck["dn"][e], act_in[prs])
         assert _rows_err(parts[prs].astype(np.float64), part) <= TOL, e
+
+
+def _forms_agree(act, act_w, parts, parts_w):
+    assert _rows_err(act_w, act.astype(np.float64)) <= 1e-5
+    # fp16 outputs: a reordered f32 sum can round to a neighbouring fp16 value, several ulps of an
+    # output that cancels towards zero -- a norm-wise bound, half an fp16 ulp of the row
+    assert _rows_err(parts_w.astype(np.float64), parts.astype(np.float64)) <= 2.0 ** -11
 
 
 def test_ckpt_experts_decode_m11(gpu, ckpt):
@@ -112,9 +124,26 @@ def test_ckpt_experts_decode_m11(gpu, ckpt):
     P = 11
     x, eids, deids, eoff, plist, items, nitp = _route(gpu, rng, P)
     act, act_w, parts, parts_w = _run(gpu, ckpt, x, deids, eoff, plist, items, nitp, 8 * P)
-    assert np.array_equal(act.view(np.uint32), act_w.view(np.uint32))
-    assert np.array_equal(parts.view(np.uint16), parts_w.view(np.uint16))
+    _forms_agree(act, act_w, parts, parts_w)
     _check_pairs(ckpt, x, eids, act, parts, list(range(8 * P)))
+    _check_pairs(ckpt, x, eids, act_w, parts_w, list(range(8 * P)), act_in=act)
+
+
+def test_ckpt_pairs_ragged(gpu, ckpt):
+    """The pair walk at pair counts that are not a multiple of 8 (the grid's padding): 1 and 13."""
+    rng = np.random.default_rng(48)
+    x, eids, deids, *_ = _route(gpu, rng, 2)
+    dx = torch.from_numpy(x).to(gpu)
+    for np_ in (1, 13):
+        print(f"[case] IQ3_S up + Q6_K down pair walk, {np_} pairs", flush=True)
+        act = torch.full((np_ + 3, moe.FF), -7.0, dtype=torch.float32, device=gpu)
+        parts = torch.full((np_ + 3, moe.HID), -7.0, dtype=torch.float16, device=gpu)
+        ops.moe_up3s_pairs(ckpt["ptbl"], deids[:np_], dx, ckpt["gridf"], act[:np_])
+        ops.moe_dn6_pairs(ckpt["ptbl_dn"], deids[:np_], act[:np_], parts[:np_])
+        torch.cuda.synchronize()
+        a, pt = act.cpu().numpy(), parts.cpu().numpy()
+        assert np.all(a[np_:] == -7.0) and np.all(pt[np_:] == -7.0)   # nothing past the pairs
+        _check_pairs(ckpt, x, eids, a, pt, list(range(np_)))
 
 
 def test_ckpt_experts_prefill_m2048(gpu, ckpt):
@@ -123,21 +152,24 @@ def test_ckpt_experts_prefill_m2048(gpu, ckpt):
     P = 2048
     x, eids, deids, eoff, plist, items, nitp = _route(gpu, rng, P)
     act, act_w, parts, parts_w = _run(gpu, ckpt, x, deids, eoff, plist, items, nitp, 8 * P)
-    assert np.array_equal(act.view(np.uint32), act_w.view(np.uint32))
-    assert np.array_equal(parts.view(np.uint16), parts_w.view(np.uint16))
+    _forms_agree(act, act_w, parts, parts_w)
     again = _run(gpu, ckpt, x, deids, eoff, plist, items, nitp, 8 * P)
     assert np.array_equal(again[0].view(np.uint32), act.view(np.uint32))
+    assert np.array_equal(again[1].view(np.uint32), act_w.view(np.uint32))
     assert np.array_equal(again[2].view(np.uint16), parts.view(np.uint16))
+    assert np.array_equal(again[3].view(np.uint16), parts_w.view(np.uint16))
     # the largest bins (several 64-token passes) and a spread of others
     cnt = np.bincount(eids, minlength=moe.E)
     big = np.argsort(-cnt)[:2]
     pairs = [int(p) for e in big for p in np.nonzero(eids == e)[0][::7]]
     pairs += [int(p) for p in np.random.default_rng(5).choice(8 * P, 48, replace=False)]
     _check_pairs(ckpt, x, eids, act, parts, sorted(set(pairs)))
+    _check_pairs(ckpt, x, eids, act_w, parts_w, sorted(set(pairs)), act_in=act)
 
 
-@pytest.mark.parametrize("P", [11, 300])
+@pytest.mark.parametrize("P", [1, 11, 16, 17, 300])
 def test_ckpt_shared_q80(gpu, ckpt, P):
+    """P <= 16 runs the decode (GEMV-shaped) form, larger P the LDS-staged one."""
     print(f"[case] Q8_0 shared expert P={P}", flush=True)
     rng = np.random.default_rng(45 + P)
     x = synth.bf16_round(0.05 * rng.standard_normal((P, moe.HID)).astype(np.float32))

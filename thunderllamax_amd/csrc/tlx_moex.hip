@@ -67,7 +67,17 @@ struct GxLds {
   int orow[TOK];
 };
 
-__device__ __forceinline__ float gx_h2f(const uint8_t* p) { return tlx_h2f(tlx_ldu<uint16_t>(p)); }
+// Weight bytes are read through global-address-space pointers: the compiler then emits global
+// loads, which count on the vector-memory counter only -- flat loads also count on the LDS one, so
+// every wait for an LDS read would wait for the weight loads in flight as well.  Records are only
+// 2-B aligned (110-, 210- and 34-B blocks): gx_ld reads through an under-aligned type.
+using gbyte = const __attribute__((address_space(1))) uint8_t;
+
+template <typename T>
+__device__ __forceinline__ T gx_ld(gbyte* p) {
+  typedef T __attribute__((aligned(1))) T1;
+  return *reinterpret_cast<const __attribute__((address_space(1))) T1*>(p);
+}
 
 __device__ __forceinline__ void gx_store16(_Float16* dst, const float* v) {
 #pragma unroll
@@ -92,25 +102,25 @@ template <> struct GxRaw<GX_Q6K> { uint32_t ds; u4_t ql, qh; };   // d | sc << 1
 template <> struct GxRaw<GX_Q80> { uint32_t d; u4_t q; };
 
 template <int CLS>
-__device__ __forceinline__ GxRaw<CLS> gx_fetch(const uint8_t* row, int k0) {
+__device__ __forceinline__ GxRaw<CLS> gx_fetch(gbyte* row, int k0) {
   GxRaw<CLS> r;
   if constexpr (CLS == GX_IQ3S) {
-    const uint8_t* b = row + (size_t)(k0 >> 8) * 110;
+    gbyte* b = row + (size_t)(k0 >> 8) * 110;
     const int kib = k0 & 255, j = kib >> 5, hf = (kib >> 4) & 1;
     const uint32_t nib = (b[106 + (j >> 1)] >> (4 * (j & 1))) & 15u;
-    r.dn = tlx_ldu<uint16_t>(b) | (nib << 16);
-    r.qs = tlx_ldu<uint32_t>(b + 2 + 8 * j + 4 * hf);
-    r.hs = ((uint32_t)(b[66 + j] >> (4 * hf)) & 15u) | ((uint32_t)tlx_ldu<uint16_t>(b + 74 + 4 * j + 2 * hf) << 8);
+    r.dn = gx_ld<uint16_t>(b) | (nib << 16);
+    r.qs = gx_ld<uint32_t>(b + 2 + 8 * j + 4 * hf);
+    r.hs = ((uint32_t)(b[66 + j] >> (4 * hf)) & 15u) | ((uint32_t)gx_ld<uint16_t>(b + 74 + 4 * j + 2 * hf) << 8);
   } else if constexpr (CLS == GX_Q6K) {
-    const uint8_t* b = row + (size_t)(k0 >> 8) * 210;
+    gbyte* b = row + (size_t)(k0 >> 8) * 210;
     const int kib = k0 & 255, h = kib >> 7, g = (kib >> 5) & 3, l0 = kib & 31;
-    r.ds = tlx_ldu<uint16_t>(b + 208) | ((uint32_t)b[192 + 8 * h + (l0 >> 4) + 2 * g] << 16) | ((uint32_t)kib << 24);
-    r.ql = tlx_ldu<u4_t>(b + 64 * h + 32 * (g & 1) + l0);
-    r.qh = tlx_ldu<u4_t>(b + 128 + 32 * h + l0);
+    r.ds = gx_ld<uint16_t>(b + 208) | ((uint32_t)b[192 + 8 * h + (l0 >> 4) + 2 * g] << 16) | ((uint32_t)kib << 24);
+    r.ql = gx_ld<u4_t>(b + 64 * h + 32 * (g & 1) + l0);
+    r.qh = gx_ld<u4_t>(b + 128 + 32 * h + l0);
   } else {
-    const uint8_t* b = row + (size_t)(k0 >> 5) * 34;
-    r.d = tlx_ldu<uint16_t>(b);
-    r.q = tlx_ldu<u4_t>(b + 2 + 16 * ((k0 >> 4) & 1));
+    gbyte* b = row + (size_t)(k0 >> 5) * 34;
+    r.d = gx_ld<uint16_t>(b);
+    r.q = gx_ld<u4_t>(b + 2 + 16 * ((k0 >> 4) & 1));
   }
   return r;
 }
@@ -149,7 +159,7 @@ __device__ __forceinline__ void gx_decode(float* v, const GxRaw<CLS>& r, const f
 }
 
 template <int CLS>
-__device__ __forceinline__ void gx_dequant16(float* v, const uint8_t* row, int k0, const float4* grid) {
+__device__ __forceinline__ void gx_dequant16(float* v, gbyte* row, int k0, const float4* grid) {
   gx_decode<CLS>(v, gx_fetch<CLS>(row, k0), grid);
 }
 
@@ -173,23 +183,23 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
 
   // the work item: token list, weight matrices
   int beg = 0, ntot = 0;
-  const uint8_t* wg = nullptr;
-  const uint8_t* wu = nullptr;
+  gbyte* wg = nullptr;
+  gbyte* wu = nullptr;
   if constexpr (FORM == GX_SORTED) {
     beg = a.eoff[item];
     ntot = a.eoff[item + 1] - beg;
     if (ntot <= 0) return;   // uniform per workgroup
-    wg = reinterpret_cast<const uint8_t*>(a.ptbl[item]);
+    wg = reinterpret_cast<gbyte*>(a.ptbl[item]);
   } else if constexpr (FORM == GX_PAIRS) {
     beg = item;
     ntot = 1;
-    wg = reinterpret_cast<const uint8_t*>(a.ptbl[a.eids[item]]);
+    wg = reinterpret_cast<gbyte*>(a.ptbl[a.eids[item]]);
   } else {
     beg = item * TOK;
     ntot = min(TOK, a.P - beg);
-    wg = a.w0;
+    wg = (gbyte*)a.w0;
   }
-  if constexpr (UP) wu = FORM == GX_DENSE ? a.w1 : wg + kIq3sGate;
+  if constexpr (UP) wu = FORM == GX_DENSE ? (gbyte*)a.w1 : wg + kIq3sGate;
   if constexpr (GRID) {
     for (int i = t; i < 512; i += kGxThreads) L.grid[i] = reinterpret_cast<const float4*>(a.grid)[i];
   }
@@ -218,7 +228,7 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
     constexpr int NU = NR * (kGxKc / 16) / kGxThreads;       // units per thread (1 or 2)
     constexpr int NX = (TOK * kGxKc / 8 + kGxThreads - 1) / kGxThreads;   // activation pieces per thread
     static_assert(NR * (kGxKc / 16) % kGxThreads == 0, "units");
-    const uint8_t* urow[NU];
+    gbyte* urow[NU];
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
       const int R = (t + i * kGxThreads) >> 2;
@@ -318,6 +328,285 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
 
 #undef GX_FETCH
 
+// ------------------------------------------------------------------ decode form (GEMV-shaped)
+// Items of at most 16 tokens -- the pair walk (one token a pair) and the shared expert at P <= 16
+// -- bypass the LDS weight stage: a 16-row tile (gate+up: the gate tile and its up tile) is walked
+// by KS waves, each over K / KS of k, in units of 256 weights.  Lane (col, kq) fetches the bytes
+// of row col that hold its 64 weights of a unit (contiguous in the record where the class allows)
+// straight into registers, a few units ahead, and builds the B operand of each of the unit's 8
+// k-steps from them.  Which 8 weights a lane feeds a step is a fixed permutation of the unit's k
+// (gv_koff); the activations -- fp16 in LDS, natural k order -- are read at the same k, so the
+// products and their sums are those of the LDS-staged form up to the order of the fp32 sums.
+constexpr int kGvTok = 16;
+
+template <int CLS> struct GvRaw;
+template <> struct GvRaw<GX_IQ3S> { u4_t qs; uint32_t sg0, sg1, dq, sc; };    // dq: d | qh pair << 16
+template <> struct GvRaw<GX_Q6K> { u4_t ql0, ql1, qh0, qh1; uint32_t sc, d; };  // sc: 4 scale bytes
+template <> struct GvRaw<GX_Q80> { u4_t q0, q1, q2, q3; uint32_t d; };          // d: two blocks' d
+
+// Lane kq's bytes of unit u of a row.
+// IQ3_S (110-B block = unit): weights 64 kq .. 64 kq + 63 -- index bytes qs[16 kq ..], high bits
+// qh[2 kq], qh[2 kq + 1], sign bytes signs[8 kq ..], scale byte 106 + kq (sub-blocks 2 kq, 2 kq + 1).
+// Q6_K (210-B block = unit): ql bytes 32 kq .. 32 kq + 31, both nibbles (half h = kq / 2, c = kq % 2:
+// weights 128 h + 32 c + l and 128 h + 64 + 32 c + l), qh bytes 32 h .. 32 h + 31, scale bytes
+// 8 h + 2 c + {0, 1, 4, 5}.
+// Q8_0 (8 blocks of 34 B = unit): blocks 2 kq and 2 kq + 1.
+template <int CLS>
+__device__ __forceinline__ GvRaw<CLS> gv_fetch(gbyte* row, int u, int kq) {
+  GvRaw<CLS> r;
+  if constexpr (CLS == GX_IQ3S) {
+    gbyte* b = row + (size_t)u * 110;
+    r.qs = gx_ld<u4_t>(b + 2 + 16 * kq);
+    const uint64_t sg = gx_ld<uint64_t>(b + 74 + 8 * kq);
+    r.sg0 = (uint32_t)sg;
+    r.sg1 = (uint32_t)(sg >> 32);
+    r.dq = gx_ld<uint16_t>(b) | ((uint32_t)gx_ld<uint16_t>(b + 66 + 2 * kq) << 16);
+    r.sc = b[106 + kq];
+  } else if constexpr (CLS == GX_Q6K) {
+    gbyte* b = row + (size_t)u * 210;
+    const int h = kq >> 1, c = kq & 1;
+    r.ql0 = gx_ld<u4_t>(b + 32 * kq);
+    r.ql1 = gx_ld<u4_t>(b + 32 * kq + 16);
+    r.qh0 = gx_ld<u4_t>(b + 128 + 32 * h);
+    r.qh1 = gx_ld<u4_t>(b + 128 + 32 * h + 16);
+    r.sc = gx_ld<uint16_t>(b + 192 + 8 * h + 2 * c) | ((uint32_t)gx_ld<uint16_t>(b + 196 + 8 * h + 2 * c) << 16);
+    r.d = gx_ld<uint16_t>(b + 208);
+  } else {
+    gbyte* b = row + (size_t)u * 272 + 68 * kq;
+    r.q0 = gx_ld<u4_t>(b + 2);
+    r.q1 = gx_ld<u4_t>(b + 18);
+    r.q2 = gx_ld<u4_t>(b + 36);
+    r.q3 = gx_ld<u4_t>(b + 52);
+    r.d = gx_ld<uint16_t>(b) | ((uint32_t)gx_ld<uint16_t>(b + 34) << 16);
+  }
+  return r;
+}
+
+// the unit-relative k of the 8 weights lane kq feeds k-step s (they are consecutive)
+template <int CLS>
+__device__ __forceinline__ int gv_koff(int kq, int s) {
+  if constexpr (CLS == GX_Q6K) return 128 * (kq >> 1) + 32 * (kq & 1) + 64 * (s >> 2) + 8 * (s & 3);
+  return 64 * kq + 8 * s;
+}
+
+// IQ3_S lookups of the decode form, in LDS: the grid as fp16 (4 halves an entry, 8 B -- exact for
+// the IQ3_S grid's integer levels; other values take one extra rounding, to fp16, before the
+// product) and the fp16 sign masks of 4 weights per sign nibble (16 entries: all in distinct
+// banks, so a wave's lookups do not conflict)
+struct GvLut {
+  uint2 grid[512];
+  uint2 smask[16];
+};
+
+template <bool G> struct GvLutSlot { GvLut v; };
+template <> struct GvLutSlot<false> {};
+
+template <int NT>
+__device__ __forceinline__ void gv_lut_fill(GvLut& L, const float* gridf, int t) {
+  for (int i = t; i < 512; i += NT) {
+    const float4 g = reinterpret_cast<const float4*>(gridf)[i];
+    L.grid[i] = uint2{(uint32_t)tlx_f2h_bits(g.x) | ((uint32_t)tlx_f2h_bits(g.y) << 16),
+                      (uint32_t)tlx_f2h_bits(g.z) | ((uint32_t)tlx_f2h_bits(g.w) << 16)};
+  }
+  if (t < 16)
+    L.smask[t] = uint2{((t & 1u) << 15) | (((t >> 1) & 1u) << 31), (((t >> 2) & 1u) << 15) | (((t >> 3) & 1u) << 31)};
+}
+
+// fp16 pair {db * lo(g2), db * hi(g2)}, each the f32 product (exact here: db has at most 16
+// significant bits, a grid level at most 4) rounded once to fp16 -- v_fma_mix takes the fp16 halves
+// of g2 as operands, so the grid needs no widening
+__device__ __forceinline__ uint32_t gv_mix2(float db, uint32_t g2) {
+  uint32_t r;
+  asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+      : "=&v"(r)
+      : "v"(db), "v"(g2));
+  return r;
+}
+
+// fp16 pairs {bytes 0, 1} (hi = 0) or {bytes 2, 3} (hi = 1) of v as the integers byte - bias: v_perm
+// puts 0x64 above each byte (the fp16 1024 + byte, exact), a packed fp16 add takes 1024 + bias off
+// (exact: small integers)
+__device__ __forceinline__ uint32_t gv_bytes_h2(uint32_t v, int hi, float bias) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  const uint32_t p = __builtin_amdgcn_perm(0x64646464u, v, hi ? 0x04030402u : 0x04010400u);
+  const _Float16 o = (_Float16)(1024.f + bias);
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p) - h2_t{o, o});
+}
+
+// B operand of k-step s: fp16 of the GGUF values, the product of the block scale and the integer
+// level rounded to fp16 -- for IQ3_S and Q8_0 the product is exact in f32, so these are gx_decode's
+// operands bit for bit; Q6_K's can exceed f32's 24 bits, where gx_decode rounds twice (to f32, then
+// fp16) and v_fma_mix may round once, an fp16 ulp apart in rare ties
+template <int CLS, int S>
+__device__ __forceinline__ h8_t gv_decode(const GvRaw<CLS>& r, int kq, const GvLut* lut) {
+  if constexpr (CLS == GX_IQ3S) {
+    const float db = tlx_h2f((uint16_t)(r.dq & 0xFFFFu)) * (float)(1u + 2u * ((r.sc >> (4 * (S >> 2))) & 15u));
+    const uint32_t qsw = r.qs[S >> 1] >> (16 * (S & 1));
+    const uint32_t qh = r.dq >> (16 + 2 * S);
+    const uint2 g0 = lut->grid[(qsw & 255u) | ((qh & 1u) << 8)];
+    const uint2 g1 = lut->grid[((qsw >> 8) & 255u) | ((qh & 2u) << 7)];
+    const uint32_t sb = (S < 4 ? r.sg0 : r.sg1) >> (8 * (S & 3));
+    const uint2 m0 = lut->smask[sb & 15u], m1 = lut->smask[(sb >> 4) & 15u];
+    const u4_t h = {gv_mix2(db, g0.x) ^ m0.x, gv_mix2(db, g0.y) ^ m0.y, gv_mix2(db, g1.x) ^ m1.x, gv_mix2(db, g1.y) ^ m1.y};
+    return __builtin_bit_cast(h8_t, h);
+  } else if constexpr (CLS == GX_Q6K) {
+    constexpr int n = S >> 2, q = S & 3;
+    const u4_t& ql = (q < 2) ? r.ql0 : r.ql1;
+    const u4_t& qv = (q < 2) ? r.qh0 : r.qh1;
+    const uint32_t sh = 2u * (uint32_t)(kq & 1) + 4u * n;   // the quarter's 2 high bits
+    const float t = tlx_h2f((uint16_t)r.d) * (float)(int8_t)(uint8_t)(r.sc >> (8 * ((q >> 1) + 2 * n)));
+    u4_t h;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t q4 = ((ql[2 * (q & 1) + j] >> (4 * n)) & 0x0F0F0F0Fu) | (((qv[2 * (q & 1) + j] >> sh) & 0x03030303u) << 4);
+      h[2 * j] = gv_mix2(t, gv_bytes_h2(q4, 0, 32.f));       // t * (q - 32)
+      h[2 * j + 1] = gv_mix2(t, gv_bytes_h2(q4, 1, 32.f));
+    }
+    return __builtin_bit_cast(h8_t, h);
+  } else {
+    constexpr int blk = S >> 2, q = S & 3;
+    const u4_t& qv = blk ? ((q < 2) ? r.q2 : r.q3) : ((q < 2) ? r.q0 : r.q1);
+    const float d = tlx_h2f((uint16_t)(r.d >> (16 * blk)));
+    u4_t h;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t u4 = qv[2 * (q & 1) + j] ^ 0x80808080u;   // int8 + 128
+      h[2 * j] = gv_mix2(d, gv_bytes_h2(u4, 0, 128.f));
+      h[2 * j + 1] = gv_mix2(d, gv_bytes_h2(u4, 1, 128.f));
+    }
+    return __builtin_bit_cast(h8_t, h);
+  }
+}
+
+template <int CLS, bool UP, int FORM, int KS, int NW>
+struct GvShape {
+  static constexpr int K = UP ? kHid : kFf, NU = K / 256, NM = UP ? 2 : 1;
+  static constexpr int TW = NW / KS;                     // tiles per workgroup (NW waves)
+  static constexpr int RB = (UP ? kFf : kHid) / (16 * TW);   // workgroups per item
+  static constexpr int TOKR = FORM == GX_PAIRS ? 1 : kGvTok;   // staged token rows
+  static constexpr int LDX = K + 8;                      // token row stride (halfs)
+};
+
+template <int CLS, bool UP, int FORM, int KS, int NW>
+__global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
+  using S = GvShape<CLS, UP, FORM, KS, NW>;
+  constexpr int NT = 64 * NW;
+  constexpr int K = S::K, NU = S::NU, NM = S::NM, TW = S::TW, RB = S::RB, TOKR = S::TOKR, LDX = S::LDX;
+  constexpr int ROWB = K / GxFmt<CLS>::kPer * GxFmt<CLS>::kBlk;
+  constexpr int UW = NU / KS;                            // units per wave
+  constexpr int DEPTH = UW < 4 ? UW : 4;                 // units in flight
+  constexpr bool GRID = CLS == GX_IQ3S;
+  static_assert(NU % KS == 0 && NW % KS == 0, "k split");
+  __shared__ _Float16 xs[TOKR * LDX];
+  __shared__ GvLutSlot<GRID> lslot;
+  __shared__ f4_t red[KS > 1 ? (KS - 1) * TW * NM * 64 : 1];
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 15, kq = lane >> 4;
+  const int tile = wave / KS, kp = wave % KS;
+  // the XCD-aware order of gx_kernel: an item's workgroups on one XCD
+  const int slot = (int)blockIdx.x >> 3;
+  const int rb = slot % RB, item = slot / RB * 8 + ((int)blockIdx.x & 7);
+  if (item >= a.items) return;
+
+  int beg, nt;
+  gbyte* wg;
+  if constexpr (FORM == GX_PAIRS) {
+    beg = item;
+    nt = 1;
+    wg = reinterpret_cast<gbyte*>(a.ptbl[a.eids[item]]);
+  } else {
+    beg = item * kGvTok;
+    nt = min(kGvTok, a.P - beg);
+    wg = (gbyte*)a.w0;
+  }
+  gbyte* wu = UP ? (FORM == GX_DENSE ? (gbyte*)a.w1 : wg + kIq3sGate) : wg;
+  const GvLut* lut = nullptr;
+  if constexpr (GRID) {
+    gv_lut_fill<NT>(lslot.v, a.grid, t);
+    lut = &lslot.v;
+  }
+  // token rows, fp16 (round to nearest even); rows past the item repeat its last (not stored)
+  for (int pc = t; pc < TOKR * (K / 8); pc += NT) {
+    const int r = pc / (K / 8), k8 = pc - r * (K / 8);
+    const int xr = FORM == GX_PAIRS ? (UP ? beg >> 3 : beg) : beg + min(r, nt - 1);
+    const float4* src = reinterpret_cast<const float4*>(a.x + (size_t)xr * K + 8 * k8);
+    const float4 u = src[0], v = src[1];
+    const h8_t h = {(_Float16)u.x, (_Float16)u.y, (_Float16)u.z, (_Float16)u.w,
+                    (_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+    *reinterpret_cast<h8_t*>(xs + r * LDX + 8 * k8) = h;
+  }
+
+  const int n = rb * (16 * TW) + 16 * tile + col;   // output column (weight row) of the lane
+  gbyte* rows[NM];
+  rows[0] = wg + (size_t)n * ROWB;
+  if constexpr (UP) rows[NM - 1] = wu + (size_t)n * ROWB;
+  const int u0 = kp * UW;
+  GvRaw<CLS> raw[UW][NM];
+#pragma unroll
+  for (int u = 0; u < DEPTH; ++u)
+#pragma unroll
+    for (int m = 0; m < NM; ++m) raw[u][m] = gv_fetch<CLS>(rows[m], u0 + u, kq);
+  __syncthreads();   // token rows, lookups
+  const _Float16* xrow = xs + (FORM == GX_PAIRS ? 0 : col) * LDX;
+  f4_t acc[NM];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) acc[m] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < UW; ++u) {
+    if (u + DEPTH < UW) {
+#pragma unroll
+      for (int m = 0; m < NM; ++m) raw[u + DEPTH][m] = gv_fetch<CLS>(rows[m], u0 + u + DEPTH, kq);
+    }
+    const _Float16* xu = xrow + 256 * (u0 + u);
+#define GV_STEP(SS)                                                                          \
+  {                                                                                          \
+    const h8_t ax = *reinterpret_cast<const h8_t*>(xu + gv_koff<CLS>(kq, SS));               \
+    _Pragma("unroll") for (int m = 0; m < NM; ++m) {                                         \
+      const h8_t bw = gv_decode<CLS, SS>(raw[u][m], kq, lut);                        \
+      acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, bw, acc[m], 0, 0, 0);              \
+    }                                                                                        \
+  }
+    GV_STEP(0) GV_STEP(1) GV_STEP(2) GV_STEP(3) GV_STEP(4) GV_STEP(5) GV_STEP(6) GV_STEP(7)
+#undef GV_STEP
+  }
+  // k-split: the tile's waves add in kp order
+  if constexpr (KS > 1) {
+    if (kp != 0) {
+#pragma unroll
+      for (int m = 0; m < NM; ++m) red[(((kp - 1) * TW + tile) * NM + m) * 64 + lane] = acc[m];
+    }
+    __syncthreads();
+    if (kp != 0) return;
+#pragma unroll
+    for (int j = 1; j < KS; ++j)
+#pragma unroll
+      for (int m = 0; m < NM; ++m) acc[m] += red[(((j - 1) * TW + tile) * NM + m) * 64 + lane];
+  }
+  // lane (col, kq) holds tokens 4 kq + r of column n
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int tk = 4 * kq + r;
+    if (tk >= nt) continue;
+    const size_t o = (size_t)(beg + (FORM == GX_PAIRS ? 0 : tk));
+    if constexpr (UP) {
+      const float gv = acc[0][r], uv = acc[NM - 1][r];
+      reinterpret_cast<float*>(a.out)[o * kFf + n] = gv / (1.f + expf(-gv)) * uv;
+    } else if constexpr (FORM == GX_DENSE) {
+      reinterpret_cast<float*>(a.out)[o * kHid + n] = acc[0][r];
+    } else {
+      reinterpret_cast<_Float16*>(a.out)[o * kHid + n] = (_Float16)acc[0][r];
+    }
+  }
+}
+
+template <int CLS, bool UP, int FORM, int KS, int NW>
+int gv_launch(const GxArgs& a, int items, hipStream_t st) {
+  GxArgs b = a;
+  b.items = items;
+  gv_kernel<CLS, UP, FORM, KS, NW><<<(unsigned)((items + 7) / 8 * 8 * GvShape<CLS, UP, FORM, KS, NW>::RB), 64 * NW, 0, st>>>(b);
+  return tlx_launch_status();
+}
+
 // ------------------------------------------------------------------ dequantizers (bit-exact)
 // One thread per (row, 16-weight piece).
 template <int CLS>
@@ -335,7 +624,7 @@ __global__ __launch_bounds__(256) void gx_dequant_kernel(const uint8_t* __restri
   const int pi = (int)(u - r * np);
   const int64_t rowb = (int64_t)kdim / GxFmt<CLS>::kPer * GxFmt<CLS>::kBlk;
   float v[16];
-  gx_dequant16<CLS>(v, w + r * rowb, 16 * pi, grid);
+  gx_dequant16<CLS>(v, (gbyte*)w + r * rowb, 16 * pi, grid);
   const int64_t o = r * kdim + 16 * pi;
   if (out_f16) {
 #pragma unroll
@@ -397,7 +686,7 @@ extern "C" int tlx_moe_up3s_pairs(const uint64_t* ptbl, const uint16_t* eids, co
   TLX_RET_IF(!tlx_aligned(ptbl, 8) || !tlx_aligned(xs, 16) || !tlx_aligned(gridf, 16) || !tlx_aligned(ys, 4), TLX_E_ALIGN);
   GxArgs a{};
   a.ptbl = ptbl; a.eids = eids; a.x = xs; a.grid = gridf; a.out = ys;
-  return gx_launch<GX_IQ3S, true, GX_PAIRS>(a, np, (hipStream_t)stream);
+  return gv_launch<GX_IQ3S, true, GX_PAIRS, 4, 4>(a, np, (hipStream_t)stream);
 }
 
 extern "C" int tlx_moe_dn6(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
@@ -419,7 +708,7 @@ extern "C" int tlx_moe_dn6_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, 
   TLX_RET_IF(!tlx_aligned(ptbl_dn, 8) || !tlx_aligned(act, 16) || !tlx_aligned(parts, 2), TLX_E_ALIGN);
   GxArgs a{};
   a.ptbl = ptbl_dn; a.eids = eids; a.x = act; a.out = parts;
-  return gx_launch<GX_Q6K, false, GX_PAIRS>(a, np, (hipStream_t)stream);
+  return gv_launch<GX_Q6K, false, GX_PAIRS, 1, 4>(a, np, (hipStream_t)stream);
 }
 
 extern "C" int tlx_moe_shared8(const void* wg, const void* wu, const void* wd, const float* x, float* y, float* act,
@@ -429,6 +718,15 @@ extern "C" int tlx_moe_shared8(const void* wg, const void* wu, const void* wd, c
   TLX_RET_IF(!tlx_aligned(wg, 2) || !tlx_aligned(wu, 2) || !tlx_aligned(wd, 2), TLX_E_ALIGN);
   TLX_RET_IF(!tlx_aligned(x, 16) || !tlx_aligned(act, 16) || !tlx_aligned(y, 4), TLX_E_ALIGN);
   hipStream_t st = (hipStream_t)stream;
+  if (P <= kGvTok) {   // decode: the GEMV-shaped form, k split over the waves of a tile
+    GxArgs a{};
+    a.w0 = (const uint8_t*)wg; a.w1 = (const uint8_t*)wu; a.x = x; a.out = act; a.P = P;
+    int r = gv_launch<GX_Q80, true, GX_DENSE, 8, 8>(a, 1, st);
+    TLX_RET_IF(r != TLX_OK, r);
+    GxArgs b{};
+    b.w0 = (const uint8_t*)wd; b.x = act; b.out = y; b.P = P;
+    return gv_launch<GX_Q80, false, GX_DENSE, 2, 8>(b, 1, st);
+  }
   const int items = (P + gx_tok<GX_DENSE>() - 1) / gx_tok<GX_DENSE>();
   GxArgs a{};
   a.w0 = (const uint8_t*)wg; a.w1 = (const uint8_t*)wu; a.x = x; a.out = act; a.P = P;
