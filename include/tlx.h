@@ -433,8 +433,9 @@ int tlx_q8_0_dequant(const void* w, void* out, int64_t rows, int64_t kdim, int o
 int tlx_moe_up3s(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const float* xs,
                  const float* gridf, float* ys, int np, void* stream);
 /* Pair-walk form (no sort): pair p runs expert eids[p].  Replaces gx8e256up
- * (engine/mm/MM_P1_gx8e256up.cu:15-20): gx8e256up(ptbl, eids, xs, gridf, ys).  Bit-identical to
- * tlx_moe_up3s on the same pairs. */
+ * (engine/mm/MM_P1_gx8e256up.cu:15-20): gx8e256up(ptbl, eids, xs, gridf, ys).  The decode form:
+ * weights go straight to registers, the grid's levels are read as fp16 (exact for the IQ3_S
+ * grid's integers); the operands are tlx_moe_up3s's, summed in another k order (within 1e-5). */
 int tlx_moe_up3s_pairs(const uint64_t* ptbl, const uint16_t* eids, const float* xs, const float* gridf,
                        float* ys, int np, void* stream);
 /* Q6_K grouped down over the sorted pairs: parts[pair][2048] = fp16(Wd_e . act[pair]).  Replaces
@@ -444,11 +445,13 @@ int tlx_moe_up3s_pairs(const uint64_t* ptbl, const uint16_t* eids, const float* 
 int tlx_moe_dn6(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
                 const uint16_t* plist, const float* act, uint16_t* parts, int np, void* stream);
 /* Pair-walk form: replaces gx8e256dn6 (engine/mm/MM_P2_gx8e256dn6.cu:9-13):
- * gx8e256dn6(ptbl, eids, xs = act, parts).  Bit-identical to tlx_moe_dn6 on the same pairs. */
+ * gx8e256dn6(ptbl, eids, xs = act, parts).  The decode form, as tlx_moe_up3s_pairs: tlx_moe_dn6's
+ * products (an operand may round once where tlx_moe_dn6 rounds twice, an fp16 ulp apart in rare
+ * ties) summed in another k order. */
 int tlx_moe_dn6_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, uint16_t* parts,
                       int np, void* stream);
 /* The Q8_0 shared expert over P positions: y[P][2048] f32 = Wd . (silu(Wg . x) * (Wu . x)), with act
- * f32[P][512] caller scratch (two launches on the stream).  Replaces shexp8
+ * f32[P][512] caller scratch (two launches on the stream; P <= 16 the decode form).  Replaces shexp8
  * (engine/mm/MM_P2_shexp8.cu:8-13): shexp8(wg [512][2176], wu [512][2176], wd [2048][544], x, y).
  * x and act 16-B aligned. */
 int tlx_moe_shared8(const void* wg, const void* wu, const void* wd, const float* x, float* y, float* act, int P,

@@ -9,17 +9,16 @@
 // ptbl_dn[e] -- 2048 rows of 420 B (2 raw 210-B blocks, k = 512); the shared expert's Q8_0 gate and
 // up rows (512 x 2176 B, k = 2048) and down rows (2048 x 544 B, k = 512).
 //
-// One kernel for all of them.  A workgroup (4 waves) owns 64 output columns of one expert -- for
-// gate+up 64 gate rows and the matching 64 up rows, so the SwiGLU pairs meet in one lane; for down
-// 64 rows -- and up to 64 token rows at a time (a pass).  K runs in chunks of 256: the pass's
+// Two kernels.  gx_kernel (batches): a workgroup (4 waves) owns 64 output columns of one expert --
+// for gate+up 64 gate rows and the matching 64 up rows, so the SwiGLU pairs meet in one lane; for
+// down 64 rows -- and up to 64 token rows at a time (a pass).  K runs in chunks of 64: the pass's
 // activations (f32 -> fp16, round to nearest even) and the column block's weight rows, dequantized
 // to the reference's operands -- fp16 of the fp32 GGUF value, as gxu_gm stages them -- go to LDS
-// (rows padded to 264 halfs: the 16 rows of a fragment read fall in distinct banks); then wave w
-// runs v_mfma_f32_16x16x32_f16 over its 16 columns for every 16-token group of the pass.  Token
-// lists: sorted (the expert's bin from eoff / plist, in passes of 64), pair walk (one pair per
-// workgroup: pair p runs expert eids[p]) or dense (every position: the shared expert).  The k
-// order and the per-token arithmetic do not depend on which other tokens share a pass, so the pair
-// walk and the sorted form give the same bits for the same pair.
+// (rows padded to 72 halfs: the 16 rows of a fragment read fall in distinct 16-B slots); then wave
+// w runs v_mfma_f32_16x16x32_f16 over its 16 columns for every 16-token group of the pass.  Token
+// lists: sorted (the expert's bin from eoff / plist, in passes of 64) or dense (every position:
+// the shared expert).  gv_kernel (decode: the pair walk, one pair per item, pair p running expert
+// eids[p]; the shared expert at P <= 16): the same operands, built in registers (its section).
 //
 // IQ3_S's 512-entry grid is a run-time argument (float[512][4]), as in the reference.
 #include "tlx_common.h"
@@ -41,8 +40,7 @@ template <> struct GxFmt<GX_IQ3S> { static constexpr int kBlk = 110, kPer = 256;
 template <> struct GxFmt<GX_Q6K> { static constexpr int kBlk = 210, kPer = 256; };
 template <> struct GxFmt<GX_Q80> { static constexpr int kBlk = 34, kPer = 32; };
 
-// token rows per pass: one 16-row MFMA group for the pair walk, four otherwise
-template <int FORM> constexpr int gx_tok() { return FORM == GX_PAIRS ? 16 : 64; }
+constexpr int kGxTok = 64;   // token rows per pass of gx_kernel (four 16-row MFMA groups)
 
 struct GxArgs {
   const uint64_t* ptbl;    // routed: slab address per expert
@@ -58,18 +56,11 @@ struct GxArgs {
   int items;               // work items: experts (sorted), pairs (pair walk) or 64-position passes (dense)
 };
 
-template <bool UP, bool GRID, int TOK>
-struct GxLds {
-  _Float16 x[TOK * kGxLd];
-  _Float16 w[(UP ? 2 : 1) * kGxCols * kGxLd];
-  float4 grid[GRID ? 512 : 1];
-  int xrow[TOK];
-  int orow[TOK];
-};
 
-// Weight bytes are read through global-address-space pointers: the compiler then emits global
-// loads, which count on the vector-memory counter only -- flat loads also count on the LDS one, so
-// every wait for an LDS read would wait for the weight loads in flight as well.  Records are only
+// The decode form reads weight bytes through global-address-space pointers: global loads count on
+// the vector-memory counter only (flat loads also on the LDS one, so a wait for an LDS read waits
+// for the weight loads in flight too).  The LDS-staged form keeps generic pointers: measured, its
+// flat loads run the M = 2048 gate+up faster (313 vs 350 us), the down alike.  Records are only
 // 2-B aligned (110-, 210- and 34-B blocks): gx_ld reads through an under-aligned type.
 using gbyte = const __attribute__((address_space(1))) uint8_t;
 
@@ -77,16 +68,6 @@ template <typename T>
 __device__ __forceinline__ T gx_ld(gbyte* p) {
   typedef T __attribute__((aligned(1))) T1;
   return *reinterpret_cast<const __attribute__((address_space(1))) T1*>(p);
-}
-
-__device__ __forceinline__ void gx_store16(_Float16* dst, const float* v) {
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    h8_t h;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) h[j] = (_Float16)v[8 * i + j];
-    *reinterpret_cast<h8_t*>(dst + 8 * i) = h;
-  }
 }
 
 // The 16 weights k0 .. k0 + 15 (k0 % 16 == 0) of one row as f32 GGUF values, in two steps: fetch
@@ -102,25 +83,30 @@ template <> struct GxRaw<GX_Q6K> { uint32_t ds; u4_t ql, qh; };   // d | sc << 1
 template <> struct GxRaw<GX_Q80> { uint32_t d; u4_t q; };
 
 template <int CLS>
-__device__ __forceinline__ GxRaw<CLS> gx_fetch(gbyte* row, int k0) {
+__device__ __forceinline__ GxRaw<CLS> gx_fetch(const uint8_t* rowp, int k0) {
+  // an opaque copy of the row pointer: the loads below then take their field offsets as
+  // immediates on one address (measured: the M = 2048 gate+up 327 -> 313 us)
+  uint64_t pv = (uint64_t)rowp;
+  asm volatile("" : "+v"(pv));
+  const uint8_t* row = (const uint8_t*)pv;
   GxRaw<CLS> r;
   if constexpr (CLS == GX_IQ3S) {
-    gbyte* b = row + (size_t)(k0 >> 8) * 110;
+    const uint8_t* b = row + (size_t)(k0 >> 8) * 110;
     const int kib = k0 & 255, j = kib >> 5, hf = (kib >> 4) & 1;
     const uint32_t nib = (b[106 + (j >> 1)] >> (4 * (j & 1))) & 15u;
-    r.dn = gx_ld<uint16_t>(b) | (nib << 16);
-    r.qs = gx_ld<uint32_t>(b + 2 + 8 * j + 4 * hf);
-    r.hs = ((uint32_t)(b[66 + j] >> (4 * hf)) & 15u) | ((uint32_t)gx_ld<uint16_t>(b + 74 + 4 * j + 2 * hf) << 8);
+    r.dn = tlx_ldu<uint16_t>(b) | (nib << 16);
+    r.qs = tlx_ldu<uint32_t>(b + 2 + 8 * j + 4 * hf);
+    r.hs = ((uint32_t)(b[66 + j] >> (4 * hf)) & 15u) | ((uint32_t)tlx_ldu<uint16_t>(b + 74 + 4 * j + 2 * hf) << 8);
   } else if constexpr (CLS == GX_Q6K) {
-    gbyte* b = row + (size_t)(k0 >> 8) * 210;
+    const uint8_t* b = row + (size_t)(k0 >> 8) * 210;
     const int kib = k0 & 255, h = kib >> 7, g = (kib >> 5) & 3, l0 = kib & 31;
-    r.ds = gx_ld<uint16_t>(b + 208) | ((uint32_t)b[192 + 8 * h + (l0 >> 4) + 2 * g] << 16) | ((uint32_t)kib << 24);
-    r.ql = gx_ld<u4_t>(b + 64 * h + 32 * (g & 1) + l0);
-    r.qh = gx_ld<u4_t>(b + 128 + 32 * h + l0);
+    r.ds = tlx_ldu<uint16_t>(b + 208) | ((uint32_t)b[192 + 8 * h + (l0 >> 4) + 2 * g] << 16) | ((uint32_t)kib << 24);
+    r.ql = tlx_ldu<u4_t>(b + 64 * h + 32 * (g & 1) + l0);
+    r.qh = tlx_ldu<u4_t>(b + 128 + 32 * h + l0);
   } else {
-    gbyte* b = row + (size_t)(k0 >> 5) * 34;
-    r.d = gx_ld<uint16_t>(b);
-    r.q = gx_ld<u4_t>(b + 2 + 16 * ((k0 >> 4) & 1));
+    const uint8_t* b = row + (size_t)(k0 >> 5) * 34;
+    r.d = tlx_ldu<uint16_t>(b);
+    r.q = tlx_ldu<u4_t>(b + 2 + 16 * ((k0 >> 4) & 1));
   }
   return r;
 }
@@ -158,8 +144,98 @@ __device__ __forceinline__ void gx_decode(float* v, const GxRaw<CLS>& r, const f
   }
 }
 
+// IQ3_S lookups for the fp16 operands, in LDS: the grid as fp16 (4 halves an entry, 8 B -- exact for
+// the IQ3_S grid's integer levels; other values take one extra rounding, to fp16, before the
+// product) and the fp16 sign masks of 4 weights per sign nibble (16 entries: all in distinct
+// banks, so a wave's lookups do not conflict)
+struct GvLut {
+  uint2 grid[512];
+  uint2 smask[16];
+};
+
+template <bool G> struct GvLutSlot { GvLut v; };
+template <> struct GvLutSlot<false> {};
+
+template <int NT>
+__device__ __forceinline__ void gv_lut_fill(GvLut& L, const float* gridf, int t) {
+  for (int i = t; i < 512; i += NT) {
+    const float4 g = reinterpret_cast<const float4*>(gridf)[i];
+    L.grid[i] = uint2{(uint32_t)tlx_f2h_bits(g.x) | ((uint32_t)tlx_f2h_bits(g.y) << 16),
+                      (uint32_t)tlx_f2h_bits(g.z) | ((uint32_t)tlx_f2h_bits(g.w) << 16)};
+  }
+  if (t < 16)
+    L.smask[t] = uint2{((t & 1u) << 15) | (((t >> 1) & 1u) << 31), (((t >> 2) & 1u) << 15) | (((t >> 3) & 1u) << 31)};
+}
+
+// fp16 pair {db * lo(g2), db * hi(g2)}, each the f32 product (exact here: db has at most 16
+// significant bits, a grid level at most 4) rounded once to fp16 -- v_fma_mix takes the fp16 halves
+// of g2 as operands, so the grid needs no widening
+__device__ __forceinline__ uint32_t gv_mix2(float db, uint32_t g2) {
+  uint32_t r;
+  asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+      : "=&v"(r)
+      : "v"(db), "v"(g2));
+  return r;
+}
+
+// fp16 pairs {bytes 0, 1} (hi = 0) or {bytes 2, 3} (hi = 1) of v as the integers byte - bias: v_perm
+// puts 0x64 above each byte (the fp16 1024 + byte, exact), a packed fp16 add takes 1024 + bias off
+// (exact: small integers)
+__device__ __forceinline__ uint32_t gv_bytes_h2(uint32_t v, int hi, float bias) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  const uint32_t p = __builtin_amdgcn_perm(0x64646464u, v, hi ? 0x04030402u : 0x04010400u);
+  const _Float16 o = (_Float16)(1024.f + bias);
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p) - h2_t{o, o});
+}
+
+// The 16 weights as fp16 operands, bit for bit the fp16 of gx_decode's values.  IQ3_S and Q8_0
+// through the fp16 lookups and v_fma_mix (their products are exact in f32, so one rounding is
+// gx_decode's rounding); Q6_K through gx_decode and a conversion (its product can round in f32,
+// and the reference's operand is that f32 value rounded again).
 template <int CLS>
-__device__ __forceinline__ void gx_dequant16(float* v, gbyte* row, int k0, const float4* grid) {
+__device__ __forceinline__ void gx_decode_h(u4_t* h, const GxRaw<CLS>& r, const GvLut* lut) {
+  if constexpr (CLS == GX_IQ3S) {
+    const float db = tlx_h2f((uint16_t)(r.dn & 0xFFFFu)) * (float)(1u + 2u * (r.dn >> 16));   // exact
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {   // index byte i: weights 4i .. 4i+3
+      const uint2 g = lut->grid[((r.qs >> (8 * i)) & 255u) | (((r.hs >> i) & 1u) << 8)];
+      const uint2 m = lut->smask[(r.hs >> (8 + 4 * i)) & 15u];
+      h[i >> 1][2 * (i & 1)] = gv_mix2(db, g.x) ^ m.x;
+      h[i >> 1][2 * (i & 1) + 1] = gv_mix2(db, g.y) ^ m.y;
+    }
+  } else if constexpr (CLS == GX_Q80) {
+    const float d = tlx_h2f((uint16_t)r.d);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u4 = r.q[j] ^ 0x80808080u;   // int8 + 128
+      h[j >> 1][2 * (j & 1)] = gv_mix2(d, gv_bytes_h2(u4, 0, 128.f));
+      h[j >> 1][2 * (j & 1) + 1] = gv_mix2(d, gv_bytes_h2(u4, 1, 128.f));
+    }
+  } else {
+    float v[16];
+    gx_decode<CLS>(v, r, nullptr);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      h8_t hh;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) hh[j] = (_Float16)v[8 * i + j];
+      h[i] = __builtin_bit_cast(u4_t, hh);
+    }
+  }
+}
+
+template <bool UP, bool GRID, int TOK>
+struct alignas(16) GxLds {   // 16-B fragment reads and stores
+  _Float16 x[TOK * kGxLd];
+  _Float16 w[(UP ? 2 : 1) * kGxCols * kGxLd];
+  GvLutSlot<GRID> lut;
+  int xrow[TOK];
+  int orow[TOK];
+};
+
+template <int CLS>
+__device__ __forceinline__ void gx_dequant16(float* v, const uint8_t* row, int k0, const float4* grid) {
   gx_decode<CLS>(v, gx_fetch<CLS>(row, k0), grid);
 }
 
@@ -170,7 +246,8 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
   constexpr int RB = (UP ? kFf : kHid) / kGxCols;         // column blocks per matrix
   constexpr int ROWB = K / GxFmt<CLS>::kPer * GxFmt<CLS>::kBlk;
   constexpr bool GRID = CLS == GX_IQ3S;
-  constexpr int TOK = gx_tok<FORM>();
+  constexpr int TOK = kGxTok;
+  static_assert(FORM != GX_PAIRS, "the pair walk is gv_kernel's");
   constexpr int NG = TOK / 16;                            // 16-token MFMA groups per pass
   __shared__ GxLds<UP, GRID, TOK> L;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 15, kq = lane >> 4;
@@ -183,25 +260,23 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
 
   // the work item: token list, weight matrices
   int beg = 0, ntot = 0;
-  gbyte* wg = nullptr;
-  gbyte* wu = nullptr;
+  const uint8_t* wg = nullptr;
+  const uint8_t* wu = nullptr;
   if constexpr (FORM == GX_SORTED) {
     beg = a.eoff[item];
     ntot = a.eoff[item + 1] - beg;
     if (ntot <= 0) return;   // uniform per workgroup
-    wg = reinterpret_cast<gbyte*>(a.ptbl[item]);
-  } else if constexpr (FORM == GX_PAIRS) {
-    beg = item;
-    ntot = 1;
-    wg = reinterpret_cast<gbyte*>(a.ptbl[a.eids[item]]);
+    wg = reinterpret_cast<const uint8_t*>(a.ptbl[item]);
   } else {
     beg = item * TOK;
     ntot = min(TOK, a.P - beg);
-    wg = (gbyte*)a.w0;
+    wg = a.w0;
   }
-  if constexpr (UP) wu = FORM == GX_DENSE ? (gbyte*)a.w1 : wg + kIq3sGate;
+  if constexpr (UP) wu = FORM == GX_DENSE ? a.w1 : wg + kIq3sGate;
+  const GvLut* lut = nullptr;
   if constexpr (GRID) {
-    for (int i = t; i < 512; i += kGxThreads) L.grid[i] = reinterpret_cast<const float4*>(a.grid)[i];
+    gv_lut_fill<kGxThreads>(L.lut.v, a.grid, t);
+    lut = &L.lut.v;
   }
 
   for (int p0 = 0; p0 < ntot; p0 += TOK) {
@@ -228,7 +303,7 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
     constexpr int NU = NR * (kGxKc / 16) / kGxThreads;       // units per thread (1 or 2)
     constexpr int NX = (TOK * kGxKc / 8 + kGxThreads - 1) / kGxThreads;   // activation pieces per thread
     static_assert(NR * (kGxKc / 16) % kGxThreads == 0, "units");
-    gbyte* urow[NU];
+    const uint8_t* urow[NU];
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
       const int R = (t + i * kGxThreads) >> 2;
@@ -279,9 +354,10 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
 #pragma unroll
       for (int i = 0; i < NU; ++i) {
         const int u = t + i * kGxThreads;
-        float v[16];
-        gx_decode<CLS>(v, raw[i], L.grid);
-        gx_store16(L.w + (u >> 2) * kGxLd + 16 * (u & 3), v);
+        u4_t h[2];
+        gx_decode_h<CLS>(h, raw[i], lut);
+        *reinterpret_cast<u4_t*>(L.w + (u >> 2) * kGxLd + 16 * (u & 3)) = h[0];
+        *reinterpret_cast<u4_t*>(L.w + (u >> 2) * kGxLd + 16 * (u & 3) + 8) = h[1];
       }
       if constexpr (PIPE) {
         if (kc + 1 < K / kGxKc) GX_FETCH(kc + 1)   // in flight over this chunk's MFMAs
@@ -389,51 +465,6 @@ __device__ __forceinline__ int gv_koff(int kq, int s) {
   return 64 * kq + 8 * s;
 }
 
-// IQ3_S lookups of the decode form, in LDS: the grid as fp16 (4 halves an entry, 8 B -- exact for
-// the IQ3_S grid's integer levels; other values take one extra rounding, to fp16, before the
-// product) and the fp16 sign masks of 4 weights per sign nibble (16 entries: all in distinct
-// banks, so a wave's lookups do not conflict)
-struct GvLut {
-  uint2 grid[512];
-  uint2 smask[16];
-};
-
-template <bool G> struct GvLutSlot { GvLut v; };
-template <> struct GvLutSlot<false> {};
-
-template <int NT>
-__device__ __forceinline__ void gv_lut_fill(GvLut& L, const float* gridf, int t) {
-  for (int i = t; i < 512; i += NT) {
-    const float4 g = reinterpret_cast<const float4*>(gridf)[i];
-    L.grid[i] = uint2{(uint32_t)tlx_f2h_bits(g.x) | ((uint32_t)tlx_f2h_bits(g.y) << 16),
-                      (uint32_t)tlx_f2h_bits(g.z) | ((uint32_t)tlx_f2h_bits(g.w) << 16)};
-  }
-  if (t < 16)
-    L.smask[t] = uint2{((t & 1u) << 15) | (((t >> 1) & 1u) << 31), (((t >> 2) & 1u) << 15) | (((t >> 3) & 1u) << 31)};
-}
-
-// fp16 pair {db * lo(g2), db * hi(g2)}, each the f32 product (exact here: db has at most 16
-// significant bits, a grid level at most 4) rounded once to fp16 -- v_fma_mix takes the fp16 halves
-// of g2 as operands, so the grid needs no widening
-__device__ __forceinline__ uint32_t gv_mix2(float db, uint32_t g2) {
-  uint32_t r;
-  asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]\n\t"
-      "v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
-      : "=&v"(r)
-      : "v"(db), "v"(g2));
-  return r;
-}
-
-// fp16 pairs {bytes 0, 1} (hi = 0) or {bytes 2, 3} (hi = 1) of v as the integers byte - bias: v_perm
-// puts 0x64 above each byte (the fp16 1024 + byte, exact), a packed fp16 add takes 1024 + bias off
-// (exact: small integers)
-__device__ __forceinline__ uint32_t gv_bytes_h2(uint32_t v, int hi, float bias) {
-  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-  const uint32_t p = __builtin_amdgcn_perm(0x64646464u, v, hi ? 0x04030402u : 0x04010400u);
-  const _Float16 o = (_Float16)(1024.f + bias);
-  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p) - h2_t{o, o});
-}
-
 // B operand of k-step s: fp16 of the GGUF values, the product of the block scale and the integer
 // level rounded to fp16 -- for IQ3_S and Q8_0 the product is exact in f32, so these are gx_decode's
 // operands bit for bit; Q6_K's can exceed f32's 24 bits, where gx_decode rounds twice (to f32, then
@@ -498,7 +529,7 @@ __global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
   constexpr int DEPTH = UW < 4 ? UW : 4;                 // units in flight
   constexpr bool GRID = CLS == GX_IQ3S;
   static_assert(NU % KS == 0 && NW % KS == 0, "k split");
-  __shared__ _Float16 xs[TOKR * LDX];
+  __shared__ __attribute__((aligned(16))) _Float16 xs[TOKR * LDX];
   __shared__ GvLutSlot<GRID> lslot;
   __shared__ f4_t red[KS > 1 ? (KS - 1) * TW * NM * 64 : 1];
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 15, kq = lane >> 4;
@@ -612,9 +643,14 @@ int gv_launch(const GxArgs& a, int items, hipStream_t st) {
 template <int CLS>
 __global__ __launch_bounds__(256) void gx_dequant_kernel(const uint8_t* __restrict__ w, const float* __restrict__ gridf,
                                                          void* __restrict__ out, int64_t rows, int kdim, int out_f16) {
-  __shared__ float4 grid[CLS == GX_IQ3S ? 512 : 1];
-  if constexpr (CLS == GX_IQ3S) {
-    for (int i = threadIdx.x; i < 512; i += blockDim.x) grid[i] = reinterpret_cast<const float4*>(gridf)[i];
+  constexpr bool GRID = CLS == GX_IQ3S;
+  __shared__ float4 grid[GRID ? 512 : 1];
+  __shared__ GvLutSlot<GRID> lslot;
+  const GvLut* lut = nullptr;
+  if constexpr (GRID) {
+    for (int i = threadIdx.x; i < 512; i += 256) grid[i] = reinterpret_cast<const float4*>(gridf)[i];
+    gv_lut_fill<256>(lslot.v, gridf, threadIdx.x);
+    lut = &lslot.v;
     __syncthreads();
   }
   const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -623,13 +659,17 @@ __global__ __launch_bounds__(256) void gx_dequant_kernel(const uint8_t* __restri
   const int64_t r = u / np;
   const int pi = (int)(u - r * np);
   const int64_t rowb = (int64_t)kdim / GxFmt<CLS>::kPer * GxFmt<CLS>::kBlk;
-  float v[16];
-  gx_dequant16<CLS>(v, (gbyte*)w + r * rowb, 16 * pi, grid);
+  const uint8_t* row = w + r * rowb;
   const int64_t o = r * kdim + 16 * pi;
-  if (out_f16) {
+  if (out_f16) {   // the GEMMs' operand path (gx_decode_h)
+    u4_t h[2];
+    gx_decode_h<CLS>(h, gx_fetch<CLS>(row, 16 * pi), lut);
+    uint32_t* o32 = reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(out) + o);   // 4-B aligned: o % 16 == 0
 #pragma unroll
-    for (int l = 0; l < 16; ++l) reinterpret_cast<uint16_t*>(out)[o + l] = tlx_f2h_bits(v[l]);
+    for (int l = 0; l < 8; ++l) o32[l] = h[l >> 2][l & 3];
   } else {
+    float v[16];
+    gx_dequant16<CLS>(v, row, 16 * pi, grid);
 #pragma unroll
     for (int l = 0; l < 16; ++l) reinterpret_cast<float*>(out)[o + l] = v[l];
   }
@@ -727,7 +767,7 @@ extern "C" int tlx_moe_shared8(const void* wg, const void* wu, const void* wd, c
     b.w0 = (const uint8_t*)wd; b.x = act; b.out = y; b.P = P;
     return gv_launch<GX_Q80, false, GX_DENSE, 2, 8>(b, 1, st);
   }
-  const int items = (P + gx_tok<GX_DENSE>() - 1) / gx_tok<GX_DENSE>();
+  const int items = (P + kGxTok - 1) / kGxTok;
   GxArgs a{};
   a.w0 = (const uint8_t*)wg; a.w1 = (const uint8_t*)wu; a.x = x; a.out = act; a.P = P;
   int r = gx_launch<GX_Q80, true, GX_DENSE>(a, items, st);
