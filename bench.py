@@ -57,8 +57,8 @@ matrix -> packed rows -> packed7) in GB/s of bytes read + written.
 
 ``moe`` is config 5: the whole MoE layer at M=11 and M=2048 as ``ops.moe_layer`` runs it by
 default -- M=11: top-8 from N(0,1) logits, the pair-walk IQ4_XS gate+up and down (no sort)
-with the shared expert's chunks in the same two launches, combine, all on one stream; M=2048: top-8, sort, grouped gate+up and down, the
-shared expert on a second stream, combine -- seeded expert weights, the layer's launches per
+with the shared expert's chunks in the same two launches, combine, all on one stream; M=2048: top-8, sort, grouped gate+up and down with
+the shared expert's workgroups in the same two launches, combine -- seeded expert weights, the layer's launches per
 step captured in one HIP graph (``ms_other_shared_stream``: the shared expert on the other
 choice of stream; ``ms_sorted_grouped`` at M=11: the grouped route); each step reads a
 different copy of the 257 expert slabs (3 copies, 1.3 GB), so at M=11 the weights come from
@@ -426,8 +426,8 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
             ops.moe_layer(logits, sg, x, hres, y, c["ptbl"], c["ptbl_dn"], c["ptbl_sh"], iq4nl, sc, stream=st,
                           overlap_shared=overlap, layout=layout, pair_walk=pair_walk)
 
-        walk = P <= ops.MOE_PAIR_WALK_MAX_P   # the layer's defaults: pair walk, shared expert on one stream
-        t_other = time_graph(lambda st: layer(st, walk), steps, warmup, torch)
+        walk = P <= ops.MOE_PAIR_WALK_MAX_P   # the layer's defaults: the shared expert in the routed launches
+        t_other = time_graph(lambda st: layer(st, True), steps, warmup, torch)
         t_raw = time_graph(lambda st: layer(st, None, LAYOUT_RAW), steps, warmup, torch)
         t_grouped = time_graph(lambda st: layer(st, False, pair_walk=False), steps, warmup, torch) if walk else None
         t = time_graph(lambda st: layer(st), steps, warmup, torch)
@@ -437,7 +437,7 @@ def moe_leg(ops, formats, synth, torch, dev, steps, warmup):
         tflops = flops / (t * 1e-3) / 1e12
         gbs = wbytes / (t * 1e-3) / 1e9
         route = ("top-8, pair walk (no sort) with the shared expert in its two launches" if walk else
-                 "top-8, sort, grouped expert GEMMs, shared expert on a second stream")
+                 "top-8, sort, grouped expert GEMMs with the shared expert in their two launches")
         out[f"M{P}"] = {"ms": round(t, 4), "tflops": round(tflops, 2), "route": route,
                         "experts_hit": hit, "weight_gbs": round(gbs, 1),
                         "ms_other_shared_stream": round(t_other, 4), "ms_gguf_row_slabs": round(t_raw, 4),

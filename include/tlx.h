@@ -399,6 +399,20 @@ int tlx_moe_dn4_pairs_sh(const uint64_t* ptbl_dn, const uint16_t* eids, const fl
                          uint16_t* parts, const uint64_t* ptbl_sh_dn, const float* sact, float* shared, int P,
                          int layout, void* stream);
 
+/* The grouped forms (tlx_moe_up4 / tlx_moe_dn4 over the sorted pairs) and the shared expert's
+ * gate+up / down over the P positions in one launch each, where both sides run their MFMA forms
+ * (np > 512 / 160 and P > 256; else the two launches): the shared expert's workgroups follow the
+ * routed ones and fill the routed grid's last, partial round.  No counterpart in the reference
+ * (its shared expert is separate launches, engine/mm/MM_P7_lib.py:449-511 sequences them); the
+ * outputs are those of the separate calls bit for bit.  sact (f32 [P][512]) and shared (f32
+ * [P][2048]) as tlx_moe_shared's act / out; ptbl_sh / ptbl_sh_dn one slab pointer each. */
+int tlx_moe_up4_sh(const uint64_t* ptbl, const uint32_t* items, const uint32_t* nitp, const int* eoff,
+                   const uint16_t* plist, const float* xs, const float* iq4nl, float* ys, int np,
+                   const uint64_t* ptbl_sh, float* sact, int P, int layout, void* stream);
+int tlx_moe_dn4_sh(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
+                   const uint16_t* plist, const float* act, const float* iq4nl, uint16_t* parts, int np,
+                   const uint64_t* ptbl_sh_dn, const float* sact, float* shared, int P, int layout, void* stream);
+
 /* Shared expert over all P positions: act[P][512] (caller scratch) then out[P][2048] f32.
  * ptbl_sh = {gate/up slab, down slab}.  Replaces shgu32 / shdn32 (engine/mm/MM_P2_ports.py:195-201
  * restates them) with the IQ4_XS weights of the benchmark's MoE configuration. */

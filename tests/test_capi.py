@@ -147,3 +147,18 @@ def test_moe_checkpoint_classes_argument_validation():
     assert L.tlx_moe_shared8(p, p, p, p, p, p + 4, 4, None) == _lib.TLX_E_ALIGN  # act 16-B aligned
     assert L.tlx_iq3s_dequant(p, p, p, 1, 384, 0, None) == _lib.TLX_E_ARG        # kdim % 256
     assert L.tlx_q8_0_dequant(p + 1, p, 1, 256, 0, None) == _lib.TLX_E_ALIGN
+
+
+def test_moe_grouped_shared_fused_argument_validation():
+    """The grouped forms with the shared expert in the same launch reject bad sizes, layouts and
+    alignment before any launch."""
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(64)
+    p = (ctypes.addressof(buf) + 15) & ~15
+    R = _lib.LAYOUT_RAW
+    assert L.tlx_moe_up4_sh(p, p, p, p, p, p, p, p, 0, p, p, 4, R, None) == _lib.TLX_E_ARG       # no pairs
+    assert L.tlx_moe_up4_sh(p, p, p, p, p, p, p, p, 32, p, p, 0, R, None) == _lib.TLX_E_ARG      # no positions
+    assert L.tlx_moe_up4_sh(p, p, p, p, p, p, p, p, 32, p, p, 4, 7, None) == _lib.TLX_E_ARG      # layout
+    assert L.tlx_moe_up4_sh(p, p, p, p, p, p, p, p, 32, p, p + 4, 4, R, None) == _lib.TLX_E_ALIGN   # sact
+    assert L.tlx_moe_dn4_sh(p, p, p, p, p, p, p, p, 16385, p, p, p, 4, R, None) == _lib.TLX_E_ARG
+    assert L.tlx_moe_dn4_sh(p, p, p, p, p, p, p, p, 32, p, p, p + 4, 4, R, None) == _lib.TLX_E_ALIGN  # shared

@@ -190,6 +190,58 @@ def _check_layer(ex, x, logits, sg, hres, out, pairs, positions):
     assert np.all(np.abs(out["y"][positions] - yref) <= 4e-6 * scale + 1e-30)
 
 
+@pytest.mark.parametrize("P", [100, 300, 2048])
+def test_moe_grouped_shared_fused(gpu, experts, experts_tiled, P):
+    """moe_up4_sh / moe_dn4_sh -- the grouped forms and the shared expert in one launch each where
+    both sides run their MFMA forms (P = 300, 2048), two launches otherwise (P = 100: the shared
+    expert's GEMV form) -- against moe_up4 / moe_dn4 / moe_shared, bit for bit, GGUF rows and
+    tiled slabs; and the oracle on sampled pairs and positions."""
+    print(f"[case] grouped forms + shared expert in one launch, P={P}", flush=True)
+    rng = np.random.default_rng(80 + P)
+    x, logits, sg, hres = _inputs(rng, P)
+    np_ = 8 * P
+    dx = torch.from_numpy(x).to(gpu)
+    eids = torch.empty(P, 8, dtype=torch.int16, device=gpu)
+    gates = torch.empty(P, 8, dtype=torch.float32, device=gpu)
+    ops.moe_topk(torch.from_numpy(logits).to(gpu), eids, gates)
+    eoff = torch.empty(257, dtype=torch.int32, device=gpu)
+    plist = torch.empty(np_, dtype=torch.int16, device=gpu)
+    items = torch.empty(ops.moe_max_items(np_), dtype=torch.int32, device=gpu)
+    nitp = torch.empty(1, dtype=torch.int32, device=gpu)
+    ops.moe_sort(eids, eoff, plist, items, nitp)
+    for ex, lay in ((experts, LAYOUT_RAW), (experts_tiled, LAYOUT_TILED)):
+        bufs = {k: torch.full(shape, -3.0, dtype=dt, device=gpu) for k, (shape, dt) in dict(
+            act=((np_, moe.FF), torch.float32), parts=((np_, moe.HID), torch.float16),
+            sact=((P, moe.FF), torch.float32), shared=((P, moe.HID), torch.float32)).items()}
+        fused = {k: torch.full_like(v, -5.0) for k, v in bufs.items()}
+        ops.moe_up4(ex["ptbl"], items, nitp, eoff, plist, dx, ex["iq4nl"], bufs["act"], layout=lay)
+        ops.moe_dn4(ex["ptbl_dn"], items, nitp, eoff, plist, bufs["act"], ex["iq4nl"], bufs["parts"], layout=lay)
+        ops.moe_shared(ex["ptbl_sh"], dx, ex["iq4nl"], bufs["sact"], bufs["shared"], layout=lay)
+        ops.moe_up4_sh(ex["ptbl"], items, nitp, eoff, plist, dx, ex["iq4nl"], fused["act"], ex["ptbl_sh"][0:1],
+                       fused["sact"], layout=lay)
+        ops.moe_dn4_sh(ex["ptbl_dn"], items, nitp, eoff, plist, fused["act"], ex["iq4nl"], fused["parts"],
+                       ex["ptbl_sh"][1:2], fused["sact"], fused["shared"], layout=lay)
+        torch.cuda.synchronize()
+        for k in bufs:
+            a, b = bufs[k].cpu().numpy(), fused[k].cpu().numpy()
+            assert np.array_equal(a.view(np.uint16 if a.dtype == np.float16 else np.uint32),
+                                  b.view(np.uint16 if b.dtype == np.float16 else np.uint32)), (lay, k)
+    out = {k: v.cpu().numpy() for k, v in fused.items()}
+    out.update(eids=eids.cpu().numpy(), gates=gates.cpu().numpy())
+    ev, _ = moe.topk_ref(logits)
+    pairs = [int(p) for p in np.random.default_rng(9).choice(np_, 24, replace=False)]
+    by_e = {}
+    for pair in pairs:
+        by_e.setdefault(int(ev[pair // 8, pair % 8]), []).append(pair)
+    for e, prs in by_e.items():
+        act = moe.up_ref(experts["gu"][e], x[[p // 8 for p in prs]])
+        assert _rows_err(out["act"][prs], act) <= TOL, e
+        assert _rows_err(out["parts"][prs].astype(np.float64), moe.down_ref(experts["dn"][e], act)) <= TOL, e
+    pos = sorted(int(p) for p in np.random.default_rng(10).choice(P, 8, replace=False))
+    sh = moe.down_ref(experts["dn"][moe.E], moe.up_ref(experts["gu"][moe.E], x[pos]))
+    assert _rows_err(out["shared"][pos], sh) <= TOL
+
+
 def test_moe_layer_unscaled_overflow(gpu, experts):
     """Config 5's hidden states as the benchmark states them, N(0,1) unscaled (the other tests
     scale them by 0.05): about a fifth of the fp16 parts overflow, as the reference's fp16 parts

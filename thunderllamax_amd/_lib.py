@@ -88,6 +88,8 @@ SIGNATURES = {
     "tlx_moe_shared": [_p, _p, _p, _p, _p, _i, _i, _p],
     "tlx_moe_up4_pairs_sh": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _p],
     "tlx_moe_dn4_pairs_sh": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _p],
+    "tlx_moe_up4_sh": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _p, _i, _i, _p],
+    "tlx_moe_dn4_sh": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _i, _i, _p],
     "tlx_pack_iq4_tiled": [_p, _p, _i, _i, _p],
     "tlx_moe_combine": [_p, _p, _p, _p, _p, _p, _i, _p],
     "tlx_iq3s_dequant": [_p, _p, _p, _i64, _i64, _i, _p],

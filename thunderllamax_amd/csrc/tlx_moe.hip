@@ -540,18 +540,19 @@ __device__ __forceinline__ void moe_pf_tile(MoePfLds& L, const void* base, const
   }
 }
 
+// workgroup id (of this kind's part of the grid, a multiple of 8 from the grid's start)
 template <int KIND, bool TL>
-__global__ __launch_bounds__(kPfThreads, 1) void moe_pf_kernel(
-    const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff, const uint16_t* __restrict__ plist,
-    const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp, const float* __restrict__ xs,
-    const float* __restrict__ iq4nl, void* __restrict__ out, int P) {
+__device__ __forceinline__ void moe_pf_body(MoePfLds& L, const uint64_t* __restrict__ ptbl,
+                                            const int* __restrict__ eoff, const uint16_t* __restrict__ plist,
+                                            const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp,
+                                            const float* __restrict__ xs, const float* __restrict__ iq4nl,
+                                            void* __restrict__ out, int P, int id) {
   constexpr bool kDense = KIND == MOE_DN_DENSE || KIND == MOE_UP_DENSE;
   constexpr bool kUp = KIND == MOE_UP || KIND == MOE_UP_DENSE;
   constexpr int kS = moe_pf_stripes<KIND>();
-  __shared__ MoePfLds L;
   const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
   // XCD x = id % 8 runs the kS stripes of items x, x + 8, ... one item after another
-  const int id = (int)blockIdx.x, l = id >> 3;
+  const int l = id >> 3;
   const int stripe = l % kS, item = (l / kS) * 8 + (id & 7);
 
   int m0, ntok;
@@ -593,6 +594,33 @@ __global__ __launch_bounds__(kPfThreads, 1) void moe_pf_kernel(
   }
 }
 
+template <int KIND, bool TL>
+__global__ __launch_bounds__(kPfThreads, 1) void moe_pf_kernel(
+    const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff, const uint16_t* __restrict__ plist,
+    const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp, const float* __restrict__ xs,
+    const float* __restrict__ iq4nl, void* __restrict__ out, int P) {
+  __shared__ MoePfLds L;
+  moe_pf_body<KIND, TL>(L, ptbl, eoff, plist, items, nitp, xs, iq4nl, out, P, (int)blockIdx.x);
+}
+
+// The grouped gate+up and the shared expert's gate+up in one launch: workgroups below nrb run the
+// routed items, the rest the shared expert's dense chunks (after the routed ones: they fill the
+// last, partial round of routed workgroups).  Each part is its own launch's code, so the outputs
+// are the separate launches' bit for bit.
+template <bool TL>
+__global__ __launch_bounds__(kPfThreads, 1) void moe_pf_sh_kernel(
+    const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff, const uint16_t* __restrict__ plist,
+    const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp, const float* __restrict__ xs,
+    const float* __restrict__ iq4nl, void* __restrict__ out, const uint64_t* __restrict__ ptbl_sh,
+    float* __restrict__ sact, int P, int nrb) {
+  __shared__ MoePfLds L;
+  const int id = (int)blockIdx.x;
+  if (id < nrb)
+    moe_pf_body<MOE_UP, TL>(L, ptbl, eoff, plist, items, nitp, xs, iq4nl, out, 0, id);
+  else
+    moe_pf_body<MOE_UP_DENSE, TL>(L, ptbl_sh, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, sact, P, id - nrb);
+}
+
 // ------------------------------------------------------------------ grouped IQ4_XS down GEMM (prefill)
 // The down projection's K (512) is short enough for an item's activations to stay in LDS: a
 // workgroup stages its item's act rows once (fp16, MFMA k order, 96 KB at 96 tokens) and then
@@ -612,7 +640,7 @@ template <int KIND, int NG, bool TL>
 __device__ __forceinline__ void moe_pd_tile(MoePdLds& L, const void* base, const float* __restrict__ xs,
                                             const float* __restrict__ iq4nl, void* __restrict__ out,
                                             const uint16_t* __restrict__ plist, int m0, int ntok, int wave,
-                                            int lane) {
+                                            int lane, int dstripe) {
   constexpr bool kDense = KIND == MOE_DN_DENSE;
   constexpr int kNb = kFf / 256;                     // blocks per row (2)
   constexpr int kRowBytes = kNb * 136;
@@ -637,8 +665,8 @@ __device__ __forceinline__ void moe_pd_tile(MoePdLds& L, const void* base, const
     }
   };
 
-  // the stripes of this workgroup: all 4 (routed items), or blockIdx.y (dense chunks)
-  const int s0 = kDense ? (int)blockIdx.y : 0, s1 = kDense ? s0 + 1 : 4;
+  // the stripes of this workgroup: all 4 (routed items), or dstripe (dense chunks)
+  const int s0 = kDense ? dstripe : 0, s1 = kDense ? s0 + 1 : 4;
   MoeWs W[RING];
 #pragma unroll
   for (int r = 0; r < RING - 1; ++r) load_w(W[r], 4 * s0 + r);   // first: in flight during the staging and the table
@@ -758,14 +786,13 @@ __device__ __forceinline__ void moe_pd_tile(MoePdLds& L, const void* base, const
 
 // one workgroup per item (routed: all 4 stripes) or per (kDenseTok-position chunk, stripe) (dense)
 template <int KIND, bool TL>
-__global__ __launch_bounds__(kPfThreads, 1) void moe_pd_kernel(
-    const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff, const uint16_t* __restrict__ plist,
-    const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp, const float* __restrict__ xs,
-    const float* __restrict__ iq4nl, void* __restrict__ out, int P, int tok) {
+__device__ __forceinline__ void moe_pd_body(MoePdLds& L, const uint64_t* __restrict__ ptbl,
+                                            const int* __restrict__ eoff, const uint16_t* __restrict__ plist,
+                                            const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp,
+                                            const float* __restrict__ xs, const float* __restrict__ iq4nl,
+                                            void* __restrict__ out, int P, int tok, int item, int dstripe) {
   constexpr bool kDense = KIND == MOE_DN_DENSE;
-  __shared__ MoePdLds L;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int item = (int)blockIdx.x;
   int m0, ntok;
   const void* base;
   if constexpr (kDense) {
@@ -784,12 +811,41 @@ __global__ __launch_bounds__(kPfThreads, 1) void moe_pd_kernel(
     base = (const void*)(ptbl[e]);
   }
   switch ((ntok + 15) >> 4) {   // workgroup-uniform; dense chunks have <= 32 positions
-    case 1: moe_pd_tile<KIND, 1, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane); break;
-    case 2: moe_pd_tile<KIND, 2, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane); break;
-    case 3: if constexpr (!kDense) moe_pd_tile<KIND, 3, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane); break;
-    case 4: if constexpr (!kDense) moe_pd_tile<KIND, 4, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane); break;
-    case 5: if constexpr (!kDense) moe_pd_tile<KIND, 5, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane); break;
-    default: if constexpr (!kDense) moe_pd_tile<KIND, 6, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane); break;
+    case 1: moe_pd_tile<KIND, 1, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane, dstripe); break;
+    case 2: moe_pd_tile<KIND, 2, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane, dstripe); break;
+    case 3: if constexpr (!kDense) moe_pd_tile<KIND, 3, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane, 0); break;
+    case 4: if constexpr (!kDense) moe_pd_tile<KIND, 4, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane, 0); break;
+    case 5: if constexpr (!kDense) moe_pd_tile<KIND, 5, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane, 0); break;
+    default: if constexpr (!kDense) moe_pd_tile<KIND, 6, TL>(L, base, xs, iq4nl, out, plist, m0, ntok, wave, lane, 0); break;
+  }
+}
+
+template <int KIND, bool TL>
+__global__ __launch_bounds__(kPfThreads, 1) void moe_pd_kernel(
+    const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff, const uint16_t* __restrict__ plist,
+    const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp, const float* __restrict__ xs,
+    const float* __restrict__ iq4nl, void* __restrict__ out, int P, int tok) {
+  __shared__ MoePdLds L;
+  moe_pd_body<KIND, TL>(L, ptbl, eoff, plist, items, nitp, xs, iq4nl, out, P, tok, (int)blockIdx.x, (int)blockIdx.y);
+}
+
+// The grouped down and the shared expert's down in one launch: workgroups below nitems run the
+// routed items, the rest the shared expert's (chunk, stripe) pairs, stripe fastest -- each part
+// its own launch's code, so the outputs are the separate launches' bit for bit.
+template <bool TL>
+__global__ __launch_bounds__(kPfThreads, 1) void moe_pd_sh_kernel(
+    const uint64_t* __restrict__ ptbl, const int* __restrict__ eoff, const uint16_t* __restrict__ plist,
+    const uint32_t* __restrict__ items, const uint32_t* __restrict__ nitp, const float* __restrict__ act,
+    const float* __restrict__ iq4nl, void* __restrict__ out, int tok, const uint64_t* __restrict__ ptbl_sh,
+    const float* __restrict__ sact, float* __restrict__ shared, int P, int nitems) {
+  __shared__ MoePdLds L;
+  const int id = (int)blockIdx.x;
+  if (id < nitems) {
+    moe_pd_body<MOE_DN, TL>(L, ptbl, eoff, plist, items, nitp, act, iq4nl, out, 0, tok, id, 0);
+  } else {
+    const int d = id - nitems;
+    moe_pd_body<MOE_DN_DENSE, TL>(L, ptbl_sh, nullptr, nullptr, nullptr, nullptr, sact, iq4nl, shared, P, 0, d >> 2,
+                                  d & 3);
   }
 }
 
@@ -1244,27 +1300,85 @@ extern "C" int tlx_moe_dn4_pairs_sh(const uint64_t* ptbl_dn, const uint16_t* eid
   return tlx_launch_status();
 }
 
+// the shared expert's gate+up (act) and down (out) alone: GEMV forms up to kGvSharedMaxP positions
+int moe_shared_up(bool tl, int P, hipStream_t st, const uint64_t* ptbl_sh, const float* xs, const float* iq4nl,
+                  float* act) {
+  if (P <= kGvSharedMaxP)
+    moe_gv_launch<MOE_UP_DENSE>(tl, moe_gv_grid<MOE_UP_DENSE>((P + kTok - 1) / kTok), st, ptbl_sh, nullptr, nullptr,
+                                nullptr, nullptr, nullptr, xs, iq4nl, act, P);
+  else
+    moe_pf_launch<MOE_UP_DENSE>(tl, (P + kDenseTok - 1) / kDenseTok, st, ptbl_sh, nullptr, nullptr, nullptr, nullptr,
+                                xs, iq4nl, act, P);
+  return tlx_launch_status();
+}
+
+int moe_shared_dn(bool tl, int P, hipStream_t st, const uint64_t* ptbl_sh_dn, const float* act, const float* iq4nl,
+                  float* out) {
+  if (P <= kGvSharedMaxP)
+    moe_gv_launch<MOE_DN_DENSE>(tl, moe_gv_grid<MOE_DN_DENSE>((P + kTok - 1) / kTok), st, ptbl_sh_dn, nullptr,
+                                nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
+  else
+    moe_pd_launch<MOE_DN_DENSE>(tl, (P + kDenseTok - 1) / kDenseTok, st, ptbl_sh_dn, nullptr, nullptr, nullptr,
+                                nullptr, act, iq4nl, out, P);
+  return tlx_launch_status();
+}
+
 extern "C" int tlx_moe_shared(const uint64_t* ptbl_sh, const float* xs, const float* iq4nl, float* act, float* out,
                               int P, int layout, void* stream) {
   TLX_RET_IF(P < 1 || !moe_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(xs, 16) || !tlx_aligned(act, 16) || !tlx_aligned(out, 16), TLX_E_ALIGN);
   const bool tl = layout == TLX_LAYOUT_TILED;
   const hipStream_t st = (hipStream_t)stream;
-  const int chunks = (P + kTok - 1) / kTok;
-  if (P <= kGvSharedMaxP) {
-    moe_gv_launch<MOE_UP_DENSE>(tl, moe_gv_grid<MOE_UP_DENSE>(chunks), st, ptbl_sh, nullptr, nullptr, nullptr, nullptr,
-                                nullptr, xs, iq4nl, act, P);
-    int rc = tlx_launch_status();
-    TLX_RET_IF(rc != TLX_OK, rc);
-    moe_gv_launch<MOE_DN_DENSE>(tl, moe_gv_grid<MOE_DN_DENSE>(chunks), st, ptbl_sh + 1, nullptr, nullptr, nullptr,
-                                nullptr, nullptr, act, iq4nl, out, P);
-    return tlx_launch_status();
-  }
-  const int dchunks = (P + kDenseTok - 1) / kDenseTok;
-  moe_pf_launch<MOE_UP_DENSE>(tl, dchunks, st, ptbl_sh, nullptr, nullptr, nullptr, nullptr, xs, iq4nl, act, P);
-  int rc = tlx_launch_status();
+  const int rc = moe_shared_up(tl, P, st, ptbl_sh, xs, iq4nl, act);
   TLX_RET_IF(rc != TLX_OK, rc);
-  moe_pd_launch<MOE_DN_DENSE>(tl, dchunks, st, ptbl_sh + 1, nullptr, nullptr, nullptr, nullptr, act, iq4nl, out, P);
+  return moe_shared_dn(tl, P, st, ptbl_sh + 1, act, iq4nl, out);
+}
+
+extern "C" int tlx_moe_up4_sh(const uint64_t* ptbl, const uint32_t* items, const uint32_t* nitp, const int* eoff,
+                              const uint16_t* plist, const float* xs, const float* iq4nl, float* ys, int np,
+                              const uint64_t* ptbl_sh, float* sact, int P, int layout, void* stream) {
+  TLX_RET_IF(np < 1 || np > kMaxPairs || P < 1 || !moe_layout_ok(layout), TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(xs, 16) || !tlx_aligned(ys, 16) || !tlx_aligned(sact, 16), TLX_E_ALIGN);
+  const bool tl = layout == TLX_LAYOUT_TILED;
+  const hipStream_t st = (hipStream_t)stream;
+  if (np <= kGvUpMaxPairs || P <= kGvSharedMaxP) {   // a GEMV form on either side: the two launches
+    const int rc = tlx_moe_up4(ptbl, items, nitp, eoff, plist, xs, iq4nl, ys, np, layout, stream);
+    TLX_RET_IF(rc != TLX_OK, rc);
+    return moe_shared_up(tl, P, st, ptbl_sh, xs, iq4nl, sact);
+  }
+  const int nrb = moe_pf_grid<MOE_UP>(moe_max_items(np));
+  const int grid = nrb + moe_pf_grid<MOE_UP_DENSE>((P + kDenseTok - 1) / kDenseTok);
+  if (tl)
+    moe_pf_sh_kernel<true><<<grid, kPfThreads, 0, st>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, ptbl_sh, sact,
+                                                       P, nrb);
+  else
+    moe_pf_sh_kernel<false><<<grid, kPfThreads, 0, st>>>(ptbl, eoff, plist, items, nitp, xs, iq4nl, ys, ptbl_sh, sact,
+                                                        P, nrb);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_moe_dn4_sh(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
+                              const uint16_t* plist, const float* act, const float* iq4nl, uint16_t* parts, int np,
+                              const uint64_t* ptbl_sh_dn, const float* sact, float* shared, int P, int layout,
+                              void* stream) {
+  TLX_RET_IF(np < 1 || np > kMaxPairs || P < 1 || !moe_layout_ok(layout), TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(act, 16) || !tlx_aligned(parts, 16) || !tlx_aligned(sact, 16) || !tlx_aligned(shared, 16),
+             TLX_E_ALIGN);
+  const bool tl = layout == TLX_LAYOUT_TILED;
+  const hipStream_t st = (hipStream_t)stream;
+  if (np <= kGvDnMaxPairs || P <= kGvSharedMaxP) {
+    const int rc = tlx_moe_dn4(ptbl_dn, items, nitp, eoff, plist, act, iq4nl, parts, np, layout, stream);
+    TLX_RET_IF(rc != TLX_OK, rc);
+    return moe_shared_dn(tl, P, st, ptbl_sh_dn, sact, iq4nl, shared);
+  }
+  const int nitems = moe_max_items(np);
+  const int grid = nitems + 4 * ((P + kDenseTok - 1) / kDenseTok);
+  if (tl)
+    moe_pd_sh_kernel<true><<<grid, kPfThreads, 0, st>>>(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts,
+                                                       moe_item_tok(np), ptbl_sh_dn, sact, shared, P, nitems);
+  else
+    moe_pd_sh_kernel<false><<<grid, kPfThreads, 0, st>>>(ptbl_dn, eoff, plist, items, nitp, act, iq4nl, parts,
+                                                        moe_item_tok(np), ptbl_sh_dn, sact, shared, P, nitems);
   return tlx_launch_status();
 }
 

@@ -735,6 +735,49 @@ def moe_dn4_pairs_sh(ptbl_dn, eids, act, iq4nl, parts, ptbl_sh_dn, sact, shared,
          parts.data_ptr(), ptbl_sh_dn.data_ptr(), sact.data_ptr(), shared.data_ptr(), P, layout, _stream(stream))
 
 
+def moe_up4_sh(ptbl, items, nitp, eoff, plist, xs, iq4nl, ys, ptbl_sh, sact, stream=None, layout=LAYOUT_RAW):
+    """moe_up4 over the sorted pairs and the shared expert's gate+up (ptbl_sh[0] into sact
+    [P][512], P = xs.shape[0]) in one launch where both run the MFMA forms (else the two
+    launches); outputs those of moe_up4 and moe_shared's gate+up bit for bit."""
+    n = ys.shape[0]
+    P = xs.shape[0]
+    _need(ptbl, 256 * 8, "ptbl")
+    _need(ptbl_sh, 8, "ptbl_sh")
+    _need(eoff, 257 * 4, "eoff")
+    _need(plist, n * 2, "plist")
+    _need(items, moe_max_items(n) * 4, "items")
+    _need(xs, max(P, n // 8) * 2048 * 4, "xs")
+    _need(ys, n * 512 * 4, "ys")
+    _need(sact, P * 512 * 4, "sact")
+    _need(iq4nl, 64, "iq4nl")
+    _dev(ptbl, ptbl_sh, eoff, plist, items, nitp, xs, iq4nl, ys, sact)
+    call("tlx_moe_up4_sh", ptbl.data_ptr(), items.data_ptr(), nitp.data_ptr(), eoff.data_ptr(), plist.data_ptr(),
+         xs.data_ptr(), iq4nl.data_ptr(), ys.data_ptr(), n, ptbl_sh.data_ptr(), sact.data_ptr(), P, layout,
+         _stream(stream))
+
+
+def moe_dn4_sh(ptbl_dn, items, nitp, eoff, plist, act, iq4nl, parts, ptbl_sh_dn, sact, shared, stream=None,
+               layout=LAYOUT_RAW):
+    """moe_dn4 over the sorted pairs and the shared expert's down projection (ptbl_sh_dn[0],
+    sact [P][512] into shared [P][2048] f32, P = sact.shape[0]) in one launch where both run the
+    MFMA forms (else the two launches); outputs those of the separate calls bit for bit."""
+    n = act.shape[0]
+    P = sact.shape[0]
+    _need(ptbl_dn, 256 * 8, "ptbl_dn")
+    _need(ptbl_sh_dn, 8, "ptbl_sh_dn")
+    _need(eoff, 257 * 4, "eoff")
+    _need(plist, n * 2, "plist")
+    _need(items, moe_max_items(n) * 4, "items")
+    _need(act, n * 512 * 4, "act")
+    _need(parts, n * 2048 * 2, "parts")
+    _need(shared, P * 2048 * 4, "shared")
+    _need(iq4nl, 64, "iq4nl")
+    _dev(ptbl_dn, ptbl_sh_dn, eoff, plist, items, nitp, act, iq4nl, parts, sact, shared)
+    call("tlx_moe_dn4_sh", ptbl_dn.data_ptr(), items.data_ptr(), nitp.data_ptr(), eoff.data_ptr(), plist.data_ptr(),
+         act.data_ptr(), iq4nl.data_ptr(), parts.data_ptr(), n, ptbl_sh_dn.data_ptr(), sact.data_ptr(),
+         shared.data_ptr(), P, layout, _stream(stream))
+
+
 def moe_shared(ptbl_sh, xs, iq4nl, act, out, stream=None, layout=LAYOUT_RAW):
     """Shared expert over all positions: act [P][512] (scratch), out [P][2048] f32."""
     P = xs.shape[0]
@@ -866,19 +909,19 @@ def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, s
     the reference's prefill sequence, :451-499) or the pair walk (gate+up and down per pair on
     the router's ids, no sort: its decode sequence, :501-507), the shared expert, and the
     combine into y.  Both give the same bits.  pair_walk None picks the pair walk for
-    P <= MOE_PAIR_WALK_MAX_P.  With overlap_shared the shared expert (which needs neither the
-    routing nor the routed experts) runs on a second stream, joined before the combine; the work
-    and the results are the same, and a graph captured from the call keeps the two branches
-    concurrent.  overlap_shared None overlaps on the grouped path only: at pair-walk sizes the
-    shared expert's work is small against what the fork and join of the second stream add to a
-    graph replay, and on one stream it rides in the pair walk's two launches
-    (moe_up4_pairs_sh / moe_dn4_pairs_sh).  layout: the expert slabs' (all of them, shared
-    expert included)."""
+    P <= MOE_PAIR_WALK_MAX_P.  By default the shared expert rides in the routed launches (the pair
+    walk's: moe_up4_pairs_sh / moe_dn4_pairs_sh; the grouped forms': moe_up4_sh / moe_dn4_sh),
+    where it fills the routed grids' last rounds.  With overlap_shared it runs on a second stream
+    instead, joined before the combine (it needs neither the routing nor the routed experts);
+    the results are the same bits.  Measured in graph replays: the second stream is slower on
+    both paths -- a replay runs the captured branch on the same queue, after the routed kernels
+    (P=2048: 253 vs 271 us), and its fork and join cost a decode-size replay 4-10 us.  layout:
+    the expert slabs' (all of them, shared expert included)."""
     sc = scratch
     if pair_walk is None:
         pair_walk = xs.shape[0] <= MOE_PAIR_WALK_MAX_P
     if overlap_shared is None:
-        overlap_shared = not pair_walk
+        overlap_shared = False
     cur = stream if isinstance(stream, torch.cuda.Stream) else torch.cuda.current_stream()
     side = None
     if overlap_shared:
@@ -901,11 +944,16 @@ def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, s
         moe_dn4_pairs(ptbl_dn, eids, sc.act, iq4nl, sc.parts, stream=cur, layout=layout)
     else:
         moe_sort(sc.eids, sc.eoff, sc.plist, sc.items, sc.nitp, stream=cur)
-        moe_up4(ptbl, sc.items, sc.nitp, sc.eoff, sc.plist, xs, iq4nl, sc.act, stream=cur, layout=layout)
-        moe_dn4(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, iq4nl, sc.parts, stream=cur, layout=layout)
-    if side is None:
-        moe_shared(ptbl_sh, xs, iq4nl, sc.sact, sc.shared, stream=cur, layout=layout)
-    else:
+        if side is None:   # the shared expert rides in the grouped launches
+            moe_up4_sh(ptbl, sc.items, sc.nitp, sc.eoff, sc.plist, xs, iq4nl, sc.act, ptbl_sh[0:1], sc.sact,
+                       stream=cur, layout=layout)
+            moe_dn4_sh(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, iq4nl, sc.parts, ptbl_sh[1:2],
+                       sc.sact, sc.shared, stream=cur, layout=layout)
+        else:
+            moe_up4(ptbl, sc.items, sc.nitp, sc.eoff, sc.plist, xs, iq4nl, sc.act, stream=cur, layout=layout)
+            moe_dn4(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, iq4nl, sc.parts, stream=cur,
+                    layout=layout)
+    if side is not None:
         cur.wait_stream(side)
     moe_combine(sc.parts, sc.gates, sg, sc.shared, hres, y, stream=cur)
     return y
