@@ -460,8 +460,7 @@ int tlx_moe_dn6(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* 
                 const uint16_t* plist, const float* act, uint16_t* parts, int np, void* stream);
 /* Pair-walk form: replaces gx8e256dn6 (engine/mm/MM_P2_gx8e256dn6.cu:9-13):
  * gx8e256dn6(ptbl, eids, xs = act, parts).  The decode form, as tlx_moe_up3s_pairs: tlx_moe_dn6's
- * products (an operand may round once where tlx_moe_dn6 rounds twice, an fp16 ulp apart in rare
- * ties) summed in another k order. */
+ * operands summed in another k order. */
 int tlx_moe_dn6_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, uint16_t* parts,
                       int np, void* stream);
 /* The Q8_0 shared expert over P positions: y[P][2048] f32 = Wd . (silu(Wg . x) * (Wu . x)), with act

@@ -37,6 +37,30 @@ __device__ __forceinline__ uint16_t tlx_f2h_bits(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// fp16 pair {s * lo(h2), s * hi(h2)}: v_fma_mix takes the two fp16 halves of h2 as operands and
+// rounds each product to fp16 once, from the exact value (measured: 1 + 2^-11 + 2^-40 gives
+// 1 + 2^-10, not the 1.0 an intermediate f32 rounding would).  So it is the reference's fp16(f32
+// product) bit for bit only where the product is exact in f32 -- a block scale of <= 18
+// significant bits (fp16 d times a small integer) times a level of <= 6 -- and is not used for
+// a*q - b forms (Q4_K / Q5_K), whose f32 result can round.
+__device__ __forceinline__ uint32_t tlx_mix2_f16(float s, uint32_t h2) {
+  uint32_t r;
+  asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+      : "=&v"(r)
+      : "v"(s), "v"(h2));
+  return r;
+}
+
+// fp16 pair of bytes {0, 1} (hi = 0) or {2, 3} (hi = 1) of v as the integers byte - bias: v_perm
+// puts 0x64 above each byte (the fp16 1024 + byte, exact), a packed fp16 add takes 1024 + bias off
+// (exact: small integers).
+__device__ __forceinline__ uint32_t tlx_bytes_h2(uint32_t v, int hi, float bias) {
+  const uint32_t p = __builtin_amdgcn_perm(0x64646464u, v, hi ? 0x04030402u : 0x04010400u);
+  const _Float16 o = (_Float16)(1024.f + bias);
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p) - h2_t{o, o});
+}
+
 // Loads through a byte pointer whose alignment is only known to be 2 (raw GGUF blocks).
 template <typename T>
 __device__ __forceinline__ T tlx_ldu(const uint8_t* p) {

@@ -167,32 +167,10 @@ __device__ __forceinline__ void gv_lut_fill(GvLut& L, const float* gridf, int t)
     L.smask[t] = uint2{((t & 1u) << 15) | (((t >> 1) & 1u) << 31), (((t >> 2) & 1u) << 15) | (((t >> 3) & 1u) << 31)};
 }
 
-// fp16 pair {db * lo(g2), db * hi(g2)}, each the f32 product (exact here: db has at most 16
-// significant bits, a grid level at most 4) rounded once to fp16 -- v_fma_mix takes the fp16 halves
-// of g2 as operands, so the grid needs no widening
-__device__ __forceinline__ uint32_t gv_mix2(float db, uint32_t g2) {
-  uint32_t r;
-  asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]\n\t"
-      "v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
-      : "=&v"(r)
-      : "v"(db), "v"(g2));
-  return r;
-}
-
-// fp16 pairs {bytes 0, 1} (hi = 0) or {bytes 2, 3} (hi = 1) of v as the integers byte - bias: v_perm
-// puts 0x64 above each byte (the fp16 1024 + byte, exact), a packed fp16 add takes 1024 + bias off
-// (exact: small integers)
-__device__ __forceinline__ uint32_t gv_bytes_h2(uint32_t v, int hi, float bias) {
-  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-  const uint32_t p = __builtin_amdgcn_perm(0x64646464u, v, hi ? 0x04030402u : 0x04010400u);
-  const _Float16 o = (_Float16)(1024.f + bias);
-  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p) - h2_t{o, o});
-}
-
-// The 16 weights as fp16 operands, bit for bit the fp16 of gx_decode's values.  IQ3_S and Q8_0
-// through the fp16 lookups and v_fma_mix (their products are exact in f32, so one rounding is
-// gx_decode's rounding); Q6_K through gx_decode and a conversion (its product can round in f32,
-// and the reference's operand is that f32 value rounded again).
+// The 16 weights as fp16 operands, bit for bit the fp16 of gx_decode's values: the products of a
+// block scale and an integer level are exact in f32 for all three classes (IQ3_S: fp16 d times
+// 1 + 2 nib times a level <= 15, <= 20 bits; Q8_0: d times an int8, <= 19; Q6_K: d times an int8
+// scale times q - 32, <= 23), so v_fma_mix's one rounding to fp16 is the reference's.
 template <int CLS>
 __device__ __forceinline__ void gx_decode_h(u4_t* h, const GxRaw<CLS>& r, const GvLut* lut) {
   if constexpr (CLS == GX_IQ3S) {
@@ -201,26 +179,26 @@ __device__ __forceinline__ void gx_decode_h(u4_t* h, const GxRaw<CLS>& r, const 
     for (int i = 0; i < 4; ++i) {   // index byte i: weights 4i .. 4i+3
       const uint2 g = lut->grid[((r.qs >> (8 * i)) & 255u) | (((r.hs >> i) & 1u) << 8)];
       const uint2 m = lut->smask[(r.hs >> (8 + 4 * i)) & 15u];
-      h[i >> 1][2 * (i & 1)] = gv_mix2(db, g.x) ^ m.x;
-      h[i >> 1][2 * (i & 1) + 1] = gv_mix2(db, g.y) ^ m.y;
+      h[i >> 1][2 * (i & 1)] = tlx_mix2_f16(db, g.x) ^ m.x;
+      h[i >> 1][2 * (i & 1) + 1] = tlx_mix2_f16(db, g.y) ^ m.y;
     }
   } else if constexpr (CLS == GX_Q80) {
     const float d = tlx_h2f((uint16_t)r.d);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t u4 = r.q[j] ^ 0x80808080u;   // int8 + 128
-      h[j >> 1][2 * (j & 1)] = gv_mix2(d, gv_bytes_h2(u4, 0, 128.f));
-      h[j >> 1][2 * (j & 1) + 1] = gv_mix2(d, gv_bytes_h2(u4, 1, 128.f));
+      h[j >> 1][2 * (j & 1)] = tlx_mix2_f16(d, tlx_bytes_h2(u4, 0, 128.f));
+      h[j >> 1][2 * (j & 1) + 1] = tlx_mix2_f16(d, tlx_bytes_h2(u4, 1, 128.f));
     }
-  } else {
-    float v[16];
-    gx_decode<CLS>(v, r, nullptr);
+  } else {   // Q6_K: t = d * sc, weights l = 0 .. 15 of quarter g
+    const float t = tlx_h2f((uint16_t)(r.ds & 0xFFFFu)) * (float)(int8_t)(uint8_t)(r.ds >> 16);
+    const uint32_t g = (r.ds >> 29) & 3u;   // (kib >> 5) & 3
+    const uint32_t nsh = (g >> 1) * 4u, hsh = 2u * g;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      h8_t hh;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) hh[j] = (_Float16)v[8 * i + j];
-      h[i] = __builtin_bit_cast(u4_t, hh);
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t q4 = ((r.ql[j] >> nsh) & 0x0F0F0F0Fu) | (((r.qh[j] >> hsh) & 0x03030303u) << 4);
+      h[j >> 1][2 * (j & 1)] = tlx_mix2_f16(t, tlx_bytes_h2(q4, 0, 32.f));   // t * (q - 32)
+      h[j >> 1][2 * (j & 1) + 1] = tlx_mix2_f16(t, tlx_bytes_h2(q4, 1, 32.f));
     }
   }
 }
@@ -466,9 +444,7 @@ __device__ __forceinline__ int gv_koff(int kq, int s) {
 }
 
 // B operand of k-step s: fp16 of the GGUF values, the product of the block scale and the integer
-// level rounded to fp16 -- for IQ3_S and Q8_0 the product is exact in f32, so these are gx_decode's
-// operands bit for bit; Q6_K's can exceed f32's 24 bits, where gx_decode rounds twice (to f32, then
-// fp16) and v_fma_mix may round once, an fp16 ulp apart in rare ties
+// level rounded to fp16 (exact in f32 for the three classes: gx_decode's operands bit for bit)
 template <int CLS, int S>
 __device__ __forceinline__ h8_t gv_decode(const GvRaw<CLS>& r, int kq, const GvLut* lut) {
   if constexpr (CLS == GX_IQ3S) {
@@ -479,7 +455,7 @@ __device__ __forceinline__ h8_t gv_decode(const GvRaw<CLS>& r, int kq, const GvL
     const uint2 g1 = lut->grid[((qsw >> 8) & 255u) | ((qh & 2u) << 7)];
     const uint32_t sb = (S < 4 ? r.sg0 : r.sg1) >> (8 * (S & 3));
     const uint2 m0 = lut->smask[sb & 15u], m1 = lut->smask[(sb >> 4) & 15u];
-    const u4_t h = {gv_mix2(db, g0.x) ^ m0.x, gv_mix2(db, g0.y) ^ m0.y, gv_mix2(db, g1.x) ^ m1.x, gv_mix2(db, g1.y) ^ m1.y};
+    const u4_t h = {tlx_mix2_f16(db, g0.x) ^ m0.x, tlx_mix2_f16(db, g0.y) ^ m0.y, tlx_mix2_f16(db, g1.x) ^ m1.x, tlx_mix2_f16(db, g1.y) ^ m1.y};
     return __builtin_bit_cast(h8_t, h);
   } else if constexpr (CLS == GX_Q6K) {
     constexpr int n = S >> 2, q = S & 3;
@@ -491,8 +467,8 @@ __device__ __forceinline__ h8_t gv_decode(const GvRaw<CLS>& r, int kq, const GvL
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const uint32_t q4 = ((ql[2 * (q & 1) + j] >> (4 * n)) & 0x0F0F0F0Fu) | (((qv[2 * (q & 1) + j] >> sh) & 0x03030303u) << 4);
-      h[2 * j] = gv_mix2(t, gv_bytes_h2(q4, 0, 32.f));       // t * (q - 32)
-      h[2 * j + 1] = gv_mix2(t, gv_bytes_h2(q4, 1, 32.f));
+      h[2 * j] = tlx_mix2_f16(t, tlx_bytes_h2(q4, 0, 32.f));       // t * (q - 32)
+      h[2 * j + 1] = tlx_mix2_f16(t, tlx_bytes_h2(q4, 1, 32.f));
     }
     return __builtin_bit_cast(h8_t, h);
   } else {
@@ -503,8 +479,8 @@ __device__ __forceinline__ h8_t gv_decode(const GvRaw<CLS>& r, int kq, const GvL
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const uint32_t u4 = qv[2 * (q & 1) + j] ^ 0x80808080u;   // int8 + 128
-      h[2 * j] = gv_mix2(d, gv_bytes_h2(u4, 0, 128.f));
-      h[2 * j + 1] = gv_mix2(d, gv_bytes_h2(u4, 1, 128.f));
+      h[2 * j] = tlx_mix2_f16(d, tlx_bytes_h2(u4, 0, 128.f));
+      h[2 * j + 1] = tlx_mix2_f16(d, tlx_bytes_h2(u4, 1, 128.f));
     }
     return __builtin_bit_cast(h8_t, h);
   }

@@ -311,6 +311,8 @@ __device__ __forceinline__ void pf_kq_dequant(const PfKq& r, _Float16* bt, int r
       w[2 * i + 1] = pf_pack2(f[2], f[3]);
     }
   } else {
+    // A * (q - 32) has at most 11 + 7 + 5 = 23 significant bits: exact in f32, so v_fma_mix's
+    // one rounding of the product (the level as an fp16 integer) is fp16(f32 product)
     const int hp = s >> 2, g = s & 3;
     const float d = tlx_h2f((uint16_t)r.hdr.x);
     const int sci = (8 * hp + h + 2 * g) & 3;
@@ -319,11 +321,8 @@ __device__ __forceinline__ void pf_kq_dequant(const PfKq& r, _Float16* bt, int r
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t qv = ((r.q[i] >> nsh) & 0x0F0F0F0Fu) | (((r.hb[i] >> hsh) & 0x03030303u) << 4);
-      float f[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) f[e] = A * (float)((int)((qv >> (8 * e)) & 0xFFu) - 32);
-      w[2 * i] = pf_pack2(f[0], f[1]);
-      w[2 * i + 1] = pf_pack2(f[2], f[3]);
+      w[2 * i] = tlx_mix2_f16(A, tlx_bytes_h2(qv, 0, 32.f));
+      w[2 * i + 1] = tlx_mix2_f16(A, tlx_bytes_h2(qv, 1, 32.f));
     }
   }
   *reinterpret_cast<u4_t*>(bt + pf_frag(row, 2 * h)) = u4_t{w[0], w[1], w[2], w[3]};
