@@ -463,6 +463,17 @@ int tlx_moe_dn6(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* 
  * operands summed in another k order. */
 int tlx_moe_dn6_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, uint16_t* parts,
                       int np, void* stream);
+/* The sorted forms (tlx_moe_up3s / tlx_moe_dn6) and the Q8_0 shared expert's gate+up / down
+ * (tlx_moe_shared8's two launches) in one launch each above P = 16 (else the two launches): the
+ * shared expert's workgroups follow the routed ones.  No counterpart in the reference (gxu_gm /
+ * gxm_dn6 and shexp8 are separate launches); outputs those of the separate calls bit for bit.
+ * sact f32 [P][512] (16-B aligned) and shared f32 [P][2048] as tlx_moe_shared8's act / y. */
+int tlx_moe_up3s_sh(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const float* xs,
+                    const float* gridf, float* ys, int np, const void* wg8, const void* wu8, float* sact, int P,
+                    void* stream);
+int tlx_moe_dn6_sh(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
+                   const uint16_t* plist, const float* act, uint16_t* parts, int np, const void* wd8,
+                   const float* sact, float* shared, int P, void* stream);
 /* The Q8_0 shared expert over P positions: y[P][2048] f32 = Wd . (silu(Wg . x) * (Wu . x)), with act
  * f32[P][512] caller scratch (two launches on the stream; P <= 16 the decode form).  Replaces shexp8
  * (engine/mm/MM_P2_shexp8.cu:8-13): shexp8(wg [512][2176], wu [512][2176], wd [2048][544], x, y).

@@ -162,3 +162,17 @@ def test_moe_grouped_shared_fused_argument_validation():
     assert L.tlx_moe_up4_sh(p, p, p, p, p, p, p, p, 32, p, p + 4, 4, R, None) == _lib.TLX_E_ALIGN   # sact
     assert L.tlx_moe_dn4_sh(p, p, p, p, p, p, p, p, 16385, p, p, p, 4, R, None) == _lib.TLX_E_ARG
     assert L.tlx_moe_dn4_sh(p, p, p, p, p, p, p, p, 32, p, p, p + 4, 4, R, None) == _lib.TLX_E_ALIGN  # shared
+
+
+def test_moe_checkpoint_fused_argument_validation():
+    """The checkpoint-class sorted forms with the shared expert in the same launch reject bad
+    sizes and alignment before any launch."""
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(64)
+    p = (ctypes.addressof(buf) + 15) & ~15
+    assert L.tlx_moe_up3s_sh(p, p, p, p, p, p, 0, p, p, p, 4, None) == _lib.TLX_E_ARG          # no pairs
+    assert L.tlx_moe_up3s_sh(p, p, p, p, p, p, 32, p, p, p, 0, None) == _lib.TLX_E_ARG         # no positions
+    assert L.tlx_moe_up3s_sh(p, p, p, p, p, p, 32, p, p, p + 4, 4, None) == _lib.TLX_E_ALIGN   # sact
+    assert L.tlx_moe_up3s_sh(p, p, p, p + 4, p, p, 32, p, p, p, 4, None) == _lib.TLX_E_ALIGN   # xs
+    assert L.tlx_moe_dn6_sh(p, None, None, p, p, p, p, 16385, p, p, p, 4, None) == _lib.TLX_E_ARG
+    assert L.tlx_moe_dn6_sh(p, None, None, p, p, p, p, 32, p + 1, p, p, 4, None) == _lib.TLX_E_ALIGN  # wd8

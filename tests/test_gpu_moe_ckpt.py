@@ -183,6 +183,35 @@ def test_ckpt_shared_q80(gpu, ckpt, P):
     assert _rows_err(y.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("P", [11, 300])
+def test_ckpt_grouped_shared_fused(gpu, ckpt, P):
+    """moe_up3s_sh / moe_dn6_sh (the sorted forms and the Q8_0 shared expert in one launch each
+    above P = 16, two launches at P = 11) against moe_up3s / moe_dn6 / moe_shared8, bit for bit."""
+    print(f"[case] sorted forms + Q8_0 shared expert in one launch, P={P}", flush=True)
+    rng = np.random.default_rng(60 + P)
+    x, eids, deids, eoff, plist, items, nitp = _route(gpu, rng, P)
+    dx = torch.from_numpy(x).to(gpu)
+    np_ = 8 * P
+    mk = lambda shape, dt, v: torch.full(shape, v, dtype=dt, device=gpu)
+    sep = dict(act=mk((np_, moe.FF), torch.float32, -3.0), parts=mk((np_, moe.HID), torch.float16, -3.0),
+               sact=mk((P, moe.FF), torch.float32, -3.0), shared=mk((P, moe.HID), torch.float32, -3.0))
+    fus = {k: torch.full_like(v, -5.0) for k, v in sep.items()}
+    wg8, wu8, wd8 = ckpt["dsh"]
+    ops.moe_up3s(ckpt["ptbl"], eoff, plist, dx, ckpt["gridf"], sep["act"])
+    ops.moe_dn6(ckpt["ptbl_dn"], items, nitp, eoff, plist, sep["act"], sep["parts"])
+    ops.moe_shared8(wg8, wu8, wd8, dx, sep["shared"], sep["sact"])
+    ops.moe_up3s_sh(ckpt["ptbl"], eoff, plist, dx, ckpt["gridf"], fus["act"], wg8, wu8, fus["sact"])
+    ops.moe_dn6_sh(ckpt["ptbl_dn"], items, nitp, eoff, plist, fus["act"], fus["parts"], wd8, fus["sact"],
+                   fus["shared"])
+    torch.cuda.synchronize()
+    for k in sep:
+        a, b = sep[k].cpu().numpy(), fus[k].cpu().numpy()
+        v = np.uint16 if a.dtype == np.float16 else np.uint32
+        assert np.array_equal(a.view(v), b.view(v)), k
+    ref = moe.shared8_ref(*ckpt["shared"], x)
+    assert _rows_err(fus["shared"].cpu().numpy(), ref) <= TOL
+
+
 def test_ckpt_argument_validation(gpu, ckpt):
     dx = torch.zeros(2, moe.HID, device=gpu)
     act = torch.empty(16, moe.FF, dtype=torch.float32, device=gpu)

@@ -217,8 +217,10 @@ __device__ __forceinline__ void gx_dequant16(float* v, const uint8_t* row, int k
   gx_decode<CLS>(v, gx_fetch<CLS>(row, k0), grid);
 }
 
-template <int CLS, bool UP, int FORM>
-__global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
+// blk: the workgroup's index in its part of the grid (parts start at multiples of 8); L: any
+// GxLds<UP, *, kGxTok> that holds the IQ3_S lookups when CLS needs them
+template <int CLS, bool UP, int FORM, typename LDS>
+__device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
   constexpr int K = UP ? kHid : kFf;
   constexpr int NR = (UP ? 2 : 1) * kGxCols;              // staged weight rows
   constexpr int RB = (UP ? kFf : kHid) / kGxCols;         // column blocks per matrix
@@ -227,13 +229,12 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
   constexpr int TOK = kGxTok;
   static_assert(FORM != GX_PAIRS, "the pair walk is gv_kernel's");
   constexpr int NG = TOK / 16;                            // 16-token MFMA groups per pass
-  __shared__ GxLds<UP, GRID, TOK> L;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 15, kq = lane >> 4;
   // Workgroups go to the 8 XCDs round robin (block b to XCD b % 8), each XCD with its own L2.  The RB
   // column blocks of one item are all placed on one XCD, so the item's activation rows -- read by
   // every column block -- come from HBM once and from that XCD's L2 after.
-  const int slot = (int)blockIdx.x >> 3;
-  const int rb = slot % RB, item = slot / RB * 8 + ((int)blockIdx.x & 7);
+  const int slot = blk >> 3;
+  const int rb = slot % RB, item = slot / RB * 8 + (blk & 7);
   if (item >= a.items) return;   // the grid is padded to a multiple of 8 items
 
   // the work item: token list, weight matrices
@@ -381,6 +382,26 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
 }
 
 #undef GX_FETCH
+
+template <int CLS, bool UP, int FORM>
+__global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
+  __shared__ GxLds<UP, CLS == GX_IQ3S, kGxTok> L;
+  gx_body<CLS, UP, FORM>(L, a, (int)blockIdx.x);
+}
+
+// The sorted form (class RCLS) and the Q8_0 shared expert's dense form in one launch: workgroups
+// below nra run the routed experts (args a), the rest the shared expert (args b) -- each part its
+// own launch's code, so the outputs are the separate launches' bit for bit.  The shared expert's
+// workgroups come last, filling the routed grid's last round.
+template <int RCLS, bool UP>
+__global__ __launch_bounds__(kGxThreads) void gx_sh_kernel(const GxArgs a, const GxArgs b, int nra) {
+  __shared__ GxLds<UP, RCLS == GX_IQ3S, kGxTok> L;
+  const int blk = (int)blockIdx.x;
+  if (blk < nra)
+    gx_body<RCLS, UP, GX_SORTED>(L, a, blk);
+  else
+    gx_body<GX_Q80, UP, GX_DENSE>(L, b, blk - nra);
+}
 
 // ------------------------------------------------------------------ decode form (GEMV-shaped)
 // Items of at most 16 tokens -- the pair walk (one token a pair) and the shared expert at P <= 16
@@ -727,6 +748,76 @@ extern "C" int tlx_moe_dn6_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, 
   return gv_launch<GX_Q6K, false, GX_PAIRS, 1, 4>(a, np, (hipStream_t)stream);
 }
 
+// the shared expert's two launches (decode form at P <= kGvTok)
+static int moe_shared8_up(const void* wg, const void* wu, const float* x, float* act, int P, hipStream_t st) {
+  GxArgs a{};
+  a.w0 = (const uint8_t*)wg; a.w1 = (const uint8_t*)wu; a.x = x; a.out = act; a.P = P;
+  if (P <= kGvTok) return gv_launch<GX_Q80, true, GX_DENSE, 8, 8>(a, 1, st);
+  return gx_launch<GX_Q80, true, GX_DENSE>(a, (P + kGxTok - 1) / kGxTok, st);
+}
+
+static int moe_shared8_dn(const void* wd, const float* act, float* y, int P, hipStream_t st) {
+  GxArgs b{};
+  b.w0 = (const uint8_t*)wd; b.x = act; b.out = y; b.P = P;
+  if (P <= kGvTok) return gv_launch<GX_Q80, false, GX_DENSE, 2, 8>(b, 1, st);
+  return gx_launch<GX_Q80, false, GX_DENSE>(b, (P + kGxTok - 1) / kGxTok, st);
+}
+
+// routed sorted form (a, kE items) + the shared expert's dense form (b) in one launch, P > kGvTok
+template <int RCLS, bool UP>
+static int gx_sh_launch(const GxArgs& a, const GxArgs& b, hipStream_t st) {
+  constexpr int RB = (UP ? kFf : kHid) / kGxCols;
+  GxArgs ra = a, sb = b;
+  ra.items = kE;
+  sb.items = (b.P + kGxTok - 1) / kGxTok;
+  const int nra = (kE + 7) / 8 * 8 * RB, nsb = (sb.items + 7) / 8 * 8 * RB;
+  gx_sh_kernel<RCLS, UP><<<(unsigned)(nra + nsb), kGxThreads, 0, st>>>(ra, sb, nra);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_moe_up3s_sh(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const float* xs,
+                               const float* gridf, float* ys, int np, const void* wg8, const void* wu8, float* sact,
+                               int P, void* stream) {
+  TLX_RET_IF(!ptbl || !eoff || !plist || !xs || !gridf || !ys || !wg8 || !wu8 || !sact, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs || P < 1 || P > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(ptbl, 8) || !tlx_aligned(xs, 16) || !tlx_aligned(gridf, 16) || !tlx_aligned(ys, 4),
+             TLX_E_ALIGN);
+  TLX_RET_IF(!tlx_aligned(wg8, 2) || !tlx_aligned(wu8, 2) || !tlx_aligned(sact, 16), TLX_E_ALIGN);
+  const hipStream_t st = (hipStream_t)stream;
+  GxArgs a{};
+  a.ptbl = ptbl; a.eoff = eoff; a.plist = plist; a.x = xs; a.grid = gridf; a.out = ys;
+  if (P <= kGvTok) {   // the shared expert's decode form is another kernel: two launches
+    const int rc = gx_launch<GX_IQ3S, true, GX_SORTED>(a, kE, st);
+    TLX_RET_IF(rc != TLX_OK, rc);
+    return moe_shared8_up(wg8, wu8, xs, sact, P, st);
+  }
+  GxArgs b{};
+  b.w0 = (const uint8_t*)wg8; b.w1 = (const uint8_t*)wu8; b.x = xs; b.out = sact; b.P = P;
+  return gx_sh_launch<GX_IQ3S, true>(a, b, st);
+}
+
+extern "C" int tlx_moe_dn6_sh(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
+                              const uint16_t* plist, const float* act, uint16_t* parts, int np, const void* wd8,
+                              const float* sact, float* shared, int P, void* stream) {
+  (void)items;   // the reference's slots; this form walks eoff / plist itself
+  (void)nitp;
+  TLX_RET_IF(!ptbl_dn || !eoff || !plist || !act || !parts || !wd8 || !sact || !shared, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs || P < 1 || P > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(ptbl_dn, 8) || !tlx_aligned(act, 16) || !tlx_aligned(parts, 2), TLX_E_ALIGN);
+  TLX_RET_IF(!tlx_aligned(wd8, 2) || !tlx_aligned(sact, 16) || !tlx_aligned(shared, 4), TLX_E_ALIGN);
+  const hipStream_t st = (hipStream_t)stream;
+  GxArgs a{};
+  a.ptbl = ptbl_dn; a.eoff = eoff; a.plist = plist; a.x = act; a.out = parts;
+  if (P <= kGvTok) {
+    const int rc = gx_launch<GX_Q6K, false, GX_SORTED>(a, kE, st);
+    TLX_RET_IF(rc != TLX_OK, rc);
+    return moe_shared8_dn(wd8, sact, shared, P, st);
+  }
+  GxArgs b{};
+  b.w0 = (const uint8_t*)wd8; b.x = sact; b.out = shared; b.P = P;
+  return gx_sh_launch<GX_Q6K, false>(a, b, st);
+}
+
 extern "C" int tlx_moe_shared8(const void* wg, const void* wu, const void* wd, const float* x, float* y, float* act,
                                int P, void* stream) {
   TLX_RET_IF(!wg || !wu || !wd || !x || !y || !act, TLX_E_ARG);
@@ -734,21 +825,7 @@ extern "C" int tlx_moe_shared8(const void* wg, const void* wu, const void* wd, c
   TLX_RET_IF(!tlx_aligned(wg, 2) || !tlx_aligned(wu, 2) || !tlx_aligned(wd, 2), TLX_E_ALIGN);
   TLX_RET_IF(!tlx_aligned(x, 16) || !tlx_aligned(act, 16) || !tlx_aligned(y, 4), TLX_E_ALIGN);
   hipStream_t st = (hipStream_t)stream;
-  if (P <= kGvTok) {   // decode: the GEMV-shaped form, k split over the waves of a tile
-    GxArgs a{};
-    a.w0 = (const uint8_t*)wg; a.w1 = (const uint8_t*)wu; a.x = x; a.out = act; a.P = P;
-    int r = gv_launch<GX_Q80, true, GX_DENSE, 8, 8>(a, 1, st);
-    TLX_RET_IF(r != TLX_OK, r);
-    GxArgs b{};
-    b.w0 = (const uint8_t*)wd; b.x = act; b.out = y; b.P = P;
-    return gv_launch<GX_Q80, false, GX_DENSE, 2, 8>(b, 1, st);
-  }
-  const int items = (P + kGxTok - 1) / kGxTok;
-  GxArgs a{};
-  a.w0 = (const uint8_t*)wg; a.w1 = (const uint8_t*)wu; a.x = x; a.out = act; a.P = P;
-  int r = gx_launch<GX_Q80, true, GX_DENSE>(a, items, st);
+  const int r = moe_shared8_up(wg, wu, x, act, P, st);   // decode (P <= 16): the GEMV-shaped form
   TLX_RET_IF(r != TLX_OK, r);
-  GxArgs b{};
-  b.w0 = (const uint8_t*)wd; b.x = act; b.out = y; b.P = P;
-  return gx_launch<GX_Q80, false, GX_DENSE>(b, items, st);
+  return moe_shared8_dn(wd, act, y, P, st);
 }

@@ -848,6 +848,45 @@ def moe_dn6(ptbl_dn, items, nitp, eoff, plist, act, parts, stream=None):
          n, _stream(stream))
 
 
+def moe_up3s_sh(ptbl, eoff, plist, xs, gridf, ys, wg8, wu8, sact, stream=None):
+    """moe_up3s over the sorted pairs and the Q8_0 shared expert's gate+up (wg8 / wu8 rows, into
+    sact [P][512], P = xs.shape[0]) in one launch above P = 16 (else the two launches); outputs
+    those of moe_up3s and moe_shared8's gate+up bit for bit."""
+    n = ys.shape[0]
+    P = xs.shape[0]
+    _need(ptbl, 256 * 8, "ptbl")
+    _need(eoff, 257 * 4, "eoff")
+    _need(plist, n * 2, "plist")
+    _need(xs, max(P, (n + 7) // 8) * 2048 * 4, "xs")
+    _need(ys, n * 512 * 4, "ys")
+    _need(gridf, 512 * 16, "gridf")
+    _need(wg8, 512 * 2176, "wg8")
+    _need(wu8, 512 * 2176, "wu8")
+    _need(sact, P * 512 * 4, "sact")
+    _dev(ptbl, eoff, plist, xs, gridf, ys, wg8, wu8, sact)
+    call("tlx_moe_up3s_sh", ptbl.data_ptr(), eoff.data_ptr(), plist.data_ptr(), xs.data_ptr(), gridf.data_ptr(),
+         ys.data_ptr(), n, wg8.data_ptr(), wu8.data_ptr(), sact.data_ptr(), P, _stream(stream))
+
+
+def moe_dn6_sh(ptbl_dn, items, nitp, eoff, plist, act, parts, wd8, sact, shared, stream=None):
+    """moe_dn6 over the sorted pairs and the Q8_0 shared expert's down projection (wd8 rows, sact
+    [P][512] into shared [P][2048] f32, P = sact.shape[0]) in one launch above P = 16 (else the
+    two launches); outputs those of the separate calls bit for bit."""
+    n = act.shape[0]
+    P = sact.shape[0]
+    _need(ptbl_dn, 256 * 8, "ptbl_dn")
+    _need(eoff, 257 * 4, "eoff")
+    _need(plist, n * 2, "plist")
+    _need(act, n * 512 * 4, "act")
+    _need(parts, n * 2048 * 2, "parts")
+    _need(wd8, 2048 * 544, "wd8")
+    _need(shared, P * 2048 * 4, "shared")
+    _dev(ptbl_dn, eoff, plist, act, parts, wd8, sact, shared)
+    call("tlx_moe_dn6_sh", ptbl_dn.data_ptr(), None if items is None else items.data_ptr(),
+         None if nitp is None else nitp.data_ptr(), eoff.data_ptr(), plist.data_ptr(), act.data_ptr(),
+         parts.data_ptr(), n, wd8.data_ptr(), sact.data_ptr(), shared.data_ptr(), P, _stream(stream))
+
+
 def moe_dn6_pairs(ptbl_dn, eids, act, parts, stream=None):
     """gx8e256dn6(ptbl, eids, act, parts): pair p runs Q6_K expert eids[p] on act[p], no sort."""
     n = act.shape[0]
@@ -965,15 +1004,15 @@ def moe_layer_ckpt(logits, sg, xs, hres, y, ptbl, ptbl_dn, shared8, gridf, scrat
     top-8, then the pair walk (P <= MOE_PAIR_WALK_MAX_P by default) or sort + grouped forms for
     the IQ3_S gate+up, the down projection -- ``down`` "q6k" (Q6_K slabs, the checkpoint's layers
     34/38/39) or "iq4" (IQ4_XS GGUF-row slabs, iq4nl given) -- the Q8_0 shared expert
-    (shared8 = (wg, wu, wd) rows), and the combine into y.  overlap_shared as moe_layer's: the
-    shared expert on a second stream, joined before the combine; None overlaps on the grouped
-    path only (measured in graphs: P=2048 663 -> 652 us; P=11 77 -> 79 us, the fork and join
-    costing more than the overlap saves)."""
+    (shared8 = (wg, wu, wd) rows), and the combine into y.  overlap_shared as moe_layer's: by
+    default the shared expert rides in the grouped launches (moe_up3s_sh / moe_dn6_sh; the pair
+    walk keeps its own two launches, the decode form being another kernel); with it, on a second
+    stream joined before the combine."""
     sc = scratch
     if pair_walk is None:
         pair_walk = xs.shape[0] <= MOE_PAIR_WALK_MAX_P
     if overlap_shared is None:
-        overlap_shared = not pair_walk
+        overlap_shared = False
     cur = stream if isinstance(stream, torch.cuda.Stream) else torch.cuda.current_stream()
     side = None
     if overlap_shared:
@@ -984,6 +1023,10 @@ def moe_layer_ckpt(logits, sg, xs, hres, y, ptbl, ptbl_dn, shared8, gridf, scrat
         moe_shared8(*shared8, xs, sc.shared, sc.sact, stream=side)
     moe_topk(logits, sc.eids, sc.gates, stream=cur)
     eids = sc.eids.view(-1)
+    wg8, wu8, wd8 = shared8
+    # the shared expert in the grouped launches (the Q6_K down layers; with an IQ4_XS down the
+    # shared expert keeps its own two launches)
+    fused = side is None and not pair_walk and down == "q6k"
     if pair_walk:
         moe_up3s_pairs(ptbl, eids, xs, gridf, sc.act, stream=cur)
         if down == "q6k":
@@ -992,15 +1035,21 @@ def moe_layer_ckpt(logits, sg, xs, hres, y, ptbl, ptbl_dn, shared8, gridf, scrat
             moe_dn4_pairs(ptbl_dn, eids, sc.act, iq4nl, sc.parts, stream=cur)
     else:
         moe_sort(sc.eids, sc.eoff, sc.plist, sc.items, sc.nitp, stream=cur)
-        moe_up3s(ptbl, sc.eoff, sc.plist, xs, gridf, sc.act, stream=cur)
-        if down == "q6k":
+        if fused:
+            moe_up3s_sh(ptbl, sc.eoff, sc.plist, xs, gridf, sc.act, wg8, wu8, sc.sact, stream=cur)
+        else:
+            moe_up3s(ptbl, sc.eoff, sc.plist, xs, gridf, sc.act, stream=cur)
+        if fused:
+            moe_dn6_sh(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, sc.parts, wd8, sc.sact, sc.shared,
+                       stream=cur)
+        elif down == "q6k":
             moe_dn6(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, sc.parts, stream=cur)
         else:
             moe_dn4(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, iq4nl, sc.parts, stream=cur)
-    if side is None:
-        moe_shared8(*shared8, xs, sc.shared, sc.sact, stream=cur)
-    else:
+    if side is not None:
         cur.wait_stream(side)
+    elif not fused:
+        moe_shared8(*shared8, xs, sc.shared, sc.sact, stream=cur)
     moe_combine(sc.parts, sc.gates, sg, sc.shared, hres, y, stream=cur)
     return y
 
