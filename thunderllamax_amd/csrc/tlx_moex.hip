@@ -9,9 +9,9 @@
 // ptbl_dn[e] -- 2048 rows of 420 B (2 raw 210-B blocks, k = 512); the shared expert's Q8_0 gate and
 // up rows (512 x 2176 B, k = 2048) and down rows (2048 x 544 B, k = 512).
 //
-// Two kernels.  gx_kernel (batches): a workgroup (4 waves) owns 64 output columns of one expert --
-// for gate+up 64 gate rows and the matching 64 up rows, so the SwiGLU pairs meet in one lane; for
-// down 64 rows -- and up to 64 token rows at a time (a pass).  K runs in chunks of 64: the pass's
+// Two kernels.  gx_kernel (batches): a workgroup owns 16 output columns per wave of one expert --
+// gate+up: 4 waves, 64 gate rows and the matching 64 up rows, so the SwiGLU pairs meet in one
+// lane; down: 8 waves, 128 rows -- and up to 64 token rows at a time (a pass).  K runs in chunks of 64: the pass's
 // activations (f32 -> fp16, round to nearest even) and the column block's weight rows, dequantized
 // to the reference's operands -- fp16 of the fp32 GGUF value, as gxu_gm stages them -- go to LDS
 // (rows padded to 72 halfs: the 16 rows of a fragment read fall in distinct 16-B slots); then wave
@@ -26,10 +26,11 @@
 namespace {
 
 constexpr int kHid = 2048, kFf = 512, kE = 256, kMaxPairs = 16384;
-constexpr int kGxCols = 64;         // output columns per workgroup
+// waves per staged-form workgroup, 16 output columns each (measured at M = 2048: gate+up 4 / 8 /
+// 16 waves 313 / 332 / 409 us; down 235 / 204 / 267 us)
+template <bool UP> constexpr int gx_waves() { return UP ? 4 : 8; }
 constexpr int kGxKc = 64;           // k per chunk (LDS stage)
 constexpr int kGxLd = kGxKc + 8;    // LDS row stride (halfs): fragment reads of 16 rows hit 16 distinct 16-B slots
-constexpr int kGxThreads = 256;
 constexpr uint32_t kIq3sGate = kFf * 880;   // GATE_B: the up rows' offset in an IQ3_S slab
 
 enum GxCls { GX_IQ3S = 0, GX_Q6K = 1, GX_Q80 = 2 };
@@ -206,7 +207,7 @@ __device__ __forceinline__ void gx_decode_h(u4_t* h, const GxRaw<CLS>& r, const 
 template <bool UP, bool GRID, int TOK>
 struct alignas(16) GxLds {   // 16-B fragment reads and stores
   _Float16 x[TOK * kGxLd];
-  _Float16 w[(UP ? 2 : 1) * kGxCols * kGxLd];
+  _Float16 w[(UP ? 2 : 1) * 16 * gx_waves<UP>() * kGxLd];
   GvLutSlot<GRID> lut;
   int xrow[TOK];
   int orow[TOK];
@@ -222,8 +223,9 @@ __device__ __forceinline__ void gx_dequant16(float* v, const uint8_t* row, int k
 template <int CLS, bool UP, int FORM, typename LDS>
 __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
   constexpr int K = UP ? kHid : kFf;
-  constexpr int NR = (UP ? 2 : 1) * kGxCols;              // staged weight rows
-  constexpr int RB = (UP ? kFf : kHid) / kGxCols;         // column blocks per matrix
+  constexpr int NW = gx_waves<UP>(), NT = 64 * NW, CO = 16 * NW;   // waves, threads, output columns
+  constexpr int NR = (UP ? 2 : 1) * CO;                   // staged weight rows
+  constexpr int RB = (UP ? kFf : kHid) / CO;              // column blocks per matrix
   constexpr int ROWB = K / GxFmt<CLS>::kPer * GxFmt<CLS>::kBlk;
   constexpr bool GRID = CLS == GX_IQ3S;
   constexpr int TOK = kGxTok;
@@ -254,7 +256,7 @@ __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
   if constexpr (UP) wu = FORM == GX_DENSE ? a.w1 : wg + kIq3sGate;
   const GvLut* lut = nullptr;
   if constexpr (GRID) {
-    gv_lut_fill<kGxThreads>(L.lut.v, a.grid, t);
+    gv_lut_fill<NT>(L.lut.v, a.grid, t);
     lut = &L.lut.v;
   }
 
@@ -279,14 +281,14 @@ __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
       for (int m = 0; m < (UP ? 2 : 1); ++m) acc[g][m] = f4_t{0.f, 0.f, 0.f, 0.f};
 
     // the thread's weight units (staged row R, 16-weight piece q) and activation pieces
-    constexpr int NU = NR * (kGxKc / 16) / kGxThreads;       // units per thread (1 or 2)
-    constexpr int NX = (TOK * kGxKc / 8 + kGxThreads - 1) / kGxThreads;   // activation pieces per thread
-    static_assert(NR * (kGxKc / 16) % kGxThreads == 0, "units");
+    constexpr int NU = NR * (kGxKc / 16) / NT;       // units per thread (1 or 2)
+    constexpr int NX = (TOK * kGxKc / 8 + NT - 1) / NT;   // activation pieces per thread
+    static_assert(NR * (kGxKc / 16) % NT == 0, "units");
     const uint8_t* urow[NU];
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
-      const int R = (t + i * kGxThreads) >> 2;
-      urow[i] = ((UP && R >= kGxCols) ? wu : wg) + (size_t)(rb * kGxCols + (R & (kGxCols - 1))) * ROWB;
+      const int R = (t + i * NT) >> 2;
+      urow[i] = ((UP && R >= CO) ? wu : wg) + (size_t)(rb * CO + (R & (CO - 1))) * ROWB;
     }
     GxRaw<CLS> raw[NU];
     float4 xv[NX][2];
@@ -297,7 +299,7 @@ __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
     __syncthreads();   // the token rows are visible
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-      const int pc = t + i * kGxThreads;
+      const int pc = t + i * NT;
       const int xr = pc < TOK * kGxKc / 8 ? L.xrow[pc >> 3] : -1;
       xz[i] = xr < 0;
       xo[i] = (xr < 0 ? 0 : xr) * K + 8 * (pc & 7);
@@ -305,7 +307,7 @@ __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
 #define GX_FETCH(KC)                                                                                 \
   {                                                                                                  \
     _Pragma("unroll") for (int i = 0; i < NU; ++i)                                                   \
-      raw[i] = gx_fetch<CLS>(urow[i], (KC) * kGxKc + 16 * ((t + i * kGxThreads) & 3));               \
+      raw[i] = gx_fetch<CLS>(urow[i], (KC) * kGxKc + 16 * ((t + i * NT) & 3));                       \
     _Pragma("unroll") for (int i = 0; i < NX; ++i) {                                                 \
       const float4* src = reinterpret_cast<const float4*>(a.x + (size_t)xo[i] + (KC) * kGxKc);       \
       xv[i][0] = src[0];                                                                             \
@@ -321,7 +323,7 @@ __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
       __syncthreads();   // the previous chunk's fragment reads are done
 #pragma unroll
       for (int i = 0; i < NX; ++i) {
-        const int pc = t + i * kGxThreads;
+        const int pc = t + i * NT;
         if (pc < TOK * kGxKc / 8) {
           const float4 z = float4{0.f, 0.f, 0.f, 0.f};
           const float4 u = xz[i] ? z : xv[i][0], w = xz[i] ? z : xv[i][1];
@@ -332,7 +334,7 @@ __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
       }
 #pragma unroll
       for (int i = 0; i < NU; ++i) {
-        const int u = t + i * kGxThreads;
+        const int u = t + i * NT;
         u4_t h[2];
         gx_decode_h<CLS>(h, raw[i], lut);
         *reinterpret_cast<u4_t*>(L.w + (u >> 2) * kGxLd + 16 * (u & 3)) = h[0];
@@ -347,7 +349,7 @@ __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
         const int ko = 32 * s + 8 * kq;
         const h8_t bg = *reinterpret_cast<const h8_t*>(L.w + (16 * wave + col) * kGxLd + ko);
         h8_t bu;
-        if constexpr (UP) bu = *reinterpret_cast<const h8_t*>(L.w + (kGxCols + 16 * wave + col) * kGxLd + ko);
+        if constexpr (UP) bu = *reinterpret_cast<const h8_t*>(L.w + (CO + 16 * wave + col) * kGxLd + ko);
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
           if (g < ng) {
@@ -359,7 +361,7 @@ __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
       }
     }
     // lane (col, kq) holds tokens 16 g + 4 kq + r of output column rb * 64 + 16 wave + col
-    const int n = rb * kGxCols + 16 * wave + col;
+    const int n = rb * CO + 16 * wave + col;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       if (g >= ng) break;
@@ -384,7 +386,7 @@ __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
 #undef GX_FETCH
 
 template <int CLS, bool UP, int FORM>
-__global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
+__global__ __launch_bounds__(64 * gx_waves<UP>()) void gx_kernel(const GxArgs a) {
   __shared__ GxLds<UP, CLS == GX_IQ3S, kGxTok> L;
   gx_body<CLS, UP, FORM>(L, a, (int)blockIdx.x);
 }
@@ -394,7 +396,7 @@ __global__ __launch_bounds__(kGxThreads) void gx_kernel(const GxArgs a) {
 // own launch's code, so the outputs are the separate launches' bit for bit.  The shared expert's
 // workgroups come last, filling the routed grid's last round.
 template <int RCLS, bool UP>
-__global__ __launch_bounds__(kGxThreads) void gx_sh_kernel(const GxArgs a, const GxArgs b, int nra) {
+__global__ __launch_bounds__(64 * gx_waves<UP>()) void gx_sh_kernel(const GxArgs a, const GxArgs b, int nra) {
   __shared__ GxLds<UP, RCLS == GX_IQ3S, kGxTok> L;
   const int blk = (int)blockIdx.x;
   if (blk < nra)
@@ -674,10 +676,10 @@ __global__ __launch_bounds__(256) void gx_dequant_kernel(const uint8_t* __restri
 
 template <int CLS, bool UP, int FORM>
 int gx_launch(const GxArgs& a, int items, hipStream_t st) {
-  constexpr int RB = (UP ? kFf : kHid) / kGxCols;
+  constexpr int RB = (UP ? kFf : kHid) / (16 * gx_waves<UP>());
   GxArgs b = a;
   b.items = items;
-  gx_kernel<CLS, UP, FORM><<<(unsigned)((items + 7) / 8 * 8 * RB), kGxThreads, 0, st>>>(b);
+  gx_kernel<CLS, UP, FORM><<<(unsigned)((items + 7) / 8 * 8 * RB), 64 * gx_waves<UP>(), 0, st>>>(b);
   return tlx_launch_status();
 }
 
@@ -766,12 +768,12 @@ static int moe_shared8_dn(const void* wd, const float* act, float* y, int P, hip
 // routed sorted form (a, kE items) + the shared expert's dense form (b) in one launch, P > kGvTok
 template <int RCLS, bool UP>
 static int gx_sh_launch(const GxArgs& a, const GxArgs& b, hipStream_t st) {
-  constexpr int RB = (UP ? kFf : kHid) / kGxCols;
+  constexpr int RB = (UP ? kFf : kHid) / (16 * gx_waves<UP>());
   GxArgs ra = a, sb = b;
   ra.items = kE;
   sb.items = (b.P + kGxTok - 1) / kGxTok;
   const int nra = (kE + 7) / 8 * 8 * RB, nsb = (sb.items + 7) / 8 * 8 * RB;
-  gx_sh_kernel<RCLS, UP><<<(unsigned)(nra + nsb), kGxThreads, 0, st>>>(ra, sb, nra);
+  gx_sh_kernel<RCLS, UP><<<(unsigned)(nra + nsb), 64 * gx_waves<UP>(), 0, st>>>(ra, sb, nra);
   return tlx_launch_status();
 }
 
