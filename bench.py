@@ -97,7 +97,9 @@ TRAFFIC = {
     "merged_attnqkv_q6": 875_961_139,   # pfm_gemm_kernel: F 399,043.4  W 57,344
     "merged_gdnqg": 568_197_120,        # pfm_gemm_kernel: F 244,672.0  W 65,536
     "moe_m11": 153_883_750,             # topk + pair-walk gate+up and down (shared inside) + combine: F 74,775.3  W 726.5
-    "moe_m2048": 854_722_048,           # topk, sort, grouped gate+up / down, shared two, combine: F 349,518.3  W 135,652.9
+    "moe_m2048": 863_987_917,           # topk, sort, grouped gate+up / down with the shared expert, combine: F 354,038.1  W 135,662.0
+    "ckpt_m11": 161_291_981,            # checkpoint classes: topk, pair-walk IQ3_S up / Q6_K down, Q8_0 shared two, combine: F 78,392.6  W 726.5
+    "ckpt_m2048": 933_744_128,          # checkpoint classes: topk, sort, sorted up / down with the shared expert, combine: F 388,178.3  W 135,502.9
     "sweep": 12_030_388_122,            # one decode step: F 5,591,363.3  W 565,699.3
 }
 PEAK_F16_TFLOPS = 2500.0
@@ -489,13 +491,14 @@ def moe_ckpt_leg(ops, formats, synth, torch, dev, steps, warmup):
         wbytes = hit * (2 * F * 880 + H * 420) + 2 * F * 2176 + H * 544
         tflops = flops / (t * 1e-3) / 1e12
         gbs = wbytes / (t * 1e-3) / 1e9
-        route = "pair walk" if P <= ops.MOE_PAIR_WALK_MAX_P else "sort + grouped forms"
+        route = "pair walk" if P <= ops.MOE_PAIR_WALK_MAX_P else "sort + sorted forms with the shared expert inside"
         out[f"M{P}"] = {"ms": round(t, 4), "tflops": round(tflops, 2), "experts_hit": hit, "weight_gbs": round(gbs, 1),
                         "route": route,
                         "roofline": (hbm_roofline(gbs, f"checkpoint-class MoE layer ({route}; graph): expert bytes / "
-                                                       "layer time") if P <= 64 else
+                                                       "layer time", traffic=TRAFFIC.get(f"ckpt_m{P}")) if P <= 64 else
                                      mfma_roofline(tflops, f"checkpoint-class MoE layer ({route}; graph): "
-                                                           "2*3*512*2048*9*M / layer time"))}
+                                                           "2*3*512*2048*9*M / layer time",
+                                                   traffic=TRAFFIC.get(f"ckpt_m{P}")))}
     return out
 
 
