@@ -539,8 +539,15 @@ __global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 15, kq = lane >> 4;
   const int tile = wave / KS, kp = wave % KS;
   // the XCD-aware order of gx_kernel: an item's workgroups on one XCD
-  const int slot = (int)blockIdx.x >> 3;
-  const int rb = slot % RB, item = slot / RB * 8 + ((int)blockIdx.x & 7);
+  int rb, item;
+  if constexpr (FORM == GX_DENSE) {   // one item at decode: its column blocks over all XCDs
+    rb = (int)blockIdx.x % RB;
+    item = (int)blockIdx.x / RB;
+  } else {
+    const int slot = (int)blockIdx.x >> 3;
+    rb = slot % RB;
+    item = slot / RB * 8 + ((int)blockIdx.x & 7);
+  }
   if (item >= a.items) return;
 
   int beg, nt;
@@ -561,7 +568,9 @@ __global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
     lut = &lslot.v;
   }
   // token rows, fp16 (round to nearest even); rows past the item repeat its last (not stored)
-  for (int pc = t; pc < TOKR * (K / 8); pc += NT) {
+  // (dense: the item's nt rows only -- the lanes of rows past it read unstaged LDS, and their
+  // MFMA rows are never stored)
+  for (int pc = t; pc < (FORM == GX_DENSE ? nt : TOKR) * (K / 8); pc += NT) {
     const int r = pc / (K / 8), k8 = pc - r * (K / 8);
     const int xr = FORM == GX_PAIRS ? (UP ? beg >> 3 : beg) : beg + min(r, nt - 1);
     const float4* src = reinterpret_cast<const float4*>(a.x + (size_t)xr * K + 8 * k8);
@@ -638,7 +647,9 @@ template <int CLS, bool UP, int FORM, int KS, int NW>
 int gv_launch(const GxArgs& a, int items, hipStream_t st) {
   GxArgs b = a;
   b.items = items;
-  gv_kernel<CLS, UP, FORM, KS, NW><<<(unsigned)((items + 7) / 8 * 8 * GvShape<CLS, UP, FORM, KS, NW>::RB), 64 * NW, 0, st>>>(b);
+  constexpr int RB = GvShape<CLS, UP, FORM, KS, NW>::RB;
+  const int nblk = FORM == GX_DENSE ? items * RB : (items + 7) / 8 * 8 * RB;
+  gv_kernel<CLS, UP, FORM, KS, NW><<<(unsigned)nblk, 64 * NW, 0, st>>>(b);
   return tlx_launch_status();
 }
 
