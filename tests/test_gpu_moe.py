@@ -437,13 +437,14 @@ def test_moe_pair_walk_with_shared_expert(gpu, experts, experts_tiled, P, lay):
 
 
 def test_moe_layer_overlapped_equals_sequential(gpu, experts):
-    """ops.moe_layer with the shared expert on a second stream gives the sequential calls'
-    results bit for bit, eagerly and in every replay of a captured graph (eager work and
-    synchronizations between the replays); at P = 11 with its defaults there (the pair walk, one
-    stream) and with the shared expert on the second stream beside the pair walk and beside the
-    sorted, grouped forms; at P = 300 with its defaults there (grouped, second stream)."""
-    print("[case] moe_layer overlapped vs sequential P=11 / 300", flush=True)
-    for P, pw, ov in ((11, None, None), (11, True, True), (11, False, True), (300, None, None)):
+    """ops.moe_layer gives the separate sequential calls' results bit for bit, eagerly and in every
+    replay of a captured graph (eager work and synchronizations between the replays): at P = 11
+    with its defaults (the pair walk with the shared expert inside its launches) and with the
+    shared expert on a second stream beside the pair walk and beside the sorted, grouped forms;
+    at P = 300 with its defaults (the grouped forms with the shared expert inside) and with the
+    shared expert on a second stream."""
+    print("[case] moe_layer routes vs sequential P=11 / 300", flush=True)
+    for P, pw, ov in ((11, None, None), (11, True, True), (11, False, True), (300, None, None), (300, None, True)):
         print(f"[case] moe_layer P={P} pair_walk={pw} overlap={ov}", flush=True)
         rng = np.random.default_rng(31 + P)
         x, logits, sg, hres = _inputs(rng, P)

@@ -255,3 +255,39 @@ def test_ckpt_layer(gpu, ckpt, P):
     yref = moe.combine_ref(pp, g, sg, shared, hres)
     scale = np.abs(hres) + np.einsum("pr,prk->pk", np.abs(g), np.abs(pp.astype(np.float64))) + np.abs(sg)[:, None] * np.abs(shared)
     assert np.all(np.abs(y.cpu().numpy() - yref) <= 4e-6 * scale + 1e-30)
+
+
+@pytest.mark.parametrize("P", [11, 300])
+def test_ckpt_layer_graph_replays(gpu, ckpt, P):
+    """ops.moe_layer_ckpt captured in a graph: every replay (eager work and synchronizations
+    between them) equals the eager layer bit for bit, with the shared expert in the routed
+    launches (P = 300) or its own (P = 11), and with it on a second stream."""
+    rng = np.random.default_rng(70 + P)
+    x = synth.bf16_round(0.05 * rng.standard_normal((P, moe.HID)).astype(np.float32))
+    dl = torch.from_numpy(rng.standard_normal((P, moe.E)).astype(np.float32)).to(gpu)
+    dsg = torch.from_numpy((1.0 / (1.0 + np.exp(-rng.standard_normal(P)))).astype(np.float32)).to(gpu)
+    dh = torch.from_numpy(rng.standard_normal((P, moe.HID)).astype(np.float32)).to(gpu)
+    dx = torch.from_numpy(x).to(gpu)
+    for ov in (None, True):
+        print(f"[case] checkpoint-class layer graph replays P={P} overlap={ov}", flush=True)
+        sc = ops.MoeScratch(P, gpu)
+        y = torch.empty(P, moe.HID, dtype=torch.float32, device=gpu)
+        args = (dl, dsg, dx, dh, y, ckpt["ptbl"], ckpt["ptbl_dn"], ckpt["dsh"], ckpt["gridf"], sc)
+        ops.moe_layer_ckpt(*args, overlap_shared=ov)
+        torch.cuda.synchronize()
+        ref = y.cpu().numpy().copy()
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            ops.moe_layer_ckpt(*args, stream=st, overlap_shared=ov)
+        torch.cuda.current_stream().wait_stream(st)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            ops.moe_layer_ckpt(*args, stream=st, overlap_shared=ov)
+        for _ in range(3):
+            y.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), ref.view(np.uint32))
