@@ -67,7 +67,7 @@ struct __attribute__((aligned(16))) PfLds {
       uint32_t tbl[4096 * 2];             // IQ3_XXS: sign-folded grid table, 4 fp16 per entry
       u4_t w[2][kBN * 4];                 // IQ3_XXS: packed7 units of one 128-k chunk: [group][r*4+c]
     };
-    u4_t kq[2][kWaves][4][TLX_WAVE];      // k-quants: two stages of each wave's 16-B weight pieces
+    u4_t kq[2][kWaves][5][TLX_WAVE];      // k-quants: two stages of each wave's 16-B weight pieces
   };
 };
 
@@ -199,7 +199,7 @@ __host__ __device__ constexpr int pf_block_bytes(int f) {
 // fields) the 48-B aligned covers of its 32 ql bytes and of its 32 qh bytes and the 32-B cover of
 // d and the scales (8).  Piece p of a wave's sub-block goes to slab byte 16 p (row p / P, piece
 // p % P); lanes past 32 P re-load the last piece.
-template <int FMT> constexpr int pf_kq_pieces() { return FMT == PF_Q4K ? 3 : FMT == PF_Q5K ? 5 : 8; }
+template <int FMT> constexpr int pf_kq_pieces() { return FMT == PF_Q4K ? 3 : FMT == PF_Q5K ? 5 : 10; }
 template <int FMT> constexpr int pf_kq_dmas() { return (32 * pf_kq_pieces<FMT>() + TLX_WAVE - 1) / TLX_WAVE; }
 
 // Byte offset from the row start of piece q (0 .. P-1) of sub-block j.
@@ -212,14 +212,15 @@ __device__ __forceinline__ uint32_t pf_kq_piece_off(int j, int q) {
   } else if constexpr (FMT == PF_Q5K) {
     return blk + (q < 3 ? 16u * (uint32_t)q : 16u * (uint32_t)q + 32u * (s >> 1));
   } else {
-    // ql bytes start at blk + 20 + 64 h' + 32 (g & 1), qh bytes at blk + 148 + 32 h': both 4 (b + 1)
-    // mod 16 past a 16-B boundary (blk = 212 b is 4 b mod 16); the header cover starts at blk rounded
-    // down.  A cover that starts on a boundary needs 2 pieces: its third re-loads the second.
-    const uint32_t hp = s >> 2, g = s & 3, m = 4u * ((b + 1u) & 3u), mh = 4u * (b & 3u);
-    const uint32_t need = m == 0 ? 2u : 3u;
-    if (q < 3) return blk + 20u + 64u * hp + 32u * (g & 1u) - m + 16u * min((uint32_t)q, need - 1u);
-    if (q < 6) return blk + 148u + 32u * hp - m + 16u * min((uint32_t)q - 3u, need - 1u);
-    return blk - mh + 16u * ((uint32_t)q - 6u);
+    // Q6_K is staged a half-block (128 weights = sub-blocks 4 h' .. 4 h' + 3, one 128-k chunk) at a
+    // time: its 64 ql bytes start at blk + 20 + 64 h', its 32 qh bytes at blk + 148 + 32 h', both
+    // 4 (b + 1) mod 16 past a 16-B boundary (blk = 212 b is 4 b mod 16); the header cover (d, the
+    // 16 scales) starts at blk rounded down.  Pieces 0-4: the ql cover, 5-7: the qh cover, 8-9: the
+    // header; a cover that starts on a boundary needs one piece fewer, which re-loads its last.
+    const uint32_t hp = s >> 2, m = 4u * ((b + 1u) & 3u), mh = 4u * (b & 3u);
+    if (q < 5) return blk + 20u + 64u * hp - m + 16u * min((uint32_t)q, m == 0 ? 3u : 4u);
+    if (q < 8) return blk + 148u + 32u * hp - m + 16u * min((uint32_t)q - 5u, m == 0 ? 1u : 2u);
+    return blk - mh + 16u * ((uint32_t)q - 8u);
   }
 }
 
@@ -258,16 +259,16 @@ __device__ __forceinline__ void pf_kq_read(PfKq& r, const PfLds& L, int stage, i
     r.hdr = *reinterpret_cast<const u4_t*>(cb);
     r.hb = *reinterpret_cast<const u4_t*>(cb + 16 + 16 * h);
     r.q = *reinterpret_cast<const u4_t*>(cb + 48 + 16 * h);
-  } else {
+  } else {   // the row's half-block slab: ql cover (80 B), qh cover (48 B), header cover (32 B)
     const uint32_t b = (uint32_t)(j >> 3), s = (uint32_t)(j & 7);
     const uint32_t m = 4u * ((b + 1u) & 3u), mh = 4u * (b & 3u);
-    const uint32_t* ql = reinterpret_cast<const uint32_t*>(cb + m + 16 * h);
-    const uint32_t* qh = reinterpret_cast<const uint32_t*>(cb + 48 + m + 16 * h);
+    const uint32_t* ql = reinterpret_cast<const uint32_t*>(cb + m + 32 * (s & 1) + 16 * h);
+    const uint32_t* qh = reinterpret_cast<const uint32_t*>(cb + 80 + m + 16 * h);
     r.q = u4_t{ql[0], ql[1], ql[2], ql[3]};
     r.hb = u4_t{qh[0], qh[1], qh[2], qh[3]};
-    r.hdr.x = *reinterpret_cast<const uint16_t*>(cb + 96 + mh + 2);
+    r.hdr.x = *reinterpret_cast<const uint16_t*>(cb + 128 + mh + 2);
     const uint32_t i = 8u * (s >> 2) + (uint32_t)h + 2u * (s & 3u);
-    r.sc = *reinterpret_cast<const uint32_t*>(cb + 96 + mh + 4 + (i & ~3u));
+    r.sc = *reinterpret_cast<const uint32_t*>(cb + 128 + mh + 4 + (i & ~3u));
   }
 }
 
@@ -363,10 +364,16 @@ __device__ __forceinline__ void pf_step(PfLds& L, f4_t (&acc)[kMI][8], const PfA
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Ring stage of sub-block j's pieces: Q4_K / Q5_K stage each sub-block (stage j % 2), Q6_K each
+// half-block (stage (j / 4) % 2)
+template <int FMT>
+__device__ __forceinline__ int pf_kq_stage(int j) { return FMT == PF_Q6P ? (j >> 2) & 1 : j & 1; }
+
 // One k-step of a k-quant segment: the operand loads of step t; the decode of sub-block t + 1
-// (staged at step t - 1: the two activation loads issued after it may still be in flight); the
-// weight pieces of sub-block t + 2 into the stage sub-block t used; the activations of step t + 2;
-// the MFMAs, which the scheduler interleaves with the decode; the barrier.
+// (staged at step t - 1 at the latest: the two activation loads issued after it may still be in
+// flight); the weight pieces of sub-block t + 2 into the stage sub-block t used (Q6_K: on the
+// steps before a half-block starts, its whole half-block into the other stage); the activations
+// of step t + 2; the MFMAs, which the scheduler interleaves with the decode; the barrier.
 template <int FMT>
 __device__ __forceinline__ void pf_kq_step(PfLds& L, f4_t (&acc)[kMI][8], const PfArgs& g, const int* bg, int aoff,
                                            int t, int ra, int wave, int wm, int lane) {
@@ -375,9 +382,15 @@ __device__ __forceinline__ void pf_kq_step(PfLds& L, f4_t (&acc)[kMI][8], const 
   const int j1 = min(t + 1, g.tlast);
   asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
   PfKq kr;
-  pf_kq_read<FMT>(kr, L, (t + 1) & 1, j1, wave, lane);
+  pf_kq_read<FMT>(kr, L, pf_kq_stage<FMT>(j1), j1, wave, lane);
   pf_kq_dequant<FMT>(kr, L.b[(t + 1) & 1], (int)threadIdx.x >> 1, j1, lane & 1);
-  pf_kq_dma<FMT>(L, t & 1, g.wkq, g.rowb, min(t + 2, g.tlast), wave, lane);
+  bool wdma = true;   // weight pieces issued this step (wave-uniform)
+  if constexpr (FMT == PF_Q6P) {
+    wdma = ((t + 2) & 3) == 0 && t + 2 <= g.tlast;
+    if (wdma) pf_kq_dma<FMT>(L, pf_kq_stage<FMT>(t + 2), g.wkq, g.rowb, t + 2, wave, lane);
+  } else {
+    pf_kq_dma<FMT>(L, t & 1, g.wkq, g.rowb, min(t + 2, g.tlast), wave, lane);
+  }
   const int ra2 = ra == 0 ? 2 : ra - 1;
   pf_dma_a(L.a[ra2], g.x, g.m0, g.K, min(t + 2, g.tlast), wave, lane);
   pf_mfma<0, kMI>(acc, f);
@@ -385,9 +398,16 @@ __device__ __forceinline__ void pf_kq_step(PfLds& L, f4_t (&acc)[kMI][8], const 
   // activations stay in flight
   __builtin_amdgcn_sched_barrier(0);
   static_assert(kLdW == 2, "the wait counts below assume 2 A loads per wave per step");
-  if constexpr (pf_kq_dmas<FMT>() == 2) asm volatile("s_waitcnt vmcnt(4)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else if constexpr (pf_kq_dmas<FMT>() == 3) asm volatile("s_waitcnt vmcnt(5)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(6)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (FMT == PF_Q6P) {
+    static_assert(pf_kq_dmas<FMT>() == 5, "Q6_K: 5 weight loads on a half-block step");
+    if (wdma) asm volatile("s_waitcnt vmcnt(7)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(2)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  } else if constexpr (pf_kq_dmas<FMT>() == 2) {
+    asm volatile("s_waitcnt vmcnt(4)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  } else {
+    static_assert(pf_kq_dmas<FMT>() == 3, "Q4_K / Q5_K: 2 or 3 weight loads a step");
+    asm volatile("s_waitcnt vmcnt(5)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
   __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -485,14 +505,18 @@ __device__ __forceinline__ void pf_tile(PfLds& L, const u4_t* __restrict__ w1, c
     // decoded (every segment starts on a 128-k chunk)
     g.rowb = (uint32_t)(pf_block_bytes(FMT) * (K >> 8));
     g.wkq = wkq + (size_t)(nt * kBN) * g.rowb;
-    pf_kq_dma<FMT>(L, s0 & 1, g.wkq, g.rowb, s0, wave, lane);
-    pf_kq_dma<FMT>(L, (s0 + 1) & 1, g.wkq, g.rowb, s0 + 1, wave, lane);
+    if constexpr (FMT == PF_Q6P) {   // the half-block of sub-blocks s0 .. s0 + 3
+      pf_kq_dma<FMT>(L, (s0 >> 2) & 1, g.wkq, g.rowb, s0, wave, lane);
+    } else {
+      pf_kq_dma<FMT>(L, s0 & 1, g.wkq, g.rowb, s0, wave, lane);
+      pf_kq_dma<FMT>(L, (s0 + 1) & 1, g.wkq, g.rowb, s0 + 1, wave, lane);
+    }
     pf_dma_a(L.a[0], x, g.m0, K, s0, wave, lane);
     pf_dma_a(L.a[1], x, g.m0, K, s0 + 1, wave, lane);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __syncthreads();
     PfKq kr;
-    pf_kq_read<FMT>(kr, L, s0 & 1, s0, wave, lane);
+    pf_kq_read<FMT>(kr, L, pf_kq_stage<FMT>(s0), s0, wave, lane);
     pf_kq_dequant<FMT>(kr, L.b[s0 & 1], threadIdx.x >> 1, s0, lane & 1);
     __syncthreads();
   }
