@@ -191,15 +191,17 @@ __host__ __device__ constexpr int pf_block_bytes(int f) {
   return f == PF_Q4K ? 144 : f == PF_Q5K ? 176 : f == PF_Q6P ? 212 : 128;
 }
 
-// K-quant weights reach the B tile through LDS: at step t each wave DMAs (16-B LDS-DMA loads, one
-// 1 KB slab per instruction) the aligned 16-B pieces that cover what its 32 tile rows need for
-// sub-block t + 2 into a two-stage ring; at step t + 1 the thread pair of each row decodes
-// sub-block t + 2 from there.  Pieces per row (P): Q4_K the 16-B header and the 32 qs bytes of the
-// sub-block pair (3); Q5_K the header, the 32 qh bytes and the 32 qs bytes (5); Q6_K (4-B aligned
-// fields) the 48-B aligned covers of its 32 ql bytes and of its 32 qh bytes and the 32-B cover of
-// d and the scales (8).  Piece p of a wave's sub-block goes to slab byte 16 p (row p / P, piece
-// p % P); lanes past 32 P re-load the last piece.
-template <int FMT> constexpr int pf_kq_pieces() { return FMT == PF_Q4K ? 3 : FMT == PF_Q5K ? 5 : 10; }
+// K-quant weights reach the B tile through LDS, a half-block (128 weights: sub-blocks 4h'..4h'+3,
+// one 128-k chunk) at a time: on the step before a half-block starts each wave DMAs (16-B LDS-DMA
+// loads, one 1 KB slab per instruction) the aligned 16-B pieces that cover what its 32 tile rows
+// need for it into one stage of a two-stage ring; on each step the thread pair of each row decodes
+// the next sub-block from there.  Pieces per row (P): Q4_K the 16-B header and the half-block's
+// 64 qs bytes (5); Q5_K the header, the 32 qh bytes and the 64 qs bytes (7); Q6_K (4-B aligned
+// fields) the 80-B cover of its 64 ql bytes, the 48-B cover of its 32 qh bytes and the 32-B cover
+// of d and the scales (10).  Staged per sub-block instead, the header (and Q5_K's qh bytes, Q6_K's
+// shared ql / qh bytes) moved 2-4 times per half-block.  Piece p of a wave's half-block goes to
+// slab byte 16 p (row p / P, piece p % P); lanes past 32 P re-load the last piece.
+template <int FMT> constexpr int pf_kq_pieces() { return FMT == PF_Q4K ? 5 : FMT == PF_Q5K ? 7 : 10; }
 template <int FMT> constexpr int pf_kq_dmas() { return (32 * pf_kq_pieces<FMT>() + TLX_WAVE - 1) / TLX_WAVE; }
 
 // Byte offset from the row start of piece q (0 .. P-1) of sub-block j.
@@ -207,10 +209,10 @@ template <int FMT>
 __device__ __forceinline__ uint32_t pf_kq_piece_off(int j, int q) {
   const uint32_t b = (uint32_t)(j >> 3), s = (uint32_t)(j & 7);
   const uint32_t blk = (uint32_t)pf_block_bytes(FMT) * b;
-  if constexpr (FMT == PF_Q4K) {
-    return blk + (q == 0 ? 0u : 16u * (uint32_t)q + 32u * (s >> 1));
-  } else if constexpr (FMT == PF_Q5K) {
-    return blk + (q < 3 ? 16u * (uint32_t)q : 16u * (uint32_t)q + 32u * (s >> 1));
+  if constexpr (FMT == PF_Q4K) {   // header, then the half-block's 64 qs bytes
+    return blk + (q == 0 ? 0u : 16u * (uint32_t)q + 64u * (s >> 2));
+  } else if constexpr (FMT == PF_Q5K) {   // header, the 32 qh bytes, then the half-block's 64 qs bytes
+    return blk + (q < 3 ? 16u * (uint32_t)q : 16u * (uint32_t)q + 64u * (s >> 2));
   } else {
     // Q6_K is staged a half-block (128 weights = sub-blocks 4 h' .. 4 h' + 3, one 128-k chunk) at a
     // time: its 64 ql bytes start at blk + 20 + 64 h', its 32 qh bytes at blk + 148 + 32 h', both
@@ -252,13 +254,13 @@ __device__ __forceinline__ void pf_kq_read(PfKq& r, const PfLds& L, int stage, i
   constexpr int P = pf_kq_pieces<FMT>();
   const int h = lane & 1;
   const uint8_t* cb = reinterpret_cast<const uint8_t*>(&L.kq[stage][wave][0][0]) + 16 * P * (lane >> 1);
-  if constexpr (FMT == PF_Q4K) {
+  if constexpr (FMT == PF_Q4K) {   // sub-block j's pair (j & 7) / 2 of the half-block's two
     r.hdr = *reinterpret_cast<const u4_t*>(cb);
-    r.q = *reinterpret_cast<const u4_t*>(cb + 16 + 16 * h);
+    r.q = *reinterpret_cast<const u4_t*>(cb + 16 + 32 * ((j >> 1) & 1) + 16 * h);
   } else if constexpr (FMT == PF_Q5K) {
     r.hdr = *reinterpret_cast<const u4_t*>(cb);
     r.hb = *reinterpret_cast<const u4_t*>(cb + 16 + 16 * h);
-    r.q = *reinterpret_cast<const u4_t*>(cb + 48 + 16 * h);
+    r.q = *reinterpret_cast<const u4_t*>(cb + 48 + 32 * ((j >> 1) & 1) + 16 * h);
   } else {   // the row's half-block slab: ql cover (80 B), qh cover (48 B), header cover (32 B)
     const uint32_t b = (uint32_t)(j >> 3), s = (uint32_t)(j & 7);
     const uint32_t m = 4u * ((b + 1u) & 3u), mh = 4u * (b & 3u);
@@ -364,16 +366,15 @@ __device__ __forceinline__ void pf_step(PfLds& L, f4_t (&acc)[kMI][8], const PfA
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Ring stage of sub-block j's pieces: Q4_K / Q5_K stage each sub-block (stage j % 2), Q6_K each
-// half-block (stage (j / 4) % 2)
+// Ring stage of sub-block j's pieces: each half-block (128 k) has a stage, alternating
 template <int FMT>
-__device__ __forceinline__ int pf_kq_stage(int j) { return FMT == PF_Q6P ? (j >> 2) & 1 : j & 1; }
+__device__ __forceinline__ int pf_kq_stage(int j) { return (j >> 2) & 1; }
 
 // One k-step of a k-quant segment: the operand loads of step t; the decode of sub-block t + 1
 // (staged at step t - 1 at the latest: the two activation loads issued after it may still be in
-// flight); the weight pieces of sub-block t + 2 into the stage sub-block t used (Q6_K: on the
-// steps before a half-block starts, its whole half-block into the other stage); the activations
-// of step t + 2; the MFMAs, which the scheduler interleaves with the decode; the barrier.
+// flight); on the step before a half-block starts (t + 2 = 0 mod 4), that half-block's pieces
+// into the other stage; the activations of step t + 2; the MFMAs, which the scheduler
+// interleaves with the decode; the barrier.
 template <int FMT>
 __device__ __forceinline__ void pf_kq_step(PfLds& L, f4_t (&acc)[kMI][8], const PfArgs& g, const int* bg, int aoff,
                                            int t, int ra, int wave, int wm, int lane) {
@@ -384,13 +385,8 @@ __device__ __forceinline__ void pf_kq_step(PfLds& L, f4_t (&acc)[kMI][8], const 
   PfKq kr;
   pf_kq_read<FMT>(kr, L, pf_kq_stage<FMT>(j1), j1, wave, lane);
   pf_kq_dequant<FMT>(kr, L.b[(t + 1) & 1], (int)threadIdx.x >> 1, j1, lane & 1);
-  bool wdma = true;   // weight pieces issued this step (wave-uniform)
-  if constexpr (FMT == PF_Q6P) {
-    wdma = ((t + 2) & 3) == 0 && t + 2 <= g.tlast;
-    if (wdma) pf_kq_dma<FMT>(L, pf_kq_stage<FMT>(t + 2), g.wkq, g.rowb, t + 2, wave, lane);
-  } else {
-    pf_kq_dma<FMT>(L, t & 1, g.wkq, g.rowb, min(t + 2, g.tlast), wave, lane);
-  }
+  const bool wdma = ((t + 2) & 3) == 0 && t + 2 <= g.tlast;   // weight pieces this step (wave-uniform)
+  if (wdma) pf_kq_dma<FMT>(L, pf_kq_stage<FMT>(t + 2), g.wkq, g.rowb, t + 2, wave, lane);
   const int ra2 = ra == 0 ? 2 : ra - 1;
   pf_dma_a(L.a[ra2], g.x, g.m0, g.K, min(t + 2, g.tlast), wave, lane);
   pf_mfma<0, kMI>(acc, f);
@@ -398,15 +394,15 @@ __device__ __forceinline__ void pf_kq_step(PfLds& L, f4_t (&acc)[kMI][8], const 
   // activations stay in flight
   __builtin_amdgcn_sched_barrier(0);
   static_assert(kLdW == 2, "the wait counts below assume 2 A loads per wave per step");
-  if constexpr (FMT == PF_Q6P) {
-    static_assert(pf_kq_dmas<FMT>() == 5, "Q6_K: 5 weight loads on a half-block step");
-    if (wdma) asm volatile("s_waitcnt vmcnt(7)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(2)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  } else if constexpr (pf_kq_dmas<FMT>() == 2) {
-    asm volatile("s_waitcnt vmcnt(4)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  } else {
-    static_assert(pf_kq_dmas<FMT>() == 3, "Q4_K / Q5_K: 2 or 3 weight loads a step");
+  if (!wdma) {
+    asm volatile("s_waitcnt vmcnt(2)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  } else if constexpr (pf_kq_dmas<FMT>() == 3) {   // Q4_K
     asm volatile("s_waitcnt vmcnt(5)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  } else if constexpr (pf_kq_dmas<FMT>() == 4) {   // Q5_K
+    asm volatile("s_waitcnt vmcnt(6)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  } else {
+    static_assert(pf_kq_dmas<FMT>() == 5, "Q6_K: 5 weight loads on a half-block step");
+    asm volatile("s_waitcnt vmcnt(7)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -505,12 +501,7 @@ __device__ __forceinline__ void pf_tile(PfLds& L, const u4_t* __restrict__ w1, c
     // decoded (every segment starts on a 128-k chunk)
     g.rowb = (uint32_t)(pf_block_bytes(FMT) * (K >> 8));
     g.wkq = wkq + (size_t)(nt * kBN) * g.rowb;
-    if constexpr (FMT == PF_Q6P) {   // the half-block of sub-blocks s0 .. s0 + 3
-      pf_kq_dma<FMT>(L, (s0 >> 2) & 1, g.wkq, g.rowb, s0, wave, lane);
-    } else {
-      pf_kq_dma<FMT>(L, s0 & 1, g.wkq, g.rowb, s0, wave, lane);
-      pf_kq_dma<FMT>(L, (s0 + 1) & 1, g.wkq, g.rowb, s0 + 1, wave, lane);
-    }
+    pf_kq_dma<FMT>(L, pf_kq_stage<FMT>(s0), g.wkq, g.rowb, s0, wave, lane);   // the half-block of s0 .. s0 + 3
     pf_dma_a(L.a[0], x, g.m0, K, s0, wave, lane);
     pf_dma_a(L.a[1], x, g.m0, K, s0 + 1, wave, lane);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
