@@ -93,9 +93,9 @@ TRAFFIC = {
     "gemm_ffn_m8192": 3_557_484_339,    # pf_gemm<FFN> (no split tiles): F 1,597,788.9  W 278,528
     "gemm_down_m8192": 1_753_614_131,   # pf_gemm<RES> + pf_fix: F 692,386.6 + 49,180.0  W 196,611.9 + 32,768.7
     "w4a8_ffn_m2048": 1_595_100_365,    # p8_quant + p8w4_ffn: F 10,256 + 728,025.6  W 11,520 + 69,632
-    "merged_attnqkv_i3": 398_648_115,   # pfm_gemm_kernel: F 165,769.0  W 57,344
-    "merged_attnqkv_q6": 652_394_086,   # pfm_gemm_kernel: F 399,043.4  W 57,344
-    "merged_gdnqg": 542_371_430,        # pfm_gemm_kernel: F 244,672.0  W 65,536
+    "merged_attnqkv_i3": 398_648_115,   # pfm_gemm_kernel: F 165,980.4  W 57,344
+    "merged_attnqkv_q6": 652_394_086,   # pfm_gemm_kernel: F 289,879.8  W 57,344
+    "merged_gdnqg": 542_371_430,        # pfm_gemm_kernel: F 232,061.8  W 65,536
     "moe_m11": 153_883_750,             # topk + pair-walk gate+up and down (shared inside) + combine: F 74,775.3  W 726.5
     "moe_m2048": 863_987_917,           # topk, sort, grouped gate+up / down with the shared expert, combine: F 354,038.1  W 135,662.0
     "ckpt_m11": 161_291_981,            # checkpoint classes: topk, pair-walk IQ3_S up / Q6_K down, Q8_0 shared two, combine: F 78,392.6  W 726.5
