@@ -35,4 +35,6 @@ def within_one_ulp(got16, ideal):
     up = np.nextafter(r16, np.float16(np.inf)).astype(np.float64)
     dn = np.nextafter(r16, np.float16(-np.inf)).astype(np.float64)
     r = r16.astype(np.float64)
-    return (got == r) | (got == up) | (got == dn)
+    ideal = np.asarray(ideal, dtype=np.float64)
+    side = np.where(ideal > r, up, np.where(ideal < r, dn, r))   # the neighbour toward the ideal
+    return (got == r) | (got == side)

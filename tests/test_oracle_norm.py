@@ -35,3 +35,18 @@ def test_scale_invariance_and_add():
     hh, ideal, _ = norm.add_rms_ref(x, att, nw)
     assert np.array_equal(hh, x + att.astype(np.float32))
     assert np.allclose(ideal, norm.rms_ref(hh, nw)[0], rtol=0, atol=0)
+
+
+def test_within_one_ulp_accepts_only_the_ideal_side():
+    """The fp16 check the producer tests use: the rounded ideal, or its neighbour on the ideal's
+    side (an fp32 chain can cross that midpoint only); the other neighbour and 2 ulps fail."""
+    ideal = np.array([1.0 + 0.3 * 2.0 ** -10, 1.0 - 0.3 * 2.0 ** -11, 3.0, -2.0 - 0.4 * 2.0 ** -9])
+    r = ideal.astype(np.float16)
+    up = np.nextafter(r, np.float16(np.inf))
+    dn = np.nextafter(r, np.float16(-np.inf))
+    toward = np.where(ideal > r.astype(np.float64), up, dn)
+    away = np.where(ideal > r.astype(np.float64), dn, up)
+    assert norm.within_one_ulp(r, ideal).all()
+    assert list(norm.within_one_ulp(toward, ideal)) == [True, True, False, True]   # 3.0 is exact
+    assert not norm.within_one_ulp(away, ideal).any()
+    assert not norm.within_one_ulp(np.nextafter(toward, toward + (toward - r)), ideal).any()
