@@ -52,6 +52,13 @@ __device__ __forceinline__ uint32_t tlx_mix2_f16(float s, uint32_t h2) {
   return r;
 }
 
+// An MFMA does not wait for a VALU result in its source registers: 2 wait states must separate the
+// write and the read, and the compiler inserts none after inline asm it does not look into (such as
+// the v_fma_mix above).  An operand built by tlx_mix2_f16 and read by an MFMA directly passes
+// through this guard first: its nops sit after the operand's last write (the asm takes the operand
+// as an input) and before the MFMA (which takes it as an output).
+__device__ __forceinline__ void tlx_mfma_operand_guard(u4_t& h) { asm volatile("s_nop 2" : "+v"(h)); }
+
 // fp16 pair of bytes {0, 1} (hi = 0) or {2, 3} (hi = 1) of v as the integers byte - bias: v_perm
 // puts 0x64 above each byte (the fp16 1024 + byte, exact), a packed fp16 add takes 1024 + bias off
 // (exact: small integers).

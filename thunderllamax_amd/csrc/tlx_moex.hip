@@ -483,6 +483,7 @@ __device__ __forceinline__ h8_t gv_decode(const GvRaw<CLS>& r, int kq, const GvL
     const uint2 g1 = lut->grid[((qsw >> 8) & 255u) | ((qh & 2u) << 7)];
     const uint32_t sb = (S < 4 ? r.sg0 : r.sg1) >> (8 * (S & 3));
     const uint2 m0 = lut->smask[sb & 15u], m1 = lut->smask[(sb >> 4) & 15u];
+    // (each word's last write is the sign XOR, an instruction the compiler sees: no guard needed)
     const u4_t h = {tlx_mix2_f16(db, g0.x) ^ m0.x, tlx_mix2_f16(db, g0.y) ^ m0.y, tlx_mix2_f16(db, g1.x) ^ m1.x, tlx_mix2_f16(db, g1.y) ^ m1.y};
     return __builtin_bit_cast(h8_t, h);
   } else if constexpr (CLS == GX_Q6K) {
@@ -498,6 +499,7 @@ __device__ __forceinline__ h8_t gv_decode(const GvRaw<CLS>& r, int kq, const GvL
       h[2 * j] = tlx_mix2_f16(t, tlx_bytes_h2(q4, 0, 32.f));       // t * (q - 32)
       h[2 * j + 1] = tlx_mix2_f16(t, tlx_bytes_h2(q4, 1, 32.f));
     }
+    tlx_mfma_operand_guard(h);
     return __builtin_bit_cast(h8_t, h);
   } else {
     constexpr int blk = S >> 2, q = S & 3;
@@ -510,6 +512,7 @@ __device__ __forceinline__ h8_t gv_decode(const GvRaw<CLS>& r, int kq, const GvL
       h[2 * j] = tlx_mix2_f16(d, tlx_bytes_h2(u4, 0, 128.f));
       h[2 * j + 1] = tlx_mix2_f16(d, tlx_bytes_h2(u4, 1, 128.f));
     }
+    tlx_mfma_operand_guard(h);
     return __builtin_bit_cast(h8_t, h);
   }
 }
@@ -653,6 +656,170 @@ int gv_launch(const GxArgs& a, int items, hipStream_t st) {
   return tlx_launch_status();
 }
 
+// ------------------------------------------------------------------ batched down, register decode
+// Down projections of batches (an expert's sorted pairs, or a chunk of positions for the shared
+// expert) with the item's activations resident in LDS: a workgroup stages up to kGqTok token rows
+// of act as fp16 once per pass, then its 8 waves walk 2048 / RB weight rows of the item in 16-row
+// tiles (a contiguous run of tiles a wave).  Each lane fetches the bytes of its 64 weights of a
+// 256-weight unit straight into registers (gv_fetch, DEPTH units ahead) and builds each k-step's 8
+// operands there (gv_decode: the other forms' operands bit for bit); every operand feeds all of the
+// pass's 16-token groups.  The weights are the MFMA's first operand, so a lane's four outputs are
+// four consecutive rows of one token: one 8-B (fp16 parts) or 16-B (f32) store.
+constexpr int kGqTok = 128;
+constexpr int kGqLdx = kFf + 8;   // token row stride (halfs): a fragment's 16 rows fall in distinct banks
+
+struct alignas(16) GqLds {
+  _Float16 x[kGqTok * kGqLdx];
+  int orow[kGqTok];
+};
+
+template <int CLS> constexpr int gq_unit_bytes() { return CLS == GX_Q80 ? 8 * 34 : GxFmt<CLS>::kBlk; }
+
+// The wave's tiles for one pass of NG token groups: per unit, 8 k-steps of one decoded operand
+// and NG MFMAs; the next unit's bytes into the freed ring slot; a tile's outputs after its last unit.
+template <int CLS, int FORM, int NU, int UNITS, int DEPTH, int NG, typename F>
+__device__ __forceinline__ void gq_tiles(const GqLds& L, const GxArgs& a, GvRaw<CLS> (&raw)[DEPTH], F& fetch,
+                                         int tile0, int nt, int col, int kq) {
+  const _Float16* xl = L.x + col * kGqLdx;   // token row 16 g + col: + 16 g kGqLdx
+  f4_t acc[NG];
+  for (int q0 = 0; q0 < UNITS; q0 += DEPTH) {
+#pragma unroll
+    for (int r = 0; r < DEPTH; ++r) {
+      const int q = q0 + r;
+      if (r % NU == 0) {   // DEPTH % NU == 0: unit r % NU of tile q / NU
+#pragma unroll
+        for (int g = 0; g < NG; ++g) acc[g] = f4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      const _Float16* xu = xl + 256 * (r % NU);
+#define GQ_STEP(SS)                                                                                  \
+  {                                                                                                  \
+    const h8_t bw = gv_decode<CLS, SS>(raw[r], kq, nullptr);                                         \
+    _Pragma("unroll") for (int g = 0; g < NG; ++g) {                                                 \
+      const h8_t ax = *reinterpret_cast<const h8_t*>(xu + 16 * g * kGqLdx + gv_koff<CLS>(kq, SS));   \
+      acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bw, ax, acc[g], 0, 0, 0);                      \
+    }                                                                                                \
+  }
+      GQ_STEP(0) GQ_STEP(1) GQ_STEP(2) GQ_STEP(3) GQ_STEP(4) GQ_STEP(5) GQ_STEP(6) GQ_STEP(7)
+#undef GQ_STEP
+      raw[r] = fetch(min(q + DEPTH, UNITS - 1));   // past the end: the last unit again
+      if (r % NU == NU - 1) {
+        // lane (col, kq) holds rows 4 kq .. 4 kq + 3 of the tile for token 16 g + col
+        const int n0 = 16 * (tile0 + q / NU) + 4 * kq;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const int tk = 16 * g + col;
+          if (tk < nt) {
+            const size_t o = (size_t)L.orow[tk] * kHid + n0;
+            if constexpr (FORM == GX_DENSE) {
+              *reinterpret_cast<f4_t*>(reinterpret_cast<float*>(a.out) + o) = acc[g];
+            } else {
+              const h2_t lo = {(_Float16)acc[g][0], (_Float16)acc[g][1]};
+              const h2_t hi = {(_Float16)acc[g][2], (_Float16)acc[g][3]};
+              *reinterpret_cast<uint2*>(reinterpret_cast<_Float16*>(a.out) + o) =
+                  uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// blk: the workgroup's index in its part of the grid (parts start at multiples of 8)
+template <int CLS, int FORM, int RB, int DEPTH>
+__device__ __forceinline__ void gq_dn_body(GqLds& L, const GxArgs& a, int blk) {
+  constexpr int K = kFf, NU = K / 256, NW = 8;
+  constexpr int ROWB = NU * gq_unit_bytes<CLS>();
+  constexpr int TILES = kHid / 16 / RB, TPW = TILES / NW, UNITS = TPW * NU;
+  static_assert(TILES % NW == 0 && UNITS % DEPTH == 0 && DEPTH % NU == 0, "tiling");
+  static_assert(FORM != GX_PAIRS, "the pair walk is gv_kernel's");
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 15, kq = lane >> 4;
+  // an item's RB workgroups on one XCD (block b runs on XCD b % 8): its act rows come from HBM once
+  const int slot = blk >> 3;
+  const int rb = slot % RB, item = slot / RB * 8 + (blk & 7);
+  if (item >= a.items) return;
+  int beg, ntot;
+  gbyte* w;
+  if constexpr (FORM == GX_SORTED) {
+    beg = a.eoff[item];
+    ntot = a.eoff[item + 1] - beg;
+    w = reinterpret_cast<gbyte*>(a.ptbl[item]);
+  } else {
+    beg = item * kGqTok;
+    ntot = min(kGqTok, a.P - beg);
+    w = (gbyte*)a.w0;
+  }
+  if (ntot <= 0) return;   // uniform per workgroup
+  const int tile0 = rb * TILES + wave * TPW;
+  gbyte* wrow = w + (size_t)(16 * tile0 + col) * ROWB;   // the lane's row in the wave's first tile
+  auto fetch = [&](int q) { return gv_fetch<CLS>(wrow + (size_t)(16 * (q / NU)) * ROWB, q % NU, kq); };
+
+  for (int p0 = 0; p0 < ntot; p0 += kGqTok) {
+    const int nt = min(kGqTok, ntot - p0), ng = (nt + 15) >> 4;
+    // the first units' loads do not depend on the staging: issued first
+    GvRaw<CLS> raw[DEPTH];
+#pragma unroll
+    for (int r = 0; r < DEPTH; ++r) raw[r] = fetch(r);
+    __syncthreads();   // the previous pass is done with the rows
+    if (t < nt) L.orow[t] = FORM == GX_SORTED ? (int)a.plist[beg + p0 + t] : beg + p0 + t;
+    __syncthreads();
+    // the pass's token rows as fp16 (round to nearest even); rows nt .. 16 ng - 1 zero.  Thread t
+    // converts k-piece t % 64 of rows t / 64 + 8 j, four rows' loads in flight at a time.
+    {
+      const int k8 = t & 63, r0 = t >> 6;
+      for (int j0 = 0; j0 < 2 * ng; j0 += 4) {
+        float4 v[4][2];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = r0 + 8 * (j0 + j);
+          const int xr = r < nt ? L.orow[r] : 0;
+          const float4* src = reinterpret_cast<const float4*>(a.x + (size_t)xr * K + 8 * k8);
+          v[j][0] = src[0];
+          v[j][1] = src[1];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = r0 + 8 * (j0 + j);
+          if (r < 16 * ng) {
+            const bool z = r >= nt;
+            const float4 u = z ? float4{0.f, 0.f, 0.f, 0.f} : v[j][0], s = z ? float4{0.f, 0.f, 0.f, 0.f} : v[j][1];
+            const h8_t h = {(_Float16)u.x, (_Float16)u.y, (_Float16)u.z, (_Float16)u.w,
+                            (_Float16)s.x, (_Float16)s.y, (_Float16)s.z, (_Float16)s.w};
+            *reinterpret_cast<h8_t*>(L.x + r * kGqLdx + 8 * k8) = h;
+          }
+        }
+      }
+    }
+    __syncthreads();
+
+    // the tile walk, specialized on the pass's group count (no branch around a load or an MFMA)
+    switch (ng) {
+      case 1: gq_tiles<CLS, FORM, NU, UNITS, DEPTH, 1>(L, a, raw, fetch, tile0, nt, col, kq); break;
+      case 2: gq_tiles<CLS, FORM, NU, UNITS, DEPTH, 2>(L, a, raw, fetch, tile0, nt, col, kq); break;
+      case 3: gq_tiles<CLS, FORM, NU, UNITS, DEPTH, 3>(L, a, raw, fetch, tile0, nt, col, kq); break;
+      case 4: gq_tiles<CLS, FORM, NU, UNITS, DEPTH, 4>(L, a, raw, fetch, tile0, nt, col, kq); break;
+      case 5: gq_tiles<CLS, FORM, NU, UNITS, DEPTH, 5>(L, a, raw, fetch, tile0, nt, col, kq); break;
+      case 6: gq_tiles<CLS, FORM, NU, UNITS, DEPTH, 6>(L, a, raw, fetch, tile0, nt, col, kq); break;
+      case 7: gq_tiles<CLS, FORM, NU, UNITS, DEPTH, 7>(L, a, raw, fetch, tile0, nt, col, kq); break;
+      default: gq_tiles<CLS, FORM, NU, UNITS, DEPTH, 8>(L, a, raw, fetch, tile0, nt, col, kq); break;
+    }
+  }
+}
+
+template <int CLS, int FORM, int RB, int DEPTH>
+__global__ __launch_bounds__(512) void gq_dn_kernel(const GxArgs a) {
+  __shared__ GqLds L;
+  gq_dn_body<CLS, FORM, RB, DEPTH>(L, a, (int)blockIdx.x);
+}
+
+#ifndef GQ_RRB
+#define GQ_RRB 1
+#endif
+#ifndef GQ_DEPTH
+#define GQ_DEPTH 2
+#endif
+constexpr int kGqRrb = GQ_RRB, kGqDepth = GQ_DEPTH;
+
 // ------------------------------------------------------------------ dequantizers (bit-exact)
 // One thread per (row, 16-weight piece).
 template <int CLS>
@@ -744,6 +911,17 @@ extern "C" int tlx_moe_up3s_pairs(const uint64_t* ptbl, const uint16_t* eids, co
   return gv_launch<GX_IQ3S, true, GX_PAIRS, 4, 4>(a, np, (hipStream_t)stream);
 }
 
+// the routed Q6_K down over the sorted pairs: the register-decode form (8-B stores a lane), else the
+// LDS-staged one
+static int dn6_sorted(GxArgs a, hipStream_t st) {
+  a.items = kE;
+  if (tlx_aligned(a.out, 8)) {
+    gq_dn_kernel<GX_Q6K, GX_SORTED, kGqRrb, kGqDepth><<<(unsigned)((kE + 7) / 8 * 8 * kGqRrb), 512, 0, st>>>(a);
+    return tlx_launch_status();
+  }
+  return gx_launch<GX_Q6K, false, GX_SORTED>(a, kE, st);
+}
+
 extern "C" int tlx_moe_dn6(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
                            const uint16_t* plist, const float* act, uint16_t* parts, int np, void* stream) {
   (void)items;   // the reference's slots; this form walks eoff / plist itself
@@ -753,7 +931,7 @@ extern "C" int tlx_moe_dn6(const uint64_t* ptbl_dn, const uint32_t* items, const
   TLX_RET_IF(!tlx_aligned(ptbl_dn, 8) || !tlx_aligned(act, 16) || !tlx_aligned(parts, 2), TLX_E_ALIGN);
   GxArgs a{};
   a.ptbl = ptbl_dn; a.eoff = eoff; a.plist = plist; a.x = act; a.out = parts;
-  return gx_launch<GX_Q6K, false, GX_SORTED>(a, kE, (hipStream_t)stream);
+  return dn6_sorted(a, (hipStream_t)stream);
 }
 
 extern "C" int tlx_moe_dn6_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, uint16_t* parts,
@@ -827,7 +1005,14 @@ extern "C" int tlx_moe_dn6_sh(const uint64_t* ptbl_dn, const uint32_t* items, co
   GxArgs a{};
   a.ptbl = ptbl_dn; a.eoff = eoff; a.plist = plist; a.x = act; a.out = parts;
   if (P <= kGvTok) {
-    const int rc = gx_launch<GX_Q6K, false, GX_SORTED>(a, kE, st);
+    const int rc = dn6_sorted(a, st);
+    TLX_RET_IF(rc != TLX_OK, rc);
+    return moe_shared8_dn(wd8, sact, shared, P, st);
+  }
+  if (tlx_aligned(parts, 8)) {
+    // the routed register-decode form and the shared expert's staged form: two launches (their LDS
+    // footprints differ: in one launch the shared part would run at one workgroup per CU)
+    const int rc = dn6_sorted(a, st);
     TLX_RET_IF(rc != TLX_OK, rc);
     return moe_shared8_dn(wd8, sact, shared, P, st);
   }
