@@ -99,7 +99,7 @@ TRAFFIC = {
     "moe_m11": 153_883_750,             # topk + pair-walk gate+up and down (shared inside) + combine: F 74,775.3  W 726.5
     "moe_m2048": 863_987_917,           # topk, sort, grouped gate+up / down with the shared expert, combine: F 354,038.1  W 135,662.0
     "ckpt_m11": 161_291_981,            # checkpoint classes: topk, pair-walk IQ3_S up / Q6_K down, Q8_0 shared two, combine: F 78,392.6  W 726.5
-    "ckpt_m2048": 933_744_128,          # checkpoint classes: topk, sort, sorted up / down with the shared expert, combine: F 388,178.3  W 135,502.9
+    "ckpt_m2048": 959_237_530,          # checkpoint classes: topk, sort, sorted up with the shared expert, register-decode down, shared down, combine: F 388,133.1  W 160,466.9
     "sweep": 12_030_388_122,            # one decode step: F 5,591,363.3  W 565,699.3
 }
 PEAK_F16_TFLOPS = 2500.0

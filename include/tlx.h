@@ -465,8 +465,10 @@ int tlx_moe_dn6_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float
                       int np, void* stream);
 /* The sorted forms (tlx_moe_up3s / tlx_moe_dn6) and the Q8_0 shared expert's gate+up / down
  * (tlx_moe_shared8's two launches) in one launch each above P = 16 (else the two launches): the
- * shared expert's workgroups follow the routed ones.  No counterpart in the reference (gxu_gm /
- * gxm_dn6 and shexp8 are separate launches); outputs those of the separate calls bit for bit.
+ * shared expert's workgroups follow the routed ones.  The down keeps two launches whenever parts
+ * is 8-B aligned (the routed register-decode form and the shared expert's staged form have LDS
+ * footprints one launch cannot share).  No counterpart in the reference (gxu_gm / gxm_dn6 and
+ * shexp8 are separate launches); outputs those of the separate calls bit for bit.
  * sact f32 [P][512] (16-B aligned) and shared f32 [P][2048] as tlx_moe_shared8's act / y. */
 int tlx_moe_up3s_sh(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const float* xs,
                     const float* gridf, float* ys, int np, const void* wg8, const void* wu8, float* sact, int P,

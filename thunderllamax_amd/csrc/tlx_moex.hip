@@ -9,17 +9,19 @@
 // ptbl_dn[e] -- 2048 rows of 420 B (2 raw 210-B blocks, k = 512); the shared expert's Q8_0 gate and
 // up rows (512 x 2176 B, k = 2048) and down rows (2048 x 544 B, k = 512).
 //
-// Two kernels.  gx_kernel (batches): a workgroup owns 16 output columns per wave of one expert --
-// gate+up: 4 waves, 64 gate rows and the matching 64 up rows, so the SwiGLU pairs meet in one
-// lane; down: 8 waves, 128 rows -- and the token rows a pass at a time (128 sorted, 64 dense).  K
-// runs in chunks of 64: the pass's activations (f32 -> fp16, round to nearest even) and the column
-// block's weight rows, dequantized
-// to the reference's operands -- fp16 of the fp32 GGUF value, as gxu_gm stages them -- go to LDS
+// Three kernels.  gx_kernel (batches: gate+up, the shared expert's down, and the routed down where
+// parts is not 8-B aligned): a workgroup owns 16 output columns per wave of one expert -- gate+up:
+// 4 waves, 64 gate rows and the matching 64 up rows, so the SwiGLU pairs meet in one lane; down: 8
+// waves, 128 rows -- and the token rows a pass at a time (128 sorted, 64 dense).  K runs in chunks
+// of 64: the pass's activations (f32 -> fp16, round to nearest even) and the column block's weight
+// rows, dequantized to the reference's operands -- fp16 of the fp32 GGUF value, as gxu_gm stages them -- go to LDS
 // (rows padded to 72 halfs: the 16 rows of a fragment read fall in distinct 16-B slots); then wave
 // w runs v_mfma_f32_16x16x32_f16 over its 16 columns for every 16-token group of the pass.  Token
 // lists: sorted (the expert's bin from eoff / plist, in passes of 128) or dense (every position:
 // the shared expert).  gv_kernel (decode: the pair walk, one pair per item, pair p running expert
 // eids[p]; the shared expert at P <= 16): the same operands, built in registers (its section).
+// gq_dn_kernel (the routed down over the sorted pairs): gv_kernel's register-built operands with
+// the expert's activations resident in LDS (its section).
 //
 // IQ3_S's 512-entry grid is a run-time argument (float[512][4]), as in the reference.
 #include "tlx_common.h"
