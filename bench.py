@@ -98,8 +98,8 @@ TRAFFIC = {
     "merged_gdnqg": 542_371_430,        # pfm_gemm_kernel: F 232,061.8  W 65,536
     "moe_m11": 153_883_750,             # topk + pair-walk gate+up and down (shared inside) + combine: F 74,775.3  W 726.5
     "moe_m2048": 863_987_917,           # topk, sort, grouped gate+up / down with the shared expert, combine: F 354,038.1  W 135,662.0
-    "ckpt_m11": 161_291_981,            # checkpoint classes: topk, pair-walk IQ3_S up / Q6_K down, Q8_0 shared two, combine: F 78,392.6  W 726.5
-    "ckpt_m2048": 959_237_530,          # checkpoint classes: topk, sort, sorted up with the shared expert, register-decode down, shared down, combine: F 388,133.1  W 160,466.9
+    "ckpt_m11": 162_036_224,            # checkpoint classes, tiled slabs: topk, pair-walk IQ3_S up / Q6_K down, Q8_0 shared two, combine: F 78,755.9  W 726.6
+    "ckpt_m2048": 940_513_792,          # checkpoint classes, tiled slabs: topk, sort, sorted up with the shared expert, register-decode down, shared down, combine: F 371,744.2  W 174,973.3
     "sweep": 12_030_388_122,            # one decode step: F 5,591,363.3  W 565,699.3
 }
 PEAK_F16_TFLOPS = 2500.0
@@ -458,16 +458,23 @@ def moe_ckpt_leg(ops, formats, synth, torch, dev, steps, warmup):
     """The MoE layer with the reference checkpoint's weight classes (IQ3_S routed gate/up, Q6_K
     routed down, Q8_0 shared expert; ops.moe_layer_ckpt) at M=11 and M=2048, config 5's shapes,
     seeded weights (a synthetic IQ3_S grid), two copies of the slabs rotated (906 MB), graph
-    replays; FLOPs and expert bytes counted as for config 5."""
+    replays; FLOPs and expert bytes counted as for config 5.  The routed slabs are timed as tiled
+    records (tlx_pack_iq3s_tiled / tlx_pack_q6k_tiled, the layout's headline) and as GGUF rows."""
+    from thunderllamax_amd._lib import LAYOUT_RAW, LAYOUT_TILED
     rng = np.random.default_rng(20261205)
     E, H, F = 256, 2048, 512
-    sets = []
+    sets = {LAYOUT_RAW: [], LAYOUT_TILED: []}
     for _ in range(2):
         gu, dn, shared = synth.moe_ckpt_slabs(rng, E)
         dgu = [torch.from_numpy(a).to(dev) for a in gu]
         ddn = [torch.from_numpy(a).to(dev) for a in dn]
-        sets.append(dict(keep=(dgu, ddn), ptbl=formats.pointer_table(dgu, dev), ptbl_dn=formats.pointer_table(ddn, dev),
-                         sh=[torch.from_numpy(np.ascontiguousarray(a).reshape(-1)).to(dev) for a in shared]))
+        sh = [torch.from_numpy(np.ascontiguousarray(a).reshape(-1)).to(dev) for a in shared]
+        tgu = [ops.pack_iq3s_tiled(a, torch.empty_like(a), 2 * F, H) for a in dgu]
+        tdn = [ops.pack_q6k_tiled(a, torch.empty_like(a), H, F) for a in ddn]
+        sets[LAYOUT_RAW].append(dict(keep=(dgu, ddn), ptbl=formats.pointer_table(dgu, dev),
+                                     ptbl_dn=formats.pointer_table(ddn, dev), sh=sh))
+        sets[LAYOUT_TILED].append(dict(keep=(tgu, tdn), ptbl=formats.pointer_table(tgu, dev),
+                                       ptbl_dn=formats.pointer_table(tdn, dev), sh=sh))
     gridf = torch.from_numpy(synth.iq3s_grid(rng).reshape(-1)).to(dev)
     out = {"workload": "MoE layer with the checkpoint's classes: 256 IQ3_S gate/up + Q6_K down experts, Q8_0 shared "
                        "expert, hidden 2048, FF 512, top-8; hidden states bf16(0.05 * N(0,1))"}
@@ -480,11 +487,13 @@ def moe_ckpt_leg(ops, formats, synth, torch, dev, steps, warmup):
         y = torch.empty(P, H, device=dev)
         state = {"i": 0}
 
-        def layer(st):
-            c = sets[state["i"] % 2]
+        def layer(st, layout=LAYOUT_TILED):
+            c = sets[layout][state["i"] % 2]
             state["i"] += 1
-            ops.moe_layer_ckpt(logits, sg, x, hres, y, c["ptbl"], c["ptbl_dn"], c["sh"], gridf, sc, stream=st)
+            ops.moe_layer_ckpt(logits, sg, x, hres, y, c["ptbl"], c["ptbl_dn"], c["sh"], gridf, sc, stream=st,
+                               layout=layout)
 
+        t_rows = time_graph(lambda st: layer(st, LAYOUT_RAW), steps, warmup, torch)
         t = time_graph(layer, steps, warmup, torch)
         hit = int(torch.unique(sc.eids).numel())
         flops = 2.0 * 3 * F * H * (8 * P + P)
@@ -493,7 +502,7 @@ def moe_ckpt_leg(ops, formats, synth, torch, dev, steps, warmup):
         gbs = wbytes / (t * 1e-3) / 1e9
         route = "pair walk" if P <= ops.MOE_PAIR_WALK_MAX_P else "sort + sorted forms with the shared expert inside"
         out[f"M{P}"] = {"ms": round(t, 4), "tflops": round(tflops, 2), "experts_hit": hit, "weight_gbs": round(gbs, 1),
-                        "route": route,
+                        "route": route, "slabs": "tiled records", "ms_gguf_rows": round(t_rows, 4),
                         "roofline": (hbm_roofline(gbs, f"checkpoint-class MoE layer ({route}; graph): expert bytes / "
                                                        "layer time", traffic=TRAFFIC.get(f"ckpt_m{P}")) if P <= 64 else
                                      mfma_roofline(tflops, f"checkpoint-class MoE layer ({route}; graph): "

@@ -431,7 +431,21 @@ int tlx_moe_combine(const uint16_t* parts, const float* gates, const float* sg, 
  * the reference's: IQ3_S gate/up slab = 512 gate rows, then 512 up rows from byte 450,560, 880 B a
  * row (k = 2048); Q6_K down slab = 2048 rows of 420 B (raw 210-B blocks, k = 512); slab addresses
  * 2-B aligned.  gridf: the IQ3_S grid as float[512][4], passed at run time as by the reference.
- * np = number of pairs (8 per position), <= 16384; the sorted forms take tlx_moe_sort's eoff / plist. */
+ * np = number of pairs (8 per position), <= 16384; the sorted forms take tlx_moe_sort's eoff / plist.
+ * layout (the routed forms' argument before the stream): TLX_LAYOUT_RAW for slabs of GGUF rows as
+ * above, TLX_LAYOUT_TILED for slabs repacked by tlx_pack_iq3s_tiled / tlx_pack_q6k_tiled (same
+ * size, same results bit for bit: every lane's bytes of a block are one contiguous run). */
+
+/* GGUF IQ3_S rows u8[N][K/256*110] -> tiled records u8[N/16][K/256][1760]; GGUF Q6_K rows
+ * u8[N][K/256*210] -> u8[N/16][K/256][3360] (N % 16 == 0, K % 256 == 0).  Record (tile, block), lane
+ * l = 16 kq + r (row r of the tile): IQ3_S [qs: lane l's 16 B qs[16kq..] | signs: 8 B signs[8kq..] |
+ * qh: 2 B qh[2kq..] | scale byte kq | 16 rows' d]; Q6_K [ql: lane l's 32 B ql[32kq..] | qh: row r's
+ * 32 B qh[32h..] at 32 (16 h + r) | sc: 4 B sc[8h + 2c + {0,1,4,5}] (h = kq/2, c = kq%2) | 16 rows' d].
+ * A pure byte permutation: an expert slab keeps its size and its up rows their offset.  No reference
+ * counterpart (the reference reads GGUF rows, engine/mm/MM_E_gxu_gm.cu:86-93 and
+ * engine/mm/MM_B_gxm_dn6.cu:18-25); the load-time repack for the layout argument above. */
+int tlx_pack_iq3s_tiled(const void* src, void* tiled, int N, int K, void* stream);
+int tlx_pack_q6k_tiled(const void* src, void* tiled, int N, int K, void* stream);
 
 /* IQ3_S dequant (dq_iq3_s, engine/mm/MM_P0_d2_repack.py:95-120): 110-B blocks
  * [d f16][qs 64][qh 8][signs 32][scales 4]; out f32 or (out_f16) fp16 [rows][kdim], kdim % 256. */
@@ -445,24 +459,24 @@ int tlx_q8_0_dequant(const void* w, void* out, int64_t rows, int64_t kdim, int o
  * silu(Wg_e . x[pair >> 3]) * (Wu_e . x[pair >> 3]).  Replaces gxu_gm
  * (engine/mm/MM_E_gxu_gm.cu:86-93): gxu_gm(ptbl, eoff, plist, xs f32[P][2048], gridf, ys). */
 int tlx_moe_up3s(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const float* xs,
-                 const float* gridf, float* ys, int np, void* stream);
+                 const float* gridf, float* ys, int np, int layout, void* stream);
 /* Pair-walk form (no sort): pair p runs expert eids[p].  Replaces gx8e256up
  * (engine/mm/MM_P1_gx8e256up.cu:15-20): gx8e256up(ptbl, eids, xs, gridf, ys).  The decode form:
  * weights go straight to registers, the grid's levels are read as fp16 (exact for the IQ3_S
  * grid's integers); the operands are tlx_moe_up3s's, summed in another k order (within 1e-5). */
 int tlx_moe_up3s_pairs(const uint64_t* ptbl, const uint16_t* eids, const float* xs, const float* gridf,
-                       float* ys, int np, void* stream);
+                       float* ys, int np, int layout, void* stream);
 /* Q6_K grouped down over the sorted pairs: parts[pair][2048] = fp16(Wd_e . act[pair]).  Replaces
  * gxm_dn6 (engine/mm/MM_B_gxm_dn6.cu:18-25): gxm_dn6(ptbl, items, nitp, eoff, plist,
  * xs = act f32[NPAIR][512], parts), same positional order; items / nitp are accepted (may be null)
  * and not read: this form walks eoff / plist. */
 int tlx_moe_dn6(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
-                const uint16_t* plist, const float* act, uint16_t* parts, int np, void* stream);
+                const uint16_t* plist, const float* act, uint16_t* parts, int np, int layout, void* stream);
 /* Pair-walk form: replaces gx8e256dn6 (engine/mm/MM_P2_gx8e256dn6.cu:9-13):
  * gx8e256dn6(ptbl, eids, xs = act, parts).  The decode form, as tlx_moe_up3s_pairs: tlx_moe_dn6's
  * operands summed in another k order. */
 int tlx_moe_dn6_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, uint16_t* parts,
-                      int np, void* stream);
+                      int np, int layout, void* stream);
 /* The sorted forms (tlx_moe_up3s / tlx_moe_dn6) and the Q8_0 shared expert's gate+up / down
  * (tlx_moe_shared8's two launches) in one launch each above P = 16 (else the two launches): the
  * shared expert's workgroups follow the routed ones.  The down keeps two launches whenever parts
@@ -472,10 +486,10 @@ int tlx_moe_dn6_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float
  * sact f32 [P][512] (16-B aligned) and shared f32 [P][2048] as tlx_moe_shared8's act / y. */
 int tlx_moe_up3s_sh(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const float* xs,
                     const float* gridf, float* ys, int np, const void* wg8, const void* wu8, float* sact, int P,
-                    void* stream);
+                    int layout, void* stream);
 int tlx_moe_dn6_sh(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
                    const uint16_t* plist, const float* act, uint16_t* parts, int np, const void* wd8,
-                   const float* sact, float* shared, int P, void* stream);
+                   const float* sact, float* shared, int P, int layout, void* stream);
 /* The Q8_0 shared expert over P positions: y[P][2048] f32 = Wd . (silu(Wg . x) * (Wu . x)), with act
  * f32[P][512] caller scratch (two launches on the stream; P <= 16 the decode form).  Replaces shexp8
  * (engine/mm/MM_P2_shexp8.cu:8-13): shexp8(wg [512][2176], wu [512][2176], wd [2048][544], x, y).

@@ -14,6 +14,12 @@
   (/root/reference/engine/mm/MM_P0_d2_repack.py:78-93 gives the block: d, scales_h, scales_l,
   qs) into MFMA lane order.  Pinned by the inverse, by hand-placed bytes, and, on the GPU, by
   the GEMMs over tiled slabs equal to those over the GGUF rows bit for bit.
+* ``pack_iq3s_tiled`` / ``pack_q6k_tiled`` and their inverses -- this library's tiled IQ3_S /
+  Q6_K expert slabs for the checkpoint-class MoE GEMMs (no reference counterpart): byte
+  permutations of GGUF IQ3_S rows (/root/reference/engine/mm/MM_P0_d2_repack.py:95-120 gives the
+  block: d, qs, qh, signs, scales) and Q6_K rows (ql, qh, scales, d) into lane order.  Pinned by
+  the inverses, by hand-placed bytes, and, on the GPU, by every routed form over tiled slabs
+  equal to the GGUF-row form bit for bit.
 """
 import numpy as np
 
@@ -213,3 +219,74 @@ def unpack_iq4_tiled(rec, kdim):
     qs = r[:, :, 128:].reshape(t, nb, 2, 4, 16, 16).transpose(0, 1, 4, 2, 3, 5).reshape(t, nb, 16, 128)
     blk = np.concatenate([hdr, qs], axis=3).transpose(0, 2, 1, 3)                   # [t, r, b, 136]
     return np.ascontiguousarray(blk.reshape(16 * t, 136 * nb))
+
+
+# Tiled checkpoint-class slabs (this library's decode layout for the MoE checkpoint classes): per
+# 16-row tile and 256-weight block, the bytes each lane (col, kq) of a wave fetches for its 64
+# weights of the block, in lane order (lane l = 16 kq + col), so every wave load is one contiguous
+# run.  Same bytes as the GGUF rows, permuted; a tile's record has the 16 rows' block size.
+_Q6_SC = np.array([[0, 1, 4, 5], [2, 3, 6, 7], [8, 9, 12, 13], [10, 11, 14, 15]])   # lane kq's scale bytes
+
+
+def pack_iq3s_tiled(raw_rows, kdim):
+    """GGUF IQ3_S rows u8[N, 110*NB] (N % 16 == 0) -> tiled records u8[N/16, NB, 1760].
+
+    Record (tile t, block b), row r = 16t + col, lane l = 16 kq + col: ``[0, 1024)`` lane l's 16 index
+    bytes ``qs[16kq .. 16kq + 15]`` (block bytes 2..65); ``[1024, 1536)`` its 8 sign bytes
+    ``signs[8kq ..]`` (bytes 74..105); ``[1536, 1664)`` its 2 high-bit bytes ``qh[2kq, 2kq + 1]``
+    (bytes 66..73); ``[1664, 1728)`` its scale byte ``scales[kq]`` (bytes 106..109); ``[1728, 1760)``
+    row col's d (bytes 0..1)."""
+    x = np.ascontiguousarray(raw_rows, dtype=np.uint8)
+    n, nb = len(x), kdim // 256
+    assert n % 16 == 0 and x.shape[1] == 110 * nb
+    blk = x.reshape(n // 16, 16, nb, 110).transpose(0, 2, 1, 3)             # [t, b, col, 110]
+    def lanes(lo, per):                                                      # [t, b, kq, col, per]
+        return blk[..., lo:lo + 4 * per].reshape(n // 16, nb, 16, 4, per).transpose(0, 1, 3, 2, 4)
+    parts = [lanes(2, 16), lanes(74, 8), lanes(66, 2), lanes(106, 1)]
+    flat = [a.reshape(n // 16, nb, -1) for a in parts] + [blk[..., 0:2].reshape(n // 16, nb, 32)]
+    return np.ascontiguousarray(np.concatenate(flat, axis=2))
+
+
+def unpack_iq3s_tiled(rec, kdim):
+    """Inverse of :func:`pack_iq3s_tiled` -> GGUF IQ3_S rows u8[16*T, 110*NB]."""
+    nb = kdim // 256
+    r = np.ascontiguousarray(rec, dtype=np.uint8).reshape(-1, nb, 1760)
+    t = len(r)
+    def rows(lo, per):                                                       # -> [t, b, col, 4 per]
+        return r[:, :, lo:lo + 64 * per].reshape(t, nb, 4, 16, per).transpose(0, 1, 3, 2, 4).reshape(t, nb, 16, 4 * per)
+    blk = np.concatenate([r[:, :, 1728:1760].reshape(t, nb, 16, 2), rows(0, 16), rows(1536, 2), rows(1024, 8),
+                          rows(1664, 1)], axis=3)                            # d, qs, qh, signs, scales
+    return np.ascontiguousarray(blk.transpose(0, 2, 1, 3).reshape(16 * t, 110 * nb))
+
+
+def pack_q6k_tiled(raw_rows, kdim):
+    """GGUF Q6_K rows u8[N, 210*NB] (N % 16 == 0) -> tiled records u8[N/16, NB, 3360].
+
+    Record (tile t, block b), row r = 16t + col, lane l = 16 kq + col: ``[0, 2048)`` lane l's 32 low
+    bytes ``ql[32kq .. 32kq + 31]``; ``[2048, 3072)`` at ``32 (16h + col)`` row col's high bytes
+    ``qh[32h .. 32h + 31]`` (h = 0, 1); ``[3072, 3328)`` lane l's 4 scale bytes ``sc[8h + 2c + {0, 1,
+    4, 5}]`` (h = kq / 2, c = kq % 2); ``[3328, 3360)`` row col's d (bytes 208..209)."""
+    x = np.ascontiguousarray(raw_rows, dtype=np.uint8)
+    n, nb = len(x), kdim // 256
+    assert n % 16 == 0 and x.shape[1] == 210 * nb
+    blk = x.reshape(n // 16, 16, nb, 210).transpose(0, 2, 1, 3)             # [t, b, col, 210]
+    ql = blk[..., 0:128].reshape(n // 16, nb, 16, 4, 32).transpose(0, 1, 3, 2, 4)
+    qh = blk[..., 128:192].reshape(n // 16, nb, 16, 2, 32).transpose(0, 1, 3, 2, 4)
+    sc = blk[..., 192 + _Q6_SC].transpose(0, 1, 3, 2, 4)                     # [t, b, kq, col, 4]
+    flat = [a.reshape(n // 16, nb, -1) for a in (ql, qh, sc)] + [blk[..., 208:210].reshape(n // 16, nb, 32)]
+    return np.ascontiguousarray(np.concatenate(flat, axis=2))
+
+
+def unpack_q6k_tiled(rec, kdim):
+    """Inverse of :func:`pack_q6k_tiled` -> GGUF Q6_K rows u8[16*T, 210*NB]."""
+    nb = kdim // 256
+    r = np.ascontiguousarray(rec, dtype=np.uint8).reshape(-1, nb, 3360)
+    t = len(r)
+    ql = r[:, :, 0:2048].reshape(t, nb, 4, 16, 32).transpose(0, 1, 3, 2, 4).reshape(t, nb, 16, 128)
+    qh = r[:, :, 2048:3072].reshape(t, nb, 2, 16, 32).transpose(0, 1, 3, 2, 4).reshape(t, nb, 16, 64)
+    scl = r[:, :, 3072:3328].reshape(t, nb, 4, 16, 4).transpose(0, 1, 3, 2, 4)   # [t, b, col, kq, 4]
+    sc = np.empty((t, nb, 16, 16), dtype=np.uint8)
+    sc[..., _Q6_SC] = scl
+    d = r[:, :, 3328:3360].reshape(t, nb, 16, 2)
+    blk = np.concatenate([ql, qh, sc, d], axis=3)
+    return np.ascontiguousarray(blk.transpose(0, 2, 1, 3).reshape(16 * t, 210 * nb))

@@ -137,12 +137,18 @@ def test_moe_checkpoint_classes_argument_validation():
     L = _lib.lib()
     buf = ctypes.create_string_buffer(64)
     p = (ctypes.addressof(buf) + 15) & ~15
-    assert L.tlx_moe_up3s(p, p, p, p, p, p, 0, None) == _lib.TLX_E_ARG          # no pairs
-    assert L.tlx_moe_up3s(p, p, p, p, p, p, 16385, None) == _lib.TLX_E_ARG      # more than the sort supports
-    assert L.tlx_moe_up3s(p, p, p, p + 4, p, p, 8, None) == _lib.TLX_E_ALIGN    # xs 16-B aligned
-    assert L.tlx_moe_up3s_pairs(p, p, p, p + 8, p, 8, None) == _lib.TLX_E_ALIGN # gridf 16-B aligned
-    assert L.tlx_moe_dn6(p, None, None, p, p, p, p, 0, None) == _lib.TLX_E_ARG
-    assert L.tlx_moe_dn6_pairs(p, p, p + 4, p, 8, None) == _lib.TLX_E_ALIGN
+    R, T = _lib.LAYOUT_RAW, _lib.LAYOUT_TILED
+    assert L.tlx_moe_up3s(p, p, p, p, p, p, 0, R, None) == _lib.TLX_E_ARG          # no pairs
+    assert L.tlx_moe_up3s(p, p, p, p, p, p, 16385, R, None) == _lib.TLX_E_ARG      # more than the sort supports
+    assert L.tlx_moe_up3s(p, p, p, p, p, p, 8, _lib.LAYOUT_PACKED, None) == _lib.TLX_E_ARG   # layout
+    assert L.tlx_moe_up3s(p, p, p, p + 4, p, p, 8, T, None) == _lib.TLX_E_ALIGN    # xs 16-B aligned
+    assert L.tlx_moe_up3s_pairs(p, p, p, p + 8, p, 8, R, None) == _lib.TLX_E_ALIGN # gridf 16-B aligned
+    assert L.tlx_moe_up3s_pairs(p, p, p, p, p, 8, 7, None) == _lib.TLX_E_ARG
+    assert L.tlx_moe_dn6(p, None, None, p, p, p, p, 0, R, None) == _lib.TLX_E_ARG
+    assert L.tlx_moe_dn6(p, None, None, p, p, p, p, 8, _lib.LAYOUT_PACK7, None) == _lib.TLX_E_ARG
+    assert L.tlx_moe_dn6_pairs(p, p, p + 4, p, 8, T, None) == _lib.TLX_E_ALIGN
+    assert L.tlx_pack_iq3s_tiled(p, p, 8, 256, None) == _lib.TLX_E_ARG            # N % 16
+    assert L.tlx_pack_q6k_tiled(p, p, 16, 384, None) == _lib.TLX_E_ARG            # K % 256
     assert L.tlx_moe_shared8(p, p, p, p, p, p, 0, None) == _lib.TLX_E_ARG
     assert L.tlx_moe_shared8(p, p, p, p, p, p + 4, 4, None) == _lib.TLX_E_ALIGN  # act 16-B aligned
     assert L.tlx_iq3s_dequant(p, p, p, 1, 384, 0, None) == _lib.TLX_E_ARG        # kdim % 256
@@ -170,9 +176,12 @@ def test_moe_checkpoint_fused_argument_validation():
     L = _lib.lib()
     buf = ctypes.create_string_buffer(64)
     p = (ctypes.addressof(buf) + 15) & ~15
-    assert L.tlx_moe_up3s_sh(p, p, p, p, p, p, 0, p, p, p, 4, None) == _lib.TLX_E_ARG          # no pairs
-    assert L.tlx_moe_up3s_sh(p, p, p, p, p, p, 32, p, p, p, 0, None) == _lib.TLX_E_ARG         # no positions
-    assert L.tlx_moe_up3s_sh(p, p, p, p, p, p, 32, p, p, p + 4, 4, None) == _lib.TLX_E_ALIGN   # sact
-    assert L.tlx_moe_up3s_sh(p, p, p, p + 4, p, p, 32, p, p, p, 4, None) == _lib.TLX_E_ALIGN   # xs
-    assert L.tlx_moe_dn6_sh(p, None, None, p, p, p, p, 16385, p, p, p, 4, None) == _lib.TLX_E_ARG
-    assert L.tlx_moe_dn6_sh(p, None, None, p, p, p, p, 32, p + 1, p, p, 4, None) == _lib.TLX_E_ALIGN  # wd8
+    R = _lib.LAYOUT_RAW
+    assert L.tlx_moe_up3s_sh(p, p, p, p, p, p, 0, p, p, p, 4, R, None) == _lib.TLX_E_ARG          # no pairs
+    assert L.tlx_moe_up3s_sh(p, p, p, p, p, p, 32, p, p, p, 0, R, None) == _lib.TLX_E_ARG         # no positions
+    assert L.tlx_moe_up3s_sh(p, p, p, p, p, p, 32, p, p, p, 4, 5, None) == _lib.TLX_E_ARG         # layout
+    assert L.tlx_moe_up3s_sh(p, p, p, p, p, p, 32, p, p, p + 4, 4, R, None) == _lib.TLX_E_ALIGN   # sact
+    assert L.tlx_moe_up3s_sh(p, p, p, p + 4, p, p, 32, p, p, p, 4, R, None) == _lib.TLX_E_ALIGN   # xs
+    assert L.tlx_moe_dn6_sh(p, None, None, p, p, p, p, 16385, p, p, p, 4, R, None) == _lib.TLX_E_ARG
+    assert L.tlx_moe_dn6_sh(p, None, None, p, p, p, p, 32, p, p, p, 4, 9, None) == _lib.TLX_E_ARG   # layout
+    assert L.tlx_moe_dn6_sh(p, None, None, p, p, p, p, 32, p + 1, p, p, 4, R, None) == _lib.TLX_E_ALIGN  # wd8

@@ -16,9 +16,9 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import gemv, moe, quants
+from oracle import gemv, layouts, moe, quants
 from thunderllamax_amd import formats, ops, synth
-from thunderllamax_amd._lib import TlxError, call
+from thunderllamax_amd._lib import LAYOUT_RAW, LAYOUT_TILED, TlxError, call
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -212,6 +212,72 @@ def test_ckpt_grouped_shared_fused(gpu, ckpt, P):
     assert _rows_err(fus["shared"].cpu().numpy(), ref) <= TOL
 
 
+def test_ckpt_tiled_repack_matches_oracle(gpu, ckpt):
+    """tlx_pack_iq3s_tiled / tlx_pack_q6k_tiled on an expert's slabs: byte for byte the oracle's
+    records (which the CPU tests invert back to the GGUF rows)."""
+    print("[case] IQ3_S / Q6_K tiled repack, expert 5's slabs", flush=True)
+    gu, dn = ckpt["gu"][5], ckpt["dn"][5]
+    tgu = ops.pack_iq3s_tiled(ckpt["dgu"][5], torch.empty_like(ckpt["dgu"][5]), 2 * moe.FF, moe.HID)
+    tdn = ops.pack_q6k_tiled(ckpt["ddn"][5], torch.empty_like(ckpt["ddn"][5]), moe.HID, moe.FF)
+    torch.cuda.synchronize()
+    assert np.array_equal(tgu.cpu().numpy(), layouts.pack_iq3s_tiled(gu.reshape(2 * moe.FF, -1), moe.HID).reshape(-1))
+    assert np.array_equal(tdn.cpu().numpy(), layouts.pack_q6k_tiled(dn.reshape(moe.HID, -1), moe.FF).reshape(-1))
+
+
+@pytest.fixture(scope="module")
+def ckpt_tiled(gpu, ckpt):
+    tgu = [ops.pack_iq3s_tiled(s, torch.empty_like(s), 2 * moe.FF, moe.HID) for s in ckpt["dgu"]]
+    tdn = [ops.pack_q6k_tiled(s, torch.empty_like(s), moe.HID, moe.FF) for s in ckpt["ddn"]]
+    torch.cuda.synchronize()
+    return {"tgu": tgu, "tdn": tdn, "ptbl": formats.pointer_table(tgu, gpu), "ptbl_dn": formats.pointer_table(tdn, gpu)}
+
+
+@pytest.mark.parametrize("P", [11, 300])
+def test_ckpt_tiled_forms_bit_identical(gpu, ckpt, ckpt_tiled, P):
+    """Every checkpoint-class routed form over the tiled slabs (layout=LAYOUT_TILED) against the same
+    form over the GGUF rows, bit for bit: the pair walks, the sorted forms, the forms with the shared
+    expert, and the down's staged form (parts not 8-B aligned)."""
+    print(f"[case] checkpoint-class forms on tiled slabs vs GGUF rows, P={P}", flush=True)
+    rng = np.random.default_rng(80 + P)
+    x, eids, deids, eoff, plist, items, nitp = _route(gpu, rng, P)
+    dx = torch.from_numpy(x).to(gpu)
+    np_ = 8 * P
+    wg8, wu8, wd8 = ckpt["dsh"]
+
+    def run(lay):
+        pt, pd = (ckpt["ptbl"], ckpt["ptbl_dn"]) if lay == LAYOUT_RAW else (ckpt_tiled["ptbl"], ckpt_tiled["ptbl_dn"])
+        o = {}
+        o["act"] = torch.full((np_, moe.FF), -3.0, device=gpu)
+        ops.moe_up3s(pt, eoff, plist, dx, ckpt["gridf"], o["act"], layout=lay)
+        o["act_w"] = torch.full_like(o["act"], -3.0)
+        ops.moe_up3s_pairs(pt, deids, dx, ckpt["gridf"], o["act_w"], layout=lay)
+        o["parts"] = torch.full((np_, moe.HID), -3.0, dtype=torch.float16, device=gpu)
+        ops.moe_dn6(pd, items, nitp, eoff, plist, o["act"], o["parts"], layout=lay)
+        o["parts_w"] = torch.full_like(o["parts"], -3.0)
+        ops.moe_dn6_pairs(pd, deids, o["act"], o["parts_w"], layout=lay)
+        buf = torch.full((np_ * moe.HID + 1,), -3.0, dtype=torch.float16, device=gpu)
+        o["parts_u"] = buf[1:].view(np_, moe.HID)   # 2-B aligned: the staged form
+        ops.moe_dn6(pd, items, nitp, eoff, plist, o["act"], o["parts_u"], layout=lay)
+        o["act_sh"] = torch.full_like(o["act"], -3.0)
+        o["sact"] = torch.full((P, moe.FF), -3.0, device=gpu)
+        ops.moe_up3s_sh(pt, eoff, plist, dx, ckpt["gridf"], o["act_sh"], wg8, wu8, o["sact"], layout=lay)
+        o["shared"] = torch.full((P, moe.HID), -3.0, device=gpu)
+        o["parts_sh"] = torch.full_like(o["parts"], -3.0)
+        ops.moe_dn6_sh(pd, items, nitp, eoff, plist, o["act"], o["parts_sh"], wd8, o["sact"], o["shared"], layout=lay)
+        buf2 = torch.full((np_ * moe.HID + 1,), -3.0, dtype=torch.float16, device=gpu)
+        o["parts_shu"] = buf2[1:].view(np_, moe.HID)
+        ops.moe_dn6_sh(pd, items, nitp, eoff, plist, o["act"], o["parts_shu"], wd8, o["sact"], o["shared"],
+                       layout=lay)
+        torch.cuda.synchronize()
+        return {k: v.cpu().numpy() for k, v in o.items()}
+
+    raw, til = run(LAYOUT_RAW), run(LAYOUT_TILED)
+    for k in raw:
+        v = np.uint16 if raw[k].dtype == np.float16 else np.uint32
+        assert np.array_equal(raw[k].view(v), til[k].view(v)), k
+    _check_pairs(ckpt, x, eids, til["act"], til["parts"], list(range(0, np_, 7)))
+
+
 def test_ckpt_argument_validation(gpu, ckpt):
     dx = torch.zeros(2, moe.HID, device=gpu)
     act = torch.empty(16, moe.FF, dtype=torch.float32, device=gpu)
@@ -221,10 +287,10 @@ def test_ckpt_argument_validation(gpu, ckpt):
                            torch.empty(24, moe.FF, dtype=torch.float32, device=gpu))
     with pytest.raises(TlxError):     # xs not 16-B aligned
         call("tlx_moe_up3s_pairs", ckpt["ptbl"].data_ptr(), eids.data_ptr(), dx.data_ptr() + 8,
-             ckpt["gridf"].data_ptr(), act.data_ptr(), 16, None)
+             ckpt["gridf"].data_ptr(), act.data_ptr(), 16, LAYOUT_RAW, None)
     with pytest.raises(TlxError):     # more pairs than the sort supports
         call("tlx_moe_dn6_pairs", ckpt["ptbl_dn"].data_ptr(), eids.data_ptr(), act.data_ptr(), act.data_ptr(),
-             16385, None)
+             16385, LAYOUT_TILED, None)
 
 
 @pytest.mark.parametrize("P", [11, 300])

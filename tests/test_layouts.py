@@ -109,3 +109,48 @@ def test_iq4_tiled_slab_places_bytes_by_hand():
         for ib in range(8):
             o = 128 + 1024 * (ib // 4) + 16 * (16 * (ib % 4) + r)
             assert np.array_equal(rec[t, b, o:o + 16], row[8 + 16 * ib:8 + 16 * ib + 16])
+
+
+@pytest.mark.parametrize("rows,kdim", [(16, 256), (32, 2048), (48, 512)])
+def test_ckpt_tiled_slabs_invert(rows, kdim):
+    rng = np.random.default_rng(rows + 7 * kdim)
+    a = rng.integers(0, 256, (rows, 110 * (kdim // 256)), dtype=np.uint8)
+    rec = layouts.pack_iq3s_tiled(a, kdim)
+    assert rec.shape == (rows // 16, kdim // 256, 1760)
+    assert np.array_equal(layouts.unpack_iq3s_tiled(rec, kdim), a)
+    b = rng.integers(0, 256, (rows, 210 * (kdim // 256)), dtype=np.uint8)
+    rec = layouts.pack_q6k_tiled(b, kdim)
+    assert rec.shape == (rows // 16, kdim // 256, 3360)
+    assert np.array_equal(layouts.unpack_q6k_tiled(rec, kdim), b)
+
+
+def test_ckpt_tiled_slabs_place_bytes_by_hand():
+    """Bytes placed by the record rules written out, lane l = 16 kq + col.  IQ3_S: index byte j of
+    lane l at 16 l + j (block byte 2 + 16 kq + j), sign byte j at 1024 + 8 l + j (74 + 8 kq + j),
+    high-bit byte j at 1536 + 2 l + j (66 + 2 kq + j), scale byte at 1664 + l (106 + kq), d byte j at
+    1728 + 2 col + j.  Q6_K: low byte j at 32 l + j (32 kq + j), high byte j of half h at
+    2048 + 32 (16 h + col) + j (128 + 32 h + j), scale slot s at 3072 + 4 l + s (192 + 8 (kq / 2) +
+    2 (kq % 2) + (0, 1, 4, 5)[s]), d byte j at 3328 + 2 col + j (208 + j)."""
+    rng = np.random.default_rng(9)
+    kdim = 512
+    a = rng.integers(0, 256, (32, 220), dtype=np.uint8)
+    b = rng.integers(0, 256, (32, 420), dtype=np.uint8)
+    ra, rb = layouts.pack_iq3s_tiled(a, kdim), layouts.pack_q6k_tiled(b, kdim)
+    for t, blk, col, kq in [(0, 0, 0, 0), (0, 1, 5, 3), (1, 0, 15, 1), (1, 1, 9, 2)]:
+        l, ra_, rb_ = 16 * kq + col, a[16 * t + col, 110 * blk:], b[16 * t + col, 210 * blk:]
+        rec, req = ra[t, blk], rb[t, blk]
+        for j in range(16):
+            assert rec[16 * l + j] == ra_[2 + 16 * kq + j]
+        for j in range(8):
+            assert rec[1024 + 8 * l + j] == ra_[74 + 8 * kq + j]
+        for j in range(2):
+            assert rec[1536 + 2 * l + j] == ra_[66 + 2 * kq + j]
+            assert rec[1728 + 2 * col + j] == ra_[j]
+            assert req[3328 + 2 * col + j] == rb_[208 + j]
+        assert rec[1664 + l] == ra_[106 + kq]
+        for j in range(32):
+            assert req[32 * l + j] == rb_[32 * kq + j]
+            for h in range(2):
+                assert req[2048 + 32 * (16 * h + col) + j] == rb_[128 + 32 * h + j]
+        for s_, off in enumerate((0, 1, 4, 5)):
+            assert req[3072 + 4 * l + s_] == rb_[192 + 8 * (kq // 2) + 2 * (kq % 2) + off]

@@ -91,16 +91,18 @@ SIGNATURES = {
     "tlx_moe_up4_sh": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _p, _i, _i, _p],
     "tlx_moe_dn4_sh": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _i, _i, _p],
     "tlx_pack_iq4_tiled": [_p, _p, _i, _i, _p],
+    "tlx_pack_iq3s_tiled": [_p, _p, _i, _i, _p],
+    "tlx_pack_q6k_tiled": [_p, _p, _i, _i, _p],
     "tlx_moe_combine": [_p, _p, _p, _p, _p, _p, _i, _p],
     "tlx_iq3s_dequant": [_p, _p, _p, _i64, _i64, _i, _p],
     "tlx_q8_0_dequant": [_p, _p, _i64, _i64, _i, _p],
-    "tlx_moe_up3s": [_p, _p, _p, _p, _p, _p, _i, _p],
-    "tlx_moe_up3s_pairs": [_p, _p, _p, _p, _p, _i, _p],
-    "tlx_moe_dn6": [_p, _p, _p, _p, _p, _p, _p, _i, _p],
-    "tlx_moe_dn6_pairs": [_p, _p, _p, _p, _i, _p],
+    "tlx_moe_up3s": [_p, _p, _p, _p, _p, _p, _i, _i, _p],
+    "tlx_moe_up3s_pairs": [_p, _p, _p, _p, _p, _i, _i, _p],
+    "tlx_moe_dn6": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _p],
+    "tlx_moe_dn6_pairs": [_p, _p, _p, _p, _i, _i, _p],
     "tlx_moe_shared8": [_p, _p, _p, _p, _p, _p, _i, _p],
-    "tlx_moe_up3s_sh": [_p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _i, _p],
-    "tlx_moe_dn6_sh": [_p, _p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _i, _p],
+    "tlx_moe_up3s_sh": [_p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _i, _i, _p],
+    "tlx_moe_dn6_sh": [_p, _p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _i, _i, _p],
     "tlx_stream_chunk_bytes": [],
     "tlx_stream_read": [_p, ctypes.c_uint64, _p, _p],
 }

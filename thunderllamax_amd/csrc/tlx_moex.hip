@@ -23,6 +23,10 @@
 // gq_dn_kernel (the routed down over the sorted pairs): gv_kernel's register-built operands with
 // the expert's activations resident in LDS (its section).
 //
+// Every routed form also reads tiled slabs (layout TLX_LAYOUT_TILED; tlx_pack_iq3s_tiled /
+// tlx_pack_q6k_tiled, this library's own): the same bytes regrouped per 16-row tile and 256-weight
+// block so that a lane's bytes of each field are one contiguous run; only the fetches differ.
+//
 // IQ3_S's 512-entry grid is a run-time argument (float[512][4]), as in the reference.
 #include "tlx_common.h"
 
@@ -35,6 +39,8 @@ template <bool UP> constexpr int gx_waves() { return UP ? 4 : 8; }
 constexpr int kGxKc = 64;           // k per chunk (LDS stage)
 constexpr int kGxLd = kGxKc + 8;    // LDS row stride (halfs): fragment reads of 16 rows hit 16 distinct 16-B slots
 constexpr uint32_t kIq3sGate = kFf * 880;   // GATE_B: the up rows' offset in an IQ3_S slab
+constexpr int kIq3sRow = kHid / 256 * 110;   // 880 B: an IQ3_S gate/up row (k = 2048)
+constexpr int kQ6kRow = kFf / 256 * 210;     // 420 B: a Q6_K down row (k = 512)
 
 enum GxCls { GX_IQ3S = 0, GX_Q6K = 1, GX_Q80 = 2 };
 enum GxForm { GX_SORTED = 0, GX_PAIRS = 1, GX_DENSE = 2 };
@@ -89,15 +95,39 @@ template <> struct GxRaw<GX_IQ3S> { uint32_t dn, qs, hs; };   // d | nib << 16, 
 template <> struct GxRaw<GX_Q6K> { uint32_t ds; u4_t ql, qh; };   // d | sc << 16 | (kib & 255) << 24
 template <> struct GxRaw<GX_Q80> { uint32_t d; u4_t q; };
 
-template <int CLS>
-__device__ __forceinline__ GxRaw<CLS> gx_fetch(const uint8_t* rowp, int k0) {
+// TL: the slab is in the tiled layout (records of 16 rows x 256 weights; tlx_pack_iq3s_tiled /
+// tlx_pack_q6k_tiled), rowp still the row's start as if in GGUF rows (a tile spans the same bytes),
+// col the row's place in its 16-row tile.
+template <int CLS, bool TL = false>
+__device__ __forceinline__ GxRaw<CLS> gx_fetch(const uint8_t* rowp, int k0, int col = 0) {
   // an opaque copy of the row pointer: the loads below then take their field offsets as
   // immediates on one address (measured: the M = 2048 gate+up 327 -> 313 us)
   uint64_t pv = (uint64_t)rowp;
   asm volatile("" : "+v"(pv));
   const uint8_t* row = (const uint8_t*)pv;
   GxRaw<CLS> r;
-  if constexpr (CLS == GX_IQ3S) {
+  if constexpr (TL && CLS == GX_IQ3S) {
+    // record (tile, block): lane l = 16 kq + col's 16 index bytes at 16 l, 8 sign bytes at
+    // 1024 + 8 l, 2 high-bit bytes at 1536 + 2 l, scale byte at 1664 + l; d at 1728 + 2 col
+    const uint8_t* rec = row - (size_t)col * kIq3sRow + (size_t)(k0 >> 8) * 1760;
+    const int kib = k0 & 255, kq = kib >> 6, sj = (kib >> 5) & 1, hf = (kib >> 4) & 1, l = 16 * kq + col;
+    const uint32_t nib = (rec[1664 + l] >> (4 * sj)) & 15u;
+    r.dn = tlx_ldu<uint16_t>(rec + 1728 + 2 * col) | (nib << 16);
+    r.qs = tlx_ldu<uint32_t>(rec + 16 * l + 8 * sj + 4 * hf);
+    r.hs = ((uint32_t)(rec[1536 + 2 * l + sj] >> (4 * hf)) & 15u) |
+           ((uint32_t)tlx_ldu<uint16_t>(rec + 1024 + 8 * l + 4 * sj + 2 * hf) << 8);
+  } else if constexpr (TL && CLS == GX_Q6K) {
+    // record (tile, block): lane l = 16 kq + col's 32 low bytes at 32 l; row col's high bytes of
+    // half h at 2048 + 32 (16 h + col); lane l's 4 scale bytes at 3072 + 4 l; d at 3328 + 2 col
+    const uint8_t* rec = row - (size_t)col * kQ6kRow + (size_t)(k0 >> 8) * 3360;
+    const int kib = k0 & 255, h = kib >> 7, g = (kib >> 5) & 3, l0 = kib & 31;
+    const int bs = 2 * g + (l0 >> 4);   // scale byte 8 h + bs: lane kq 2 h + ((bs >> 1) & 1), slot below
+    const int ls = 16 * (2 * h + ((bs >> 1) & 1)) + col;
+    r.ds = tlx_ldu<uint16_t>(rec + 3328 + 2 * col) | ((uint32_t)rec[3072 + 4 * ls + (bs & 1) + 2 * (bs >> 2)] << 16) |
+           ((uint32_t)kib << 24);
+    r.ql = tlx_ldu<u4_t>(rec + 32 * (16 * (2 * h + (g & 1)) + col) + l0);
+    r.qh = tlx_ldu<u4_t>(rec + 2048 + 32 * (16 * h + col) + l0);
+  } else if constexpr (CLS == GX_IQ3S) {
     const uint8_t* b = row + (size_t)(k0 >> 8) * 110;
     const int kib = k0 & 255, j = kib >> 5, hf = (kib >> 4) & 1;
     const uint32_t nib = (b[106 + (j >> 1)] >> (4 * (j & 1))) & 15u;
@@ -226,7 +256,7 @@ __device__ __forceinline__ void gx_dequant16(float* v, const uint8_t* row, int k
 
 // blk: the workgroup's index in its part of the grid (parts start at multiples of 8); L: any
 // GxLds<UP, *, >= gx_tok<FORM>()> that holds the IQ3_S lookups when CLS needs them
-template <int CLS, bool UP, int FORM, typename LDS>
+template <int CLS, bool UP, int FORM, bool TL, typename LDS>
 __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
   constexpr int K = UP ? kHid : kFf;
   constexpr int NW = gx_waves<UP>(), NT = 64 * NW, CO = 16 * NW;   // waves, threads, output columns
@@ -314,7 +344,7 @@ __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
 #define GX_FETCH(KC)                                                                                 \
   {                                                                                                  \
     _Pragma("unroll") for (int i = 0; i < NU; ++i)                                                   \
-      raw[i] = gx_fetch<CLS>(urow[i], (KC) * kGxKc + 16 * ((t + i * NT) & 3));                       \
+      raw[i] = gx_fetch<CLS, TL>(urow[i], (KC) * kGxKc + 16 * ((t + i * NT) & 3), ((t + i * NT) >> 2) & 15); \
     _Pragma("unroll") for (int i = 0; i < NX; ++i) {                                                 \
       const float4* src = reinterpret_cast<const float4*>(a.x + (size_t)xo[i] + (KC) * kGxKc);       \
       xv[i][0] = src[0];                                                                             \
@@ -392,24 +422,24 @@ __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
 
 #undef GX_FETCH
 
-template <int CLS, bool UP, int FORM>
+template <int CLS, bool UP, int FORM, bool TL>
 __global__ __launch_bounds__(64 * gx_waves<UP>()) void gx_kernel(const GxArgs a) {
   __shared__ GxLds<UP, CLS == GX_IQ3S, gx_tok<FORM>()> L;
-  gx_body<CLS, UP, FORM>(L, a, (int)blockIdx.x);
+  gx_body<CLS, UP, FORM, TL>(L, a, (int)blockIdx.x);
 }
 
 // The sorted form (class RCLS) and the Q8_0 shared expert's dense form in one launch: workgroups
 // below nra run the routed experts (args a), the rest the shared expert (args b) -- each part its
 // own launch's code, so the outputs are the separate launches' bit for bit.  The shared expert's
 // workgroups come last, filling the routed grid's last round.
-template <int RCLS, bool UP>
+template <int RCLS, bool UP, bool TL>
 __global__ __launch_bounds__(64 * gx_waves<UP>()) void gx_sh_kernel(const GxArgs a, const GxArgs b, int nra) {
   __shared__ GxLds<UP, RCLS == GX_IQ3S, gx_tok<GX_SORTED>()> L;   // the larger pass
   const int blk = (int)blockIdx.x;
   if (blk < nra)
-    gx_body<RCLS, UP, GX_SORTED>(L, a, blk);
+    gx_body<RCLS, UP, GX_SORTED, TL>(L, a, blk);
   else
-    gx_body<GX_Q80, UP, GX_DENSE>(L, b, blk - nra);
+    gx_body<GX_Q80, UP, GX_DENSE, false>(L, b, blk - nra);   // the shared expert: GGUF rows
 }
 
 // ------------------------------------------------------------------ decode form (GEMV-shaped)
@@ -435,10 +465,30 @@ template <> struct GvRaw<GX_Q80> { u4_t q0, q1, q2, q3; uint32_t d; };          
 // weights 128 h + 32 c + l and 128 h + 64 + 32 c + l), qh bytes 32 h .. 32 h + 31, scale bytes
 // 8 h + 2 c + {0, 1, 4, 5}.
 // Q8_0 (8 blocks of 34 B = unit): blocks 2 kq and 2 kq + 1.
-template <int CLS>
+// TL: the tiled layout (row: the row's start as in GGUF rows; its place in the tile is the lane's
+// col): lane l = 16 kq + col's bytes are one contiguous run of every record region.
+template <int CLS, bool TL = false>
 __device__ __forceinline__ GvRaw<CLS> gv_fetch(gbyte* row, int u, int kq) {
   GvRaw<CLS> r;
-  if constexpr (CLS == GX_IQ3S) {
+  if constexpr (TL && CLS == GX_IQ3S) {
+    const int col = (int)threadIdx.x & 15, l = 16 * kq + col;
+    gbyte* rec = row - (size_t)col * kIq3sRow + (size_t)u * 1760;
+    r.qs = gx_ld<u4_t>(rec + 16 * l);
+    const uint64_t sg = gx_ld<uint64_t>(rec + 1024 + 8 * l);
+    r.sg0 = (uint32_t)sg;
+    r.sg1 = (uint32_t)(sg >> 32);
+    r.dq = gx_ld<uint16_t>(rec + 1728 + 2 * col) | ((uint32_t)gx_ld<uint16_t>(rec + 1536 + 2 * l) << 16);
+    r.sc = rec[1664 + l];
+  } else if constexpr (TL && CLS == GX_Q6K) {
+    const int col = (int)threadIdx.x & 15, l = 16 * kq + col;
+    gbyte* rec = row - (size_t)col * kQ6kRow + (size_t)u * 3360;
+    r.ql0 = gx_ld<u4_t>(rec + 32 * l);
+    r.ql1 = gx_ld<u4_t>(rec + 32 * l + 16);
+    r.qh0 = gx_ld<u4_t>(rec + 2048 + 32 * (16 * (kq >> 1) + col));
+    r.qh1 = gx_ld<u4_t>(rec + 2048 + 32 * (16 * (kq >> 1) + col) + 16);
+    r.sc = gx_ld<uint32_t>(rec + 3072 + 4 * l);
+    r.d = gx_ld<uint16_t>(rec + 3328 + 2 * col);
+  } else if constexpr (CLS == GX_IQ3S) {
     gbyte* b = row + (size_t)u * 110;
     r.qs = gx_ld<u4_t>(b + 2 + 16 * kq);
     const uint64_t sg = gx_ld<uint64_t>(b + 74 + 8 * kq);
@@ -528,7 +578,7 @@ struct GvShape {
   static constexpr int LDX = K + 8;                      // token row stride (halfs)
 };
 
-template <int CLS, bool UP, int FORM, int KS, int NW>
+template <int CLS, bool UP, int FORM, int KS, int NW, bool TL>
 __global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
   using S = GvShape<CLS, UP, FORM, KS, NW>;
   constexpr int NT = 64 * NW;
@@ -594,7 +644,7 @@ __global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
 #pragma unroll
   for (int u = 0; u < DEPTH; ++u)
 #pragma unroll
-    for (int m = 0; m < NM; ++m) raw[u][m] = gv_fetch<CLS>(rows[m], u0 + u, kq);
+    for (int m = 0; m < NM; ++m) raw[u][m] = gv_fetch<CLS, TL>(rows[m], u0 + u, kq);
   __syncthreads();   // token rows, lookups
   const _Float16* xrow = xs + (FORM == GX_PAIRS ? 0 : col) * LDX;
   f4_t acc[NM];
@@ -604,7 +654,7 @@ __global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
   for (int u = 0; u < UW; ++u) {
     if (u + DEPTH < UW) {
 #pragma unroll
-      for (int m = 0; m < NM; ++m) raw[u + DEPTH][m] = gv_fetch<CLS>(rows[m], u0 + u + DEPTH, kq);
+      for (int m = 0; m < NM; ++m) raw[u + DEPTH][m] = gv_fetch<CLS, TL>(rows[m], u0 + u + DEPTH, kq);
     }
     const _Float16* xu = xrow + 256 * (u0 + u);
 #define GV_STEP(SS)                                                                          \
@@ -648,13 +698,13 @@ __global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
   }
 }
 
-template <int CLS, bool UP, int FORM, int KS, int NW>
+template <int CLS, bool UP, int FORM, int KS, int NW, bool TL = false>
 int gv_launch(const GxArgs& a, int items, hipStream_t st) {
   GxArgs b = a;
   b.items = items;
   constexpr int RB = GvShape<CLS, UP, FORM, KS, NW>::RB;
   const int nblk = FORM == GX_DENSE ? items * RB : (items + 7) / 8 * 8 * RB;
-  gv_kernel<CLS, UP, FORM, KS, NW><<<(unsigned)nblk, 64 * NW, 0, st>>>(b);
+  gv_kernel<CLS, UP, FORM, KS, NW, TL><<<(unsigned)nblk, 64 * NW, 0, st>>>(b);
   return tlx_launch_status();
 }
 
@@ -728,7 +778,7 @@ __device__ __forceinline__ void gq_tiles(const GqLds& L, const GxArgs& a, GvRaw<
 }
 
 // blk: the workgroup's index in its part of the grid (parts start at multiples of 8)
-template <int CLS, int FORM, int RB, int DEPTH>
+template <int CLS, int FORM, int RB, int DEPTH, bool TL>
 __device__ __forceinline__ void gq_dn_body(GqLds& L, const GxArgs& a, int blk) {
   constexpr int K = kFf, NU = K / 256, NW = 8;
   constexpr int ROWB = NU * gq_unit_bytes<CLS>();
@@ -754,7 +804,7 @@ __device__ __forceinline__ void gq_dn_body(GqLds& L, const GxArgs& a, int blk) {
   if (ntot <= 0) return;   // uniform per workgroup
   const int tile0 = rb * TILES + wave * TPW;
   gbyte* wrow = w + (size_t)(16 * tile0 + col) * ROWB;   // the lane's row in the wave's first tile
-  auto fetch = [&](int q) { return gv_fetch<CLS>(wrow + (size_t)(16 * (q / NU)) * ROWB, q % NU, kq); };
+  auto fetch = [&](int q) { return gv_fetch<CLS, TL>(wrow + (size_t)(16 * (q / NU)) * ROWB, q % NU, kq); };
 
   for (int p0 = 0; p0 < ntot; p0 += kGqTok) {
     const int nt = min(kGqTok, ntot - p0), ng = (nt + 15) >> 4;
@@ -808,10 +858,10 @@ __device__ __forceinline__ void gq_dn_body(GqLds& L, const GxArgs& a, int blk) {
   }
 }
 
-template <int CLS, int FORM, int RB, int DEPTH>
+template <int CLS, int FORM, int RB, int DEPTH, bool TL>
 __global__ __launch_bounds__(512) void gq_dn_kernel(const GxArgs a) {
   __shared__ GqLds L;
-  gq_dn_body<CLS, FORM, RB, DEPTH>(L, a, (int)blockIdx.x);
+  gq_dn_body<CLS, FORM, RB, DEPTH, TL>(L, a, (int)blockIdx.x);
 }
 
 #ifndef GQ_RRB
@@ -859,12 +909,12 @@ __global__ __launch_bounds__(256) void gx_dequant_kernel(const uint8_t* __restri
   }
 }
 
-template <int CLS, bool UP, int FORM>
+template <int CLS, bool UP, int FORM, bool TL = false>
 int gx_launch(const GxArgs& a, int items, hipStream_t st) {
   constexpr int RB = (UP ? kFf : kHid) / (16 * gx_waves<UP>());
   GxArgs b = a;
   b.items = items;
-  gx_kernel<CLS, UP, FORM><<<(unsigned)((items + 7) / 8 * 8 * RB), 64 * gx_waves<UP>(), 0, st>>>(b);
+  gx_kernel<CLS, UP, FORM, TL><<<(unsigned)((items + 7) / 8 * 8 * RB), 64 * gx_waves<UP>(), 0, st>>>(b);
   return tlx_launch_status();
 }
 
@@ -893,56 +943,68 @@ extern "C" int tlx_q8_0_dequant(const void* w, void* out, int64_t rows, int64_t 
   return tlx_launch_status();
 }
 
+// the slabs' layout argument: GGUF rows or this library's tiled records
+static bool ckpt_layout_ok(int layout) { return layout == TLX_LAYOUT_RAW || layout == TLX_LAYOUT_TILED; }
+
 extern "C" int tlx_moe_up3s(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const float* xs,
-                            const float* gridf, float* ys, int np, void* stream) {
+                            const float* gridf, float* ys, int np, int layout, void* stream) {
   TLX_RET_IF(!ptbl || !eoff || !plist || !xs || !gridf || !ys, TLX_E_ARG);
-  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs || !ckpt_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(ptbl, 8) || !tlx_aligned(xs, 16) || !tlx_aligned(gridf, 16) || !tlx_aligned(ys, 4), TLX_E_ALIGN);
   GxArgs a{};
   a.ptbl = ptbl; a.eoff = eoff; a.plist = plist; a.x = xs; a.grid = gridf; a.out = ys;
+  if (layout == TLX_LAYOUT_TILED) return gx_launch<GX_IQ3S, true, GX_SORTED, true>(a, kE, (hipStream_t)stream);
   return gx_launch<GX_IQ3S, true, GX_SORTED>(a, kE, (hipStream_t)stream);
 }
 
 extern "C" int tlx_moe_up3s_pairs(const uint64_t* ptbl, const uint16_t* eids, const float* xs, const float* gridf,
-                                  float* ys, int np, void* stream) {
+                                  float* ys, int np, int layout, void* stream) {
   TLX_RET_IF(!ptbl || !eids || !xs || !gridf || !ys, TLX_E_ARG);
-  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs || !ckpt_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(ptbl, 8) || !tlx_aligned(xs, 16) || !tlx_aligned(gridf, 16) || !tlx_aligned(ys, 4), TLX_E_ALIGN);
   GxArgs a{};
   a.ptbl = ptbl; a.eids = eids; a.x = xs; a.grid = gridf; a.out = ys;
+  if (layout == TLX_LAYOUT_TILED) return gv_launch<GX_IQ3S, true, GX_PAIRS, 4, 4, true>(a, np, (hipStream_t)stream);
   return gv_launch<GX_IQ3S, true, GX_PAIRS, 4, 4>(a, np, (hipStream_t)stream);
 }
 
 // the routed Q6_K down over the sorted pairs: the register-decode form (8-B stores a lane), else the
 // LDS-staged one
-static int dn6_sorted(GxArgs a, hipStream_t st) {
+template <bool TL>
+static int dn6_sorted_tl(GxArgs a, hipStream_t st) {
   a.items = kE;
   if (tlx_aligned(a.out, 8)) {
-    gq_dn_kernel<GX_Q6K, GX_SORTED, kGqRrb, kGqDepth><<<(unsigned)((kE + 7) / 8 * 8 * kGqRrb), 512, 0, st>>>(a);
+    gq_dn_kernel<GX_Q6K, GX_SORTED, kGqRrb, kGqDepth, TL><<<(unsigned)((kE + 7) / 8 * 8 * kGqRrb), 512, 0, st>>>(a);
     return tlx_launch_status();
   }
-  return gx_launch<GX_Q6K, false, GX_SORTED>(a, kE, st);
+  return gx_launch<GX_Q6K, false, GX_SORTED, TL>(a, kE, st);
+}
+
+static int dn6_sorted(const GxArgs& a, int layout, hipStream_t st) {
+  return layout == TLX_LAYOUT_TILED ? dn6_sorted_tl<true>(a, st) : dn6_sorted_tl<false>(a, st);
 }
 
 extern "C" int tlx_moe_dn6(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
-                           const uint16_t* plist, const float* act, uint16_t* parts, int np, void* stream) {
+                           const uint16_t* plist, const float* act, uint16_t* parts, int np, int layout,
+                           void* stream) {
   (void)items;   // the reference's slots; this form walks eoff / plist itself
   (void)nitp;
   TLX_RET_IF(!ptbl_dn || !eoff || !plist || !act || !parts, TLX_E_ARG);
-  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs || !ckpt_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(ptbl_dn, 8) || !tlx_aligned(act, 16) || !tlx_aligned(parts, 2), TLX_E_ALIGN);
   GxArgs a{};
   a.ptbl = ptbl_dn; a.eoff = eoff; a.plist = plist; a.x = act; a.out = parts;
-  return dn6_sorted(a, (hipStream_t)stream);
+  return dn6_sorted(a, layout, (hipStream_t)stream);
 }
 
 extern "C" int tlx_moe_dn6_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, uint16_t* parts,
-                                 int np, void* stream) {
+                                 int np, int layout, void* stream) {
   TLX_RET_IF(!ptbl_dn || !eids || !act || !parts, TLX_E_ARG);
-  TLX_RET_IF(np < 1 || np > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs || !ckpt_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(ptbl_dn, 8) || !tlx_aligned(act, 16) || !tlx_aligned(parts, 2), TLX_E_ALIGN);
   GxArgs a{};
   a.ptbl = ptbl_dn; a.eids = eids; a.x = act; a.out = parts;
+  if (layout == TLX_LAYOUT_TILED) return gv_launch<GX_Q6K, false, GX_PAIRS, 1, 4, true>(a, np, (hipStream_t)stream);
   return gv_launch<GX_Q6K, false, GX_PAIRS, 1, 4>(a, np, (hipStream_t)stream);
 }
 
@@ -962,22 +1024,22 @@ static int moe_shared8_dn(const void* wd, const float* act, float* y, int P, hip
 }
 
 // routed sorted form (a, kE items) + the shared expert's dense form (b) in one launch, P > kGvTok
-template <int RCLS, bool UP>
+template <int RCLS, bool UP, bool TL>
 static int gx_sh_launch(const GxArgs& a, const GxArgs& b, hipStream_t st) {
   constexpr int RB = (UP ? kFf : kHid) / (16 * gx_waves<UP>());
   GxArgs ra = a, sb = b;
   ra.items = kE;
   sb.items = (b.P + gx_tok<GX_DENSE>() - 1) / gx_tok<GX_DENSE>();
   const int nra = (kE + 7) / 8 * 8 * RB, nsb = (sb.items + 7) / 8 * 8 * RB;
-  gx_sh_kernel<RCLS, UP><<<(unsigned)(nra + nsb), 64 * gx_waves<UP>(), 0, st>>>(ra, sb, nra);
+  gx_sh_kernel<RCLS, UP, TL><<<(unsigned)(nra + nsb), 64 * gx_waves<UP>(), 0, st>>>(ra, sb, nra);
   return tlx_launch_status();
 }
 
 extern "C" int tlx_moe_up3s_sh(const uint64_t* ptbl, const int* eoff, const uint16_t* plist, const float* xs,
                                const float* gridf, float* ys, int np, const void* wg8, const void* wu8, float* sact,
-                               int P, void* stream) {
+                               int P, int layout, void* stream) {
   TLX_RET_IF(!ptbl || !eoff || !plist || !xs || !gridf || !ys || !wg8 || !wu8 || !sact, TLX_E_ARG);
-  TLX_RET_IF(np < 1 || np > kMaxPairs || P < 1 || P > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs || P < 1 || P > kMaxPairs || !ckpt_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(ptbl, 8) || !tlx_aligned(xs, 16) || !tlx_aligned(gridf, 16) || !tlx_aligned(ys, 4),
              TLX_E_ALIGN);
   TLX_RET_IF(!tlx_aligned(wg8, 2) || !tlx_aligned(wu8, 2) || !tlx_aligned(sact, 16), TLX_E_ALIGN);
@@ -985,42 +1047,45 @@ extern "C" int tlx_moe_up3s_sh(const uint64_t* ptbl, const int* eoff, const uint
   GxArgs a{};
   a.ptbl = ptbl; a.eoff = eoff; a.plist = plist; a.x = xs; a.grid = gridf; a.out = ys;
   if (P <= kGvTok) {   // the shared expert's decode form is another kernel: two launches
-    const int rc = gx_launch<GX_IQ3S, true, GX_SORTED>(a, kE, st);
+    const int rc = layout == TLX_LAYOUT_TILED ? gx_launch<GX_IQ3S, true, GX_SORTED, true>(a, kE, st)
+                                              : gx_launch<GX_IQ3S, true, GX_SORTED>(a, kE, st);
     TLX_RET_IF(rc != TLX_OK, rc);
     return moe_shared8_up(wg8, wu8, xs, sact, P, st);
   }
   GxArgs b{};
   b.w0 = (const uint8_t*)wg8; b.w1 = (const uint8_t*)wu8; b.x = xs; b.out = sact; b.P = P;
-  return gx_sh_launch<GX_IQ3S, true>(a, b, st);
+  if (layout == TLX_LAYOUT_TILED) return gx_sh_launch<GX_IQ3S, true, true>(a, b, st);
+  return gx_sh_launch<GX_IQ3S, true, false>(a, b, st);
 }
 
 extern "C" int tlx_moe_dn6_sh(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
                               const uint16_t* plist, const float* act, uint16_t* parts, int np, const void* wd8,
-                              const float* sact, float* shared, int P, void* stream) {
+                              const float* sact, float* shared, int P, int layout, void* stream) {
   (void)items;   // the reference's slots; this form walks eoff / plist itself
   (void)nitp;
   TLX_RET_IF(!ptbl_dn || !eoff || !plist || !act || !parts || !wd8 || !sact || !shared, TLX_E_ARG);
-  TLX_RET_IF(np < 1 || np > kMaxPairs || P < 1 || P > kMaxPairs, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs || P < 1 || P > kMaxPairs || !ckpt_layout_ok(layout), TLX_E_ARG);
   TLX_RET_IF(!tlx_aligned(ptbl_dn, 8) || !tlx_aligned(act, 16) || !tlx_aligned(parts, 2), TLX_E_ALIGN);
   TLX_RET_IF(!tlx_aligned(wd8, 2) || !tlx_aligned(sact, 16) || !tlx_aligned(shared, 4), TLX_E_ALIGN);
   const hipStream_t st = (hipStream_t)stream;
   GxArgs a{};
   a.ptbl = ptbl_dn; a.eoff = eoff; a.plist = plist; a.x = act; a.out = parts;
   if (P <= kGvTok) {
-    const int rc = dn6_sorted(a, st);
+    const int rc = dn6_sorted(a, layout, st);
     TLX_RET_IF(rc != TLX_OK, rc);
     return moe_shared8_dn(wd8, sact, shared, P, st);
   }
   if (tlx_aligned(parts, 8)) {
     // the routed register-decode form and the shared expert's staged form: two launches (their LDS
     // footprints differ: in one launch the shared part would run at one workgroup per CU)
-    const int rc = dn6_sorted(a, st);
+    const int rc = dn6_sorted(a, layout, st);
     TLX_RET_IF(rc != TLX_OK, rc);
     return moe_shared8_dn(wd8, sact, shared, P, st);
   }
   GxArgs b{};
   b.w0 = (const uint8_t*)wd8; b.x = sact; b.out = shared; b.P = P;
-  return gx_sh_launch<GX_Q6K, false>(a, b, st);
+  if (layout == TLX_LAYOUT_TILED) return gx_sh_launch<GX_Q6K, false, true>(a, b, st);
+  return gx_sh_launch<GX_Q6K, false, false>(a, b, st);
 }
 
 extern "C" int tlx_moe_shared8(const void* wg, const void* wu, const void* wd, const float* x, float* y, float* act,
@@ -1033,4 +1098,64 @@ extern "C" int tlx_moe_shared8(const void* wg, const void* wu, const void* wd, c
   const int r = moe_shared8_up(wg, wu, x, act, P, st);   // decode (P <= 16): the GEMV-shaped form
   TLX_RET_IF(r != TLX_OK, r);
   return moe_shared8_dn(wd, act, y, P, st);
+}
+
+// ------------------------------------------------------------------ tiled checkpoint slabs
+// One thread per output byte of record (tile, block): the byte's lane l = 16 kq + col (or row col)
+// names the GGUF row 16 tile + col and the block byte it copies.
+template <int CLS>
+__global__ __launch_bounds__(256) void pack_ckpt_tiled_kernel(const uint8_t* __restrict__ src,
+                                                              uint8_t* __restrict__ dst, long nbytes, int nb) {
+  constexpr int REC = CLS == GX_IQ3S ? 1760 : 3360, BB = CLS == GX_IQ3S ? 110 : 210;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nbytes) return;
+  const long u = i / REC;
+  const int o = (int)(i - u * REC);
+  const long tile = u / nb;
+  const int b = (int)(u - tile * nb);
+  int col, sb;   // row in the tile, byte in its block
+  if constexpr (CLS == GX_IQ3S) {
+    if (o < 1024) {
+      col = (o >> 4) & 15; sb = 2 + 16 * (o >> 8) + (o & 15);
+    } else if (o < 1536) {
+      const int q = o - 1024; col = (q >> 3) & 15; sb = 74 + 8 * (q >> 7) + (q & 7);
+    } else if (o < 1664) {
+      const int q = o - 1536; col = (q >> 1) & 15; sb = 66 + 2 * (q >> 5) + (q & 1);
+    } else if (o < 1728) {
+      const int q = o - 1664; col = q & 15; sb = 106 + (q >> 4);
+    } else {
+      const int q = o - 1728; col = q >> 1; sb = q & 1;
+    }
+  } else {
+    if (o < 2048) {
+      col = (o >> 5) & 15; sb = 32 * (o >> 9) + (o & 31);
+    } else if (o < 3072) {
+      const int q = o - 2048; col = (q >> 5) & 15; sb = 128 + 32 * (q >> 9) + (q & 31);
+    } else if (o < 3328) {
+      const int q = o - 3072, kq = q >> 6, s = q & 3;
+      col = (q >> 2) & 15; sb = 192 + 8 * (kq >> 1) + 2 * (kq & 1) + (s & 1) + 4 * (s >> 1);
+    } else {
+      const int q = o - 3328; col = q >> 1; sb = 208 + (q & 1);
+    }
+  }
+  dst[i] = src[(tile * 16 + col) * (long)nb * BB + (long)b * BB + sb];
+}
+
+template <int CLS>
+static int pack_ckpt_tiled(const void* src, void* tiled, int N, int K, void* stream) {
+  TLX_RET_IF(!src || !tiled, TLX_E_ARG);
+  TLX_RET_IF(N < 16 || (N % 16) || K < 256 || (K % 256), TLX_E_ARG);
+  const long nbytes = (long)(N / 16) * (K / 256) * (CLS == GX_IQ3S ? 1760 : 3360);
+  TLX_RET_IF((nbytes + 255) / 256 > 0x7fffffff, TLX_E_ARG);
+  pack_ckpt_tiled_kernel<CLS><<<(unsigned)((nbytes + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      (const uint8_t*)src, (uint8_t*)tiled, nbytes, K / 256);
+  return tlx_launch_status();
+}
+
+extern "C" int tlx_pack_iq3s_tiled(const void* src, void* tiled, int N, int K, void* stream) {
+  return pack_ckpt_tiled<GX_IQ3S>(src, tiled, N, K, stream);
+}
+
+extern "C" int tlx_pack_q6k_tiled(const void* src, void* tiled, int N, int K, void* stream) {
+  return pack_ckpt_tiled<GX_Q6K>(src, tiled, N, K, stream);
 }

@@ -543,6 +543,27 @@ def pack_iq4_tiled(src, tiled, N, K, stream=None):
     return tiled
 
 
+def pack_iq3s_tiled(src, tiled, N, K, stream=None):
+    """IQ3_S GGUF rows u8[N][K/256*110] -> the tiled records the checkpoint-class expert GEMMs read
+    with ``layout=LAYOUT_TILED`` (same size: a byte permutation per 16-row tile and 256-k block)."""
+    nbytes = N * (K // 256) * 110
+    _need(src, nbytes, "src")
+    _need(tiled, nbytes, "tiled")
+    _dev(src, tiled)
+    call("tlx_pack_iq3s_tiled", src.data_ptr(), tiled.data_ptr(), N, K, _stream(stream))
+    return tiled
+
+
+def pack_q6k_tiled(src, tiled, N, K, stream=None):
+    """Q6_K GGUF rows u8[N][K/256*210] -> the tiled records of ``layout=LAYOUT_TILED`` (same size)."""
+    nbytes = N * (K // 256) * 210
+    _need(src, nbytes, "src")
+    _need(tiled, nbytes, "tiled")
+    _dev(src, tiled)
+    call("tlx_pack_q6k_tiled", src.data_ptr(), tiled.data_ptr(), N, K, _stream(stream))
+    return tiled
+
+
 def p8_quant(x16, xq, sx, rs, stream=None):
     """Per (row, 128-k chunk) int8 quantization of fp16 activations (pfk_q8: kernel(x, xq, sx, rs))."""
     M, K = x16.shape
@@ -805,9 +826,10 @@ def moe_combine(parts, gates, sg, shared, hres, y, stream=None):
 
 
 # ---- the checkpoint's classes: IQ3_S routed gate/up, Q6_K routed down, Q8_0 shared expert
-def moe_up3s(ptbl, eoff, plist, xs, gridf, ys, stream=None):
+def moe_up3s(ptbl, eoff, plist, xs, gridf, ys, stream=None, layout=LAYOUT_RAW):
     """gxu_gm(ptbl, eoff, plist, xs, gridf, ys) over the sorted pairs (IQ3_S slabs: 512 gate rows
-    then 512 up rows 450,560 B in, 880 B a row): ys[pair][512] = silu(Wg_e . x[pos]) * (Wu_e . x[pos])."""
+    then 512 up rows 450,560 B in, 880 B a row): ys[pair][512] = silu(Wg_e . x[pos]) * (Wu_e . x[pos]).
+    ``layout=LAYOUT_TILED``: slabs repacked by pack_iq3s_tiled (same results bit for bit)."""
     n = ys.shape[0]
     _need(ptbl, 256 * 8, "ptbl")
     _need(eoff, 257 * 4, "eoff")
@@ -817,10 +839,10 @@ def moe_up3s(ptbl, eoff, plist, xs, gridf, ys, stream=None):
     _need(gridf, 512 * 16, "gridf")
     _dev(ptbl, eoff, plist, xs, gridf, ys)
     call("tlx_moe_up3s", ptbl.data_ptr(), eoff.data_ptr(), plist.data_ptr(), xs.data_ptr(), gridf.data_ptr(),
-         ys.data_ptr(), n, _stream(stream))
+         ys.data_ptr(), n, layout, _stream(stream))
 
 
-def moe_up3s_pairs(ptbl, eids, xs, gridf, ys, stream=None):
+def moe_up3s_pairs(ptbl, eids, xs, gridf, ys, stream=None, layout=LAYOUT_RAW):
     """gx8e256up(ptbl, eids, xs, gridf, ys): pair p runs IQ3_S expert eids[p] on x[p >> 3], no sort."""
     n = ys.shape[0]
     _need(ptbl, 256 * 8, "ptbl")
@@ -830,12 +852,13 @@ def moe_up3s_pairs(ptbl, eids, xs, gridf, ys, stream=None):
     _need(gridf, 512 * 16, "gridf")
     _dev(ptbl, eids, xs, gridf, ys)
     call("tlx_moe_up3s_pairs", ptbl.data_ptr(), eids.data_ptr(), xs.data_ptr(), gridf.data_ptr(), ys.data_ptr(),
-         n, _stream(stream))
+         n, layout, _stream(stream))
 
 
-def moe_dn6(ptbl_dn, items, nitp, eoff, plist, act, parts, stream=None):
+def moe_dn6(ptbl_dn, items, nitp, eoff, plist, act, parts, stream=None, layout=LAYOUT_RAW):
     """gxm_dn6(ptbl, items, nitp, eoff, plist, act, parts) over the sorted pairs (Q6_K slabs of
-    2048 rows x 420 B): parts[pair][2048] = fp16(Wd_e . act[pair])."""
+    2048 rows x 420 B): parts[pair][2048] = fp16(Wd_e . act[pair]).  ``layout=LAYOUT_TILED``: slabs
+    repacked by pack_q6k_tiled."""
     n = act.shape[0]
     _need(ptbl_dn, 256 * 8, "ptbl_dn")
     _need(eoff, 257 * 4, "eoff")
@@ -845,10 +868,10 @@ def moe_dn6(ptbl_dn, items, nitp, eoff, plist, act, parts, stream=None):
     _dev(ptbl_dn, eoff, plist, act, parts)
     call("tlx_moe_dn6", ptbl_dn.data_ptr(), 0 if items is None else items.data_ptr(),
          0 if nitp is None else nitp.data_ptr(), eoff.data_ptr(), plist.data_ptr(), act.data_ptr(), parts.data_ptr(),
-         n, _stream(stream))
+         n, layout, _stream(stream))
 
 
-def moe_up3s_sh(ptbl, eoff, plist, xs, gridf, ys, wg8, wu8, sact, stream=None):
+def moe_up3s_sh(ptbl, eoff, plist, xs, gridf, ys, wg8, wu8, sact, stream=None, layout=LAYOUT_RAW):
     """moe_up3s over the sorted pairs and the Q8_0 shared expert's gate+up (wg8 / wu8 rows, into
     sact [P][512], P = xs.shape[0]) in one launch above P = 16 (else the two launches); outputs
     those of moe_up3s and moe_shared8's gate+up bit for bit."""
@@ -865,10 +888,10 @@ def moe_up3s_sh(ptbl, eoff, plist, xs, gridf, ys, wg8, wu8, sact, stream=None):
     _need(sact, P * 512 * 4, "sact")
     _dev(ptbl, eoff, plist, xs, gridf, ys, wg8, wu8, sact)
     call("tlx_moe_up3s_sh", ptbl.data_ptr(), eoff.data_ptr(), plist.data_ptr(), xs.data_ptr(), gridf.data_ptr(),
-         ys.data_ptr(), n, wg8.data_ptr(), wu8.data_ptr(), sact.data_ptr(), P, _stream(stream))
+         ys.data_ptr(), n, wg8.data_ptr(), wu8.data_ptr(), sact.data_ptr(), P, layout, _stream(stream))
 
 
-def moe_dn6_sh(ptbl_dn, items, nitp, eoff, plist, act, parts, wd8, sact, shared, stream=None):
+def moe_dn6_sh(ptbl_dn, items, nitp, eoff, plist, act, parts, wd8, sact, shared, stream=None, layout=LAYOUT_RAW):
     """moe_dn6 over the sorted pairs and the Q8_0 shared expert's down projection (wd8 rows, sact
     [P][512] into shared [P][2048] f32, P = sact.shape[0]) in one launch above P = 16 (else the
     two launches); outputs those of the separate calls bit for bit."""
@@ -884,10 +907,10 @@ def moe_dn6_sh(ptbl_dn, items, nitp, eoff, plist, act, parts, wd8, sact, shared,
     _dev(ptbl_dn, eoff, plist, act, parts, wd8, sact, shared)
     call("tlx_moe_dn6_sh", ptbl_dn.data_ptr(), None if items is None else items.data_ptr(),
          None if nitp is None else nitp.data_ptr(), eoff.data_ptr(), plist.data_ptr(), act.data_ptr(),
-         parts.data_ptr(), n, wd8.data_ptr(), sact.data_ptr(), shared.data_ptr(), P, _stream(stream))
+         parts.data_ptr(), n, wd8.data_ptr(), sact.data_ptr(), shared.data_ptr(), P, layout, _stream(stream))
 
 
-def moe_dn6_pairs(ptbl_dn, eids, act, parts, stream=None):
+def moe_dn6_pairs(ptbl_dn, eids, act, parts, stream=None, layout=LAYOUT_RAW):
     """gx8e256dn6(ptbl, eids, act, parts): pair p runs Q6_K expert eids[p] on act[p], no sort."""
     n = act.shape[0]
     _need(ptbl_dn, 256 * 8, "ptbl_dn")
@@ -895,7 +918,7 @@ def moe_dn6_pairs(ptbl_dn, eids, act, parts, stream=None):
     _need(act, n * 512 * 4, "act")
     _need(parts, n * 2048 * 2, "parts")
     _dev(ptbl_dn, eids, act, parts)
-    call("tlx_moe_dn6_pairs", ptbl_dn.data_ptr(), eids.data_ptr(), act.data_ptr(), parts.data_ptr(), n,
+    call("tlx_moe_dn6_pairs", ptbl_dn.data_ptr(), eids.data_ptr(), act.data_ptr(), parts.data_ptr(), n, layout,
          _stream(stream))
 
 
@@ -999,7 +1022,7 @@ def moe_layer(logits, sg, xs, hres, y, ptbl, ptbl_dn, ptbl_sh, iq4nl, scratch, s
 
 
 def moe_layer_ckpt(logits, sg, xs, hres, y, ptbl, ptbl_dn, shared8, gridf, scratch, stream=None, down="q6k",
-                   iq4nl=None, pair_walk=None, overlap_shared=None):
+                   iq4nl=None, pair_walk=None, overlap_shared=None, layout=LAYOUT_RAW):
     """One MoE layer with the reference checkpoint's classes, the same sequence as moe_layer:
     top-8, then the pair walk (P <= MOE_PAIR_WALK_MAX_P by default) or sort + grouped forms for
     the IQ3_S gate+up, the down projection -- ``down`` "q6k" (Q6_K slabs, the checkpoint's layers
@@ -1007,7 +1030,8 @@ def moe_layer_ckpt(logits, sg, xs, hres, y, ptbl, ptbl_dn, shared8, gridf, scrat
     (shared8 = (wg, wu, wd) rows), and the combine into y.  overlap_shared as moe_layer's: by
     default the shared expert rides in the grouped launches (moe_up3s_sh / moe_dn6_sh; the pair
     walk keeps its own two launches, the decode form being another kernel); with it, on a second
-    stream joined before the combine."""
+    stream joined before the combine.  ``layout`` (LAYOUT_RAW or LAYOUT_TILED) is that of the routed
+    slabs, gate/up and down alike (pack_iq3s_tiled, pack_q6k_tiled / pack_iq4_tiled)."""
     sc = scratch
     if pair_walk is None:
         pair_walk = xs.shape[0] <= MOE_PAIR_WALK_MAX_P
@@ -1028,24 +1052,25 @@ def moe_layer_ckpt(logits, sg, xs, hres, y, ptbl, ptbl_dn, shared8, gridf, scrat
     # shared expert keeps its own two launches)
     fused = side is None and not pair_walk and down == "q6k"
     if pair_walk:
-        moe_up3s_pairs(ptbl, eids, xs, gridf, sc.act, stream=cur)
+        moe_up3s_pairs(ptbl, eids, xs, gridf, sc.act, stream=cur, layout=layout)
         if down == "q6k":
-            moe_dn6_pairs(ptbl_dn, eids, sc.act, sc.parts, stream=cur)
+            moe_dn6_pairs(ptbl_dn, eids, sc.act, sc.parts, stream=cur, layout=layout)
         else:
-            moe_dn4_pairs(ptbl_dn, eids, sc.act, iq4nl, sc.parts, stream=cur)
+            moe_dn4_pairs(ptbl_dn, eids, sc.act, iq4nl, sc.parts, stream=cur, layout=layout)
     else:
         moe_sort(sc.eids, sc.eoff, sc.plist, sc.items, sc.nitp, stream=cur)
         if fused:
-            moe_up3s_sh(ptbl, sc.eoff, sc.plist, xs, gridf, sc.act, wg8, wu8, sc.sact, stream=cur)
+            moe_up3s_sh(ptbl, sc.eoff, sc.plist, xs, gridf, sc.act, wg8, wu8, sc.sact, stream=cur, layout=layout)
         else:
-            moe_up3s(ptbl, sc.eoff, sc.plist, xs, gridf, sc.act, stream=cur)
+            moe_up3s(ptbl, sc.eoff, sc.plist, xs, gridf, sc.act, stream=cur, layout=layout)
         if fused:
             moe_dn6_sh(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, sc.parts, wd8, sc.sact, sc.shared,
-                       stream=cur)
+                       stream=cur, layout=layout)
         elif down == "q6k":
-            moe_dn6(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, sc.parts, stream=cur)
+            moe_dn6(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, sc.parts, stream=cur, layout=layout)
         else:
-            moe_dn4(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, iq4nl, sc.parts, stream=cur)
+            moe_dn4(ptbl_dn, sc.items, sc.nitp, sc.eoff, sc.plist, sc.act, iq4nl, sc.parts, stream=cur,
+                    layout=layout)
     if side is not None:
         cur.wait_stream(side)
     elif not fused:
