@@ -369,7 +369,7 @@ __device__ __forceinline__ void gx_body(LDS& L, const GxArgs& a, int blk) {
 #pragma unroll
       for (int i = 0; i < NX; ++i) {
         const int pc = t + i * NT;
-        if (pc < TOK * kGxKc / 8) {
+        if (pc < 16 * ng * (kGxKc / 8)) {   // the pass's 16-token groups only (the MFMAs read no other row)
           const float4 z = float4{0.f, 0.f, 0.f, 0.f};
           const float4 u = xz[i] ? z : xv[i][0], w = xz[i] ? z : xv[i][1];
           const h8_t h = {(_Float16)u.x, (_Float16)u.y, (_Float16)u.z, (_Float16)u.w,
