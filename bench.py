@@ -500,7 +500,8 @@ def moe_ckpt_leg(ops, formats, synth, torch, dev, steps, warmup):
         wbytes = hit * (2 * F * 880 + H * 420) + 2 * F * 2176 + H * 544
         tflops = flops / (t * 1e-3) / 1e12
         gbs = wbytes / (t * 1e-3) / 1e9
-        route = "pair walk" if P <= ops.MOE_PAIR_WALK_MAX_P else "sort + sorted forms with the shared expert inside"
+        route = ("pair walk with the shared expert inside" if P <= ops.MOE_PAIR_WALK_MAX_P else
+                 "sort + sorted forms with the shared expert inside")
         out[f"M{P}"] = {"ms": round(t, 4), "tflops": round(tflops, 2), "experts_hit": hit, "weight_gbs": round(gbs, 1),
                         "route": route, "slabs": "tiled records", "ms_gguf_rows": round(t_rows, 4),
                         "roofline": (hbm_roofline(gbs, f"checkpoint-class MoE layer ({route}; graph): expert bytes / "

@@ -490,6 +490,17 @@ int tlx_moe_up3s_sh(const uint64_t* ptbl, const int* eoff, const uint16_t* plist
 int tlx_moe_dn6_sh(const uint64_t* ptbl_dn, const uint32_t* items, const uint32_t* nitp, const int* eoff,
                    const uint16_t* plist, const float* act, uint16_t* parts, int np, const void* wd8,
                    const float* sact, float* shared, int P, int layout, void* stream);
+/* The pair walks (tlx_moe_up3s_pairs / tlx_moe_dn6_pairs) and the Q8_0 shared expert's decode forms
+ * (tlx_moe_shared8's two launches) in one launch each at P <= 16 (else the two launches): the shared
+ * expert's workgroups follow the pairs' and read their token rows from memory (no LDS staging, so
+ * the pair walk keeps its occupancy).  No counterpart in the reference (gx8e256up / gx8e256dn6 and
+ * shexp8 are separate launches); outputs those of the separate calls bit for bit.  sact f32 [P][512]
+ * (16-B aligned) and shared f32 [P][2048] as tlx_moe_shared8's act / y. */
+int tlx_moe_up3s_pairs_sh(const uint64_t* ptbl, const uint16_t* eids, const float* xs, const float* gridf,
+                          float* ys, int np, const void* wg8, const void* wu8, float* sact, int P, int layout,
+                          void* stream);
+int tlx_moe_dn6_pairs_sh(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, uint16_t* parts, int np,
+                         const void* wd8, const float* sact, float* shared, int P, int layout, void* stream);
 /* The Q8_0 shared expert over P positions: y[P][2048] f32 = Wd . (silu(Wg . x) * (Wu . x)), with act
  * f32[P][512] caller scratch (two launches on the stream; P <= 16 the decode form).  Replaces shexp8
  * (engine/mm/MM_P2_shexp8.cu:8-13): shexp8(wg [512][2176], wu [512][2176], wd [2048][544], x, y).

@@ -185,3 +185,8 @@ def test_moe_checkpoint_fused_argument_validation():
     assert L.tlx_moe_dn6_sh(p, None, None, p, p, p, p, 16385, p, p, p, 4, R, None) == _lib.TLX_E_ARG
     assert L.tlx_moe_dn6_sh(p, None, None, p, p, p, p, 32, p, p, p, 4, 9, None) == _lib.TLX_E_ARG   # layout
     assert L.tlx_moe_dn6_sh(p, None, None, p, p, p, p, 32, p + 1, p, p, 4, R, None) == _lib.TLX_E_ALIGN  # wd8
+    assert L.tlx_moe_up3s_pairs_sh(p, p, p, p, p, 0, p, p, p, 1, R, None) == _lib.TLX_E_ARG          # no pairs
+    assert L.tlx_moe_up3s_pairs_sh(p, p, p, p, p, 8, p, p, p, 1, 2, None) == _lib.TLX_E_ARG          # layout
+    assert L.tlx_moe_up3s_pairs_sh(p, p, p, p, p, 8, p, p, p + 4, 1, R, None) == _lib.TLX_E_ALIGN    # sact
+    assert L.tlx_moe_dn6_pairs_sh(p, p, p, p, 8, p, p, p, 0, R, None) == _lib.TLX_E_ARG              # no positions
+    assert L.tlx_moe_dn6_pairs_sh(p, p, p, p, 8, p, p + 4, p, 1, R, None) == _lib.TLX_E_ALIGN        # sact

@@ -278,6 +278,36 @@ def test_ckpt_tiled_forms_bit_identical(gpu, ckpt, ckpt_tiled, P):
     _check_pairs(ckpt, x, eids, til["act"], til["parts"], list(range(0, np_, 7)))
 
 
+@pytest.mark.parametrize("P,lay", [(1, LAYOUT_RAW), (11, LAYOUT_TILED), (16, LAYOUT_RAW), (17, LAYOUT_TILED)])
+def test_ckpt_pairs_shared_fused(gpu, ckpt, ckpt_tiled, P, lay):
+    """moe_up3s_pairs_sh / moe_dn6_pairs_sh (the pair walks and the Q8_0 shared expert in one launch
+    each at P <= 16, the two launches at P = 17) against moe_up3s_pairs / moe_dn6_pairs /
+    moe_shared8, bit for bit; the shared expert against the oracle."""
+    print(f"[case] pair walks + Q8_0 shared expert in one launch, P={P} layout={lay}", flush=True)
+    rng = np.random.default_rng(90 + P)
+    x, eids, deids, eoff, plist, items, nitp = _route(gpu, rng, P)
+    dx = torch.from_numpy(x).to(gpu)
+    np_ = 8 * P
+    pt, pd = (ckpt["ptbl"], ckpt["ptbl_dn"]) if lay == LAYOUT_RAW else (ckpt_tiled["ptbl"], ckpt_tiled["ptbl_dn"])
+    mk = lambda shape, dt, v: torch.full(shape, v, dtype=dt, device=gpu)
+    sep = dict(act=mk((np_, moe.FF), torch.float32, -3.0), parts=mk((np_, moe.HID), torch.float16, -3.0),
+               sact=mk((P, moe.FF), torch.float32, -3.0), shared=mk((P, moe.HID), torch.float32, -3.0))
+    fus = {k: torch.full_like(v, -5.0) for k, v in sep.items()}
+    wg8, wu8, wd8 = ckpt["dsh"]
+    ops.moe_up3s_pairs(pt, deids, dx, ckpt["gridf"], sep["act"], layout=lay)
+    ops.moe_dn6_pairs(pd, deids, sep["act"], sep["parts"], layout=lay)
+    ops.moe_shared8(wg8, wu8, wd8, dx, sep["shared"], sep["sact"])
+    ops.moe_up3s_pairs_sh(pt, deids, dx, ckpt["gridf"], fus["act"], wg8, wu8, fus["sact"], layout=lay)
+    ops.moe_dn6_pairs_sh(pd, deids, fus["act"], fus["parts"], wd8, fus["sact"], fus["shared"], layout=lay)
+    torch.cuda.synchronize()
+    for k in sep:
+        a, b = sep[k].cpu().numpy(), fus[k].cpu().numpy()
+        v = np.uint16 if a.dtype == np.float16 else np.uint32
+        assert np.array_equal(a.view(v), b.view(v)), k
+    ref = moe.shared8_ref(*ckpt["shared"], x)
+    assert _rows_err(fus["shared"].cpu().numpy(), ref) <= TOL
+
+
 def test_ckpt_argument_validation(gpu, ckpt):
     dx = torch.zeros(2, moe.HID, device=gpu)
     act = torch.empty(16, moe.FF, dtype=torch.float32, device=gpu)

@@ -100,6 +100,8 @@ SIGNATURES = {
     "tlx_moe_up3s_pairs": [_p, _p, _p, _p, _p, _i, _i, _p],
     "tlx_moe_dn6": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _p],
     "tlx_moe_dn6_pairs": [_p, _p, _p, _p, _i, _i, _p],
+    "tlx_moe_up3s_pairs_sh": [_p, _p, _p, _p, _p, _i, _p, _p, _p, _i, _i, _p],
+    "tlx_moe_dn6_pairs_sh": [_p, _p, _p, _p, _i, _p, _p, _p, _i, _i, _p],
     "tlx_moe_shared8": [_p, _p, _p, _p, _p, _p, _i, _p],
     "tlx_moe_up3s_sh": [_p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _i, _i, _p],
     "tlx_moe_dn6_sh": [_p, _p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _i, _i, _p],

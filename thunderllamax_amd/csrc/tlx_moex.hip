@@ -586,8 +586,12 @@ struct GvShape {
   static constexpr int LDX = K + 8;                      // token row stride (halfs)
 };
 
-template <int CLS, bool UP, int FORM, int KS, int NW, bool TL>
-__global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
+// XD (the dense form at P <= kGvTok): the token rows are read from memory (f32 -> fp16, as staged)
+// a unit at a time instead of staged in LDS -- no LDS but the k-split sums, so the form can share a
+// launch with a pair walk (tlx_moe_up3s_pairs_sh) without lowering its occupancy; the same operands.
+template <int CLS, bool UP, int FORM, int KS, int NW, bool TL, bool XD>
+__device__ __forceinline__ void gv_body(_Float16* xs, GvLutSlot<CLS == GX_IQ3S>& lslot, f4_t* red, const GxArgs& a,
+                                        int blk) {
   using S = GvShape<CLS, UP, FORM, KS, NW>;
   constexpr int NT = 64 * NW;
   constexpr int K = S::K, NU = S::NU, NM = S::NM, TW = S::TW, RB = S::RB, TOKR = S::TOKR, LDX = S::LDX;
@@ -596,20 +600,18 @@ __global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
   constexpr int DEPTH = UW < 4 ? UW : 4;                 // units in flight
   constexpr bool GRID = CLS == GX_IQ3S;
   static_assert(NU % KS == 0 && NW % KS == 0, "k split");
-  __shared__ __attribute__((aligned(16))) _Float16 xs[TOKR * LDX];
-  __shared__ GvLutSlot<GRID> lslot;
-  __shared__ f4_t red[KS > 1 ? (KS - 1) * TW * NM * 64 : 1];
+  static_assert(!XD || FORM == GX_DENSE, "direct token rows: the dense form");
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 15, kq = lane >> 4;
   const int tile = wave / KS, kp = wave % KS;
   // the XCD-aware order of gx_kernel: an item's workgroups on one XCD
   int rb, item;
   if constexpr (FORM == GX_DENSE) {   // one item at decode: its column blocks over all XCDs
-    rb = (int)blockIdx.x % RB;
-    item = (int)blockIdx.x / RB;
+    rb = blk % RB;
+    item = blk / RB;
   } else {
-    const int slot = (int)blockIdx.x >> 3;
+    const int slot = blk >> 3;
     rb = slot % RB;
-    item = slot / RB * 8 + ((int)blockIdx.x & 7);
+    item = slot / RB * 8 + (blk & 7);
   }
   if (item >= a.items) return;
 
@@ -633,7 +635,7 @@ __global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
   // token rows, fp16 (round to nearest even); rows past the item repeat its last (not stored)
   // (dense: the item's nt rows only -- the lanes of rows past it read unstaged LDS, and their
   // MFMA rows are never stored)
-  for (int pc = t; pc < (FORM == GX_DENSE ? nt : TOKR) * (K / 8); pc += NT) {
+  for (int pc = t; pc < (XD ? 0 : FORM == GX_DENSE ? nt : TOKR) * (K / 8); pc += NT) {
     const int r = pc / (K / 8), k8 = pc - r * (K / 8);
     const int xr = FORM == GX_PAIRS ? (UP ? beg >> 3 : beg) : beg + min(r, nt - 1);
     const float4* src = reinterpret_cast<const float4*>(a.x + (size_t)xr * K + 8 * k8);
@@ -655,6 +657,7 @@ __global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
     for (int m = 0; m < NM; ++m) raw[u][m] = gv_fetch<CLS, TL>(rows[m], u0 + u, kq);
   __syncthreads();   // token rows, lookups
   const _Float16* xrow = xs + (FORM == GX_PAIRS ? 0 : col) * LDX;
+  const float* xgrow = a.x + (size_t)(beg + min(col, nt - 1)) * K;   // XD: the lane's token row
   f4_t acc[NM];
 #pragma unroll
   for (int m = 0; m < NM; ++m) acc[m] = f4_t{0.f, 0.f, 0.f, 0.f};
@@ -665,15 +668,37 @@ __global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
       for (int m = 0; m < NM; ++m) raw[u + DEPTH][m] = gv_fetch<CLS, TL>(rows[m], u0 + u + DEPTH, kq);
     }
     const _Float16* xu = xrow + 256 * (u0 + u);
+    // XD: the lane's activations of half a unit (4 k-steps) in registers at a time
+    float4 xd[XD ? 8 : 1][1];
+    auto xload = [&](int h) {
+      if constexpr (XD) {
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+          const float4* src = reinterpret_cast<const float4*>(xgrow + 256 * (u0 + u) + gv_koff<CLS>(kq, 4 * h + s2));
+          xd[2 * s2][0] = src[0];
+          xd[2 * s2 + 1][0] = src[1];
+        }
+      }
+    };
+    xload(0);
 #define GV_STEP(SS)                                                                          \
   {                                                                                          \
-    const h8_t ax = *reinterpret_cast<const h8_t*>(xu + gv_koff<CLS>(kq, SS));               \
+    h8_t ax;                                                                                 \
+    if constexpr (XD) {                                                                      \
+      const float4 p0 = xd[2 * ((SS) & 3)][0], p1 = xd[2 * ((SS) & 3) + 1][0];               \
+      ax = h8_t{(_Float16)p0.x, (_Float16)p0.y, (_Float16)p0.z, (_Float16)p0.w,              \
+                (_Float16)p1.x, (_Float16)p1.y, (_Float16)p1.z, (_Float16)p1.w};             \
+    } else {                                                                                 \
+      ax = *reinterpret_cast<const h8_t*>(xu + gv_koff<CLS>(kq, SS));                        \
+    }                                                                                        \
     _Pragma("unroll") for (int m = 0; m < NM; ++m) {                                         \
       const h8_t bw = gv_decode<CLS, SS>(raw[u][m], kq, lut);                        \
       acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, bw, acc[m], 0, 0, 0);              \
     }                                                                                        \
   }
-    GV_STEP(0) GV_STEP(1) GV_STEP(2) GV_STEP(3) GV_STEP(4) GV_STEP(5) GV_STEP(6) GV_STEP(7)
+    GV_STEP(0) GV_STEP(1) GV_STEP(2) GV_STEP(3)
+    xload(1);
+    GV_STEP(4) GV_STEP(5) GV_STEP(6) GV_STEP(7)
 #undef GV_STEP
   }
   // k-split: the tile's waves add in kp order
@@ -704,6 +729,34 @@ __global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
       reinterpret_cast<_Float16*>(a.out)[o * kHid + n] = (_Float16)acc[0][r];
     }
   }
+}
+
+template <int CLS, bool UP, int FORM, int KS, int NW, bool TL>
+__global__ __launch_bounds__(64 * NW) void gv_kernel(const GxArgs a) {
+  using S = GvShape<CLS, UP, FORM, KS, NW>;
+  __shared__ __attribute__((aligned(16))) _Float16 xs[S::TOKR * S::LDX];
+  __shared__ GvLutSlot<CLS == GX_IQ3S> lslot;
+  __shared__ f4_t red[KS > 1 ? (KS - 1) * S::TW * S::NM * 64 : 1];
+  gv_body<CLS, UP, FORM, KS, NW, TL, false>(xs, lslot, red, a, (int)blockIdx.x);
+}
+
+// The pair walk (class RCLS, 4 waves, KSR) and the Q8_0 shared expert's dense form at P <= kGvTok
+// (direct token rows, 4 waves, KSS) in one launch: workgroups below nra walk the pairs (args a), the
+// rest run the shared expert (args b) -- each part its own code, the separate launches' bits.
+template <int RCLS, bool UP, int KSR, bool TL, int KSS>
+__global__ __launch_bounds__(256) void gv_psh_kernel(const GxArgs a, const GxArgs b, int nra) {
+  using SR = GvShape<RCLS, UP, GX_PAIRS, KSR, 4>;
+  using SS = GvShape<GX_Q80, UP, GX_DENSE, KSS, 4>;
+  constexpr int RR = KSR > 1 ? (KSR - 1) * SR::TW * SR::NM * 64 : 1, RS = KSS > 1 ? (KSS - 1) * SS::TW * SS::NM * 64 : 1;
+  __shared__ __attribute__((aligned(16))) _Float16 xs[SR::TOKR * SR::LDX];
+  __shared__ GvLutSlot<RCLS == GX_IQ3S> lslot;
+  __shared__ GvLutSlot<false> nolut;
+  __shared__ f4_t red[RR > RS ? RR : RS];
+  const int blk = (int)blockIdx.x;
+  if (blk < nra)
+    gv_body<RCLS, UP, GX_PAIRS, KSR, 4, TL, false>(xs, lslot, red, a, blk);
+  else
+    gv_body<GX_Q80, UP, GX_DENSE, KSS, 4, false, true>(xs, nolut, red, b, blk - nra);
 }
 
 template <int CLS, bool UP, int FORM, int KS, int NW, bool TL = false>
@@ -1016,19 +1069,34 @@ extern "C" int tlx_moe_dn6_pairs(const uint64_t* ptbl_dn, const uint16_t* eids, 
   return gv_launch<GX_Q6K, false, GX_PAIRS, 1, 4>(a, np, (hipStream_t)stream);
 }
 
+// the shared expert's decode k-split (4 waves a workgroup: the shape the pair walks' launches share)
+constexpr int kShKsUp = 4, kShKsDn = 2;
+
 // the shared expert's two launches (decode form at P <= kGvTok)
 static int moe_shared8_up(const void* wg, const void* wu, const float* x, float* act, int P, hipStream_t st) {
   GxArgs a{};
   a.w0 = (const uint8_t*)wg; a.w1 = (const uint8_t*)wu; a.x = x; a.out = act; a.P = P;
-  if (P <= kGvTok) return gv_launch<GX_Q80, true, GX_DENSE, 8, 8>(a, 1, st);
+  if (P <= kGvTok) return gv_launch<GX_Q80, true, GX_DENSE, kShKsUp, 4>(a, 1, st);
   return gx_launch<GX_Q80, true, GX_DENSE>(a, (P + gx_tok<GX_DENSE>() - 1) / gx_tok<GX_DENSE>(), st);
 }
 
 static int moe_shared8_dn(const void* wd, const float* act, float* y, int P, hipStream_t st) {
   GxArgs b{};
   b.w0 = (const uint8_t*)wd; b.x = act; b.out = y; b.P = P;
-  if (P <= kGvTok) return gv_launch<GX_Q80, false, GX_DENSE, 2, 8>(b, 1, st);
+  if (P <= kGvTok) return gv_launch<GX_Q80, false, GX_DENSE, kShKsDn, 4>(b, 1, st);
   return gx_launch<GX_Q80, false, GX_DENSE>(b, (P + gx_tok<GX_DENSE>() - 1) / gx_tok<GX_DENSE>(), st);
+}
+
+// the pair walk (a, np items) + the shared expert's dense form with direct token rows (b, P <= kGvTok)
+template <int RCLS, bool UP, int KSR, bool TL, int KSS>
+static int gv_psh_launch(const GxArgs& a, int np, const GxArgs& b, hipStream_t st) {
+  GxArgs ra = a, sb = b;
+  ra.items = np;
+  sb.items = 1;
+  const int nra = (np + 7) / 8 * 8 * GvShape<RCLS, UP, GX_PAIRS, KSR, 4>::RB;
+  const int nsb = GvShape<GX_Q80, UP, GX_DENSE, KSS, 4>::RB;
+  gv_psh_kernel<RCLS, UP, KSR, TL, KSS><<<(unsigned)(nra + nsb), 256, 0, st>>>(ra, sb, nra);
+  return tlx_launch_status();
 }
 
 // routed sorted form (a, kE items) + the shared expert's dense form (b) in one launch, P > kGvTok
@@ -1106,6 +1174,51 @@ extern "C" int tlx_moe_shared8(const void* wg, const void* wu, const void* wd, c
   const int r = moe_shared8_up(wg, wu, x, act, P, st);   // decode (P <= 16): the GEMV-shaped form
   TLX_RET_IF(r != TLX_OK, r);
   return moe_shared8_dn(wd, act, y, P, st);
+}
+
+extern "C" int tlx_moe_up3s_pairs_sh(const uint64_t* ptbl, const uint16_t* eids, const float* xs, const float* gridf,
+                                     float* ys, int np, const void* wg8, const void* wu8, float* sact, int P,
+                                     int layout, void* stream) {
+  TLX_RET_IF(!ptbl || !eids || !xs || !gridf || !ys || !wg8 || !wu8 || !sact, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs || P < 1 || P > kMaxPairs || !ckpt_layout_ok(layout), TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(ptbl, 8) || !tlx_aligned(xs, 16) || !tlx_aligned(gridf, 16) || !tlx_aligned(ys, 4),
+             TLX_E_ALIGN);
+  TLX_RET_IF(!tlx_aligned(wg8, 2) || !tlx_aligned(wu8, 2) || !tlx_aligned(sact, 16), TLX_E_ALIGN);
+  const hipStream_t st = (hipStream_t)stream;
+  GxArgs a{};
+  a.ptbl = ptbl; a.eids = eids; a.x = xs; a.grid = gridf; a.out = ys;
+  if (P > kGvTok) {   // the shared expert's batch form is another kernel: two launches
+    const int rc = layout == TLX_LAYOUT_TILED ? gv_launch<GX_IQ3S, true, GX_PAIRS, 4, 4, true>(a, np, st)
+                                              : gv_launch<GX_IQ3S, true, GX_PAIRS, 4, 4>(a, np, st);
+    TLX_RET_IF(rc != TLX_OK, rc);
+    return moe_shared8_up(wg8, wu8, xs, sact, P, st);
+  }
+  GxArgs b{};
+  b.w0 = (const uint8_t*)wg8; b.w1 = (const uint8_t*)wu8; b.x = xs; b.out = sact; b.P = P;
+  if (layout == TLX_LAYOUT_TILED) return gv_psh_launch<GX_IQ3S, true, 4, true, kShKsUp>(a, np, b, st);
+  return gv_psh_launch<GX_IQ3S, true, 4, false, kShKsUp>(a, np, b, st);
+}
+
+extern "C" int tlx_moe_dn6_pairs_sh(const uint64_t* ptbl_dn, const uint16_t* eids, const float* act, uint16_t* parts,
+                                    int np, const void* wd8, const float* sact, float* shared, int P, int layout,
+                                    void* stream) {
+  TLX_RET_IF(!ptbl_dn || !eids || !act || !parts || !wd8 || !sact || !shared, TLX_E_ARG);
+  TLX_RET_IF(np < 1 || np > kMaxPairs || P < 1 || P > kMaxPairs || !ckpt_layout_ok(layout), TLX_E_ARG);
+  TLX_RET_IF(!tlx_aligned(ptbl_dn, 8) || !tlx_aligned(act, 16) || !tlx_aligned(parts, 2), TLX_E_ALIGN);
+  TLX_RET_IF(!tlx_aligned(wd8, 2) || !tlx_aligned(sact, 16) || !tlx_aligned(shared, 4), TLX_E_ALIGN);
+  const hipStream_t st = (hipStream_t)stream;
+  GxArgs a{};
+  a.ptbl = ptbl_dn; a.eids = eids; a.x = act; a.out = parts;
+  if (P > kGvTok) {
+    const int rc = layout == TLX_LAYOUT_TILED ? gv_launch<GX_Q6K, false, GX_PAIRS, 1, 4, true>(a, np, st)
+                                              : gv_launch<GX_Q6K, false, GX_PAIRS, 1, 4>(a, np, st);
+    TLX_RET_IF(rc != TLX_OK, rc);
+    return moe_shared8_dn(wd8, sact, shared, P, st);
+  }
+  GxArgs b{};
+  b.w0 = (const uint8_t*)wd8; b.x = sact; b.out = shared; b.P = P;
+  if (layout == TLX_LAYOUT_TILED) return gv_psh_launch<GX_Q6K, false, 1, true, kShKsDn>(a, np, b, st);
+  return gv_psh_launch<GX_Q6K, false, 1, false, kShKsDn>(a, np, b, st);
 }
 
 // ------------------------------------------------------------------ tiled checkpoint slabs

@@ -922,6 +922,41 @@ def moe_dn6_pairs(ptbl_dn, eids, act, parts, stream=None, layout=LAYOUT_RAW):
          _stream(stream))
 
 
+def moe_up3s_pairs_sh(ptbl, eids, xs, gridf, ys, wg8, wu8, sact, stream=None, layout=LAYOUT_RAW):
+    """moe_up3s_pairs and the Q8_0 shared expert's gate+up (wg8 / wu8 rows, into sact [P][512],
+    P = sact.shape[0]) in one launch at P <= 16 (else the two launches); outputs those of
+    moe_up3s_pairs and moe_shared8's gate+up bit for bit."""
+    n = ys.shape[0]
+    P = sact.shape[0]
+    _need(ptbl, 256 * 8, "ptbl")
+    _need(eids, n * 2, "eids")
+    _need(xs, max(P, (n + 7) // 8) * 2048 * 4, "xs")
+    _need(ys, n * 512 * 4, "ys")
+    _need(gridf, 512 * 16, "gridf")
+    _need(wg8, 512 * 2176, "wg8")
+    _need(wu8, 512 * 2176, "wu8")
+    _need(sact, P * 512 * 4, "sact")
+    _dev(ptbl, eids, xs, gridf, ys, wg8, wu8, sact)
+    call("tlx_moe_up3s_pairs_sh", ptbl.data_ptr(), eids.data_ptr(), xs.data_ptr(), gridf.data_ptr(), ys.data_ptr(),
+         n, wg8.data_ptr(), wu8.data_ptr(), sact.data_ptr(), P, layout, _stream(stream))
+
+
+def moe_dn6_pairs_sh(ptbl_dn, eids, act, parts, wd8, sact, shared, stream=None, layout=LAYOUT_RAW):
+    """moe_dn6_pairs and the Q8_0 shared expert's down projection (wd8 rows, sact [P][512] into
+    shared [P][2048] f32) in one launch at P <= 16 (else the two launches); the separate calls' bits."""
+    n = act.shape[0]
+    P = sact.shape[0]
+    _need(ptbl_dn, 256 * 8, "ptbl_dn")
+    _need(eids, n * 2, "eids")
+    _need(act, n * 512 * 4, "act")
+    _need(parts, n * 2048 * 2, "parts")
+    _need(wd8, 2048 * 544, "wd8")
+    _need(shared, P * 2048 * 4, "shared")
+    _dev(ptbl_dn, eids, act, parts, wd8, sact, shared)
+    call("tlx_moe_dn6_pairs_sh", ptbl_dn.data_ptr(), eids.data_ptr(), act.data_ptr(), parts.data_ptr(), n,
+         wd8.data_ptr(), sact.data_ptr(), shared.data_ptr(), P, layout, _stream(stream))
+
+
 def moe_shared8(wg, wu, wd, x, y, act, stream=None):
     """shexp8(wg, wu, wd, x, y): the Q8_0 shared expert over P = x.shape[0] positions,
     y[P][2048] f32 = Wd . (silu(Wg . x) * (Wu . x)); act: caller scratch f32 [P][512]."""
@@ -1028,9 +1063,9 @@ def moe_layer_ckpt(logits, sg, xs, hres, y, ptbl, ptbl_dn, shared8, gridf, scrat
     the IQ3_S gate+up, the down projection -- ``down`` "q6k" (Q6_K slabs, the checkpoint's layers
     34/38/39) or "iq4" (IQ4_XS GGUF-row slabs, iq4nl given) -- the Q8_0 shared expert
     (shared8 = (wg, wu, wd) rows), and the combine into y.  overlap_shared as moe_layer's: by
-    default the shared expert rides in the grouped launches (moe_up3s_sh / moe_dn6_sh; the pair
-    walk keeps its own two launches, the decode form being another kernel); with it, on a second
-    stream joined before the combine.  ``layout`` (LAYOUT_RAW or LAYOUT_TILED) is that of the routed
+    default the shared expert rides in the routed launches (the pair walk's moe_up3s_pairs_sh /
+    moe_dn6_pairs_sh, the grouped forms' moe_up3s_sh / moe_dn6_sh); with it, on a second stream
+    joined before the combine.  ``layout`` (LAYOUT_RAW or LAYOUT_TILED) is that of the routed
     slabs, gate/up and down alike (pack_iq3s_tiled, pack_q6k_tiled / pack_iq4_tiled)."""
     sc = scratch
     if pair_walk is None:
@@ -1048,15 +1083,19 @@ def moe_layer_ckpt(logits, sg, xs, hres, y, ptbl, ptbl_dn, shared8, gridf, scrat
     moe_topk(logits, sc.eids, sc.gates, stream=cur)
     eids = sc.eids.view(-1)
     wg8, wu8, wd8 = shared8
-    # the shared expert in the grouped launches (the Q6_K down layers; with an IQ4_XS down the
+    # the shared expert in the routed launches (the Q6_K down layers; with an IQ4_XS down the
     # shared expert keeps its own two launches)
-    fused = side is None and not pair_walk and down == "q6k"
+    fused = side is None and down == "q6k"
     if pair_walk:
-        moe_up3s_pairs(ptbl, eids, xs, gridf, sc.act, stream=cur, layout=layout)
-        if down == "q6k":
-            moe_dn6_pairs(ptbl_dn, eids, sc.act, sc.parts, stream=cur, layout=layout)
+        if fused:
+            moe_up3s_pairs_sh(ptbl, eids, xs, gridf, sc.act, wg8, wu8, sc.sact, stream=cur, layout=layout)
+            moe_dn6_pairs_sh(ptbl_dn, eids, sc.act, sc.parts, wd8, sc.sact, sc.shared, stream=cur, layout=layout)
         else:
-            moe_dn4_pairs(ptbl_dn, eids, sc.act, iq4nl, sc.parts, stream=cur, layout=layout)
+            moe_up3s_pairs(ptbl, eids, xs, gridf, sc.act, stream=cur, layout=layout)
+            if down == "q6k":
+                moe_dn6_pairs(ptbl_dn, eids, sc.act, sc.parts, stream=cur, layout=layout)
+            else:
+                moe_dn4_pairs(ptbl_dn, eids, sc.act, iq4nl, sc.parts, stream=cur, layout=layout)
     else:
         moe_sort(sc.eids, sc.eoff, sc.plist, sc.items, sc.nitp, stream=cur)
         if fused:
