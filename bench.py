@@ -98,8 +98,8 @@ TRAFFIC = {
     "merged_gdnqg": 542_371_430,        # pfm_gemm_kernel: F 232,061.8  W 65,536
     "moe_m11": 153_883_750,             # topk + pair-walk gate+up and down (shared inside) + combine: F 74,775.3  W 726.5
     "moe_m2048": 863_987_917,           # topk, sort, grouped gate+up / down with the shared expert, combine: F 354,038.1  W 135,662.0
-    "ckpt_m11": 162_036_224,            # checkpoint classes, tiled slabs: topk, pair-walk IQ3_S up / Q6_K down, Q8_0 shared two, combine: F 78,755.9  W 726.6
-    "ckpt_m2048": 940_513_792,          # checkpoint classes, tiled slabs: topk, sort, sorted up with the shared expert, register-decode down, shared down, combine: F 371,744.2  W 174,973.3
+    "ckpt_m11": 161_757_081,            # checkpoint classes, tiled slabs: topk, pair-walk IQ3_S up / Q6_K down with the Q8_0 shared expert inside, combine: F 78,619.7  W 726.5
+    "ckpt_m2048": 939_681_894,          # checkpoint classes, tiled slabs: topk, sort, sorted up with the shared expert, register-decode down, shared down, combine: F 371,734.4  W 174,189.3
     "sweep": 12_030_388_122,            # one decode step: F 5,591,363.3  W 565,699.3
 }
 PEAK_F16_TFLOPS = 2500.0
