@@ -657,7 +657,7 @@ __device__ __forceinline__ void gv_body(_Float16* xs, GvLutSlot<CLS == GX_IQ3S>&
     for (int m = 0; m < NM; ++m) raw[u][m] = gv_fetch<CLS, TL>(rows[m], u0 + u, kq);
   __syncthreads();   // token rows, lookups
   const _Float16* xrow = xs + (FORM == GX_PAIRS ? 0 : col) * LDX;
-  const float* xgrow = a.x + (size_t)(beg + min(col, nt - 1)) * K;   // XD: the lane's token row
+  const float* xgrow = XD ? a.x + (size_t)(beg + min(col, nt - 1)) * K : nullptr;   // XD: the lane's token row
   f4_t acc[NM];
 #pragma unroll
   for (int m = 0; m < NM; ++m) acc[m] = f4_t{0.f, 0.f, 0.f, 0.f};
