@@ -232,7 +232,7 @@ def ckpt_tiled(gpu, ckpt):
     return {"tgu": tgu, "tdn": tdn, "ptbl": formats.pointer_table(tgu, gpu), "ptbl_dn": formats.pointer_table(tdn, gpu)}
 
 
-@pytest.mark.parametrize("P", [11, 300])
+@pytest.mark.parametrize("P", [11, 300, 2048])
 def test_ckpt_tiled_forms_bit_identical(gpu, ckpt, ckpt_tiled, P):
     """Every checkpoint-class routed form over the tiled slabs (layout=LAYOUT_TILED) against the same
     form over the GGUF rows, bit for bit: the pair walks, the sorted forms, the forms with the shared
@@ -275,7 +275,7 @@ def test_ckpt_tiled_forms_bit_identical(gpu, ckpt, ckpt_tiled, P):
     for k in raw:
         v = np.uint16 if raw[k].dtype == np.float16 else np.uint32
         assert np.array_equal(raw[k].view(v), til[k].view(v)), k
-    _check_pairs(ckpt, x, eids, til["act"], til["parts"], list(range(0, np_, 7)))
+    _check_pairs(ckpt, x, eids, til["act"], til["parts"], list(range(0, np_, 7 if P <= 300 else 509)))
 
 
 @pytest.mark.parametrize("P,lay", [(1, LAYOUT_RAW), (11, LAYOUT_TILED), (16, LAYOUT_RAW), (17, LAYOUT_TILED)])
